@@ -1,0 +1,449 @@
+"""CPU oracle for the Block-ELL SwiGLU FFN path — TEST INFRASTRUCTURE ONLY.
+
+This module restates, in numpy, the arithmetic of the reference's Block-ELL
+SwiGLU forward so that the HIP kernels can be checked against it.  It is the
+checker, never the product: only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import it.  The shipped path
+(``looped_blockell``) never imports, calls or falls back to anything here.
+
+Every function cites the reference file:line it restates.  How each function is
+pinned (closed forms, invariants from the reference's own tests, brute force on
+tiny inputs) is listed in ``PINS`` at the bottom of this file; the tests in
+``tests/test_oracle.py`` enforce each pin.
+
+Layout conventions (reference ``looped_blockell/layers/block_ell.py:1-8``):
+  values      [R, K, B, B]  tile values[r, k] is [B_in, B_out]
+  col_indices [R, K] int32  input column-block of each tile; -1 marks a dead
+                            slot that contributes nothing
+                            (``looped_blockell/opt/cms.py:229-230``)
+  weight      [out, in] = [R*B, C*B]
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+__all__ = [
+    "BlockELLConfig", "k_for_density", "random_topology", "dense_to_block_ell",
+    "block_ell_to_dense", "create_block_ell_from_dense", "block_ell_matmul",
+    "silu", "swiglu_fwd", "rmsnorm", "looped_swiglu", "ternary_quantize_blocks",
+    "activation_quantize_int8", "encode_ternary", "pack_ternary",
+    "unpack_ternary", "ternary_block_partials", "ternary_fixed_point",
+    "ternary_matmul", "ternary_swiglu_fwd", "bf16_round",
+]
+
+
+# --------------------------------------------------------------------------
+# format
+# --------------------------------------------------------------------------
+
+@dataclass
+class BlockELLConfig:
+    """Geometry of one Block-ELL weight (``looped_blockell/layers/block_ell.py:19-50``)."""
+
+    R: int
+    C: int
+    K: int
+    B: int = 16
+
+    def __post_init__(self) -> None:
+        # block_ell.py:26-30
+        if self.K > self.C:
+            raise ValueError(f"K ({self.K}) cannot exceed C ({self.C})")
+        if any(v < 1 for v in (self.R, self.C, self.K, self.B)):
+            raise ValueError("R, C, K, B must all be >= 1")
+
+    @property
+    def out_features(self) -> int:
+        return self.R * self.B
+
+    @property
+    def in_features(self) -> int:
+        return self.C * self.B
+
+    @property
+    def total_blocks(self) -> int:
+        return self.R * self.K
+
+    @property
+    def density(self) -> float:
+        return self.K / self.C
+
+
+def k_for_density(C: int, density: float) -> int:
+    """``K = max(1, int(C * density))`` (``looped_blockell/layers/mlp.py:44``)."""
+    return max(1, int(C * density))
+
+
+def random_topology(R: int, C: int, K: int, rng: np.random.Generator) -> np.ndarray:
+    """K distinct, unsorted column blocks per row (``block_ell.py:69-76``).
+
+    The reference draws with ``jax.random.choice(replace=False)``; the stream is
+    JAX's, so this restatement keeps only the contract (distinct, unsorted,
+    uniform) and uses numpy's generator.
+    """
+    out = np.empty((R, K), dtype=np.int32)
+    for r in range(R):
+        out[r] = rng.choice(C, size=K, replace=False)
+    return out
+
+
+def dense_to_block_ell(weight: np.ndarray, tile_size: int = 16):
+    """Dense [out, in] -> (values [R, C, B_in, B_out], sequential col_indices).
+
+    Restates ``interop/convert_checkpoint.py:114-131`` (density 1.0).
+    """
+    out_f, in_f = weight.shape
+    B = tile_size
+    R, C = out_f // B, in_f // B
+    blocks = weight.reshape(R, B, C, B).transpose(0, 2, 3, 1)
+    col = np.tile(np.arange(C, dtype=np.int32), (R, 1))
+    return np.ascontiguousarray(blocks), col
+
+
+def block_ell_to_dense(values: np.ndarray, col_indices: np.ndarray, out_features: int,
+                       in_features: int) -> np.ndarray:
+    """Scatter Block-ELL to dense [out, in]; tile [B_in, B_out] lands transposed.
+
+    Restates ``interop/convert_checkpoint.py:134-148`` and
+    ``looped_blockell/layers/block_ell.py:118-146``.  Dead slots (col < 0) are
+    skipped.
+    """
+    R, K, B, _ = values.shape
+    dense = np.zeros((out_features, in_features), dtype=values.dtype)
+    for r in range(R):
+        for k in range(K):
+            c = int(col_indices[r, k])
+            if c < 0:
+                continue
+            dense[r * B:(r + 1) * B, c * B:(c + 1) * B] = values[r, k].T
+    return dense
+
+
+def create_block_ell_from_dense(dense: np.ndarray, tile_size: int = 16, density: float = 0.5):
+    """Top-K tiles per row by Frobenius norm, sorted indices.
+
+    Restates ``looped_blockell/layers/block_ell.py:79-115``.
+    """
+    out_f, in_f = dense.shape
+    B = tile_size
+    if out_f % B or in_f % B:
+        raise ValueError(f"Dimensions ({out_f}, {in_f}) must be divisible by tile_size {B}")
+    R, C = out_f // B, in_f // B
+    K = k_for_density(C, density)
+    blocks = dense.reshape(R, B, C, B).transpose(0, 2, 3, 1)       # [R, C, B_in, B_out]
+    norms = np.sqrt(np.sum(blocks.astype(np.float64) ** 2, axis=(2, 3)))
+    top = np.argsort(-norms, axis=1, kind="stable")[:, :K]
+    col = np.sort(top, axis=1).astype(np.int32)
+    values = np.take_along_axis(blocks, col[:, :, None, None], axis=1)
+    return np.ascontiguousarray(values), col, BlockELLConfig(R=R, C=C, K=K, B=B)
+
+
+# --------------------------------------------------------------------------
+# block-sparse matmul and the SwiGLU FFN
+# --------------------------------------------------------------------------
+
+def block_ell_matmul(x: np.ndarray, values: np.ndarray, col_indices: np.ndarray,
+                     chunk: int = 1024) -> np.ndarray:
+    """``y[n, r*B+D] = sum_k sum_d x[n, col[r,k]*B+d] * values[r,k,d,D]``.
+
+    Restates ``looped_blockell/layers/block_ell.py:149-182``: tile the input
+    into [.., C, B], gather the K column tiles of every block row, contract over
+    (k, d).  The contraction runs as R batched [n, K*B] x [K*B, B] products in
+    the dtype of the inputs.  Dead slots (col < 0) contribute zero
+    (``looped_blockell/opt/cms.py:229-230``); the JAX layer achieves the same
+    by zeroing dead values (``looped_blockell/layers/mlp.py:73-77``).
+    Tokens are processed ``chunk`` at a time to bound the gather's memory.
+    """
+    lead = x.shape[:-1]
+    R, K, B, B2 = values.shape
+    assert B == B2
+    F = x.shape[-1]
+    assert F % B == 0, "in_features must be a multiple of B"
+    C = F // B
+    xf = x.reshape(-1, C, B)
+    n = xf.shape[0]
+    dtype = np.result_type(x.dtype, values.dtype)
+    out = np.zeros((n, R, B), dtype=dtype)
+    col = col_indices.astype(np.int64)
+    alive = col >= 0
+    safe = np.where(alive, col, 0)
+    w = np.where(alive[:, :, None, None], values, 0).astype(dtype)          # [R,K,B,B]
+    w2 = w.reshape(R, K * B, B)                                             # [R, K*B_in, B_out]
+    for s in range(0, n, chunk):
+        xs = xf[s:s + chunk].astype(dtype)                                  # [n, C, B]
+        g = xs[:, safe.reshape(-1), :].reshape(xs.shape[0], R, K * B)       # [n, R, K*B]
+        out[s:s + chunk] = np.matmul(g.transpose(1, 0, 2), w2).transpose(1, 0, 2)
+    return out.reshape(*lead, R * B)
+
+
+def silu(z: np.ndarray) -> np.ndarray:
+    """``silu(z) = z * sigmoid(z)`` (``looped_blockell/layers/mlp.py:137``, jax.nn.silu)."""
+    z = np.asarray(z)
+    return z / (1.0 + np.exp(-z))
+
+
+def swiglu_fwd(x, gate, up, down, add_residual: bool = False, h_round=None):
+    """``out = W_down(silu(W_gate x) * W_up x) (+ x)``.
+
+    Restates ``looped_blockell/layers/mlp.py:119-145`` (SwiGLU branch) and the
+    reference operator's optional residual epilogue
+    (``csrc/block_ell/swiglu_fwd.cuh:60-84``).  ``gate``/``up``/``down`` are
+    ``(values, col_indices)`` pairs.  ``h_round`` optionally rounds the hidden
+    state (e.g. to bf16) before the down projection.
+    Returns ``(out, h, gate_pre_act, up_output)``.
+    """
+    g = block_ell_matmul(x, *gate)
+    u = block_ell_matmul(x, *up)
+    h = silu(g) * u
+    if h_round is not None:
+        h = h_round(h)
+    out = block_ell_matmul(h, *down)
+    if add_residual:
+        out = out + x
+    return out, h, g, u
+
+
+def rmsnorm(x: np.ndarray, scale: np.ndarray, eps: float = 1e-5) -> np.ndarray:
+    """``x / sqrt(mean(x^2) + eps) * scale`` (``looped_blockell/layers/norms.py:14-15``)."""
+    ms = np.mean(x * x, axis=-1, keepdims=True)
+    return x / np.sqrt(ms + eps) * scale
+
+
+def looped_swiglu(h, norm_scale, gate, up, down, L: int, eps: float = 1e-5, state_round=None):
+    """L applications of the pre-norm residual FFN block with shared weights.
+
+    ``h <- h + SwiGLU(RMSNorm(h))`` (``looped_blockell/layers/transformer_block.py:84``;
+    the MLP part of ``csrc/loop/persistent_core.cu:315-335``).  ``state_round``
+    optionally rounds the carried state after each iteration (e.g. to bf16).
+    """
+    for _ in range(L):
+        y, *_ = swiglu_fwd(rmsnorm(h, norm_scale, eps), gate, up, down)
+        h = h + y
+        if state_round is not None:
+            h = state_round(h)
+    return h
+
+
+# --------------------------------------------------------------------------
+# ternary path (weights {-1,0,+1} with one scale per block, int8 activations)
+# --------------------------------------------------------------------------
+
+def ternary_quantize_blocks(w: np.ndarray):
+    """Per-block absmean ternary quantisation of values [R, K, B, B].
+
+    Restates ``bonsai-test/bitlinear.py:34-55`` with the group = one B x B block:
+    ``s = max(mean|w|, 1e-8)``, ``t = clamp(round(w / s), -1, 1)``, computed in
+    float32.  Returns ``(t int8 [R,K,B,B], s float32 [R,K])``.
+    """
+    w = np.asarray(w, dtype=np.float32)
+    R, K, B, _ = w.shape
+    flat = w.reshape(R * K, B * B)
+    s = np.maximum(np.mean(np.abs(flat), axis=1, dtype=np.float32), np.float32(1e-8)).astype(np.float32)
+    t = np.clip(np.rint(flat / s[:, None]), -1, 1).astype(np.int8)
+    return t.reshape(R, K, B, B), s.reshape(R, K)
+
+
+def activation_quantize_int8(x: np.ndarray):
+    """Per-token absmax int8 quantisation.
+
+    Restates ``bonsai-test/bitlinear.py:58-69`` for 8 bits, kept in integer form:
+    ``absmax = max(max|x|, 1e-8)``, ``scale = 128 / absmax`` (float32, correctly
+    rounded), ``q = clamp(rint(x * scale), -128, 127)`` (round-half-to-even).
+    The dequantisation multiplier returned is ``sx = absmax / 128`` (exact: a
+    power-of-two division).  Returns ``(q int8, sx float32 [rows])``.
+    """
+    x = np.asarray(x, dtype=np.float32)
+    absmax = np.maximum(np.max(np.abs(x), axis=-1), np.float32(1e-8)).astype(np.float32)
+    scale = (np.float32(128.0) / absmax).astype(np.float32)
+    q = np.clip(np.rint(x * scale[..., None]), -128, 127).astype(np.int8)
+    sx = (absmax / np.float32(128.0)).astype(np.float32)
+    return q, sx
+
+
+# 2-bit code per weight: 0 -> 0b00, +1 -> 0b01, -1 -> 0b11 (0b10 decodes to 0).
+_CODE = {0: 0, 1: 1, -1: 3}
+_DECODE = np.array([0, 1, 0, -1], dtype=np.int8)
+
+
+def encode_ternary(t: np.ndarray) -> np.ndarray:
+    """Map {-1,0,+1} to 2-bit codes {0b11, 0b00, 0b01}."""
+    t = np.asarray(t)
+    if not np.all(np.isin(t, (-1, 0, 1))):
+        raise ValueError("ternary codes must be in {-1, 0, +1}")
+    return (t.astype(np.int64) & 3).astype(np.uint32)
+
+
+def pack_ternary(t: np.ndarray) -> np.ndarray:
+    """Pack ternary tiles [R, K, B_in, B_out] into uint32 words [R, K, B_out, B_in/16].
+
+    This 2-bit storage format is defined by this build (the reference has no
+    packed ternary format; only the arithmetic of ``bonsai-test/bitlinear.py``).
+    Word (r, k, D, e) holds the 16 weights t[r, k, 16e + i, D], i = 0..15; the
+    2-bit code of input index i sits at bit ``8*(i % 4) + 2*(i // 4)``, so that
+    ``(word >> 2q) & 0x03030303`` yields the codes of i = 4q..4q+3 in bytes 0..3.
+    """
+    t = np.asarray(t)
+    R, K, Bi, Bo = t.shape
+    if Bi % 16:
+        raise ValueError("B must be a multiple of 16 for the packed ternary format")
+    codes = encode_ternary(t).transpose(0, 1, 3, 2).reshape(R, K, Bo, Bi // 16, 16)
+    i = np.arange(16)
+    shifts = (8 * (i % 4) + 2 * (i // 4)).astype(np.uint32)
+    words = np.zeros((R, K, Bo, Bi // 16), dtype=np.uint32)
+    for j in range(16):
+        words |= (codes[..., j] << shifts[j]).astype(np.uint32)
+    return words
+
+
+def unpack_ternary(words: np.ndarray) -> np.ndarray:
+    """Inverse of :func:`pack_ternary`; returns int8 [R, K, B_in, B_out]."""
+    R, K, Bo, E = words.shape
+    i = np.arange(16)
+    shifts = (8 * (i % 4) + 2 * (i // 4)).astype(np.uint32)
+    codes = (words[..., None] >> shifts) & np.uint32(3)                # [R,K,Bo,E,16]
+    t = _DECODE[codes.astype(np.int64)].reshape(R, K, Bo, E * 16)
+    return np.ascontiguousarray(t.transpose(0, 1, 3, 2))
+
+
+def ternary_block_partials(q: np.ndarray, t: np.ndarray, col_indices: np.ndarray) -> np.ndarray:
+    """Exact integer block partials ``P[n, r, k, j] = sum_i q[n, col*B+i] * t[r,k,i,j]``.
+
+    The build's definition of the ternary Block-ELL product (the per-group
+    arithmetic of ``bonsai-test/bitlinear.py:34-69`` with group = one block).
+    Dead slots give P = 0.  Computed in int64.
+    """
+    n = q.shape[0]
+    R, K, B, _ = t.shape
+    qf = q.astype(np.int64).reshape(n, -1, B)
+    P = np.zeros((n, R, K, B), dtype=np.int64)
+    for r in range(R):
+        for k in range(K):
+            c = int(col_indices[r, k])
+            if c < 0:
+                continue
+            P[:, r, k, :] = qf[:, c, :] @ t[r, k].astype(np.int64)
+    return P
+
+
+def ternary_fixed_point(scales: np.ndarray, col_indices: np.ndarray, B: int):
+    """Per-row fixed-point form of the fp32 block scales used by the kernels.
+
+    For each block row r the kernels replace ``s[r,k]`` by ``m[r,k] * 2**-e[r]``
+    with integer ``m`` small enough that ``sum_k m * P`` cannot overflow int32
+    for any int8 input: ``m_max = floor((2**31 - 1) / (K_alive * B * 128))``
+    capped at ``2**16 - 1``; ``e[r]`` is the largest integer with
+    ``max_k s[r,k] * 2**e <= m_max``; ``m = rint(s * 2**e)``.
+    Returns ``(m int64 [R,K], e int64 [R])``.  Rows with no live block get e = 0.
+    """
+    s = np.asarray(scales, dtype=np.float32)
+    R, K = s.shape
+    alive = np.asarray(col_indices) >= 0
+    m = np.zeros((R, K), dtype=np.int64)
+    e = np.zeros(R, dtype=np.int64)
+    for r in range(R):
+        ka = int(alive[r].sum())
+        if ka == 0:
+            continue
+        mmax = min((2 ** 31 - 1) // (ka * B * 128), 2 ** 16 - 1)
+        smax = float(np.max(np.where(alive[r], s[r], 0)))
+        if smax <= 0.0:
+            continue
+        er = math.floor(math.log2(mmax / smax))
+        while smax * 2.0 ** er > mmax:
+            er -= 1
+        while smax * 2.0 ** (er + 1) <= mmax:
+            er += 1
+        e[r] = er
+        m[r] = np.where(alive[r], np.rint(s[r].astype(np.float64) * 2.0 ** er), 0).astype(np.int64)
+    return m, e
+
+
+def ternary_matmul(q: np.ndarray, sq: np.ndarray, t: np.ndarray, scales: np.ndarray,
+                   col_indices: np.ndarray, exact_scales: bool = True):
+    """Ternary Block-ELL product with int8 activations.
+
+    ``y[n, r*B+j] = sq[n] * sum_k s[r,k] * P[n,r,k,j]`` (float64) when
+    ``exact_scales``; otherwise the kernels' fixed-point form
+    ``y = f32(f32(sum_k m*P) * 2**-e) * sq`` evaluated exactly as the kernels do
+    (int64 sum, then two float32 roundings).  Returns ``(y, acc)`` where ``acc``
+    is the int64 ``sum_k m*P`` (``None`` when ``exact_scales``).
+    """
+    P = ternary_block_partials(q, t, col_indices)                       # [n,R,K,B]
+    n, R, K, B = P.shape
+    if exact_scales:
+        y = np.einsum("nrkj,rk->nrj", P.astype(np.float64), scales.astype(np.float64))
+        return (y * sq.astype(np.float64)[:, None, None]).reshape(n, R * B), None
+    m, e = ternary_fixed_point(scales, col_indices, B)
+    acc = np.einsum("nrkj,rk->nrj", P, m)                               # int64 [n,R,B]
+    assert np.all(np.abs(acc) < 2 ** 31)
+    mult = np.ldexp(np.float32(1.0), -e).astype(np.float32)              # [R]
+    y = (acc.astype(np.float32) * mult[None, :, None]).astype(np.float32)
+    y = (y * sq.astype(np.float32)[:, None, None]).astype(np.float32)
+    return y.reshape(n, R * B), acc
+
+
+def ternary_swiglu_fwd(x: np.ndarray, gate, up, down, add_residual: bool = False,
+                       exact_scales: bool = True, h_round=None, hq_given=None):
+    """Ternary SwiGLU FFN: int8 x, ternary gate/up, re-quantised h, ternary down.
+
+    ``gate``/``up``/``down`` are ``(t [R,K,B,B] int8, s [R,K] f32, col [R,K])``.
+    Activations are quantised per token (``bonsai-test/bitlinear.py:58-69``);
+    the hidden state is re-quantised per token over d_ff before the down
+    projection.  ``h_round`` rounds h (e.g. to bf16) before re-quantisation, as
+    the kernels store h in bf16.  ``hq_given = (hq, sh)`` substitutes the
+    kernel's own re-quantised hidden state for the down projection.
+    Returns a dict with xq, sx, g, u, h, hq, sh, out (and the integer
+    accumulators when ``exact_scales`` is False).
+    """
+    xq, sx = activation_quantize_int8(x)
+    g, acc_g = ternary_matmul(xq, sx, *gate, exact_scales=exact_scales)
+    u, acc_u = ternary_matmul(xq, sx, *up, exact_scales=exact_scales)
+    h = silu(g) * u
+    if h_round is not None:
+        h = h_round(h)
+    if hq_given is None:
+        hq, sh = activation_quantize_int8(h)
+    else:
+        hq, sh = hq_given
+    out, acc_d = ternary_matmul(hq, sh, *down, exact_scales=exact_scales)
+    if add_residual:
+        out = out + np.asarray(x, dtype=out.dtype)
+    return dict(xq=xq, sx=sx, g=g, u=u, h=h, hq=hq, sh=sh, out=out,
+                acc_g=acc_g, acc_u=acc_u, acc_d=acc_d)
+
+
+def bf16_round(a: np.ndarray) -> np.ndarray:
+    """Round float32 values to the nearest bfloat16 (ties to even), as float32."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    nan = np.isnan(a)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    out = rounded.astype(np.uint32).view(np.float32)
+    return np.where(nan, a, out).astype(np.float32)
+
+
+# How each function is pinned (enforced in tests/test_oracle.py).
+PINS = {
+    "BlockELLConfig": "reference tests/test_block_ell.py:17-22 known answers; K>C and <1 errors",
+    "k_for_density": "reference tests/test_block_ell.py:75-88 (K shrinks with density); closed form",
+    "random_topology": "reference tests/test_block_ell.py:25-31 (shape, dtype, per-row uniqueness)",
+    "dense_to_block_ell": "reference tests/test_interop.py:131-148 (shape (16,4,16,16), sequential cols, round trip)",
+    "block_ell_to_dense": "round trips (tests/test_block_ell.py:34-39, test_interop.py:132-140); tile-transpose special case",
+    "create_block_ell_from_dense": "round trip at density 1.0; top-K by Frobenius norm on a hand-built matrix",
+    "block_ell_matmul": "== x @ W.T of block_ell_to_dense (tests/test_block_ell.py:42-54); brute-force loops; "
+                        "identity tiles; sentinel contributes 0; linearity",
+    "silu": "closed form values (silu(0)=0, silu(z)-silu(-z)=z)",
+    "swiglu_fwd": "brute-force dense SwiGLU on tiny shapes; residual adds x exactly",
+    "rmsnorm": "constant-vector closed form; unit-RMS invariance; scale linearity",
+    "looped_swiglu": "L=0 identity; L=1 equals one block; L=2 equals composition",
+    "ternary_quantize_blocks": "hand-worked block; round-half-even cases; codes in {-1,0,1}",
+    "activation_quantize_int8": "hand-worked rows incl. ties and the -128/127 clamps; bitlinear dequant identity",
+    "pack_ternary": "hand-computed words; round trip over all codes",
+    "ternary_block_partials": "brute-force scalar loops; |P| <= B*128 extreme case",
+    "ternary_fixed_point": "m*2^-e within 2^-15 relative of s; worst-case sum fits int32",
+    "ternary_matmul": "exact == dense int matmul of unpacked tiles; fixed-point within 2^-14 of exact",
+}

@@ -1,0 +1,368 @@
+"""Pins for the CPU oracle (oracle/oracle.py).
+
+Each test checks one oracle function against something the oracle's own formula
+does not restate: the reference's test invariants and known answers, closed
+forms, or brute-force scalar loops on tiny inputs.  Planted-mistake tests at
+the end show that the checks would catch a transposed tile, a dropped block or
+a wrong rounding mode.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+
+def rng(seed=0):
+    return np.random.default_rng(seed)
+
+
+# ---------------------------------------------------------------- format
+
+def test_config_properties_known_answers():
+    # reference tests/test_block_ell.py:17-22
+    cfg = O.BlockELLConfig(R=4, C=8, K=3, B=16)
+    assert cfg.out_features == 64
+    assert cfg.in_features == 128
+    assert cfg.density == 0.375
+    assert cfg.total_blocks == 12
+
+
+def test_config_validation():
+    with pytest.raises(ValueError):
+        O.BlockELLConfig(R=1, C=2, K=3, B=16)
+    with pytest.raises(ValueError):
+        O.BlockELLConfig(R=0, C=2, K=1, B=16)
+
+
+def test_k_for_density():
+    # reference looped_blockell/layers/mlp.py:44 and tests/test_block_ell.py:75-88
+    assert O.k_for_density(32, 0.25) == 8
+    assert O.k_for_density(128, 0.25) == 32
+    assert O.k_for_density(32, 0.125) == 4
+    assert O.k_for_density(64, 0.10) == 6
+    assert O.k_for_density(224, 0.10) == 22
+    assert O.k_for_density(3, 0.1) == 1
+    assert O.k_for_density(6, 0.5) < O.k_for_density(6, 1.0)
+
+
+def test_random_topology_unique_unsorted():
+    # reference tests/test_block_ell.py:25-31
+    col = O.random_topology(64, 32, 8, rng(1))
+    assert col.shape == (64, 8) and col.dtype == np.int32
+    for r in range(64):
+        assert len(np.unique(col[r])) == 8
+    assert col.min() >= 0 and col.max() < 32
+    assert any(np.any(np.diff(col[r]) < 0) for r in range(64))  # not sorted
+
+
+def test_dense_to_block_ell_shapes_and_round_trip():
+    # reference tests/test_interop.py:131-148
+    w = rng(2).standard_normal((256, 64)).astype(np.float32)
+    values, col = O.dense_to_block_ell(w, tile_size=16)
+    assert values.shape == (16, 4, 16, 16)
+    assert col.shape == (16, 4)
+    np.testing.assert_array_equal(col, np.tile(np.arange(4, dtype=np.int32), (16, 1)))
+    back = O.block_ell_to_dense(values, col, 256, 64)
+    np.testing.assert_allclose(back, w, atol=1e-6)
+
+
+def test_tile_orientation_special_case():
+    # A single tile whose [B_in, B_out] entry (d=1, D=3) is 1 must land at dense[out=3, in=c*B+1].
+    B = 4
+    values = np.zeros((1, 1, B, B), dtype=np.float32)
+    values[0, 0, 1, 3] = 1.0
+    col = np.array([[2]], dtype=np.int32)
+    dense = O.block_ell_to_dense(values, col, B, 3 * B)
+    expect = np.zeros((B, 3 * B), dtype=np.float32)
+    expect[3, 2 * B + 1] = 1.0
+    np.testing.assert_array_equal(dense, expect)
+
+
+def test_from_dense_round_trip_and_topk():
+    # reference tests/test_block_ell.py:34-39
+    w = rng(3).standard_normal((64, 128)).astype(np.float32)
+    v, c, cfg = O.create_block_ell_from_dense(w, tile_size=16, density=1.0)
+    np.testing.assert_allclose(O.block_ell_to_dense(v, c, 64, 128), w, atol=1e-5)
+    # hand-built: row 0 has big tiles at columns 3 and 1; density 0.5 of C=4 -> K=2
+    w = np.full((16, 64), 0.01, dtype=np.float32)
+    w[:, 48:64] = 5.0
+    w[:, 16:32] = 2.0
+    v, c, cfg = O.create_block_ell_from_dense(w, tile_size=16, density=0.5)
+    assert cfg.K == 2
+    np.testing.assert_array_equal(c, [[1, 3]])       # sorted
+    np.testing.assert_array_equal(v[0, 1], np.full((16, 16), 5.0, dtype=np.float32))
+
+
+# ---------------------------------------------------------------- matmul
+
+def brute_matmul(x, values, col):
+    n, F = x.shape
+    R, K, B, _ = values.shape
+    y = np.zeros((n, R * B))
+    for t in range(n):
+        for r in range(R):
+            for k in range(K):
+                c = col[r, k]
+                if c < 0:
+                    continue
+                for d in range(B):
+                    xv = x[t, c * B + d]
+                    for D in range(B):
+                        y[t, r * B + D] += xv * values[r, k, d, D]
+    return y
+
+
+def test_matmul_matches_dense_at_density_one():
+    # reference tests/test_block_ell.py:42-54
+    g = rng(4)
+    W = g.standard_normal((32, 64))
+    x = g.standard_normal((2, 8, 64))
+    v, c, _ = O.create_block_ell_from_dense(W, tile_size=16, density=1.0)
+    np.testing.assert_allclose(O.block_ell_matmul(x, v, c), x @ W.T, atol=1e-10)
+
+
+def test_matmul_matches_dense_expansion_sparse():
+    g = rng(5)
+    R, C, K, B = 6, 5, 2, 8
+    values = g.standard_normal((R, K, B, B))
+    col = O.random_topology(R, C, K, g)
+    x = g.standard_normal((7, C * B))
+    W = O.block_ell_to_dense(values, col, R * B, C * B)
+    np.testing.assert_allclose(O.block_ell_matmul(x, values, col), x @ W.T, atol=1e-10)
+
+
+def test_matmul_brute_force_with_sentinel():
+    g = rng(6)
+    R, C, K, B = 3, 4, 3, 4
+    values = g.standard_normal((R, K, B, B))
+    col = O.random_topology(R, C, K, g)
+    col[1, 2] = -1
+    col[2, :] = -1
+    x = g.standard_normal((5, C * B))
+    y = O.block_ell_matmul(x, values, col, chunk=2)
+    np.testing.assert_allclose(y, brute_matmul(x, values, col), atol=1e-10)
+    assert np.all(y[:, 2 * B:3 * B] == 0)
+
+
+def test_matmul_identity_tiles_gather():
+    B, C = 4, 3
+    values = np.tile(np.eye(B)[None, None], (2, 1, 1, 1))
+    col = np.array([[2], [0]], dtype=np.int32)
+    x = np.arange(2 * C * B, dtype=np.float64).reshape(2, C * B)
+    y = O.block_ell_matmul(x, values, col)
+    np.testing.assert_array_equal(y[:, :B], x[:, 2 * B:3 * B])
+    np.testing.assert_array_equal(y[:, B:], x[:, :B])
+
+
+def test_matmul_linearity():
+    g = rng(7)
+    values = g.standard_normal((4, 2, 8, 8))
+    col = O.random_topology(4, 3, 2, g)
+    x1, x2 = g.standard_normal((3, 24)), g.standard_normal((3, 24))
+    a = O.block_ell_matmul(2.0 * x1 - 3.0 * x2, values, col)
+    b = 2.0 * O.block_ell_matmul(x1, values, col) - 3.0 * O.block_ell_matmul(x2, values, col)
+    np.testing.assert_allclose(a, b, atol=1e-10)
+
+
+# ---------------------------------------------------------------- SwiGLU / norm / loop
+
+def test_silu_closed_forms():
+    assert O.silu(np.array(0.0)) == 0.0
+    z = np.linspace(-8, 8, 33)
+    np.testing.assert_allclose(O.silu(z) - O.silu(-z), z, atol=1e-12)
+    np.testing.assert_allclose(O.silu(np.array([1.0])), [1.0 / (1.0 + math.exp(-1.0))], rtol=1e-15)
+
+
+def test_swiglu_brute_dense():
+    g = rng(8)
+    B, dm, dff = 4, 12, 16
+    Cm, Cf = dm // B, dff // B
+    Rf, Rm = dff // B, dm // B
+    gate = (g.standard_normal((Rf, 2, B, B)), O.random_topology(Rf, Cm, 2, g))
+    up = (g.standard_normal((Rf, 2, B, B)), O.random_topology(Rf, Cm, 2, g))
+    down = (g.standard_normal((Rm, 3, B, B)), O.random_topology(Rm, Cf, 3, g))
+    x = g.standard_normal((5, dm))
+    Wg = O.block_ell_to_dense(*gate, dff, dm)
+    Wu = O.block_ell_to_dense(*up, dff, dm)
+    Wd = O.block_ell_to_dense(*down, dm, dff)
+    a, b = x @ Wg.T, x @ Wu.T
+    h = a / (1 + np.exp(-a)) * b
+    out, h2, g2, u2 = O.swiglu_fwd(x, gate, up, down, add_residual=True)
+    np.testing.assert_allclose(out, h @ Wd.T + x, atol=1e-10)
+    np.testing.assert_allclose(h2, h, atol=1e-12)
+    out0, *_ = O.swiglu_fwd(x, gate, up, down, add_residual=False)
+    np.testing.assert_allclose(out - out0, x, atol=1e-12)
+
+
+def test_rmsnorm_closed_forms():
+    x = np.full((2, 8), 3.0)
+    np.testing.assert_allclose(O.rmsnorm(x, np.ones(8), eps=0.0), np.ones((2, 8)), atol=1e-15)
+    x = np.array([[3.0, 4.0]])   # mean square 12.5
+    np.testing.assert_allclose(O.rmsnorm(x, np.array([1.0, 2.0]), eps=0.0),
+                               [[3 / math.sqrt(12.5), 8 / math.sqrt(12.5)]], rtol=1e-15)
+    x = rng(9).standard_normal((3, 16))
+    s = rng(10).standard_normal(16)
+    np.testing.assert_allclose(O.rmsnorm(10 * x, s, eps=0.0), O.rmsnorm(x, s, eps=0.0), rtol=1e-12)
+
+
+def test_looped_composition():
+    g = rng(11)
+    B, dm, dff = 4, 8, 16
+    gate = (0.1 * g.standard_normal((4, 1, B, B)), O.random_topology(4, 2, 1, g))
+    up = (0.1 * g.standard_normal((4, 1, B, B)), O.random_topology(4, 2, 1, g))
+    down = (0.1 * g.standard_normal((2, 2, B, B)), O.random_topology(2, 4, 2, g))
+    h = g.standard_normal((3, dm))
+    s = np.ones(dm)
+    np.testing.assert_array_equal(O.looped_swiglu(h, s, gate, up, down, L=0), h)
+    one = h + O.swiglu_fwd(O.rmsnorm(h, s), gate, up, down)[0]
+    np.testing.assert_allclose(O.looped_swiglu(h, s, gate, up, down, L=1), one, atol=1e-12)
+    two = one + O.swiglu_fwd(O.rmsnorm(one, s), gate, up, down)[0]
+    np.testing.assert_allclose(O.looped_swiglu(h, s, gate, up, down, L=2), two, atol=1e-12)
+
+
+# ---------------------------------------------------------------- ternary
+
+def test_ternary_quantize_hand_block():
+    # mean|w| = (0.4+0.2+0.1+0.3)/4 = 0.25 (exact in float32 via the chosen values)
+    w = np.array([0.5, -0.25, 0.125, 0.125], dtype=np.float32).reshape(1, 1, 2, 2)
+    t, s = O.ternary_quantize_blocks(w)
+    assert s[0, 0] == np.float32(0.25)
+    # w/s = 2, -1, 0.5, 0.5 -> round-half-even: 2 -> clamp 1, -1, 0, 0
+    np.testing.assert_array_equal(t.reshape(-1), [1, -1, 0, 0])
+    t0, s0 = O.ternary_quantize_blocks(np.zeros((1, 1, 2, 2), np.float32))
+    assert s0[0, 0] == np.float32(1e-8) and np.all(t0 == 0)
+
+
+def test_activation_quantize_hand_rows():
+    x = np.array([[1.0, -1.0, 0.5, 0.25],
+                  [2.0, 1.0 / 256 * 2, -3 / 256 * 2, 0.0]], dtype=np.float32)
+    q, sx = O.activation_quantize_int8(x)
+    # row 0: absmax 1, scale 128: 128 -> clamp 127, -128, 64, 32
+    np.testing.assert_array_equal(q[0], [127, -128, 64, 32])
+    # row 1: absmax 2, scale 64: 128->127, 0.5 -> 0 (half to even), -1.5 -> -2, 0
+    np.testing.assert_array_equal(q[1], [127, 0, -2, 0])
+    np.testing.assert_array_equal(sx, np.array([1.0 / 128, 2.0 / 128], np.float32))
+    qz, sz = O.activation_quantize_int8(np.zeros((1, 4), np.float32))
+    assert np.all(qz == 0) and sz[0] == np.float32(1e-8 / 128)
+
+
+def test_activation_quantize_matches_bitlinear_dequant():
+    # bonsai-test/bitlinear.py:58-69 returns x_q / scale; our (q, sx) must give q * (absmax/128)
+    x = rng(12).standard_normal((6, 32)).astype(np.float32)
+    q, sx = O.activation_quantize_int8(x)
+    absmax = np.abs(x).max(axis=1)
+    scale = np.float32(128) / absmax.astype(np.float32)
+    deq_ref = np.clip(np.rint(x * scale[:, None]), -128, 127) / scale[:, None]
+    np.testing.assert_allclose(q * sx[:, None], deq_ref, rtol=1e-6)
+
+
+def test_pack_known_words():
+    t = np.zeros((1, 1, 16, 1), dtype=np.int8)
+    t[0, 0, 0, 0] = 1      # i=0 -> bit 0, code 01
+    t[0, 0, 5, 0] = -1     # i=5 -> bit 8*1 + 2*1 = 10, code 11
+    t[0, 0, 15, 0] = 1     # i=15 -> bit 8*3 + 2*3 = 30, code 01
+    w = O.pack_ternary(t)
+    assert w.shape == (1, 1, 1, 1)
+    assert int(w[0, 0, 0, 0]) == (1 << 0) | (3 << 10) | (1 << 30)
+    # byte-extraction property used by the kernels
+    word = int(w[0, 0, 0, 0])
+    for qd in range(4):
+        b = (word >> (2 * qd)) & 0x03030303
+        for lane in range(4):
+            code = (b >> (8 * lane)) & 3
+            assert [0, 1, 0, -1][code] == t[0, 0, 4 * qd + lane, 0]
+
+
+def test_pack_round_trip_all_codes():
+    t = rng(13).integers(-1, 2, size=(3, 2, 64, 64)).astype(np.int8)
+    np.testing.assert_array_equal(O.unpack_ternary(O.pack_ternary(t)), t)
+    with pytest.raises(ValueError):
+        O.pack_ternary(np.full((1, 1, 16, 16), 2, np.int8))
+
+
+def test_partials_brute_force_and_extreme():
+    g = rng(14)
+    R, C, K, B = 2, 3, 2, 16
+    t = g.integers(-1, 2, size=(R, K, B, B)).astype(np.int8)
+    col = O.random_topology(R, C, K, g)
+    col[1, 1] = -1
+    q = g.integers(-128, 128, size=(3, C * B)).astype(np.int8)
+    P = O.ternary_block_partials(q, t, col)
+    for n in range(3):
+        for r in range(R):
+            for k in range(K):
+                for j in range(B):
+                    c = col[r, k]
+                    ref = 0 if c < 0 else sum(int(q[n, c * B + i]) * int(t[r, k, i, j]) for i in range(B))
+                    assert P[n, r, k, j] == ref
+    # extreme: all -128 against all -1 gives B*128
+    tq = -np.ones((1, 1, 64, 64), np.int8)
+    qq = np.full((1, 64), -128, np.int8)
+    assert O.ternary_block_partials(qq, tq, np.zeros((1, 1), np.int32)).max() == 64 * 128
+
+
+def test_fixed_point_scales_bounds():
+    g = rng(15)
+    for K, B in ((4, 64), (16, 64), (8, 32), (32, 16)):
+        s = np.abs(g.standard_normal((5, K))).astype(np.float32) * 0.02 + 1e-3
+        col = np.zeros((5, K), np.int32)
+        m, e = O.ternary_fixed_point(s, col, B)
+        approx = m * np.ldexp(1.0, -e)[:, None]
+        rel = np.abs(approx - s) / s.max(axis=1, keepdims=True)
+        assert rel.max() <= 2.0 ** -13
+        assert (m.max(axis=1) * K * B * 128 < 2 ** 31).all()
+
+
+def test_ternary_matmul_dense_equivalence():
+    g = rng(16)
+    R, C, K, B = 3, 4, 2, 16
+    t = g.integers(-1, 2, size=(R, K, B, B)).astype(np.int8)
+    s = (np.abs(g.standard_normal((R, K))) * 0.02 + 0.01).astype(np.float32)
+    col = O.random_topology(R, C, K, g)
+    x = g.standard_normal((4, C * B)).astype(np.float32)
+    q, sq = O.activation_quantize_int8(x)
+    y, _ = O.ternary_matmul(q, sq, t, s, col, exact_scales=True)
+    W = O.block_ell_to_dense(t.astype(np.float64) * s[:, :, None, None], col, R * B, C * B)
+    np.testing.assert_allclose(y, (q.astype(np.float64) * sq[:, None]) @ W.T, rtol=1e-12, atol=1e-12)
+    yf, acc = O.ternary_matmul(q, sq, t, s, col, exact_scales=False)
+    assert np.abs(yf - y).max() <= 2.0 ** -12 * np.abs(y).max()
+
+
+# ---------------------------------------------------------------- planted mistakes
+
+def test_planted_transposed_tile_is_caught():
+    g = rng(17)
+    values = g.standard_normal((3, 2, 8, 8))
+    col = O.random_topology(3, 4, 2, g)
+    x = g.standard_normal((4, 32))
+    wrong = O.block_ell_matmul(x, values.transpose(0, 1, 3, 2), col)
+    W = O.block_ell_to_dense(values, col, 24, 32)
+    assert np.abs(wrong - x @ W.T).max() > 1e-3
+
+
+def test_planted_dropped_block_is_caught():
+    g = rng(18)
+    values = g.standard_normal((3, 2, 8, 8))
+    col = O.random_topology(3, 4, 2, g)
+    x = g.standard_normal((4, 32))
+    c2 = col.copy()
+    c2[0, 1] = -1
+    assert np.abs(O.block_ell_matmul(x, values, c2) - brute_matmul(x, values, col)).max() > 1e-3
+
+
+def test_planted_round_half_away_is_caught():
+    x = np.array([[2.0, 0.5 / 64.0, 2.5 / 64.0]], dtype=np.float32)
+    q, _ = O.activation_quantize_int8(x)            # scale 64: 0.5 -> 0 and 2.5 -> 2
+    np.testing.assert_array_equal(q[0, 1:], [0, 2])
+    away = np.sign(x * 64) * np.floor(np.abs(x * 64) + 0.5)
+    assert not np.array_equal(q[0, 1:], away[0, 1:].astype(np.int8))
+
+
+def test_bf16_round():
+    a = np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -2.5, 3.14159], np.float32)
+    r = O.bf16_round(a)
+    np.testing.assert_array_equal(r[:4], np.array([1.0, 1.0, 1.0 + 2 ** -6, -2.5], np.float32))
+    assert abs(r[4] - 3.140625) < 1e-7
