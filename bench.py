@@ -1,0 +1,321 @@
+#!/usr/bin/env python3
+"""Benchmark of the Block-ELL SwiGLU FFN forward on one MI355X.
+
+Headline (one JSON line on stdout): the bf16 Block-ELL SwiGLU FFN at
+d_model=1024, d_ff=4096, B=32, 25% density, 16384 tokens — effective TFLOP/s
+over nonzero blocks (plus tokens/s), inputs resident in HBM, one step = one
+forward pass.  The line also carries:
+  roofline      the dominant kernel's achieved vs peak, timed with HIP events
+                on the stream the kernel runs on;
+  cpu_baseline  the CPU oracle (numpy gather + matmul restatement of the
+                reference layer) timed on the host cores on the same workload;
+  extra         the other workloads (ternary FFN, looped block L=8, decode).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only-main]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "looped-blockell-tpu_amd")
+for _p in (ROOT, PKG_DIR):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "effective TFLOP/s (nonzero blocks) + tokens/s, Block-ELL SwiGLU FFN"
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_INT8_TOPS = 5000.0       # MI355X dense int8 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+
+WORKLOADS = {
+    "bf16": dict(d_model=1024, d_ff=4096, B=32, density=0.25, N=16384, seed=1002),
+    "ternary": dict(d_model=2048, d_ff=8192, B=64, density=0.125, N=8192, seed=1003),
+    "looped": dict(d_model=1024, d_ff=4096, B=32, density=0.25, N=32 * 512, L=8, seed=1004),
+    "decode": dict(d_model=4096, d_ff=14336, B=64, density=0.10, N=16, seed=1005, copies=12),
+}
+
+
+def geometry(w):
+    B = w["B"]
+    Cm, Cf = w["d_model"] // B, w["d_ff"] // B
+    Kg = max(1, int(Cm * w["density"]))
+    Kd = max(1, int(Cf * w["density"]))
+    Rf, Rm = w["d_ff"] // B, w["d_model"] // B
+    return Rf, Rm, Cm, Cf, Kg, Kd
+
+
+def nonzero_flops(w):
+    Rf, Rm, _, _, Kg, Kd = geometry(w)
+    B = w["B"]
+    return 2.0 * w["N"] * B * B * (Rf * 2 * Kg + Rm * Kd) * w.get("L", 1)
+
+
+def algorithmic_bytes(w, ternary=False):
+    """Weights + indices (+ scales) + input read once + output written once; h excluded."""
+    Rf, Rm, _, _, Kg, Kd = geometry(w)
+    B = w["B"]
+    blocks = Rf * 2 * Kg + Rm * Kd
+    if ternary:
+        return blocks * (B * B // 4 + 4 + 4) + w["N"] * w["d_model"] * (1 + 2) + w["N"] * 4
+    return blocks * (B * B * 2 + 4) + w["N"] * w["d_model"] * 2 * 2
+
+
+# ---------------------------------------------------------------------------------------------
+
+def make_bell(R, C, K, B, gen, device, std=0.02):
+    import torch
+    vals = (torch.randn(R, K, B, B, generator=gen, device=device) * std).to(torch.bfloat16)
+    cols = torch.argsort(torch.rand(R, C, generator=gen, device=device), dim=1)[:, :K].to(torch.int32).contiguous()
+    return vals, cols
+
+
+def make_ffn(w, device, gen):
+    Rf, Rm, Cm, Cf, Kg, Kd = geometry(w)
+    B = w["B"]
+    g = make_bell(Rf, Cm, Kg, B, gen, device)
+    u = make_bell(Rf, Cm, Kg, B, gen, device)
+    d = make_bell(Rm, Cf, Kd, B, gen, device)
+    return g, u, d
+
+
+def make_ternary(R, C, K, B, gen, device):
+    import torch
+    from looped_blockell import kernels
+    t = torch.randint(-1, 2, (R, K, B, B), generator=gen, device=device, dtype=torch.int8)
+    lat = torch.randn(R, K, B * B, generator=gen, device=device) * 0.02
+    s = lat.abs().mean(dim=2).clamp_min(1e-8).float().contiguous()
+    cols = torch.argsort(torch.rand(R, C, generator=gen, device=device), dim=1)[:, :K].to(torch.int32).contiguous()
+    return kernels.pack_ternary(t), s, cols
+
+
+def time_steps(step, steps, warmup):
+    """Run `warmup` untimed steps, then exactly `steps` timed ones.
+
+    Returns (ms_per_step from the host clock between two synchronisations,
+    list of per-launch durations from HIP events on the current stream).
+    """
+    import torch
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        step(i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    per = [a.elapsed_time(b) for a, b in ev]
+    return wall_ms / steps, per
+
+
+def median(xs):
+    s = sorted(xs)
+    n = len(s)
+    return s[n // 2] if n % 2 else 0.5 * (s[n // 2 - 1] + s[n // 2])
+
+
+# ---------------------------------------------------------------------------------------------
+
+def bench_bf16(steps, warmup, device):
+    import torch
+    from looped_blockell import kernels
+    w = WORKLOADS["bf16"]
+    gen = torch.Generator(device=device).manual_seed(w["seed"])
+    g, u, d = make_ffn(w, device, gen)
+    x = torch.randn(w["N"], w["d_model"], generator=gen, device=device).to(torch.bfloat16)
+    args = (*g, *u, *d)
+    out = {}
+
+    def step(i):
+        out["y"] = kernels.swiglu_fwd(x, *args, add_residual=False)
+
+    ms, per = time_steps(step, steps, warmup)
+    flops = nonzero_flops(w)
+    kern_ms = sum(per) / len(per)
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    res = dict(
+        ms_per_step=ms, value=flops / (ms * 1e-3) / 1e12, tokens_per_s=w["N"] / (ms * 1e-3),
+        kernel_ms_avg=kern_ms, kernel_ms_median=median(per),
+        roofline=dict(bound="mfma", achieved=achieved, peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
+                      frac=achieved / PEAK_BF16_TFLOPS, traffic=None,
+                      kernel="panel_kernel<32,8,false> (fused gate/up + SiLU*mul + down, one launch per step)",
+                      algorithmic_flops_per_launch=flops,
+                      algorithmic_bytes_per_launch=algorithmic_bytes(w)),
+    )
+    assert torch.isfinite(out["y"].float()).all()
+    return res
+
+
+def bench_ternary(steps, warmup, device):
+    import torch
+    from looped_blockell import kernels
+    w = WORKLOADS["ternary"]
+    gen = torch.Generator(device=device).manual_seed(w["seed"])
+    Rf, Rm, Cm, Cf, Kg, Kd = geometry(w)
+    B = w["B"]
+    g = make_ternary(Rf, Cm, Kg, B, gen, device)
+    u = make_ternary(Rf, Cm, Kg, B, gen, device)
+    d = make_ternary(Rm, Cf, Kd, B, gen, device)
+    x = torch.randn(w["N"], w["d_model"], generator=gen, device=device).to(torch.bfloat16)
+    xq, sx = kernels.quantize_act_int8(x)
+
+    def step(i):
+        kernels.ternary_swiglu_fwd(xq, sx, g, u, d)
+
+    ms, per = time_steps(step, steps, warmup)
+    ops = nonzero_flops(w)
+    tops = ops / (ms * 1e-3) / 1e12
+    return dict(workload="ternary 2-bit weights / int8 activations SwiGLU FFN, d_model=2048 d_ff=8192 B=64 "
+                         "density=0.125 N=8192 (forward from xq, sx)",
+                ms_per_step=ms, value=tops, unit="TOP/s", tokens_per_s=w["N"] / (ms * 1e-3),
+                frac_of_int8_peak=tops / PEAK_INT8_TOPS, algorithmic_ops=ops,
+                algorithmic_bytes=algorithmic_bytes(w, ternary=True))
+
+
+def bench_looped(steps, warmup, device):
+    import torch
+    from looped_blockell import kernels
+    w = WORKLOADS["looped"]
+    gen = torch.Generator(device=device).manual_seed(w["seed"])
+    g, u, d = make_ffn(w, device, gen)
+    h = torch.randn(w["N"], w["d_model"], generator=gen, device=device).to(torch.bfloat16)
+    scale = torch.ones(w["d_model"], device=device)
+
+    def step(i):
+        kernels.looped_swiglu(h, scale, *g, *u, *d, L=w["L"], eps=1e-5)
+
+    ms, per = time_steps(step, steps, warmup)
+    flops = nonzero_flops(w)
+    tf = flops / (ms * 1e-3) / 1e12
+    return dict(workload="looped RMSNorm -> SwiGLU -> residual, L=8 shared weights, d_model=1024 d_ff=4096 B=32 "
+                         "density=0.25 N=32x512 (one persistent launch)",
+                ms_per_step=ms, value=tf, unit="TFLOP/s", tokens_per_s=w["N"] / (ms * 1e-3),
+                token_iterations_per_s=w["N"] * w["L"] / (ms * 1e-3), frac_of_bf16_peak=tf / PEAK_BF16_TFLOPS,
+                kernel_ms_avg=sum(per) / len(per))
+
+
+def bench_decode(steps, warmup, device):
+    import torch
+    from looped_blockell import kernels
+    w = WORKLOADS["decode"]
+    gen = torch.Generator(device=device).manual_seed(w["seed"])
+    copies = [make_ffn(w, device, gen) for _ in range(w["copies"])]   # > 256 MB: defeats the MALL
+    x = torch.randn(w["N"], w["d_model"], generator=gen, device=device).to(torch.bfloat16)
+
+    def step(i):
+        g, u, d = copies[i % len(copies)]
+        kernels.swiglu_fwd(x, *g, *u, *d, add_residual=False)
+
+    ms, per = time_steps(step, steps, warmup)
+    byts = algorithmic_bytes(w)
+    gbs = byts / (ms * 1e-3) / 1e9
+    return dict(workload="decode SwiGLU FFN, 16 tokens, d_model=4096 d_ff=14336 B=64 density=0.10, "
+                         f"{w['copies']} rotating weight copies",
+                ms_per_step=ms, value=gbs, unit="GB/s", frac_of_hbm_peak=gbs / PEAK_HBM_GBS,
+                tflops=nonzero_flops(w) / (ms * 1e-3) / 1e12, algorithmic_bytes=byts,
+                kernel_ms_avg=sum(per) / len(per))
+
+
+def cpu_baseline():
+    """The oracle (numpy, float32) on the headline workload's full token count."""
+    import numpy as np
+    from oracle import oracle as O
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        threads = len(os.sched_getaffinity(0))
+    w = WORKLOADS["bf16"]
+    Rf, Rm, Cm, Cf, Kg, Kd = geometry(w)
+    B = w["B"]
+    rng = np.random.default_rng(w["seed"])
+
+    def bw(R, C, K):
+        return (rng.standard_normal((R, K, B, B)) * 0.02).astype(np.float32), O.random_topology(R, C, K, rng)
+
+    g, u, d = bw(Rf, Cm, Kg), bw(Rf, Cm, Kg), bw(Rm, Cf, Kd)
+    n = w["N"]
+    x = rng.standard_normal((n, w["d_model"])).astype(np.float32)
+    O.swiglu_fwd(x[:256], g, u, d)  # warm-up
+    t0 = time.perf_counter()
+    O.swiglu_fwd(x, g, u, d)
+    dt = time.perf_counter() - t0
+    flops = nonzero_flops(dict(w, N=n))
+    return dict(value=flops / dt / 1e12, unit="TFLOP/s", tokens_per_s=n / dt, seconds=dt, cores=threads,
+                kind="port",
+                sample=f"headline workload, all {n} tokens, float32 numpy oracle "
+                       "(gather + batched matmul restatement of the reference layer)")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only-main", action="store_true", help="headline workload only (for profiling)")
+    ap.add_argument("--only", default="", help="comma list of extra workloads to run: ternary,looped,decode")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (the Block-ELL FFN path is single-GPU; "
+              "no multi-GPU figure is produced). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from looped_blockell import kernels
+    kernels.ops()
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+
+    main_res = bench_bf16(args.steps, args.warmup, device)
+    extra = {}
+    if not args.only_main:
+        todo = [s for s in args.only.split(",") if s] or ["ternary", "looped", "decode"]
+        fns = dict(ternary=bench_ternary, looped=bench_looped, decode=bench_decode)
+        for name in todo:
+            st = max(5, args.steps // (4 if name == "looped" else 1))
+            try:
+                extra[name] = fns[name](st, max(2, args.warmup), device)
+            except Exception as e:  # report, keep the headline line
+                extra[name] = dict(error=f"{type(e).__name__}: {e}")
+    cpu = None
+    if not args.no_cpu and not args.only_main:
+        cpu = cpu_baseline()
+
+    w = WORKLOADS["bf16"]
+    line = {
+        "metric": METRIC,
+        "value": main_res["value"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": main_res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random N(0,0.02) weights, random per-row topology, x ~ N(0,1))",
+        "config": {"workload": "bf16 Block-ELL SwiGLU FFN forward, d_model=1024 d_ff=4096 B=32 density=0.25 "
+                               "N=16384 tokens",
+                   "d_model": w["d_model"], "d_ff": w["d_ff"], "B": w["B"], "density": w["density"],
+                   "tokens": w["N"], "parallelism": "single GPU"},
+        "tokens_per_s": main_res["tokens_per_s"],
+        "kernel_ms_avg": main_res["kernel_ms_avg"],
+        "roofline": main_res["roofline"],
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,197 @@
+/*
+ * lbk.h — C ABI of the MI355X (gfx950) Block-ELL SwiGLU FFN library (liblbk.so).
+ *
+ * Everything here is plain C: pointers, sizes, status codes.  No torch types.
+ * The library never allocates, frees or synchronises: callers own every buffer
+ * (inputs, outputs, workspace) and pass the HIP stream the work is queued on.
+ * Entry points are reentrant and keep no global state; a workspace buffer may
+ * be shared by calls only if those calls do not overlap in time.
+ *
+ * Block-ELL layout (reference looped_blockell/layers/block_ell.py:1-8, :53-66):
+ *   values      [R, K, B, B]  bf16; tile values[r, k] is [B_in, B_out]
+ *   col_idx     [R, K]        int32; input column block of each tile,
+ *                             -1 = dead slot, skipped
+ *                             (reference looped_blockell/opt/cms.py:229-230)
+ *   B in {16, 32, 64}; the weight maps in = C*B features to out = R*B features.
+ * Activations are row-major [N, features] bf16 with a row stride in elements.
+ * bf16 values travel as uint16_t bit patterns.
+ */
+#ifndef LBK_H
+#define LBK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LBK_VERSION 1
+
+/* Status codes (never exceptions across the ABI). */
+enum {
+    LBK_OK = 0,
+    LBK_ERR_NULL = 1,          /* a required pointer is NULL */
+    LBK_ERR_TILE = 2,          /* B not in {16, 32, 64} (or ternary B not a multiple of 16) */
+    LBK_ERR_SHAPE = 3,         /* inconsistent R / K / features between operands */
+    LBK_ERR_ALIGN = 4,         /* pointer or row stride not 16-byte aligned */
+    LBK_ERR_WORKSPACE = 5,     /* workspace missing or smaller than required */
+    LBK_ERR_LAUNCH = 6,        /* HIP reported an error launching a kernel */
+    LBK_ERR_ARG = 7,           /* other invalid argument (N < 0, L < 0, eps < 0 ...) */
+    LBK_ERR_COLUMN = 8         /* reserved: column index >= C found by lbk_check_columns */
+};
+
+/* One Block-ELL weight with bf16 tiles. */
+typedef struct lbk_bell {
+    const uint16_t* values;    /* [R, K, B, B] bf16, tile [B_in, B_out], contiguous */
+    const int32_t* col_idx;    /* [R, K] int32, -1 = dead slot */
+    int32_t R, K, B;
+} lbk_bell;
+
+/* One ternary Block-ELL weight (format defined by this library):
+ *   packed [R, K, B_out, B_in/16] uint32 — word (r,k,D,e) holds t[r,k,16e+i,D],
+ *          i = 0..15, as a 2-bit code at bit 8*(i%4) + 2*(i/4);
+ *          code 0b00 -> 0, 0b01 -> +1, 0b11 -> -1 (0b10 decodes to 0);
+ *   scales [R, K] fp32 — one absmean scale per block. */
+typedef struct lbk_bell_ternary {
+    const uint32_t* packed;
+    const float* scales;
+    const int32_t* col_idx;
+    int32_t R, K, B;
+} lbk_bell_ternary;
+
+/* Human-readable text of a status code (static storage). */
+const char* lbk_status_string(int status);
+int lbk_version(void);
+
+/*
+ * Validate that every column index lies in [-1, C).  Writes the number of
+ * offending entries to *bad_count_dev (device int32, zeroed by this call).
+ * Replaces nothing in the reference (the reference CUDA op does not check
+ * columns, csrc/block_ell/swiglu_fwd.cu:236-256); used by the torch layer's
+ * debug checks.
+ */
+int lbk_check_columns(const int32_t* col_idx, int64_t count, int32_t C, int32_t* bad_count_dev,
+                      void* stream);
+
+/*
+ * y[N, R*B] = x[N, C*B] (Block-ELL) W   (+ bias[R*B] if bias != NULL)
+ * Replaces block_ell_matmul (reference looped_blockell/layers/block_ell.py:149-182)
+ * plus BlockELLLinear's bias (reference looped_blockell/layers/mlp.py:82).
+ */
+int lbk_block_ell_matmul_bf16(const uint16_t* x, int64_t N, int32_t in_features, int64_t ldx,
+                              const lbk_bell* w, const float* bias, uint16_t* y, int64_t ldy,
+                              void* stream);
+
+/*
+ * Workspace bytes needed by lbk_swiglu_fwd_bf16 for this geometry (0 when the
+ * fused single-kernel path applies and no intermediates are requested).
+ */
+size_t lbk_swiglu_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate,
+                                  const lbk_bell* up, const lbk_bell* down, int want_intermediates);
+
+/*
+ * out[N, d_model] = W_down( silu(W_gate x) * (W_up x) )  (+ x if add_residual)
+ * Optional outputs (NULL to skip; all [N, d_ff] bf16, row stride d_ff):
+ *   h_out = silu(gate)*up, gate_pre_out = W_gate x, up_out = W_up x.
+ * Replaces titan::block_ell_swiglu_fwd and ..._with_intermediate
+ * (reference csrc/block_ell/block_ell_ops.cpp:51-76, csrc/block_ell/swiglu_fwd.cuh:75-141).
+ * x and out are contiguous [N, d_model].
+ */
+int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model,
+                        const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                        int add_residual, uint16_t* out,
+                        uint16_t* h_out, uint16_t* gate_pre_out, uint16_t* up_out,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * out = x / sqrt(mean(x^2) + eps) * scale, rows of length d (bf16 in/out, fp32 math).
+ * Replaces rmsnorm_cuda (reference csrc/loop/persistent_core.cuh:76-92) with the
+ * layer-API semantics of looped_blockell/layers/norms.py:14-15.
+ */
+int lbk_rmsnorm_bf16(const uint16_t* x, int64_t N, int32_t d, const float* scale, float eps,
+                     uint16_t* out, void* stream);
+
+/*
+ * h_out = h + e-injection: decay*h + dt*e with dt = softplus(log_dt),
+ * decay = exp(-dt*exp(log_A)).  Replaces diagonal_injection_cuda
+ * (reference csrc/loop/persistent_core.cuh:58-73, interop/pt_model.py:923-935).
+ * h_out may alias h.
+ */
+int lbk_diagonal_injection_bf16(const uint16_t* h, const uint16_t* e, const float* log_A,
+                                const float* log_dt, int64_t N, int32_t d, uint16_t* h_out,
+                                void* stream);
+
+/*
+ * Looped pre-norm FFN block with shared weights, applied L times:
+ *   h <- h + SwiGLU(RMSNorm(h; norm_scale, eps))
+ * h_in, h_out: [N, d_model] bf16 (may alias).  The carried state stays in fp32
+ * inside the persistent kernel; h_out is rounded to bf16 once at the end.
+ * Replaces the MLP loop of persistent_mlp_step (reference csrc/loop/persistent_core.cu:315-335,
+ * schema csrc/loop/loop_ops.cpp:52-66) and the L-fold application of the
+ * core block (reference looped_blockell/looping/looped_model.py:293-350).
+ */
+size_t lbk_looped_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate,
+                                  const lbk_bell* up, const lbk_bell* down);
+int lbk_looped_swiglu_bf16(const uint16_t* h_in, int64_t N, int32_t d_model,
+                           const float* norm_scale, float eps, int32_t L,
+                           const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                           uint16_t* h_out, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/*
+ * Per-token absmax int8 quantisation of bf16 activations:
+ *   absmax = max(max|x|, 1e-8); q = clamp(rint(x * (128/absmax)), -128, 127);
+ *   sx = absmax / 128 (the dequantisation multiplier).
+ * Restates activation_quantize (reference bonsai-test/bitlinear.py:58-69) in
+ * integer form.  x row stride ldx elements; xq contiguous [N, F].
+ */
+int lbk_quantize_act_int8(const uint16_t* x, int64_t N, int32_t F, int64_t ldx, int8_t* xq,
+                          float* sx, void* stream);
+
+/*
+ * Pack ternary tiles t[R, K, B, B] int8 in {-1,0,+1} ([B_in, B_out]) into the
+ * 2-bit format of lbk_bell_ternary.packed.  Device to device.
+ */
+int lbk_pack_ternary(const int8_t* t, int32_t R, int32_t K, int32_t B, uint32_t* packed,
+                     void* stream);
+
+/*
+ * Per-block absmean ternary quantisation of latent weights values[R,K,B,B]
+ * (bf16): s = max(mean|w|, 1e-8), t = clamp(rint(w/s), -1, 1), written packed.
+ * Restates ternary_quantize (reference bonsai-test/bitlinear.py:34-55) with
+ * the group = one B x B block.
+ */
+int lbk_ternary_quantize_weights_bf16(const uint16_t* values, int32_t R, int32_t K, int32_t B,
+                                      uint32_t* packed, float* scales, void* stream);
+
+/*
+ * Ternary Block-ELL product: y[n, r*B+j] = sx[n] * sum_k s[r,k] * P[n,r,k,j],
+ * P = int32 block partial of xq against the ternary tile.  y bf16 [N, R*B].
+ * If partials != NULL the kernel also stores every P as int32 [N, R, K, B]
+ * (dead slots store 0) — the exact integer accumulators before scaling.
+ */
+int lbk_ternary_matmul(const int8_t* xq, const float* sx, int64_t N, int32_t in_features,
+                       const lbk_bell_ternary* w, uint16_t* y, int32_t* partials, void* stream);
+
+/*
+ * Ternary SwiGLU FFN on int8 activations (xq, sx from lbk_quantize_act_int8):
+ *   g, u = ternary gate/up products; h = silu(g) * u (stored bf16);
+ *   (hq, sh) = per-token int8 re-quantisation of h over d_ff;
+ *   out = ternary down product of (hq, sh)  (+ x_resid if not NULL), bf16.
+ * Optional outputs: h_out [N, d_ff] bf16, hq_out [N, d_ff] int8, sh_out [N] fp32.
+ * The workspace (see lbk_ternary_swiglu_workspace_bytes) holds h, hq and sh
+ * when the optional outputs are not given.
+ */
+size_t lbk_ternary_swiglu_workspace_bytes(int64_t N, const lbk_bell_ternary* gate);
+int lbk_swiglu_fwd_ternary(const int8_t* xq, const float* sx, int64_t N, int32_t d_model,
+                           const lbk_bell_ternary* gate, const lbk_bell_ternary* up,
+                           const lbk_bell_ternary* down, const uint16_t* x_resid,
+                           uint16_t* out, uint16_t* h_out, int8_t* hq_out, float* sh_out,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LBK_H */

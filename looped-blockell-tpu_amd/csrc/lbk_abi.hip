@@ -1,0 +1,323 @@
+// lbk_abi.hip — the extern "C" entry points declared in include/lbk.h.
+//
+// Each entry point validates its arguments on the host (pointers, tile size,
+// shape consistency, alignment), chooses a kernel path and queues the kernels
+// on the caller's stream.  Nothing is allocated, freed or synchronised here.
+#include "lbk.h"
+#include "lbk_internal.h"
+
+#include <string.h>
+
+using namespace lbk;
+
+namespace {
+
+inline bool a16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool a8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+inline bool tile_ok(int B) { return B == 16 || B == 32 || B == 64; }
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+int check_bell(const lbk_bell* w) {
+  if (!w) return LBK_ERR_NULL;
+  if (!tile_ok(w->B)) return LBK_ERR_TILE;
+  if (w->R < 0 || w->K < 0) return LBK_ERR_SHAPE;
+  if ((int64_t)w->R * w->K > 0 && (!w->values || !w->col_idx)) return LBK_ERR_NULL;
+  if (w->values && !a8(w->values)) return LBK_ERR_ALIGN;
+  return LBK_OK;
+}
+
+int check_tern(const lbk_bell_ternary* w) {
+  if (!w) return LBK_ERR_NULL;
+  if (!tile_ok(w->B)) return LBK_ERR_TILE;
+  if (w->R < 0 || w->K < 0) return LBK_ERR_SHAPE;
+  if ((int64_t)w->R * w->K > 0 && (!w->packed || !w->scales || !w->col_idx)) return LBK_ERR_NULL;
+  if (w->packed && !a16(w->packed)) return LBK_ERR_ALIGN;
+  return LBK_OK;
+}
+
+// Shared geometry check of a gate/up/down triple; returns status, fills d_ff.
+template <typename W>
+int check_ffn(const W* gate, const W* up, const W* down, int32_t d_model, int64_t* d_ff) {
+  if (gate->R != up->R) return LBK_ERR_SHAPE;
+  if (gate->B != up->B || gate->B != down->B) return LBK_ERR_TILE;
+  const int B = gate->B;
+  if (d_model <= 0 || d_model % B) return LBK_ERR_SHAPE;
+  if ((int64_t)down->R * B != d_model) return LBK_ERR_SHAPE;
+  *d_ff = (int64_t)gate->R * B;
+  return LBK_OK;
+}
+
+int swiglu_general(const uint16_t* x, int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
+                   const lbk_bell* down, const uint16_t* resid, uint16_t* out, uint16_t* h,
+                   uint16_t* gate_pre, uint16_t* up_out, hipStream_t st) {
+  const int B = gate->B;
+  const int64_t d_ff = (int64_t)gate->R * B;
+  RowblockLaunch a{};
+  a.x = x; a.N = N; a.ldx = d_model; a.C = d_model / B; a.R = gate->R;
+  a.v0 = gate->values; a.c0 = gate->col_idx; a.K0 = gate->K;
+  a.v1 = up->values; a.c1 = up->col_idx; a.K1 = up->K;
+  a.y = h; a.ldy = d_ff; a.aux0 = gate_pre; a.aux1 = up_out; a.ldaux = d_ff;
+  if (launch_rowblock(B, 1, a, st) != 0) return LBK_ERR_LAUNCH;
+  RowblockLaunch d{};
+  d.x = h; d.N = N; d.ldx = d_ff; d.C = gate->R; d.R = down->R;
+  d.v0 = down->values; d.c0 = down->col_idx; d.K0 = down->K;
+  d.resid = resid; d.ldr = d_model;
+  d.y = out; d.ldy = d_model;
+  if (launch_rowblock(B, 2, d, st) != 0) return LBK_ERR_LAUNCH;
+  return LBK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* lbk_status_string(int s) {
+  switch (s) {
+    case LBK_OK: return "ok";
+    case LBK_ERR_NULL: return "a required pointer is NULL";
+    case LBK_ERR_TILE: return "tile size B must be 16, 32 or 64 (and equal across gate/up/down)";
+    case LBK_ERR_SHAPE: return "inconsistent shapes between operands";
+    case LBK_ERR_ALIGN: return "pointer or row stride not suitably aligned (16 bytes for activations)";
+    case LBK_ERR_WORKSPACE: return "workspace missing or too small";
+    case LBK_ERR_LAUNCH: return "HIP kernel launch failed";
+    case LBK_ERR_ARG: return "invalid argument";
+    case LBK_ERR_COLUMN: return "column index out of range";
+    default: return "unknown status";
+  }
+}
+
+int lbk_version(void) { return LBK_VERSION; }
+
+int lbk_check_columns(const int32_t* col_idx, int64_t count, int32_t C, int32_t* bad_count_dev, void* stream) {
+  if (!bad_count_dev || (count > 0 && !col_idx)) return LBK_ERR_NULL;
+  if (count < 0 || C < 0) return LBK_ERR_ARG;
+  return launch_check_columns(col_idx, count, C, bad_count_dev, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+int lbk_block_ell_matmul_bf16(const uint16_t* x, int64_t N, int32_t in_features, int64_t ldx, const lbk_bell* w,
+                              const float* bias, uint16_t* y, int64_t ldy, void* stream) {
+  int st = check_bell(w);
+  if (st) return st;
+  if (N < 0) return LBK_ERR_ARG;
+  if (in_features <= 0 || in_features % w->B) return LBK_ERR_SHAPE;
+  if (N == 0) return LBK_OK;
+  if (!x || !y) return LBK_ERR_NULL;
+  if (ldx < in_features || ldy < (int64_t)w->R * w->B) return LBK_ERR_SHAPE;
+  if (!a16(x) || (ldx % 8) || !a16(y) || (ldy % 8)) return LBK_ERR_ALIGN;
+  RowblockLaunch a{};
+  a.x = x; a.N = N; a.ldx = ldx; a.C = in_features / w->B; a.R = w->R;
+  a.v0 = w->values; a.c0 = w->col_idx; a.K0 = w->K;
+  a.bias = bias; a.y = y; a.ldy = ldy;
+  return launch_rowblock(w->B, 0, a, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+static bool use_panel(const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, int32_t d_model) {
+  (void)up;
+  return panel_supported(gate->B, d_model, gate->R, down->R, down->K);
+}
+
+size_t lbk_swiglu_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
+                                  const lbk_bell* down, int want_intermediates) {
+  if (!gate || !up || !down || N <= 0) return 0;
+  if (want_intermediates) return 0;  // h goes to the caller's h_out
+  if (use_panel(gate, up, down, d_model)) return 0;
+  return align256((size_t)N * gate->R * gate->B * 2);
+}
+
+int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
+                        const lbk_bell* down, int add_residual, uint16_t* out, uint16_t* h_out,
+                        uint16_t* gate_pre_out, uint16_t* up_out, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  int st;
+  if ((st = check_bell(gate)) || (st = check_bell(up)) || (st = check_bell(down))) return st;
+  int64_t d_ff = 0;
+  if ((st = check_ffn(gate, up, down, d_model, &d_ff))) return st;
+  if (N < 0) return LBK_ERR_ARG;
+  if (N == 0) return LBK_OK;
+  if (!x || !out) return LBK_ERR_NULL;
+  if (!a16(x) || !a16(out) || (d_model % 8)) return LBK_ERR_ALIGN;
+  for (const void* p : {(const void*)h_out, (const void*)gate_pre_out, (const void*)up_out})
+    if (p && !a16(p)) return LBK_ERR_ALIGN;
+  const bool inter = h_out || gate_pre_out || up_out;
+  if (!inter && use_panel(gate, up, down, d_model)) {
+    PanelArgs p{};
+    p.x = x; p.N = N; p.d_model = d_model;
+    p.vg = gate->values; p.cg = gate->col_idx; p.Kg = gate->K;
+    p.vu = up->values; p.cu = up->col_idx; p.Ku = up->K;
+    p.R_ff = gate->R;
+    p.vd = down->values; p.cd = down->col_idx; p.Kd = down->K;
+    p.R_m = down->R;
+    p.add_residual = add_residual ? 1 : 0;
+    p.L = 1; p.eps = 0.f; p.norm_scale = nullptr;
+    p.out = out;
+    return launch_panel(gate->B, false, p, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+  }
+  uint16_t* h = h_out;
+  if (!h) {
+    const size_t need = align256((size_t)N * d_ff * 2);
+    if (!workspace || workspace_bytes < need) return LBK_ERR_WORKSPACE;
+    if (!a16(workspace)) return LBK_ERR_ALIGN;
+    h = static_cast<uint16_t*>(workspace);
+  }
+  return swiglu_general(x, N, d_model, gate, up, down, add_residual ? x : nullptr, out, h, gate_pre_out, up_out,
+                        S(stream));
+}
+
+int lbk_rmsnorm_bf16(const uint16_t* x, int64_t N, int32_t d, const float* scale, float eps, uint16_t* out,
+                     void* stream) {
+  if (N < 0 || d <= 0 || !(eps >= 0.f)) return LBK_ERR_ARG;
+  if (N == 0) return LBK_OK;
+  if (!x || !scale || !out) return LBK_ERR_NULL;
+  return launch_rmsnorm(x, N, d, scale, eps, out, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+int lbk_diagonal_injection_bf16(const uint16_t* h, const uint16_t* e, const float* log_A, const float* log_dt,
+                                int64_t N, int32_t d, uint16_t* h_out, void* stream) {
+  if (N < 0 || d <= 0) return LBK_ERR_ARG;
+  if (N == 0) return LBK_OK;
+  if (!h || !e || !log_A || !log_dt || !h_out) return LBK_ERR_NULL;
+  return launch_injection(h, e, log_A, log_dt, N, d, h_out, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+size_t lbk_looped_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
+                                  const lbk_bell* down) {
+  if (!gate || !up || !down || N <= 0) return 0;
+  if (use_panel(gate, up, down, d_model)) return 0;
+  return align256((size_t)N * d_model * 2) + align256((size_t)N * gate->R * gate->B * 2);
+}
+
+int lbk_looped_swiglu_bf16(const uint16_t* h_in, int64_t N, int32_t d_model, const float* norm_scale, float eps,
+                           int32_t L, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                           uint16_t* h_out, void* workspace, size_t workspace_bytes, void* stream) {
+  int st;
+  if ((st = check_bell(gate)) || (st = check_bell(up)) || (st = check_bell(down))) return st;
+  int64_t d_ff = 0;
+  if ((st = check_ffn(gate, up, down, d_model, &d_ff))) return st;
+  if (N < 0 || L < 0 || !(eps >= 0.f)) return LBK_ERR_ARG;
+  if (N == 0) return LBK_OK;
+  if (!h_in || !h_out || !norm_scale) return LBK_ERR_NULL;
+  if (!a16(h_in) || !a16(h_out) || (d_model % 8)) return LBK_ERR_ALIGN;
+  hipStream_t s = S(stream);
+  if (L == 0) {
+    if (h_out != h_in &&
+        hipMemcpyAsync(h_out, h_in, (size_t)N * d_model * 2, hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return LBK_ERR_LAUNCH;
+    return LBK_OK;
+  }
+  if (use_panel(gate, up, down, d_model)) {
+    PanelArgs p{};
+    p.x = h_in; p.N = N; p.d_model = d_model;
+    p.vg = gate->values; p.cg = gate->col_idx; p.Kg = gate->K;
+    p.vu = up->values; p.cu = up->col_idx; p.Ku = up->K;
+    p.R_ff = gate->R;
+    p.vd = down->values; p.cd = down->col_idx; p.Kd = down->K;
+    p.R_m = down->R;
+    p.add_residual = 1;
+    p.norm_scale = norm_scale; p.eps = eps; p.L = L;
+    p.out = h_out;
+    return launch_panel(gate->B, true, p, s) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+  }
+  const size_t nbytes = align256((size_t)N * d_model * 2), hbytes = align256((size_t)N * d_ff * 2);
+  if (!workspace || workspace_bytes < nbytes + hbytes) return LBK_ERR_WORKSPACE;
+  if (!a16(workspace)) return LBK_ERR_ALIGN;
+  uint16_t* normed = static_cast<uint16_t*>(workspace);
+  uint16_t* h = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + nbytes);
+  const uint16_t* cur = h_in;
+  for (int l = 0; l < L; ++l) {
+    if (launch_rmsnorm(cur, N, d_model, norm_scale, eps, normed, s) != 0) return LBK_ERR_LAUNCH;
+    if ((st = swiglu_general(normed, N, d_model, gate, up, down, cur, h_out, h, nullptr, nullptr, s))) return st;
+    cur = h_out;
+  }
+  return LBK_OK;
+}
+
+int lbk_quantize_act_int8(const uint16_t* x, int64_t N, int32_t F, int64_t ldx, int8_t* xq, float* sx,
+                          void* stream) {
+  if (N < 0 || F <= 0 || ldx < F) return LBK_ERR_ARG;
+  if (N == 0) return LBK_OK;
+  if (!x || !xq || !sx) return LBK_ERR_NULL;
+  if ((F % 8) || (ldx % 8) || !a16(x) || !a8(xq)) return LBK_ERR_ALIGN;
+  return launch_quantize_act(x, N, F, ldx, xq, sx, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+int lbk_pack_ternary(const int8_t* t, int32_t R, int32_t K, int32_t B, uint32_t* packed, void* stream) {
+  if (!tile_ok(B)) return LBK_ERR_TILE;
+  if (R < 0 || K < 0) return LBK_ERR_SHAPE;
+  if ((int64_t)R * K == 0) return LBK_OK;
+  if (!t || !packed) return LBK_ERR_NULL;
+  return launch_pack_ternary(t, R, K, B, packed, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+int lbk_ternary_quantize_weights_bf16(const uint16_t* values, int32_t R, int32_t K, int32_t B, uint32_t* packed,
+                                      float* scales, void* stream) {
+  if (!tile_ok(B)) return LBK_ERR_TILE;
+  if (R < 0 || K < 0) return LBK_ERR_SHAPE;
+  if ((int64_t)R * K == 0) return LBK_OK;
+  if (!values || !packed || !scales) return LBK_ERR_NULL;
+  return launch_ternary_quantize_weights(values, R, K, B, packed, scales, S(stream)) == 0 ? LBK_OK
+                                                                                           : LBK_ERR_LAUNCH;
+}
+
+int lbk_ternary_matmul(const int8_t* xq, const float* sx, int64_t N, int32_t in_features,
+                       const lbk_bell_ternary* w, uint16_t* y, int32_t* partials, void* stream) {
+  int st = check_tern(w);
+  if (st) return st;
+  if (N < 0) return LBK_ERR_ARG;
+  if (in_features <= 0 || in_features % w->B) return LBK_ERR_SHAPE;
+  if (N == 0) return LBK_OK;
+  if (!xq || !sx || !y) return LBK_ERR_NULL;
+  if (!a16(xq) || !a8(y)) return LBK_ERR_ALIGN;
+  TernaryLaunch a{};
+  a.xq = xq; a.sx = sx; a.N = N; a.C = in_features / w->B;
+  a.p0 = w->packed; a.s0 = w->scales; a.c0 = w->col_idx; a.K0 = w->K;
+  a.R = w->R; a.y = y; a.partials = partials;
+  return launch_ternary(w->B, 0, a, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+size_t lbk_ternary_swiglu_workspace_bytes(int64_t N, const lbk_bell_ternary* gate) {
+  if (!gate || N <= 0) return 0;
+  const size_t d_ff = (size_t)gate->R * gate->B;
+  return align256((size_t)N * d_ff * 2) + align256((size_t)N * d_ff) + align256((size_t)N * 4);
+}
+
+int lbk_swiglu_fwd_ternary(const int8_t* xq, const float* sx, int64_t N, int32_t d_model,
+                           const lbk_bell_ternary* gate, const lbk_bell_ternary* up, const lbk_bell_ternary* down,
+                           const uint16_t* x_resid, uint16_t* out, uint16_t* h_out, int8_t* hq_out,
+                           float* sh_out, void* workspace, size_t workspace_bytes, void* stream) {
+  int st;
+  if ((st = check_tern(gate)) || (st = check_tern(up)) || (st = check_tern(down))) return st;
+  int64_t d_ff = 0;
+  if ((st = check_ffn(gate, up, down, d_model, &d_ff))) return st;
+  if (N < 0) return LBK_ERR_ARG;
+  if (N == 0) return LBK_OK;
+  if (!xq || !sx || !out) return LBK_ERR_NULL;
+  if (!a16(xq) || !a16(out)) return LBK_ERR_ALIGN;
+  const size_t hb = align256((size_t)N * d_ff * 2), qb = align256((size_t)N * d_ff);
+  char* ws = static_cast<char*>(workspace);
+  const bool need_ws = !h_out || !hq_out || !sh_out;
+  if (need_ws) {
+    if (!ws || workspace_bytes < lbk_ternary_swiglu_workspace_bytes(N, gate)) return LBK_ERR_WORKSPACE;
+    if (!a16(ws)) return LBK_ERR_ALIGN;
+  }
+  uint16_t* h = h_out ? h_out : reinterpret_cast<uint16_t*>(ws);
+  int8_t* hq = hq_out ? hq_out : reinterpret_cast<int8_t*>(ws + hb);
+  float* sh = sh_out ? sh_out : reinterpret_cast<float*>(ws + hb + qb);
+  if (!a16(h) || !a16(hq)) return LBK_ERR_ALIGN;
+  hipStream_t s = S(stream);
+  TernaryLaunch a{};
+  a.xq = xq; a.sx = sx; a.N = N; a.C = d_model / gate->B;
+  a.p0 = gate->packed; a.s0 = gate->scales; a.c0 = gate->col_idx; a.K0 = gate->K;
+  a.p1 = up->packed; a.s1 = up->scales; a.c1 = up->col_idx; a.K1 = up->K;
+  a.R = gate->R; a.y = h;
+  if (launch_ternary(gate->B, 1, a, s) != 0) return LBK_ERR_LAUNCH;
+  if (launch_quantize_act(h, N, (int)d_ff, d_ff, hq, sh, s) != 0) return LBK_ERR_LAUNCH;
+  TernaryLaunch d{};
+  d.xq = hq; d.sx = sh; d.N = N; d.C = gate->R;
+  d.p0 = down->packed; d.s0 = down->scales; d.c0 = down->col_idx; d.K0 = down->K;
+  d.R = down->R; d.resid = x_resid; d.y = out;
+  if (launch_ternary(gate->B, 0, d, s) != 0) return LBK_ERR_LAUNCH;
+  return LBK_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,192 @@
+// lbk_device.h — device-side building blocks shared by the gfx950 kernels.
+//
+// MFMA fragment conventions (v_mfma_f32_16x16x32_bf16, checked on the GPU by
+// tests/test_gpu_lanes.py):
+//   A (16 x 32, M x K): lane l holds row l%16, k = 8*(l/16) .. +7  (8 bf16)
+//   B (32 x 16, K x N): lane l holds col l%16, k = 8*(l/16) .. +7
+//   C (16 x 16):        lane l holds col l%16, rows 4*(l/16) + v, v = 0..3
+// A and B only need the same k assignment, so any k permutation shared by both
+// operands gives the same product.
+//
+// Weight tiles arrive as [B_in, B_out] (output index contiguous), but the B
+// operand wants 8 consecutive *input* indices per lane.  load_wraw/wraw_to_frag
+// transpose in registers: with CW = B/16 output columns per lane, lane (j, g)
+// loads the CW contiguous outputs CW*j .. CW*j+CW-1 of 8 consecutive input
+// rows, then v_perm splits them into CW fragments.  Fragment m of a lane then
+// carries output column CW*j + m, so a tile of B outputs is covered by CW
+// MFMAs whose column n maps to output CW*n + m, and after the MFMAs every lane
+// owns CW *contiguous* outputs per row — which makes the stores contiguous.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lbk {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf2f(uint32_t b16) { return __uint_as_float(b16 << 16); }
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round-to-nearest-even float -> bf16 (hardware v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
+  bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  __bf16 h = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ f32x4 mfma_bf16(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// int8 MFMAs: 16x16x64 (16 bytes of K per lane) and 16x16x32 (8 bytes).
+__device__ __forceinline__ i32x4 mfma_i8_k64(const i32x4& a, const i32x4& b, const i32x4& c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ i32x4 mfma_i8_k32(long a, long b, const i32x4& c) {
+  return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float silu_f(float z) {
+  // z * sigmoid(z) = z / (1 + exp(-z)); exp via the hardware exp2.
+  return z * __builtin_amdgcn_rcpf(1.0f + __expf(-z));
+}
+
+// Wave-uniform value (forces scalar registers / scalar branches).
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// ---------------------------------------------------------------------------
+// Weight tiles: raw transposing loads and conversion to B fragments.
+// NKS = number of 32-deep k-steps per tile, CW = output columns per lane.
+// For B = 16 the single k-step is half filled: lanes with g >= 2 carry zeros.
+// ---------------------------------------------------------------------------
+template <int B> struct TileShape;
+template <> struct TileShape<16> { static constexpr int NKS = 1, CW = 1; };
+template <> struct TileShape<32> { static constexpr int NKS = 1, CW = 2; };
+template <> struct TileShape<64> { static constexpr int NKS = 2, CW = 4; };
+
+template <int B> struct WRaw;
+template <> struct WRaw<16> { uint32_t v[8]; };       // one bf16 per row (zero-extended)
+template <> struct WRaw<32> { uint32_t v[8]; };       // two bf16 per row
+template <> struct WRaw<64> { u32x2 v[2][8]; };       // four bf16 per row, per k-step
+
+template <int B>
+__device__ __forceinline__ void load_wraw(const uint16_t* __restrict__ tile, int lane, WRaw<B>& r);
+
+template <>
+__device__ __forceinline__ void load_wraw<16>(const uint16_t* __restrict__ tile, int lane, WRaw<16>& r) {
+  const int j = lane & 15, g = lane >> 4;
+  if (g < 2) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) r.v[t] = tile[(8 * g + t) * 16 + j];
+  } else {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) r.v[t] = 0;
+  }
+}
+template <>
+__device__ __forceinline__ void load_wraw<32>(const uint16_t* __restrict__ tile, int lane, WRaw<32>& r) {
+  const int j = lane & 15, g = lane >> 4;
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(tile) + (8 * g) * 16 + j;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) r.v[t] = p[t * 16];
+}
+template <>
+__device__ __forceinline__ void load_wraw<64>(const uint16_t* __restrict__ tile, int lane, WRaw<64>& r) {
+  const int j = lane & 15, g = lane >> 4;
+  const u32x2* p = reinterpret_cast<const u32x2*>(tile) + (8 * g) * 16 + j;
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) r.v[s][t] = p[(32 * s + t) * 16];
+}
+
+// f[ks][m]: fragment for k-step ks and output sub-column m.
+template <int B>
+__device__ __forceinline__ void wraw_to_frag(const WRaw<B>& r, u32x4 (&f)[TileShape<B>::NKS][TileShape<B>::CW]);
+
+template <>
+__device__ __forceinline__ void wraw_to_frag<16>(const WRaw<16>& r, u32x4 (&f)[1][1]) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) f[0][0][u] = r.v[2 * u] | (r.v[2 * u + 1] << 16);
+}
+template <>
+__device__ __forceinline__ void wraw_to_frag<32>(const WRaw<32>& r, u32x4 (&f)[1][2]) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    f[0][0][u] = __builtin_amdgcn_perm(r.v[2 * u + 1], r.v[2 * u], 0x05040100u);
+    f[0][1][u] = __builtin_amdgcn_perm(r.v[2 * u + 1], r.v[2 * u], 0x07060302u);
+  }
+}
+template <>
+__device__ __forceinline__ void wraw_to_frag<64>(const WRaw<64>& r, u32x4 (&f)[2][4]) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const u32x2 a = r.v[s][2 * u], b = r.v[s][2 * u + 1];
+      f[s][0][u] = __builtin_amdgcn_perm(b[0], a[0], 0x05040100u);
+      f[s][1][u] = __builtin_amdgcn_perm(b[0], a[0], 0x07060302u);
+      f[s][2][u] = __builtin_amdgcn_perm(b[1], a[1], 0x05040100u);
+      f[s][3][u] = __builtin_amdgcn_perm(b[1], a[1], 0x07060302u);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// A fragments.  Row pointer `row` points at element (token, column-block
+// start); ks selects the 32-deep k-step.  For B = 16, lanes g >= 2 carry zeros.
+// ---------------------------------------------------------------------------
+template <int B>
+__device__ __forceinline__ u32x4 load_afrag(const uint16_t* row, int ks, int g) {
+  if (B == 16 && g >= 2) return u32x4{0, 0, 0, 0};
+  return *reinterpret_cast<const u32x4*>(row + 32 * ks + 8 * g);
+}
+
+// Store CW contiguous bf16 values.
+template <int CW>
+__device__ __forceinline__ void store_bf16(uint16_t* p, const float (&v)[CW]);
+template <>
+__device__ __forceinline__ void store_bf16<1>(uint16_t* p, const float (&v)[1]) { *p = f2bf(v[0]); }
+template <>
+__device__ __forceinline__ void store_bf16<2>(uint16_t* p, const float (&v)[2]) {
+  *reinterpret_cast<uint32_t*>(p) = pack2_bf16(v[0], v[1]);
+}
+template <>
+__device__ __forceinline__ void store_bf16<4>(uint16_t* p, const float (&v)[4]) {
+  u32x2 w = {pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3])};
+  *reinterpret_cast<u32x2*>(p) = w;
+}
+
+// Load CW contiguous bf16 values as floats.
+template <int CW>
+__device__ __forceinline__ void load_bf16(const uint16_t* p, float (&v)[CW]);
+template <>
+__device__ __forceinline__ void load_bf16<1>(const uint16_t* p, float (&v)[1]) { v[0] = bf2f(*p); }
+template <>
+__device__ __forceinline__ void load_bf16<2>(const uint16_t* p, float (&v)[2]) {
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+  v[0] = bf_lo(w);
+  v[1] = bf_hi(w);
+}
+template <>
+__device__ __forceinline__ void load_bf16<4>(const uint16_t* p, float (&v)[4]) {
+  const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+  v[0] = bf_lo(w[0]);
+  v[1] = bf_hi(w[0]);
+  v[2] = bf_lo(w[1]);
+  v[3] = bf_hi(w[1]);
+}
+
+}  // namespace lbk

@@ -1,0 +1,487 @@
+// torch_ops.cpp — thin PyTorch-ROCm extension: registers the titan:: operators
+// over the C ABI of liblbk.so (include/lbk.h).
+//
+// The reference registers the same schemas for its CUDA kernels
+// (csrc/block_ell/block_ell_ops.cpp:49-98, csrc/loop/loop_ops.cpp:36-67); the
+// schemas below keep those names, arguments and return types, and add the ops
+// this library exposes beyond them (block_ell_matmul, looped_swiglu, rmsnorm,
+// diagonal_injection and the ternary family).  PyTorch on ROCm dispatches HIP
+// tensors under the CUDA key.  Every op checks its inputs with TORCH_CHECK
+// (a Python RuntimeError), makes inputs contiguous, allocates its outputs and
+// queues the work on the current stream; C ABI status codes become errors.
+#include <ATen/ATen.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <torch/library.h>
+
+#include <vector>
+
+#include "lbk.h"
+
+namespace {
+
+void* cur_stream(const at::Tensor& t) {
+  return (void*)c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream();
+}
+
+#define LBK_CALL(opname, expr)                                                                    \
+  do {                                                                                            \
+    const int _st = (expr);                                                                       \
+    TORCH_CHECK(_st == LBK_OK, "titan::" opname ": ", lbk_status_string(_st), " (status ", _st, ")"); \
+  } while (0)
+
+const uint16_t* bf(const at::Tensor& t) { return reinterpret_cast<const uint16_t*>(t.data_ptr()); }
+uint16_t* bfm(at::Tensor& t) { return reinterpret_cast<uint16_t*>(t.data_ptr()); }
+
+void check_gpu(const at::Tensor& t, const char* op, const char* name) {
+  TORCH_CHECK(t.is_cuda(), "titan::", op, ": ", name, " must be a GPU (HIP) tensor");
+}
+
+// values [R,K,B,B] bf16 + col_idx [R,K] int32 -> lbk_bell (tensors made contiguous in place)
+lbk_bell make_bell(at::Tensor& v, at::Tensor& c, const char* op, const char* name) {
+  check_gpu(v, op, name);
+  check_gpu(c, op, name);
+  TORCH_CHECK(v.scalar_type() == at::kBFloat16, "titan::", op, ": ", name, " values must be bf16");
+  TORCH_CHECK(c.scalar_type() == at::kInt, "titan::", op, ": ", name, " col_indices must be int32");
+  TORCH_CHECK(v.dim() == 4 && v.size(2) == v.size(3), "titan::", op, ": ", name,
+              " values must be [R, K, B, B], got ", v.sizes());
+  TORCH_CHECK(c.dim() == 2 && c.size(0) == v.size(0) && c.size(1) == v.size(1), "titan::", op, ": ", name,
+              " col_indices must be [R, K] matching values, got ", c.sizes());
+  v = v.contiguous();
+  c = c.contiguous();
+  return lbk_bell{bf(v), c.data_ptr<int32_t>(), (int32_t)v.size(0), (int32_t)v.size(1), (int32_t)v.size(2)};
+}
+
+lbk_bell_ternary make_tern(at::Tensor& p, at::Tensor& s, at::Tensor& c, const char* op, const char* name) {
+  check_gpu(p, op, name);
+  check_gpu(s, op, name);
+  check_gpu(c, op, name);
+  TORCH_CHECK(p.scalar_type() == at::kInt || p.scalar_type() == at::kUInt32, "titan::", op, ": ", name,
+              " packed must be int32/uint32 words");
+  TORCH_CHECK(s.scalar_type() == at::kFloat, "titan::", op, ": ", name, " scales must be fp32");
+  TORCH_CHECK(c.scalar_type() == at::kInt, "titan::", op, ": ", name, " col_indices must be int32");
+  TORCH_CHECK(p.dim() == 4 && p.size(3) * 16 == p.size(2), "titan::", op, ": ", name,
+              " packed must be [R, K, B, B/16], got ", p.sizes());
+  TORCH_CHECK(s.dim() == 2 && s.size(0) == p.size(0) && s.size(1) == p.size(1), "titan::", op, ": ", name,
+              " scales must be [R, K]");
+  TORCH_CHECK(c.dim() == 2 && c.size(0) == p.size(0) && c.size(1) == p.size(1), "titan::", op, ": ", name,
+              " col_indices must be [R, K]");
+  p = p.contiguous();
+  s = s.contiguous();
+  c = c.contiguous();
+  return lbk_bell_ternary{reinterpret_cast<const uint32_t*>(p.data_ptr()), s.data_ptr<float>(),
+                          c.data_ptr<int32_t>(), (int32_t)p.size(0), (int32_t)p.size(1), (int32_t)p.size(2)};
+}
+
+at::Tensor check_x2d(const at::Tensor& x, const char* op) {
+  check_gpu(x, op, "x");
+  TORCH_CHECK(x.scalar_type() == at::kBFloat16, "titan::", op, ": x must be bf16");
+  TORCH_CHECK(x.dim() == 2, "titan::", op, ": x must be 2D [N, d_model], got ", x.sizes());
+  return x.contiguous();
+}
+
+at::Tensor workspace(size_t bytes, const at::Tensor& like) {
+  return at::empty({(int64_t)std::max<size_t>(bytes, 1)}, like.options().dtype(at::kByte));
+}
+
+// ------------------------------------------------------------------ bf16 SwiGLU
+std::vector<at::Tensor> swiglu_impl(const at::Tensor& x_, at::Tensor vg, at::Tensor cg, at::Tensor vu,
+                                    at::Tensor cu, at::Tensor vd, at::Tensor cd, bool add_residual,
+                                    bool intermediates) {
+  const char* op = intermediates ? "block_ell_swiglu_fwd_with_intermediate" : "block_ell_swiglu_fwd";
+  at::Tensor x = check_x2d(x_, op);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  lbk_bell g = make_bell(vg, cg, op, "gate"), u = make_bell(vu, cu, op, "up"), d = make_bell(vd, cd, op, "down");
+  const int64_t N = x.size(0), d_model = x.size(1);
+  TORCH_CHECK((int64_t)d.R * d.B == d_model, "titan::", op, ": values_down R_model=", d.R,
+              " inconsistent with d_model=", d_model);
+  TORCH_CHECK(g.R == u.R, "titan::", op, ": gate and up must have same R_ff");
+  const int64_t d_ff = (int64_t)g.R * g.B;
+  at::Tensor out = at::empty({N, d_model}, x.options());
+  std::vector<at::Tensor> res{out};
+  uint16_t *h = nullptr, *gp = nullptr, *uo = nullptr;
+  if (intermediates) {
+    at::Tensor th = at::empty({N, d_ff}, x.options()), tg = at::empty({N, d_ff}, x.options()),
+               tu = at::empty({N, d_ff}, x.options());
+    h = bfm(th);
+    gp = bfm(tg);
+    uo = bfm(tu);
+    res.push_back(th);
+    res.push_back(tg);
+    res.push_back(tu);
+  }
+  const size_t wsb = lbk_swiglu_workspace_bytes(N, (int32_t)d_model, &g, &u, &d, intermediates ? 1 : 0);
+  at::Tensor ws = wsb ? workspace(wsb, x) : at::Tensor();
+  LBK_CALL("block_ell_swiglu_fwd",
+           lbk_swiglu_fwd_bf16(bf(x), N, (int32_t)d_model, &g, &u, &d, add_residual ? 1 : 0, bfm(out), h, gp, uo,
+                               wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(x)));
+  return res;
+}
+
+at::Tensor swiglu_fwd(const at::Tensor& x, const at::Tensor& vg, const at::Tensor& cg, const at::Tensor& vu,
+                      const at::Tensor& cu, const at::Tensor& vd, const at::Tensor& cd, bool add_residual) {
+  return swiglu_impl(x, vg, cg, vu, cu, vd, cd, add_residual, false)[0];
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> swiglu_fwd_inter(
+    const at::Tensor& x, const at::Tensor& vg, const at::Tensor& cg, const at::Tensor& vu, const at::Tensor& cu,
+    const at::Tensor& vd, const at::Tensor& cd, bool add_residual) {
+  auto r = swiglu_impl(x, vg, cg, vu, cu, vd, cd, add_residual, true);
+  return {r[0], r[1], r[2], r[3]};
+}
+
+at::Tensor block_ell_matmul(const at::Tensor& x_, const at::Tensor& v_, const at::Tensor& c_,
+                            const c10::optional<at::Tensor>& bias) {
+  const char* op = "block_ell_matmul";
+  at::Tensor v = v_, c = c_;
+  at::Tensor x = check_x2d(x_, op);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  lbk_bell w = make_bell(v, c, op, "weight");
+  TORCH_CHECK(x.size(1) % w.B == 0, "titan::block_ell_matmul: in_features ", x.size(1), " not a multiple of B=", w.B);
+  const int64_t N = x.size(0), out_f = (int64_t)w.R * w.B;
+  at::Tensor b;
+  const float* bp = nullptr;
+  if (bias.has_value() && bias->defined()) {
+    b = bias->to(at::kFloat).contiguous();
+    TORCH_CHECK(b.numel() == out_f, "titan::block_ell_matmul: bias must have out_features elements");
+    bp = b.data_ptr<float>();
+  }
+  at::Tensor y = at::empty({N, out_f}, x.options());
+  LBK_CALL("block_ell_matmul", lbk_block_ell_matmul_bf16(bf(x), N, (int32_t)x.size(1), x.size(1), &w, bp, bfm(y),
+                                                         out_f, cur_stream(x)));
+  return y;
+}
+
+// ------------------------------------------------------------------ norm / loop
+at::Tensor rmsnorm(const at::Tensor& x_, const at::Tensor& scale_, double eps) {
+  at::Tensor x = check_x2d(x_, "rmsnorm");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  at::Tensor s = scale_.to(x.device(), at::kFloat).contiguous();
+  TORCH_CHECK(s.numel() == x.size(1), "titan::rmsnorm: scale must have d elements");
+  at::Tensor out = at::empty_like(x);
+  LBK_CALL("rmsnorm", lbk_rmsnorm_bf16(bf(x), x.size(0), (int32_t)x.size(1), s.data_ptr<float>(), (float)eps,
+                                       bfm(out), cur_stream(x)));
+  return out;
+}
+
+at::Tensor diagonal_injection(const at::Tensor& h_, const at::Tensor& e_, const at::Tensor& log_A,
+                              const at::Tensor& log_dt) {
+  at::Tensor h = check_x2d(h_, "diagonal_injection");
+  at::Tensor e = check_x2d(e_, "diagonal_injection");
+  TORCH_CHECK(e.sizes() == h.sizes(), "titan::diagonal_injection: e must match h");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(h.device());
+  at::Tensor la = log_A.to(h.device(), at::kFloat).contiguous(), ld = log_dt.to(h.device(), at::kFloat).contiguous();
+  TORCH_CHECK(la.numel() == h.size(1) && ld.numel() == h.size(1), "titan::diagonal_injection: log_A/log_dt must be [d_model]");
+  at::Tensor out = at::empty_like(h);
+  LBK_CALL("diagonal_injection", lbk_diagonal_injection_bf16(bf(h), bf(e), la.data_ptr<float>(), ld.data_ptr<float>(),
+                                                             h.size(0), (int32_t)h.size(1), bfm(out), cur_stream(h)));
+  return out;
+}
+
+at::Tensor looped_impl(const at::Tensor& h, const at::Tensor& scale_, at::Tensor vg, at::Tensor cg, at::Tensor vu,
+                       at::Tensor cu, at::Tensor vd, at::Tensor cd, int64_t L, double eps, const char* op) {
+  at::Tensor x = check_x2d(h, op);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  lbk_bell g = make_bell(vg, cg, op, "gate"), u = make_bell(vu, cu, op, "up"), d = make_bell(vd, cd, op, "down");
+  at::Tensor s = scale_.to(x.device(), at::kFloat).contiguous();
+  TORCH_CHECK(s.numel() == x.size(1), "titan::", op, ": norm scale must have d_model elements");
+  TORCH_CHECK(L >= 0, "titan::", op, ": L must be >= 0");
+  at::Tensor out = at::empty_like(x);
+  const size_t wsb = lbk_looped_workspace_bytes(x.size(0), (int32_t)x.size(1), &g, &u, &d);
+  at::Tensor ws = wsb ? workspace(wsb, x) : at::Tensor();
+  LBK_CALL("looped_swiglu", lbk_looped_swiglu_bf16(bf(x), x.size(0), (int32_t)x.size(1), s.data_ptr<float>(),
+                                                   (float)eps, (int32_t)L, &g, &u, &d, bfm(out),
+                                                   wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(x)));
+  return out;
+}
+
+at::Tensor looped_swiglu(const at::Tensor& h, const at::Tensor& scale, const at::Tensor& vg, const at::Tensor& cg,
+                         const at::Tensor& vu, const at::Tensor& cu, const at::Tensor& vd, const at::Tensor& cd,
+                         int64_t L, double eps) {
+  return looped_impl(h, scale, vg, cg, vu, cu, vd, cd, L, eps, "looped_swiglu");
+}
+
+// Reference semantics (csrc/loop/persistent_core.cu:273-338): injection once,
+// then for each core block: h = h + SwiGLU(RMSNorm(h, eps=1e-6)).
+at::Tensor persistent_mlp_step(const at::Tensor& h, const at::Tensor& e, const at::Tensor& log_A,
+                               const at::Tensor& log_dt, at::TensorList norm_scales, at::TensorList gate_values,
+                               at::TensorList gate_col_idx, at::TensorList up_values, at::TensorList up_col_idx,
+                               at::TensorList down_values, at::TensorList down_col_idx) {
+  const size_t n_core = norm_scales.size();
+  TORCH_CHECK(n_core > 0, "persistent_mlp_step: n_core must be > 0");
+  TORCH_CHECK(gate_values.size() == n_core && gate_col_idx.size() == n_core && up_values.size() == n_core &&
+                  up_col_idx.size() == n_core && down_values.size() == n_core && down_col_idx.size() == n_core,
+              "persistent_mlp_step: all weight vector sizes must equal n_core");
+  TORCH_CHECK(h.dim() == 2, "persistent_mlp_step: h must be 2D [N, d_model], got shape ", h.sizes());
+  TORCH_CHECK(h.scalar_type() == at::kBFloat16, "persistent_mlp_step: h must be bf16");
+  at::Tensor cur = diagonal_injection(h, e, log_A, log_dt);
+  for (size_t i = 0; i < n_core; ++i)
+    cur = looped_impl(cur, norm_scales[i], gate_values[i], gate_col_idx[i], up_values[i], up_col_idx[i],
+                      down_values[i], down_col_idx[i], 1, 1e-6, "persistent_mlp_step");
+  return cur;
+}
+
+// ------------------------------------------------------------------ ternary
+std::tuple<at::Tensor, at::Tensor> quantize_act_int8(const at::Tensor& x_) {
+  at::Tensor x = check_x2d(x_, "quantize_act_int8");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  at::Tensor q = at::empty(x.sizes(), x.options().dtype(at::kChar));
+  at::Tensor s = at::empty({x.size(0)}, x.options().dtype(at::kFloat));
+  LBK_CALL("quantize_act_int8", lbk_quantize_act_int8(bf(x), x.size(0), (int32_t)x.size(1), x.size(1),
+                                                      q.data_ptr<int8_t>(), s.data_ptr<float>(), cur_stream(x)));
+  return {q, s};
+}
+
+at::Tensor pack_ternary(const at::Tensor& t_) {
+  check_gpu(t_, "pack_ternary", "t");
+  TORCH_CHECK(t_.scalar_type() == at::kChar, "titan::pack_ternary: t must be int8");
+  TORCH_CHECK(t_.dim() == 4 && t_.size(2) == t_.size(3), "titan::pack_ternary: t must be [R, K, B, B]");
+  at::Tensor t = t_.contiguous();
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(t.device());
+  const int64_t B = t.size(2);
+  TORCH_CHECK(B == 16 || B == 32 || B == 64, "titan::pack_ternary: B must be 16, 32 or 64");
+  at::Tensor p = at::empty({t.size(0), t.size(1), B, B / 16}, t.options().dtype(at::kInt));
+  LBK_CALL("pack_ternary", lbk_pack_ternary(t.data_ptr<int8_t>(), (int32_t)t.size(0), (int32_t)t.size(1),
+                                            (int32_t)B, reinterpret_cast<uint32_t*>(p.data_ptr()), cur_stream(t)));
+  return p;
+}
+
+std::tuple<at::Tensor, at::Tensor> ternary_quantize_weights(const at::Tensor& v_) {
+  check_gpu(v_, "ternary_quantize_weights", "values");
+  TORCH_CHECK(v_.dim() == 4 && v_.size(2) == v_.size(3), "titan::ternary_quantize_weights: values must be [R,K,B,B]");
+  at::Tensor v = v_.to(at::kBFloat16).contiguous();
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(v.device());
+  const int64_t B = v.size(2);
+  at::Tensor p = at::empty({v.size(0), v.size(1), B, B / 16}, v.options().dtype(at::kInt));
+  at::Tensor s = at::empty({v.size(0), v.size(1)}, v.options().dtype(at::kFloat));
+  LBK_CALL("ternary_quantize_weights",
+           lbk_ternary_quantize_weights_bf16(bf(v), (int32_t)v.size(0), (int32_t)v.size(1), (int32_t)B,
+                                             reinterpret_cast<uint32_t*>(p.data_ptr()), s.data_ptr<float>(),
+                                             cur_stream(v)));
+  return {p, s};
+}
+
+at::Tensor check_int8_x(const at::Tensor& xq_, const at::Tensor& sx, const char* op) {
+  check_gpu(xq_, op, "xq");
+  check_gpu(sx, op, "sx");
+  TORCH_CHECK(xq_.scalar_type() == at::kChar, "titan::", op, ": xq must be int8");
+  TORCH_CHECK(xq_.dim() == 2, "titan::", op, ": xq must be 2D [N, features]");
+  TORCH_CHECK(sx.scalar_type() == at::kFloat && sx.numel() == xq_.size(0), "titan::", op,
+              ": sx must be fp32 [N]");
+  return xq_.contiguous();
+}
+
+std::tuple<at::Tensor, at::Tensor> ternary_matmul(const at::Tensor& xq_, const at::Tensor& sx_, const at::Tensor& p_,
+                                                  const at::Tensor& s_, const at::Tensor& c_, bool want_partials) {
+  const char* op = "ternary_matmul";
+  at::Tensor p = p_, s = s_, c = c_;
+  at::Tensor xq = check_int8_x(xq_, sx_, op);
+  at::Tensor sx = sx_.contiguous();
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(xq.device());
+  lbk_bell_ternary w = make_tern(p, s, c, op, "weight");
+  const int64_t N = xq.size(0), out_f = (int64_t)w.R * w.B;
+  at::Tensor y = at::empty({N, out_f}, xq.options().dtype(at::kBFloat16));
+  at::Tensor part = want_partials ? at::empty({N, w.R, w.K, w.B}, xq.options().dtype(at::kInt))
+                                  : at::empty({0}, xq.options().dtype(at::kInt));
+  LBK_CALL("ternary_matmul", lbk_ternary_matmul(xq.data_ptr<int8_t>(), sx.data_ptr<float>(), N, (int32_t)xq.size(1),
+                                                &w, bfm(y), want_partials ? part.data_ptr<int32_t>() : nullptr,
+                                                cur_stream(xq)));
+  return {y, part};
+}
+
+std::vector<at::Tensor> tern_swiglu_impl(const at::Tensor& xq_, const at::Tensor& sx_, at::Tensor pg, at::Tensor sg,
+                                         at::Tensor cg, at::Tensor pu, at::Tensor su, at::Tensor cu, at::Tensor pd,
+                                         at::Tensor sd, at::Tensor cd, const c10::optional<at::Tensor>& x_resid,
+                                         bool inter) {
+  const char* op = inter ? "block_ell_swiglu_fwd_ternary_with_intermediate" : "block_ell_swiglu_fwd_ternary";
+  at::Tensor xq = check_int8_x(xq_, sx_, op);
+  at::Tensor sx = sx_.contiguous();
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(xq.device());
+  lbk_bell_ternary g = make_tern(pg, sg, cg, op, "gate"), u = make_tern(pu, su, cu, op, "up"),
+                   d = make_tern(pd, sd, cd, op, "down");
+  const int64_t N = xq.size(0), d_model = xq.size(1), d_ff = (int64_t)g.R * g.B;
+  TORCH_CHECK((int64_t)d.R * d.B == d_model, "titan::", op, ": down R inconsistent with d_model");
+  at::Tensor xr;
+  const uint16_t* xrp = nullptr;
+  if (x_resid.has_value() && x_resid->defined()) {
+    xr = check_x2d(*x_resid, op);
+    TORCH_CHECK(xr.size(0) == N && xr.size(1) == d_model, "titan::", op, ": x_resid must be [N, d_model]");
+    xrp = bf(xr);
+  }
+  at::Tensor out = at::empty({N, d_model}, xq.options().dtype(at::kBFloat16));
+  std::vector<at::Tensor> res{out};
+  uint16_t* h = nullptr;
+  int8_t* hq = nullptr;
+  float* sh = nullptr;
+  at::Tensor ws;
+  size_t wsb = 0;
+  if (inter) {
+    at::Tensor th = at::empty({N, d_ff}, xq.options().dtype(at::kBFloat16));
+    at::Tensor tq = at::empty({N, d_ff}, xq.options().dtype(at::kChar));
+    at::Tensor ts = at::empty({N}, xq.options().dtype(at::kFloat));
+    h = bfm(th);
+    hq = tq.data_ptr<int8_t>();
+    sh = ts.data_ptr<float>();
+    res.push_back(th);
+    res.push_back(tq);
+    res.push_back(ts);
+  } else {
+    wsb = lbk_ternary_swiglu_workspace_bytes(N, &g);
+    ws = workspace(wsb, xq);
+  }
+  LBK_CALL("block_ell_swiglu_fwd_ternary",
+           lbk_swiglu_fwd_ternary(xq.data_ptr<int8_t>(), sx.data_ptr<float>(), N, (int32_t)d_model, &g, &u, &d, xrp,
+                                  bfm(out), h, hq, sh, wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(xq)));
+  return res;
+}
+
+at::Tensor tern_swiglu(const at::Tensor& xq, const at::Tensor& sx, const at::Tensor& pg, const at::Tensor& sg,
+                       const at::Tensor& cg, const at::Tensor& pu, const at::Tensor& su, const at::Tensor& cu,
+                       const at::Tensor& pd, const at::Tensor& sd, const at::Tensor& cd,
+                       const c10::optional<at::Tensor>& x_resid) {
+  return tern_swiglu_impl(xq, sx, pg, sg, cg, pu, su, cu, pd, sd, cd, x_resid, false)[0];
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> tern_swiglu_inter(
+    const at::Tensor& xq, const at::Tensor& sx, const at::Tensor& pg, const at::Tensor& sg, const at::Tensor& cg,
+    const at::Tensor& pu, const at::Tensor& su, const at::Tensor& cu, const at::Tensor& pd, const at::Tensor& sd,
+    const at::Tensor& cd, const c10::optional<at::Tensor>& x_resid) {
+  auto r = tern_swiglu_impl(xq, sx, pg, sg, cg, pu, su, cu, pd, sd, cd, x_resid, true);
+  return {r[0], r[1], r[2], r[3]};
+}
+
+at::Tensor check_columns(const at::Tensor& c_, int64_t C) {
+  check_gpu(c_, "check_columns", "col_indices");
+  TORCH_CHECK(c_.scalar_type() == at::kInt, "titan::check_columns: col_indices must be int32");
+  at::Tensor c = c_.contiguous();
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(c.device());
+  at::Tensor bad = at::empty({}, c.options());
+  LBK_CALL("check_columns", lbk_check_columns(c.data_ptr<int32_t>(), c.numel(), (int32_t)C, bad.data_ptr<int32_t>(),
+                                              cur_stream(c)));
+  return bad;
+}
+
+// HIP has no access-policy window; weight residency comes from the fused
+// kernels (LDS panels, L2/MALL reuse).  The ops stay in the schema so callers
+// written against the reference keep working (csrc/loop/loop_ops.cpp:39-46).
+void pin_weights_l2(at::TensorList) {}
+void unpin_weights_l2() {}
+
+}  // namespace
+
+TORCH_LIBRARY(titan, m) {
+  // reference schemas (csrc/block_ell/block_ell_ops.cpp:51-76, csrc/loop/loop_ops.cpp:39-66)
+  m.def("block_ell_swiglu_fwd(Tensor x, Tensor v_gate, Tensor ci_gate, Tensor v_up, Tensor ci_up, "
+        "Tensor v_down, Tensor ci_down, bool add_residual) -> Tensor");
+  m.def("block_ell_swiglu_fwd_with_intermediate(Tensor x, Tensor v_gate, Tensor ci_gate, Tensor v_up, "
+        "Tensor ci_up, Tensor v_down, Tensor ci_down, bool add_residual) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("pin_weights_l2(Tensor[] weights) -> ()");
+  m.def("unpin_weights_l2() -> ()");
+  m.def("persistent_mlp_step(Tensor h, Tensor e, Tensor log_A, Tensor log_dt, Tensor[] norm_scales, "
+        "Tensor[] gate_values, Tensor[] gate_col_idx, Tensor[] up_values, Tensor[] up_col_idx, "
+        "Tensor[] down_values, Tensor[] down_col_idx) -> Tensor");
+  // ops beyond the reference's set
+  m.def("block_ell_matmul(Tensor x, Tensor values, Tensor col_indices, Tensor? bias=None) -> Tensor");
+  m.def("looped_swiglu(Tensor h, Tensor norm_scale, Tensor v_gate, Tensor ci_gate, Tensor v_up, Tensor ci_up, "
+        "Tensor v_down, Tensor ci_down, int L, float eps=1e-05) -> Tensor");
+  m.def("rmsnorm(Tensor x, Tensor scale, float eps=1e-05) -> Tensor");
+  m.def("diagonal_injection(Tensor h, Tensor e, Tensor log_A, Tensor log_dt) -> Tensor");
+  m.def("quantize_act_int8(Tensor x) -> (Tensor, Tensor)");
+  m.def("pack_ternary(Tensor t) -> Tensor");
+  m.def("ternary_quantize_weights(Tensor values) -> (Tensor, Tensor)");
+  m.def("ternary_matmul(Tensor xq, Tensor sx, Tensor packed, Tensor scales, Tensor col_indices, "
+        "bool want_partials=False) -> (Tensor, Tensor)");
+  m.def("block_ell_swiglu_fwd_ternary(Tensor xq, Tensor sx, Tensor p_gate, Tensor s_gate, Tensor ci_gate, "
+        "Tensor p_up, Tensor s_up, Tensor ci_up, Tensor p_down, Tensor s_down, Tensor ci_down, "
+        "Tensor? x_resid=None) -> Tensor");
+  m.def("block_ell_swiglu_fwd_ternary_with_intermediate(Tensor xq, Tensor sx, Tensor p_gate, Tensor s_gate, "
+        "Tensor ci_gate, Tensor p_up, Tensor s_up, Tensor ci_up, Tensor p_down, Tensor s_down, Tensor ci_down, "
+        "Tensor? x_resid=None) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("check_columns(Tensor col_indices, int C) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(titan, CUDA, m) {
+  m.impl("block_ell_swiglu_fwd", &swiglu_fwd);
+  m.impl("block_ell_swiglu_fwd_with_intermediate", &swiglu_fwd_inter);
+  m.impl("pin_weights_l2", &pin_weights_l2);
+  m.impl("persistent_mlp_step", &persistent_mlp_step);
+  m.impl("block_ell_matmul", &block_ell_matmul);
+  m.impl("looped_swiglu", &looped_swiglu);
+  m.impl("rmsnorm", &rmsnorm);
+  m.impl("diagonal_injection", &diagonal_injection);
+  m.impl("quantize_act_int8", &quantize_act_int8);
+  m.impl("pack_ternary", &pack_ternary);
+  m.impl("ternary_quantize_weights", &ternary_quantize_weights);
+  m.impl("ternary_matmul", &ternary_matmul);
+  m.impl("block_ell_swiglu_fwd_ternary", &tern_swiglu);
+  m.impl("block_ell_swiglu_fwd_ternary_with_intermediate", &tern_swiglu_inter);
+  m.impl("check_columns", &check_columns);
+}
+
+TORCH_LIBRARY_IMPL(titan, CompositeExplicitAutograd, m) { m.impl("unpin_weights_l2", &unpin_weights_l2); }
+
+// Meta (shape-only) implementations, as the reference provides for FakeTensor tracing
+// (csrc/block_ell/block_ell_ops.cpp:179-237, csrc/loop/loop_ops.cpp:125-156).
+TORCH_LIBRARY_IMPL(titan, Meta, m) {
+  m.impl("block_ell_swiglu_fwd", [](const at::Tensor& x, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+                                    const at::Tensor&, const at::Tensor&, const at::Tensor&, bool) {
+    return at::empty_like(x);
+  });
+  m.impl("block_ell_swiglu_fwd_with_intermediate",
+         [](const at::Tensor& x, const at::Tensor& vg, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+            const at::Tensor&, const at::Tensor&, bool) {
+           const int64_t N = x.size(0), d_ff = vg.size(0) * vg.size(2);
+           return std::make_tuple(at::empty_like(x), at::empty({N, d_ff}, x.options()),
+                                  at::empty({N, d_ff}, x.options()), at::empty({N, d_ff}, x.options()));
+         });
+  m.impl("pin_weights_l2", [](at::TensorList) {});
+  m.impl("persistent_mlp_step",
+         [](const at::Tensor& h, const at::Tensor&, const at::Tensor&, const at::Tensor&, at::TensorList,
+            at::TensorList, at::TensorList, at::TensorList, at::TensorList, at::TensorList,
+            at::TensorList) { return at::empty_like(h); });
+  m.impl("block_ell_matmul", [](const at::Tensor& x, const at::Tensor& v, const at::Tensor&,
+                                const c10::optional<at::Tensor>&) {
+    return at::empty({x.size(0), v.size(0) * v.size(2)}, x.options());
+  });
+  m.impl("looped_swiglu", [](const at::Tensor& h, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+                             const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t,
+                             double) { return at::empty_like(h); });
+  m.impl("rmsnorm", [](const at::Tensor& x, const at::Tensor&, double) { return at::empty_like(x); });
+  m.impl("diagonal_injection", [](const at::Tensor& h, const at::Tensor&, const at::Tensor&, const at::Tensor&) {
+    return at::empty_like(h);
+  });
+  m.impl("quantize_act_int8", [](const at::Tensor& x) {
+    return std::make_tuple(at::empty(x.sizes(), x.options().dtype(at::kChar)),
+                           at::empty({x.size(0)}, x.options().dtype(at::kFloat)));
+  });
+  m.impl("pack_ternary", [](const at::Tensor& t) {
+    return at::empty({t.size(0), t.size(1), t.size(2), t.size(2) / 16}, t.options().dtype(at::kInt));
+  });
+  m.impl("ternary_quantize_weights", [](const at::Tensor& v) {
+    return std::make_tuple(at::empty({v.size(0), v.size(1), v.size(2), v.size(2) / 16}, v.options().dtype(at::kInt)),
+                           at::empty({v.size(0), v.size(1)}, v.options().dtype(at::kFloat)));
+  });
+  m.impl("ternary_matmul", [](const at::Tensor& xq, const at::Tensor&, const at::Tensor& p, const at::Tensor&,
+                              const at::Tensor&, bool want) {
+    return std::make_tuple(at::empty({xq.size(0), p.size(0) * p.size(2)}, xq.options().dtype(at::kBFloat16)),
+                           want ? at::empty({xq.size(0), p.size(0), p.size(1), p.size(2)}, xq.options().dtype(at::kInt))
+                                : at::empty({0}, xq.options().dtype(at::kInt)));
+  });
+  m.impl("block_ell_swiglu_fwd_ternary",
+         [](const at::Tensor& xq, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+            const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+            const at::Tensor&, const c10::optional<at::Tensor>&) {
+           return at::empty(xq.sizes(), xq.options().dtype(at::kBFloat16));
+         });
+  m.impl("block_ell_swiglu_fwd_ternary_with_intermediate",
+         [](const at::Tensor& xq, const at::Tensor&, const at::Tensor& pg, const at::Tensor&, const at::Tensor&,
+            const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+            const at::Tensor&, const c10::optional<at::Tensor>&) {
+           const int64_t N = xq.size(0), d_ff = pg.size(0) * pg.size(2);
+           return std::make_tuple(at::empty(xq.sizes(), xq.options().dtype(at::kBFloat16)),
+                                  at::empty({N, d_ff}, xq.options().dtype(at::kBFloat16)),
+                                  at::empty({N, d_ff}, xq.options().dtype(at::kChar)),
+                                  at::empty({N}, xq.options().dtype(at::kFloat)));
+         });
+  m.impl("check_columns", [](const at::Tensor& c, int64_t) { return at::empty({}, c.options()); });
+}

@@ -1,0 +1,98 @@
+"""ctypes binding of the C ABI in include/lbk.h (liblbk.so).
+
+This is the binding a non-torch caller would use; it mirrors the header one to
+one.  Pointers are plain integers (device addresses), streams are raw HIP
+stream handles.  ``check`` turns a status code into a RuntimeError carrying
+``lbk_status_string``.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liblbk.so")
+
+LBK_OK = 0
+LBK_ERR_NULL = 1
+LBK_ERR_TILE = 2
+LBK_ERR_SHAPE = 3
+LBK_ERR_ALIGN = 4
+LBK_ERR_WORKSPACE = 5
+LBK_ERR_LAUNCH = 6
+LBK_ERR_ARG = 7
+LBK_ERR_COLUMN = 8
+
+
+class Bell(C.Structure):
+    """``lbk_bell``: one Block-ELL weight with bf16 tiles [B_in, B_out]."""
+
+    _fields_ = [("values", C.c_void_p), ("col_idx", C.c_void_p),
+                ("R", C.c_int32), ("K", C.c_int32), ("B", C.c_int32)]
+
+
+class BellTernary(C.Structure):
+    """``lbk_bell_ternary``: packed 2-bit tiles, fp32 block scales, column indices."""
+
+    _fields_ = [("packed", C.c_void_p), ("scales", C.c_void_p), ("col_idx", C.c_void_p),
+                ("R", C.c_int32), ("K", C.c_int32), ("B", C.c_int32)]
+
+
+# (name, restype, argtypes) for every entry point of include/lbk.h
+_P = C.c_void_p
+_I64 = C.c_int64
+_I32 = C.c_int32
+_SZ = C.c_size_t
+_F = C.c_float
+_PB = C.POINTER(Bell)
+_PT = C.POINTER(BellTernary)
+SIGNATURES = {
+    "lbk_status_string": (C.c_char_p, [C.c_int]),
+    "lbk_version": (C.c_int, []),
+    "lbk_check_columns": (C.c_int, [_P, _I64, _I32, _P, _P]),
+    "lbk_block_ell_matmul_bf16": (C.c_int, [_P, _I64, _I32, _I64, _PB, _P, _P, _I64, _P]),
+    "lbk_swiglu_workspace_bytes": (_SZ, [_I64, _I32, _PB, _PB, _PB, C.c_int]),
+    "lbk_swiglu_fwd_bf16": (C.c_int, [_P, _I64, _I32, _PB, _PB, _PB, C.c_int, _P, _P, _P, _P, _P, _SZ, _P]),
+    "lbk_rmsnorm_bf16": (C.c_int, [_P, _I64, _I32, _P, _F, _P, _P]),
+    "lbk_diagonal_injection_bf16": (C.c_int, [_P, _P, _P, _P, _I64, _I32, _P, _P]),
+    "lbk_looped_workspace_bytes": (_SZ, [_I64, _I32, _PB, _PB, _PB]),
+    "lbk_looped_swiglu_bf16": (C.c_int, [_P, _I64, _I32, _P, _F, _I32, _PB, _PB, _PB, _P, _P, _SZ, _P]),
+    "lbk_quantize_act_int8": (C.c_int, [_P, _I64, _I32, _I64, _P, _P, _P]),
+    "lbk_pack_ternary": (C.c_int, [_P, _I32, _I32, _I32, _P, _P]),
+    "lbk_ternary_quantize_weights_bf16": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P]),
+    "lbk_ternary_matmul": (C.c_int, [_P, _P, _I64, _I32, _PT, _P, _P, _P]),
+    "lbk_ternary_swiglu_workspace_bytes": (_SZ, [_I64, _PT]),
+    "lbk_swiglu_fwd_ternary": (C.c_int, [_P, _P, _I64, _I32, _PT, _PT, _PT, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+}
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> C.CDLL:
+    """Load liblbk.so and attach the prototypes.  Raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ImportError(f"liblbk.so not built at {path}; run looped-blockell-tpu_amd/build.py")
+    lib = C.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def status_string(code: int) -> str:
+    return load().lbk_status_string(code).decode()
+
+
+def check(code: int, what: str = "lbk") -> None:
+    if code != LBK_OK:
+        raise RuntimeError(f"{what}: {status_string(code)} (status {code})")
+
+
+def exported_symbols() -> list[str]:
+    return list(SIGNATURES)

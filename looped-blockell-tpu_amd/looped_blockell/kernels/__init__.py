@@ -1,0 +1,147 @@
+"""HIP (gfx950) kernels of the Block-ELL SwiGLU path, exposed as torch operators.
+
+Loading this package loads ``_titan_ext.so`` (built by
+``looped-blockell-tpu_amd/build.py``), which registers the ``titan::`` operator
+namespace over the C ABI of ``liblbk.so``.  There is no fallback: if the
+extension is missing, :func:`ops` raises, and every operator raises on CPU
+tensors.
+
+The operator names and schemas follow the reference's torch.library
+registrations (``csrc/block_ell/block_ell_ops.cpp:49-98``,
+``csrc/loop/loop_ops.cpp:36-67``); the reference package's
+``looped_blockell/kernels/__init__.py:1`` is an empty placeholder this module
+fills.
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+EXT_PATH = os.path.join(_HERE, "_titan_ext.so")
+LIB_PATH = os.path.join(_HERE, "liblbk.so")
+
+_loaded = False
+
+
+def ops():
+    """Return ``torch.ops.titan`` after loading the extension (raises if not built)."""
+    global _loaded
+    if not _loaded:
+        if not os.path.exists(EXT_PATH):
+            raise ImportError(
+                f"titan extension not built ({EXT_PATH} missing); run looped-blockell-tpu_amd/build.py")
+        torch.ops.load_library(EXT_PATH)
+        _loaded = True
+    return torch.ops.titan
+
+
+def loaded_native_paths() -> list[str]:
+    return [EXT_PATH, LIB_PATH]
+
+
+def _gpu(*ts):
+    for t in ts:
+        if isinstance(t, torch.Tensor) and not t.is_cuda and t.device.type != "meta":
+            raise RuntimeError("looped_blockell kernels run on the GPU only; got a CPU tensor")
+
+
+# ---------------------------------------------------------------- bf16 path
+
+def block_ell_matmul(x: torch.Tensor, values: torch.Tensor, col_indices: torch.Tensor,
+                     bias: torch.Tensor | None = None) -> torch.Tensor:
+    """x [..., C*B] -> [..., R*B] through the Block-ELL weight (tiles [B_in, B_out])."""
+    _gpu(x, values, col_indices)
+    lead = x.shape[:-1]
+    y = ops().block_ell_matmul(x.reshape(-1, x.shape[-1]).to(torch.bfloat16), values, col_indices, bias)
+    return y.reshape(*lead, y.shape[-1])
+
+
+def swiglu_fwd(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual: bool = False):
+    """``titan::block_ell_swiglu_fwd``: W_down(silu(W_gate x) * W_up x) (+ x)."""
+    _gpu(x, v_gate, v_down)
+    return ops().block_ell_swiglu_fwd(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual)
+
+
+def swiglu_fwd_with_intermediate(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual: bool = False):
+    """Returns ``(result, h, gate_pre_act, up_output)`` like the reference op."""
+    _gpu(x, v_gate, v_down)
+    return ops().block_ell_swiglu_fwd_with_intermediate(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down,
+                                                        add_residual)
+
+
+def looped_swiglu(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L: int, eps: float = 1e-5):
+    """L applications of h <- h + SwiGLU(RMSNorm(h)) with shared weights, one persistent launch."""
+    _gpu(h, v_gate, v_down)
+    return ops().looped_swiglu(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L, eps)
+
+
+def rmsnorm(x, scale, eps: float = 1e-5):
+    _gpu(x)
+    return ops().rmsnorm(x, scale, eps)
+
+
+def diagonal_injection(h, e, log_A, log_dt):
+    _gpu(h, e)
+    return ops().diagonal_injection(h, e, log_A, log_dt)
+
+
+def persistent_mlp_step(h, e, log_A, log_dt, norm_scales, gate_values, gate_col_idx, up_values, up_col_idx,
+                        down_values, down_col_idx):
+    """``titan::persistent_mlp_step``: injection, then h += SwiGLU(RMSNorm(h)) per core block."""
+    _gpu(h, e)
+    return ops().persistent_mlp_step(h, e, log_A, log_dt, list(norm_scales), list(gate_values),
+                                     list(gate_col_idx), list(up_values), list(up_col_idx), list(down_values),
+                                     list(down_col_idx))
+
+
+def pin_weights_l2(weights) -> None:
+    """Kept for API compatibility; HIP has no access-policy window (no-op)."""
+    ops().pin_weights_l2(list(weights))
+
+
+def unpin_weights_l2() -> None:
+    ops().unpin_weights_l2()
+
+
+def check_columns(col_indices: torch.Tensor, C: int) -> torch.Tensor:
+    """Device int32 count of column indices outside [-1, C)."""
+    _gpu(col_indices)
+    return ops().check_columns(col_indices, C)
+
+
+# ---------------------------------------------------------------- ternary path
+
+def quantize_act_int8(x):
+    """Per-token absmax int8: returns (q int8 [N, F], sx fp32 [N]) with x ~= q * sx."""
+    _gpu(x)
+    return ops().quantize_act_int8(x)
+
+
+def pack_ternary(t):
+    _gpu(t)
+    return ops().pack_ternary(t)
+
+
+def ternary_quantize_weights(values):
+    _gpu(values)
+    return ops().ternary_quantize_weights(values)
+
+
+def ternary_matmul(xq, sx, packed, scales, col_indices, want_partials: bool = False):
+    _gpu(xq, packed)
+    return ops().ternary_matmul(xq, sx, packed, scales, col_indices, want_partials)
+
+
+def ternary_swiglu_fwd(xq, sx, gate, up, down, x_resid=None):
+    """gate/up/down are (packed, scales, col_indices) triples."""
+    _gpu(xq)
+    return ops().block_ell_swiglu_fwd_ternary(xq, sx, *gate, *up, *down, x_resid)
+
+
+def ternary_swiglu_fwd_with_intermediate(xq, sx, gate, up, down, x_resid=None):
+    """Returns (out, h bf16, hq int8, sh fp32)."""
+    _gpu(xq)
+    return ops().block_ell_swiglu_fwd_ternary_with_intermediate(xq, sx, *gate, *up, *down, x_resid)

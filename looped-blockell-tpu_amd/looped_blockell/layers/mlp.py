@@ -1,0 +1,117 @@
+"""Block-ELL MLP layers (PyTorch), mirroring the reference's Flax module.
+
+Reference: ``looped_blockell/layers/mlp.py``.
+
+Weight layout per projection:
+  values:      [R, K, B, B] parameter (tiles [B_in, B_out]), init N(0, 0.02)
+  col_indices: [R, K] int32 buffer (topology, updated externally by pruning)
+  alive_mask:  [R, K] bool buffer; dead tiles contribute nothing
+  bias:        [out_features] parameter, zeros (BlockELLLinear only)
+
+``MLPBlock(use_swiglu=True)`` runs the whole SwiGLU FFN as one fused HIP
+operator (``titan::block_ell_swiglu_fwd``); its projections carry no bias, as
+in the reference's PyTorch mirror (``interop/pt_model.py:865-867``) and its CUDA
+operator (``csrc/block_ell/swiglu_fwd.cuh:75-84``).
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .. import kernels
+from .block_ell import BlockELLConfig, BlockELLTensor, create_random_topology
+
+
+class BlockELLLinear(nn.Module):
+    """Single Block-ELL linear layer (reference ``mlp.py:28-95``).
+
+    ``K = max(1, int(C * density))``; at density 1.0 the topology is sequential,
+    otherwise random and seeded from ``hash((out_features, in_features))`` so
+    that layers of equal shape start with the same topology, as in the
+    reference (``mlp.py:84-95``).
+    """
+
+    def __init__(self, out_features: int, in_features: int, tile_size: int = 16, density: float = 1.0,
+                 dtype: torch.dtype = torch.bfloat16, bias: bool = True, device=None):
+        super().__init__()
+        B = tile_size
+        if out_features % B or in_features % B:
+            raise ValueError("features must be multiples of tile_size")
+        self.out_features, self.in_features, self.tile_size = out_features, in_features, B
+        self.density, self.dtype = density, dtype
+        self.R, self.C = out_features // B, in_features // B
+        self.K = max(1, int(self.C * density))
+        self.values = nn.Parameter(torch.randn(self.R, self.K, B, B, device=device) * 0.02)
+        self.bias = nn.Parameter(torch.zeros(out_features, device=device)) if bias else None
+        self.register_buffer("col_indices", self._init_topology().to(device))
+        self.register_buffer("alive_mask", torch.ones(self.R, self.K, dtype=torch.bool, device=device))
+        self._eff_cache = None
+
+    def _init_topology(self) -> torch.Tensor:
+        if self.density >= 1.0:
+            return torch.arange(self.C, dtype=torch.int32).repeat(self.R, 1)[:, :self.K].contiguous()
+        seed = hash((self.out_features, self.in_features)) % 2 ** 31
+        return create_random_topology(self.R, self.C, self.K, seed)
+
+    @property
+    def config(self) -> BlockELLConfig:
+        return BlockELLConfig(R=self.R, C=self.C, K=self.K, B=self.tile_size)
+
+    def effective_col_indices(self) -> torch.Tensor:
+        """col_indices with dead tiles (alive_mask False) set to the -1 sentinel (cached per version)."""
+        key = (self.col_indices.data_ptr(), self.col_indices._version, self.alive_mask.data_ptr(),
+               self.alive_mask._version)
+        if self._eff_cache is None or self._eff_cache[0] != key:
+            eff = torch.where(self.alive_mask, self.col_indices, torch.full_like(self.col_indices, -1))
+            self._eff_cache = (key, eff.to(torch.int32).contiguous())
+        return self._eff_cache[1]
+
+    def kernel_values(self) -> torch.Tensor:
+        return self.values.to(torch.bfloat16)
+
+    def as_block_ell(self) -> BlockELLTensor:
+        return BlockELLTensor(self.kernel_values(), self.effective_col_indices(), self.config)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return kernels.block_ell_matmul(x, self.kernel_values(), self.effective_col_indices(), self.bias)
+
+
+class MLPBlock(nn.Module):
+    """Block-ELL MLP (reference ``mlp.py:98-168``).
+
+    SwiGLU: ``out = w_down(silu(w_gate(x)) * w_up(x))`` as one fused operator.
+    GELU:   ``out = fc2(gelu(fc1(x)))`` with two Block-ELL products.
+    """
+
+    def __init__(self, d_model: int, d_ff: int, use_swiglu: bool = False, dropout: float = 0.0,
+                 tile_size: int = 16, density: float = 1.0, dtype: torch.dtype = torch.bfloat16, device=None):
+        super().__init__()
+        self.d_model, self.d_ff, self.use_swiglu, self.dropout = d_model, d_ff, use_swiglu, dropout
+        kw = dict(tile_size=tile_size, density=density, dtype=dtype, device=device)
+        if use_swiglu:
+            self.w_gate = BlockELLLinear(d_ff, d_model, bias=False, **kw)
+            self.w_up = BlockELLLinear(d_ff, d_model, bias=False, **kw)
+            self.w_down = BlockELLLinear(d_model, d_ff, bias=False, **kw)
+        else:
+            self.fc1 = BlockELLLinear(d_ff, d_model, **kw)
+            self.fc2 = BlockELLLinear(d_model, d_ff, **kw)
+
+    def swiglu_weights(self):
+        """(v_gate, ci_gate, v_up, ci_up, v_down, ci_down) in kernel form."""
+        out = []
+        for lin in (self.w_gate, self.w_up, self.w_down):
+            out += [lin.kernel_values(), lin.effective_col_indices()]
+        return tuple(out)
+
+    def forward(self, x: torch.Tensor, deterministic: bool = True) -> torch.Tensor:
+        lead = x.shape[:-1]
+        if self.use_swiglu:
+            x2 = x.reshape(-1, self.d_model).to(torch.bfloat16).contiguous()
+            out = kernels.swiglu_fwd(x2, *self.swiglu_weights(), add_residual=False).reshape(*lead, self.d_model)
+        else:
+            out = self.fc2(F.gelu(self.fc1(x).float()).to(torch.bfloat16))
+        if self.dropout > 0.0 and not deterministic:
+            out = F.dropout(out, p=self.dropout, training=True)
+        return out

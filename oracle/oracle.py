@@ -336,7 +336,7 @@ def ternary_fixed_point(scales: np.ndarray, col_indices: np.ndarray, B: int):
     with integer ``m`` small enough that ``sum_k m * P`` cannot overflow int32
     for any int8 input: ``m_max = floor((2**31 - 1) / (K_alive * B * 128))``
     capped at ``2**16 - 1``; ``e[r]`` is the largest integer with
-    ``max_k s[r,k] * 2**e <= m_max``; ``m = rint(s * 2**e)``.
+    ``max_k |s[r,k]| * 2**e <= m_max``; ``m = rint(s * 2**e)``.
     Returns ``(m int64 [R,K], e int64 [R])``.  Rows with no live block get e = 0.
     """
     s = np.asarray(scales, dtype=np.float32)
@@ -348,9 +348,10 @@ def ternary_fixed_point(scales: np.ndarray, col_indices: np.ndarray, B: int):
         ka = int(alive[r].sum())
         if ka == 0:
             continue
-        mmax = min((2 ** 31 - 1) // (ka * B * 128), 2 ** 16 - 1)
-        smax = float(np.max(np.where(alive[r], s[r], 0)))
-        if smax <= 0.0:
+        mmax = max(1, min((2 ** 31 - 1) // (ka * B * 128), 2 ** 16 - 1))
+        smax = float(np.max(np.where(alive[r], np.abs(s[r]), 0)))
+        if not (0.0 < smax < math.inf):
+            m[r] = np.where(alive[r], np.rint(s[r].astype(np.float64)), 0).astype(np.int64)
             continue
         er = math.floor(math.log2(mmax / smax))
         while smax * 2.0 ** er > mmax:

@@ -1,0 +1,154 @@
+"""Shared helpers for the tests: seeded synthetic inputs and C-ABI calls.
+
+GPU parity tests call the kernels through the C ABI (ctypes over liblbk.so)
+with device memory owned by torch, and compare against the CPU oracle.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from oracle import oracle as O
+
+
+# ------------------------------------------------------------------ inputs
+
+def bell_weight(rng, R, C_, K, B, std=0.02, sentinel=()):
+    """(values float32 bf16-representable [R,K,B,B], col int32 [R,K]) with optional dead slots."""
+    vals = O.bf16_round((rng.standard_normal((R, K, B, B)) * std).astype(np.float32))
+    col = O.random_topology(R, C_, K, rng)
+    for (r, k) in sentinel:
+        col[r, k] = -1
+    return vals, col
+
+
+def ffn_weights(rng, d_model, d_ff, B, density, sentinel_frac=0.0, std=0.02):
+    Cm, Cf = d_model // B, d_ff // B
+    Kg = O.k_for_density(Cm, density)
+    Kd = O.k_for_density(Cf, density)
+    Rf, Rm = d_ff // B, d_model // B
+    g = bell_weight(rng, Rf, Cm, Kg, B, std)
+    u = bell_weight(rng, Rf, Cm, Kg, B, std)
+    d = bell_weight(rng, Rm, Cf, Kd, B, std)
+    if sentinel_frac > 0:
+        for w in (g, u, d):
+            mask = rng.random(w[1].shape) < sentinel_frac
+            w[1][mask] = -1
+    return g, u, d
+
+
+def act(rng, N, F):
+    return O.bf16_round(rng.standard_normal((N, F)).astype(np.float32))
+
+
+def rel_err(y, ref):
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    den = max(np.abs(ref).max(), 1e-30)
+    return float(np.abs(y - ref).max() / den), float(np.abs(y - ref).max())
+
+
+# ------------------------------------------------------------------ torch <-> numpy
+
+def to_gpu_bf16(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(torch.bfloat16).cuda()
+
+
+def to_gpu(a, dtype=None):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.cuda()
+
+
+def to_np(t):
+    import torch
+    if t.dtype == torch.bfloat16:
+        t = t.float()
+    return t.detach().cpu().numpy()
+
+
+# ------------------------------------------------------------------ C ABI through ctypes
+
+def abi():
+    from looped_blockell import abi as A
+    A.load()
+    return A
+
+
+def stream():
+    import torch
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def ptr(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else C.c_void_p(0)
+
+
+def bell_struct(vals_t, col_t):
+    A = abi()
+    R, K, B, _ = vals_t.shape
+    return A.Bell(vals_t.data_ptr(), col_t.data_ptr(), R, K, B)
+
+
+def tern_struct(packed_t, scales_t, col_t):
+    A = abi()
+    R, K, B, _ = packed_t.shape
+    return A.BellTernary(packed_t.data_ptr(), scales_t.data_ptr(), col_t.data_ptr(), R, K, B)
+
+
+def gpu_weight(w):
+    import torch
+    vals, col = w
+    return to_gpu_bf16(vals), to_gpu(col.astype(np.int32))
+
+
+def abi_matmul(x_t, w_t, bias_t=None):
+    import torch
+    A = abi()
+    vals_t, col_t = w_t
+    N, F = x_t.shape
+    R, K, B, _ = vals_t.shape
+    y = torch.empty(N, R * B, dtype=torch.bfloat16, device=x_t.device)
+    wb = bell_struct(vals_t, col_t)
+    A.check(A.load().lbk_block_ell_matmul_bf16(ptr(x_t), N, F, F, C.byref(wb), ptr(bias_t), ptr(y), R * B,
+                                               stream()), "matmul")
+    return y
+
+
+def abi_swiglu(x_t, g_t, u_t, d_t, add_residual=False, intermediates=False):
+    import torch
+    A = abi()
+    lib = A.load()
+    N, dm = x_t.shape
+    gb, ub, db = bell_struct(*g_t), bell_struct(*u_t), bell_struct(*d_t)
+    d_ff = g_t[0].shape[0] * g_t[0].shape[2]
+    out = torch.empty(N, dm, dtype=torch.bfloat16, device=x_t.device)
+    h = gp = uo = None
+    if intermediates:
+        h, gp, uo = (torch.empty(N, d_ff, dtype=torch.bfloat16, device=x_t.device) for _ in range(3))
+    wsb = lib.lbk_swiglu_workspace_bytes(N, dm, C.byref(gb), C.byref(ub), C.byref(db), 1 if intermediates else 0)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x_t.device)
+    A.check(lib.lbk_swiglu_fwd_bf16(ptr(x_t), N, dm, C.byref(gb), C.byref(ub), C.byref(db),
+                                    1 if add_residual else 0, ptr(out), ptr(h), ptr(gp), ptr(uo),
+                                    ptr(ws) if wsb else C.c_void_p(0), wsb, stream()), "swiglu")
+    return out, h, gp, uo
+
+
+def abi_looped(h_t, scale_t, g_t, u_t, d_t, L, eps):
+    import torch
+    A = abi()
+    lib = A.load()
+    N, dm = h_t.shape
+    gb, ub, db = bell_struct(*g_t), bell_struct(*u_t), bell_struct(*d_t)
+    out = torch.empty_like(h_t)
+    wsb = lib.lbk_looped_workspace_bytes(N, dm, C.byref(gb), C.byref(ub), C.byref(db))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=h_t.device)
+    A.check(lib.lbk_looped_swiglu_bf16(ptr(h_t), N, dm, ptr(scale_t), C.c_float(eps), L, C.byref(gb), C.byref(ub),
+                                       C.byref(db), ptr(out), ptr(ws) if wsb else C.c_void_p(0), wsb, stream()),
+            "looped")
+    return out

@@ -1,0 +1,183 @@
+"""GPU parity of the bf16 Block-ELL kernels against the CPU oracle (through the C ABI).
+
+Tolerance (bf16 path): max|y - y_ref| <= 1e-2 * max|y_ref|, y_ref the oracle
+evaluated in float64 on the same bf16-rounded inputs; the absolute error is
+reported in the assertion message.
+"""
+
+import numpy as np
+import pytest
+
+import lbk_testlib as T
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+@pytest.mark.parametrize("B", [16, 32, 64])
+@pytest.mark.parametrize("N", [1, 5, 33, 64, 130])
+def test_matmul_parity(gpu, B, N):
+    rng = np.random.default_rng(100 + B + N)
+    R, C_, K = 5, 7, 3
+    _say(f"matmul B={B} N={N}")
+    w = T.bell_weight(rng, R, C_, K, B, sentinel=[(1, 2), (4, 0)])
+    x = T.act(rng, N, C_ * B)
+    bias = rng.standard_normal(R * B).astype(np.float32) * 0.1
+    y = T.to_np(T.abi_matmul(T.to_gpu_bf16(x), T.gpu_weight(w), T.to_gpu(bias)))
+    ref = O.block_ell_matmul(x.astype(np.float64), w[0].astype(np.float64), w[1]) + bias
+    rel, ab = T.rel_err(y, ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
+def test_matmul_density_one_equals_dense(gpu):
+    # reference tests/test_block_ell.py:42-54 on the GPU: Block-ELL at density 1.0 == x @ W.T
+    rng = np.random.default_rng(7)
+    W = O.bf16_round(rng.standard_normal((64, 128)).astype(np.float32))
+    v, c, _ = O.create_block_ell_from_dense(W, tile_size=32, density=1.0)
+    x = T.act(rng, 40, 128)
+    y = T.to_np(T.abi_matmul(T.to_gpu_bf16(x), (T.to_gpu_bf16(v), T.to_gpu(c))))
+    rel, ab = T.rel_err(y, x.astype(np.float64) @ W.T.astype(np.float64))
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
+def test_matmul_out_of_range_column_is_skipped(gpu):
+    rng = np.random.default_rng(8)
+    vals, col = T.bell_weight(rng, 3, 4, 2, 32)
+    col[0, 1] = 4            # == C: out of range, contributes nothing
+    col[2, 0] = 1000
+    x = T.act(rng, 9, 128)
+    y = T.to_np(T.abi_matmul(T.to_gpu_bf16(x), (T.to_gpu_bf16(vals), T.to_gpu(col))))
+    col_ref = col.copy()
+    col_ref[col_ref >= 4] = -1
+    ref = O.block_ell_matmul(x.astype(np.float64), vals.astype(np.float64), col_ref)
+    assert T.rel_err(y, ref)[0] <= TOL
+
+
+SWIGLU_CASES = [
+    # (d_model, d_ff, B, density, N, sentinel_frac)   panel path unless noted
+    (256, 1024, 16, 0.25, 512, 0.0),      # config-1 geometry
+    (256, 1024, 16, 0.25, 77, 0.1),       # ragged N, dead slots
+    (512, 1024, 32, 0.25, 130, 0.0),
+    (1024, 4096, 32, 0.25, 200, 0.05),    # config-2 geometry, small N
+    (128, 512, 64, 0.5, 70, 0.0),         # B = 64 -> general two-kernel path
+    (2048, 1024, 32, 0.125, 40, 0.0),     # d_model > 1024 -> general path
+]
+
+
+@pytest.mark.parametrize("case", SWIGLU_CASES)
+@pytest.mark.parametrize("resid", [False, True])
+def test_swiglu_parity(gpu, case, resid):
+    d_model, d_ff, B, dens, N, sf = case
+    _say(f"swiglu {case} resid={resid}")
+    rng = np.random.default_rng(hash(case) % 2 ** 31)
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, dens, sentinel_frac=sf)
+    x = T.act(rng, N, d_model)
+    out, *_ = T.abi_swiglu(T.to_gpu_bf16(x), T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d), add_residual=resid)
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref, *_ = O.swiglu_fwd(x.astype(np.float64), f64(g), f64(u), f64(d), add_residual=resid)
+    rel, ab = T.rel_err(T.to_np(out), ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
+@pytest.mark.parametrize("case", [(256, 1024, 16, 0.25, 100), (1024, 4096, 32, 0.25, 64), (128, 256, 64, 1.0, 33)])
+def test_swiglu_with_intermediates(gpu, case):
+    d_model, d_ff, B, dens, N = case
+    _say(f"swiglu intermediates {case}")
+    rng = np.random.default_rng(11)
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, dens)
+    x = T.act(rng, N, d_model)
+    out, h, gp, uo = T.abi_swiglu(T.to_gpu_bf16(x), T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d),
+                                  add_residual=False, intermediates=True)
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref, h_ref, g_ref, u_ref = O.swiglu_fwd(x.astype(np.float64), f64(g), f64(u), f64(d))
+    for got, want, name in ((out, ref, "out"), (h, h_ref, "h"), (gp, g_ref, "gate"), (uo, u_ref, "up")):
+        rel, ab = T.rel_err(T.to_np(got), want)
+        assert rel <= TOL, f"{name}: rel {rel} abs {ab}"
+
+
+def test_swiglu_full_config2_sampled_rows(gpu):
+    """Config 2 at full size (N=16384); rows are independent, so sampled rows are checked."""
+    rng = np.random.default_rng(1002)
+    d_model, d_ff, B, N = 1024, 4096, 32, 16384
+    _say("swiglu config-2 full size")
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25)
+    x = T.act(rng, N, d_model)
+    out, *_ = T.abi_swiglu(T.to_gpu_bf16(x), T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d))
+    out = T.to_np(out)
+    rows = np.sort(rng.choice(N, 384, replace=False))
+    rows = np.concatenate([rows, [0, N - 1]])
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref, *_ = O.swiglu_fwd(x[rows].astype(np.float64), f64(g), f64(u), f64(d))
+    rel, ab = T.rel_err(out[rows], ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+    assert np.isfinite(out).all()
+
+
+def test_swiglu_deterministic(gpu):
+    rng = np.random.default_rng(5)
+    g, u, d = T.ffn_weights(rng, 512, 2048, 32, 0.25)
+    x = T.to_gpu_bf16(T.act(rng, 300, 512))
+    ws = [T.gpu_weight(w) for w in (g, u, d)]
+    a = T.to_np(T.abi_swiglu(x, *ws)[0])
+    b = T.to_np(T.abi_swiglu(x, *ws)[0])
+    assert np.array_equal(a, b)
+
+
+LOOP_CASES = [
+    # (d_model, d_ff, B, density, N, L)
+    (256, 1024, 16, 0.25, 100, 3),
+    (1024, 4096, 32, 0.25, 130, 8),       # config-4 geometry
+    (128, 512, 64, 0.5, 40, 2),           # general path (per-iteration launches)
+]
+
+
+@pytest.mark.parametrize("case", LOOP_CASES)
+def test_looped_parity(gpu, case):
+    d_model, d_ff, B, dens, N, L = case
+    _say(f"looped {case}")
+    rng = np.random.default_rng(hash(case) % 2 ** 31)
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, dens)
+    h = T.act(rng, N, d_model)
+    scale = (1.0 + 0.1 * rng.standard_normal(d_model)).astype(np.float32)
+    out = T.abi_looped(T.to_gpu_bf16(h), T.to_gpu(scale), T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d), L,
+                       1e-5)
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref = O.looped_swiglu(h.astype(np.float64), scale.astype(np.float64), f64(g), f64(u), f64(d), L=L, eps=1e-5)
+    rel, ab = T.rel_err(T.to_np(out), ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
+def test_looped_config4_sampled_rows(gpu):
+    """Config 4 at full size (32 x 512 tokens, L = 8, norm scale ones); sampled rows vs the oracle."""
+    rng = np.random.default_rng(1004)
+    d_model, d_ff, B, N, L = 1024, 4096, 32, 32 * 512, 8
+    _say("looped config-4 full size")
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25)
+    h = T.act(rng, N, d_model)
+    scale = np.ones(d_model, np.float32)
+    out = T.to_np(T.abi_looped(T.to_gpu_bf16(h), T.to_gpu(scale), T.gpu_weight(g), T.gpu_weight(u),
+                               T.gpu_weight(d), L, 1e-5))
+    rows = np.sort(rng.choice(N, 128, replace=False))
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref = O.looped_swiglu(h[rows].astype(np.float64), scale.astype(np.float64), f64(g), f64(u), f64(d), L=L)
+    rel, ab = T.rel_err(out[rows], ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
+def test_looped_L0_and_L1(gpu):
+    rng = np.random.default_rng(9)
+    g, u, d = T.ffn_weights(rng, 256, 1024, 16, 0.25)
+    h = T.act(rng, 20, 256)
+    scale = np.ones(256, np.float32)
+    ws = [T.gpu_weight(w) for w in (g, u, d)]
+    o0 = T.to_np(T.abi_looped(T.to_gpu_bf16(h), T.to_gpu(scale), *ws, 0, 1e-5))
+    assert np.array_equal(o0, h)
+    o1 = T.to_np(T.abi_looped(T.to_gpu_bf16(h), T.to_gpu(scale), *ws, 1, 1e-5))
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref = h + O.swiglu_fwd(O.rmsnorm(h.astype(np.float64), np.ones(256)), f64(g), f64(u), f64(d))[0]
+    assert T.rel_err(o1, ref)[0] <= TOL

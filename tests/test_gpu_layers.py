@@ -1,0 +1,161 @@
+"""GPU tests of the torch-facing API: layer modules, titan:: operators and their
+error behaviour, checked against the CPU oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+import lbk_testlib as T
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def f64(w):
+    return (w[0].astype(np.float64), w[1])
+
+
+def test_titan_swiglu_ops_match_oracle(gpu):
+    from looped_blockell import kernels
+    rng = np.random.default_rng(21)
+    g, u, d = T.ffn_weights(rng, 1024, 4096, 32, 0.25)
+    x = T.act(rng, 96, 1024)
+    ws = [t for w in (g, u, d) for t in T.gpu_weight(w)]
+    out = kernels.swiglu_fwd(T.to_gpu_bf16(x), *ws, add_residual=True)
+    ref, h_ref, g_ref, u_ref = O.swiglu_fwd(x.astype(np.float64), f64(g), f64(u), f64(d), add_residual=True)
+    assert T.rel_err(T.to_np(out), ref)[0] <= TOL
+    r, h, gp, uo = kernels.swiglu_fwd_with_intermediate(T.to_gpu_bf16(x), *ws, add_residual=True)
+    for got, want in ((r, ref), (h, h_ref), (gp, g_ref), (uo, u_ref)):
+        assert T.rel_err(T.to_np(got), want)[0] <= TOL
+
+
+def test_mlpblock_layer(gpu):
+    from looped_blockell.layers import MLPBlock
+    torch.manual_seed(0)
+    m = MLPBlock(256, 1024, use_swiglu=True, tile_size=16, density=0.25, device="cuda")
+    m.w_down.alive_mask[3, 2] = False           # a pruned tile
+    x = torch.randn(2, 50, 256, device="cuda").to(torch.bfloat16)
+    y = m(x)
+    assert y.shape == (2, 50, 256) and y.dtype == torch.bfloat16
+
+    def w(lin):
+        col = lin.col_indices.cpu().numpy().copy()
+        col[~lin.alive_mask.cpu().numpy()] = -1
+        return lin.values.detach().to(torch.bfloat16).float().cpu().numpy().astype(np.float64), col
+
+    ref, *_ = O.swiglu_fwd(T.to_np(x).reshape(100, 256).astype(np.float64), w(m.w_gate), w(m.w_up), w(m.w_down))
+    assert T.rel_err(T.to_np(y).reshape(100, 256), ref)[0] <= TOL
+
+
+def test_gelu_mlpblock_and_linear_bias(gpu):
+    from looped_blockell.layers import BlockELLLinear, MLPBlock
+    torch.manual_seed(1)
+    lin = BlockELLLinear(128, 256, tile_size=32, density=0.5, device="cuda")
+    with torch.no_grad():
+        lin.bias.copy_(torch.randn(128) * 0.1)
+    x = torch.randn(7, 256, device="cuda").to(torch.bfloat16)
+    y = lin(x)
+    ref = O.block_ell_matmul(T.to_np(x).astype(np.float64),
+                             lin.values.detach().to(torch.bfloat16).float().cpu().numpy().astype(np.float64),
+                             lin.col_indices.cpu().numpy()) + lin.bias.detach().cpu().numpy()
+    assert T.rel_err(T.to_np(y), ref)[0] <= TOL
+    m = MLPBlock(128, 512, use_swiglu=False, tile_size=16, density=1.0, device="cuda")
+    assert m(x[:, :128].contiguous()).shape == (7, 128)
+
+
+def test_rmsnorm_and_injection_ops(gpu):
+    from looped_blockell import kernels
+    from looped_blockell.layers import RMSNorm
+    rng = np.random.default_rng(22)
+    x = T.act(rng, 33, 1024)
+    norm = RMSNorm(1024, device="cuda")
+    with torch.no_grad():
+        norm.scale.copy_(torch.from_numpy((1 + 0.1 * rng.standard_normal(1024)).astype(np.float32)))
+    y = norm(T.to_gpu_bf16(x))
+    ref = O.rmsnorm(x.astype(np.float64), norm.scale.detach().cpu().numpy().astype(np.float64), 1e-5)
+    assert T.rel_err(T.to_np(y), ref)[0] <= TOL
+    e = T.act(rng, 33, 1024)
+    la = (0.3 * rng.standard_normal(1024)).astype(np.float32)
+    ld = (0.5 * rng.standard_normal(1024)).astype(np.float32)
+    hi = kernels.diagonal_injection(T.to_gpu_bf16(x), T.to_gpu_bf16(e), T.to_gpu(la), T.to_gpu(ld))
+    dt = np.log1p(np.exp(ld.astype(np.float64)))
+    ref = np.exp(-dt * np.exp(la.astype(np.float64))) * x + dt * e        # interop/pt_model.py:930-935
+    assert T.rel_err(T.to_np(hi), ref)[0] <= TOL
+
+
+def test_persistent_mlp_step_matches_reference_semantics(gpu):
+    from looped_blockell import kernels
+    rng = np.random.default_rng(23)
+    d_model, d_ff, B, N = 256, 1024, 16, 70
+    blocks = [T.ffn_weights(rng, d_model, d_ff, B, 0.25) for _ in range(2)]
+    scales = [(1 + 0.1 * rng.standard_normal(d_model)).astype(np.float32) for _ in range(2)]
+    h, e = T.act(rng, N, d_model), T.act(rng, N, d_model)
+    la = (0.2 * rng.standard_normal(d_model)).astype(np.float32)
+    ld = (0.2 * rng.standard_normal(d_model)).astype(np.float32)
+    gw = [[T.gpu_weight(w) for w in blk] for blk in blocks]
+    out = kernels.persistent_mlp_step(
+        T.to_gpu_bf16(h), T.to_gpu_bf16(e), T.to_gpu(la), T.to_gpu(ld), [T.to_gpu_bf16(s) for s in scales],
+        [b[0][0] for b in gw], [b[0][1] for b in gw], [b[1][0] for b in gw], [b[1][1] for b in gw],
+        [b[2][0] for b in gw], [b[2][1] for b in gw])
+    # reference: csrc/loop/persistent_core.cu:273-338 (injection once, then per core block, eps 1e-6)
+    dt = np.log1p(np.exp(ld.astype(np.float64)))
+    cur = np.exp(-dt * np.exp(la.astype(np.float64))) * h + dt * e
+    for blk, s in zip(blocks, scales):
+        sb = O.bf16_round(s).astype(np.float64)
+        cur = cur + O.swiglu_fwd(O.rmsnorm(cur, sb, 1e-6), *(f64(w) for w in blk))[0]
+    assert T.rel_err(T.to_np(out), cur)[0] <= TOL
+    kernels.pin_weights_l2([b[0][0] for b in gw])      # no-ops kept for API compatibility
+    kernels.unpin_weights_l2()
+
+
+def test_looped_layer(gpu):
+    from looped_blockell.layers import LoopedSwiGLU
+    torch.manual_seed(2)
+    m = LoopedSwiGLU(1024, 4096, L=4, tile_size=32, density=0.25, device="cuda")
+    h = torch.randn(3, 40, 1024, device="cuda").to(torch.bfloat16)
+    y = m(h)
+    mlp = m.mlp
+
+    def w(lin):
+        return lin.values.detach().to(torch.bfloat16).float().cpu().numpy().astype(np.float64), lin.col_indices.cpu().numpy()
+
+    ref = O.looped_swiglu(T.to_np(h).reshape(120, 1024).astype(np.float64), np.ones(1024), w(mlp.w_gate),
+                          w(mlp.w_up), w(mlp.w_down), L=4, eps=1e-5)
+    assert T.rel_err(T.to_np(y).reshape(120, 1024), ref)[0] <= TOL
+
+
+def test_ternary_layer(gpu):
+    from looped_blockell.layers import TernaryMLPBlock
+    m = TernaryMLPBlock.random(512, 2048, 64, 0.125, device="cuda", seed=4)
+    x = torch.randn(2, 30, 512, device="cuda").to(torch.bfloat16)
+    y = m(x)
+    assert y.shape == x.shape and torch.isfinite(y.float()).all()
+
+    def w(tw):
+        packed = tw.packed.cpu().numpy().view(np.uint32)
+        return O.unpack_ternary(packed), tw.scales.cpu().numpy(), tw.col_indices.cpu().numpy()
+
+    ref = O.ternary_swiglu_fwd(T.to_np(x).reshape(60, 512), w(m.w_gate), w(m.w_up), w(m.w_down),
+                               exact_scales=True, h_round=O.bf16_round)
+    assert T.rel_err(T.to_np(y).reshape(60, 512), ref["out"])[0] <= TOL
+
+
+def test_op_errors(gpu):
+    from looped_blockell import kernels
+    x = torch.zeros(4, 64, device="cuda", dtype=torch.bfloat16)
+    v = torch.zeros(2, 2, 32, 32, device="cuda", dtype=torch.bfloat16)
+    c = torch.zeros(2, 2, device="cuda", dtype=torch.int32)
+    with pytest.raises(RuntimeError):          # fp32 values
+        kernels.block_ell_matmul(x, v.float(), c)
+    with pytest.raises(RuntimeError):          # int64 columns
+        kernels.block_ell_matmul(x, v, c.long())
+    with pytest.raises(RuntimeError):          # B = 24
+        kernels.block_ell_matmul(torch.zeros(4, 48, device="cuda", dtype=torch.bfloat16),
+                                 torch.zeros(2, 2, 24, 24, device="cuda", dtype=torch.bfloat16), c)
+    with pytest.raises(RuntimeError):          # down inconsistent with d_model
+        kernels.swiglu_fwd(x, v, c, v, c, v, c)
+    bad = kernels.check_columns(torch.tensor([[0, 1], [-1, 7], [2, -3]], device="cuda", dtype=torch.int32), 4)
+    assert int(bad) == 2
+    empty = kernels.block_ell_matmul(torch.zeros(0, 64, device="cuda", dtype=torch.bfloat16), v, c)
+    assert empty.shape == (0, 64)

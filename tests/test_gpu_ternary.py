@@ -1,0 +1,178 @@
+"""GPU parity of the int8 / ternary kernels against the CPU oracle.
+
+Bars: activation quantisation (xq, sx) bit-exact; packing bit-exact; the int32
+block partials bit-exact; the fixed-point scaled products bit-exact against the
+oracle's restatement of the same fixed-point arithmetic; outputs within
+1e-2 * max|ref| of the exact-scale (float64) oracle.
+"""
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import lbk_testlib as T
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def tern_weight(rng, R, C_, K, B, sentinel_frac=0.0):
+    t = rng.integers(-1, 2, size=(R, K, B, B)).astype(np.int8)
+    lat = rng.standard_normal((R, K, B, B)).astype(np.float32) * 0.02
+    s = np.maximum(np.mean(np.abs(lat.reshape(R, K, -1)), axis=2), 1e-8).astype(np.float32)
+    col = O.random_topology(R, C_, K, rng)
+    if sentinel_frac:
+        col[rng.random(col.shape) < sentinel_frac] = -1
+    return t, s, col
+
+
+def gpu_tern(w):
+    import torch
+    t, s, col = w
+    packed = O.pack_ternary(t).view(np.int32)
+    return T.to_gpu(packed), T.to_gpu(s), T.to_gpu(col.astype(np.int32))
+
+
+def test_quantize_act_bit_exact(gpu):
+    from looped_blockell import kernels
+    rng = np.random.default_rng(1)
+    x = T.act(rng, 300, 2048)
+    x[0] = 0.0                                   # absmax clamp row
+    x[1, :4] = [2.0, 1.0 / 64, -3.0 / 64, 0.0]   # ties at scale 64
+    x[1, 4:] = 0.0
+    q, s = kernels.quantize_act_int8(T.to_gpu_bf16(x))
+    q_ref, s_ref = O.activation_quantize_int8(x)
+    assert np.array_equal(T.to_np(q), q_ref)
+    assert np.array_equal(T.to_np(s), s_ref)
+
+
+def test_pack_bit_exact(gpu):
+    from looped_blockell import kernels
+    rng = np.random.default_rng(2)
+    for B in (16, 32, 64):
+        t = rng.integers(-1, 2, size=(3, 2, B, B)).astype(np.int8)
+        p = T.to_np(kernels.pack_ternary(T.to_gpu(t))).view(np.uint32)
+        assert np.array_equal(p, O.pack_ternary(t)), B
+
+
+def test_ternary_quantize_weights(gpu):
+    from looped_blockell import kernels
+    rng = np.random.default_rng(3)
+    v = T.act(rng, 4 * 3 * 64, 64).reshape(4, 3, 64, 64) * 0.02
+    v = O.bf16_round(v)
+    p, s = kernels.ternary_quantize_weights(T.to_gpu_bf16(v))
+    s = T.to_np(s)
+    t_ref, s_ref = O.ternary_quantize_blocks(v)
+    np.testing.assert_allclose(s, s_ref, rtol=1e-6)
+    # codes bit-exact given the kernel's own scale
+    t_given = np.clip(np.rint(v.reshape(12, -1) / s.reshape(12, 1)), -1, 1).astype(np.int8).reshape(v.shape)
+    assert np.array_equal(O.unpack_ternary(T.to_np(p).view(np.uint32)), t_given)
+
+
+@pytest.mark.parametrize("B", [16, 32, 64])
+@pytest.mark.parametrize("N", [1, 37, 128])
+def test_ternary_matmul_partials_and_scaling(gpu, B, N):
+    from looped_blockell import kernels
+    _say(f"ternary matmul B={B} N={N}")
+    rng = np.random.default_rng(10 + B + N)
+    R, C_, K = 4, 6, 3
+    w = tern_weight(rng, R, C_, K, B, sentinel_frac=0.15)
+    x = T.act(rng, N, C_ * B)
+    xq, sx = O.activation_quantize_int8(x)
+    y, part = kernels.ternary_matmul(T.to_gpu(xq), T.to_gpu(sx), *gpu_tern(w), want_partials=True)
+    P_ref = O.ternary_block_partials(xq, w[0], w[2])
+    assert np.array_equal(T.to_np(part).astype(np.int64), P_ref)
+    # fixed-point scaled product: bit-exact before the bf16 output rounding
+    y_fix, _ = O.ternary_matmul(xq, sx, w[0], w[1], w[2], exact_scales=False)
+    assert np.array_equal(T.to_np(y), O.bf16_round(y_fix))
+    y_exact, _ = O.ternary_matmul(xq, sx, w[0], w[1], w[2], exact_scales=True)
+    assert T.rel_err(T.to_np(y), y_exact)[0] <= TOL
+
+
+def test_ternary_extreme_partials(gpu):
+    """All-(-128) activations against all-(-1) tiles: P = B*128 per block, no overflow."""
+    from looped_blockell import kernels
+    B, K, R, C_ = 64, 16, 2, 16
+    t = -np.ones((R, K, B, B), np.int8)
+    s = np.full((R, K), 0.02, np.float32)
+    col = np.tile(np.arange(K, dtype=np.int32), (R, 1))
+    xq = np.full((3, C_ * B), -128, np.int8)
+    sx = np.ones(3, np.float32)
+    y, part = kernels.ternary_matmul(T.to_gpu(xq), T.to_gpu(sx), *gpu_tern((t, s, col)), want_partials=True)
+    assert (T.to_np(part) == B * 128).all()
+    y_fix, acc = O.ternary_matmul(xq, sx, t, s, col, exact_scales=False)
+    assert np.array_equal(T.to_np(y), O.bf16_round(y_fix))
+
+
+TERN_CASES = [
+    # (d_model, d_ff, B, density, N)
+    (512, 2048, 64, 0.125, 100),
+    (256, 1024, 32, 0.25, 65),
+    (128, 512, 16, 0.25, 33),
+    (2048, 8192, 64, 0.125, 64),    # config-3 geometry, small N
+]
+
+
+@pytest.mark.parametrize("case", TERN_CASES)
+@pytest.mark.parametrize("resid", [False, True])
+def test_ternary_swiglu(gpu, case, resid):
+    from looped_blockell import kernels
+    d_model, d_ff, B, dens, N = case
+    _say(f"ternary swiglu {case} resid={resid}")
+    rng = np.random.default_rng(hash(case) % 2 ** 31)
+    Kg, Kd = O.k_for_density(d_model // B, dens), O.k_for_density(d_ff // B, dens)
+    g = tern_weight(rng, d_ff // B, d_model // B, Kg, B)
+    u = tern_weight(rng, d_ff // B, d_model // B, Kg, B)
+    d = tern_weight(rng, d_model // B, d_ff // B, Kd, B)
+    x = T.act(rng, N, d_model)
+    xq, sx = O.activation_quantize_int8(x)
+    xg = T.to_gpu_bf16(x)
+    out, h, hq, sh = kernels.ternary_swiglu_fwd_with_intermediate(
+        T.to_gpu(xq), T.to_gpu(sx), gpu_tern(g), gpu_tern(u), gpu_tern(d), xg if resid else None)
+    out, h, hq, sh = T.to_np(out), T.to_np(h), T.to_np(hq), T.to_np(sh)
+    # h re-quantisation is bit-exact given the kernel's h
+    hq_ref, sh_ref = O.activation_quantize_int8(h)
+    assert np.array_equal(hq, hq_ref) and np.array_equal(sh, sh_ref)
+    # gate/up: fixed-point products are bit-exact; h within tolerance (SiLU uses the device exp)
+    gf, _ = O.ternary_matmul(xq, sx, *g, exact_scales=False)
+    uf, _ = O.ternary_matmul(xq, sx, *u, exact_scales=False)
+    assert T.rel_err(h, O.bf16_round(O.silu(gf.astype(np.float64)) * uf))[0] <= TOL
+    # down: bit-exact given the kernel's hq (plus the residual in fp32)
+    yd, _ = O.ternary_matmul(hq, sh, *d, exact_scales=False)
+    if resid:
+        yd = (yd + x).astype(np.float32)
+    assert np.array_equal(out, O.bf16_round(yd))
+    # whole FFN against the exact-scale oracle
+    ref = O.ternary_swiglu_fwd(x, g, u, d, add_residual=resid, exact_scales=True, h_round=O.bf16_round)
+    rel, ab = T.rel_err(out, ref["out"])
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
+def test_ternary_config3_full_sampled_rows(gpu):
+    """Config 3 at full size (N=8192); bit-exact checks on sampled rows."""
+    from looped_blockell import kernels
+    _say("ternary config-3 full size")
+    rng = np.random.default_rng(1003)
+    d_model, d_ff, B, N = 2048, 8192, 64, 8192
+    g = tern_weight(rng, d_ff // B, d_model // B, 4, B)
+    u = tern_weight(rng, d_ff // B, d_model // B, 4, B)
+    d = tern_weight(rng, d_model // B, d_ff // B, 16, B)
+    x = T.act(rng, N, d_model)
+    xg = T.to_gpu_bf16(x)
+    xq_t, sx_t = kernels.quantize_act_int8(xg)
+    out, h, hq, sh = kernels.ternary_swiglu_fwd_with_intermediate(xq_t, sx_t, gpu_tern(g), gpu_tern(u),
+                                                                  gpu_tern(d))
+    rows = np.sort(rng.choice(N, 256, replace=False))
+    xq, sx = O.activation_quantize_int8(x[rows])
+    assert np.array_equal(T.to_np(xq_t)[rows], xq) and np.array_equal(T.to_np(sx_t)[rows], sx)
+    hq_r, sh_r = T.to_np(hq)[rows], T.to_np(sh)[rows]
+    yd, _ = O.ternary_matmul(hq_r, sh_r, *d, exact_scales=False)
+    assert np.array_equal(T.to_np(out)[rows], O.bf16_round(yd))
+    ref = O.ternary_swiglu_fwd(x[rows], g, u, d, exact_scales=True, h_round=O.bf16_round)
+    assert T.rel_err(T.to_np(out)[rows], ref["out"])[0] <= TOL
