@@ -153,8 +153,10 @@ def test_op_errors(gpu):
     with pytest.raises(RuntimeError):          # B = 24
         kernels.block_ell_matmul(torch.zeros(4, 48, device="cuda", dtype=torch.bfloat16),
                                  torch.zeros(2, 2, 24, 24, device="cuda", dtype=torch.bfloat16), c)
-    with pytest.raises(RuntimeError):          # down inconsistent with d_model
-        kernels.swiglu_fwd(x, v, c, v, c, v, c)
+    v3 = torch.zeros(3, 2, 32, 32, device="cuda", dtype=torch.bfloat16)
+    c3 = torch.zeros(3, 2, device="cuda", dtype=torch.int32)
+    with pytest.raises(RuntimeError):          # down R*B = 96 inconsistent with d_model = 64
+        kernels.swiglu_fwd(x, v, c, v, c, v3, c3)
     bad = kernels.check_columns(torch.tensor([[0, 1], [-1, 7], [2, -3]], device="cuda", dtype=torch.int32), 4)
     assert int(bad) == 2
     empty = kernels.block_ell_matmul(torch.zeros(0, 64, device="cuda", dtype=torch.bfloat16), v, c)
