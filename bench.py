@@ -147,7 +147,7 @@ def bench_bf16(steps, warmup, device):
         kernel_ms_avg=kern_ms, kernel_ms_median=median(per),
         roofline=dict(bound="mfma", achieved=achieved, peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
                       frac=achieved / PEAK_BF16_TFLOPS, traffic=None,
-                      kernel="panel_kernel<32,8,false> (fused gate/up + SiLU*mul + down, one launch per step)",
+                      kernel="gu_kernel<32,4,false> + dn_kernel<32,4,4> (gate/up + SiLU*mul, then down; one launch pair per step)",
                       algorithmic_flops_per_launch=flops,
                       algorithmic_bytes_per_launch=algorithmic_bytes(w)),
     )

@@ -24,16 +24,21 @@ PKG = os.path.join(HERE, "looped_blockell")
 LIB = os.path.join(PKG, "liblbk.so")
 EXT = os.path.join(PKG, "_titan_ext.so")
 
-HIP_SOURCES = ["lbk_bf16.hip", "lbk_ternary.hip", "lbk_abi.hip"]
+HIP_SOURCES = ["lbk_bf16.hip", "lbk_split.hip", "lbk_ternary.hip", "lbk_abi.hip"]
 ARCH = os.environ.get("LBK_OFFLOAD_ARCH", "gfx950")
 
-# Packed-fp32 VALU forms are kept out of the generated code; MFMA results are
-# kept in VGPR form so loop-carried accumulators are not shuffled through AGPRs.
+# Packed-fp32 VALU forms are kept out of the generated code.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
+# Per-file extras.  VGPR-form MFMA keeps small loop-carried accumulators out of
+# AGPR shuffles (the row-block kernels); the split SwiGLU kernels are left to the
+# default allocator.
+FILE_FLAGS = {
+    "lbk_bf16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "lbk_ternary.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
 
 
 def _run(cmd: list[str]) -> None:
@@ -54,9 +59,16 @@ def hipcc() -> str:
 
 
 def build_lib() -> str:
-    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    objs = []
+    for src in HIP_SOURCES:
+        obj = os.path.join(objdir, src.replace(".hip", ".o"))
+        _run([hipcc(), *HIP_FLAGS, *FILE_FLAGS.get(src, []), f"-I{INCLUDE}", f"-I{CSRC}", "-c",
+              os.path.join(CSRC, src), "-o", obj])
+        objs.append(obj)
     tmp = LIB + ".tmp"
-    _run([hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", tmp])
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, LIB)
     return LIB
 

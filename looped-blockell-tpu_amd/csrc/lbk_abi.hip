@@ -112,16 +112,34 @@ int lbk_block_ell_matmul_bf16(const uint16_t* x, int64_t N, int32_t in_features,
   return launch_rowblock(w->B, 0, a, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
 }
 
-static bool use_panel(const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, int32_t d_model) {
-  (void)up;
-  return panel_supported(gate->B, d_model, gate->R, down->R, down->K);
+static bool use_split(const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, int32_t d_model) {
+  return split_supported(gate->B, d_model, gate->R, down->R, gate->K, up->K, down->K);
+}
+
+static int swiglu_split(const uint16_t* x, const float* xf, const float* norm_scale, float eps, int64_t N,
+                        int32_t d_model, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                        const uint16_t* resid, float* state, uint16_t* out, uint16_t* h, uint16_t* gate_pre,
+                        uint16_t* up_out, hipStream_t st) {
+  GUArgs g{};
+  g.x = x; g.xf = xf; g.N = N; g.d_model = d_model; g.norm_scale = norm_scale; g.eps = eps;
+  g.vg = gate->values; g.cg = gate->col_idx; g.Kg = gate->K;
+  g.vu = up->values; g.cu = up->col_idx; g.Ku = up->K;
+  g.R_ff = gate->R;
+  g.h = h; g.gpre = gate_pre; g.uout = up_out;
+  if (launch_gu(gate->B, xf != nullptr, g, st) != 0) return LBK_ERR_LAUNCH;
+  DNArgs d{};
+  d.h = h; d.N = N; d.d_ff = (int64_t)gate->R * gate->B; d.d_model = d_model;
+  d.vd = down->values; d.cd = down->col_idx; d.Kd = down->K;
+  d.R_m = down->R; d.C_d = gate->R;
+  d.resid = resid; d.state = state; d.out = out;
+  return launch_dn(gate->B, d, st) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
 }
 
 size_t lbk_swiglu_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
                                   const lbk_bell* down, int want_intermediates) {
+  (void)d_model;
   if (!gate || !up || !down || N <= 0) return 0;
   if (want_intermediates) return 0;  // h goes to the caller's h_out
-  if (use_panel(gate, up, down, d_model)) return 0;
   return align256((size_t)N * gate->R * gate->B * 2);
 }
 
@@ -139,20 +157,6 @@ int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk
   if (!a16(x) || !a16(out) || (d_model % 8)) return LBK_ERR_ALIGN;
   for (const void* p : {(const void*)h_out, (const void*)gate_pre_out, (const void*)up_out})
     if (p && !a16(p)) return LBK_ERR_ALIGN;
-  const bool inter = h_out || gate_pre_out || up_out;
-  if (!inter && use_panel(gate, up, down, d_model)) {
-    PanelArgs p{};
-    p.x = x; p.N = N; p.d_model = d_model;
-    p.vg = gate->values; p.cg = gate->col_idx; p.Kg = gate->K;
-    p.vu = up->values; p.cu = up->col_idx; p.Ku = up->K;
-    p.R_ff = gate->R;
-    p.vd = down->values; p.cd = down->col_idx; p.Kd = down->K;
-    p.R_m = down->R;
-    p.add_residual = add_residual ? 1 : 0;
-    p.L = 1; p.eps = 0.f; p.norm_scale = nullptr;
-    p.out = out;
-    return launch_panel(gate->B, false, p, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
-  }
   uint16_t* h = h_out;
   if (!h) {
     const size_t need = align256((size_t)N * d_ff * 2);
@@ -160,6 +164,9 @@ int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk
     if (!a16(workspace)) return LBK_ERR_ALIGN;
     h = static_cast<uint16_t*>(workspace);
   }
+  if (use_split(gate, up, down, d_model))
+    return swiglu_split(x, nullptr, nullptr, 0.f, N, d_model, gate, up, down, add_residual ? x : nullptr, nullptr,
+                        out, h, gate_pre_out, up_out, S(stream));
   return swiglu_general(x, N, d_model, gate, up, down, add_residual ? x : nullptr, out, h, gate_pre_out, up_out,
                         S(stream));
 }
@@ -182,9 +189,9 @@ int lbk_diagonal_injection_bf16(const uint16_t* h, const uint16_t* e, const floa
 
 size_t lbk_looped_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
                                   const lbk_bell* down) {
-  if (!gate || !up || !down || N <= 0) return 0;
-  if (use_panel(gate, up, down, d_model)) return 0;
-  return align256((size_t)N * d_model * 2) + align256((size_t)N * gate->R * gate->B * 2);
+  if (!gate || !up || !down || N <= 0 || d_model <= 0) return 0;
+  // fp32 carried state (or the bf16 normed copy on the general path) + h
+  return align256((size_t)N * d_model * 4) + align256((size_t)N * gate->R * gate->B * 2);
 }
 
 int lbk_looped_swiglu_bf16(const uint16_t* h_in, int64_t N, int32_t d_model, const float* norm_scale, float eps,
@@ -205,24 +212,21 @@ int lbk_looped_swiglu_bf16(const uint16_t* h_in, int64_t N, int32_t d_model, con
       return LBK_ERR_LAUNCH;
     return LBK_OK;
   }
-  if (use_panel(gate, up, down, d_model)) {
-    PanelArgs p{};
-    p.x = h_in; p.N = N; p.d_model = d_model;
-    p.vg = gate->values; p.cg = gate->col_idx; p.Kg = gate->K;
-    p.vu = up->values; p.cu = up->col_idx; p.Ku = up->K;
-    p.R_ff = gate->R;
-    p.vd = down->values; p.cd = down->col_idx; p.Kd = down->K;
-    p.R_m = down->R;
-    p.add_residual = 1;
-    p.norm_scale = norm_scale; p.eps = eps; p.L = L;
-    p.out = h_out;
-    return launch_panel(gate->B, true, p, s) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
-  }
-  const size_t nbytes = align256((size_t)N * d_model * 2), hbytes = align256((size_t)N * d_ff * 2);
-  if (!workspace || workspace_bytes < nbytes + hbytes) return LBK_ERR_WORKSPACE;
+  const size_t sbytes = align256((size_t)N * d_model * 4), hbytes = align256((size_t)N * d_ff * 2);
+  if (!workspace || workspace_bytes < sbytes + hbytes) return LBK_ERR_WORKSPACE;
   if (!a16(workspace)) return LBK_ERR_ALIGN;
+  uint16_t* h = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + sbytes);
+  if (use_split(gate, up, down, d_model) && a16(norm_scale)) {
+    // fp32 state carried across the L applications; bf16 written once, after the last
+    float* state = static_cast<float*>(workspace);
+    if (launch_bf16_to_f32(h_in, N * d_model, state, s) != 0) return LBK_ERR_LAUNCH;
+    for (int l = 0; l < L; ++l)
+      if ((st = swiglu_split(nullptr, state, norm_scale, eps, N, d_model, gate, up, down, nullptr, state,
+                             l == L - 1 ? h_out : nullptr, h, nullptr, nullptr, s)))
+        return st;
+    return LBK_OK;
+  }
   uint16_t* normed = static_cast<uint16_t*>(workspace);
-  uint16_t* h = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + nbytes);
   const uint16_t* cur = h_in;
   for (int l = 0; l < L; ++l) {
     if (launch_rmsnorm(cur, N, d_model, norm_scale, eps, normed, s) != 0) return LBK_ERR_LAUNCH;

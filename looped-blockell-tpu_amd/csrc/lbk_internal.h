@@ -24,25 +24,38 @@ struct RowblockLaunch {
 // mode: 0 = product (+bias), 1 = gate/up with SiLU*mul, 2 = down (+residual)
 int launch_rowblock(int B, int mode, const RowblockLaunch& a, hipStream_t st);
 
-struct PanelArgs {
-  const uint16_t* x;       // [N, d_model]
+
+// two-kernel SwiGLU: gate/up (+optional RMSNorm prologue) -> h, then down (+residual / fp32 state)
+struct GUArgs {
+  const uint16_t* x;        // [N, d_model] bf16 input (plain mode)
+  const float* xf;          // [N, d_model] fp32 state (RMSNorm mode)
   int64_t N;
   int d_model;
+  const float* norm_scale;  // RMSNorm mode: [d_model]
+  float eps;
   const uint16_t* vg; const int32_t* cg; int Kg;
   const uint16_t* vu; const int32_t* cu; int Ku;
   int R_ff;
+  uint16_t* h;              // [N, d_ff] silu(g) * u
+  uint16_t* gpre;           // [N, d_ff] optional gate pre-activation
+  uint16_t* uout;           // [N, d_ff] optional up output
+};
+struct DNArgs {
+  const uint16_t* h;        // [N, d_ff]
+  int64_t N;
+  int64_t d_ff;
+  int d_model;
   const uint16_t* vd; const int32_t* cd; int Kd;
   int R_m;
-  int add_residual;        // forward only: accumulate on top of x
-  const float* norm_scale; // looped only: [d_model]
-  float eps;
-  int L;                   // looped only: number of applications
-  uint16_t* out;           // [N, d_model]
+  int C_d;                  // d_ff / B
+  const uint16_t* resid;    // optional bf16 residual [N, d_model]
+  float* state;             // optional fp32 state [N, d_model]: read as residual, written back
+  uint16_t* out;            // optional bf16 output [N, d_model]
 };
-
-size_t panel_lds_bytes(int B, int d_model, int R_ff, int R_m);
-bool panel_supported(int B, int d_model, int R_ff, int R_m, int Kd);
-int launch_panel(int B, bool norm, const PanelArgs& p, hipStream_t st);
+bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd);
+int launch_gu(int B, bool norm, const GUArgs& a, hipStream_t st);
+int launch_dn(int B, const DNArgs& a, hipStream_t st);
+int launch_bf16_to_f32(const uint16_t* x, int64_t n, float* y, hipStream_t st);
 
 int launch_rmsnorm(const uint16_t* x, int64_t N, int d, const float* scale, float eps, uint16_t* out,
                    hipStream_t st);

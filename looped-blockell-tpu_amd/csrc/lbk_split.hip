@@ -1,0 +1,521 @@
+// lbk_split.hip — the SwiGLU FFN as two register-lean kernels (gfx950, bf16 MFMA).
+//
+// gu_kernel<B, MT, NORM>: a workgroup owns 16*MT tokens.  Their input rows sit
+// in LDS as an XOR-swizzled panel (optionally RMSNorm-ed on the way in from an
+// fp32 state).  Eight waves (two per SIMD) each stream their own d_ff block rows
+// (r = w, w+8, ...): gate and up tiles are consumed in (gate k, up k) pairs from
+// a 2-deep register ring that runs across row boundaries, and h = silu(g) * u
+// is stored as bf16.  No barrier after the panel is built, so the second wave
+// on each SIMD hides the first one's load latency.
+//
+// dn_kernel<B, MT, RPW>: a workgroup owns 16*MT tokens and all d_model outputs;
+// wave w keeps RPW down block rows of fp32 accumulators in registers for the
+// whole kernel.  h is staged through LDS four column blocks at a time (double
+// buffered, next stage's global loads in flight while the current one is
+// consumed); each wave finds its tiles of a stage with a ballot over its
+// column-index rows held in registers, and streams them row by row through a
+// three-slot register shift (two tiles in flight while one is consumed).  The epilogue
+// adds the residual, or carries an fp32 state for the looped block.
+#include "lbk_device.h"
+#include "lbk_internal.h"
+
+namespace lbk {
+
+// 16-byte chunk c of row `row` lives at chunk c ^ (row & 15); rows must span a
+// multiple of 16 chunks (256 bytes)
+__device__ __forceinline__ uint32_t swz_addr(int row, int chunk, int rowb) {
+  return (uint32_t)(row * rowb + ((chunk ^ (row & 15)) << 4));
+}
+__device__ __forceinline__ u32x4 lds16(const unsigned char* base, uint32_t off) {
+  return *reinterpret_cast<const u32x4*>(base + off);
+}
+
+// ===========================================================================
+// gate/up
+// ===========================================================================
+template <int B>
+struct GUPair {
+  WRaw<B> g, u;
+  int cg, cu;   // input column blocks (-1: none)
+};
+
+template <int B>
+__device__ __forceinline__ void gu_pair_load(GUPair<B>& P, const GUArgs& a, int r, int k, int colg, int colu,
+                                             int cin, int lane) {
+  P.cg = -1;
+  P.cu = -1;
+  if (k < a.Kg) {
+    const int c = __builtin_amdgcn_readlane(colg, k);
+    if (c >= 0 && c < cin) {
+      P.cg = c;
+      load_wraw<B>(a.vg + ((int64_t)r * a.Kg + k) * B * B, lane, P.g);
+    }
+  }
+  if (k < a.Ku) {
+    const int c = __builtin_amdgcn_readlane(colu, k);
+    if (c >= 0 && c < cin) {
+      P.cu = c;
+      load_wraw<B>(a.vu + ((int64_t)r * a.Ku + k) * B * B, lane, P.u);
+    }
+  }
+}
+
+template <int B, int MT>
+__device__ __forceinline__ void gu_pair_compute(const GUPair<B>& P, const unsigned char* xp, int rowb, int i, int g,
+                                                f32x4 (&ag)[MT][TileShape<B>::CW],
+                                                f32x4 (&au)[MT][TileShape<B>::CW]) {
+  constexpr int CW = TileShape<B>::CW;
+  if (P.cg >= 0) {
+    u32x4 f[1][CW];
+    wraw_to_frag<B>(P.g, f);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const u32x4 av = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0}
+                                           : lds16(xp, swz_addr(16 * mt + i, P.cg * (B / 8) + g, rowb));
+#pragma unroll
+      for (int m = 0; m < CW; ++m) ag[mt][m] = mfma_bf16(av, f[0][m], ag[mt][m]);
+    }
+  }
+  if (P.cu >= 0) {
+    u32x4 f[1][CW];
+    wraw_to_frag<B>(P.u, f);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const u32x4 av = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0}
+                                           : lds16(xp, swz_addr(16 * mt + i, P.cu * (B / 8) + g, rowb));
+#pragma unroll
+      for (int m = 0; m < CW; ++m) au[mt][m] = mfma_bf16(av, f[0][m], au[mt][m]);
+    }
+  }
+}
+
+template <int B, int MT, bool NORM>
+__global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
+  constexpr int CW = TileShape<B>::CW;
+  constexpr int TM = 16 * MT;
+  static_assert(TileShape<B>::NKS == 1, "gate/up kernel handles B <= 32");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int d_model = a.d_model;
+  const int rowb = d_model * 2;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = uniform(tid >> 6);
+  const int i = lane & 15, g = lane >> 4;
+  const int64_t t0 = (int64_t)blockIdx.x * TM;
+  const int cin = d_model / B;
+  const int64_t d_ff = (int64_t)a.R_ff * B;
+
+  // ---- input panel
+  if constexpr (!NORM) {
+    const int cpr = d_model / 8;
+    for (int e = tid; e < TM * cpr; e += 512) {
+      const int row = e / cpr, c = e - row * cpr;
+      const int64_t t = t0 + row;
+      u32x4 v = {0, 0, 0, 0};
+      if (t < a.N) v = *reinterpret_cast<const u32x4*>(a.x + t * d_model + 8 * c);
+      *reinterpret_cast<u32x4*>(smem + swz_addr(row, c, rowb)) = v;
+    }
+  } else {
+    // fp32 state rows -> RMSNorm -> bf16 panel; one wave per row, 8 contiguous values per lane per step
+    for (int row = w; row < TM; row += 8) {
+      const int64_t t = t0 + row;
+      const float* xr = a.xf + (t < a.N ? t : 0) * d_model;
+      float ss = 0.f;
+      for (int c = 8 * lane; c < d_model; c += 512) {
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(xr + c);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(xr + c + 4);
+        ss += v0[0] * v0[0] + v0[1] * v0[1] + v0[2] * v0[2] + v0[3] * v0[3];
+        ss += v1[0] * v1[0] + v1[1] * v1[1] + v1[2] * v1[2] + v1[3] * v1[3];
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+      const float rs = (t < a.N) ? 1.0f / sqrtf(ss / (float)d_model + a.eps) : 0.f;
+      for (int c = 8 * lane; c < d_model; c += 512) {
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(xr + c);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(xr + c + 4);
+        const f32x4 s0 = *reinterpret_cast<const f32x4*>(a.norm_scale + c);
+        const f32x4 s1 = *reinterpret_cast<const f32x4*>(a.norm_scale + c + 4);
+        const u32x4 o = {pack2_bf16(v0[0] * rs * s0[0], v0[1] * rs * s0[1]),
+                         pack2_bf16(v0[2] * rs * s0[2], v0[3] * rs * s0[3]),
+                         pack2_bf16(v1[0] * rs * s1[0], v1[1] * rs * s1[1]),
+                         pack2_bf16(v1[2] * rs * s1[2], v1[3] * rs * s1[3])};
+        *reinterpret_cast<u32x4*>(smem + swz_addr(row, c / 8, rowb)) = o;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- stream this wave's rows: r = w + 8*n; flattened (row, k) pairs, 2-deep ring
+  // kmax >= 1 so that rows with no tiles (K = 0) still store h = silu(0) * 0 = 0
+  const int kmax = (a.Kg > a.Ku ? a.Kg : a.Ku) > 0 ? (a.Kg > a.Ku ? a.Kg : a.Ku) : 1;
+  const int nrows = (a.R_ff - w + 7) / 8;        // rows of this wave
+  if (nrows <= 0) return;
+  const int total = nrows * kmax;
+
+  int colg = -1, colu = -1, colg_n = -1, colu_n = -1;  // column lists of the current / next row
+  auto load_cols = [&](int n, int& cgv, int& cuv) {
+    cgv = -1;
+    cuv = -1;
+    if (n < nrows) {
+      const int r = w + 8 * n;
+      if (lane < a.Kg) cgv = a.cg[(int64_t)r * a.Kg + lane];
+      if (lane < a.Ku) cuv = a.cu[(int64_t)r * a.Ku + lane];
+    }
+  };
+  load_cols(0, colg, colu);
+  load_cols(1, colg_n, colu_n);
+
+  // ring slots carry the pair at stream index p (row p / kmax, slot p % kmax)
+  GUPair<B> P0, P1;
+  // the first two pairs may straddle the first row boundary
+  {
+    gu_pair_load<B>(P0, a, w, 0, colg, colu, cin, lane);
+    if (1 < total) {
+      if (1 < kmax) gu_pair_load<B>(P1, a, w, 1, colg, colu, cin, lane);
+      else gu_pair_load<B>(P1, a, w + 8, 0, colg_n, colu_n, cin, lane);
+    }
+  }
+  f32x4 ag[MT][CW], au[MT][CW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int m = 0; m < CW; ++m) {
+      ag[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+      au[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+  int n = 0, k = 0;   // row / slot of the pair being consumed
+  auto finish_row = [&]() {
+    const int r = w + 8 * n;
+    const int64_t col0 = (int64_t)r * B + CW * i;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t t = t0 + 16 * mt + 4 * g + v;
+        float o[CW], gv[CW], uv[CW];
+#pragma unroll
+        for (int m = 0; m < CW; ++m) {
+          gv[m] = ag[mt][m][v];
+          uv[m] = au[mt][m][v];
+          o[m] = silu_f(gv[m]) * uv[m];
+        }
+        if (t < a.N) {
+          store_bf16<CW>(a.h + t * d_ff + col0, o);
+          if (a.gpre) store_bf16<CW>(a.gpre + t * d_ff + col0, gv);
+          if (a.uout) store_bf16<CW>(a.uout + t * d_ff + col0, uv);
+        }
+      }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int m = 0; m < CW; ++m) {
+        ag[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        au[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+  };
+  // refill a ring slot with stream index p2 (called after advance(), so p2 lies in
+  // row n or n+1, whose column lists are cached)
+  auto refill = [&](GUPair<B>& P, int p2) {
+    if (p2 >= total) return;
+    const int n2 = p2 / kmax, k2 = p2 - n2 * kmax;
+    if (n2 == n) gu_pair_load<B>(P, a, w + 8 * n2, k2, colg, colu, cin, lane);
+    else gu_pair_load<B>(P, a, w + 8 * n2, k2, colg_n, colu_n, cin, lane);
+  };
+  auto advance = [&]() {
+    if (++k == kmax) {
+      finish_row();
+      k = 0;
+      ++n;
+      colg = colg_n;
+      colu = colu_n;
+      load_cols(n + 1, colg_n, colu_n);
+    }
+  };
+
+  // consume pair p, move (n, k) to pair p+1, then load pair p+2 (row n or n+1)
+  for (int p = 0; p < total; p += 2) {
+    gu_pair_compute<B, MT>(P0, smem, rowb, i, g, ag, au);
+    advance();
+    refill(P0, p + 2);
+    if (p + 1 < total) {
+      gu_pair_compute<B, MT>(P1, smem, rowb, i, g, ag, au);
+      advance();
+      refill(P1, p + 3);
+    }
+  }
+}
+
+// ===========================================================================
+// down
+// ===========================================================================
+// h column blocks per LDS stage: 256 bytes of each token row (16 chunks)
+template <int B>
+struct DnStage { static constexpr int G = 128 / B; };
+
+// Hits of a stage in (row, column block, slot) order.  Lane j holds hit skip+j:
+// its column block within the stage (list_cb) and its weight slot k (list_k);
+// ends[rho] is the cumulative hit count through row rho (uniform).  Returns the
+// total.  A row may name one column block more than once, so the total can
+// exceed 64 and the caller then walks it in batches of 64.
+template <int B, int RPW>
+__device__ __forceinline__ int dn_hits(int c0, int ncb, const int (&colreg)[RPW], int lane, int skip, int& list_cb,
+                                       int& list_k, int (&ends)[RPW]) {
+  int n = 0;
+  list_cb = 0;
+  list_k = 0;
+#pragma unroll
+  for (int rho = 0; rho < RPW; ++rho) {
+#pragma unroll
+    for (int cb = 0; cb < DnStage<B>::G; ++cb) {
+      if (cb >= ncb) break;
+      uint64_t m = __ballot(colreg[rho] == c0 + cb);
+      while (m) {
+        if (lane == n - skip) {
+          list_cb = cb;
+          list_k = __builtin_ctzll(m);
+        }
+        m &= m - 1;
+        ++n;
+      }
+    }
+    ends[rho] = n;
+  }
+  return n;
+}
+
+// weight tile of hit q (row rho of this wave, slot k from the hit list)
+template <int B, int RPW>
+__device__ __forceinline__ void dn_tile_load(WRaw<B>& T, const DNArgs& a, int w, int rho, int list_k, int idx,
+                                             int lane) {
+  const int k = __builtin_amdgcn_readlane(list_k, idx);
+  load_wraw<B>(a.vd + ((int64_t)(w * RPW + rho) * a.Kd + k) * B * B, lane, T);
+}
+
+template <int B, int MT, int RPW>
+__global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
+  constexpr int CW = TileShape<B>::CW;
+  constexpr int TM = 16 * MT;
+  constexpr int G = DnStage<B>::G;
+  constexpr int SROWB = G * B * 2;                   // bytes per token row of a stage (256)
+  constexpr int SBYTES = TM * SROWB;                 // bytes per stage
+  constexpr int CHUNKS = SBYTES / 16;                // 16-byte chunks per stage
+  constexpr int PER_T = (CHUNKS + 511) / 512;        // chunks per thread per stage
+  static_assert(TileShape<B>::NKS == 1, "down kernel handles B <= 32");
+  static_assert(SROWB == 256, "stage rows must cover 16 chunks");
+  __shared__ __attribute__((aligned(16))) unsigned char stages[2][SBYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = uniform(tid >> 6);
+  const int i = lane & 15, g = lane >> 4;
+  const int64_t t0 = (int64_t)blockIdx.x * TM;
+  const int d_model = a.d_model;
+  const int64_t d_ff = a.d_ff;
+  const int C = a.C_d;
+  const int nstages = (C + G - 1) / G;
+
+  int colreg[RPW];
+#pragma unroll
+  for (int rho = 0; rho < RPW; ++rho) {
+    const int rm = w * RPW + rho;
+    colreg[rho] = (rm < a.R_m && lane < a.Kd) ? a.cd[(int64_t)rm * a.Kd + lane] : -2;
+  }
+
+  f32x4 acc[RPW][MT][CW];
+#pragma unroll
+  for (int rho = 0; rho < RPW; ++rho)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int m = 0; m < CW; ++m) acc[rho][mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // stage loader: chunk e of stage s -> (token row, 16-byte chunk within the row)
+  u32x4 sreg[PER_T];
+  auto stage_fetch = [&](int s) {
+#pragma unroll
+    for (int u = 0; u < PER_T; ++u) {
+      const int e = tid + 512 * u;
+      sreg[u] = u32x4{0, 0, 0, 0};
+      if (e < CHUNKS) {
+        const int row = e / (SROWB / 16), c = e - row * (SROWB / 16);
+        const int64_t t = t0 + row;
+        const int64_t col = (int64_t)s * G * B + 8 * c;
+        if (t < a.N && col < d_ff) sreg[u] = *reinterpret_cast<const u32x4*>(a.h + t * d_ff + col);
+      }
+    }
+  };
+  auto stage_store = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < PER_T; ++u) {
+      const int e = tid + 512 * u;
+      if (e < CHUNKS) {
+        const int row = e / (SROWB / 16), c = e - row * (SROWB / 16);
+        *reinterpret_cast<u32x4*>(&stages[buf][0] + swz_addr(row, c, SROWB)) = sreg[u];
+      }
+    }
+  };
+
+  stage_fetch(0);
+  stage_store(0);
+  __syncthreads();
+  for (int s = 0; s < nstages; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < nstages) stage_fetch(s + 1);
+    // this wave's tiles reading stage s, row by row; a 2-deep ring of weight
+    // tiles runs across the rows (hit q sits in slot q & 1)
+    const int c0 = s * G;
+    const int ncb = (C - c0) < G ? (C - c0) : G;
+    const unsigned char* sb = &stages[buf][0];
+    for (int skip = 0;; skip += 64) {
+      int list_cb, list_k, ends[RPW];
+      const int nall = dn_hits<B, RPW>(c0, ncb, colreg, lane, skip, list_cb, list_k, ends);
+      const int bend = (nall - skip) < 64 ? nall : skip + 64;
+      // row of hit q (uniform): the first rho with q < ends[rho]
+      auto row_of = [&](int q) {
+        int r = 0;
+#pragma unroll
+        for (int rho = 0; rho + 1 < RPW; ++rho) r += (q >= ends[rho]) ? 1 : 0;
+        return r;
+      };
+      // three-slot shift register of weight tiles: D0 holds hit q, D1 hit q+1,
+      // D2 hit q+2; hit q+3 is requested as q is consumed
+      WRaw<B> D0, D1, D2;
+      if (skip < bend) dn_tile_load<B, RPW>(D0, a, w, row_of(skip), list_k, 0, lane);
+      if (skip + 1 < bend) dn_tile_load<B, RPW>(D1, a, w, row_of(skip + 1), list_k, 1, lane);
+      if (skip + 2 < bend) dn_tile_load<B, RPW>(D2, a, w, row_of(skip + 2), list_k, 2, lane);
+      int q = skip;
+#pragma unroll
+      for (int rr = 0; rr < RPW; ++rr) {
+        const int e = ends[rr] < bend ? ends[rr] : bend;
+        for (; q < e; ++q) {
+          u32x4 f[1][CW];
+          wraw_to_frag<B>(D0, f);
+          D0 = D1;
+          D1 = D2;
+          if (q + 3 < bend) dn_tile_load<B, RPW>(D2, a, w, row_of(q + 3), list_k, q + 3 - skip, lane);
+          const int cb = __builtin_amdgcn_readlane(list_cb, q - skip);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const u32x4 av = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0}
+                                                 : lds16(sb, swz_addr(16 * mt + i, cb * (B / 8) + g, SROWB));
+#pragma unroll
+            for (int m = 0; m < CW; ++m) acc[rr][mt][m] = mfma_bf16(av, f[0][m], acc[rr][mt][m]);
+          }
+        }
+      }
+      if (nall <= skip + 64) break;
+    }
+    if (s + 1 < nstages) stage_store(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: + residual (bf16) or + fp32 state; store bf16 (and the state)
+#pragma unroll
+  for (int rho = 0; rho < RPW; ++rho) {
+    const int rm = w * RPW + rho;
+    if (rm >= a.R_m) continue;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t t = t0 + 16 * mt + 4 * g + v;
+        if (t >= a.N) continue;
+        const int64_t off = t * d_model + rm * B + CW * i;
+        float o[CW];
+#pragma unroll
+        for (int m = 0; m < CW; ++m) o[m] = acc[rho][mt][m][v];
+        if (a.state) {
+#pragma unroll
+          for (int m = 0; m < CW; ++m) {
+            o[m] += a.state[off + m];
+            a.state[off + m] = o[m];
+          }
+        } else if (a.resid) {
+          float rv[CW];
+          load_bf16<CW>(a.resid + off, rv);
+#pragma unroll
+          for (int m = 0; m < CW; ++m) o[m] += rv[m];
+        }
+        if (a.out) store_bf16<CW>(a.out + off, o);
+      }
+  }
+}
+
+// state <- float(x), fp32 copy of a bf16 tensor
+__global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t* __restrict__ x, int64_t n,
+                                                          float* __restrict__ y) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx < n) y[idx] = bf2f(x[idx]);
+}
+
+// ===========================================================================
+// host side
+// ===========================================================================
+static int gu_mt(int d_model) { return d_model <= 1024 ? 4 : (d_model <= 2048 ? 2 : 0); }
+
+static int dn_rpw(int R_m) {
+  for (int rpw : {1, 2, 4})
+    if (8 * rpw >= R_m) return rpw;
+  return -1;
+}
+
+bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd) {
+  if (B != 16 && B != 32) return false;
+  if (Kg > 64 || Ku > 64 || Kd > 64) return false;   // one lane per slot in the column lookups
+  if (d_model % 128) return false;                    // swizzled panel rows
+  if (gu_mt(d_model) == 0) return false;
+  if (R_m * B != d_model || dn_rpw(R_m) < 0) return false;
+  if ((R_ff * B) % 8) return false;
+  return true;
+}
+
+template <int B, int MT, bool NORM>
+static int launch_gu_t(const GUArgs& a, hipStream_t st) {
+  auto kern = gu_kernel<B, MT, NORM>;
+  static bool configured = false;
+  if (!configured) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 163840) != hipSuccess)
+      return -1;
+    configured = true;
+  }
+  const int TM = 16 * MT;
+  const size_t lds = (size_t)TM * a.d_model * 2;
+  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + TM - 1) / TM)), dim3(512), lds, st, a);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_gu(int B, bool norm, const GUArgs& a, hipStream_t st) {
+  if (a.N == 0) return 0;
+  const int mt = gu_mt(a.d_model);
+#define LBK_GU(BB, MM)                                                                         \
+  if (B == BB && mt == MM) return norm ? launch_gu_t<BB, MM, true>(a, st) : launch_gu_t<BB, MM, false>(a, st);
+  LBK_GU(16, 4) LBK_GU(16, 2) LBK_GU(32, 4) LBK_GU(32, 2)
+#undef LBK_GU
+  return -2;
+}
+
+template <int B, int MT, int RPW>
+static int launch_dn_t(const DNArgs& a, hipStream_t st) {
+  const int TM = 16 * MT;
+  hipLaunchKernelGGL((dn_kernel<B, MT, RPW>), dim3((unsigned)((a.N + TM - 1) / TM)), dim3(512), 0, st, a);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_dn(int B, const DNArgs& a, hipStream_t st) {
+  if (a.N == 0) return 0;
+  const int rpw = dn_rpw(a.R_m);
+#define LBK_DN(BB, RR)                                                   \
+  if (B == BB && rpw == RR) return launch_dn_t<BB, 4, RR>(a, st);
+  LBK_DN(16, 1) LBK_DN(16, 2) LBK_DN(16, 4) LBK_DN(32, 1) LBK_DN(32, 2) LBK_DN(32, 4)
+#undef LBK_DN
+  return -2;
+}
+
+int launch_bf16_to_f32(const uint16_t* x, int64_t n, float* y, hipStream_t st) {
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(bf16_to_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, n, y);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace lbk

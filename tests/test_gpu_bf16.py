@@ -100,6 +100,43 @@ def test_swiglu_with_intermediates(gpu, case):
         assert rel <= TOL, f"{name}: rel {rel} abs {ab}"
 
 
+@pytest.mark.parametrize("case", [(256, 1024, 16), (128, 512, 16), (1024, 4096, 32)])
+def test_swiglu_duplicate_and_empty_columns(gpu, case):
+    """Rows that name one column block several times sum every copy (as the oracle's
+    per-slot sum does); a down row whose 64 slots all fall in one 128-column stage
+    makes that stage's hit list longer than one wave; empty rows give zeros."""
+    d_model, d_ff, B = case
+    _say(f"swiglu duplicate columns {case}")
+    rng = np.random.default_rng(21)
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25)
+    g[1][0, :] = g[1][0, 0]                      # every gate slot of row 0 -> one column
+    u[1][1, :] = -1                              # up row 1 empty -> h row block 1 == 0
+    Kd = 64
+    Cf = d_ff // B
+    dv = O.bf16_round((rng.standard_normal((d_model // B, Kd, B, B)) * 0.02).astype(np.float32))
+    dc = rng.integers(0, Cf, size=(d_model // B, Kd)).astype(np.int32)
+    dc[0, :] = rng.integers(0, min(Cf, 128 // B), size=Kd)   # row 0: all slots in the first stage
+    d = (dv, dc)
+    x = T.act(rng, 70, d_model)
+    out, *_ = T.abi_swiglu(T.to_gpu_bf16(x), T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d), add_residual=True)
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref, *_ = O.swiglu_fwd(x.astype(np.float64), f64(g), f64(u), f64(d), add_residual=True)
+    rel, ab = T.rel_err(T.to_np(out), ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
+def test_swiglu_zero_k(gpu):
+    """K = 0 everywhere: h == 0, so out == x (with the residual) / 0 (without)."""
+    rng = np.random.default_rng(22)
+    d_model, d_ff, B = 256, 512, 16
+    z = lambda R: (np.zeros((R, 0, B, B), np.float32), np.zeros((R, 0), np.int32))
+    x = T.act(rng, 40, d_model)
+    out, h, _, _ = T.abi_swiglu(T.to_gpu_bf16(x), T.gpu_weight(z(d_ff // B)), T.gpu_weight(z(d_ff // B)),
+                                T.gpu_weight(z(d_model // B)), add_residual=True, intermediates=True)
+    assert np.array_equal(T.to_np(out), x)
+    assert not T.to_np(h).any()
+
+
 def test_swiglu_full_config2_sampled_rows(gpu):
     """Config 2 at full size (N=16384); rows are independent, so sampled rows are checked."""
     rng = np.random.default_rng(1002)

@@ -106,8 +106,10 @@ def test_abi_swiglu_shape_and_workspace_checks():
     assert need >= 4 * 256 * 2
     assert lib.lbk_swiglu_fwd_bf16(x, 4, 64, C.byref(g64), C.byref(u64), C.byref(d64), 0, out, None, None, None,
                                    None, 0, s) == A.LBK_ERR_WORKSPACE
-    # the fused panel path needs none
-    assert lib.lbk_swiglu_workspace_bytes(4, 64, C.byref(g), C.byref(u), C.byref(d), 0) == 0
+    # every path stages h in the workspace unless intermediates go to the caller's h_out
+    assert lib.lbk_swiglu_workspace_bytes(4, 64, C.byref(g), C.byref(u), C.byref(d), 0) >= 4 * 256 * 2
+    assert lib.lbk_swiglu_workspace_bytes(4, 64, C.byref(g), C.byref(u), C.byref(d), 1) == 0
+    assert lib.lbk_looped_workspace_bytes(4, 64, C.byref(g), C.byref(u), C.byref(d)) >= 4 * 64 * 4 + 4 * 256 * 2
     # looped: negative L / eps
     assert lib.lbk_looped_swiglu_bf16(x, 4, 64, C.c_void_p(0x5000), C.c_float(1e-5), -1, C.byref(g), C.byref(u),
                                       C.byref(d), out, None, 0, s) == A.LBK_ERR_ARG
