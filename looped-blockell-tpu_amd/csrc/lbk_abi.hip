@@ -116,20 +116,49 @@ static bool use_split(const lbk_bell* gate, const lbk_bell* up, const lbk_bell* 
   return split_supported(gate->B, d_model, gate->R, down->R, gate->K, up->K, down->K);
 }
 
+// Packed copies of gate/up/down (fragment-major tiles) at the start of a workspace.
+struct PackedFFN {
+  const void* g; const void* u; const void* d;
+  size_t bytes;
+};
+
+static size_t packed_ffn_bytes(const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down) {
+  const int B = gate->B;
+  return align256(packed_bf16_bytes((int64_t)gate->R * gate->K, B)) +
+         align256(packed_bf16_bytes((int64_t)up->R * up->K, B)) +
+         align256(packed_bf16_bytes((int64_t)down->R * down->K, B));
+}
+
+static int pack_ffn(const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, char* ws, PackedFFN* out,
+                    hipStream_t st) {
+  const int B = gate->B;
+  char* p = ws;
+  const lbk_bell* ws3[3] = {gate, up, down};
+  const void** dst[3] = {&out->g, &out->u, &out->d};
+  for (int t = 0; t < 3; ++t) {
+    const int64_t nt = (int64_t)ws3[t]->R * ws3[t]->K;
+    *dst[t] = p;
+    if (launch_pack_bf16(ws3[t]->values, nt, B, reinterpret_cast<uint32_t*>(p), st) != 0) return LBK_ERR_LAUNCH;
+    p += align256(packed_bf16_bytes(nt, B));
+  }
+  out->bytes = (size_t)(p - ws);
+  return LBK_OK;
+}
+
 static int swiglu_split(const uint16_t* x, const float* xf, const float* norm_scale, float eps, int64_t N,
                         int32_t d_model, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
-                        const uint16_t* resid, float* state, uint16_t* out, uint16_t* h, uint16_t* gate_pre,
-                        uint16_t* up_out, hipStream_t st) {
+                        const PackedFFN& pk, const uint16_t* resid, float* state, uint16_t* out, uint16_t* h,
+                        uint16_t* gate_pre, uint16_t* up_out, hipStream_t st) {
   GUArgs g{};
   g.x = x; g.xf = xf; g.N = N; g.d_model = d_model; g.norm_scale = norm_scale; g.eps = eps;
-  g.vg = gate->values; g.cg = gate->col_idx; g.Kg = gate->K;
-  g.vu = up->values; g.cu = up->col_idx; g.Ku = up->K;
+  g.pg = pk.g; g.cg = gate->col_idx; g.Kg = gate->K;
+  g.pu = pk.u; g.cu = up->col_idx; g.Ku = up->K;
   g.R_ff = gate->R;
   g.h = h; g.gpre = gate_pre; g.uout = up_out;
   if (launch_gu(gate->B, xf != nullptr, g, st) != 0) return LBK_ERR_LAUNCH;
   DNArgs d{};
   d.h = h; d.N = N; d.d_ff = (int64_t)gate->R * gate->B; d.d_model = d_model;
-  d.vd = down->values; d.cd = down->col_idx; d.Kd = down->K;
+  d.pd = pk.d; d.cd = down->col_idx; d.Kd = down->K;
   d.R_m = down->R; d.C_d = gate->R;
   d.resid = resid; d.state = state; d.out = out;
   return launch_dn(gate->B, d, st) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
@@ -137,10 +166,11 @@ static int swiglu_split(const uint16_t* x, const float* xf, const float* norm_sc
 
 size_t lbk_swiglu_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
                                   const lbk_bell* down, int want_intermediates) {
-  (void)d_model;
   if (!gate || !up || !down || N <= 0) return 0;
-  if (want_intermediates) return 0;  // h goes to the caller's h_out
-  return align256((size_t)N * gate->R * gate->B * 2);
+  // [packed gate/up/down tiles (split path)] [h, unless it goes to the caller's h_out]
+  size_t b = use_split(gate, up, down, d_model) ? packed_ffn_bytes(gate, up, down) : 0;
+  if (!want_intermediates) b += align256((size_t)N * gate->R * gate->B * 2);
+  return b;
 }
 
 int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
@@ -157,18 +187,23 @@ int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk
   if (!a16(x) || !a16(out) || (d_model % 8)) return LBK_ERR_ALIGN;
   for (const void* p : {(const void*)h_out, (const void*)gate_pre_out, (const void*)up_out})
     if (p && !a16(p)) return LBK_ERR_ALIGN;
-  uint16_t* h = h_out;
-  if (!h) {
-    const size_t need = align256((size_t)N * d_ff * 2);
-    if (!workspace || workspace_bytes < need) return LBK_ERR_WORKSPACE;
+  const bool split = use_split(gate, up, down, d_model);
+  const size_t pbytes = split ? packed_ffn_bytes(gate, up, down) : 0;
+  const size_t hbytes = h_out ? 0 : align256((size_t)N * d_ff * 2);
+  if (pbytes + hbytes > 0) {
+    if (!workspace || workspace_bytes < pbytes + hbytes) return LBK_ERR_WORKSPACE;
     if (!a16(workspace)) return LBK_ERR_ALIGN;
-    h = static_cast<uint16_t*>(workspace);
   }
-  if (use_split(gate, up, down, d_model))
-    return swiglu_split(x, nullptr, nullptr, 0.f, N, d_model, gate, up, down, add_residual ? x : nullptr, nullptr,
-                        out, h, gate_pre_out, up_out, S(stream));
-  return swiglu_general(x, N, d_model, gate, up, down, add_residual ? x : nullptr, out, h, gate_pre_out, up_out,
-                        S(stream));
+  char* ws = static_cast<char*>(workspace);
+  uint16_t* h = h_out ? h_out : reinterpret_cast<uint16_t*>(ws + pbytes);
+  hipStream_t s = S(stream);
+  if (split) {
+    PackedFFN pk{};
+    if ((st = pack_ffn(gate, up, down, ws, &pk, s))) return st;
+    return swiglu_split(x, nullptr, nullptr, 0.f, N, d_model, gate, up, down, pk, add_residual ? x : nullptr,
+                        nullptr, out, h, gate_pre_out, up_out, s);
+  }
+  return swiglu_general(x, N, d_model, gate, up, down, add_residual ? x : nullptr, out, h, gate_pre_out, up_out, s);
 }
 
 int lbk_rmsnorm_bf16(const uint16_t* x, int64_t N, int32_t d, const float* scale, float eps, uint16_t* out,
@@ -190,8 +225,9 @@ int lbk_diagonal_injection_bf16(const uint16_t* h, const uint16_t* e, const floa
 size_t lbk_looped_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
                                   const lbk_bell* down) {
   if (!gate || !up || !down || N <= 0 || d_model <= 0) return 0;
-  // fp32 carried state (or the bf16 normed copy on the general path) + h
-  return align256((size_t)N * d_model * 4) + align256((size_t)N * gate->R * gate->B * 2);
+  // [fp32 carried state (or the bf16 normed copy on the general path)] [h] [packed tiles]
+  return align256((size_t)N * d_model * 4) + align256((size_t)N * gate->R * gate->B * 2) +
+         (use_split(gate, up, down, d_model) ? packed_ffn_bytes(gate, up, down) : 0);
 }
 
 int lbk_looped_swiglu_bf16(const uint16_t* h_in, int64_t N, int32_t d_model, const float* norm_scale, float eps,
@@ -212,21 +248,26 @@ int lbk_looped_swiglu_bf16(const uint16_t* h_in, int64_t N, int32_t d_model, con
       return LBK_ERR_LAUNCH;
     return LBK_OK;
   }
+  const bool split = use_split(gate, up, down, d_model) && a16(norm_scale);
   const size_t sbytes = align256((size_t)N * d_model * 4), hbytes = align256((size_t)N * d_ff * 2);
-  if (!workspace || workspace_bytes < sbytes + hbytes) return LBK_ERR_WORKSPACE;
+  const size_t pbytes = use_split(gate, up, down, d_model) ? packed_ffn_bytes(gate, up, down) : 0;
+  if (!workspace || workspace_bytes < sbytes + hbytes + pbytes) return LBK_ERR_WORKSPACE;
   if (!a16(workspace)) return LBK_ERR_ALIGN;
-  uint16_t* h = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + sbytes);
-  if (use_split(gate, up, down, d_model) && a16(norm_scale)) {
+  char* ws = static_cast<char*>(workspace);
+  uint16_t* h = reinterpret_cast<uint16_t*>(ws + sbytes);
+  if (split) {
     // fp32 state carried across the L applications; bf16 written once, after the last
-    float* state = static_cast<float*>(workspace);
+    float* state = reinterpret_cast<float*>(ws);
+    PackedFFN pk{};
+    if ((st = pack_ffn(gate, up, down, ws + sbytes + hbytes, &pk, s))) return st;
     if (launch_bf16_to_f32(h_in, N * d_model, state, s) != 0) return LBK_ERR_LAUNCH;
     for (int l = 0; l < L; ++l)
-      if ((st = swiglu_split(nullptr, state, norm_scale, eps, N, d_model, gate, up, down, nullptr, state,
+      if ((st = swiglu_split(nullptr, state, norm_scale, eps, N, d_model, gate, up, down, pk, nullptr, state,
                              l == L - 1 ? h_out : nullptr, h, nullptr, nullptr, s)))
         return st;
     return LBK_OK;
   }
-  uint16_t* normed = static_cast<uint16_t*>(workspace);
+  uint16_t* normed = reinterpret_cast<uint16_t*>(ws);
   const uint16_t* cur = h_in;
   for (int l = 0; l < L; ++l) {
     if (launch_rmsnorm(cur, N, d_model, norm_scale, eps, normed, s) != 0) return LBK_ERR_LAUNCH;

@@ -190,4 +190,54 @@ int launch_injection(const uint16_t* h, const uint16_t* e, const float* log_A, c
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// ---------------------------------------------------------------------------
+// bf16 tiles [T, B, B] ([B_in, B_out] each) -> fragment-major packed tiles
+// (layout described with PackedTile in lbk_device.h); one thread per dword
+// ---------------------------------------------------------------------------
+template <int B>
+__global__ __launch_bounds__(256) void pack_bf16_kernel(const uint16_t* __restrict__ values, int64_t ndw,
+                                                        uint32_t* __restrict__ packed) {
+  constexpr int NKS = TileShape<B>::NKS, CW = TileShape<B>::CW;
+  constexpr int PER_TILE = PackedTile<B>::U32X4 * 4;   // dwords per packed tile
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= ndw) return;
+  const int64_t tile = idx / PER_TILE;
+  int r = (int)(idx - tile * PER_TILE);
+  const int u = r & 3;
+  r >>= 2;
+  const int m = r % CW;
+  r /= CW;
+  const int ks = r % NKS;
+  const int l = r / NKS;
+  const int j = l & 15, g = l >> 4;
+  const int k = 32 * ks + 8 * g + 2 * u, c = CW * j + m;
+  const uint16_t* w = values + tile * B * B;
+  packed[idx] = (uint32_t)w[k * B + c] | ((uint32_t)w[(k + 1) * B + c] << 16);
+}
+
+size_t packed_bf16_bytes(int64_t ntiles, int B) {
+  switch (B) {
+    case 16: return (size_t)ntiles * PackedTile<16>::U32X4 * 16;
+    case 32: return (size_t)ntiles * PackedTile<32>::U32X4 * 16;
+    case 64: return (size_t)ntiles * PackedTile<64>::U32X4 * 16;
+    default: return 0;
+  }
+}
+
+int launch_pack_bf16(const uint16_t* values, int64_t ntiles, int B, uint32_t* packed, hipStream_t st) {
+  if (ntiles == 0) return 0;
+  int64_t ndw;
+  switch (B) {
+    case 16: ndw = ntiles * PackedTile<16>::U32X4 * 4; break;
+    case 32: ndw = ntiles * PackedTile<32>::U32X4 * 4; break;
+    case 64: ndw = ntiles * PackedTile<64>::U32X4 * 4; break;
+    default: return -2;
+  }
+  const unsigned grid = (unsigned)((ndw + 255) / 256);
+  if (B == 16) hipLaunchKernelGGL(pack_bf16_kernel<16>, dim3(grid), dim3(256), 0, st, values, ndw, packed);
+  if (B == 32) hipLaunchKernelGGL(pack_bf16_kernel<32>, dim3(grid), dim3(256), 0, st, values, ndw, packed);
+  if (B == 64) hipLaunchKernelGGL(pack_bf16_kernel<64>, dim3(grid), dim3(256), 0, st, values, ndw, packed);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 }  // namespace lbk

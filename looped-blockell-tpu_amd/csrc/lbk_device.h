@@ -70,7 +70,8 @@ __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirs
 // ---------------------------------------------------------------------------
 // Weight tiles: raw transposing loads and conversion to B fragments.
 // NKS = number of 32-deep k-steps per tile, CW = output columns per lane.
-// For B = 16 the single k-step is half filled: lanes with g >= 2 carry zeros.
+// For B = 16 the single k-step is half filled: lanes with g >= 2 carry a zero A
+// operand (their B operand repeats lanes g - 2 and is multiplied by zero).
 // ---------------------------------------------------------------------------
 template <int B> struct TileShape;
 template <> struct TileShape<16> { static constexpr int NKS = 1, CW = 1; };
@@ -85,16 +86,14 @@ template <> struct WRaw<64> { u32x2 v[2][8]; };       // four bf16 per row, per 
 template <int B>
 __device__ __forceinline__ void load_wraw(const uint16_t* __restrict__ tile, int lane, WRaw<B>& r);
 
+// Lanes g >= 2 repeat the rows of lanes g - 2 (every lane issues the same loads,
+// so the loop around them needs no branch); their A operand is zero, so these
+// duplicates contribute nothing.
 template <>
 __device__ __forceinline__ void load_wraw<16>(const uint16_t* __restrict__ tile, int lane, WRaw<16>& r) {
-  const int j = lane & 15, g = lane >> 4;
-  if (g < 2) {
+  const int j = lane & 15, g = (lane >> 4) & 1;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) r.v[t] = tile[(8 * g + t) * 16 + j];
-  } else {
-#pragma unroll
-    for (int t = 0; t < 8; ++t) r.v[t] = 0;
-  }
+  for (int t = 0; t < 8; ++t) r.v[t] = tile[(8 * g + t) * 16 + j];
 }
 template <>
 __device__ __forceinline__ void load_wraw<32>(const uint16_t* __restrict__ tile, int lane, WRaw<32>& r) {
@@ -142,6 +141,34 @@ __device__ __forceinline__ void wraw_to_frag<64>(const WRaw<64>& r, u32x4 (&f)[2
       f[s][2][u] = __builtin_amdgcn_perm(b[1], a[1], 0x05040100u);
       f[s][3][u] = __builtin_amdgcn_perm(b[1], a[1], 0x07060302u);
     }
+}
+
+// ---------------------------------------------------------------------------
+// Fragment-major ("packed") bf16 tiles.  Tile t holds, for every lane l of a
+// wave, that lane's B fragments f[ks][m] (as wraw_to_frag would build them) as
+// NKS*CW consecutive 16-byte chunks at packed[(t*64 + l)*NKS*CW + ks*CW + m].
+// A lane then fetches all its operands of a tile with NKS*CW dwordx4 loads and
+// no register transposition.  For B = 16 only lanes 0..31 are stored (512
+// bytes per tile); lanes 32..63 read lanes 0..31 (their A operand is zero).
+// The chunk's dword u of fragment (ks, m) of lane (j = l%16, g = l/16) is
+//   W[k][c] | W[k+1][c] << 16,  k = 32*ks + 8*g + 2*u,  c = CW*j + m.
+// ---------------------------------------------------------------------------
+template <int B>
+struct PackedTile {
+  static constexpr int CHUNKS = TileShape<B>::NKS * TileShape<B>::CW;   // 16-byte chunks per lane
+  static constexpr int LANES = B == 16 ? 32 : 64;                       // lanes stored per tile
+  static constexpr int U32X4 = LANES * CHUNKS;                          // chunks per tile
+};
+
+template <int B>
+__device__ __forceinline__ void load_pfrag(const u32x4* __restrict__ tile, int lane,
+                                           u32x4 (&f)[TileShape<B>::NKS][TileShape<B>::CW]) {
+  constexpr int NKS = TileShape<B>::NKS, CW = TileShape<B>::CW;
+  const u32x4* p = tile + (B == 16 ? (lane & 31) : lane) * (NKS * CW);
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+    for (int m = 0; m < CW; ++m) f[ks][m] = p[ks * CW + m];
 }
 
 // ---------------------------------------------------------------------------

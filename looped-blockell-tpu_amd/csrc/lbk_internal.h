@@ -24,6 +24,10 @@ struct RowblockLaunch {
 // mode: 0 = product (+bias), 1 = gate/up with SiLU*mul, 2 = down (+residual)
 int launch_rowblock(int B, int mode, const RowblockLaunch& a, hipStream_t st);
 
+// bf16 tiles -> fragment-major packed tiles (PackedTile<B> in lbk_device.h)
+int launch_pack_bf16(const uint16_t* values, int64_t ntiles, int B, uint32_t* packed, hipStream_t st);
+size_t packed_bf16_bytes(int64_t ntiles, int B);
+
 
 // two-kernel SwiGLU: gate/up (+optional RMSNorm prologue) -> h, then down (+residual / fp32 state)
 struct GUArgs {
@@ -33,8 +37,8 @@ struct GUArgs {
   int d_model;
   const float* norm_scale;  // RMSNorm mode: [d_model]
   float eps;
-  const uint16_t* vg; const int32_t* cg; int Kg;
-  const uint16_t* vu; const int32_t* cu; int Ku;
+  const void* pg; const int32_t* cg; int Kg;   // packed gate tiles
+  const void* pu; const int32_t* cu; int Ku;   // packed up tiles
   int R_ff;
   uint16_t* h;              // [N, d_ff] silu(g) * u
   uint16_t* gpre;           // [N, d_ff] optional gate pre-activation
@@ -45,7 +49,7 @@ struct DNArgs {
   int64_t N;
   int64_t d_ff;
   int d_model;
-  const uint16_t* vd; const int32_t* cd; int Kd;
+  const void* pd; const int32_t* cd; int Kd;   // packed down tiles
   int R_m;
   int C_d;                  // d_ff / B
   const uint16_t* resid;    // optional bf16 residual [N, d_model]

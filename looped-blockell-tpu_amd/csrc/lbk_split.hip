@@ -1,12 +1,14 @@
 // lbk_split.hip — the SwiGLU FFN as two register-lean kernels (gfx950, bf16 MFMA).
 //
-// gu_kernel<B, MT, NORM>: a workgroup owns 16*MT tokens.  Their input rows sit
-// in LDS as an XOR-swizzled panel (optionally RMSNorm-ed on the way in from an
-// fp32 state).  Eight waves (two per SIMD) each stream their own d_ff block rows
-// (r = w, w+8, ...): gate and up tiles are consumed in (gate k, up k) pairs from
-// a 2-deep register ring that runs across row boundaries, and h = silu(g) * u
-// is stored as bf16.  No barrier after the panel is built, so the second wave
-// on each SIMD hides the first one's load latency.
+// gu_kernel<B, MT, NORM, INTER>: a workgroup owns 16*MT tokens.  Their input
+// rows sit in LDS as an XOR-swizzled panel (optionally RMSNorm-ed on the way in
+// from an fp32 state), next to a table of the gate/up column indices.  Eight
+// waves (two per SIMD) each stream their own d_ff block rows (r = w, w+8, ...):
+// gate and up tiles are consumed in (gate k, up k) pairs from a 2-deep register
+// ring that runs across row boundaries.  The loop issues the same loads on every
+// position (dead slots are zeroed in the fragment, not branched around), so the
+// compiler's memory-counter waits stay exact and two positions stay in flight.
+// h = silu(g) * u is stored as bf16 (and the pre-activations when INTER).
 //
 // dn_kernel<B, MT, RPW>: a workgroup owns 16*MT tokens and all d_model outputs;
 // wave w keeps RPW down block rows of fp32 accumulators in registers for the
@@ -33,63 +35,15 @@ __device__ __forceinline__ u32x4 lds16(const unsigned char* base, uint32_t off) 
 // ===========================================================================
 // gate/up
 // ===========================================================================
+// One ring slot: the gate and up tiles of one stream position and their input
+// column blocks (-1: dead slot, contributes zero).
 template <int B>
-struct GUPair {
-  WRaw<B> g, u;
-  int cg, cu;   // input column blocks (-1: none)
+struct GUSlot {
+  u32x4 g[1][TileShape<B>::CW], u[1][TileShape<B>::CW];
+  int cg, cu;
 };
 
-template <int B>
-__device__ __forceinline__ void gu_pair_load(GUPair<B>& P, const GUArgs& a, int r, int k, int colg, int colu,
-                                             int cin, int lane) {
-  P.cg = -1;
-  P.cu = -1;
-  if (k < a.Kg) {
-    const int c = __builtin_amdgcn_readlane(colg, k);
-    if (c >= 0 && c < cin) {
-      P.cg = c;
-      load_wraw<B>(a.vg + ((int64_t)r * a.Kg + k) * B * B, lane, P.g);
-    }
-  }
-  if (k < a.Ku) {
-    const int c = __builtin_amdgcn_readlane(colu, k);
-    if (c >= 0 && c < cin) {
-      P.cu = c;
-      load_wraw<B>(a.vu + ((int64_t)r * a.Ku + k) * B * B, lane, P.u);
-    }
-  }
-}
-
-template <int B, int MT>
-__device__ __forceinline__ void gu_pair_compute(const GUPair<B>& P, const unsigned char* xp, int rowb, int i, int g,
-                                                f32x4 (&ag)[MT][TileShape<B>::CW],
-                                                f32x4 (&au)[MT][TileShape<B>::CW]) {
-  constexpr int CW = TileShape<B>::CW;
-  if (P.cg >= 0) {
-    u32x4 f[1][CW];
-    wraw_to_frag<B>(P.g, f);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const u32x4 av = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0}
-                                           : lds16(xp, swz_addr(16 * mt + i, P.cg * (B / 8) + g, rowb));
-#pragma unroll
-      for (int m = 0; m < CW; ++m) ag[mt][m] = mfma_bf16(av, f[0][m], ag[mt][m]);
-    }
-  }
-  if (P.cu >= 0) {
-    u32x4 f[1][CW];
-    wraw_to_frag<B>(P.u, f);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const u32x4 av = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0}
-                                           : lds16(xp, swz_addr(16 * mt + i, P.cu * (B / 8) + g, rowb));
-#pragma unroll
-      for (int m = 0; m < CW; ++m) au[mt][m] = mfma_bf16(av, f[0][m], au[mt][m]);
-    }
-  }
-}
-
-template <int B, int MT, bool NORM>
+template <int B, int MT, bool NORM, bool INTER>
 __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
   constexpr int CW = TileShape<B>::CW;
   constexpr int TM = 16 * MT;
@@ -104,7 +58,17 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
   const int64_t t0 = (int64_t)blockIdx.x * TM;
   const int cin = d_model / B;
   const int64_t d_ff = (int64_t)a.R_ff * B;
+  const int K = a.Kg;                        // == a.Ku >= 1
+  // column table after the panel: (gate col, up col) per (row, slot), -1 if dead
+  int2* ctab = reinterpret_cast<int2*>(smem + (size_t)TM * rowb);
 
+  // ---- column table
+  for (int e = tid; e < a.R_ff * K; e += 512) {
+    int cg = a.cg[e], cu = a.cu[e];
+    cg = (cg >= 0 && cg < cin) ? cg : -1;
+    cu = (cu >= 0 && cu < cin) ? cu : -1;
+    ctab[e] = make_int2(cg, cu);
+  }
   // ---- input panel
   if constexpr (!NORM) {
     const int cpr = d_model / 8;
@@ -145,47 +109,86 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
   }
   __syncthreads();
 
-  // ---- stream this wave's rows: r = w + 8*n; flattened (row, k) pairs, 2-deep ring
-  // kmax >= 1 so that rows with no tiles (K = 0) still store h = silu(0) * 0 = 0
-  const int kmax = (a.Kg > a.Ku ? a.Kg : a.Ku) > 0 ? (a.Kg > a.Ku ? a.Kg : a.Ku) : 1;
-  const int nrows = (a.R_ff - w + 7) / 8;        // rows of this wave
+  // ---- stream this wave's rows r = w + 8n through a two-slot ring of (gate,
+  // up) tile pairs.  Each row takes an even number of positions KP (an odd K
+  // gets one dead padding position), so slot parity repeats per row; every
+  // position issues the same loads (dead ones re-read the row's last tile and
+  // are zeroed in the fragment), so the compiler's memory-counter waits stay
+  // exact and two positions stay in flight across row boundaries.
+  const int nrows = (a.R_ff - w + 7) / 8;
   if (nrows <= 0) return;
-  const int total = nrows * kmax;
+  const int KP = K + (K & 1);
 
-  int colg = -1, colu = -1, colg_n = -1, colu_n = -1;  // column lists of the current / next row
-  auto load_cols = [&](int n, int& cgv, int& cuv) {
-    cgv = -1;
-    cuv = -1;
-    if (n < nrows) {
-      const int r = w + 8 * n;
-      if (lane < a.Kg) cgv = a.cg[(int64_t)r * a.Kg + lane];
-      if (lane < a.Ku) cuv = a.cu[(int64_t)r * a.Ku + lane];
+  int rn = 0, rk = 0;   // next position to fetch
+  auto fetch = [&](GUSlot<B>& S) {
+    const bool live = rn < nrows && rk < K;
+    const int rr = rn < nrows ? rn : nrows - 1;
+    const int kk = rk < K ? rk : K - 1;
+    const int64_t e = (int64_t)(w + 8 * rr) * K + kk;
+    load_pfrag<B>(static_cast<const u32x4*>(a.pg) + e * PackedTile<B>::U32X4, lane, S.g);
+    load_pfrag<B>(static_cast<const u32x4*>(a.pu) + e * PackedTile<B>::U32X4, lane, S.u);
+    const int2 c = ctab[e];
+    S.cg = live ? c.x : -1;
+    S.cu = live ? c.y : -1;
+    if (++rk == KP) {
+      rk = 0;
+      ++rn;
     }
   };
-  load_cols(0, colg, colu);
-  load_cols(1, colg_n, colu_n);
 
-  // ring slots carry the pair at stream index p (row p / kmax, slot p % kmax)
-  GUPair<B> P0, P1;
-  // the first two pairs may straddle the first row boundary
-  {
-    gu_pair_load<B>(P0, a, w, 0, colg, colu, cin, lane);
-    if (1 < total) {
-      if (1 < kmax) gu_pair_load<B>(P1, a, w, 1, colg, colu, cin, lane);
-      else gu_pair_load<B>(P1, a, w + 8, 0, colg_n, colu_n, cin, lane);
-    }
-  }
   f32x4 ag[MT][CW], au[MT][CW];
+  auto compute = [&](const GUSlot<B>& S) {
+    const int cg = uniform(S.cg), cu = uniform(S.cu);
+    u32x4 fg[1][CW], fu[1][CW];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+    for (int m = 0; m < CW; ++m)
 #pragma unroll
-    for (int m = 0; m < CW; ++m) {
-      ag[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-      au[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int v = 0; v < 4; ++v) {
+        fg[0][m][v] = cg >= 0 ? S.g[0][m][v] : 0u;
+        fu[0][m][v] = cu >= 0 ? S.u[0][m][v] : 0u;
+      }
+    const int chg = (cg >= 0 ? cg : 0) * (B / 8) + g, chu = (cu >= 0 ? cu : 0) * (B / 8) + g;
+    u32x4 avg[MT], avu[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      avg[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(smem, swz_addr(16 * mt + i, chg, rowb));
+      avu[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(smem, swz_addr(16 * mt + i, chu, rowb));
     }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int m = 0; m < CW; ++m) ag[mt][m] = mfma_bf16(avg[mt], fg[0][m], ag[mt][m]);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int m = 0; m < CW; ++m) au[mt][m] = mfma_bf16(avu[mt], fu[0][m], au[mt][m]);
+  };
 
-  int n = 0, k = 0;   // row / slot of the pair being consumed
-  auto finish_row = [&]() {
+  GUSlot<B> P0, P1;
+  __builtin_amdgcn_sched_barrier(0);
+  fetch(P0);
+  __builtin_amdgcn_sched_barrier(0);
+  fetch(P1);
+  __builtin_amdgcn_sched_barrier(0);
+  for (int n = 0; n < nrows; ++n) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int m = 0; m < CW; ++m) {
+        ag[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        au[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    // the scheduling barriers keep each slot's fragment conversion after the
+    // other slot's refill, so the wait before it covers only that slot's loads
+    for (int k = 0; k < KP; k += 2) {
+      compute(P0);
+      fetch(P0);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(P1);
+      fetch(P1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // epilogue of row r: h = silu(g) * u (and the pre-activations)
     const int r = w + 8 * n;
     const int64_t col0 = (int64_t)r * B + CW * i;
 #pragma unroll
@@ -202,47 +205,12 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
         }
         if (t < a.N) {
           store_bf16<CW>(a.h + t * d_ff + col0, o);
-          if (a.gpre) store_bf16<CW>(a.gpre + t * d_ff + col0, gv);
-          if (a.uout) store_bf16<CW>(a.uout + t * d_ff + col0, uv);
+          if constexpr (INTER) {
+            if (a.gpre) store_bf16<CW>(a.gpre + t * d_ff + col0, gv);
+            if (a.uout) store_bf16<CW>(a.uout + t * d_ff + col0, uv);
+          }
         }
       }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int m = 0; m < CW; ++m) {
-        ag[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-        au[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-  };
-  // refill a ring slot with stream index p2 (called after advance(), so p2 lies in
-  // row n or n+1, whose column lists are cached)
-  auto refill = [&](GUPair<B>& P, int p2) {
-    if (p2 >= total) return;
-    const int n2 = p2 / kmax, k2 = p2 - n2 * kmax;
-    if (n2 == n) gu_pair_load<B>(P, a, w + 8 * n2, k2, colg, colu, cin, lane);
-    else gu_pair_load<B>(P, a, w + 8 * n2, k2, colg_n, colu_n, cin, lane);
-  };
-  auto advance = [&]() {
-    if (++k == kmax) {
-      finish_row();
-      k = 0;
-      ++n;
-      colg = colg_n;
-      colu = colu_n;
-      load_cols(n + 1, colg_n, colu_n);
-    }
-  };
-
-  // consume pair p, move (n, k) to pair p+1, then load pair p+2 (row n or n+1)
-  for (int p = 0; p < total; p += 2) {
-    gu_pair_compute<B, MT>(P0, smem, rowb, i, g, ag, au);
-    advance();
-    refill(P0, p + 2);
-    if (p + 1 < total) {
-      gu_pair_compute<B, MT>(P1, smem, rowb, i, g, ag, au);
-      advance();
-      refill(P1, p + 3);
-    }
   }
 }
 
@@ -286,10 +254,11 @@ __device__ __forceinline__ int dn_hits(int c0, int ncb, const int (&colreg)[RPW]
 
 // weight tile of hit q (row rho of this wave, slot k from the hit list)
 template <int B, int RPW>
-__device__ __forceinline__ void dn_tile_load(WRaw<B>& T, const DNArgs& a, int w, int rho, int list_k, int idx,
-                                             int lane) {
+__device__ __forceinline__ void dn_tile_load(u32x4 (&T)[1][TileShape<B>::CW], const DNArgs& a, int w, int rho,
+                                             int list_k, int idx, int lane) {
   const int k = __builtin_amdgcn_readlane(list_k, idx);
-  load_wraw<B>(a.vd + ((int64_t)(w * RPW + rho) * a.Kd + k) * B * B, lane, T);
+  load_pfrag<B>(static_cast<const u32x4*>(a.pd) + ((int64_t)(w * RPW + rho) * a.Kd + k) * PackedTile<B>::U32X4,
+                lane, T);
 }
 
 template <int B, int MT, int RPW>
@@ -380,7 +349,7 @@ __global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
       };
       // three-slot shift register of weight tiles: D0 holds hit q, D1 hit q+1,
       // D2 hit q+2; hit q+3 is requested as q is consumed
-      WRaw<B> D0, D1, D2;
+      u32x4 D0[1][CW], D1[1][CW], D2[1][CW];
       if (skip < bend) dn_tile_load<B, RPW>(D0, a, w, row_of(skip), list_k, 0, lane);
       if (skip + 1 < bend) dn_tile_load<B, RPW>(D1, a, w, row_of(skip + 1), list_k, 1, lane);
       if (skip + 2 < bend) dn_tile_load<B, RPW>(D2, a, w, row_of(skip + 2), list_k, 2, lane);
@@ -390,9 +359,12 @@ __global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
         const int e = ends[rr] < bend ? ends[rr] : bend;
         for (; q < e; ++q) {
           u32x4 f[1][CW];
-          wraw_to_frag<B>(D0, f);
-          D0 = D1;
-          D1 = D2;
+#pragma unroll
+          for (int m = 0; m < CW; ++m) {
+            f[0][m] = D0[0][m];
+            D0[0][m] = D1[0][m];
+            D1[0][m] = D2[0][m];
+          }
           if (q + 3 < bend) dn_tile_load<B, RPW>(D2, a, w, row_of(q + 3), list_k, q + 3 - skip, lane);
           const int cb = __builtin_amdgcn_readlane(list_cb, q - skip);
 #pragma unroll
@@ -460,19 +432,25 @@ static int dn_rpw(int R_m) {
   return -1;
 }
 
+static size_t gu_lds(int d_model, int R_ff, int K, int mt) {
+  return (size_t)16 * mt * d_model * 2 + (size_t)R_ff * K * 8;
+}
+
 bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd) {
   if (B != 16 && B != 32) return false;
-  if (Kg > 64 || Ku > 64 || Kd > 64) return false;   // one lane per slot in the column lookups
+  if (Kg != Ku || Kg < 1) return false;               // gate and up stream in lockstep
+  if (Kd > 64) return false;                          // one lane per slot in the down column lookup
   if (d_model % 128) return false;                    // swizzled panel rows
-  if (gu_mt(d_model) == 0) return false;
+  const int mt = gu_mt(d_model);
+  if (mt == 0 || gu_lds(d_model, R_ff, Kg, mt) > 163840) return false;
   if (R_m * B != d_model || dn_rpw(R_m) < 0) return false;
   if ((R_ff * B) % 8) return false;
   return true;
 }
 
-template <int B, int MT, bool NORM>
+template <int B, int MT, bool NORM, bool INTER>
 static int launch_gu_t(const GUArgs& a, hipStream_t st) {
-  auto kern = gu_kernel<B, MT, NORM>;
+  auto kern = gu_kernel<B, MT, NORM, INTER>;
   static bool configured = false;
   if (!configured) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 163840) != hipSuccess)
@@ -480,7 +458,7 @@ static int launch_gu_t(const GUArgs& a, hipStream_t st) {
     configured = true;
   }
   const int TM = 16 * MT;
-  const size_t lds = (size_t)TM * a.d_model * 2;
+  const size_t lds = gu_lds(a.d_model, a.R_ff, a.Kg, MT);
   hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + TM - 1) / TM)), dim3(512), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
@@ -488,8 +466,12 @@ static int launch_gu_t(const GUArgs& a, hipStream_t st) {
 int launch_gu(int B, bool norm, const GUArgs& a, hipStream_t st) {
   if (a.N == 0) return 0;
   const int mt = gu_mt(a.d_model);
-#define LBK_GU(BB, MM)                                                                         \
-  if (B == BB && mt == MM) return norm ? launch_gu_t<BB, MM, true>(a, st) : launch_gu_t<BB, MM, false>(a, st);
+  const bool inter = a.gpre || a.uout;
+#define LBK_GU(BB, MM)                                                                          \
+  if (B == BB && mt == MM) {                                                                    \
+    if (norm) return launch_gu_t<BB, MM, true, false>(a, st);                                   \
+    return inter ? launch_gu_t<BB, MM, false, true>(a, st) : launch_gu_t<BB, MM, false, false>(a, st); \
+  }
   LBK_GU(16, 4) LBK_GU(16, 2) LBK_GU(32, 4) LBK_GU(32, 2)
 #undef LBK_GU
   return -2;
