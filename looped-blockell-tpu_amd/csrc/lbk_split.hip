@@ -217,48 +217,68 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
 // ===========================================================================
 // down
 // ===========================================================================
-// h column blocks per LDS stage: 256 bytes of each token row (16 chunks)
+// h column blocks per LDS stage: 512 bytes of each token row (32 chunks)
 template <int B>
-struct DnStage { static constexpr int G = 128 / B; };
+struct DnStage { static constexpr int G = 256 / B; };
 
-// Hits of a stage in (row, column block, slot) order.  Lane j holds hit skip+j:
-// its column block within the stage (list_cb) and its weight slot k (list_k);
-// ends[rho] is the cumulative hit count through row rho (uniform).  Returns the
-// total.  A row may name one column block more than once, so the total can
-// exceed 64 and the caller then walks it in batches of 64.
-template <int B, int RPW>
-__device__ __forceinline__ int dn_hits(int c0, int ncb, const int (&colreg)[RPW], int lane, int skip, int& list_cb,
-                                       int& list_k, int (&ends)[RPW]) {
-  int n = 0;
-  list_cb = 0;
-  list_k = 0;
-#pragma unroll
-  for (int rho = 0; rho < RPW; ++rho) {
-#pragma unroll
-    for (int cb = 0; cb < DnStage<B>::G; ++cb) {
-      if (cb >= ncb) break;
-      uint64_t m = __ballot(colreg[rho] == c0 + cb);
-      while (m) {
-        if (lane == n - skip) {
-          list_cb = cb;
-          list_k = __builtin_ctzll(m);
-        }
-        m &= m - 1;
-        ++n;
-      }
-    }
-    ends[rho] = n;
-  }
-  return n;
+// Per-wave hit lists of one stage, one per down row rho of the wave: lane j of
+// v[rho] holds the row's j-th hit as e = dead << 15 | cb << 6 | k (column block
+// cb within the stage, weight slot k), in slot order.  A row with an odd number
+// of hits gets a dead copy of its last hit appended, so a two-slot ring consumes
+// every row with the same slot parity.  pcnt[rho] is the padded count, tot the
+// sum (all uniform).
+template <int RPW>
+struct HitList {
+  int v[RPW];
+  int pcnt[RPW];
+  int tot;
+};
+
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
 }
 
-// weight tile of hit q (row rho of this wave, slot k from the hit list)
-template <int B, int RPW>
-__device__ __forceinline__ void dn_tile_load(u32x4 (&T)[1][TileShape<B>::CW], const DNArgs& a, int w, int rho,
-                                             int list_k, int idx, int lane) {
-  const int k = __builtin_amdgcn_readlane(list_k, idx);
-  load_pfrag<B>(static_cast<const u32x4*>(a.pd) + ((int64_t)(w * RPW + rho) * a.Kd + k) * PackedTile<B>::U32X4,
-                lane, T);
+template <int RPW>
+__device__ __forceinline__ void dn_build(HitList<RPW>& L, int c0, int ncb, const int (&colreg)[RPW], int lane) {
+  L.tot = 0;
+#pragma unroll
+  for (int rho = 0; rho < RPW; ++rho) {
+    const int cb = colreg[rho] - c0;
+    const bool hit = cb >= 0 && cb < ncb;
+    const uint64_t m = __ballot(hit);
+    const int cnt = __builtin_popcountll(m);
+    // hits first (in slot order), then the other lanes: a permutation of the wave
+    const int dst = hit ? lanes_below(m) : cnt + lanes_below(~m);
+    int v = __builtin_amdgcn_ds_permute(dst << 2, (cb << 6) | lane);
+    if (cnt & 1) {
+      const int last = __builtin_amdgcn_readlane(v, cnt - 1);
+      v = lane == cnt ? (last | (1 << 15)) : v;
+    }
+    L.v[rho] = v;
+    L.pcnt[rho] = cnt + (cnt & 1);
+    L.tot += L.pcnt[rho];
+  }
+}
+
+// entry at position q of the list (q < L.tot); returns the row in rho
+template <int RPW>
+__device__ __forceinline__ int hit_entry(const HitList<RPW>& L, int q, int& rho) {
+  int r = 0, base = 0;
+#pragma unroll
+  for (int rr = 0; rr + 1 < RPW; ++rr) {
+    const bool past = q >= base + L.pcnt[rr] && r == rr;
+    base += past ? L.pcnt[rr] : 0;
+    r += past ? 1 : 0;
+  }
+  rho = r;
+  const int j = q - base;
+  int e = __builtin_amdgcn_readlane(L.v[0], j);
+#pragma unroll
+  for (int rr = 1; rr < RPW; ++rr) {
+    const int er = __builtin_amdgcn_readlane(L.v[rr], j);
+    e = r == rr ? er : e;
+  }
+  return e;
 }
 
 template <int B, int MT, int RPW>
@@ -266,12 +286,12 @@ __global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
   constexpr int CW = TileShape<B>::CW;
   constexpr int TM = 16 * MT;
   constexpr int G = DnStage<B>::G;
-  constexpr int SROWB = G * B * 2;                   // bytes per token row of a stage (256)
+  constexpr int SROWB = G * B * 2;                   // bytes per token row of a stage (512)
   constexpr int SBYTES = TM * SROWB;                 // bytes per stage
   constexpr int CHUNKS = SBYTES / 16;                // 16-byte chunks per stage
   constexpr int PER_T = (CHUNKS + 511) / 512;        // chunks per thread per stage
   static_assert(TileShape<B>::NKS == 1, "down kernel handles B <= 32");
-  static_assert(SROWB == 256, "stage rows must cover 16 chunks");
+  static_assert(SROWB % 256 == 0, "stage rows must cover multiples of 16 chunks");
   __shared__ __attribute__((aligned(16))) unsigned char stages[2][SBYTES];
 
   const int tid = threadIdx.x;
@@ -283,6 +303,7 @@ __global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
   const int64_t d_ff = a.d_ff;
   const int C = a.C_d;
   const int nstages = (C + G - 1) / G;
+  const u32x4* pd = static_cast<const u32x4*>(a.pd);
 
   int colreg[RPW];
 #pragma unroll
@@ -325,60 +346,85 @@ __global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
     }
   };
 
+  // ring slots: weight fragments and column block (-1: dead entry)
+  struct Slot {
+    u32x4 f[1][CW];
+    int cb;
+  };
+  HitList<RPW> cur, nxt;
+  // position q of the stream made of the current stage's list followed by the
+  // next stage's list; beyond both, a dead re-read of this wave's first tile
+  auto fetch = [&](Slot& S, int q) {
+    int e = 1 << 15, rho = 0;
+    if (q < cur.tot) e = hit_entry<RPW>(cur, q, rho);
+    else if (q - cur.tot < nxt.tot) e = hit_entry<RPW>(nxt, q - cur.tot, rho);
+    const int rm = (w * RPW + rho) < a.R_m ? w * RPW + rho : a.R_m - 1;
+    const int k = e & 63;
+    load_pfrag<B>(pd + ((int64_t)rm * a.Kd + k) * PackedTile<B>::U32X4, lane, S.f);
+    S.cb = (e >> 15) ? -1 : ((e >> 6) & 63);
+  };
+  auto compute = [&](const Slot& S, const unsigned char* sb, f32x4 (&ac)[MT][CW]) {
+    const int cb = uniform(S.cb);
+    u32x4 f[CW];
+#pragma unroll
+    for (int m = 0; m < CW; ++m)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) f[m][v] = cb >= 0 ? S.f[0][m][v] : 0u;
+    const int ch = (cb >= 0 ? cb : 0) * (B / 8) + g;
+    u32x4 av[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      av[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(sb, swz_addr(16 * mt + i, ch, SROWB));
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int m = 0; m < CW; ++m) ac[mt][m] = mfma_bf16(av[mt], f[m], ac[mt][m]);
+  };
+
+  const bool any_rows = (w * RPW < a.R_m) && a.Kd > 0;
+  Slot S0, S1;
+  nxt.tot = 0;
+  dn_build<RPW>(cur, 0, (C < G ? C : G), colreg, lane);
+  if (nstages > 1) dn_build<RPW>(nxt, G, (C - G) < G ? (C - G) : G, colreg, lane);
   stage_fetch(0);
   stage_store(0);
+  bool ring_ok = false;   // S0/S1 hold positions 0 and 1 of the current stage
   __syncthreads();
   for (int s = 0; s < nstages; ++s) {
     const int buf = s & 1;
-    if (s + 1 < nstages) stage_fetch(s + 1);
-    // this wave's tiles reading stage s, row by row; a 2-deep ring of weight
-    // tiles runs across the rows (hit q sits in slot q & 1)
-    const int c0 = s * G;
-    const int ncb = (C - c0) < G ? (C - c0) : G;
     const unsigned char* sb = &stages[buf][0];
-    for (int skip = 0;; skip += 64) {
-      int list_cb, list_k, ends[RPW];
-      const int nall = dn_hits<B, RPW>(c0, ncb, colreg, lane, skip, list_cb, list_k, ends);
-      const int bend = (nall - skip) < 64 ? nall : skip + 64;
-      // row of hit q (uniform): the first rho with q < ends[rho]
-      auto row_of = [&](int q) {
-        int r = 0;
-#pragma unroll
-        for (int rho = 0; rho + 1 < RPW; ++rho) r += (q >= ends[rho]) ? 1 : 0;
-        return r;
-      };
-      // three-slot shift register of weight tiles: D0 holds hit q, D1 hit q+1,
-      // D2 hit q+2; hit q+3 is requested as q is consumed
-      u32x4 D0[1][CW], D1[1][CW], D2[1][CW];
-      if (skip < bend) dn_tile_load<B, RPW>(D0, a, w, row_of(skip), list_k, 0, lane);
-      if (skip + 1 < bend) dn_tile_load<B, RPW>(D1, a, w, row_of(skip + 1), list_k, 1, lane);
-      if (skip + 2 < bend) dn_tile_load<B, RPW>(D2, a, w, row_of(skip + 2), list_k, 2, lane);
-      int q = skip;
+    if (s + 1 < nstages) stage_fetch(s + 1);
+    if (any_rows && cur.tot > 0) {
+      if (!ring_ok) {
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(S0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(S1, 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      int q = 0;
 #pragma unroll
       for (int rr = 0; rr < RPW; ++rr) {
-        const int e = ends[rr] < bend ? ends[rr] : bend;
-        for (; q < e; ++q) {
-          u32x4 f[1][CW];
-#pragma unroll
-          for (int m = 0; m < CW; ++m) {
-            f[0][m] = D0[0][m];
-            D0[0][m] = D1[0][m];
-            D1[0][m] = D2[0][m];
-          }
-          if (q + 3 < bend) dn_tile_load<B, RPW>(D2, a, w, row_of(q + 3), list_k, q + 3 - skip, lane);
-          const int cb = __builtin_amdgcn_readlane(list_cb, q - skip);
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const u32x4 av = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0}
-                                                 : lds16(sb, swz_addr(16 * mt + i, cb * (B / 8) + g, SROWB));
-#pragma unroll
-            for (int m = 0; m < CW; ++m) acc[rr][mt][m] = mfma_bf16(av, f[0][m], acc[rr][mt][m]);
-          }
+        for (int j = 0; j < cur.pcnt[rr]; j += 2) {
+          compute(S0, sb, acc[rr]);
+          fetch(S0, q + 2);
+          __builtin_amdgcn_sched_barrier(0);
+          compute(S1, sb, acc[rr]);
+          fetch(S1, q + 3);
+          __builtin_amdgcn_sched_barrier(0);
+          q += 2;
         }
       }
-      if (nall <= skip + 64) break;
     }
+    // the ring now holds positions 0 and 1 of the next stage iff this stage ran and the next has hits
+    ring_ok = any_rows && cur.tot > 0 && nxt.tot > 0;
     if (s + 1 < nstages) stage_store(buf ^ 1);
+    cur = nxt;
+    nxt.tot = 0;
+    if (s + 2 < nstages) {
+      const int c2 = (s + 2) * G;
+      dn_build<RPW>(nxt, c2, (C - c2) < G ? (C - c2) : G, colreg, lane);
+    }
     __syncthreads();
   }
 
@@ -439,7 +485,7 @@ static size_t gu_lds(int d_model, int R_ff, int K, int mt) {
 bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd) {
   if (B != 16 && B != 32) return false;
   if (Kg != Ku || Kg < 1) return false;               // gate and up stream in lockstep
-  if (Kd > 64) return false;                          // one lane per slot in the down column lookup
+  if (Kd > 63) return false;                          // one lane per slot; <= 4 * 64 hit-list entries
   if (d_model % 128) return false;                    // swizzled panel rows
   const int mt = gu_mt(d_model);
   if (mt == 0 || gu_lds(d_model, R_ff, Kg, mt) > 163840) return false;

@@ -100,22 +100,23 @@ def test_swiglu_with_intermediates(gpu, case):
         assert rel <= TOL, f"{name}: rel {rel} abs {ab}"
 
 
+@pytest.mark.parametrize("Kd", [63, 64])
 @pytest.mark.parametrize("case", [(256, 1024, 16), (128, 512, 16), (1024, 4096, 32)])
-def test_swiglu_duplicate_and_empty_columns(gpu, case):
+def test_swiglu_duplicate_and_empty_columns(gpu, case, Kd):
     """Rows that name one column block several times sum every copy (as the oracle's
-    per-slot sum does); a down row whose 64 slots all fall in one 128-column stage
-    makes that stage's hit list longer than one wave; empty rows give zeros."""
+    per-slot sum does); a down row whose slots all fall in the first LDS stage
+    gives that stage a full hit list; empty rows give zeros.  Kd = 63 runs the
+    two-kernel split path, Kd = 64 the row-block path."""
     d_model, d_ff, B = case
-    _say(f"swiglu duplicate columns {case}")
+    _say(f"swiglu duplicate columns {case} Kd={Kd}")
     rng = np.random.default_rng(21)
     g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25)
     g[1][0, :] = g[1][0, 0]                      # every gate slot of row 0 -> one column
     u[1][1, :] = -1                              # up row 1 empty -> h row block 1 == 0
-    Kd = 64
     Cf = d_ff // B
     dv = O.bf16_round((rng.standard_normal((d_model // B, Kd, B, B)) * 0.02).astype(np.float32))
     dc = rng.integers(0, Cf, size=(d_model // B, Kd)).astype(np.int32)
-    dc[0, :] = rng.integers(0, min(Cf, 128 // B), size=Kd)   # row 0: all slots in the first stage
+    dc[0, :] = rng.integers(0, min(Cf, 256 // B), size=Kd)   # row 0: all slots in the first stage
     d = (dv, dc)
     x = T.act(rng, 70, d_model)
     out, *_ = T.abi_swiglu(T.to_gpu_bf16(x), T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d), add_residual=True)
