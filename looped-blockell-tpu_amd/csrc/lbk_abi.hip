@@ -135,10 +135,12 @@ static int pack_ffn(const lbk_bell* gate, const lbk_bell* up, const lbk_bell* do
   char* p = ws;
   const lbk_bell* ws3[3] = {gate, up, down};
   const void** dst[3] = {&out->g, &out->u, &out->d};
+  const int cols[3] = {down->R, down->R, gate->R};   // input column blocks: d_model / B, d_model / B, d_ff / B
   for (int t = 0; t < 3; ++t) {
     const int64_t nt = (int64_t)ws3[t]->R * ws3[t]->K;
     *dst[t] = p;
-    if (launch_pack_bf16(ws3[t]->values, nt, B, reinterpret_cast<uint32_t*>(p), st) != 0) return LBK_ERR_LAUNCH;
+    if (launch_pack_bf16(ws3[t]->values, ws3[t]->col_idx, nt, cols[t], B, reinterpret_cast<uint32_t*>(p), st) != 0)
+      return LBK_ERR_LAUNCH;
     p += align256(packed_bf16_bytes(nt, B));
   }
   out->bytes = (size_t)(p - ws);

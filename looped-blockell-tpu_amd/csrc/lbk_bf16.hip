@@ -191,17 +191,25 @@ int launch_injection(const uint16_t* h, const uint16_t* e, const float* log_A, c
 }
 
 // ---------------------------------------------------------------------------
-// bf16 tiles [T, B, B] ([B_in, B_out] each) -> fragment-major packed tiles
-// (layout described with PackedTile in lbk_device.h); one thread per dword
+// bf16 tiles [R*K, B, B] ([B_in, B_out] each) -> fragment-major packed tiles
+// (layout described with PackedTile in lbk_device.h), one thread per dword.
+// Tiles of dead slots (col < 0 or col >= C) are written as zeros, and one
+// extra zero tile follows the R*K tiles, so kernels can point padding and dead
+// positions at zero weights instead of masking them.
 // ---------------------------------------------------------------------------
 template <int B>
-__global__ __launch_bounds__(256) void pack_bf16_kernel(const uint16_t* __restrict__ values, int64_t ndw,
-                                                        uint32_t* __restrict__ packed) {
+__global__ __launch_bounds__(256) void pack_bf16_kernel(const uint16_t* __restrict__ values,
+                                                        const int32_t* __restrict__ col, int64_t ntiles, int C,
+                                                        int64_t ndw, uint32_t* __restrict__ packed) {
   constexpr int NKS = TileShape<B>::NKS, CW = TileShape<B>::CW;
   constexpr int PER_TILE = PackedTile<B>::U32X4 * 4;   // dwords per packed tile
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= ndw) return;
   const int64_t tile = idx / PER_TILE;
+  if (tile >= ntiles || col[tile] < 0 || col[tile] >= C) {
+    packed[idx] = 0u;
+    return;
+  }
   int r = (int)(idx - tile * PER_TILE);
   const int u = r & 3;
   r >>= 2;
@@ -217,26 +225,21 @@ __global__ __launch_bounds__(256) void pack_bf16_kernel(const uint16_t* __restri
 
 size_t packed_bf16_bytes(int64_t ntiles, int B) {
   switch (B) {
-    case 16: return (size_t)ntiles * PackedTile<16>::U32X4 * 16;
-    case 32: return (size_t)ntiles * PackedTile<32>::U32X4 * 16;
-    case 64: return (size_t)ntiles * PackedTile<64>::U32X4 * 16;
+    case 16: return (size_t)(ntiles + 1) * PackedTile<16>::U32X4 * 16;
+    case 32: return (size_t)(ntiles + 1) * PackedTile<32>::U32X4 * 16;
+    case 64: return (size_t)(ntiles + 1) * PackedTile<64>::U32X4 * 16;
     default: return 0;
   }
 }
 
-int launch_pack_bf16(const uint16_t* values, int64_t ntiles, int B, uint32_t* packed, hipStream_t st) {
-  if (ntiles == 0) return 0;
-  int64_t ndw;
-  switch (B) {
-    case 16: ndw = ntiles * PackedTile<16>::U32X4 * 4; break;
-    case 32: ndw = ntiles * PackedTile<32>::U32X4 * 4; break;
-    case 64: ndw = ntiles * PackedTile<64>::U32X4 * 4; break;
-    default: return -2;
-  }
+int launch_pack_bf16(const uint16_t* values, const int32_t* col, int64_t ntiles, int C, int B, uint32_t* packed,
+                     hipStream_t st) {
+  const int64_t ndw = (int64_t)(packed_bf16_bytes(ntiles, B) / 4);
+  if (ndw == 0) return -2;
   const unsigned grid = (unsigned)((ndw + 255) / 256);
-  if (B == 16) hipLaunchKernelGGL(pack_bf16_kernel<16>, dim3(grid), dim3(256), 0, st, values, ndw, packed);
-  if (B == 32) hipLaunchKernelGGL(pack_bf16_kernel<32>, dim3(grid), dim3(256), 0, st, values, ndw, packed);
-  if (B == 64) hipLaunchKernelGGL(pack_bf16_kernel<64>, dim3(grid), dim3(256), 0, st, values, ndw, packed);
+  if (B == 16) hipLaunchKernelGGL(pack_bf16_kernel<16>, dim3(grid), dim3(256), 0, st, values, col, ntiles, C, ndw, packed);
+  if (B == 32) hipLaunchKernelGGL(pack_bf16_kernel<32>, dim3(grid), dim3(256), 0, st, values, col, ntiles, C, ndw, packed);
+  if (B == 64) hipLaunchKernelGGL(pack_bf16_kernel<64>, dim3(grid), dim3(256), 0, st, values, col, ntiles, C, ndw, packed);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -24,9 +24,11 @@ struct RowblockLaunch {
 // mode: 0 = product (+bias), 1 = gate/up with SiLU*mul, 2 = down (+residual)
 int launch_rowblock(int B, int mode, const RowblockLaunch& a, hipStream_t st);
 
-// bf16 tiles -> fragment-major packed tiles (PackedTile<B> in lbk_device.h)
-int launch_pack_bf16(const uint16_t* values, int64_t ntiles, int B, uint32_t* packed, hipStream_t st);
-size_t packed_bf16_bytes(int64_t ntiles, int B);
+// bf16 tiles -> fragment-major packed tiles (PackedTile<B> in lbk_device.h); dead
+// slots (col < 0 or >= C) become zero tiles and one zero tile is appended at index ntiles
+int launch_pack_bf16(const uint16_t* values, const int32_t* col, int64_t ntiles, int C, int B, uint32_t* packed,
+                     hipStream_t st);
+size_t packed_bf16_bytes(int64_t ntiles, int B);   // includes the appended zero tile
 
 
 // two-kernel SwiGLU: gate/up (+optional RMSNorm prologue) -> h, then down (+residual / fp32 state)

@@ -23,11 +23,6 @@
 
 namespace lbk {
 
-// 16-byte chunk c of row `row` lives at chunk c ^ (row & 15); rows must span a
-// multiple of 16 chunks (256 bytes)
-__device__ __forceinline__ uint32_t swz_addr(int row, int chunk, int rowb) {
-  return (uint32_t)(row * rowb + ((chunk ^ (row & 15)) << 4));
-}
 __device__ __forceinline__ u32x4 lds16(const unsigned char* base, uint32_t off) {
   return *reinterpret_cast<const u32x4*>(base + off);
 }
@@ -35,22 +30,37 @@ __device__ __forceinline__ u32x4 lds16(const unsigned char* base, uint32_t off) 
 // ===========================================================================
 // gate/up
 // ===========================================================================
-// One ring slot: the gate and up tiles of one stream position and their input
-// column blocks (-1: dead slot, contributes zero).
+// Panel layout shared by the kernels here: token row 16*mt + i of a tile of
+// 16*MT rows is stored at row slot i*MT + mt (so the MT rows a lane reads are
+// ROWB apart and fit the ds_read immediate offset), and 16-byte chunk c of it
+// at chunk c ^ i (i = row & 15), which keeps the eight lanes of one LDS read
+// phase on distinct banks.
+template <int MT>
+__device__ __forceinline__ uint32_t panel_addr(int row, int chunk, int rowb) {
+  const int i = row & 15, mt = row >> 4;
+  return (uint32_t)((i * MT + mt) * rowb + ((chunk ^ i) << 4));
+}
+
+// One ring slot: the gate and up fragments of one stream position and their
+// input column blocks (dead slots point at the packed zero tile and column 0).
 template <int B>
 struct GUSlot {
   u32x4 g[1][TileShape<B>::CW], u[1][TileShape<B>::CW];
   int cg, cu;
 };
 
+// gate/up panel row stride: 2048 bytes (MT = 4, d_model <= 1024) or 4096 (MT = 2)
+template <int MT>
+struct GUPanel { static constexpr int ROWB = 8192 / MT; };
+
 template <int B, int MT, bool NORM, bool INTER>
 __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
   constexpr int CW = TileShape<B>::CW;
   constexpr int TM = 16 * MT;
+  constexpr int ROWB = GUPanel<MT>::ROWB;
   static_assert(TileShape<B>::NKS == 1, "gate/up kernel handles B <= 32");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int d_model = a.d_model;
-  const int rowb = d_model * 2;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = uniform(tid >> 6);
@@ -59,14 +69,15 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
   const int cin = d_model / B;
   const int64_t d_ff = (int64_t)a.R_ff * B;
   const int K = a.Kg;                        // == a.Ku >= 1
-  // column table after the panel: (gate col, up col) per (row, slot), -1 if dead
-  int2* ctab = reinterpret_cast<int2*>(smem + (size_t)TM * rowb);
+  const int64_t ztile = (int64_t)a.R_ff * K; // index of the packed zero tile
+  // column table after the panel: (gate col, up col) per (row, slot); dead -> 0
+  int2* ctab = reinterpret_cast<int2*>(smem + (size_t)TM * ROWB);
 
   // ---- column table
   for (int e = tid; e < a.R_ff * K; e += 512) {
     int cg = a.cg[e], cu = a.cu[e];
-    cg = (cg >= 0 && cg < cin) ? cg : -1;
-    cu = (cu >= 0 && cu < cin) ? cu : -1;
+    cg = (cg >= 0 && cg < cin) ? cg : 0;
+    cu = (cu >= 0 && cu < cin) ? cu : 0;
     ctab[e] = make_int2(cg, cu);
   }
   // ---- input panel
@@ -77,7 +88,7 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
       const int64_t t = t0 + row;
       u32x4 v = {0, 0, 0, 0};
       if (t < a.N) v = *reinterpret_cast<const u32x4*>(a.x + t * d_model + 8 * c);
-      *reinterpret_cast<u32x4*>(smem + swz_addr(row, c, rowb)) = v;
+      *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, c, ROWB)) = v;
     }
   } else {
     // fp32 state rows -> RMSNorm -> bf16 panel; one wave per row, 8 contiguous values per lane per step
@@ -103,7 +114,7 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
                          pack2_bf16(v0[2] * rs * s0[2], v0[3] * rs * s0[3]),
                          pack2_bf16(v1[0] * rs * s1[0], v1[1] * rs * s1[1]),
                          pack2_bf16(v1[2] * rs * s1[2], v1[3] * rs * s1[3])};
-        *reinterpret_cast<u32x4*>(smem + swz_addr(row, c / 8, rowb)) = o;
+        *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, c / 8, ROWB)) = o;
       }
     }
   }
@@ -111,25 +122,26 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
 
   // ---- stream this wave's rows r = w + 8n through a two-slot ring of (gate,
   // up) tile pairs.  Each row takes an even number of positions KP (an odd K
-  // gets one dead padding position), so slot parity repeats per row; every
-  // position issues the same loads (dead ones re-read the row's last tile and
-  // are zeroed in the fragment), so the compiler's memory-counter waits stay
-  // exact and two positions stay in flight across row boundaries.
+  // gets one padding position that reads the zero tile), so slot parity repeats
+  // per row; every position issues the same loads, so the compiler's
+  // memory-counter waits stay exact and two positions stay in flight across
+  // row boundaries.
   const int nrows = (a.R_ff - w + 7) / 8;
   if (nrows <= 0) return;
   const int KP = K + (K & 1);
+  const u32x4* pg = static_cast<const u32x4*>(a.pg);
+  const u32x4* pu = static_cast<const u32x4*>(a.pu);
+  const uint32_t lbase = (uint32_t)(i * MT * ROWB);   // this lane's first panel row
 
   int rn = 0, rk = 0;   // next position to fetch
   auto fetch = [&](GUSlot<B>& S) {
     const bool live = rn < nrows && rk < K;
-    const int rr = rn < nrows ? rn : nrows - 1;
-    const int kk = rk < K ? rk : K - 1;
-    const int64_t e = (int64_t)(w + 8 * rr) * K + kk;
-    load_pfrag<B>(static_cast<const u32x4*>(a.pg) + e * PackedTile<B>::U32X4, lane, S.g);
-    load_pfrag<B>(static_cast<const u32x4*>(a.pu) + e * PackedTile<B>::U32X4, lane, S.u);
-    const int2 c = ctab[e];
-    S.cg = live ? c.x : -1;
-    S.cu = live ? c.y : -1;
+    const int64_t e = live ? (int64_t)(w + 8 * rn) * K + rk : ztile;
+    load_pfrag<B>(pg + e * PackedTile<B>::U32X4, lane, S.g);
+    load_pfrag<B>(pu + e * PackedTile<B>::U32X4, lane, S.u);
+    const int2 c = ctab[live ? e : 0];
+    S.cg = c.x;
+    S.cu = c.y;
     if (++rk == KP) {
       rk = 0;
       ++rn;
@@ -139,29 +151,22 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
   f32x4 ag[MT][CW], au[MT][CW];
   auto compute = [&](const GUSlot<B>& S) {
     const int cg = uniform(S.cg), cu = uniform(S.cu);
-    u32x4 fg[1][CW], fu[1][CW];
-#pragma unroll
-    for (int m = 0; m < CW; ++m)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        fg[0][m][v] = cg >= 0 ? S.g[0][m][v] : 0u;
-        fu[0][m][v] = cu >= 0 ? S.u[0][m][v] : 0u;
-      }
-    const int chg = (cg >= 0 ? cg : 0) * (B / 8) + g, chu = (cu >= 0 ? cu : 0) * (B / 8) + g;
+    const uint32_t ag0 = lbase + (((cg * (B / 8) + g) ^ i) << 4);
+    const uint32_t au0 = lbase + (((cu * (B / 8) + g) ^ i) << 4);
     u32x4 avg[MT], avu[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      avg[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(smem, swz_addr(16 * mt + i, chg, rowb));
-      avu[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(smem, swz_addr(16 * mt + i, chu, rowb));
+      avg[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(smem, ag0 + mt * ROWB);
+      avu[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(smem, au0 + mt * ROWB);
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int m = 0; m < CW; ++m) ag[mt][m] = mfma_bf16(avg[mt], fg[0][m], ag[mt][m]);
+      for (int m = 0; m < CW; ++m) ag[mt][m] = mfma_bf16(avg[mt], S.g[0][m], ag[mt][m]);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int m = 0; m < CW; ++m) au[mt][m] = mfma_bf16(avu[mt], fu[0][m], au[mt][m]);
+      for (int m = 0; m < CW; ++m) au[mt][m] = mfma_bf16(avu[mt], S.u[0][m], au[mt][m]);
   };
 
   GUSlot<B> P0, P1;
@@ -178,8 +183,8 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
         ag[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
         au[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-    // the scheduling barriers keep each slot's fragment conversion after the
-    // other slot's refill, so the wait before it covers only that slot's loads
+    // the scheduling barriers keep each slot's use after the other slot's
+    // refill, so the wait before it covers only that slot's loads
     for (int k = 0; k < KP; k += 2) {
       compute(P0);
       fetch(P0);
@@ -221,15 +226,16 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
 template <int B>
 struct DnStage { static constexpr int G = 256 / B; };
 
-// Per-wave hit lists of one stage, one per down row rho of the wave: lane j of
-// v[rho] holds the row's j-th hit as e = dead << 15 | cb << 6 | k (column block
-// cb within the stage, weight slot k), in slot order.  A row with an odd number
-// of hits gets a dead copy of its last hit appended, so a two-slot ring consumes
-// every row with the same slot parity.  pcnt[rho] is the padded count, tot the
-// sum (all uniform).
+// Per-wave fetch list of one stage: position q (lane q % 64 of v[q / 64]) holds
+// desc = tile << 6 | cb -- the packed down tile (row * Kd + slot) and its column
+// block within the stage.  Positions run over the wave's rows in order, hits of
+// a row in slot order; a row with an odd hit count gets one padding position on
+// the packed zero tile, so a two-slot ring consumes every row with the same
+// slot parity.  pcnt[rho] is the padded count of row rho, tot their sum (even).
+// A stage holds at most RPW * (Kd + 1) <= 256 positions.
 template <int RPW>
-struct HitList {
-  int v[RPW];
+struct FetchList {
+  int v[4];
   int pcnt[RPW];
   int tot;
 };
@@ -238,47 +244,61 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
 }
 
-template <int RPW>
-__device__ __forceinline__ void dn_build(HitList<RPW>& L, int c0, int ncb, const int (&colreg)[RPW], int lane) {
-  L.tot = 0;
+// write `val` of the lanes in `m` (in lane order) to positions base, base+1, ...
+// of the list; positions outside [base, base + popcount(m)) keep their values
+__device__ __forceinline__ void list_scatter(int (&v)[4], uint64_t m, int base, int val, int lane) {
+  const int cnt = __builtin_popcountll(m);
+  if (cnt == 0) return;
+  const int rank = lanes_below(m);
+  const bool src = (m >> lane) & 1;
 #pragma unroll
-  for (int rho = 0; rho < RPW; ++rho) {
-    const int cb = colreg[rho] - c0;
-    const bool hit = cb >= 0 && cb < ncb;
-    const uint64_t m = __ballot(hit);
-    const int cnt = __builtin_popcountll(m);
-    // hits first (in slot order), then the other lanes: a permutation of the wave
-    const int dst = hit ? lanes_below(m) : cnt + lanes_below(~m);
-    int v = __builtin_amdgcn_ds_permute(dst << 2, (cb << 6) | lane);
-    if (cnt & 1) {
-      const int last = __builtin_amdgcn_readlane(v, cnt - 1);
-      v = lane == cnt ? (last | (1 << 15)) : v;
-    }
-    L.v[rho] = v;
-    L.pcnt[rho] = cnt + (cnt & 1);
-    L.tot += L.pcnt[rho];
+  for (int t = 0; t < 4; ++t) {
+    const int lo = base - 64 * t, hi = base + cnt - 64 * t;   // range of this target, in its lanes
+    if (hi <= 0 || lo >= 64) continue;
+    const int clo = lo > 0 ? lo : 0, chi = hi < 64 ? hi : 64;
+    // participants: source lanes whose position lands in this target
+    const int pos = base + rank - 64 * t;
+    const bool part = src && pos >= 0 && pos < 64;
+    const uint64_t pm = __ballot(part);
+    // a full permutation: participants -> their lanes, the others -> the lanes outside [clo, chi)
+    const int orank = lanes_below(~pm);
+    const int dst = part ? pos : (orank < clo ? orank : orank + (chi - clo));
+    const int got = __builtin_amdgcn_ds_permute(dst << 2, val);
+    if (lane >= clo && lane < chi) v[t] = got;
   }
 }
 
-// entry at position q of the list (q < L.tot); returns the row in rho
+__device__ __forceinline__ void list_set(int (&v)[4], int q, int val, int lane) {
+  const int t = q >> 6, l = q & 63;
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    if (t == u && lane == l) v[u] = val;
+}
+
+__device__ __forceinline__ int list_get(const int (&v)[4], int q) {
+  const int l = q & 63, t = q >> 6;
+  const int e0 = __builtin_amdgcn_readlane(v[0], l), e1 = __builtin_amdgcn_readlane(v[1], l);
+  const int e2 = __builtin_amdgcn_readlane(v[2], l), e3 = __builtin_amdgcn_readlane(v[3], l);
+  return t == 0 ? e0 : (t == 1 ? e1 : (t == 2 ? e2 : e3));
+}
+
 template <int RPW>
-__device__ __forceinline__ int hit_entry(const HitList<RPW>& L, int q, int& rho) {
-  int r = 0, base = 0;
+__device__ __forceinline__ void dn_build(FetchList<RPW>& L, int c0, int ncb, const int (&colreg)[RPW], int w,
+                                         int Kd, int ztile, int lane) {
+  int tot = 0;
 #pragma unroll
-  for (int rr = 0; rr + 1 < RPW; ++rr) {
-    const bool past = q >= base + L.pcnt[rr] && r == rr;
-    base += past ? L.pcnt[rr] : 0;
-    r += past ? 1 : 0;
-  }
-  rho = r;
-  const int j = q - base;
-  int e = __builtin_amdgcn_readlane(L.v[0], j);
+  for (int t = 0; t < 4; ++t) L.v[t] = 0;
 #pragma unroll
-  for (int rr = 1; rr < RPW; ++rr) {
-    const int er = __builtin_amdgcn_readlane(L.v[rr], j);
-    e = r == rr ? er : e;
+  for (int rho = 0; rho < RPW; ++rho) {
+    const int cb = colreg[rho] - c0;
+    const uint64_t m = __ballot(cb >= 0 && cb < ncb);
+    const int cnt = __builtin_popcountll(m);
+    list_scatter(L.v, m, tot, (((w * RPW + rho) * Kd + lane) << 6) | (cb & 63), lane);
+    if (cnt & 1) list_set(L.v, tot + cnt, ztile << 6, lane);
+    L.pcnt[rho] = cnt + (cnt & 1);
+    tot += L.pcnt[rho];
   }
-  return e;
+  L.tot = tot;
 }
 
 template <int B, int MT, int RPW>
@@ -304,12 +324,13 @@ __global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
   const int C = a.C_d;
   const int nstages = (C + G - 1) / G;
   const u32x4* pd = static_cast<const u32x4*>(a.pd);
+  const int ztile = a.R_m * a.Kd;   // packed zero tile
 
   int colreg[RPW];
 #pragma unroll
   for (int rho = 0; rho < RPW; ++rho) {
     const int rm = w * RPW + rho;
-    colreg[rho] = (rm < a.R_m && lane < a.Kd) ? a.cd[(int64_t)rm * a.Kd + lane] : -2;
+    colreg[rho] = (rm < a.R_m && lane < a.Kd) ? a.cd[(int64_t)rm * a.Kd + lane] : -1;
   }
 
   f32x4 acc[RPW][MT][CW];
@@ -341,51 +362,45 @@ __global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
       const int e = tid + 512 * u;
       if (e < CHUNKS) {
         const int row = e / (SROWB / 16), c = e - row * (SROWB / 16);
-        *reinterpret_cast<u32x4*>(&stages[buf][0] + swz_addr(row, c, SROWB)) = sreg[u];
+        *reinterpret_cast<u32x4*>(&stages[buf][0] + panel_addr<MT>(row, c, SROWB)) = sreg[u];
       }
     }
   };
 
-  // ring slots: weight fragments and column block (-1: dead entry)
+  // ring slots: weight fragments and column block
   struct Slot {
     u32x4 f[1][CW];
     int cb;
   };
-  HitList<RPW> cur, nxt;
+  FetchList<RPW> cur, nxt;
   // position q of the stream made of the current stage's list followed by the
-  // next stage's list; beyond both, a dead re-read of this wave's first tile
+  // next stage's; beyond both, the zero tile
   auto fetch = [&](Slot& S, int q) {
-    int e = 1 << 15, rho = 0;
-    if (q < cur.tot) e = hit_entry<RPW>(cur, q, rho);
-    else if (q - cur.tot < nxt.tot) e = hit_entry<RPW>(nxt, q - cur.tot, rho);
-    const int rm = (w * RPW + rho) < a.R_m ? w * RPW + rho : a.R_m - 1;
-    const int k = e & 63;
-    load_pfrag<B>(pd + ((int64_t)rm * a.Kd + k) * PackedTile<B>::U32X4, lane, S.f);
-    S.cb = (e >> 15) ? -1 : ((e >> 6) & 63);
+    int d = ztile << 6;
+    if (q < cur.tot) d = list_get(cur.v, q);
+    else if (q - cur.tot < nxt.tot) d = list_get(nxt.v, q - cur.tot);
+    load_pfrag<B>(pd + (int64_t)(d >> 6) * PackedTile<B>::U32X4, lane, S.f);
+    S.cb = d & 63;
   };
+  const uint32_t lbase = (uint32_t)(i * MT * SROWB);
   auto compute = [&](const Slot& S, const unsigned char* sb, f32x4 (&ac)[MT][CW]) {
     const int cb = uniform(S.cb);
-    u32x4 f[CW];
-#pragma unroll
-    for (int m = 0; m < CW; ++m)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) f[m][v] = cb >= 0 ? S.f[0][m][v] : 0u;
-    const int ch = (cb >= 0 ? cb : 0) * (B / 8) + g;
+    const uint32_t a0 = lbase + (((cb * (B / 8) + g) ^ i) << 4);
     u32x4 av[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
-      av[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(sb, swz_addr(16 * mt + i, ch, SROWB));
+      av[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(sb, a0 + mt * SROWB);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int m = 0; m < CW; ++m) ac[mt][m] = mfma_bf16(av[mt], f[m], ac[mt][m]);
+      for (int m = 0; m < CW; ++m) ac[mt][m] = mfma_bf16(av[mt], S.f[0][m], ac[mt][m]);
   };
 
   const bool any_rows = (w * RPW < a.R_m) && a.Kd > 0;
   Slot S0, S1;
   nxt.tot = 0;
-  dn_build<RPW>(cur, 0, (C < G ? C : G), colreg, lane);
-  if (nstages > 1) dn_build<RPW>(nxt, G, (C - G) < G ? (C - G) : G, colreg, lane);
+  dn_build<RPW>(cur, 0, (C < G ? C : G), colreg, w, a.Kd, ztile, lane);
+  if (nstages > 1) dn_build<RPW>(nxt, G, (C - G) < G ? (C - G) : G, colreg, w, a.Kd, ztile, lane);
   stage_fetch(0);
   stage_store(0);
   bool ring_ok = false;   // S0/S1 hold positions 0 and 1 of the current stage
@@ -423,7 +438,7 @@ __global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
     nxt.tot = 0;
     if (s + 2 < nstages) {
       const int c2 = (s + 2) * G;
-      dn_build<RPW>(nxt, c2, (C - c2) < G ? (C - c2) : G, colreg, lane);
+      dn_build<RPW>(nxt, c2, (C - c2) < G ? (C - c2) : G, colreg, w, a.Kd, ztile, lane);
     }
     __syncthreads();
   }
@@ -478,8 +493,8 @@ static int dn_rpw(int R_m) {
   return -1;
 }
 
-static size_t gu_lds(int d_model, int R_ff, int K, int mt) {
-  return (size_t)16 * mt * d_model * 2 + (size_t)R_ff * K * 8;
+static size_t gu_lds(int R_ff, int K, int mt) {
+  return (size_t)16 * mt * (8192 / mt) + (size_t)R_ff * K * 8;   // panel (128 KB) + column table
 }
 
 bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd) {
@@ -488,7 +503,7 @@ bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int 
   if (Kd > 63) return false;                          // one lane per slot; <= 4 * 64 hit-list entries
   if (d_model % 128) return false;                    // swizzled panel rows
   const int mt = gu_mt(d_model);
-  if (mt == 0 || gu_lds(d_model, R_ff, Kg, mt) > 163840) return false;
+  if (mt == 0 || gu_lds(R_ff, Kg, mt) > 163840) return false;
   if (R_m * B != d_model || dn_rpw(R_m) < 0) return false;
   if ((R_ff * B) % 8) return false;
   return true;
@@ -504,7 +519,7 @@ static int launch_gu_t(const GUArgs& a, hipStream_t st) {
     configured = true;
   }
   const int TM = 16 * MT;
-  const size_t lds = gu_lds(a.d_model, a.R_ff, a.Kg, MT);
+  const size_t lds = gu_lds(a.R_ff, a.Kg, MT);
   hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + TM - 1) / TM)), dim3(512), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
