@@ -210,13 +210,14 @@ __global__ __launch_bounds__(256) void pack_bf16_kernel(const uint16_t* __restri
     packed[idx] = 0u;
     return;
   }
+  constexpr int LANES = PackedTile<B>::LANES;
   int r = (int)(idx - tile * PER_TILE);
   const int u = r & 3;
   r >>= 2;
+  const int l = r % LANES;
+  r /= LANES;
   const int m = r % CW;
-  r /= CW;
-  const int ks = r % NKS;
-  const int l = r / NKS;
+  const int ks = r / CW;
   const int j = l & 15, g = l >> 4;
   const int k = 32 * ks + 8 * g + 2 * u, c = CW * j + m;
   const uint16_t* w = values + tile * B * B;

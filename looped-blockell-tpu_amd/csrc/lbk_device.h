@@ -144,13 +144,14 @@ __device__ __forceinline__ void wraw_to_frag<64>(const WRaw<64>& r, u32x4 (&f)[2
 }
 
 // ---------------------------------------------------------------------------
-// Fragment-major ("packed") bf16 tiles.  Tile t holds, for every lane l of a
-// wave, that lane's B fragments f[ks][m] (as wraw_to_frag would build them) as
-// NKS*CW consecutive 16-byte chunks at packed[(t*64 + l)*NKS*CW + ks*CW + m].
-// A lane then fetches all its operands of a tile with NKS*CW dwordx4 loads and
-// no register transposition.  For B = 16 only lanes 0..31 are stored (512
-// bytes per tile); lanes 32..63 read lanes 0..31 (their A operand is zero).
-// The chunk's dword u of fragment (ks, m) of lane (j = l%16, g = l/16) is
+// Fragment-major ("packed") bf16 tiles.  Tile t holds the B fragments f[ks][m]
+// (as wraw_to_frag would build them) of every lane l of a wave as 16-byte
+// chunks, chunk-major: packed[(t*NKS*CW + ks*CW + m)*LANES + l].  A lane then
+// fetches all its operands of a tile with NKS*CW dwordx4 loads, each of which
+// reads one contiguous LANES*16-byte run across the wave, and no register
+// transposition is needed.  For B = 16 only lanes 0..31 are stored (512 bytes
+// per tile); lanes 32..63 read lanes 0..31 (their A operand is zero).
+// Dword u of chunk (ks, m) of lane (j = l%16, g = l/16) is
 //   W[k][c] | W[k+1][c] << 16,  k = 32*ks + 8*g + 2*u,  c = CW*j + m.
 // ---------------------------------------------------------------------------
 template <int B>
@@ -163,12 +164,12 @@ struct PackedTile {
 template <int B>
 __device__ __forceinline__ void load_pfrag(const u32x4* __restrict__ tile, int lane,
                                            u32x4 (&f)[TileShape<B>::NKS][TileShape<B>::CW]) {
-  constexpr int NKS = TileShape<B>::NKS, CW = TileShape<B>::CW;
-  const u32x4* p = tile + (B == 16 ? (lane & 31) : lane) * (NKS * CW);
+  constexpr int NKS = TileShape<B>::NKS, CW = TileShape<B>::CW, LANES = PackedTile<B>::LANES;
+  const u32x4* p = tile + (B == 16 ? (lane & 31) : lane);
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-    for (int m = 0; m < CW; ++m) f[ks][m] = p[ks * CW + m];
+    for (int m = 0; m < CW; ++m) f[ks][m] = p[(ks * CW + m) * LANES];
 }
 
 // ---------------------------------------------------------------------------

@@ -49,6 +49,9 @@ struct GUSlot {
   int cg, cu;
 };
 
+// gate/up ring depth (positions in flight + 1)
+constexpr int GU_RING = 4;
+
 // gate/up panel row stride: 2048 bytes (MT = 4, d_model <= 1024) or 4096 (MT = 2)
 template <int MT>
 struct GUPanel { static constexpr int ROWB = 8192 / MT; };
@@ -80,72 +83,56 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
     cu = (cu >= 0 && cu < cin) ? cu : 0;
     ctab[e] = make_int2(cg, cu);
   }
-  // ---- input panel
-  if constexpr (!NORM) {
-    const int cpr = d_model / 8;
-    for (int e = tid; e < TM * cpr; e += 512) {
-      const int row = e / cpr, c = e - row * cpr;
-      const int64_t t = t0 + row;
-      u32x4 v = {0, 0, 0, 0};
-      if (t < a.N) v = *reinterpret_cast<const u32x4*>(a.x + t * d_model + 8 * c);
-      *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, c, ROWB)) = v;
-    }
-  } else {
-    // fp32 state rows -> RMSNorm -> bf16 panel; one wave per row, 8 contiguous values per lane per step
-    for (int row = w; row < TM; row += 8) {
-      const int64_t t = t0 + row;
-      const float* xr = a.xf + (t < a.N ? t : 0) * d_model;
-      float ss = 0.f;
-      for (int c = 8 * lane; c < d_model; c += 512) {
-        const f32x4 v0 = *reinterpret_cast<const f32x4*>(xr + c);
-        const f32x4 v1 = *reinterpret_cast<const f32x4*>(xr + c + 4);
-        ss += v0[0] * v0[0] + v0[1] * v0[1] + v0[2] * v0[2] + v0[3] * v0[3];
-        ss += v1[0] * v1[0] + v1[1] * v1[1] + v1[2] * v1[2] + v1[3] * v1[3];
-      }
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-      const float rs = (t < a.N) ? 1.0f / sqrtf(ss / (float)d_model + a.eps) : 0.f;
-      for (int c = 8 * lane; c < d_model; c += 512) {
-        const f32x4 v0 = *reinterpret_cast<const f32x4*>(xr + c);
-        const f32x4 v1 = *reinterpret_cast<const f32x4*>(xr + c + 4);
-        const f32x4 s0 = *reinterpret_cast<const f32x4*>(a.norm_scale + c);
-        const f32x4 s1 = *reinterpret_cast<const f32x4*>(a.norm_scale + c + 4);
-        const u32x4 o = {pack2_bf16(v0[0] * rs * s0[0], v0[1] * rs * s0[1]),
-                         pack2_bf16(v0[2] * rs * s0[2], v0[3] * rs * s0[3]),
-                         pack2_bf16(v1[0] * rs * s1[0], v1[1] * rs * s1[1]),
-                         pack2_bf16(v1[2] * rs * s1[2], v1[3] * rs * s1[3])};
-        *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, c / 8, ROWB)) = o;
-      }
-    }
-  }
-  __syncthreads();
 
-  // ---- stream this wave's rows r = w + 8n through a two-slot ring of (gate,
-  // up) tile pairs.  Each row takes an even number of positions KP (an odd K
-  // gets one padding position that reads the zero tile), so slot parity repeats
-  // per row; every position issues the same loads, so the compiler's
-  // memory-counter waits stay exact and two positions stay in flight across
-  // row boundaries.
-  const int nrows = (a.R_ff - w + 7) / 8;
-  if (nrows <= 0) return;
-  const int KP = K + (K & 1);
+  // ---- stream this wave's rows r = w + 8n through a GU_RING-slot ring of
+  // (gate, up) tile pairs.  Each row takes KP positions, K rounded up to a
+  // multiple of GU_RING (padding positions read the zero tile), so slot s of the
+  // ring always holds position s of a group; every position issues the same
+  // loads, so the compiler's memory-counter waits stay exact and GU_RING - 1
+  // positions stay in flight across row boundaries.
+  const int nrows = (a.R_ff - w + 7) / 8;   // may be <= 0: such a wave only helps fill the panel
+  const int KP = (K + GU_RING - 1) / GU_RING * GU_RING;
   const u32x4* pg = static_cast<const u32x4*>(a.pg);
   const u32x4* pu = static_cast<const u32x4*>(a.pu);
   const uint32_t lbase = (uint32_t)(i * MT * ROWB);   // this lane's first panel row
 
   int rn = 0, rk = 0;   // next position to fetch
-  auto fetch = [&](GUSlot<B>& S) {
+  // weight loads of the next position (the column table is not needed yet)
+  auto fetch_w = [&](GUSlot<B>& S) {
     const bool live = rn < nrows && rk < K;
     const int64_t e = live ? (int64_t)(w + 8 * rn) * K + rk : ztile;
     load_pfrag<B>(pg + e * PackedTile<B>::U32X4, lane, S.g);
     load_pfrag<B>(pu + e * PackedTile<B>::U32X4, lane, S.u);
-    const int2 c = ctab[live ? e : 0];
+    S.cg = live ? (int)e : -1;   // position index until fetch_c replaces it by columns
+  };
+  auto fetch_c = [&](GUSlot<B>& S) {
+    const int2 c = ctab[S.cg >= 0 ? S.cg : 0];
     S.cg = c.x;
     S.cu = c.y;
     if (++rk == KP) {
       rk = 0;
       ++rn;
     }
+  };
+  auto fetch = [&](GUSlot<B>& S) {
+    fetch_w(S);
+    fetch_c(S);
+  };
+  GUSlot<B> P[GU_RING];
+  auto prefetch_ring = [&]() {
+    int sn = 0, sk = 0;
+#pragma unroll
+    for (int sl = 0; sl < GU_RING; ++sl) {
+      rn = sn;
+      rk = sk;
+      fetch_w(P[sl]);
+      if (++sk == KP) {
+        sk = 0;
+        ++sn;
+      }
+    }
+    rn = 0;
+    rk = 0;
   };
 
   f32x4 ag[MT][CW], au[MT][CW];
@@ -169,11 +156,83 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
       for (int m = 0; m < CW; ++m) au[mt][m] = mfma_bf16(avu[mt], S.u[0][m], au[mt][m]);
   };
 
-  GUSlot<B> P0, P1;
-  __builtin_amdgcn_sched_barrier(0);
-  fetch(P0);
-  __builtin_amdgcn_sched_barrier(0);
-  fetch(P1);
+  // ---- input panel: all of this thread's loads are issued before any store,
+  // and the first ring positions' weight loads go out before the barrier
+  if constexpr (!NORM) {
+    constexpr int CPR = ROWB / 16;                 // chunk capacity of a panel row
+    constexpr int PIT = TM * CPR / 512;            // chunks per thread
+    const int cpr = d_model / 8;
+    u32x4 pv[PIT];
+#pragma unroll
+    for (int it = 0; it < PIT; ++it) {
+      const int e = tid + 512 * it;
+      const int row = e / CPR, cc = e % CPR;
+      const int64_t t = t0 + row;
+      pv[it] = u32x4{0, 0, 0, 0};
+      if (cc < cpr && t < a.N) pv[it] = *reinterpret_cast<const u32x4*>(a.x + t * d_model + 8 * cc);
+    }
+    if (nrows > 0) prefetch_ring();
+#pragma unroll
+    for (int it = 0; it < PIT; ++it) {
+      const int e = tid + 512 * it;
+      const int row = e / CPR, cc = e % CPR;
+      if (cc < cpr) *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, cc, ROWB)) = pv[it];
+    }
+  } else {
+    // fp32 state rows -> RMSNorm -> bf16 panel; wave w owns rows w, w+8, ...;
+    // lane holds 8 contiguous values per 512-column step of each row
+    constexpr int RW = TM / 8;                     // rows per wave
+    constexpr int SPR = ROWB / 1024;               // 512-column steps of the widest row
+    f32x4 xv[RW][SPR][2];
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) {
+      const int64_t t = t0 + w + 8 * rr;
+#pragma unroll
+      for (int j = 0; j < SPR; ++j) {
+        const int col = 8 * lane + 512 * j;
+        xv[rr][j][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+        xv[rr][j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (col < d_model && t < a.N) {
+          xv[rr][j][0] = *reinterpret_cast<const f32x4*>(a.xf + t * d_model + col);
+          xv[rr][j][1] = *reinterpret_cast<const f32x4*>(a.xf + t * d_model + col + 4);
+        }
+      }
+    }
+    if (nrows > 0) prefetch_ring();
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) {
+      const int row = w + 8 * rr;
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < SPR; ++j)
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ss += xv[rr][j][h2][q] * xv[rr][j][h2][q];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+      const float rs = 1.0f / sqrtf(ss / (float)d_model + a.eps);
+#pragma unroll
+      for (int j = 0; j < SPR; ++j) {
+        const int col = 8 * lane + 512 * j;
+        if (col < d_model) {
+          const f32x4 s0 = *reinterpret_cast<const f32x4*>(a.norm_scale + col);
+          const f32x4 s1 = *reinterpret_cast<const f32x4*>(a.norm_scale + col + 4);
+          const f32x4 v0 = xv[rr][j][0], v1 = xv[rr][j][1];
+          const u32x4 o = {pack2_bf16(v0[0] * rs * s0[0], v0[1] * rs * s0[1]),
+                           pack2_bf16(v0[2] * rs * s0[2], v0[3] * rs * s0[3]),
+                           pack2_bf16(v1[0] * rs * s1[0], v1[1] * rs * s1[1]),
+                           pack2_bf16(v1[2] * rs * s1[2], v1[3] * rs * s1[3])};
+          *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, col / 8, ROWB)) = o;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (nrows <= 0) return;
+#pragma unroll
+  for (int sl = 0; sl < GU_RING; ++sl) fetch_c(P[sl]);
+
   __builtin_amdgcn_sched_barrier(0);
   for (int n = 0; n < nrows; ++n) {
 #pragma unroll
@@ -183,15 +242,15 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
         ag[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
         au[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-    // the scheduling barriers keep each slot's use after the other slot's
+    // the scheduling barriers keep each slot's use after the previous slot's
     // refill, so the wait before it covers only that slot's loads
-    for (int k = 0; k < KP; k += 2) {
-      compute(P0);
-      fetch(P0);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(P1);
-      fetch(P1);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int k = 0; k < KP; k += GU_RING) {
+#pragma unroll
+      for (int sl = 0; sl < GU_RING; ++sl) {
+        compute(P[sl]);
+        fetch(P[sl]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     // epilogue of row r: h = silu(g) * u (and the pre-activations)
     const int r = w + 8 * n;
