@@ -29,6 +29,19 @@ for _p in (ROOT, PKG_DIR):
         sys.path.insert(0, _p)
 
 METRIC = "effective TFLOP/s (nonzero blocks) + tokens/s, Block-ELL SwiGLU FFN"
+TRAFFIC_PROFILE_BF16 = os.path.join(ROOT, "profiles", "swiglu_bf16_gu_dn_N16384_d1024_ff4096_B32.txt")
+
+
+def profiled_traffic(path):
+    """HBM bytes per step recorded by the committed rocprofv3 counter summary, or None."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_step"):
+                    return float(line.split("=", 1)[1])
+    except OSError:
+        pass
+    return None
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_INT8_TOPS = 5000.0       # MI355X dense int8 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
@@ -146,8 +159,11 @@ def bench_bf16(steps, warmup, device):
         ms_per_step=ms, value=flops / (ms * 1e-3) / 1e12, tokens_per_s=w["N"] / (ms * 1e-3),
         kernel_ms_avg=kern_ms, kernel_ms_median=median(per),
         roofline=dict(bound="mfma", achieved=achieved, peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
-                      frac=achieved / PEAK_BF16_TFLOPS, traffic=None,
-                      kernel="gu_kernel<32,4,false> + dn_kernel<32,4,4> (gate/up + SiLU*mul, then down; one launch pair per step)",
+                      frac=achieved / PEAK_BF16_TFLOPS, traffic=profiled_traffic(TRAFFIC_PROFILE_BF16),
+                      traffic_source=os.path.relpath(TRAFFIC_PROFILE_BF16, ROOT) + " (FETCH_SIZE/WRITE_SIZE, "
+                                     "calibrated on a 256 MiB copy)",
+                      kernel="SwiGLU forward launch sequence: pack_bf16_kernel<32> x3 + gu_kernel<32,4,false,false> "
+                             "+ dn_kernel<32,4,4>, timed together with HIP events around each step",
                       algorithmic_flops_per_launch=flops,
                       algorithmic_bytes_per_launch=algorithmic_bytes(w)),
     )
@@ -264,6 +280,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-main", action="store_true", help="headline workload only (for profiling)")
     ap.add_argument("--only", default="", help="comma list of extra workloads to run: ternary,looped,decode")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run one 256 MiB device-to-device copy (a reference point for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the Block-ELL FFN path is single-GPU; "
@@ -274,6 +292,14 @@ def main():
     kernels.ops()
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+
+    if args.copy_calibration:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=device).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     main_res = bench_bf16(args.steps, args.warmup, device)
     extra = {}
