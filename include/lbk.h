@@ -84,8 +84,9 @@ int lbk_block_ell_matmul_bf16(const uint16_t* x, int64_t N, int32_t in_features,
                               void* stream);
 
 /*
- * Workspace bytes needed by lbk_swiglu_fwd_bf16 for this geometry (0 when the
- * fused single-kernel path applies and no intermediates are requested).
+ * Workspace bytes needed by lbk_swiglu_fwd_bf16 for this geometry: packed
+ * copies of the gate/up/down tiles (two-kernel path) plus the hidden state h
+ * [N, d_ff] bf16 unless want_intermediates (then the caller passes h_out).
  */
 size_t lbk_swiglu_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate,
                                   const lbk_bell* up, const lbk_bell* down, int want_intermediates);
@@ -125,8 +126,9 @@ int lbk_diagonal_injection_bf16(const uint16_t* h, const uint16_t* e, const floa
 /*
  * Looped pre-norm FFN block with shared weights, applied L times:
  *   h <- h + SwiGLU(RMSNorm(h; norm_scale, eps))
- * h_in, h_out: [N, d_model] bf16 (may alias).  The carried state stays in fp32
- * inside the persistent kernel; h_out is rounded to bf16 once at the end.
+ * h_in, h_out: [N, d_model] bf16 (may alias).  On the two-kernel path the
+ * carried state stays in fp32 in the workspace and h_out is rounded to bf16
+ * once at the end; the row-block path rounds the state to bf16 per iteration.
  * Replaces the MLP loop of persistent_mlp_step (reference csrc/loop/persistent_core.cu:315-335,
  * schema csrc/loop/loop_ops.cpp:52-66) and the L-fold application of the
  * core block (reference looped_blockell/looping/looped_model.py:293-350).
@@ -166,8 +168,12 @@ int lbk_ternary_quantize_weights_bf16(const uint16_t* values, int32_t R, int32_t
                                       uint32_t* packed, float* scales, void* stream);
 
 /*
- * Ternary Block-ELL product: y[n, r*B+j] = sx[n] * sum_k s[r,k] * P[n,r,k,j],
+ * Ternary Block-ELL product: y[n, r*B+j] ~= sx[n] * sum_k s[r,k] * P[n,r,k,j],
  * P = int32 block partial of xq against the ternary tile.  y bf16 [N, R*B].
+ * The block scales are applied in per-row fixed point: m[r,k] = rint(s[r,k] * 2^e_r)
+ * with e_r the largest exponent keeping |sum_k m * P| inside int32 for any int8
+ * input, then y = f32(f32(sum_k m * P) * 2^-e_r) * sx (within 2^-12 of exact fp32
+ * scaling).
  * If partials != NULL the kernel also stores every P as int32 [N, R, K, B]
  * (dead slots store 0) — the exact integer accumulators before scaling.
  */

@@ -4,20 +4,22 @@
 // rows sit in LDS as an XOR-swizzled panel (optionally RMSNorm-ed on the way in
 // from an fp32 state), next to a table of the gate/up column indices.  Eight
 // waves (two per SIMD) each stream their own d_ff block rows (r = w, w+8, ...):
-// gate and up tiles are consumed in (gate k, up k) pairs from a 2-deep register
-// ring that runs across row boundaries.  The loop issues the same loads on every
-// position (dead slots are zeroed in the fragment, not branched around), so the
-// compiler's memory-counter waits stay exact and two positions stay in flight.
-// h = silu(g) * u is stored as bf16 (and the pre-activations when INTER).
+// gate and up tiles are consumed in (gate k, up k) pairs from a GU_RING-deep
+// register ring that runs across row boundaries.  Weights come pre-packed in
+// fragment-major order (two dwordx4 loads per lane per B = 32 tile); every
+// position issues the same loads (padding and dead slots read the packed zero
+// tile), so the compiler's memory-counter waits stay exact.  h = silu(g) * u is
+// stored as bf16 (and the pre-activations when INTER).
 //
 // dn_kernel<B, MT, RPW>: a workgroup owns 16*MT tokens and all d_model outputs;
 // wave w keeps RPW down block rows of fp32 accumulators in registers for the
-// whole kernel.  h is staged through LDS four column blocks at a time (double
+// whole kernel.  h is staged through LDS 256 columns at a time (double
 // buffered, next stage's global loads in flight while the current one is
-// consumed); each wave finds its tiles of a stage with a ballot over its
-// column-index rows held in registers, and streams them row by row through a
-// three-slot register shift (two tiles in flight while one is consumed).  The epilogue
-// adds the residual, or carries an fp32 state for the looped block.
+// consumed).  Per stage each wave builds a flat list of its tiles (ballot over
+// its column-index rows, ds_permute into place), rows in order, each row's run
+// padded to an even length with a zero-tile entry, and streams it through a
+// two-slot ring that also prefetches the next stage's first tiles.  The
+// epilogue adds the residual, or carries an fp32 state for the looped block.
 #include "lbk_device.h"
 #include "lbk_internal.h"
 
