@@ -219,3 +219,73 @@ def test_looped_L0_and_L1(gpu):
     f64 = lambda w: (w[0].astype(np.float64), w[1])
     ref = h + O.swiglu_fwd(O.rmsnorm(h.astype(np.float64), np.ones(256)), f64(g), f64(u), f64(d))[0]
     assert T.rel_err(o1, ref)[0] <= TOL
+
+
+DECODE_CASES = [
+    # (d_model, d_ff, B, density, N, sentinel_frac)   N <= 16: the single-launch decode kernel
+    (256, 1024, 16, 0.25, 16, 0.0),
+    (512, 1024, 32, 0.25, 5, 0.1),
+    (1024, 2048, 64, 0.25, 1, 0.0),
+    (1024, 3072, 64, 0.125, 16, 0.1),
+    (128, 512, 64, 1.0, 9, 0.0),
+]
+
+
+@pytest.mark.parametrize("case", DECODE_CASES)
+@pytest.mark.parametrize("resid", [False, True])
+def test_decode_parity(gpu, case, resid):
+    d_model, d_ff, B, dens, N, sf = case
+    _say(f"decode {case} resid={resid}")
+    rng = np.random.default_rng(hash(case) % 2 ** 31 + 3)
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, dens, sentinel_frac=sf)
+    x = T.act(rng, N, d_model)
+    out, *_ = T.abi_swiglu(T.to_gpu_bf16(x), T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d), add_residual=resid)
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref, *_ = O.swiglu_fwd(x.astype(np.float64), f64(g), f64(u), f64(d), add_residual=resid)
+    rel, ab = T.rel_err(T.to_np(out), ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
+def test_decode_duplicates_and_workspace_reuse(gpu):
+    """Duplicate down columns, one workspace reused by consecutive calls (the per-call
+    tags of the decode kernel must keep the calls apart), and bitwise determinism."""
+    import torch
+    A = T.abi()
+    lib = A.load()
+    rng = np.random.default_rng(31)
+    d_model, d_ff, B, N = 512, 2048, 64, 16
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25)
+    d[1][0, :] = d[1][0, 0]
+    ws_t = [T.gpu_weight(w) for w in (g, u, d)]
+    gb, ub, db = (T.bell_struct(*w) for w in ws_t)
+    wsb = lib.lbk_swiglu_workspace_bytes(N, d_model, T.C.byref(gb), T.C.byref(ub), T.C.byref(db), 0)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    outs = []
+    for trial in range(3):
+        x = T.act(rng, N, d_model) if trial < 2 else xs
+        if trial == 0:
+            xs = x
+        xt = T.to_gpu_bf16(x)
+        out = torch.empty(N, d_model, dtype=torch.bfloat16, device="cuda")
+        A.check(lib.lbk_swiglu_fwd_bf16(T.ptr(xt), N, d_model, T.C.byref(gb), T.C.byref(ub), T.C.byref(db), 1,
+                                        T.ptr(out), None, None, None, T.ptr(ws), wsb, T.stream()), "decode")
+        ref, *_ = O.swiglu_fwd(x.astype(np.float64), f64(g), f64(u), f64(d), add_residual=True)
+        rel, ab = T.rel_err(T.to_np(out), ref)
+        assert rel <= TOL, f"trial {trial}: rel {rel} abs {ab}"
+        outs.append(T.to_np(out))
+    assert np.array_equal(outs[0], outs[2])
+
+
+def test_decode_config5_full(gpu):
+    """Config 5 geometry: 16 tokens, d_model 4096, d_ff 14336, B 64, density 0.10."""
+    rng = np.random.default_rng(1005)
+    d_model, d_ff, B, N = 4096, 14336, 64, 16
+    _say("decode config-5 full size")
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.10)
+    x = T.act(rng, N, d_model)
+    out, *_ = T.abi_swiglu(T.to_gpu_bf16(x), T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d))
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref, *_ = O.swiglu_fwd(x.astype(np.float64), f64(g), f64(u), f64(d))
+    rel, ab = T.rel_err(T.to_np(out), ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
