@@ -170,10 +170,10 @@ int lbk_ternary_quantize_weights_bf16(const uint16_t* values, int32_t R, int32_t
 /*
  * Ternary Block-ELL product: y[n, r*B+j] ~= sx[n] * sum_k s[r,k] * P[n,r,k,j],
  * P = int32 block partial of xq against the ternary tile.  y bf16 [N, R*B].
- * The block scales are applied in per-row fixed point: m[r,k] = rint(s[r,k] * 2^e_r)
- * with e_r the largest exponent keeping |sum_k m * P| inside int32 for any int8
- * input, then y = f32(f32(sum_k m * P) * 2^-e_r) * sx (within 2^-12 of exact fp32
- * scaling).
+ * The block scales are applied in per-row 8-bit fixed point: m[r,k] =
+ * rint(s[r,k] * 2^e_r) in [0, 127], e_r the largest exponent with
+ * max_k |s[r,k]| * 2^e_r <= 127, then y = f32(f32(sum_k m * P) * 2^-e_r) * sx
+ * (each scale within 2^-8 of the row's largest, relative).
  * If partials != NULL the kernel also stores every P as int32 [N, R, K, B]
  * (dead slots store 0) — the exact integer accumulators before scaling.
  */
@@ -186,10 +186,13 @@ int lbk_ternary_matmul(const int8_t* xq, const float* sx, int64_t N, int32_t in_
  *   (hq, sh) = per-token int8 re-quantisation of h over d_ff;
  *   out = ternary down product of (hq, sh)  (+ x_resid if not NULL), bf16.
  * Optional outputs: h_out [N, d_ff] bf16, hq_out [N, d_ff] int8, sh_out [N] fp32.
- * The workspace (see lbk_ternary_swiglu_workspace_bytes) holds h, hq and sh
- * when the optional outputs are not given.
+ * Block scales use the fixed point of lbk_ternary_matmul.  The workspace
+ * (lbk_ternary_swiglu_workspace_bytes, whose operands are those of the call)
+ * holds the prepared weights for the B = 64 kernels, and h / hq / sh where the
+ * optional outputs are not given; it may be NULL only when the size is 0.
  */
-size_t lbk_ternary_swiglu_workspace_bytes(int64_t N, const lbk_bell_ternary* gate);
+size_t lbk_ternary_swiglu_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell_ternary* gate,
+                                          const lbk_bell_ternary* up, const lbk_bell_ternary* down);
 int lbk_swiglu_fwd_ternary(const int8_t* xq, const float* sx, int64_t N, int32_t d_model,
                            const lbk_bell_ternary* gate, const lbk_bell_ternary* up,
                            const lbk_bell_ternary* down, const uint16_t* x_resid,

@@ -72,6 +72,27 @@ int swiglu_general(const uint16_t* x, int64_t N, int32_t d_model, const lbk_bell
   return LBK_OK;
 }
 
+struct TernSplitLayout {
+  size_t pg, pu, pd, hmax, h, total;
+};
+
+TernSplitLayout tern_split_layout(int64_t N, const lbk_bell_ternary* gate, const lbk_bell_ternary* up,
+                                  const lbk_bell_ternary* down) {
+  TernSplitLayout L{};
+  L.pg = tprep_bytes((int64_t)gate->R * gate->K, gate->R);
+  L.pu = tprep_bytes((int64_t)up->R * up->K, up->R);
+  L.pd = tprep_bytes((int64_t)down->R * down->K, down->R);
+  L.hmax = align256((size_t)tgu_slices(N) * (size_t)N * 4);
+  L.h = align256((size_t)N * gate->R * gate->B * 2);
+  L.total = L.pg + L.pu + L.pd + L.hmax + L.h;
+  return L;
+}
+
+bool tern_split(int64_t N, int32_t d_model, const lbk_bell_ternary* gate, const lbk_bell_ternary* up,
+                const lbk_bell_ternary* down) {
+  return N > 0 && tsplit_supported(gate->B, d_model, gate->R, down->R, gate->K, up->K, down->K);
+}
+
 }  // namespace
 
 extern "C" {
@@ -395,9 +416,13 @@ int lbk_ternary_matmul(const int8_t* xq, const float* sx, int64_t N, int32_t in_
   return launch_ternary(w->B, 0, a, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
 }
 
-size_t lbk_ternary_swiglu_workspace_bytes(int64_t N, const lbk_bell_ternary* gate) {
-  if (!gate || N <= 0) return 0;
-  const size_t d_ff = (size_t)gate->R * gate->B;
+size_t lbk_ternary_swiglu_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell_ternary* gate,
+                                          const lbk_bell_ternary* up, const lbk_bell_ternary* down) {
+  if (!gate || !up || !down || N <= 0) return 0;
+  if (check_tern(gate) || check_tern(up) || check_tern(down)) return 0;
+  int64_t d_ff = 0;
+  if (check_ffn(gate, up, down, d_model, &d_ff)) return 0;
+  if (tern_split(N, d_model, gate, up, down)) return tern_split_layout(N, gate, up, down).total;
   return align256((size_t)N * d_ff * 2) + align256((size_t)N * d_ff) + align256((size_t)N * 4);
 }
 
@@ -413,18 +438,48 @@ int lbk_swiglu_fwd_ternary(const int8_t* xq, const float* sx, int64_t N, int32_t
   if (N == 0) return LBK_OK;
   if (!xq || !sx || !out) return LBK_ERR_NULL;
   if (!a16(xq) || !a16(out)) return LBK_ERR_ALIGN;
-  const size_t hb = align256((size_t)N * d_ff * 2), qb = align256((size_t)N * d_ff);
   char* ws = static_cast<char*>(workspace);
+  hipStream_t s = S(stream);
+
+  if (tern_split(N, d_model, gate, up, down)) {
+    const TernSplitLayout L = tern_split_layout(N, gate, up, down);
+    if (!ws || workspace_bytes < L.total) return LBK_ERR_WORKSPACE;
+    if (!a16(ws)) return LBK_ERR_ALIGN;
+    uint16_t* h = h_out ? h_out : reinterpret_cast<uint16_t*>(ws + L.pg + L.pu + L.pd + L.hmax);
+    if (!a16(h) || (hq_out && !a16(hq_out))) return LBK_ERR_ALIGN;
+    const int C_in = d_model / gate->B;
+    TGUArgs g{};
+    TDNArgs d{};
+    if (launch_tprep(gate->packed, gate->scales, gate->col_idx, gate->R, gate->K, C_in, ws, &g.twg, &g.mg, &g.rmg,
+                     s) != 0 ||
+        launch_tprep(up->packed, up->scales, up->col_idx, up->R, up->K, C_in, ws + L.pg, &g.twu, &g.mu, &g.rmu,
+                     s) != 0 ||
+        launch_tprep(down->packed, down->scales, down->col_idx, down->R, down->K, gate->R, ws + L.pg + L.pu, &d.twd,
+                     &d.md, &d.rmd, s) != 0)
+      return LBK_ERR_LAUNCH;
+    float* hmax = reinterpret_cast<float*>(ws + L.pg + L.pu + L.pd);
+    g.xq = xq; g.sx = sx; g.N = N; g.d_model = d_model;
+    g.cg = gate->col_idx; g.cu = up->col_idx; g.K = gate->K;
+    g.R_ff = gate->R; g.H = tgu_slices(N); g.h = h; g.hmax = hmax;
+    if (launch_tgu(g, s) != 0) return LBK_ERR_LAUNCH;
+    d.h = h; d.hmax = hmax; d.H = g.H; d.N = N; d.d_ff = (int)d_ff; d.d_model = d_model;
+    d.cd = down->col_idx; d.Kd = down->K; d.R_m = down->R; d.C_d = gate->R;
+    d.resid = x_resid; d.out = out; d.hq_out = hq_out; d.sh_out = sh_out;
+    if (launch_tdn(d, s) != 0) return LBK_ERR_LAUNCH;
+    return LBK_OK;
+  }
+
+  const size_t hb = align256((size_t)N * d_ff * 2), qb = align256((size_t)N * d_ff);
   const bool need_ws = !h_out || !hq_out || !sh_out;
   if (need_ws) {
-    if (!ws || workspace_bytes < lbk_ternary_swiglu_workspace_bytes(N, gate)) return LBK_ERR_WORKSPACE;
+    if (!ws || workspace_bytes < lbk_ternary_swiglu_workspace_bytes(N, d_model, gate, up, down))
+      return LBK_ERR_WORKSPACE;
     if (!a16(ws)) return LBK_ERR_ALIGN;
   }
   uint16_t* h = h_out ? h_out : reinterpret_cast<uint16_t*>(ws);
   int8_t* hq = hq_out ? hq_out : reinterpret_cast<int8_t*>(ws + hb);
   float* sh = sh_out ? sh_out : reinterpret_cast<float*>(ws + hb + qb);
   if (!a16(h) || !a16(hq)) return LBK_ERR_ALIGN;
-  hipStream_t s = S(stream);
   TernaryLaunch a{};
   a.xq = xq; a.sx = sx; a.N = N; a.C = d_model / gate->B;
   a.p0 = gate->packed; a.s0 = gate->scales; a.c0 = gate->col_idx; a.K0 = gate->K;

@@ -107,6 +107,36 @@ struct TernaryLaunch {
 };
 // mode: 0 = product, 1 = gate/up with SiLU*mul (y = h bf16)
 int launch_ternary(int B, int mode, const TernaryLaunch& a, hipStream_t st);
+
+// two-kernel ternary SwiGLU (B = 64) on prepared weights (launch_tprep)
+typedef uint32_t tu32x4 __attribute__((ext_vector_type(4)));
+struct TGUArgs {
+  const int8_t* xq; const float* sx; int64_t N; int d_model;
+  const tu32x4* twg; const int32_t* mg; const float* rmg; const int32_t* cg;   // gate
+  const tu32x4* twu; const int32_t* mu; const float* rmu; const int32_t* cu;   // up
+  int K;                    // slots per row (gate and up alike)
+  int R_ff;
+  int H;                    // block-row slices per token block
+  uint16_t* h;              // [N, d_ff] bf16
+  float* hmax;              // [H, N] max |h| of each slice
+};
+struct TDNArgs {
+  const uint16_t* h; const float* hmax; int H; int64_t N; int d_ff; int d_model;
+  const tu32x4* twd; const int32_t* md; const float* rmd; const int32_t* cd; int Kd;
+  int R_m; int C_d;
+  const uint16_t* resid;    // optional [N, d_model]
+  uint16_t* out;            // [N, d_model]
+  int8_t* hq_out;           // optional [N, d_ff]
+  float* sh_out;            // optional [N]
+};
+size_t tprep_bytes(int64_t ntiles, int R);
+int launch_tprep(const uint32_t* packed, const float* s, const int32_t* col, int R, int K, int C, void* out,
+                 const tu32x4** tw, const int32_t** mval, const float** rmul, hipStream_t st);
+bool tsplit_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd);
+int tgu_slices(int64_t N);
+int launch_tgu(const TGUArgs& a, hipStream_t st);
+int launch_tdn(const TDNArgs& a, hipStream_t st);
+
 int launch_check_columns(const int32_t* col, int64_t count, int C, int32_t* bad, hipStream_t st);
 
 }  // namespace lbk

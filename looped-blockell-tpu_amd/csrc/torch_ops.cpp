@@ -325,10 +325,9 @@ std::vector<at::Tensor> tern_swiglu_impl(const at::Tensor& xq_, const at::Tensor
     res.push_back(th);
     res.push_back(tq);
     res.push_back(ts);
-  } else {
-    wsb = lbk_ternary_swiglu_workspace_bytes(N, &g);
-    ws = workspace(wsb, xq);
   }
+  wsb = lbk_ternary_swiglu_workspace_bytes(N, (int32_t)d_model, &g, &u, &d);
+  if (wsb) ws = workspace(wsb, xq);
   LBK_CALL("block_ell_swiglu_fwd_ternary",
            lbk_swiglu_fwd_ternary(xq.data_ptr<int8_t>(), sx.data_ptr<float>(), N, (int32_t)d_model, &g, &u, &d, xrp,
                                   bfm(out), h, hq, sh, wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(xq)));

@@ -62,7 +62,7 @@ SIGNATURES = {
     "lbk_pack_ternary": (C.c_int, [_P, _I32, _I32, _I32, _P, _P]),
     "lbk_ternary_quantize_weights_bf16": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P]),
     "lbk_ternary_matmul": (C.c_int, [_P, _P, _I64, _I32, _PT, _P, _P, _P]),
-    "lbk_ternary_swiglu_workspace_bytes": (_SZ, [_I64, _PT]),
+    "lbk_ternary_swiglu_workspace_bytes": (_SZ, [_I64, _I32, _PT, _PT, _PT]),
     "lbk_swiglu_fwd_ternary": (C.c_int, [_P, _P, _I64, _I32, _PT, _PT, _PT, _P, _P, _P, _P, _P, _P, _SZ, _P]),
 }
 

@@ -154,6 +154,79 @@ def test_ternary_swiglu(gpu, case, resid):
     assert rel <= TOL, f"rel {rel} abs {ab}"
 
 
+# B = 64 geometries served by the two-kernel path (gate/up kernel + down kernel with
+# on-the-fly re-quantisation): ragged N, every slice count (N >= 16384 -> 1 slice,
+# 8192 -> 2, fewer -> 4), slot counts that are not multiples of the ring depths (2 and 8),
+# dead slots, down rows fewer than the 8 waves, and a fully dead gate row.
+SPLIT_CASES = [
+    # (d_model, d_ff, Kg, Kd, N, sentinel_frac)
+    (256, 1024, 3, 5, 1, 0.0),
+    (256, 1024, 3, 5, 65, 0.2),
+    (512, 2048, 2, 7, 8192 + 3, 0.1),
+    (256, 512, 4, 8, 16384 + 37, 0.0),
+    (2048, 4096, 5, 3, 200, 0.3),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES)
+def test_ternary_swiglu_split(gpu, case):
+    from looped_blockell import kernels
+    d_model, d_ff, Kg, Kd, N, frac = case
+    B = 64
+    _say(f"ternary swiglu split {case}")
+    rng = np.random.default_rng(abs(hash(case)) % 2 ** 31)
+    g = tern_weight(rng, d_ff // B, d_model // B, Kg, B, sentinel_frac=frac)
+    u = tern_weight(rng, d_ff // B, d_model // B, Kg, B, sentinel_frac=frac)
+    d = tern_weight(rng, d_model // B, d_ff // B, Kd, B, sentinel_frac=frac)
+    if frac:
+        g[2][0, :] = -1                                  # a gate row with no live block
+    x = T.act(rng, N, d_model)
+    xq, sx = O.activation_quantize_int8(x)
+    xg = T.to_gpu_bf16(x)
+    args = (T.to_gpu(xq), T.to_gpu(sx), gpu_tern(g), gpu_tern(u), gpu_tern(d), xg)
+    out, h, hq, sh = kernels.ternary_swiglu_fwd_with_intermediate(*args)
+    out_ws = kernels.ternary_swiglu_fwd(*args)
+    out, h, hq, sh, out_ws = T.to_np(out), T.to_np(h), T.to_np(hq), T.to_np(sh), T.to_np(out_ws)
+    assert np.array_equal(out, out_ws)
+    hq_ref, sh_ref = O.activation_quantize_int8(h)
+    assert np.array_equal(hq, hq_ref) and np.array_equal(sh, sh_ref)
+    gf, _ = O.ternary_matmul(xq, sx, *g, exact_scales=False)
+    uf, _ = O.ternary_matmul(xq, sx, *u, exact_scales=False)
+    href = O.bf16_round(O.silu(gf.astype(np.float64)) * uf)
+    assert T.rel_err(h, href)[0] <= TOL
+    if frac:
+        assert (h[:, :B] == 0).all()
+    yd, _ = O.ternary_matmul(hq, sh, *d, exact_scales=False)
+    assert np.array_equal(out, O.bf16_round((yd + x).astype(np.float32)))
+    ref = O.ternary_swiglu_fwd(x, g, u, d, add_residual=True, exact_scales=True, h_round=O.bf16_round)
+    rel, ab = T.rel_err(out, ref["out"])
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
+def test_ternary_swiglu_split_extreme(gpu):
+    """All-(-128) activations against all-(-1) tiles with equal scales: accumulators
+    K * m * 64 * 128 within 1% of the int32 limit the fixed point is sized for, bit-exact."""
+    _say("ternary swiglu split extreme accumulators")
+    from looped_blockell import kernels
+    B, d_model, d_ff, K, N = 64, 2048, 2048, 32, 70
+    t = -np.ones((d_ff // B, K, B, B), np.int8)
+    s = np.full((d_ff // B, K), 127 / 128, np.float32)
+    col = np.tile(np.arange(K, dtype=np.int32), (d_ff // B, 1))
+    td = -np.ones((d_model // B, K, B, B), np.int8)
+    sd = np.full((d_model // B, K), 127 / 128, np.float32)
+    xq = np.full((N, d_model), -128, np.int8)
+    sx = np.full(N, 1.0 / 128, np.float32)
+    out, h, hq, sh = kernels.ternary_swiglu_fwd_with_intermediate(
+        T.to_gpu(xq), T.to_gpu(sx), gpu_tern((t, s, col)), gpu_tern((t, s, col)), gpu_tern((td, sd, col)), None)
+    h = T.to_np(h)
+    gf, acc = O.ternary_matmul(xq, sx, t, s, col, exact_scales=False)
+    m, _ = O.ternary_fixed_point(s, col, B)
+    assert acc.max() == K * m.max() * B * 128 and acc.max() > 0.99 * 2 ** 31
+    assert T.rel_err(h, O.bf16_round(O.silu(gf.astype(np.float64)) * gf))[0] <= TOL
+    yd, _ = O.ternary_matmul(T.to_np(hq), T.to_np(sh), td, sd, col, exact_scales=False)
+    assert np.array_equal(T.to_np(out), O.bf16_round(yd))
+
+
 def test_ternary_config3_full_sampled_rows(gpu):
     """Config 3 at full size (N=8192); bit-exact checks on sampled rows."""
     from looped_blockell import kernels

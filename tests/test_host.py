@@ -131,7 +131,10 @@ def test_abi_ternary_checks():
     assert lib.lbk_quantize_act_int8(C.c_void_p(0x10000), 4, 12, 12, C.c_void_p(0x20000), C.c_void_p(0x30000),
                                      s) == A.LBK_ERR_ALIGN
     assert lib.lbk_pack_ternary(C.c_void_p(0x1000), 2, 2, 40, C.c_void_p(0x2000), s) == A.LBK_ERR_TILE
-    assert lib.lbk_ternary_swiglu_workspace_bytes(8, C.byref(w)) >= 8 * 256 * 3
+    w = A.BellTernary(0x1000, 0x2000, 0x3000, 4, 2, 64)          # d_ff 256
+    wd = A.BellTernary(0x1000, 0x2000, 0x3000, 2, 2, 64)         # d_model 128
+    assert lib.lbk_ternary_swiglu_workspace_bytes(8, 128, C.byref(w), C.byref(w), C.byref(wd)) >= 8 * 256 * 3
+    assert lib.lbk_ternary_swiglu_workspace_bytes(8, 96, C.byref(w), C.byref(w), C.byref(wd)) == 0
 
 
 # ------------------------------------------------------------------ torch operator registrations
