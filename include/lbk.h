@@ -170,10 +170,10 @@ int lbk_ternary_quantize_weights_bf16(const uint16_t* values, int32_t R, int32_t
 /*
  * Ternary Block-ELL product: y[n, r*B+j] ~= sx[n] * sum_k s[r,k] * P[n,r,k,j],
  * P = int32 block partial of xq against the ternary tile.  y bf16 [N, R*B].
- * The block scales are applied in per-row 8-bit fixed point: m[r,k] =
- * rint(s[r,k] * 2^e_r) in [0, 127], e_r the largest exponent with
- * max_k |s[r,k]| * 2^e_r <= 127, then y = f32(f32(sum_k m * P) * 2^-e_r) * sx
- * (each scale within 2^-8 of the row's largest, relative).
+ * The block scales are applied in per-row fixed point: m[r,k] = rint(s[r,k] * 2^e_r)
+ * with e_r the largest exponent keeping |sum_k m * P| inside int32 for any int8
+ * input (m at most 2^16 - 1), then y = f32(f32(sum_k m * P) * 2^-e_r) * sx
+ * (within 2^-12 of exact fp32 scaling).
  * If partials != NULL the kernel also stores every P as int32 [N, R, K, B]
  * (dead slots store 0) — the exact integer accumulators before scaling.
  */

@@ -3,14 +3,21 @@
 // Arithmetic (the same as the row-block kernels of lbk_ternary.hip): for block
 // row r the fp32 block scales are used in the fixed point m[r,k] * 2^-e[r]
 // (row_fixed_point: m up to 16 bits, sum_k m * P inside int32), each block's
-// int32 partial P comes from an int8 MFMA chain started at zero, and
-// acc += m * P is one 24-bit integer multiply-add per element; the output is
+// exact int32 partial P = x . t comes from int8 MFMAs, and acc += m * P is one
+// 24-bit integer multiply-add per element; the output is
 // y = f32(f32(acc) * 2^-e[r]) * sx[token].
 //
-//   tprep_kernel  per call: packed tiles [R,K,64,4] -> fragment-major words
-//                 (lane l of a wave reads its 4 words with one dwordx4), m per
-//                 tile (zero for dead slots and for one appended zero tile),
-//                 and 2^-e[r] per row.
+// Weight encoding of the prepared tiles: every weight is stored as t + 1 in
+// {0, 1, 2} (2 bits), so a byte of weights is just (word >> 2q) & 0x03030303 (no
+// table lookup), and the MFMA computes x . (t + 1) = P + sum(x) starting from
+// C = -sum(x): the per-token sums of each 64-wide activation block are kept in
+// LDS beside the activation panel (int32, exact).
+//
+//   tprep_kernel  per call: packed tiles [R,K,64,4] -> fragment-major words in
+//                 the t + 1 encoding (lane l of a wave reads its 4 words with one
+//                 dwordx4; dead slots and one appended tile encode t = 0), m per
+//                 tile (zero for dead slots and the appended tile), and 2^-e[r]
+//                 per row.
 //   tgu_kernel    gate/up + SiLU*mul: a workgroup owns 64 tokens (int8 x panel
 //                 in LDS, XOR-swizzled) and one of H slices of the block rows;
 //                 each wave streams rows r through a ring of (gate, up) tile
@@ -29,6 +36,8 @@ namespace lbk {
 
 namespace {
 
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
 // ring depths (tile slots prefetched ahead): a gate/up slot is a (gate, up) tile pair, 32
 // MFMAs; a down slot is one tile, 4 MFMAs
 constexpr int TG_RING = 2;
@@ -46,9 +55,25 @@ __device__ __forceinline__ uint32_t tpanel_addr(int row, int chunk, int rowb) {
   return (uint32_t)((i * MT + mt) * rowb + ((chunk ^ i) << 4));
 }
 
-// 16 int8 weights {-1, 0, +1} of one fragment (16 two-bit codes)
+// 16 int8 weights t + 1 in {0, 1, 2} of one fragment (16 two-bit fields)
 __device__ __forceinline__ i32x4 tunpack(uint32_t w) {
-  return i32x4{(int)unpack4(w, 0), (int)unpack4(w, 1), (int)unpack4(w, 2), (int)unpack4(w, 3)};
+  return i32x4{(int)(w & 0x03030303u), (int)((w >> 2) & 0x03030303u), (int)((w >> 4) & 0x03030303u),
+               (int)((w >> 6) & 0x03030303u)};
+}
+
+// 2-bit codes of the storage format (00 -> 0, 01 -> +1, 11 -> -1, 10 -> 0) -> t + 1
+// (0 -> 01, +1 -> 10, -1 -> 00), field by field
+__device__ __forceinline__ uint32_t recode_t1(uint32_t w) {
+  const uint32_t b0 = w & 0x55555555u, b1 = (w >> 1) & 0x55555555u;
+  return ((b0 & ~b1) << 1) | (~w & 0x55555555u);
+}
+
+// sum of the 16 int8 values of a 16-byte chunk
+__device__ __forceinline__ int sum16_i8(const u32x4& v) {
+  int s = 0;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) s = __builtin_amdgcn_sdot4((int)v[d], 0x01010101, s, false);
+  return s;
 }
 
 }  // namespace
@@ -68,11 +93,11 @@ __global__ __launch_bounds__(64) void tprep_kernel(const uint32_t* __restrict__ 
     const int c = col[t];
     alive = c >= 0 && c < C;
   }
-  u32x4 v = {0, 0, 0, 0};
+  u32x4 v = {0x55555555u, 0x55555555u, 0x55555555u, 0x55555555u};   // t = 0
   if (alive) {
     const uint32_t* tile = packed + t * (64 * 4);
 #pragma unroll
-    for (int n = 0; n < 4; ++n) v[n] = tile[(4 * j + n) * 4 + g];   // output column 4j + n, inputs 16g..16g+15
+    for (int n = 0; n < 4; ++n) v[n] = recode_t1(tile[(4 * j + n) * 4 + g]);   // column 4j + n, inputs 16g..16g+15
   }
   tw[t * 64 + l] = v;
   if (l == 0) {
@@ -92,8 +117,8 @@ __global__ __launch_bounds__(64) void tprep_kernel(const uint32_t* __restrict__ 
 // ---------------------------------------------------------------------------
 struct TSlot {
   u32x4 wg, wu;      // fragment words of the gate and up tiles
-  int mg, mu;        // their fixed-point scales
   int cg, cu;        // input column blocks (dead -> 0, weights are zero)
+  int mg, mu;        // their fixed-point scales
 };
 
 template <int MT>
@@ -114,18 +139,25 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
   const int RH = (a.R_ff + a.H - 1) / a.H;
   const int r_lo = half * RH, r_hi = (r_lo + RH) < a.R_ff ? (r_lo + RH) : a.R_ff;
   const int64_t ztile = (int64_t)a.R_ff * K;
-  int2* ctab = reinterpret_cast<int2*>(smem + (size_t)TM * ROWB);
+  // LDS: x panel | -sum(x) per (input block, token) [32][TM] int32 | slot table
+  // {cg, cu, mg, mu} of this slice | row table {2^-e_g, 2^-e_u}.  Every per-slot and per-row
+  // value the loop needs is read from LDS: a scalar load in the loop would make each slot
+  // wait for the latest one (scalar loads return out of order).
+  constexpr int RSB = 32 * TM * 4;
+  int* rsum = reinterpret_cast<int*>(smem + (size_t)TM * ROWB);
+  int4* ctab = reinterpret_cast<int4*>(smem + (size_t)TM * ROWB + RSB);
+  float2* rtab = reinterpret_cast<float2*>(smem + (size_t)TM * ROWB + RSB + (size_t)RH * K * 16);
   float* hred = reinterpret_cast<float*>(smem);   // reused after the loop: [8 waves][TM]
   __shared__ float s_sx[TM];
 
-  // ---- column table of this slice
   for (int e = tid; e < (r_hi - r_lo) * K; e += 512) {
     const int64_t ge = (int64_t)r_lo * K + e;
     int cg = a.cg[ge], cu = a.cu[ge];
     cg = (cg >= 0 && cg < cin) ? cg : 0;
     cu = (cu >= 0 && cu < cin) ? cu : 0;
-    ctab[e] = make_int2(cg, cu);
+    ctab[e] = make_int4(cg, cu, a.mg[ge], a.mu[ge]);
   }
+  for (int e = tid; e < r_hi - r_lo; e += 512) rtab[e] = make_float2(a.rmg[r_lo + e], a.rmu[r_lo + e]);
 
   const int nrows = r_hi > r_lo + w ? (r_hi - r_lo - w + 7) / 8 : 0;
   const int KP = (K + TG_RING - 1) / TG_RING * TG_RING;
@@ -136,14 +168,14 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
     const int64_t e = live ? (int64_t)r * K + rk : ztile;
     S.wg = a.twg[e * 64 + lane];
     S.wu = a.twu[e * 64 + lane];
-    S.mg = a.mg[e];
-    S.mu = a.mu[e];
     S.cg = live ? (r - r_lo) * K + rk : -1;
   };
   auto fetch_c = [&](TSlot& S) {
-    const int2 c = ctab[S.cg >= 0 ? S.cg : 0];
+    const int4 c = ctab[S.cg >= 0 ? S.cg : 0];   // padding slots: zero tiles, any entry
     S.cg = c.x;
     S.cu = c.y;
+    S.mg = c.z;
+    S.mu = c.w;
     if (++rk == KP) {
       rk = 0;
       ++rn;
@@ -192,12 +224,24 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
       const int e = tid + 512 * it;
       *reinterpret_cast<u32x4*>(smem + tpanel_addr<MT>(e / CPR, e % CPR, ROWB)) = pv[it];
     }
+    // -sum(x) of each 64-wide block: the 4 chunks of a block sit in 4 adjacent lanes
+#pragma unroll
+    for (int it = 0; it < PIT; ++it) {
+      const int e = tid + 512 * it;
+      const int row = e / CPR, cc = e % CPR;
+      int sm = sum16_i8(pv[it]);
+      sm += __shfl_xor(sm, 1, 64);
+      sm += __shfl_xor(sm, 2, 64);
+      if ((cc & 3) == 0 && cc < cpr) rsum[(cc >> 2) * TM + row] = -sm;
+    }
   }
-  float hmax[MT][4];
+  // running max |h| per token of this lane: bf16 bit patterns of |h| (non-negative, so integer
+  // order is float order), two tokens (v, v + 1) per register
+  u16x2 hmax[MT][2];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) hmax[mt][v] = 0.f;
+    for (int v = 0; v < 2; ++v) hmax[mt][v] = u16x2{0, 0};
   __syncthreads();
 
   if (nrows > 0) {
@@ -212,11 +256,17 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
     static_assert(MT == 4, "two token tiles per step");
     auto compute = [&](const TSlot& S) {
       const int mg = uniform(S.mg), mu = uniform(S.mu);
-      const uint32_t ag0 = lbase + (((uniform(S.cg) * 4 + g) ^ i) << 4);
-      const uint32_t au0 = lbase + (((uniform(S.cu) * 4 + g) ^ i) << 4);
-      i32x4 av[MT], avu[MT];
+      const int cgc = uniform(S.cg), cuc = uniform(S.cu);
+      const uint32_t ag0 = lbase + (((cgc * 4 + g) ^ i) << 4);
+      const uint32_t au0 = lbase + (((cuc * 4 + g) ^ i) << 4);
+      const int* zg = rsum + cgc * TM + 4 * g;
+      const int* zu = rsum + cuc * TM + 4 * g;
+      i32x4 av[MT], avu[MT], cz[MT], czu[MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) av[mt] = __builtin_bit_cast(i32x4, lds16t(smem, ag0 + mt * ROWB));
+      for (int mt = 0; mt < MT; ++mt) {
+        av[mt] = __builtin_bit_cast(i32x4, lds16t(smem, ag0 + mt * ROWB));
+        cz[mt] = *reinterpret_cast<const i32x4*>(zg + 16 * mt);
+      }
       i32x4 Pp[2], f;
 #pragma unroll
       for (int q = 0; q < 17; ++q) {
@@ -228,13 +278,21 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) avu[mt] = __builtin_bit_cast(i32x4, lds16t(smem, au0 + mt * ROWB));
           }
+          if (q == 7) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) czu[mt] = *reinterpret_cast<const i32x4*>(zu + 16 * mt);
+          }
           if (q == 8) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) av[mt] = avu[mt];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) cz[mt] = czu[mt];
+#pragma unroll
+            for (int mt = 2; mt < MT; ++mt) cz[mt] = *reinterpret_cast<const i32x4*>(zu + 16 * mt);
           }
           if (hh == 0) f = tunpack(up ? S.wu[n] : S.wg[n]);
 #pragma unroll
-          for (int u = 0; u < 2; ++u) Pn[u] = mfma_i8_k64(av[2 * hh + u], f, i32x4{0, 0, 0, 0});
+          for (int u = 0; u < 2; ++u) Pn[u] = mfma_i8_k64(av[2 * hh + u], f, cz[2 * hh + u]);
         }
         if (q > 0) {
           const int pq = q - 1;
@@ -278,9 +336,13 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-      // epilogue of row r: g, u = acc * (2^-e * sx); h = silu(g) * u (bf16)
+      // epilogue of row r: with g = G * cg, u = U * cu (G, U the integer accumulators,
+      // cg = 2^-e_g * sx, cu = 2^-e_u * sx),
+      //   h = silu(g) * u = G * U / ((1 + 2^(G * k)) / (cg * cu)),  k = -log2(e) * cg,
+      // where (1 + E) / C is one fma with 1 / C (clamped finite); h is rounded to bf16
       const int r = r_lo + w + 8 * n;
-      const float fg = a.rmg[r], fu = a.rmu[r];
+      const float2 fr = rtab[r - r_lo];
+      const float fg = fr.x, fu = fr.y;
       const int64_t col0 = (int64_t)r * 64 + 4 * i;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
@@ -289,36 +351,43 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
           const int64_t t = t0 + 16 * mt + 4 * g + v;
           const float sxv = s_sx[16 * mt + 4 * g + v];
           const float cg = fg * sxv, cu = fu * sxv;
-          uint32_t hb[4];
+          const float k = cg * -1.4426950408889634f;
+          const float ic = fminf(__builtin_amdgcn_rcpf(cg * cu), 1e38f);
+          float hv[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const float gv = (float)ag[mt][q][v] * cg;
-            const float uv = (float)au[mt][q][v] * cu;
-            hb[q] = f2bf(silu_f(gv) * uv);
-            hmax[mt][v] = fmaxf(hmax[mt][v], fabsf(bf2f(hb[q])));
+            const float G = (float)ag[mt][q][v], U = (float)au[mt][q][v];
+            const float E = __builtin_amdgcn_exp2f(G * k);
+            hv[q] = (G * U) * __builtin_amdgcn_rcpf(fmaf(E, ic, ic));
           }
-          if (t < a.N)
-            *reinterpret_cast<u32x2*>(a.h + t * d_ff + col0) = u32x2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
+          const uint32_t p01 = pack2_bf16(hv[0], hv[1]), p23 = pack2_bf16(hv[2], hv[3]);
+          const u16x2 pm = __builtin_elementwise_max(__builtin_bit_cast(u16x2, p01 & 0x7fff7fffu),
+                                                     __builtin_bit_cast(u16x2, p23 & 0x7fff7fffu));
+          const unsigned short tm = pm[0] > pm[1] ? pm[0] : pm[1];
+          hmax[mt][v >> 1] = __builtin_elementwise_max(hmax[mt][v >> 1],
+                                                       (v & 1) ? u16x2{0, tm} : u16x2{tm, 0});
+          if (t < a.N) *reinterpret_cast<u32x2*>(a.h + t * d_ff + col0) = u32x2{p01, p23};
         }
     }
   }
 
   // ---- per-token max |h| of this slice: lanes of one g share tokens, then waves via LDS
+  float hm[MT][4];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      float m = hmax[mt][v];
+      float m = bf2f(hmax[mt][v >> 1][v & 1]);
 #pragma unroll
       for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-      hmax[mt][v] = m;
+      hm[mt][v] = m;
     }
   __syncthreads();   // the panel is no longer read
   if (i == 0) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) hred[w * TM + 16 * mt + 4 * g + v] = hmax[mt][v];
+      for (int v = 0; v < 4; ++v) hred[w * TM + 16 * mt + 4 * g + v] = hm[mt][v];
   }
   __syncthreads();
   if (tid < TM) {
@@ -335,8 +404,7 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
 // ---------------------------------------------------------------------------
 struct TDSlot {
   u32x4 wd;
-  int m;
-  int c;
+  int2 cm;   // input column block (dead -> 0), fixed-point scale
 };
 
 __global__ __launch_bounds__(512, 1) void tdn_kernel(TDNArgs a) {
@@ -352,6 +420,16 @@ __global__ __launch_bounds__(512, 1) void tdn_kernel(TDNArgs a) {
   const int rowb = d_ff;   // int8 panel row stride (a multiple of 256)
   const int Kd = a.Kd;
   const int64_t ztile = (int64_t)a.R_m * Kd;
+  // LDS: int8 h panel | -sum(hq) per (input block, token) [C_d][TM] int32 | slot table {c, m} |
+  // row table 2^-e (no scalar loads in the loop)
+  int* rsum = reinterpret_cast<int*>(smem + (size_t)TM * d_ff);
+  int2* dtab = reinterpret_cast<int2*>(smem + (size_t)TM * d_ff + (size_t)a.C_d * TM * 4);
+  float* rtab = reinterpret_cast<float*>(smem + (size_t)TM * d_ff + (size_t)a.C_d * TM * 4 + (size_t)a.R_m * Kd * 8);
+  for (int e = tid; e < a.R_m * Kd; e += 512) {
+    const int c = a.cd[e];
+    dtab[e] = make_int2((c >= 0 && c < a.C_d) ? c : 0, a.md[e]);
+  }
+  for (int e = tid; e < a.R_m; e += 512) rtab[e] = a.rmd[e];
 
   // ---- per-token absmax over the slices -> quantisation scale (as quantize_act_kernel)
   if (tid < TM) {
@@ -374,9 +452,7 @@ __global__ __launch_bounds__(512, 1) void tdn_kernel(TDNArgs a) {
     const int rm = w + 8 * rn;
     const int64_t e = live ? (int64_t)rm * Kd + rk : ztile;
     S.wd = a.twd[e * 64 + lane];
-    S.m = a.md[e];
-    const int c = a.cd[live ? e : 0];
-    S.c = (live && c >= 0 && c < a.C_d) ? c : 0;
+    S.cm = make_int2(live ? (int)e : 0, 0);
     if (++rk == KP) {
       rk = 0;
       ++rn;
@@ -385,7 +461,11 @@ __global__ __launch_bounds__(512, 1) void tdn_kernel(TDNArgs a) {
   TDSlot P[TD_RING];
 #pragma unroll
   for (int sl = 0; sl < TD_RING; ++sl) fetch(P[sl]);
-  __syncthreads();   // s_scale
+  __syncthreads();   // s_scale, dtab, rtab
+  // slot metadata from LDS: for the prefetched slots here, for later ones one ring cycle ahead
+  auto meta = [&](TDSlot& S) { S.cm = dtab[S.cm.x]; };   // padding slots: zero tiles, any entry
+#pragma unroll
+  for (int sl = 0; sl < TD_RING; ++sl) meta(P[sl]);
 
   // ---- panel: the 16 h rows quantised to int8.  A unit is 16 values (32 bytes of h);
   // batches of 8 units per thread are loaded before any is converted.
@@ -425,6 +505,12 @@ __global__ __launch_bounds__(512, 1) void tdn_kernel(TDNArgs a) {
         if (t >= a.N) q = u32x4{0, 0, 0, 0};
         if (a.hq_out && t < a.N && eb < units)
           *reinterpret_cast<u32x4*>(a.hq_out + t * (int64_t)d_ff + 16 * cc) = q;
+        // -sum(hq) of each 64-wide block: its 4 chunks sit in 4 adjacent lanes, all of which
+        // are in range or all clamped (units and the chunks per row are multiples of 4)
+        int sm = sum16_i8(q);
+        sm += __shfl_xor(sm, 1, 64);
+        sm += __shfl_xor(sm, 2, 64);
+        if ((cc & 3) == 0 && eb < units) rsum[(cc >> 2) * TM + row] = -sm;
         *reinterpret_cast<u32x4*>(smem + tpanel_addr<1>(row, cc, rowb)) = q;
       }
     }
@@ -432,35 +518,58 @@ __global__ __launch_bounds__(512, 1) void tdn_kernel(TDNArgs a) {
   __syncthreads();
   if (nrows <= 0) return;
 
+  // Software pipeline over the slots of a row: slot s issues its LDS read one slot early, its
+  // MFMAs (partials P) beside the multiply-adds of slot s - 1, which drain at the row's end.
   const uint32_t lbase = (uint32_t)(i * rowb);
-  i32x4 acc[4];
+  auto a_frag = [&](const TDSlot& S) {
+    return __builtin_bit_cast(i32x4, lds16t(smem, lbase + (((uniform(S.cm.x) * 4 + g) ^ i) << 4)));
+  };
+  auto c_frag = [&](const TDSlot& S) {
+    return *reinterpret_cast<const i32x4*>(rsum + uniform(S.cm.x) * TM + 4 * g);
+  };
+  auto madd = [&](i32x4 (&acc)[4], const i32x4 (&Pp)[4], int m) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        int t = __mul24(Pp[q][v], m) + acc[q][v];
+        asm("" : "+v"(t));   // keeps each tile's multiply-add a v_mad_i32_i24 (no reassociation)
+        acc[q][v] = t;
+      }
+  };
+  i32x4 acc[4], Pp[4];
+  int mp = 0;
+  i32x4 av = a_frag(P[0]), cz = c_frag(P[0]);
   __builtin_amdgcn_sched_barrier(0);
   for (int n = 0; n < nrows; ++n) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) acc[q] = i32x4{0, 0, 0, 0};
+    for (int q = 0; q < 4; ++q) {
+      acc[q] = i32x4{0, 0, 0, 0};
+      Pp[q] = i32x4{0, 0, 0, 0};
+    }
+    mp = 0;
     for (int k = 0; k < KP; k += TD_RING) {
 #pragma unroll
       for (int sl = 0; sl < TD_RING; ++sl) {
-        const int c = uniform(P[sl].c);
-        const int m = uniform(P[sl].m);
-        const i32x4 av = __builtin_bit_cast(i32x4, lds16t(smem, lbase + (((c * 4 + g) ^ i) << 4)));
+        const int m = uniform(P[sl].cm.y);
+        i32x4 Pn[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const i32x4 Pq = mfma_i8_k64(av, tunpack(P[sl].wd[q]), i32x4{0, 0, 0, 0});
+        for (int q = 0; q < 4; ++q) Pn[q] = mfma_i8_k64(av, tunpack(P[sl].wd[q]), cz);
+        madd(acc, Pp, mp);
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            int t = __mul24(Pq[v], m) + acc[q][v];
-            asm("" : "+v"(t));
-            acc[q][v] = t;
-          }
-        }
+        for (int q = 0; q < 4; ++q) Pp[q] = Pn[q];
+        mp = m;
         fetch(P[sl]);
+        meta(P[sl]);
+        av = a_frag(P[(sl + 1) % TD_RING]);   // the next slot in ring order
+        cz = c_frag(P[(sl + 1) % TD_RING]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    madd(acc, Pp, mp);
     // epilogue of down row rm: y = f32(f32(acc) * 2^-e) * sh (+ residual) -> bf16
     const int rm = w + 8 * n;
-    const float fd = a.rmd[rm];
+    const float fd = rtab[rm];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int64_t t = t0 + 4 * g + v;
@@ -505,14 +614,22 @@ int launch_tprep(const uint32_t* packed, const float* s, const int32_t* col, int
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// LDS bytes of the two kernels (dynamic part; each also has <= 256 bytes of static LDS)
+static size_t tgu_lds(int RH, int K) {
+  return (size_t)64 * 2048 + (size_t)32 * 64 * 4 + (size_t)RH * K * 16 + (size_t)RH * 8;
+}
+static size_t tdn_lds(int d_ff, int R_m, int Kd) {
+  return (size_t)16 * d_ff + (size_t)(d_ff / 64) * 16 * 4 + (size_t)R_m * Kd * 8 + (size_t)R_m * 4;
+}
+
 bool tsplit_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd) {
   if (B != 64) return false;
   if (Kg != Ku || Kg < 1 || Kd < 1) return false;
-  if (d_model % 256 || d_model > 2048) return false;     // int8 x panel rows of 2048 bytes
+  if (d_model % 256 || d_model > 2048) return false;   // int8 x panel rows of 2048 bytes
   const int64_t d_ff = (int64_t)R_ff * 64;
-  if (d_ff % 256 || 16 * d_ff + 256 > 163840) return false;   // int8 h panel of 16 rows + scales
-  if ((int64_t)64 * 2048 + (int64_t)R_ff * Kg * 8 + 256 > 163840) return false;   // panel + column table + sx
-  (void)R_m;
+  if (d_ff % 256 || d_ff > 10240) return false;         // int8 h panel of 16 rows
+  if (tgu_lds(R_ff, Kg) + 256 > 163840) return false;   // one slice (N >= 16384) holds every row
+  if (tdn_lds((int)d_ff, R_m, Kd) + 256 > 163840) return false;
   return true;
 }
 
@@ -531,8 +648,7 @@ int launch_tgu(const TGUArgs& a, hipStream_t st) {
       return -1;
     configured = true;
   }
-  const int RH = (a.R_ff + a.H - 1) / a.H;
-  const size_t lds = (size_t)64 * 2048 + (size_t)RH * a.K * 8;
+  const size_t lds = tgu_lds((a.R_ff + a.H - 1) / a.H, a.K);
   const int64_t blocks = (a.N + 63) / 64;
   hipLaunchKernelGGL(kern, dim3((unsigned)(blocks * a.H)), dim3(512), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
@@ -547,7 +663,7 @@ int launch_tdn(const TDNArgs& a, hipStream_t st) {
       return -1;
     configured = true;
   }
-  const size_t lds = (size_t)16 * a.d_ff;
+  const size_t lds = tdn_lds(a.d_ff, a.R_m, a.Kd);
   hipLaunchKernelGGL(tdn_kernel, dim3((unsigned)((a.N + 15) / 16)), dim3(512), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
