@@ -107,26 +107,41 @@ def make_ternary(R, C, K, B, gen, device):
     return kernels.pack_ternary(t), s, cols
 
 
-def time_steps(step, steps, warmup):
+def time_steps(step, steps, warmup, step_events=True):
     """Run `warmup` untimed steps, then exactly `steps` timed ones.
 
     Returns (ms_per_step from the host clock between two synchronisations,
-    list of per-launch durations from HIP events on the current stream).
+    list of per-step durations from HIP events on the current stream).  With
+    step_events=False the timed steps run back to back with no event between
+    them (a recorded event separates two launches on the GPU, which costs a
+    short kernel several microseconds), and the per-step durations come from
+    a second, untimed pass of the same steps.
     """
     import torch
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+
+    def with_events():
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        t0 = time.perf_counter()
+        for i in range(steps):
+            ev[i][0].record(stream)
+            step(i)
+            ev[i][1].record(stream)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3, [a.elapsed_time(b) for a, b in ev]
+
+    if step_events:
+        wall_ms, per = with_events()
+        return wall_ms / steps, per
     t0 = time.perf_counter()
     for i in range(steps):
-        ev[i][0].record(stream)
         step(i)
-        ev[i][1].record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
-    per = [a.elapsed_time(b) for a, b in ev]
+    _, per = with_events()
     return wall_ms / steps, per
 
 
@@ -231,7 +246,7 @@ def bench_decode(steps, warmup, device):
         g, u, d = copies[i % len(copies)]
         kernels.swiglu_fwd(x, *g, *u, *d, add_residual=False)
 
-    ms, per = time_steps(step, steps, warmup)
+    ms, per = time_steps(step, steps, warmup, step_events=False)
     byts = algorithmic_bytes(w)
     gbs = byts / (ms * 1e-3) / 1e9
     return dict(workload="decode SwiGLU FFN, 16 tokens, d_model=4096 d_ff=14336 B=64 density=0.10, "

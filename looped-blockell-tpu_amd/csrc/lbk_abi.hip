@@ -8,9 +8,6 @@
 
 #include <string.h>
 
-#include <atomic>
-#include <chrono>
-#include <random>
 
 using namespace lbk;
 
@@ -191,46 +188,11 @@ static int swiglu_split(const uint16_t* x, const float* xf, const float* norm_sc
   return launch_dn(gate->B, d, st) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
 }
 
-// ---- decode shape (N <= 16): one persistent launch, see lbk_decode.hip
+// ---- decode shape (N <= 16): gate/up and down kernels of lbk_decode.hip
 static constexpr int64_t kDecodeMaxTokens = 16;
 
-struct DecodeLayout {
-  size_t flags, rowcnt, h, parts, total;
-  int S;
-};
-
-static DecodeLayout decode_layout(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* down) {
-  DecodeLayout L{};
-  L.S = decode_splits(down->K, down->R);
-  L.flags = 0;
-  L.rowcnt = L.flags + align256((size_t)gate->R * 8);
-  L.h = L.rowcnt + align256((size_t)down->R * 8);
-  L.parts = L.h + align256((size_t)N * gate->R * gate->B * 2);
-  L.total = L.parts + align256((size_t)L.S * N * d_model * 4);
-  return L;
-}
-
-static bool use_decode(int64_t N, const lbk_bell* gate, const lbk_bell* down, bool inter) {
-  return !inter && N <= kDecodeMaxTokens &&
-         decode_grid(gate->R, down->R, decode_splits(down->K, down->R)) > 0;
-}
-
-// The decode kernel tags each call on the host, so it is not used under graph capture.
-static bool capturing(void* stream) {
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  return hipStreamIsCapturing(S(stream), &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
-}
-
-// Per-call tag for the decode kernel's flags and counters: unique within the
-// process (counter) and, from a random start, unlikely to match stale memory.
-static uint64_t next_epoch() {
-  static std::atomic<uint64_t> counter{[] {
-    std::random_device rd;
-    const uint64_t t = (uint64_t)std::chrono::steady_clock::now().time_since_epoch().count();
-    return (((uint64_t)rd() << 32) ^ (uint64_t)rd() ^ (t * 0x9E3779B97F4A7C15ull)) | 1ull;
-  }()};
-  const uint64_t e = counter.fetch_add(2, std::memory_order_relaxed);
-  return e ? e : 1;
+static bool use_decode(int64_t N, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, bool inter) {
+  return !inter && N <= kDecodeMaxTokens && decode_supported(gate->K, up->K, down->K);
 }
 
 size_t lbk_swiglu_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
@@ -239,11 +201,8 @@ size_t lbk_swiglu_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* ga
   // [packed gate/up/down tiles (split path)] [h, unless it goes to the caller's h_out]
   size_t b = use_split(gate, up, down, d_model) ? packed_ffn_bytes(gate, up, down) : 0;
   if (!want_intermediates) b += align256((size_t)N * gate->R * gate->B * 2);
-  // decode shapes run the single-launch kernel, or the path above under graph capture
-  if (use_decode(N, gate, down, want_intermediates != 0)) {
-    const size_t d = decode_layout(N, d_model, gate, down).total;
-    if (d > b) b = d;
-  }
+  // decode shapes need h only
+  if (use_decode(N, gate, up, down, want_intermediates != 0)) return align256((size_t)N * gate->R * gate->B * 2);
   return b;
 }
 
@@ -261,11 +220,13 @@ int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk
   if (!a16(x) || !a16(out) || (d_model % 8)) return LBK_ERR_ALIGN;
   for (const void* p : {(const void*)h_out, (const void*)gate_pre_out, (const void*)up_out})
     if (p && !a16(p)) return LBK_ERR_ALIGN;
-  if (use_decode(N, gate, down, h_out || gate_pre_out || up_out) && !capturing(stream)) {
-    const DecodeLayout L = decode_layout(N, d_model, gate, down);
-    if (!workspace || workspace_bytes < L.total) return LBK_ERR_WORKSPACE;
-    if (!a16(workspace)) return LBK_ERR_ALIGN;
-    char* ws = static_cast<char*>(workspace);
+  if (use_decode(N, gate, up, down, gate_pre_out || up_out)) {
+    uint16_t* hbuf = h_out;
+    if (!hbuf) {
+      if (!workspace || workspace_bytes < align256((size_t)N * d_ff * 2)) return LBK_ERR_WORKSPACE;
+      if (!a16(workspace)) return LBK_ERR_ALIGN;
+      hbuf = static_cast<uint16_t*>(workspace);
+    }
     DecodeArgs a{};
     a.x = x; a.N = (int)N; a.d_model = d_model;
     a.vg = gate->values; a.cg = gate->col_idx; a.Kg = gate->K;
@@ -273,15 +234,10 @@ int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk
     a.R_ff = gate->R;
     a.vd = down->values; a.cd = down->col_idx; a.Kd = down->K;
     a.R_m = down->R;
-    a.S = L.S;
     a.resid = add_residual ? x : nullptr;
     a.out = out;
-    a.epoch = next_epoch();
-    a.flags = reinterpret_cast<uint64_t*>(ws + L.flags);
-    a.rowcnt = reinterpret_cast<uint64_t*>(ws + L.rowcnt);
-    a.h = reinterpret_cast<uint16_t*>(ws + L.h);
-    a.parts = reinterpret_cast<float*>(ws + L.parts);
-    return launch_decode(gate->B, a, decode_grid(a.R_ff, a.R_m, a.S), S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+    a.h = hbuf;
+    return launch_decode(gate->B, a, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
   }
   const bool split = use_split(gate, up, down, d_model);
   const size_t pbytes = split ? packed_ffn_bytes(gate, up, down) : 0;

@@ -63,7 +63,7 @@ int launch_gu(int B, bool norm, const GUArgs& a, hipStream_t st);
 int launch_dn(int B, const DNArgs& a, hipStream_t st);
 int launch_bf16_to_f32(const uint16_t* x, int64_t n, float* y, hipStream_t st);
 
-// decode-shaped SwiGLU FFN (N <= 16) in one launch
+// decode-shaped SwiGLU FFN (N <= 16): gate/up kernel, then down kernel
 struct DecodeArgs {
   const uint16_t* x; int N; int d_model;
   const uint16_t* vg; const int32_t* cg; int Kg;
@@ -71,19 +71,12 @@ struct DecodeArgs {
   int R_ff;
   const uint16_t* vd; const int32_t* cd; int Kd;
   int R_m;
-  int S;                     // slot ranges per down row
   const uint16_t* resid;     // optional [N, d_model]
   uint16_t* out;             // [N, d_model]
-  uint64_t epoch;            // unique per call
-  // workspace
-  uint64_t* flags;           // [R_ff]: the epoch, once h block r is published
-  uint64_t* rowcnt;          // [R_m]: tagged count of finished units per down row
-  uint16_t* h;               // [N, d_ff]
-  float* parts;              // [S, N, d_model] unit sums
+  uint16_t* h;               // [N, d_ff] workspace (or the caller's h)
 };
-int decode_splits(int Kd, int R_m);
-int decode_grid(int R_ff, int R_m, int S);   // 0: shape not supported by the single-launch kernel
-int launch_decode(int B, const DecodeArgs& a, int grid, hipStream_t st);
+bool decode_supported(int Kg, int Ku, int Kd);
+int launch_decode(int B, const DecodeArgs& a, hipStream_t st);
 
 int launch_rmsnorm(const uint16_t* x, int64_t N, int d, const float* scale, float eps, uint16_t* out,
                    hipStream_t st);

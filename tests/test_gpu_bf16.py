@@ -223,11 +223,13 @@ def test_looped_L0_and_L1(gpu):
 
 DECODE_CASES = [
     # (d_model, d_ff, B, density, N, sentinel_frac)   N <= 16: the single-launch decode kernel
+    # (at most 24 down slots per row)
     (256, 1024, 16, 0.25, 16, 0.0),
     (512, 1024, 32, 0.25, 5, 0.1),
     (1024, 2048, 64, 0.25, 1, 0.0),
     (1024, 3072, 64, 0.125, 16, 0.1),
     (128, 512, 64, 1.0, 9, 0.0),
+    (256, 2048, 16, 0.25, 8, 0.1),      # 32 down slots per row: beyond the kernel's 24, other path
 ]
 
 
@@ -247,8 +249,8 @@ def test_decode_parity(gpu, case, resid):
 
 
 def test_decode_duplicates_and_workspace_reuse(gpu):
-    """Duplicate down columns, one workspace reused by consecutive calls (the per-call
-    tags of the decode kernel must keep the calls apart), and bitwise determinism."""
+    """Duplicate down columns, one workspace reused by consecutive calls, and bitwise
+    determinism of the decode kernels."""
     import torch
     A = T.abi()
     lib = A.load()
