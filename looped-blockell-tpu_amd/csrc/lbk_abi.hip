@@ -158,15 +158,15 @@ static int pack_ffn(const lbk_bell* gate, const lbk_bell* up, const lbk_bell* do
   const lbk_bell* ws3[3] = {gate, up, down};
   const void** dst[3] = {&out->g, &out->u, &out->d};
   const int cols[3] = {down->R, down->R, gate->R};   // input column blocks: d_model / B, d_model / B, d_ff / B
+  PackJob jobs[3];
   for (int t = 0; t < 3; ++t) {
     const int64_t nt = (int64_t)ws3[t]->R * ws3[t]->K;
     *dst[t] = p;
-    if (launch_pack_bf16(ws3[t]->values, ws3[t]->col_idx, nt, cols[t], B, reinterpret_cast<uint32_t*>(p), st) != 0)
-      return LBK_ERR_LAUNCH;
+    jobs[t] = PackJob{ws3[t]->values, ws3[t]->col_idx, nt, cols[t], reinterpret_cast<uint32_t*>(p), 0};
     p += align256(packed_bf16_bytes(nt, B));
   }
   out->bytes = (size_t)(p - ws);
-  return LBK_OK;
+  return launch_pack_bf16_multi(jobs, 3, B, st) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
 }
 
 static int swiglu_split(const uint16_t* x, const float* xf, const float* norm_scale, float eps, int64_t N,
@@ -406,13 +406,17 @@ int lbk_swiglu_fwd_ternary(const int8_t* xq, const float* sx, int64_t N, int32_t
     const int C_in = d_model / gate->B;
     TGUArgs g{};
     TDNArgs d{};
-    if (launch_tprep(gate->packed, gate->scales, gate->col_idx, gate->R, gate->K, C_in, ws, &g.twg, &g.mg, &g.rmg,
-                     s) != 0 ||
-        launch_tprep(up->packed, up->scales, up->col_idx, up->R, up->K, C_in, ws + L.pg, &g.twu, &g.mu, &g.rmu,
-                     s) != 0 ||
-        launch_tprep(down->packed, down->scales, down->col_idx, down->R, down->K, gate->R, ws + L.pg + L.pu, &d.twd,
-                     &d.md, &d.rmd, s) != 0)
-      return LBK_ERR_LAUNCH;
+    const TPrepWeight pw[3] = {{gate->packed, gate->scales, gate->col_idx, gate->R, gate->K, C_in},
+                               {up->packed, up->scales, up->col_idx, up->R, up->K, C_in},
+                               {down->packed, down->scales, down->col_idx, down->R, down->K, gate->R}};
+    void* const po[3] = {ws, ws + L.pg, ws + L.pg + L.pu};
+    const tu32x4* ptw[3];
+    const int32_t* pm[3];
+    const float* pr[3];
+    if (launch_tprep(pw, po, ptw, pm, pr, s) != 0) return LBK_ERR_LAUNCH;
+    g.twg = ptw[0]; g.mg = pm[0]; g.rmg = pr[0];
+    g.twu = ptw[1]; g.mu = pm[1]; g.rmu = pr[1];
+    d.twd = ptw[2]; d.md = pm[2]; d.rmd = pr[2];
     float* hmax = reinterpret_cast<float*>(ws + L.pg + L.pu + L.pd);
     g.xq = xq; g.sx = sx; g.N = N; g.d_model = d_model;
     g.cg = gate->col_idx; g.cu = up->col_idx; g.K = gate->K;

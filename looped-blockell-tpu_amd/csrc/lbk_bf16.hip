@@ -198,12 +198,11 @@ int launch_injection(const uint16_t* h, const uint16_t* e, const float* log_A, c
 // positions at zero weights instead of masking them.
 // ---------------------------------------------------------------------------
 template <int B>
-__global__ __launch_bounds__(256) void pack_bf16_kernel(const uint16_t* __restrict__ values,
-                                                        const int32_t* __restrict__ col, int64_t ntiles, int C,
-                                                        int64_t ndw, uint32_t* __restrict__ packed) {
-  constexpr int NKS = TileShape<B>::NKS, CW = TileShape<B>::CW;
+__device__ __forceinline__ void pack_bf16_dword(const uint16_t* __restrict__ values, const int32_t* __restrict__ col,
+                                                int64_t ntiles, int C, int64_t ndw, uint32_t* __restrict__ packed,
+                                                int64_t idx) {
+  constexpr int CW = TileShape<B>::CW;
   constexpr int PER_TILE = PackedTile<B>::U32X4 * 4;   // dwords per packed tile
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= ndw) return;
   const int64_t tile = idx / PER_TILE;
   if (tile >= ntiles || col[tile] < 0 || col[tile] >= C) {
@@ -224,6 +223,25 @@ __global__ __launch_bounds__(256) void pack_bf16_kernel(const uint16_t* __restri
   packed[idx] = (uint32_t)w[k * B + c] | ((uint32_t)w[(k + 1) * B + c] << 16);
 }
 
+template <int B>
+__global__ __launch_bounds__(256) void pack_bf16_kernel(const uint16_t* __restrict__ values,
+                                                        const int32_t* __restrict__ col, int64_t ntiles, int C,
+                                                        int64_t ndw, uint32_t* __restrict__ packed) {
+  pack_bf16_dword<B>(values, col, ntiles, C, ndw, packed, (int64_t)blockIdx.x * 256 + threadIdx.x);
+}
+
+// several weights in one launch: workgroups [first[t], first[t + 1]) pack weight t
+template <int B>
+__global__ __launch_bounds__(256) void pack_bf16_multi_kernel(PackJobs jobs) {
+  int t = 0;
+#pragma unroll
+  for (int u = 1; u < PackJobs::kMax; ++u)
+    if (u < jobs.n && (int64_t)blockIdx.x >= jobs.first[u]) t = u;
+  const PackJob& J = jobs.job[t];
+  pack_bf16_dword<B>(J.values, J.col, J.ntiles, J.C, J.ndw, J.packed,
+                     ((int64_t)blockIdx.x - jobs.first[t]) * 256 + threadIdx.x);
+}
+
 size_t packed_bf16_bytes(int64_t ntiles, int B) {
   switch (B) {
     case 16: return (size_t)(ntiles + 1) * PackedTile<16>::U32X4 * 16;
@@ -231,6 +249,26 @@ size_t packed_bf16_bytes(int64_t ntiles, int B) {
     case 64: return (size_t)(ntiles + 1) * PackedTile<64>::U32X4 * 16;
     default: return 0;
   }
+}
+
+int launch_pack_bf16_multi(const PackJob* jobs, int n, int B, hipStream_t st) {
+  if (n < 1 || n > PackJobs::kMax) return -2;
+  PackJobs J{};
+  J.n = n;
+  int64_t blocks = 0;
+  for (int t = 0; t < n; ++t) {
+    J.job[t] = jobs[t];
+    J.job[t].ndw = (int64_t)(packed_bf16_bytes(jobs[t].ntiles, B) / 4);
+    J.first[t] = blocks;
+    blocks += (J.job[t].ndw + 255) / 256;
+  }
+  if (blocks == 0 || blocks > 0x7fffffff) return -2;
+  const dim3 grid((unsigned)blocks);
+  if (B == 16) hipLaunchKernelGGL(pack_bf16_multi_kernel<16>, grid, dim3(256), 0, st, J);
+  else if (B == 32) hipLaunchKernelGGL(pack_bf16_multi_kernel<32>, grid, dim3(256), 0, st, J);
+  else if (B == 64) hipLaunchKernelGGL(pack_bf16_multi_kernel<64>, grid, dim3(256), 0, st, J);
+  else return -2;
+  return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_pack_bf16(const uint16_t* values, const int32_t* col, int64_t ntiles, int C, int B, uint32_t* packed,

@@ -29,6 +29,17 @@ int launch_rowblock(int B, int mode, const RowblockLaunch& a, hipStream_t st);
 int launch_pack_bf16(const uint16_t* values, const int32_t* col, int64_t ntiles, int C, int B, uint32_t* packed,
                      hipStream_t st);
 size_t packed_bf16_bytes(int64_t ntiles, int B);   // includes the appended zero tile
+// up to three weights packed by one launch (ndw is filled in by the launcher)
+struct PackJob {
+  const uint16_t* values; const int32_t* col; int64_t ntiles; int C; uint32_t* packed; int64_t ndw;
+};
+struct PackJobs {
+  static constexpr int kMax = 3;
+  PackJob job[kMax];
+  int64_t first[kMax];   // first workgroup of each job
+  int n;
+};
+int launch_pack_bf16_multi(const PackJob* jobs, int n, int B, hipStream_t st);
 
 
 // two-kernel SwiGLU: gate/up (+optional RMSNorm prologue) -> h, then down (+residual / fp32 state)
@@ -123,8 +134,20 @@ struct TDNArgs {
   float* sh_out;            // optional [N]
 };
 size_t tprep_bytes(int64_t ntiles, int R);
-int launch_tprep(const uint32_t* packed, const float* s, const int32_t* col, int R, int K, int C, void* out,
-                 const tu32x4** tw, const int32_t** mval, const float** rmul, hipStream_t st);
+struct TPrepWeight {
+  const uint32_t* packed; const float* s; const int32_t* col; int R, K, C;
+};
+struct TPrepJob {
+  const uint32_t* packed; const float* s; const int32_t* col; int R, K, C;
+  tu32x4* tw; int32_t* mval; float* rmul;
+};
+struct TPrepJobs {
+  TPrepJob job[3];
+  int64_t first[3];   // first workgroup of each weight
+};
+// prepares gate, up and down (w[0..2]) into out[0..2] (tprep_bytes each) in one launch
+int launch_tprep(const TPrepWeight (&w)[3], void* const (&out)[3], const tu32x4* (&tw)[3],
+                 const int32_t* (&mval)[3], const float* (&rmul)[3], hipStream_t st);
 bool tsplit_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd);
 int tgu_slices(int64_t N);
 int launch_tgu(const TGUArgs& a, hipStream_t st);

@@ -13,7 +13,7 @@
 // C = -sum(x): the per-token sums of each 64-wide activation block are kept in
 // LDS beside the activation panel (int32, exact).
 //
-//   tprep_kernel  per call: packed tiles [R,K,64,4] -> fragment-major words in
+//   tprep_kernel  per call, gate, up and down in one launch: packed tiles [R,K,64,4] -> fragment-major words in
 //                 the t + 1 encoding (lane l of a wave reads its 4 words with one
 //                 dwordx4; dead slots and one appended tile encode t = 0), m per
 //                 tile (zero for dead slots and the appended tile), and 2^-e[r]
@@ -81,11 +81,10 @@ __device__ __forceinline__ int sum16_i8(const u32x4& v) {
 // ---------------------------------------------------------------------------
 // weight preparation
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void tprep_kernel(const uint32_t* __restrict__ packed, const float* __restrict__ s,
-                                                   const int32_t* __restrict__ col, int R, int K, int C,
-                                                   u32x4* __restrict__ tw, int32_t* __restrict__ mval,
-                                                   float* __restrict__ rmul) {
-  const int64_t t = blockIdx.x;
+__device__ __forceinline__ void tprep_tile(const uint32_t* __restrict__ packed, const float* __restrict__ s,
+                                           const int32_t* __restrict__ col, int R, int K, int C,
+                                           u32x4* __restrict__ tw, int32_t* __restrict__ mval,
+                                           float* __restrict__ rmul, int64_t t) {
   const int l = threadIdx.x, j = l & 15, g = l >> 4;
   const int64_t ntiles = (int64_t)R * K;
   bool alive = false;
@@ -110,6 +109,17 @@ __global__ __launch_bounds__(64) void tprep_kernel(const uint32_t* __restrict__ 
     }
     mval[t] = m;
   }
+}
+
+// the three weights of a forward in one launch: workgroup b prepares tile b - first[t] of
+// weight t (each weight has R * K + 1 tiles, the last one the zero tile)
+__global__ __launch_bounds__(64) void tprep_kernel(TPrepJobs jobs) {
+  int t = 0;
+#pragma unroll
+  for (int u = 1; u < 3; ++u)
+    if ((int64_t)blockIdx.x >= jobs.first[u]) t = u;
+  const TPrepJob& J = jobs.job[t];
+  tprep_tile(J.packed, J.s, J.col, J.R, J.K, J.C, J.tw, J.mval, J.rmul, (int64_t)blockIdx.x - jobs.first[t]);
 }
 
 // ---------------------------------------------------------------------------
@@ -599,18 +609,28 @@ size_t tprep_bytes(int64_t ntiles, int R) {
   return al((size_t)(ntiles + 1) * 1024) + al((size_t)(ntiles + 1) * 4) + al((size_t)R * 4);
 }
 
-int launch_tprep(const uint32_t* packed, const float* s, const int32_t* col, int R, int K, int C, void* out,
-                 const u32x4** tw, const int32_t** mval, const float** rmul, hipStream_t st) {
+int launch_tprep(const TPrepWeight (&w)[3], void* const (&out)[3], const u32x4* (&tw)[3],
+                 const int32_t* (&mval)[3], const float* (&rmul)[3], hipStream_t st) {
   auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-  const int64_t nt = (int64_t)R * K;
-  char* p = static_cast<char*>(out);
-  u32x4* w = reinterpret_cast<u32x4*>(p);
-  int32_t* m = reinterpret_cast<int32_t*>(p + al((size_t)(nt + 1) * 1024));
-  float* f = reinterpret_cast<float*>(p + al((size_t)(nt + 1) * 1024) + al((size_t)(nt + 1) * 4));
-  *tw = w;
-  *mval = m;
-  *rmul = f;
-  hipLaunchKernelGGL(tprep_kernel, dim3((unsigned)(nt + 1)), dim3(64), 0, st, packed, s, col, R, K, C, w, m, f);
+  TPrepJobs J{};
+  int64_t blocks = 0;
+  for (int t = 0; t < 3; ++t) {
+    const int64_t nt = (int64_t)w[t].R * w[t].K;
+    char* p = static_cast<char*>(out[t]);
+    TPrepJob& j = J.job[t];
+    j.packed = w[t].packed; j.s = w[t].s; j.col = w[t].col;
+    j.R = w[t].R; j.K = w[t].K; j.C = w[t].C;
+    j.tw = reinterpret_cast<u32x4*>(p);
+    j.mval = reinterpret_cast<int32_t*>(p + al((size_t)(nt + 1) * 1024));
+    j.rmul = reinterpret_cast<float*>(p + al((size_t)(nt + 1) * 1024) + al((size_t)(nt + 1) * 4));
+    tw[t] = j.tw;
+    mval[t] = j.mval;
+    rmul[t] = j.rmul;
+    J.first[t] = blocks;
+    blocks += nt + 1;
+  }
+  if (blocks > 0x7fffffff) return -2;
+  hipLaunchKernelGGL(tprep_kernel, dim3((unsigned)blocks), dim3(64), 0, st, J);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
