@@ -177,13 +177,36 @@ def bench_bf16(steps, warmup, device):
                       frac=achieved / PEAK_BF16_TFLOPS, traffic=profiled_traffic(TRAFFIC_PROFILE_BF16),
                       traffic_source=os.path.relpath(TRAFFIC_PROFILE_BF16, ROOT) + " (FETCH_SIZE/WRITE_SIZE, "
                                      "calibrated on a 256 MiB copy)",
-                      kernel="SwiGLU forward launch sequence: pack_bf16_kernel<32> x3 + gu_kernel<32,4,false,false> "
-                             "+ dn_kernel<32,4,4>, timed together with HIP events around each step",
+                      kernel="SwiGLU forward launch sequence: pack_bf16_multi_kernel<32> (gate, up, down) + "
+                             "gu_kernel<32,4,false,false,false> + dn_kernel<32,4,4>, timed together with HIP events "
+                             "around each step",
                       algorithmic_flops_per_launch=flops,
                       algorithmic_bytes_per_launch=algorithmic_bytes(w)),
     )
     assert torch.isfinite(out["y"].float()).all()
     return res
+
+
+def bench_bf16_shared(steps, warmup, device):
+    """The headline workload with gate and up sharing one topology (the reference layer's
+    initialisation: both are seeded from the same hash, ``looped_blockell/layers/mlp.py:94``)."""
+    import torch
+    from looped_blockell import kernels
+    w = WORKLOADS["bf16"]
+    gen = torch.Generator(device=device).manual_seed(w["seed"])
+    g, u, d = make_ffn(w, device, gen)
+    x = torch.randn(w["N"], w["d_model"], generator=gen, device=device).to(torch.bfloat16)
+    args = (g[0], g[1], u[0], g[1], *d)   # up reads gate's column indices
+
+    def step(i):
+        kernels.swiglu_fwd(x, *args, add_residual=False)
+
+    ms, per = time_steps(step, steps, warmup)
+    flops = nonzero_flops(w)
+    return dict(workload="bf16 SwiGLU FFN as the headline workload, gate and up sharing one topology",
+                ms_per_step=ms, value=flops / (ms * 1e-3) / 1e12, unit="TFLOP/s",
+                tokens_per_s=w["N"] / (ms * 1e-3), frac_of_bf16_peak=flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                kernel_ms_avg=sum(per) / len(per))
 
 
 def bench_ternary(steps, warmup, device):
@@ -294,7 +317,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-main", action="store_true", help="headline workload only (for profiling)")
-    ap.add_argument("--only", default="", help="comma list of extra workloads to run: ternary,looped,decode")
+    ap.add_argument("--only", default="", help="comma list of extra workloads to run: shared,ternary,looped,decode")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one 256 MiB device-to-device copy (a reference point for HBM byte counters)")
     args = ap.parse_args()
@@ -319,8 +342,8 @@ def main():
     main_res = bench_bf16(args.steps, args.warmup, device)
     extra = {}
     if not args.only_main:
-        todo = [s for s in args.only.split(",") if s] or ["ternary", "looped", "decode"]
-        fns = dict(ternary=bench_ternary, looped=bench_looped, decode=bench_decode)
+        todo = [s for s in args.only.split(",") if s] or ["shared", "ternary", "looped", "decode"]
+        fns = dict(shared=bench_bf16_shared, ternary=bench_ternary, looped=bench_looped, decode=bench_decode)
         for name in todo:
             st = max(5, args.steps // (4 if name == "looped" else 1))
             try:

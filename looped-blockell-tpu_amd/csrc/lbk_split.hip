@@ -58,7 +58,7 @@ constexpr int GU_RING = 4;
 template <int MT>
 struct GUPanel { static constexpr int ROWB = 8192 / MT; };
 
-template <int B, int MT, bool NORM, bool INTER>
+template <int B, int MT, bool NORM, bool INTER, bool SHARED>
 __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
   constexpr int CW = TileShape<B>::CW;
   constexpr int TM = 16 * MT;
@@ -146,7 +146,9 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       avg[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(smem, ag0 + mt * ROWB);
-      avu[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(smem, au0 + mt * ROWB);
+      // shared topology (gate and up read the same column list): one panel read feeds both
+      if constexpr (SHARED) avu[mt] = avg[mt];
+      else avu[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(smem, au0 + mt * ROWB);
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -570,9 +572,9 @@ bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int 
   return true;
 }
 
-template <int B, int MT, bool NORM, bool INTER>
+template <int B, int MT, bool NORM, bool INTER, bool SHARED>
 static int launch_gu_t(const GUArgs& a, hipStream_t st) {
-  auto kern = gu_kernel<B, MT, NORM, INTER>;
+  auto kern = gu_kernel<B, MT, NORM, INTER, SHARED>;
   static bool configured = false;
   if (!configured) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 163840) != hipSuccess)
@@ -589,13 +591,20 @@ int launch_gu(int B, bool norm, const GUArgs& a, hipStream_t st) {
   if (a.N == 0) return 0;
   const int mt = gu_mt(a.d_model);
   const bool inter = a.gpre || a.uout;
+  // gate and up passing the same column-index buffer share their topology (the reference
+  // layer initialises both from the same seed)
+  const bool shared = a.cg == a.cu;
+#define LBK_GU2(BB, MM, SH)                                                                          \
+  if (norm) return launch_gu_t<BB, MM, true, false, SH>(a, st);                                     \
+  return inter ? launch_gu_t<BB, MM, false, true, SH>(a, st) : launch_gu_t<BB, MM, false, false, SH>(a, st);
 #define LBK_GU(BB, MM)                                                                          \
   if (B == BB && mt == MM) {                                                                    \
-    if (norm) return launch_gu_t<BB, MM, true, false>(a, st);                                   \
-    return inter ? launch_gu_t<BB, MM, false, true>(a, st) : launch_gu_t<BB, MM, false, false>(a, st); \
+    if (shared) { LBK_GU2(BB, MM, true) }                                                       \
+    LBK_GU2(BB, MM, false)                                                                      \
   }
   LBK_GU(16, 4) LBK_GU(16, 2) LBK_GU(32, 4) LBK_GU(32, 2)
 #undef LBK_GU
+#undef LBK_GU2
   return -2;
 }
 

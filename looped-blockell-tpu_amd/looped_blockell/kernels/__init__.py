@@ -73,7 +73,7 @@ def swiglu_fwd_with_intermediate(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_dow
 
 
 def looped_swiglu(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L: int, eps: float = 1e-5):
-    """L applications of h <- h + SwiGLU(RMSNorm(h)) with shared weights, one persistent launch."""
+    """L applications of h <- h + SwiGLU(RMSNorm(h)) with shared weights, in one operator call."""
     _gpu(h, v_gate, v_down)
     return ops().looped_swiglu(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L, eps)
 

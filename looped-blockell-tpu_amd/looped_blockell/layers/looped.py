@@ -3,9 +3,10 @@
 The MLP half of the reference's core block applied L times:
 ``h <- h + MLPBlock(RMSNorm(h))`` (reference ``looped_blockell/layers/transformer_block.py:83-84``,
 the core loop ``looped_blockell/looping/looped_model.py:293-350`` and the MLP path of
-``csrc/loop/persistent_core.cu:315-335``).  All L applications run in one
-persistent HIP launch (``titan::looped_swiglu``) that keeps each token tile's
-state on chip between iterations.
+``csrc/loop/persistent_core.cu:315-335``), one operator call
+(``titan::looped_swiglu``): the weights are packed once, the carried state is
+kept in fp32, and each application is a gate/up launch with the RMSNorm fused
+into its input stage followed by a down launch that adds into the state.
 """
 
 from __future__ import annotations

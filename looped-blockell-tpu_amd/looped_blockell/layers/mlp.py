@@ -99,11 +99,20 @@ class MLPBlock(nn.Module):
             self.fc2 = BlockELLLinear(d_model, d_ff, **kw)
 
     def swiglu_weights(self):
-        """(v_gate, ci_gate, v_up, ci_up, v_down, ci_down) in kernel form."""
-        out = []
-        for lin in (self.w_gate, self.w_up, self.w_down):
-            out += [lin.kernel_values(), lin.effective_col_indices()]
-        return tuple(out)
+        """(v_gate, ci_gate, v_up, ci_up, v_down, ci_down) in kernel form.
+
+        When gate and up have the same topology (as initialised: both are seeded from the
+        same hash, reference ``mlp.py:94``) the same index tensor is passed for both, which
+        lets the kernel read each activation tile once for the two products.  The comparison
+        runs once per topology version."""
+        cg, cu = self.w_gate.effective_col_indices(), self.w_up.effective_col_indices()
+        key = (self.w_gate._eff_cache[0], self.w_up._eff_cache[0])   # (pointer, version) of both
+        if getattr(self, "_shared_key", None) != key:
+            self._shared_key, self._shared = key, bool(torch.equal(cg, cu))
+        if self._shared:
+            cu = cg
+        return (self.w_gate.kernel_values(), cg, self.w_up.kernel_values(), cu,
+                self.w_down.kernel_values(), self.w_down.effective_col_indices())
 
     def forward(self, x: torch.Tensor, deterministic: bool = True) -> torch.Tensor:
         lead = x.shape[:-1]

@@ -126,6 +126,50 @@ def test_swiglu_duplicate_and_empty_columns(gpu, case, Kd):
     assert rel <= TOL, f"rel {rel} abs {ab}"
 
 
+@pytest.mark.parametrize("case", [(1024, 4096, 32, 4096 + 5), (512, 1024, 16, 300), (1024, 2048, 32, 70)])
+@pytest.mark.parametrize("intermediates", [False, True])
+def test_swiglu_shared_topology(gpu, case, intermediates):
+    """Gate and up passing one column-index buffer (the shared-topology gate/up kernel, one
+    panel read for both products) give the same bits as the same topology in two buffers,
+    and match the oracle; covers the intermediates and the looped block too."""
+    d_model, d_ff, B, N = case
+    _say(f"swiglu shared topology {case} intermediates={intermediates}")
+    rng = np.random.default_rng(23)
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25, sentinel_frac=0.1)
+    u = (u[0], g[1].copy())
+    x = T.act(rng, N, d_model)
+    xt = T.to_gpu_bf16(x)
+    gt, ut, dt = T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d)
+    shared_u = (ut[0], gt[1])                     # the same buffer as gate's indices
+    r_sep = T.abi_swiglu(xt, gt, ut, dt, add_residual=True, intermediates=intermediates)
+    r_sh = T.abi_swiglu(xt, gt, shared_u, dt, add_residual=True, intermediates=intermediates)
+    for a, b in zip(r_sep, r_sh):
+        if a is not None:
+            assert np.array_equal(T.to_np(a), T.to_np(b))
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref, *_ = O.swiglu_fwd(x.astype(np.float64), f64(g), f64(u), f64(d), add_residual=True)
+    rel, ab = T.rel_err(T.to_np(r_sh[0]), ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
+def test_looped_shared_topology(gpu):
+    """The looped block with gate and up sharing one index buffer equals the same topology in
+    two buffers, bit for bit."""
+    from looped_blockell import kernels
+    import torch
+    rng = np.random.default_rng(24)
+    d_model, d_ff, B, N = 1024, 4096, 32, 1000
+    _say("looped shared topology")
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25)
+    u = (u[0], g[1].copy())
+    gt, ut, dt = T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d)
+    h = T.to_gpu_bf16(T.act(rng, N, d_model))
+    scale = torch.ones(d_model, device="cuda")
+    a = kernels.looped_swiglu(h, scale, *gt, *ut, *dt, L=3)
+    b = kernels.looped_swiglu(h, scale, *gt, ut[0], gt[1], *dt, L=3)
+    assert np.array_equal(T.to_np(a), T.to_np(b))
+
+
 def test_swiglu_zero_k(gpu):
     """K = 0 everywhere: h == 0, so out == x (with the residual) / 0 (without)."""
     rng = np.random.default_rng(22)
