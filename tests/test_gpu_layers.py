@@ -9,6 +9,10 @@ import lbk_testlib as T
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
 TOL = 1e-2
 
 
@@ -161,3 +165,47 @@ def test_op_errors(gpu):
     assert int(bad) == 2
     empty = kernels.block_ell_matmul(torch.zeros(0, 64, device="cuda", dtype=torch.bfloat16), v, c)
     assert empty.shape == (0, 64)
+
+
+@pytest.mark.parametrize("shape", ["decode", "split", "ternary"])
+def test_graph_capture_replays(gpu, shape):
+    """The forward operators captured into a HIP graph: every replay (with eager work and a
+    synchronisation between replays) matches the eager result bit for bit.  No forward path
+    records a memset node: the kernels clear nothing through hipMemsetAsync."""
+    import torch
+    from looped_blockell import kernels
+    _say(f"graph capture {shape}")
+    rng = np.random.default_rng(40)
+    if shape == "ternary":
+        d_model, d_ff, B, N = 512, 2048, 64, 200
+        def tw(R, C_, K):
+            t = rng.integers(-1, 2, size=(R, K, B, B)).astype(np.int8)
+            s = (rng.random((R, K)) * 0.01 + 0.01).astype(np.float32)
+            col = O.random_topology(R, C_, K, rng)
+            return (T.to_gpu(O.pack_ternary(t).view(np.int32)), T.to_gpu(s), T.to_gpu(col.astype(np.int32)))
+        g, u, d = tw(d_ff // B, d_model // B, 2), tw(d_ff // B, d_model // B, 2), tw(d_model // B, d_ff // B, 4)
+        x = T.to_gpu_bf16(T.act(rng, N, d_model))
+        xq, sx = kernels.quantize_act_int8(x)
+        fn = lambda: kernels.ternary_swiglu_fwd(xq, sx, g, u, d, x)
+    else:
+        d_model, d_ff, B, N = (1024, 4096, 64, 16) if shape == "decode" else (512, 2048, 32, 300)
+        g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.125 if shape == "decode" else 0.25)
+        gt, ut, dt = T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d)
+        x = T.to_gpu_bf16(T.act(rng, N, d_model))
+        fn = lambda: kernels.swiglu_fwd(x, *gt, *ut, *dt, add_residual=True)
+    ref = fn().clone()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()                                   # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = fn()
+    junk = torch.empty(1 << 20, device="cuda")
+    for rep in range(4):
+        junk.normal_()                         # eager work between the replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), f"replay {rep} differs"
