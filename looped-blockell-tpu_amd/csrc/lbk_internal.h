@@ -68,6 +68,7 @@ struct DNArgs {
   const uint16_t* resid;    // optional bf16 residual [N, d_model]
   float* state;             // optional fp32 state [N, d_model]: read as residual, written back
   uint16_t* out;            // optional bf16 output [N, d_model]
+  int nrg;                  // row groups per token block (set by the launcher)
 };
 bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd);
 int launch_gu(int B, bool norm, const GUArgs& a, hipStream_t st);

@@ -11,9 +11,11 @@
 // tile), so the compiler's memory-counter waits stay exact.  h = silu(g) * u is
 // stored as bf16 (and the pre-activations when INTER).
 //
-// dn_kernel<B, MT, RPW>: a workgroup owns 16*MT tokens and all d_model outputs;
-// wave w keeps RPW down block rows of fp32 accumulators in registers for the
-// whole kernel.  h is staged through LDS 256 columns at a time (double
+// dn_kernel<B, MT, RPW>: a workgroup owns 16*MT tokens and a group of 8*RPW
+// down block rows (RPW = 1 as launched: wave w keeps the fp32 accumulators of
+// one row in registers for the whole kernel, two workgroups per CU).  The row
+// groups of one token block are dealt to one XCD, so the h tiles they all read
+// come from that XCD's L2 after the first group's miss.  h is staged through LDS 256 columns at a time (double
 // buffered, next stage's global loads in flight while the current one is
 // consumed).  Per stage each wave builds a flat list of its tiles (ballot over
 // its column-index rows, ds_permute into place), rows in order, each row's run
@@ -346,7 +348,7 @@ __device__ __forceinline__ int list_get(const int (&v)[4], int q) {
 }
 
 template <int RPW>
-__device__ __forceinline__ void dn_build(FetchList<RPW>& L, int c0, int ncb, const int (&colreg)[RPW], int w,
+__device__ __forceinline__ void dn_build(FetchList<RPW>& L, int c0, int ncb, const int (&colreg)[RPW], int wrow0,
                                          int Kd, int ztile, int lane) {
   int tot = 0;
 #pragma unroll
@@ -356,7 +358,7 @@ __device__ __forceinline__ void dn_build(FetchList<RPW>& L, int c0, int ncb, con
     const int cb = colreg[rho] - c0;
     const uint64_t m = __ballot(cb >= 0 && cb < ncb);
     const int cnt = __builtin_popcountll(m);
-    list_scatter(L.v, m, tot, (((w * RPW + rho) * Kd + lane) << 6) | (cb & 63), lane);
+    list_scatter(L.v, m, tot, (((wrow0 + rho) * Kd + lane) << 6) | (cb & 63), lane);
     if (cnt & 1) list_set(L.v, tot + cnt, ztile << 6, lane);
     L.pcnt[rho] = cnt + (cnt & 1);
     tot += L.pcnt[rho];
@@ -365,7 +367,7 @@ __device__ __forceinline__ void dn_build(FetchList<RPW>& L, int c0, int ncb, con
 }
 
 template <int B, int MT, int RPW>
-__global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
+__global__ __launch_bounds__(512, RPW == 1 ? 2 : 1) void dn_kernel(DNArgs a) {
   constexpr int CW = TileShape<B>::CW;
   constexpr int TM = 16 * MT;
   constexpr int G = DnStage<B>::G;
@@ -381,7 +383,18 @@ __global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
   const int lane = tid & 63;
   const int w = uniform(tid >> 6);
   const int i = lane & 15, g = lane >> 4;
-  const int64_t t0 = (int64_t)blockIdx.x * TM;
+  // workgroup -> (token block, row group).  With several row groups, the groups of one token
+  // block get workgroup ids that agree mod 8, i.e. one XCD (workgroups are dealt to the 8
+  // XCDs round robin), so the h stages every group reads come from that XCD's L2.
+  int tb = (int)blockIdx.x, rg = 0;
+  if (a.nrg > 1) {
+    const int b = (int)blockIdx.x, rest = b >> 3;
+    rg = rest % a.nrg;
+    tb = 8 * (rest / a.nrg) + (b & 7);
+  }
+  const int64_t t0 = (int64_t)tb * TM;
+  if (t0 >= a.N) return;   // the whole workgroup, before any barrier
+  const int row0 = rg * 8 * RPW;   // first down row of this workgroup
   const int d_model = a.d_model;
   const int64_t d_ff = a.d_ff;
   const int C = a.C_d;
@@ -392,7 +405,7 @@ __global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
   int colreg[RPW];
 #pragma unroll
   for (int rho = 0; rho < RPW; ++rho) {
-    const int rm = w * RPW + rho;
+    const int rm = row0 + w * RPW + rho;
     colreg[rho] = (rm < a.R_m && lane < a.Kd) ? a.cd[(int64_t)rm * a.Kd + lane] : -1;
   }
 
@@ -459,11 +472,11 @@ __global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
       for (int m = 0; m < CW; ++m) ac[mt][m] = mfma_bf16(av[mt], S.f[0][m], ac[mt][m]);
   };
 
-  const bool any_rows = (w * RPW < a.R_m) && a.Kd > 0;
+  const bool any_rows = (row0 + w * RPW < a.R_m) && a.Kd > 0;
   Slot S0, S1;
   nxt.tot = 0;
-  dn_build<RPW>(cur, 0, (C < G ? C : G), colreg, w, a.Kd, ztile, lane);
-  if (nstages > 1) dn_build<RPW>(nxt, G, (C - G) < G ? (C - G) : G, colreg, w, a.Kd, ztile, lane);
+  dn_build<RPW>(cur, 0, (C < G ? C : G), colreg, row0 + w * RPW, a.Kd, ztile, lane);
+  if (nstages > 1) dn_build<RPW>(nxt, G, (C - G) < G ? (C - G) : G, colreg, row0 + w * RPW, a.Kd, ztile, lane);
   stage_fetch(0);
   stage_store(0);
   bool ring_ok = false;   // S0/S1 hold positions 0 and 1 of the current stage
@@ -501,7 +514,7 @@ __global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
     nxt.tot = 0;
     if (s + 2 < nstages) {
       const int c2 = (s + 2) * G;
-      dn_build<RPW>(nxt, c2, (C - c2) < G ? (C - c2) : G, colreg, w, a.Kd, ztile, lane);
+      dn_build<RPW>(nxt, c2, (C - c2) < G ? (C - c2) : G, colreg, row0 + w * RPW, a.Kd, ztile, lane);
     }
     __syncthreads();
   }
@@ -509,7 +522,7 @@ __global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
   // ---- epilogue: + residual (bf16) or + fp32 state; store bf16 (and the state)
 #pragma unroll
   for (int rho = 0; rho < RPW; ++rho) {
-    const int rm = w * RPW + rho;
+    const int rm = row0 + w * RPW + rho;
     if (rm >= a.R_m) continue;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -539,22 +552,24 @@ __global__ __launch_bounds__(512, 1) void dn_kernel(DNArgs a) {
 }
 
 // state <- float(x), fp32 copy of a bf16 tensor
+// 8 elements per thread (one 16-byte load, two 16-byte stores) when x and y are 16-byte
+// aligned; the last partial group element by element
 __global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t* __restrict__ x, int64_t n,
                                                           float* __restrict__ y) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx < n) y[idx] = bf2f(x[idx]);
+  const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (e0 + 8 <= n) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(x + e0);
+    *reinterpret_cast<f32x4*>(y + e0) = f32x4{bf_lo(v[0]), bf_hi(v[0]), bf_lo(v[1]), bf_hi(v[1])};
+    *reinterpret_cast<f32x4*>(y + e0 + 4) = f32x4{bf_lo(v[2]), bf_hi(v[2]), bf_lo(v[3]), bf_hi(v[3])};
+  } else {
+    for (int64_t e = e0; e < n; ++e) y[e] = bf2f(x[e]);
+  }
 }
 
 // ===========================================================================
 // host side
 // ===========================================================================
 static int gu_mt(int d_model) { return d_model <= 1024 ? 4 : (d_model <= 2048 ? 2 : 0); }
-
-static int dn_rpw(int R_m) {
-  for (int rpw : {1, 2, 4})
-    if (8 * rpw >= R_m) return rpw;
-  return -1;
-}
 
 static size_t gu_lds(int R_ff, int K, int mt) {
   return (size_t)16 * mt * (8192 / mt) + (size_t)R_ff * K * 8;   // panel (128 KB) + column table
@@ -567,7 +582,7 @@ bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int 
   if (d_model % 128) return false;                    // swizzled panel rows
   const int mt = gu_mt(d_model);
   if (mt == 0 || gu_lds(R_ff, Kg, mt) > 163840) return false;
-  if (R_m * B != d_model || dn_rpw(R_m) < 0) return false;
+  if (R_m < 1 || R_m * B != d_model) return false;
   if ((R_ff * B) % 8) return false;
   return true;
 }
@@ -609,25 +624,29 @@ int launch_gu(int B, bool norm, const GUArgs& a, hipStream_t st) {
 }
 
 template <int B, int MT, int RPW>
-static int launch_dn_t(const DNArgs& a, hipStream_t st) {
+static int launch_dn_t(const DNArgs& a0, hipStream_t st) {
   const int TM = 16 * MT;
-  hipLaunchKernelGGL((dn_kernel<B, MT, RPW>), dim3((unsigned)((a.N + TM - 1) / TM)), dim3(512), 0, st, a);
+  DNArgs a = a0;
+  const int64_t ntb = (a.N + TM - 1) / TM;
+  a.nrg = (a.R_m + 8 * RPW - 1) / (8 * RPW);
+  const int64_t grid = a.nrg == 1 ? ntb : 8 * a.nrg * ((ntb + 7) / 8);
+  hipLaunchKernelGGL((dn_kernel<B, MT, RPW>), dim3((unsigned)grid), dim3(512), 0, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// One down row per wave (a workgroup covers 8 rows; the row groups of one token block share
+// an XCD): few accumulator registers per wave, two workgroups per CU.
 int launch_dn(int B, const DNArgs& a, hipStream_t st) {
   if (a.N == 0) return 0;
-  const int rpw = dn_rpw(a.R_m);
-#define LBK_DN(BB, RR)                                                   \
-  if (B == BB && rpw == RR) return launch_dn_t<BB, 4, RR>(a, st);
-  LBK_DN(16, 1) LBK_DN(16, 2) LBK_DN(16, 4) LBK_DN(32, 1) LBK_DN(32, 2) LBK_DN(32, 4)
-#undef LBK_DN
+  if (B == 16) return launch_dn_t<16, 4, 1>(a, st);
+  if (B == 32) return launch_dn_t<32, 4, 1>(a, st);
   return -2;
 }
 
 int launch_bf16_to_f32(const uint16_t* x, int64_t n, float* y, hipStream_t st) {
   if (n == 0) return 0;
-  hipLaunchKernelGGL(bf16_to_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, n, y);
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(y) & 15)) return -2;
+  hipLaunchKernelGGL(bf16_to_f32_kernel, dim3((unsigned)((n + 2047) / 2048)), dim3(256), 0, st, x, n, y);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -65,7 +65,8 @@ SWIGLU_CASES = [
     (512, 1024, 32, 0.25, 130, 0.0),
     (1024, 4096, 32, 0.25, 200, 0.05),    # config-2 geometry, small N
     (128, 512, 64, 0.5, 70, 0.0),         # B = 64 -> general two-kernel path
-    (2048, 1024, 32, 0.125, 40, 0.0),     # d_model > 1024 -> general path
+    (2048, 1024, 32, 0.125, 40, 0.0),     # d_model > 1024: 32-token gate/up panels, 64 down rows
+    (2048, 2048, 16, 0.125, 100, 0.05),   # 128 down rows: 16 row groups per token block
 ]
 
 
@@ -215,6 +216,7 @@ LOOP_CASES = [
     (256, 1024, 16, 0.25, 100, 3),
     (1024, 4096, 32, 0.25, 130, 8),       # config-4 geometry
     (128, 512, 64, 0.5, 40, 2),           # general path (per-iteration launches)
+    (2048, 2048, 32, 0.125, 70, 2),       # 64 down rows: 8 row groups per token block
 ]
 
 
@@ -266,7 +268,7 @@ def test_looped_L0_and_L1(gpu):
 
 
 DECODE_CASES = [
-    # (d_model, d_ff, B, density, N, sentinel_frac)   N <= 16: the single-launch decode kernel
+    # (d_model, d_ff, B, density, N, sentinel_frac)   N <= 16: the decode kernels
     # (at most 24 down slots per row)
     (256, 1024, 16, 0.25, 16, 0.0),
     (512, 1024, 32, 0.25, 5, 0.1),
