@@ -162,7 +162,7 @@ static int pack_ffn(const lbk_bell* gate, const lbk_bell* up, const lbk_bell* do
   for (int t = 0; t < 3; ++t) {
     const int64_t nt = (int64_t)ws3[t]->R * ws3[t]->K;
     *dst[t] = p;
-    jobs[t] = PackJob{ws3[t]->values, ws3[t]->col_idx, nt, cols[t], reinterpret_cast<uint32_t*>(p), 0};
+    jobs[t] = PackJob{ws3[t]->values, ws3[t]->col_idx, nt, cols[t], reinterpret_cast<uint32_t*>(p), 0, t < 2};
     p += align256(packed_bf16_bytes(nt, B));
   }
   out->bytes = (size_t)(p - ws);

@@ -200,7 +200,7 @@ int launch_injection(const uint16_t* h, const uint16_t* e, const float* log_A, c
 template <int B>
 __device__ __forceinline__ void pack_bf16_dword(const uint16_t* __restrict__ values, const int32_t* __restrict__ col,
                                                 int64_t ntiles, int C, int64_t ndw, uint32_t* __restrict__ packed,
-                                                int64_t idx) {
+                                                int64_t idx, int gu_layout) {
   constexpr int CW = TileShape<B>::CW;
   constexpr int PER_TILE = PackedTile<B>::U32X4 * 4;   // dwords per packed tile
   if (idx >= ndw) return;
@@ -218,7 +218,10 @@ __device__ __forceinline__ void pack_bf16_dword(const uint16_t* __restrict__ val
   const int m = r % CW;
   const int ks = r / CW;
   const int j = l & 15, g = l >> 4;
-  const int k = 32 * ks + 8 * g + 2 * u, c = CW * j + m;
+  const int k = 32 * ks + 8 * g + 2 * u;
+  // gate/up layout (B = 32): column 8 (j / 4) + 4 m + j % 4, so that the product with the
+  // tile as the A operand leaves 8 consecutive columns of one token in each lane
+  const int c = (B == 32 && gu_layout) ? 8 * (j >> 2) + 4 * m + (j & 3) : CW * j + m;
   const uint16_t* w = values + tile * B * B;
   packed[idx] = (uint32_t)w[k * B + c] | ((uint32_t)w[(k + 1) * B + c] << 16);
 }
@@ -227,7 +230,7 @@ template <int B>
 __global__ __launch_bounds__(256) void pack_bf16_kernel(const uint16_t* __restrict__ values,
                                                         const int32_t* __restrict__ col, int64_t ntiles, int C,
                                                         int64_t ndw, uint32_t* __restrict__ packed) {
-  pack_bf16_dword<B>(values, col, ntiles, C, ndw, packed, (int64_t)blockIdx.x * 256 + threadIdx.x);
+  pack_bf16_dword<B>(values, col, ntiles, C, ndw, packed, (int64_t)blockIdx.x * 256 + threadIdx.x, 0);
 }
 
 // several weights in one launch: workgroups [first[t], first[t + 1]) pack weight t
@@ -239,7 +242,7 @@ __global__ __launch_bounds__(256) void pack_bf16_multi_kernel(PackJobs jobs) {
     if (u < jobs.n && (int64_t)blockIdx.x >= jobs.first[u]) t = u;
   const PackJob& J = jobs.job[t];
   pack_bf16_dword<B>(J.values, J.col, J.ntiles, J.C, J.ndw, J.packed,
-                     ((int64_t)blockIdx.x - jobs.first[t]) * 256 + threadIdx.x);
+                     ((int64_t)blockIdx.x - jobs.first[t]) * 256 + threadIdx.x, J.gu_layout);
 }
 
 size_t packed_bf16_bytes(int64_t ntiles, int B) {

@@ -152,7 +152,8 @@ __device__ __forceinline__ void wraw_to_frag<64>(const WRaw<64>& r, u32x4 (&f)[2
 // transposition is needed.  For B = 16 only lanes 0..31 are stored (512 bytes
 // per tile); lanes 32..63 read lanes 0..31 (their A operand is zero).
 // Dword u of chunk (ks, m) of lane (j = l%16, g = l/16) is
-//   W[k][c] | W[k+1][c] << 16,  k = 32*ks + 8*g + 2*u,  c = CW*j + m.
+//   W[k][c] | W[k+1][c] << 16,  k = 32*ks + 8*g + 2*u,  c = CW*j + m
+// (gate/up tiles for B = 32: c = 8*(j/4) + 4*m + j%4, see the gate/up kernel).
 // ---------------------------------------------------------------------------
 template <int B>
 struct PackedTile {

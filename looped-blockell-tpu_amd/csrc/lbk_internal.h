@@ -32,6 +32,7 @@ size_t packed_bf16_bytes(int64_t ntiles, int B);   // includes the appended zero
 // up to three weights packed by one launch (ndw is filled in by the launcher)
 struct PackJob {
   const uint16_t* values; const int32_t* col; int64_t ntiles; int C; uint32_t* packed; int64_t ndw;
+  int gu_layout;   // 1: column order of the gate/up kernel's swapped product (B = 32)
 };
 struct PackJobs {
   static constexpr int kMax = 3;

@@ -5,7 +5,9 @@
 // from an fp32 state), next to a table of the gate/up column indices.  Eight
 // waves (two per SIMD) each stream their own d_ff block rows (r = w, w+8, ...):
 // gate and up tiles are consumed in (gate k, up k) pairs from a GU_RING-deep
-// register ring that runs across row boundaries.  Weights come pre-packed in
+// register ring that runs across row boundaries.  The weight tile is the A
+// operand of the MFMA, so the accumulators hold h transposed and every lane
+// stores 8 (B = 32) or 4 (B = 16) consecutive columns of one token at once.  Weights come pre-packed in
 // fragment-major order (two dwordx4 loads per lane per B = 32 tile); every
 // position issues the same loads (padding and dead slots read the packed zero
 // tile), so the compiler's memory-counter waits stay exact.  h = silu(g) * u is
@@ -39,6 +41,18 @@ __device__ __forceinline__ u32x4 lds16(const unsigned char* base, uint32_t off) 
 // ROWB apart and fit the ds_read immediate offset), and 16-byte chunk c of it
 // at chunk c ^ i (i = row & 15), which keeps the eight lanes of one LDS read
 // phase on distinct banks.
+// store NV (4 or 8) consecutive bf16 values with one 8- or 16-byte store
+template <int NV>
+__device__ __forceinline__ void store_bf16x(uint16_t* p, const float (&v)[NV]) {
+  if constexpr (NV == 8) {
+    *reinterpret_cast<u32x4*>(p) = u32x4{pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]), pack2_bf16(v[4], v[5]),
+                                         pack2_bf16(v[6], v[7])};
+  } else {
+    static_assert(NV == 4, "4 or 8 values");
+    *reinterpret_cast<u32x2*>(p) = u32x2{pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3])};
+  }
+}
+
 template <int MT>
 __device__ __forceinline__ uint32_t panel_addr(int row, int chunk, int rowb) {
   const int i = row & 15, mt = row >> 4;
@@ -55,6 +69,8 @@ struct GUSlot {
 
 // gate/up ring depth (positions in flight + 1)
 constexpr int GU_RING = 4;
+// column-table entries per thread (R_ff * K <= 512 * GU_CT_MAX)
+constexpr int GU_CT_MAX = 8;
 
 // gate/up panel row stride: 2048 bytes (MT = 4, d_model <= 1024) or 4096 (MT = 2)
 template <int MT>
@@ -80,13 +96,28 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
   // column table after the panel: (gate col, up col) per (row, slot); dead -> 0
   int2* ctab = reinterpret_cast<int2*>(smem + (size_t)TM * ROWB);
 
-  // ---- column table
-  for (int e = tid; e < a.R_ff * K; e += 512) {
-    int cg = a.cg[e], cu = a.cu[e];
-    cg = (cg >= 0 && cg < cin) ? cg : 0;
-    cu = (cu >= 0 && cu < cin) ? cu : 0;
-    ctab[e] = make_int2(cg, cu);
-  }
+  // ---- column table (at most GU_CT_MAX entries per thread): loads at clamped addresses,
+  // all issued with the panel loads, stored after them
+  const int nct = a.R_ff * K;
+  int2 ctv[GU_CT_MAX];
+  auto ctab_fetch = [&]() {
+#pragma unroll
+    for (int u = 0; u < GU_CT_MAX; ++u) {
+      const int e = tid + 512 * u;
+      const int ec = e < nct ? e : 0;
+      ctv[u] = make_int2(a.cg[ec], a.cu[ec]);
+    }
+  };
+  auto ctab_store = [&]() {
+#pragma unroll
+    for (int u = 0; u < GU_CT_MAX; ++u) {
+      const int e = tid + 512 * u;
+      int cg = ctv[u].x, cu = ctv[u].y;
+      cg = (cg >= 0 && cg < cin) ? cg : 0;
+      cu = (cu >= 0 && cu < cin) ? cu : 0;
+      if (e < nct) ctab[e] = make_int2(cg, cu);
+    }
+  };
 
   // ---- stream this wave's rows r = w + 8n through a GU_RING-slot ring of
   // (gate, up) tile pairs.  Each row takes KP positions, K rounded up to a
@@ -140,26 +171,33 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
   };
 
   f32x4 ag[MT][CW], au[MT][CW];
-  auto compute = [&](const GUSlot<B>& S) {
+  // A fragments of a position's gate and up column blocks (shared topology: gate and up
+  // read the same column list, so one panel read feeds both products)
+  struct AFrags {
+    u32x4 g[MT], u[SHARED ? 1 : MT];
+  };
+  auto load_a = [&](const GUSlot<B>& S, AFrags& A) {
     const int cg = uniform(S.cg), cu = uniform(S.cu);
     const uint32_t ag0 = lbase + (((cg * (B / 8) + g) ^ i) << 4);
     const uint32_t au0 = lbase + (((cu * (B / 8) + g) ^ i) << 4);
-    u32x4 avg[MT], avu[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      avg[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(smem, ag0 + mt * ROWB);
-      // shared topology (gate and up read the same column list): one panel read feeds both
-      if constexpr (SHARED) avu[mt] = avg[mt];
-      else avu[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(smem, au0 + mt * ROWB);
+      A.g[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(smem, ag0 + mt * ROWB);
+      if constexpr (!SHARED) A.u[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(smem, au0 + mt * ROWB);
     }
+  };
+  // The weight tile is the A operand and the panel rows the B operand, so an accumulator
+  // holds h transposed: lane (n, g) of ag[mt][m] has token 16 mt + n and h columns
+  // 8 g + 4 m + v (B = 32, with the gate/up tile packing) or 4 g + v (B = 16), v < 4.
+  auto compute = [&](const GUSlot<B>& S, const AFrags& A) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int m = 0; m < CW; ++m) ag[mt][m] = mfma_bf16(avg[mt], S.g[0][m], ag[mt][m]);
+      for (int m = 0; m < CW; ++m) ag[mt][m] = mfma_bf16(S.g[0][m], A.g[mt], ag[mt][m]);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int m = 0; m < CW; ++m) au[mt][m] = mfma_bf16(avu[mt], S.u[0][m], au[mt][m]);
+      for (int m = 0; m < CW; ++m) au[mt][m] = mfma_bf16(S.u[0][m], SHARED ? A.g[mt] : A.u[mt], au[mt][m]);
   };
 
   // ---- input panel: all of this thread's loads are issued before any store,
@@ -168,21 +206,26 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
     constexpr int CPR = ROWB / 16;                 // chunk capacity of a panel row
     constexpr int PIT = TM * CPR / 512;            // chunks per thread
     const int cpr = d_model / 8;
+    // every load at a clamped address (row t0, chunk 0 stand in for the padding), so no
+    // load sits under a branch and the waits before the stores stay exact
     u32x4 pv[PIT];
 #pragma unroll
     for (int it = 0; it < PIT; ++it) {
       const int e = tid + 512 * it;
       const int row = e / CPR, cc = e % CPR;
       const int64_t t = t0 + row;
-      pv[it] = u32x4{0, 0, 0, 0};
-      if (cc < cpr && t < a.N) pv[it] = *reinterpret_cast<const u32x4*>(a.x + t * d_model + 8 * cc);
+      const bool ok = cc < cpr && t < a.N;
+      pv[it] = *reinterpret_cast<const u32x4*>(a.x + (ok ? t : t0) * d_model + 8 * (ok ? cc : 0));
     }
+    ctab_fetch();
     if (nrows > 0) prefetch_ring();
+    ctab_store();
 #pragma unroll
     for (int it = 0; it < PIT; ++it) {
       const int e = tid + 512 * it;
       const int row = e / CPR, cc = e % CPR;
-      if (cc < cpr) *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, cc, ROWB)) = pv[it];
+      const bool ok = cc < cpr && t0 + row < a.N;
+      if (cc < cpr) *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, cc, ROWB)) = ok ? pv[it] : u32x4{0, 0, 0, 0};
     }
   } else {
     // fp32 state rows -> RMSNorm -> bf16 panel; wave w owns rows w, w+8, ...;
@@ -196,15 +239,27 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
 #pragma unroll
       for (int j = 0; j < SPR; ++j) {
         const int col = 8 * lane + 512 * j;
-        xv[rr][j][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-        xv[rr][j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (col < d_model && t < a.N) {
-          xv[rr][j][0] = *reinterpret_cast<const f32x4*>(a.xf + t * d_model + col);
-          xv[rr][j][1] = *reinterpret_cast<const f32x4*>(a.xf + t * d_model + col + 4);
-        }
+        // clamped address (row t0, column 0) for padding, zeroed after the load
+        const bool ok = col < d_model && t < a.N;
+        const float* src = a.xf + (ok ? t : t0) * d_model + (ok ? col : 0);
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(src);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + 4);
+        xv[rr][j][0] = ok ? v0 : f32x4{0.f, 0.f, 0.f, 0.f};
+        xv[rr][j][1] = ok ? v1 : f32x4{0.f, 0.f, 0.f, 0.f};
       }
     }
+    // the norm scale of this lane's columns, loaded once for all rows
+    f32x4 sc[SPR][2];
+#pragma unroll
+    for (int j = 0; j < SPR; ++j) {
+      const int col = 8 * lane + 512 * j;
+      const float* src = a.norm_scale + (col < d_model ? col : 0);
+      sc[j][0] = *reinterpret_cast<const f32x4*>(src);
+      sc[j][1] = *reinterpret_cast<const f32x4*>(src + 4);
+    }
+    ctab_fetch();
     if (nrows > 0) prefetch_ring();
+    ctab_store();
 #pragma unroll
     for (int rr = 0; rr < RW; ++rr) {
       const int row = w + 8 * rr;
@@ -221,16 +276,15 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
 #pragma unroll
       for (int j = 0; j < SPR; ++j) {
         const int col = 8 * lane + 512 * j;
-        if (col < d_model) {
-          const f32x4 s0 = *reinterpret_cast<const f32x4*>(a.norm_scale + col);
-          const f32x4 s1 = *reinterpret_cast<const f32x4*>(a.norm_scale + col + 4);
-          const f32x4 v0 = xv[rr][j][0], v1 = xv[rr][j][1];
-          const u32x4 o = {pack2_bf16(v0[0] * rs * s0[0], v0[1] * rs * s0[1]),
-                           pack2_bf16(v0[2] * rs * s0[2], v0[3] * rs * s0[3]),
-                           pack2_bf16(v1[0] * rs * s1[0], v1[1] * rs * s1[1]),
-                           pack2_bf16(v1[2] * rs * s1[2], v1[3] * rs * s1[3])};
-          *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, col / 8, ROWB)) = o;
-        }
+        // col < ROWB / 2 always: the padding columns of the panel row get zeros (no branch)
+        const f32x4 s0 = sc[j][0], s1 = sc[j][1];
+        const f32x4 v0 = xv[rr][j][0], v1 = xv[rr][j][1];
+        const u32x4 o = {pack2_bf16(v0[0] * rs * s0[0], v0[1] * rs * s0[1]),
+                         pack2_bf16(v0[2] * rs * s0[2], v0[3] * rs * s0[3]),
+                         pack2_bf16(v1[0] * rs * s1[0], v1[1] * rs * s1[1]),
+                         pack2_bf16(v1[2] * rs * s1[2], v1[3] * rs * s1[3])};
+        *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, col / 8, ROWB)) =
+            col < d_model ? o : u32x4{0, 0, 0, 0};
       }
     }
   }
@@ -239,6 +293,12 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
 #pragma unroll
   for (int sl = 0; sl < GU_RING; ++sl) fetch_c(P[sl]);
 
+  // The A fragments of position p + 1 are read from the panel while position p's MFMAs
+  // run (two register sets, alternating with the slot parity; GU_RING is even), so the
+  // LDS latency stays off the MFMA chain.
+  static_assert(GU_RING % 2 == 0, "A-fragment double buffer alternates with the slot parity");
+  AFrags A0, A1;
+  load_a(P[0], A0);
   __builtin_amdgcn_sched_barrier(0);
   for (int n = 0; n < nrows; ++n) {
 #pragma unroll
@@ -253,34 +313,41 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
     for (int k = 0; k < KP; k += GU_RING) {
 #pragma unroll
       for (int sl = 0; sl < GU_RING; ++sl) {
-        compute(P[sl]);
+        if (sl % 2 == 0) {
+          load_a(P[(sl + 1) % GU_RING], A1);
+          compute(P[sl], A0);
+        } else {
+          load_a(P[(sl + 1) % GU_RING], A0);
+          compute(P[sl], A1);
+        }
         fetch(P[sl]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // epilogue of row r: h = silu(g) * u (and the pre-activations)
+    // epilogue of row r: h = silu(g) * u (and the pre-activations); each lane stores the
+    // 4 * CW consecutive columns it holds of one token with one store
     const int r = w + 8 * n;
-    const int64_t col0 = (int64_t)r * B + CW * i;
+    const int64_t col0 = (int64_t)r * B + 4 * CW * g;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MT; ++mt) {
+      const int64_t t = t0 + 16 * mt + i;
+      float o[4 * CW], gv[4 * CW], uv[4 * CW];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int64_t t = t0 + 16 * mt + 4 * g + v;
-        float o[CW], gv[CW], uv[CW];
+      for (int m = 0; m < CW; ++m)
 #pragma unroll
-        for (int m = 0; m < CW; ++m) {
-          gv[m] = ag[mt][m][v];
-          uv[m] = au[mt][m][v];
-          o[m] = silu_f(gv[m]) * uv[m];
+        for (int v = 0; v < 4; ++v) {
+          gv[4 * m + v] = ag[mt][m][v];
+          uv[4 * m + v] = au[mt][m][v];
+          o[4 * m + v] = silu_f(gv[4 * m + v]) * uv[4 * m + v];
         }
-        if (t < a.N) {
-          store_bf16<CW>(a.h + t * d_ff + col0, o);
-          if constexpr (INTER) {
-            if (a.gpre) store_bf16<CW>(a.gpre + t * d_ff + col0, gv);
-            if (a.uout) store_bf16<CW>(a.uout + t * d_ff + col0, uv);
-          }
+      if (t < a.N) {
+        store_bf16x<4 * CW>(a.h + t * d_ff + col0, o);
+        if constexpr (INTER) {
+          if (a.gpre) store_bf16x<4 * CW>(a.gpre + t * d_ff + col0, gv);
+          if (a.uout) store_bf16x<4 * CW>(a.uout + t * d_ff + col0, uv);
         }
       }
+    }
   }
 }
 
@@ -581,7 +648,7 @@ bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int 
   if (Kd > 63) return false;                          // one lane per slot; <= 4 * 64 hit-list entries
   if (d_model % 128) return false;                    // swizzled panel rows
   const int mt = gu_mt(d_model);
-  if (mt == 0 || gu_lds(R_ff, Kg, mt) > 163840) return false;
+  if (mt == 0 || gu_lds(R_ff, Kg, mt) > 163840 || (int64_t)R_ff * Kg > 512 * GU_CT_MAX) return false;
   if (R_m < 1 || R_m * B != d_model) return false;
   if ((R_ff * B) % 8) return false;
   return true;
