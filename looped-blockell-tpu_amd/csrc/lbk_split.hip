@@ -13,13 +13,13 @@
 // tile), so the compiler's memory-counter waits stay exact.  h = silu(g) * u is
 // stored as bf16 (and the pre-activations when INTER).
 //
-// dn_kernel<B, MT, RPW>: a workgroup owns 16*MT tokens and a group of 8*RPW
-// down block rows (RPW = 1 as launched: wave w keeps the fp32 accumulators of
-// one row in registers for the whole kernel, two workgroups per CU).  The row
+// dn_kernel<B, MT, RPW>: a workgroup of DN_WAVES = 16 waves owns 16*MT tokens
+// and a group of 16*RPW down block rows (RPW = 1 as launched: wave w keeps the
+// fp32 accumulators of one row in registers for the whole kernel).  The row
 // groups of one token block are dealt to one XCD, so the h tiles they all read
-// come from that XCD's L2 after the first group's miss.  h is staged through LDS 256 columns at a time (double
-// buffered, next stage's global loads in flight while the current one is
-// consumed).  Per stage each wave builds a flat list of its tiles (ballot over
+// come from that XCD's L2 after the first group's miss.  h is staged through
+// LDS 512 columns at a time (double buffered, next stage's global loads in
+// flight while the current one is consumed).  Per stage each wave builds a flat list of its tiles (ballot over
 // its column-index rows, ds_permute into place), rows in order, each row's run
 // padded to an even length with a zero-tile entry, and streams it through a
 // two-slot ring that also prefetches the next stage's first tiles.  The
@@ -355,8 +355,12 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
 // down
 // ===========================================================================
 // h column blocks per LDS stage: 512 bytes of each token row (32 chunks)
+// down kernel shape: DN_WAVES waves (one down row each) per workgroup; a stage holds
+// DN_STAGE_COLS h columns of the workgroup's tokens
+constexpr int DN_WAVES = 16;
+constexpr int DN_STAGE_COLS = 512;
 template <int B>
-struct DnStage { static constexpr int G = 256 / B; };
+struct DnStage { static constexpr int G = DN_STAGE_COLS / B; };
 
 // Per-wave fetch list of one stage: position q (lane q % 64 of v[q / 64]) holds
 // desc = tile << 6 | cb -- the packed down tile (row * Kd + slot) and its column
@@ -434,17 +438,18 @@ __device__ __forceinline__ void dn_build(FetchList<RPW>& L, int c0, int ncb, con
 }
 
 template <int B, int MT, int RPW>
-__global__ __launch_bounds__(512, RPW == 1 ? 2 : 1) void dn_kernel(DNArgs a) {
+__global__ __launch_bounds__(64 * DN_WAVES, (RPW == 1 && DN_WAVES == 8) ? 2 : 1) void dn_kernel(DNArgs a) {
   constexpr int CW = TileShape<B>::CW;
   constexpr int TM = 16 * MT;
   constexpr int G = DnStage<B>::G;
   constexpr int SROWB = G * B * 2;                   // bytes per token row of a stage (512)
   constexpr int SBYTES = TM * SROWB;                 // bytes per stage
   constexpr int CHUNKS = SBYTES / 16;                // 16-byte chunks per stage
-  constexpr int PER_T = (CHUNKS + 511) / 512;        // chunks per thread per stage
+  constexpr int NT = 64 * DN_WAVES;                  // threads
+  constexpr int PER_T = (CHUNKS + NT - 1) / NT;      // chunks per thread per stage
   static_assert(TileShape<B>::NKS == 1, "down kernel handles B <= 32");
   static_assert(SROWB % 256 == 0, "stage rows must cover multiples of 16 chunks");
-  __shared__ __attribute__((aligned(16))) unsigned char stages[2][SBYTES];
+  extern __shared__ __attribute__((aligned(16))) unsigned char dn_smem[];   // two stages of SBYTES
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -461,7 +466,7 @@ __global__ __launch_bounds__(512, RPW == 1 ? 2 : 1) void dn_kernel(DNArgs a) {
   }
   const int64_t t0 = (int64_t)tb * TM;
   if (t0 >= a.N) return;   // the whole workgroup, before any barrier
-  const int row0 = rg * 8 * RPW;   // first down row of this workgroup
+  const int row0 = rg * DN_WAVES * RPW;   // first down row of this workgroup
   const int d_model = a.d_model;
   const int64_t d_ff = a.d_ff;
   const int C = a.C_d;
@@ -489,7 +494,7 @@ __global__ __launch_bounds__(512, RPW == 1 ? 2 : 1) void dn_kernel(DNArgs a) {
   auto stage_fetch = [&](int s) {
 #pragma unroll
     for (int u = 0; u < PER_T; ++u) {
-      const int e = tid + 512 * u;
+      const int e = tid + NT * u;
       sreg[u] = u32x4{0, 0, 0, 0};
       if (e < CHUNKS) {
         const int row = e / (SROWB / 16), c = e - row * (SROWB / 16);
@@ -502,10 +507,10 @@ __global__ __launch_bounds__(512, RPW == 1 ? 2 : 1) void dn_kernel(DNArgs a) {
   auto stage_store = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < PER_T; ++u) {
-      const int e = tid + 512 * u;
+      const int e = tid + NT * u;
       if (e < CHUNKS) {
         const int row = e / (SROWB / 16), c = e - row * (SROWB / 16);
-        *reinterpret_cast<u32x4*>(&stages[buf][0] + panel_addr<MT>(row, c, SROWB)) = sreg[u];
+        *reinterpret_cast<u32x4*>(dn_smem + buf * SBYTES + panel_addr<MT>(row, c, SROWB)) = sreg[u];
       }
     }
   };
@@ -550,7 +555,7 @@ __global__ __launch_bounds__(512, RPW == 1 ? 2 : 1) void dn_kernel(DNArgs a) {
   __syncthreads();
   for (int s = 0; s < nstages; ++s) {
     const int buf = s & 1;
-    const unsigned char* sb = &stages[buf][0];
+    const unsigned char* sb = dn_smem + buf * SBYTES;
     if (s + 1 < nstages) stage_fetch(s + 1);
     if (any_rows && cur.tot > 0) {
       if (!ring_ok) {
@@ -693,16 +698,21 @@ int launch_gu(int B, bool norm, const GUArgs& a, hipStream_t st) {
 template <int B, int MT, int RPW>
 static int launch_dn_t(const DNArgs& a0, hipStream_t st) {
   const int TM = 16 * MT;
+  constexpr size_t lds = 2 * (size_t)TM * DN_STAGE_COLS * 2;   // two stages
   DNArgs a = a0;
   const int64_t ntb = (a.N + TM - 1) / TM;
-  a.nrg = (a.R_m + 8 * RPW - 1) / (8 * RPW);
+  a.nrg = (a.R_m + DN_WAVES * RPW - 1) / (DN_WAVES * RPW);
   const int64_t grid = a.nrg == 1 ? ntb : 8 * a.nrg * ((ntb + 7) / 8);
-  hipLaunchKernelGGL((dn_kernel<B, MT, RPW>), dim3((unsigned)grid), dim3(512), 0, st, a);
+  auto kern = dn_kernel<B, MT, RPW>;
+  if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return -1;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * DN_WAVES), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// One down row per wave (a workgroup covers 8 rows; the row groups of one token block share
-// an XCD): few accumulator registers per wave, two workgroups per CU.
+// One down row per wave (a workgroup covers DN_WAVES rows; the row groups of one token block
+// share an XCD): few accumulator registers per wave, four waves per SIMD.
 int launch_dn(int B, const DNArgs& a, hipStream_t st) {
   if (a.N == 0) return 0;
   if (B == 16) return launch_dn_t<16, 4, 1>(a, st);
