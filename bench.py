@@ -178,7 +178,7 @@ def bench_bf16(steps, warmup, device):
                       traffic_source=os.path.relpath(TRAFFIC_PROFILE_BF16, ROOT) + " (FETCH_SIZE/WRITE_SIZE, "
                                      "calibrated on a 256 MiB copy)",
                       kernel="SwiGLU forward launch sequence: pack_bf16_multi_kernel<32> (gate, up, down) + "
-                             "gu_kernel<32,4,false,false,false> + dn_kernel<32,4,4>, timed together with HIP events "
+                             "gu_kernel<32,4,false,false,false> + dn_kernel<32,4,1>, timed together with HIP events "
                              "around each step",
                       algorithmic_flops_per_launch=flops,
                       algorithmic_bytes_per_launch=algorithmic_bytes(w)),
