@@ -29,7 +29,8 @@ import numpy as np
 __all__ = [
     "BlockELLConfig", "k_for_density", "random_topology", "dense_to_block_ell",
     "block_ell_to_dense", "create_block_ell_from_dense", "block_ell_matmul",
-    "silu", "swiglu_fwd", "rmsnorm", "looped_swiglu", "ternary_quantize_blocks",
+    "silu", "swiglu_fwd", "rmsnorm", "looped_swiglu", "block_ell_matmul_t",
+    "block_ell_weight_grad", "swiglu_bwd", "ternary_quantize_blocks",
     "activation_quantize_int8", "encode_ternary", "pack_ternary",
     "unpack_ternary", "ternary_block_partials", "ternary_fixed_point",
     "ternary_matmul", "ternary_swiglu_fwd", "bf16_round",
@@ -226,6 +227,87 @@ def looped_swiglu(h, norm_scale, gate, up, down, L: int, eps: float = 1e-5, stat
         if state_round is not None:
             h = state_round(h)
     return h
+
+
+# --------------------------------------------------------------------------
+# backward of the SwiGLU FFN (derived from the forward's mathematics)
+# --------------------------------------------------------------------------
+
+def block_ell_matmul_t(dy: np.ndarray, values: np.ndarray, col_indices: np.ndarray,
+                       C: int) -> np.ndarray:
+    """Input gradient of ``block_ell_matmul``: ``dx[n, c*B+d] = sum over slots (r, k) with
+    col[r,k] = c of sum_D dy[n, r*B+D] * values[r,k,d,D]``, ``C`` input column blocks.
+
+    This is ``dy @ W`` for the dense ``W = block_ell_to_dense(values, col)`` of
+    ``looped_blockell/layers/block_ell.py:109-146`` (the gradient of ``x @ W.T``).  Dead
+    slots (col < 0 or >= C) contribute nothing (``looped_blockell/opt/cms.py:229-230``).
+    """
+    R, K, B, _ = values.shape
+    lead = dy.shape[:-1]
+    yf = dy.reshape(-1, R * B)
+    dtype = np.result_type(dy.dtype, values.dtype)
+    out = np.zeros((yf.shape[0], C * B), dtype=dtype)
+    for r in range(R):
+        yr = yf[:, r * B:(r + 1) * B].astype(dtype)
+        for k in range(K):
+            c = int(col_indices[r, k])
+            if 0 <= c < C:
+                out[:, c * B:(c + 1) * B] += yr @ values[r, k].astype(dtype).T
+    return out.reshape(*lead, C * B)
+
+
+def block_ell_weight_grad(x: np.ndarray, dy: np.ndarray, col_indices: np.ndarray, B: int) -> np.ndarray:
+    """Tile gradients of ``block_ell_matmul``: ``dW[r,k,d,D] = sum_n x[n, col[r,k]*B+d] *
+    dy[n, r*B+D]`` (the [B_in, B_out] tile layout of ``looped_blockell/layers/block_ell.py:1-8``);
+    dead slots get zero tiles."""
+    R, K = col_indices.shape
+    xf = x.reshape(-1, x.shape[-1])
+    yf = dy.reshape(-1, dy.shape[-1])
+    C = xf.shape[1] // B
+    dtype = np.result_type(x.dtype, dy.dtype)
+    out = np.zeros((R, K, B, B), dtype=dtype)
+    for r in range(R):
+        yr = yf[:, r * B:(r + 1) * B].astype(dtype)
+        for k in range(K):
+            c = int(col_indices[r, k])
+            if 0 <= c < C:
+                out[r, k] = xf[:, c * B:(c + 1) * B].astype(dtype).T @ yr
+    return out
+
+
+def swiglu_bwd(grad_out, x, gate_pre_act, up_output, h, gate, up, down):
+    """Backward of ``out = W_down(silu(g) * u) + x`` with ``g = W_gate x``, ``u = W_up x``.
+
+    The operator and its saved inputs are those of the reference's
+    ``titan::block_ell_swiglu_bwd`` (``csrc/block_ell/block_ell_ops.cpp:78-97``), and its
+    steps follow the reference's launch sequence (``csrc/block_ell/swiglu_bwd.cu:700-834``):
+    ``dh = grad_out W_down`` (kernel 1a), ``dW_down = h^T grad_out`` per tile (1b), the
+    SiLU*mul backward ``dg = dh * u * silu'(g)``, ``du = dh * silu(g)`` with
+    ``silu'(g) = s + g s (1 - s)``, ``s = sigmoid(g)`` (kernel 2, ``:303-340``),
+    ``dx = dg W_gate + du W_up`` (3a) plus ``grad_out`` for the residual (3b,
+    ``:478``), and ``dW_gate = x^T dg``, ``dW_up = x^T du`` per tile (3c).  The arithmetic is
+    the chain rule of the forward, not a copy of those kernels.  ``gate``/``up``/``down`` are
+    ``(values, col_indices)`` pairs; returns ``(dx, d_gate_values, d_up_values,
+    d_down_values)``.
+    """
+    dvals, dcol = down
+    B = dvals.shape[2]
+    d_ff = gate_pre_act.shape[-1]
+    d_model = x.shape[-1]
+    g = np.asarray(gate_pre_act, dtype=np.float64)
+    u = np.asarray(up_output, dtype=np.float64)
+    dy = np.asarray(grad_out, dtype=np.float64)
+    dh = block_ell_matmul_t(dy, dvals.astype(np.float64), dcol, d_ff // B)
+    s = 1.0 / (1.0 + np.exp(-g))
+    dg = dh * u * (s + g * s * (1.0 - s))
+    du = dh * g * s
+    dx = (block_ell_matmul_t(dg, gate[0].astype(np.float64), gate[1], d_model // B)
+          + block_ell_matmul_t(du, up[0].astype(np.float64), up[1], d_model // B) + dy)
+    xd = np.asarray(x, dtype=np.float64)
+    d_gv = block_ell_weight_grad(xd, dg, gate[1], B)
+    d_uv = block_ell_weight_grad(xd, du, up[1], B)
+    d_dv = block_ell_weight_grad(np.asarray(h, dtype=np.float64), dy, dcol, B)
+    return dx, d_gv, d_uv, d_dv
 
 
 # --------------------------------------------------------------------------
@@ -441,6 +523,10 @@ PINS = {
     "swiglu_fwd": "brute-force dense SwiGLU on tiny shapes; residual adds x exactly",
     "rmsnorm": "constant-vector closed form; unit-RMS invariance; scale linearity",
     "looped_swiglu": "L=0 identity; L=1 equals one block; L=2 equals composition",
+    "block_ell_matmul_t": "== dy @ W of block_ell_to_dense; adjoint identity <A x, y> = <x, A^T y>; sentinel 0",
+    "block_ell_weight_grad": "== torch autograd of block_ell_matmul through the dense weight, gathered per tile",
+    "swiglu_bwd": "== torch float64 autograd of the dense SwiGLU FFN with residual (x and every tile); "
+                  "finite differences on tiny shapes",
     "ternary_quantize_blocks": "hand-worked block; round-half-even cases; codes in {-1,0,1}",
     "activation_quantize_int8": "hand-worked rows incl. ties and the -128/127 clamps; bitlinear dequant identity",
     "pack_ternary": "hand-computed words; round trip over all codes",

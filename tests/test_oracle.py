@@ -366,3 +366,141 @@ def test_bf16_round():
     r = O.bf16_round(a)
     np.testing.assert_array_equal(r[:4], np.array([1.0, 1.0, 1.0 + 2 ** -6, -2.5], np.float32))
     assert abs(r[4] - 3.140625) < 1e-7
+
+
+# ---------------------------------------------------------------- backward
+
+def _tile_grads_from_dense(gW, col, R, B):
+    """Gather a dense [out, in] weight gradient into [R, K, B_in, B_out] tiles (dead -> 0)."""
+    K = col.shape[1]
+    C = gW.shape[1] // B
+    out = np.zeros((R, K, B, B))
+    for r in range(R):
+        for k in range(K):
+            c = int(col[r, k])
+            if 0 <= c < C:
+                out[r, k] = gW[r * B:(r + 1) * B, c * B:(c + 1) * B].T
+    return out
+
+
+def test_matmul_t_dense_adjoint_and_sentinel():
+    g = rng(21)
+    R, C, K, B = 5, 4, 3, 4
+    values = g.standard_normal((R, K, B, B))
+    col = O.random_topology(R, C, K, g)
+    col[2, 1] = -1
+    W = O.block_ell_to_dense(values, col, R * B, C * B)
+    dy = g.standard_normal((6, R * B))
+    x = g.standard_normal((6, C * B))
+    dx = O.block_ell_matmul_t(dy, values, col, C)
+    np.testing.assert_allclose(dx, dy @ W, atol=1e-10)
+    # adjoint identity <A x, y> = <x, A^T y>
+    lhs = np.sum(O.block_ell_matmul(x, values, col) * dy)
+    np.testing.assert_allclose(lhs, np.sum(x * dx), rtol=1e-12)
+    # a dead slot contributes nothing: changing its tile leaves the result unchanged
+    v2 = values.copy()
+    v2[2, 1] += 5.0
+    np.testing.assert_array_equal(O.block_ell_matmul_t(dy, v2, col, C), dx)
+
+
+def test_weight_grad_matches_autograd():
+    torch = pytest.importorskip("torch")
+    g = rng(22)
+    R, C, K, B = 4, 5, 2, 4
+    values = g.standard_normal((R, K, B, B))
+    col = O.random_topology(R, C, K, g)
+    col[1, 0] = col[1, 1]          # duplicate column in one row
+    col[3, 1] = -1                 # dead slot
+    x = g.standard_normal((7, C * B))
+    dy = g.standard_normal((7, R * B))
+    W = torch.tensor(O.block_ell_to_dense(values, col, R * B, C * B), requires_grad=True)
+    (torch.tensor(x) @ W.T * torch.tensor(dy)).sum().backward()
+    ref = _tile_grads_from_dense(W.grad.numpy(), col, R, B)
+    np.testing.assert_allclose(O.block_ell_weight_grad(x, dy, col, B), ref, atol=1e-10)
+
+
+def _dense_sum(values, col, out_f, in_f):
+    """Dense [out, in] weight of a Block-ELL matrix with duplicate slots summed (the forward's
+    semantics; the checkpoint bridge overwrites instead)."""
+    R, K, B, _ = values.shape
+    W = np.zeros((out_f, in_f))
+    for r in range(R):
+        for k in range(K):
+            c = int(col[r, k])
+            if 0 <= c < in_f // B:
+                W[r * B:(r + 1) * B, c * B:(c + 1) * B] += values[r, k].T
+    return W
+
+
+def _bwd_case(seed, B=4, dm=12, dff=16, N=5):
+    g = rng(seed)
+    Cm, Cf, Rf, Rm = dm // B, dff // B, dff // B, dm // B
+    gate = (g.standard_normal((Rf, 2, B, B)), O.random_topology(Rf, Cm, 2, g))
+    up = (g.standard_normal((Rf, 2, B, B)), O.random_topology(Rf, Cm, 2, g))
+    down = (g.standard_normal((Rm, 3, B, B)), O.random_topology(Rm, Cf, 3, g))
+    gate[1][0, 1] = -1             # dead slot
+    down[1][1, 2] = down[1][1, 0]  # duplicate column
+    x = g.standard_normal((N, dm))
+    dy = g.standard_normal((N, dm))
+    return gate, up, down, x, dy
+
+
+def test_swiglu_bwd_matches_autograd():
+    torch = pytest.importorskip("torch")
+    B, dm, dff = 4, 12, 16
+    gate, up, down, x, dy = _bwd_case(23, B, dm, dff)
+    T = lambda a, grad=False: torch.tensor(a, dtype=torch.float64, requires_grad=grad)
+    xt = T(x, True)
+    Wg = T(_dense_sum(*gate, dff, dm), True)
+    Wu = T(_dense_sum(*up, dff, dm), True)
+    Wd = T(_dense_sum(*down, dm, dff), True)
+    a, b = xt @ Wg.T, xt @ Wu.T
+    hh = torch.nn.functional.silu(a) * b
+    out = hh @ Wd.T + xt
+    (out * T(dy)).sum().backward()
+    gx = a.detach().numpy()
+    ux = b.detach().numpy()
+    dx, dgv, duv, ddv = O.swiglu_bwd(dy, x, gx, ux, hh.detach().numpy(), gate, up, down)
+    np.testing.assert_allclose(dx, xt.grad.numpy(), atol=1e-10)
+    np.testing.assert_allclose(dgv, _tile_grads_from_dense(Wg.grad.numpy(), gate[1], dff // B, B), atol=1e-10)
+    np.testing.assert_allclose(duv, _tile_grads_from_dense(Wu.grad.numpy(), up[1], dff // B, B), atol=1e-10)
+    np.testing.assert_allclose(ddv, _tile_grads_from_dense(Wd.grad.numpy(), down[1], dm // B, B), atol=1e-10)
+    assert np.all(dgv[0, 1] == 0)
+
+
+def test_swiglu_bwd_finite_differences():
+    B, dm, dff = 4, 12, 16
+    gate, up, down, x, dy = _bwd_case(24, B, dm, dff, N=3)
+
+    def loss(xx, gv, uv, dv):
+        out, *_ = O.swiglu_fwd(xx, (gv, gate[1]), (uv, up[1]), (dv, down[1]), add_residual=True)
+        return float(np.sum(out * dy))
+
+    _, h, gx, ux = O.swiglu_fwd(x, gate, up, down)
+    dx, dgv, duv, ddv = O.swiglu_bwd(dy, x, gx, ux, h, gate, up, down)
+    eps = 1e-6
+    for (n, f) in [(0, 0), (2, 7), (1, 11)]:
+        xp, xm = x.copy(), x.copy()
+        xp[n, f] += eps
+        xm[n, f] -= eps
+        fd = (loss(xp, gate[0], up[0], down[0]) - loss(xm, gate[0], up[0], down[0])) / (2 * eps)
+        assert abs(fd - dx[n, f]) < 1e-6 * max(1.0, abs(fd))
+    for name, idx in [("g", (1, 0, 2, 3)), ("u", (3, 1, 0, 1)), ("d", (2, 2, 3, 0))]:
+        vals = {"g": gate[0], "u": up[0], "d": down[0]}
+        grads = {"g": dgv, "u": duv, "d": ddv}
+        vp = {k: v.copy() for k, v in vals.items()}
+        vm = {k: v.copy() for k, v in vals.items()}
+        vp[name][idx] += eps
+        vm[name][idx] -= eps
+        fd = (loss(x, vp["g"], vp["u"], vp["d"]) - loss(x, vm["g"], vm["u"], vm["d"])) / (2 * eps)
+        assert abs(fd - grads[name][idx]) < 1e-6 * max(1.0, abs(fd))
+
+
+def test_planted_untransposed_tile_in_backward_is_caught():
+    g = rng(25)
+    values = g.standard_normal((3, 2, 4, 4))
+    col = O.random_topology(3, 4, 2, g)
+    dy = g.standard_normal((4, 12))
+    W = O.block_ell_to_dense(values, col, 12, 16)
+    wrong = O.block_ell_matmul_t(dy, values.transpose(0, 1, 3, 2), col, 4)
+    assert np.abs(wrong - dy @ W).max() > 1e-3
