@@ -106,6 +106,34 @@ int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model,
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Workspace bytes needed by lbk_swiglu_bwd_bf16 for this geometry: the transposed
+ * column lists of the three weights, dg and du [N, d_ff] bf16, and fp32 partial
+ * tile gradients (one set per 2048 tokens).
+ */
+size_t lbk_swiglu_bwd_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate,
+                                      const lbk_bell* up, const lbk_bell* down);
+
+/*
+ * Backward of out = W_down(silu(W_gate x) * (W_up x)) + x for an output gradient
+ * grad_out [N, d_model], from the forward's saved x, gate_pre_act = W_gate x,
+ * up_output = W_up x and h (all bf16; the last three [N, d_ff], as
+ * lbk_swiglu_fwd_bf16 returns them):
+ *   dx             [N, d_model]  = dg W_gate + du W_up + grad_out
+ *   d_gate_values  [R_ff, K_g, B, B], d_up_values, d_down_values: tile gradients in the
+ *                  values layout ([B_in, B_out] tiles); dead slots (col < 0 or >= C) get 0
+ * with dh = grad_out W_down, dg = dh * up * silu'(gate), du = dh * silu(gate); fp32
+ * accumulation, dg and du rounded to bf16 before the second products (as the
+ * reference does).  No atomics: the results are deterministic.
+ * Replaces titan::block_ell_swiglu_bwd (reference csrc/block_ell/block_ell_ops.cpp:78-97,
+ * csrc/block_ell/swiglu_bwd.cu:608-834); B in {16, 32, 64}.
+ */
+int lbk_swiglu_bwd_bf16(const uint16_t* grad_out, const uint16_t* x, const uint16_t* gate_pre_act,
+                        const uint16_t* up_output, const uint16_t* h, int64_t N, int32_t d_model,
+                        const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, uint16_t* dx,
+                        uint16_t* d_gate_values, uint16_t* d_up_values, uint16_t* d_down_values,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * out = x / sqrt(mean(x^2) + eps) * scale, rows of length d (bf16 in/out, fp32 math).
  * Replaces rmsnorm_cuda (reference csrc/loop/persistent_core.cuh:76-92) with the
  * layer-API semantics of looped_blockell/layers/norms.py:14-15.

@@ -455,4 +455,110 @@ int lbk_swiglu_fwd_ternary(const int8_t* xq, const float* sx, int64_t N, int32_t
   return LBK_OK;
 }
 
+// ---- backward of the SwiGLU FFN
+// workspace: [transposed lists of down, gate, up] [dg] [du] [fp32 partial tiles]
+static size_t tlist_bytes(const lbk_bell* w, int C) {
+  return align256((size_t)C * 4) + align256((size_t)C * w->R * w->K * 4);
+}
+static int64_t dw_chunks(int64_t N) { return (N + DW_CHUNK - 1) / DW_CHUNK; }
+
+size_t lbk_swiglu_bwd_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
+                                      const lbk_bell* down) {
+  if (!gate || !up || !down || N < 0 || d_model <= 0 || !tile_ok(gate->B)) return 0;
+  const int B = gate->B;
+  const int C_in = d_model / B, C_d = gate->R;
+  const size_t d_ff = (size_t)gate->R * B;
+  const size_t tiles = (size_t)gate->R * gate->K + (size_t)up->R * up->K + (size_t)down->R * down->K;
+  return tlist_bytes(down, C_d) + tlist_bytes(gate, C_in) + tlist_bytes(up, C_in) +
+         2 * align256((size_t)N * d_ff * 2) + align256((size_t)dw_chunks(N) * tiles * B * B * 4);
+}
+
+int lbk_swiglu_bwd_bf16(const uint16_t* grad_out, const uint16_t* x, const uint16_t* gate_pre_act,
+                        const uint16_t* up_output, const uint16_t* h, int64_t N, int32_t d_model,
+                        const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, uint16_t* dx,
+                        uint16_t* d_gate_values, uint16_t* d_up_values, uint16_t* d_down_values, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  int st;
+  if ((st = check_bell(gate)) || (st = check_bell(up)) || (st = check_bell(down))) return st;
+  int64_t d_ff = 0;
+  if ((st = check_ffn(gate, up, down, d_model, &d_ff))) return st;
+  if (N < 0) return LBK_ERR_ARG;
+  const int B = gate->B;
+  const int64_t tg = (int64_t)gate->R * gate->K, tu = (int64_t)up->R * up->K, td = (int64_t)down->R * down->K;
+  if ((tg && !d_gate_values) || (tu && !d_up_values) || (td && !d_down_values)) return LBK_ERR_NULL;
+  for (const void* p : {(const void*)d_gate_values, (const void*)d_up_values, (const void*)d_down_values})
+    if (p && !a16(p)) return LBK_ERR_ALIGN;
+  if (N > 0) {
+    if (!grad_out || !x || !gate_pre_act || !up_output || !h || !dx) return LBK_ERR_NULL;
+    for (const void* p : {(const void*)grad_out, (const void*)x, (const void*)gate_pre_act, (const void*)up_output,
+                          (const void*)h, (const void*)dx})
+      if (!a16(p)) return LBK_ERR_ALIGN;
+    if (d_model % 8) return LBK_ERR_ALIGN;
+  }
+  for (const lbk_bell* w : {gate, up, down})
+    if ((int64_t)w->R * w->K > 0 && !a16(w->values)) return LBK_ERR_ALIGN;
+  const size_t need = lbk_swiglu_bwd_workspace_bytes(N, d_model, gate, up, down);
+  if (!workspace || workspace_bytes < need) return LBK_ERR_WORKSPACE;
+  if (!a16(workspace)) return LBK_ERR_ALIGN;
+  hipStream_t s = S(stream);
+  const int C_in = d_model / B, C_d = gate->R;
+  char* p = static_cast<char*>(workspace);
+  auto take = [&](size_t bytes) {
+    char* q = p;
+    p += align256(bytes);
+    return q;
+  };
+  const lbk_bell* w3[3] = {down, gate, up};
+  const int c3[3] = {C_d, C_in, C_in};
+  TListJob lj[3];
+  for (int t = 0; t < 3; ++t) {
+    lj[t].col = w3[t]->col_idx; lj[t].R = w3[t]->R; lj[t].K = w3[t]->K; lj[t].C = c3[t];
+    lj[t].cnt = reinterpret_cast<int32_t*>(take((size_t)c3[t] * 4));
+    lj[t].list = reinterpret_cast<int32_t*>(take((size_t)c3[t] * w3[t]->R * w3[t]->K * 4));
+  }
+  uint16_t* dg = reinterpret_cast<uint16_t*>(take((size_t)N * d_ff * 2));
+  uint16_t* du = reinterpret_cast<uint16_t*>(take((size_t)N * d_ff * 2));
+  float* part = reinterpret_cast<float*>(p);
+  // slots of a weight with no tiles (R * K == 0) take no part in the lists
+  int nl = 0;
+  TListJob ljn[3];
+  for (int t = 0; t < 3; ++t)
+    if ((int64_t)lj[t].R * lj[t].K > 0) ljn[nl++] = lj[t];
+  if (N > 0) {
+    if (nl && launch_tlist(ljn, nl, s)) return LBK_ERR_LAUNCH;
+    // dh = dy W_down -> dg, du
+    TProdArgs a{};
+    a.nsrc = 0;
+    if (td > 0) a.src[a.nsrc++] = TProdSrc{grad_out, d_model, down->values, down->K, lj[0].cnt, lj[0].list, td};
+    a.N = N; a.C = C_d; a.ldo = d_ff;
+    a.g = gate_pre_act; a.u = up_output; a.dg = dg; a.du = du;
+    if (launch_tprod(B, 0, a, s)) return LBK_ERR_LAUNCH;
+    // dx = dg W_gate + du W_up + dy
+    TProdArgs b{};
+    b.nsrc = 0;
+    if (tg > 0) b.src[b.nsrc++] = TProdSrc{dg, d_ff, gate->values, gate->K, lj[1].cnt, lj[1].list, tg};
+    if (tu > 0) b.src[b.nsrc++] = TProdSrc{du, d_ff, up->values, up->K, lj[2].cnt, lj[2].list, tu};
+    b.N = N; b.C = C_in; b.ldo = d_model;
+    b.resid = grad_out; b.out = dx;
+    if (launch_tprod(B, 1, b, s)) return LBK_ERR_LAUNCH;
+  }
+  // tile gradients: gate (x, dg), up (x, du), down (h, dy)
+  const int64_t nch = dw_chunks(N);
+  DWJob dj[3];
+  int nj = 0;
+  size_t poff = 0;
+  auto add = [&](const uint16_t* xx, int64_t ldx, const uint16_t* gy, int64_t ldg, const lbk_bell* w, int C,
+                 uint16_t* out) {
+    const int64_t nt = (int64_t)w->R * w->K;
+    if (nt == 0) return;
+    dj[nj++] = DWJob{xx, ldx, gy, ldg, w->col_idx, w->R, w->K, C, part + poff, out};
+    poff += (size_t)nch * nt * B * B;
+  };
+  add(x, d_model, dg, d_ff, gate, C_in, d_gate_values);
+  add(x, d_model, du, d_ff, up, C_in, d_up_values);
+  add(h, d_ff, grad_out, d_model, down, C_d, d_down_values);
+  if (nj && launch_dw(B, dj, nj, N, DW_CHUNK, s)) return LBK_ERR_LAUNCH;
+  return LBK_OK;
+}
+
 }  // extern "C"

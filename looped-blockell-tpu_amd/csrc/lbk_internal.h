@@ -155,6 +155,51 @@ int tgu_slices(int64_t N);
 int launch_tgu(const TGUArgs& a, hipStream_t st);
 int launch_tdn(const TDNArgs& a, hipStream_t st);
 
+// ---- backward of the SwiGLU FFN (lbk_bwd.hip)
+// transposed topology: for input column block c, cnt[c] slots e = r*K + k with col[e] == c at
+// list[c*R*K ...], ascending
+struct TListJob {
+  const int32_t* col; int R, K, C;
+  int32_t* cnt; int32_t* list;   // [C], [C, R*K]
+};
+struct TListJobs {
+  static constexpr int kMax = 3;
+  TListJob job[kMax];
+  int64_t first[kMax];
+  int n;
+};
+int launch_tlist(const TListJob* jobs, int n, hipStream_t st);
+// out[:, c*B ..] = sum over sources and their slots of column block c of A[:, r*B ..] W[e]^T
+struct TProdSrc {
+  const uint16_t* a; int64_t lda;   // activations [N, R*B]
+  const uint16_t* w; int K;         // raw tiles [R, K, B, B]
+  const int32_t* cnt; const int32_t* list; int64_t cap;
+};
+struct TProdArgs {
+  TProdSrc src[2]; int nsrc;
+  int64_t N; int C; int64_t ldo;    // output [N, C*B], row stride ldo (also of g, u, resid)
+  const uint16_t* g; const uint16_t* u; uint16_t* dg; uint16_t* du;   // mode 0
+  const uint16_t* resid; uint16_t* out;                               // mode 1
+};
+// mode 0: dh -> dg, du (SiLU*mul backward); mode 1: out = product + resid
+int launch_tprod(int B, int mode, const TProdArgs& a, hipStream_t st);
+// tile gradients dW[e] = X[:, col(e)]^T G[:, row(e)] through fp32 per-chunk partials
+struct DWJob {
+  const uint16_t* x; int64_t ldx;    // [N, C*B]
+  const uint16_t* gy; int64_t ldg;   // [N, R*B]
+  const int32_t* col; int R, K, C;
+  float* part;                       // [nchunk, R*K, B, B]
+  uint16_t* dw;                      // [R, K, B, B] bf16
+};
+struct DWJobs {
+  static constexpr int kMax = 3;
+  DWJob job[kMax];
+  int64_t first[kMax], rfirst[kMax];
+  int n; int64_t N; int chunk; int nchunk;
+};
+constexpr int DW_CHUNK = 2048;   // tokens per partial tile
+int launch_dw(int B, const DWJob* jobs, int n, int64_t N, int chunk, hipStream_t st);
+
 int launch_check_columns(const int32_t* col, int64_t count, int C, int32_t* bad, hipStream_t st);
 
 }  // namespace lbk

@@ -152,3 +152,20 @@ def abi_looped(h_t, scale_t, g_t, u_t, d_t, L, eps):
                                        C.byref(db), ptr(out), ptr(ws) if wsb else C.c_void_p(0), wsb, stream()),
             "looped")
     return out
+
+
+def abi_swiglu_bwd(dy_t, x_t, g_t, u_t, h_t, gate_t, up_t, down_t):
+    """Backward through the C ABI; returns (dx, d_gate_values, d_up_values, d_down_values)."""
+    import torch
+    A = abi()
+    lib = A.load()
+    N, d_model = x_t.shape
+    gb, ub, db = (bell_struct(*w) for w in (gate_t, up_t, down_t))
+    wsb = lib.lbk_swiglu_bwd_workspace_bytes(N, d_model, C.byref(gb), C.byref(ub), C.byref(db))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
+    dx = torch.empty(N, d_model, dtype=torch.bfloat16, device="cuda")
+    dvs = [torch.empty_like(w[0]) for w in (gate_t, up_t, down_t)]
+    A.check(lib.lbk_swiglu_bwd_bf16(ptr(dy_t), ptr(x_t), ptr(g_t), ptr(u_t), ptr(h_t), N, d_model, C.byref(gb),
+                                    C.byref(ub), C.byref(db), ptr(dx), ptr(dvs[0]), ptr(dvs[1]), ptr(dvs[2]),
+                                    ptr(ws), wsb, stream()), "swiglu_bwd")
+    return dx, dvs[0], dvs[1], dvs[2]

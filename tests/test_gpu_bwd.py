@@ -1,0 +1,102 @@
+"""Parity of the SwiGLU FFN backward (lbk_swiglu_bwd_bf16) against the oracle.
+
+The saved forward tensors (gate_pre_act, up_output, h) are computed by the oracle and rounded
+to bf16, then given to both sides; the oracle differentiates in float64.  Bar: max-abs error
+<= 1e-2 of max |reference| for dx and every tile gradient (the kernel rounds dg and du to bf16
+between its products, as the reference operator does).
+"""
+
+import numpy as np
+import pytest
+
+import lbk_testlib as T
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def _say(msg):
+    print(f"[bwd] {msg}", flush=True)
+
+
+def _inputs(rng, d_model, d_ff, B, dens, N, sf):
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, dens, sentinel_frac=sf)
+    x = T.act(rng, N, d_model)
+    dy = T.act(rng, N, d_model)
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    _, h, gp, uo = O.swiglu_fwd(x.astype(np.float64), f64(g), f64(u), f64(d))
+    gp, uo, h = (O.bf16_round(a.astype(np.float32)) for a in (gp, uo, h))
+    return g, u, d, x, dy, gp, uo, h
+
+
+def _run(g, u, d, x, dy, gp, uo, h):
+    G = T.to_gpu_bf16
+    return T.abi_swiglu_bwd(G(dy), G(x), G(gp), G(uo), G(h), T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d))
+
+
+BWD_CASES = [
+    # (d_model, d_ff, B, density, N, sentinel_frac)
+    (256, 1024, 16, 0.25, 100, 0.1),
+    (512, 1024, 32, 0.25, 130, 0.05),
+    (128, 512, 64, 0.5, 70, 0.0),
+    (1024, 4096, 32, 0.25, 2100, 0.0),     # two token chunks of the tile gradients, ragged tail
+]
+
+
+@pytest.mark.parametrize("case", BWD_CASES)
+def test_swiglu_bwd_parity(gpu, case):
+    d_model, d_ff, B, dens, N, sf = case
+    _say(f"parity {case}")
+    rng = np.random.default_rng(hash(case) % 2 ** 31)
+    g, u, d, x, dy, gp, uo, h = _inputs(rng, d_model, d_ff, B, dens, N, sf)
+    got = _run(g, u, d, x, dy, gp, uo, h)
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref = O.swiglu_bwd(dy, x, gp, uo, h, f64(g), f64(u), f64(d))
+    for gt, rf, name in zip(got, ref, ("dx", "d_gate", "d_up", "d_down")):
+        rel, ab = T.rel_err(T.to_np(gt), rf)
+        assert rel <= TOL, f"{name}: rel {rel} abs {ab}"
+    # dead slots get exactly zero tiles
+    for gt, w in zip(got[1:], (g, u, d)):
+        dead = w[1] < 0
+        if dead.any():
+            assert np.all(T.to_np(gt)[dead] == 0)
+
+
+def test_swiglu_bwd_duplicate_columns_and_deterministic(gpu):
+    """Two slots of a row on one column get identical gradients; two calls agree bit for bit."""
+    _say("duplicates + determinism")
+    rng = np.random.default_rng(5)
+    d_model, d_ff, B, N = 256, 512, 32, 300
+    g, u, d, x, dy, gp, uo, h = _inputs(rng, d_model, d_ff, B, 0.25, N, 0.0)
+    d[1][3, 1] = d[1][3, 0]
+    g[1][5, 1] = g[1][5, 0]
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    _, h, gp, uo = O.swiglu_fwd(x.astype(np.float64), f64(g), f64(u), f64(d))
+    gp, uo, h = (O.bf16_round(a.astype(np.float32)) for a in (gp, uo, h))
+    a = _run(g, u, d, x, dy, gp, uo, h)
+    b = _run(g, u, d, x, dy, gp, uo, h)
+    for ta, tb in zip(a, b):
+        assert np.array_equal(T.to_np(ta), T.to_np(tb))
+    ref = O.swiglu_bwd(dy, x, gp, uo, h, f64(g), f64(u), f64(d))
+    for gt, rf, name in zip(a, ref, ("dx", "d_gate", "d_up", "d_down")):
+        rel, ab = T.rel_err(T.to_np(gt), rf)
+        assert rel <= TOL, f"{name}: rel {rel} abs {ab}"
+    dd = T.to_np(a[3])
+    assert np.array_equal(dd[3, 1], dd[3, 0])
+    dg = T.to_np(a[1])
+    assert np.array_equal(dg[5, 1], dg[5, 0])
+
+
+def test_swiglu_bwd_zero_tokens(gpu):
+    """N = 0: no input gradient, all tile gradients zero."""
+    import torch
+    _say("N = 0")
+    rng = np.random.default_rng(6)
+    g, u, d = T.ffn_weights(rng, 128, 256, 16, 0.5)
+    e = torch.empty(0, 128, dtype=torch.bfloat16, device="cuda")
+    e2 = torch.empty(0, 256, dtype=torch.bfloat16, device="cuda")
+    gw, uw, dw = T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d)
+    dx, dg, du, dd = T.abi_swiglu_bwd(e, e, e2, e2, e2, gw, uw, dw)
+    for t in (dg, du, dd):
+        assert torch.count_nonzero(t).item() == 0
