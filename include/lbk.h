@@ -114,11 +114,12 @@ size_t lbk_swiglu_bwd_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell
                                       const lbk_bell* up, const lbk_bell* down);
 
 /*
- * Backward of out = W_down(silu(W_gate x) * (W_up x)) + x for an output gradient
+ * Backward of out = W_down(silu(W_gate x) * (W_up x)) (+ x) for an output gradient
  * grad_out [N, d_model], from the forward's saved x, gate_pre_act = W_gate x,
  * up_output = W_up x and h (all bf16; the last three [N, d_ff], as
  * lbk_swiglu_fwd_bf16 returns them):
- *   dx             [N, d_model]  = dg W_gate + du W_up + grad_out
+ *   dx             [N, d_model]  = dg W_gate + du W_up (+ grad_out if add_residual; the
+ *                  reference operator always adds it)
  *   d_gate_values  [R_ff, K_g, B, B], d_up_values, d_down_values: tile gradients in the
  *                  values layout ([B_in, B_out] tiles); dead slots (col < 0 or >= C) get 0
  * with dh = grad_out W_down, dg = dh * up * silu'(gate), du = dh * silu(gate); fp32
@@ -129,9 +130,9 @@ size_t lbk_swiglu_bwd_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell
  */
 int lbk_swiglu_bwd_bf16(const uint16_t* grad_out, const uint16_t* x, const uint16_t* gate_pre_act,
                         const uint16_t* up_output, const uint16_t* h, int64_t N, int32_t d_model,
-                        const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, uint16_t* dx,
-                        uint16_t* d_gate_values, uint16_t* d_up_values, uint16_t* d_down_values,
-                        void* workspace, size_t workspace_bytes, void* stream);
+                        const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, int add_residual,
+                        uint16_t* dx, uint16_t* d_gate_values, uint16_t* d_up_values,
+                        uint16_t* d_down_values, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * out = x / sqrt(mean(x^2) + eps) * scale, rows of length d (bf16 in/out, fp32 math).

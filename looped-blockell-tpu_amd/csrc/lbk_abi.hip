@@ -475,9 +475,9 @@ size_t lbk_swiglu_bwd_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell
 
 int lbk_swiglu_bwd_bf16(const uint16_t* grad_out, const uint16_t* x, const uint16_t* gate_pre_act,
                         const uint16_t* up_output, const uint16_t* h, int64_t N, int32_t d_model,
-                        const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, uint16_t* dx,
-                        uint16_t* d_gate_values, uint16_t* d_up_values, uint16_t* d_down_values, void* workspace,
-                        size_t workspace_bytes, void* stream) {
+                        const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, int add_residual,
+                        uint16_t* dx, uint16_t* d_gate_values, uint16_t* d_up_values, uint16_t* d_down_values,
+                        void* workspace, size_t workspace_bytes, void* stream) {
   int st;
   if ((st = check_bell(gate)) || (st = check_bell(up)) || (st = check_bell(down))) return st;
   int64_t d_ff = 0;
@@ -533,13 +533,13 @@ int lbk_swiglu_bwd_bf16(const uint16_t* grad_out, const uint16_t* x, const uint1
     a.N = N; a.C = C_d; a.ldo = d_ff;
     a.g = gate_pre_act; a.u = up_output; a.dg = dg; a.du = du;
     if (launch_tprod(B, 0, a, s)) return LBK_ERR_LAUNCH;
-    // dx = dg W_gate + du W_up + dy
+    // dx = dg W_gate + du W_up (+ dy)
     TProdArgs b{};
     b.nsrc = 0;
     if (tg > 0) b.src[b.nsrc++] = TProdSrc{dg, d_ff, gate->values, gate->K, lj[1].cnt, lj[1].list, tg};
     if (tu > 0) b.src[b.nsrc++] = TProdSrc{du, d_ff, up->values, up->K, lj[2].cnt, lj[2].list, tu};
     b.N = N; b.C = C_in; b.ldo = d_model;
-    b.resid = grad_out; b.out = dx;
+    b.resid = add_residual ? grad_out : nullptr; b.out = dx;
     if (launch_tprod(B, 1, b, s)) return LBK_ERR_LAUNCH;
   }
   // tile gradients: gate (x, dg), up (x, du), down (h, dy)

@@ -1,10 +1,10 @@
 // lbk_bwd.hip — backward of the Block-ELL SwiGLU FFN (gfx950, bf16 MFMA).
 //
-// With g = W_gate x, u = W_up x, h = silu(g) * u and out = W_down h + x, the
+// With g = W_gate x, u = W_up x, h = silu(g) * u and out = W_down h (+ x), the
 // gradients for an output gradient dy are
 //   dh = dy W_down                    (transposed block-sparse product)
 //   dg = dh * u * silu'(g), du = dh * silu(g)
-//   dx = dg W_gate + du W_up + dy
+//   dx = dg W_gate + du W_up (+ dy)
 //   dW[r,k] = X[:, col(r,k)]^T G[:, r]  per tile, (X, G) = (x, dg), (x, du), (h, dy).
 //
 //   tlist_kernel   transposed topology: for every input column block c the slots
@@ -16,7 +16,7 @@
 //                  d of the tile holds the 8 consecutive B_out values a lane
 //                  needs), the activation rows the B operand, so each lane ends
 //                  with 4 consecutive output columns of one token.  Epilogue:
-//                  the SiLU*mul backward (dh -> dg, du) or + dy (-> dx).
+//                  the SiLU*mul backward (dh -> dg, du) or the optional + dy (-> dx).
 //   dw_kernel      tile gradients: a workgroup owns one block row, up to 8 of
 //                  its slots (one per wave) and a chunk of tokens; 32-token
 //                  slices of X and G are staged transposed in LDS (the token
@@ -147,8 +147,8 @@ __global__ __launch_bounds__(256) void tprod_kernel(TProdArgs a) {
       store_bf16<4>(a.dg + off, dgv);
       store_bf16<4>(a.du + off, duv);
     } else {
-      float rv[4];
-      load_bf16<4>(a.resid + off, rv);
+      float rv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (a.resid) load_bf16<4>(a.resid + off, rv);
 #pragma unroll
       for (int v = 0; v < 4; ++v) o[v] = acc[m][v] + rv[v];
       store_bf16<4>(a.out + off, o);

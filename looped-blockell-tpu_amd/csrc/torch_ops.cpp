@@ -359,6 +359,52 @@ at::Tensor check_columns(const at::Tensor& c_, int64_t C) {
                                               cur_stream(c)));
   return bad;
 }
+// ------------------------------------------------------------------ bf16 SwiGLU backward
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> swiglu_bwd_impl(
+    const at::Tensor& dy_, const at::Tensor& x_, const at::Tensor& gp_, const at::Tensor& uo_, const at::Tensor& h_,
+    const at::Tensor& vg_, const at::Tensor& cg_, const at::Tensor& vu_, const at::Tensor& cu_, const at::Tensor& vd_,
+    const at::Tensor& cd_, bool add_residual, const char* op) {
+  at::Tensor vg = vg_, cg = cg_, vu = vu_, cu = cu_, vd = vd_, cd = cd_;
+  at::Tensor x = check_x2d(x_, op);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  lbk_bell g = make_bell(vg, cg, op, "gate"), u = make_bell(vu, cu, op, "up"), d = make_bell(vd, cd, op, "down");
+  const int64_t N = x.size(0), d_model = x.size(1);
+  const int64_t d_ff = (int64_t)g.R * g.B;
+  auto act = [&](const at::Tensor& t, int64_t cols, const char* name) {
+    check_gpu(t, op, name);
+    TORCH_CHECK(t.scalar_type() == at::kBFloat16, "titan::", op, ": ", name, " must be bf16");
+    TORCH_CHECK(t.dim() == 2 && t.size(0) == N && t.size(1) == cols, "titan::", op, ": ", name, " must be [", N,
+                ", ", cols, "], got ", t.sizes());
+    return t.contiguous();
+  };
+  at::Tensor dy = act(dy_, d_model, "grad_out"), gp = act(gp_, d_ff, "gate_pre_act"),
+             uo = act(uo_, d_ff, "up_output"), h = act(h_, d_ff, "h");
+  at::Tensor dx = at::empty({N, d_model}, x.options());
+  at::Tensor dvg = at::empty_like(vg), dvu = at::empty_like(vu), dvd = at::empty_like(vd);
+  const size_t wsb = lbk_swiglu_bwd_workspace_bytes(N, (int32_t)d_model, &g, &u, &d);
+  at::Tensor ws = workspace(wsb, x);
+  LBK_CALL("block_ell_swiglu_bwd",
+           lbk_swiglu_bwd_bf16(bf(dy), bf(x), bf(gp), bf(uo), bf(h), N, (int32_t)d_model, &g, &u, &d,
+                               add_residual ? 1 : 0, bfm(dx), bfm(dvg), bfm(dvu), bfm(dvd), ws.data_ptr(), wsb,
+                               cur_stream(x)));
+  return {dx, dvg, dvu, dvd};
+}
+
+// the reference operator: dx always includes grad_out (the forward's residual)
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> swiglu_bwd(
+    const at::Tensor& dy, const at::Tensor& x, const at::Tensor& gp, const at::Tensor& uo, const at::Tensor& h,
+    const at::Tensor& vg, const at::Tensor& cg, const at::Tensor& vu, const at::Tensor& cu, const at::Tensor& vd,
+    const at::Tensor& cd) {
+  return swiglu_bwd_impl(dy, x, gp, uo, h, vg, cg, vu, cu, vd, cd, true, "block_ell_swiglu_bwd");
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> swiglu_bwd_ex(
+    const at::Tensor& dy, const at::Tensor& x, const at::Tensor& gp, const at::Tensor& uo, const at::Tensor& h,
+    const at::Tensor& vg, const at::Tensor& cg, const at::Tensor& vu, const at::Tensor& cu, const at::Tensor& vd,
+    const at::Tensor& cd, bool add_residual) {
+  return swiglu_bwd_impl(dy, x, gp, uo, h, vg, cg, vu, cu, vd, cd, add_residual, "block_ell_swiglu_bwd_ex");
+}
+
 
 // HIP has no access-policy window; weight residency comes from the fused
 // kernels (LDS panels, L2/MALL reuse).  The ops stay in the schema so callers
@@ -369,11 +415,14 @@ void unpin_weights_l2() {}
 }  // namespace
 
 TORCH_LIBRARY(titan, m) {
-  // reference schemas (csrc/block_ell/block_ell_ops.cpp:51-76, csrc/loop/loop_ops.cpp:39-66)
+  // reference schemas (csrc/block_ell/block_ell_ops.cpp:51-97, csrc/loop/loop_ops.cpp:39-66)
   m.def("block_ell_swiglu_fwd(Tensor x, Tensor v_gate, Tensor ci_gate, Tensor v_up, Tensor ci_up, "
         "Tensor v_down, Tensor ci_down, bool add_residual) -> Tensor");
   m.def("block_ell_swiglu_fwd_with_intermediate(Tensor x, Tensor v_gate, Tensor ci_gate, Tensor v_up, "
         "Tensor ci_up, Tensor v_down, Tensor ci_down, bool add_residual) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("block_ell_swiglu_bwd(Tensor grad_out, Tensor x, Tensor gate_pre_act, Tensor up_out, Tensor h, "
+        "Tensor v_gate, Tensor ci_gate, Tensor v_up, Tensor ci_up, Tensor v_down, Tensor ci_down) "
+        "-> (Tensor, Tensor, Tensor, Tensor)");
   m.def("pin_weights_l2(Tensor[] weights) -> ()");
   m.def("unpin_weights_l2() -> ()");
   m.def("persistent_mlp_step(Tensor h, Tensor e, Tensor log_A, Tensor log_dt, Tensor[] norm_scales, "
@@ -381,6 +430,9 @@ TORCH_LIBRARY(titan, m) {
         "Tensor[] down_values, Tensor[] down_col_idx) -> Tensor");
   // ops beyond the reference's set
   m.def("block_ell_matmul(Tensor x, Tensor values, Tensor col_indices, Tensor? bias=None) -> Tensor");
+  m.def("block_ell_swiglu_bwd_ex(Tensor grad_out, Tensor x, Tensor gate_pre_act, Tensor up_out, Tensor h, "
+        "Tensor v_gate, Tensor ci_gate, Tensor v_up, Tensor ci_up, Tensor v_down, Tensor ci_down, "
+        "bool add_residual) -> (Tensor, Tensor, Tensor, Tensor)");
   m.def("looped_swiglu(Tensor h, Tensor norm_scale, Tensor v_gate, Tensor ci_gate, Tensor v_up, Tensor ci_up, "
         "Tensor v_down, Tensor ci_down, int L, float eps=1e-05) -> Tensor");
   m.def("rmsnorm(Tensor x, Tensor scale, float eps=1e-05) -> Tensor");
@@ -402,6 +454,8 @@ TORCH_LIBRARY(titan, m) {
 TORCH_LIBRARY_IMPL(titan, CUDA, m) {
   m.impl("block_ell_swiglu_fwd", &swiglu_fwd);
   m.impl("block_ell_swiglu_fwd_with_intermediate", &swiglu_fwd_inter);
+  m.impl("block_ell_swiglu_bwd", &swiglu_bwd);
+  m.impl("block_ell_swiglu_bwd_ex", &swiglu_bwd_ex);
   m.impl("pin_weights_l2", &pin_weights_l2);
   m.impl("persistent_mlp_step", &persistent_mlp_step);
   m.impl("block_ell_matmul", &block_ell_matmul);
@@ -432,6 +486,18 @@ TORCH_LIBRARY_IMPL(titan, Meta, m) {
            const int64_t N = x.size(0), d_ff = vg.size(0) * vg.size(2);
            return std::make_tuple(at::empty_like(x), at::empty({N, d_ff}, x.options()),
                                   at::empty({N, d_ff}, x.options()), at::empty({N, d_ff}, x.options()));
+         });
+  m.impl("block_ell_swiglu_bwd",
+         [](const at::Tensor&, const at::Tensor& x, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+            const at::Tensor& vg, const at::Tensor&, const at::Tensor& vu, const at::Tensor&, const at::Tensor& vd,
+            const at::Tensor&) {
+           return std::make_tuple(at::empty_like(x), at::empty_like(vg), at::empty_like(vu), at::empty_like(vd));
+         });
+  m.impl("block_ell_swiglu_bwd_ex",
+         [](const at::Tensor&, const at::Tensor& x, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+            const at::Tensor& vg, const at::Tensor&, const at::Tensor& vu, const at::Tensor&, const at::Tensor& vd,
+            const at::Tensor&, bool) {
+           return std::make_tuple(at::empty_like(x), at::empty_like(vg), at::empty_like(vu), at::empty_like(vd));
          });
   m.impl("pin_weights_l2", [](at::TensorList) {});
   m.impl("persistent_mlp_step",

@@ -55,7 +55,8 @@ SIGNATURES = {
     "lbk_swiglu_workspace_bytes": (_SZ, [_I64, _I32, _PB, _PB, _PB, C.c_int]),
     "lbk_swiglu_fwd_bf16": (C.c_int, [_P, _I64, _I32, _PB, _PB, _PB, C.c_int, _P, _P, _P, _P, _P, _SZ, _P]),
     "lbk_swiglu_bwd_workspace_bytes": (_SZ, [_I64, _I32, _PB, _PB, _PB]),
-    "lbk_swiglu_bwd_bf16": (C.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _PB, _PB, _PB, _P, _P, _P, _P, _P, _SZ, _P]),
+    "lbk_swiglu_bwd_bf16": (C.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _PB, _PB, _PB, C.c_int, _P, _P, _P, _P, _P,
+                                      _SZ, _P]),
     "lbk_rmsnorm_bf16": (C.c_int, [_P, _I64, _I32, _P, _F, _P, _P]),
     "lbk_diagonal_injection_bf16": (C.c_int, [_P, _P, _P, _P, _I64, _I32, _P, _P]),
     "lbk_looped_workspace_bytes": (_SZ, [_I64, _I32, _PB, _PB, _PB]),

@@ -72,6 +72,48 @@ def swiglu_fwd_with_intermediate(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_dow
                                                         add_residual)
 
 
+def swiglu_bwd(grad_out, x, gate_pre_act, up_out, h, v_gate, ci_gate, v_up, ci_up, v_down, ci_down,
+               add_residual: bool = True):
+    """``titan::block_ell_swiglu_bwd``: returns ``(dx, d_v_gate, d_v_up, d_v_down)`` from the
+    forward's saved ``x``, ``gate_pre_act``, ``up_out`` and ``h``.  ``dx`` includes
+    ``grad_out`` (the forward's residual) as in the reference operator unless
+    ``add_residual`` is False."""
+    _gpu(grad_out, x, v_gate, v_down)
+    if add_residual:
+        return ops().block_ell_swiglu_bwd(grad_out, x, gate_pre_act, up_out, h, v_gate, ci_gate, v_up, ci_up,
+                                          v_down, ci_down)
+    return ops().block_ell_swiglu_bwd_ex(grad_out, x, gate_pre_act, up_out, h, v_gate, ci_gate, v_up, ci_up,
+                                         v_down, ci_down, False)
+
+
+class _SwiGLUFunction(torch.autograd.Function):
+    """Differentiable SwiGLU FFN: the forward saves (x, h, gate_pre_act, up_out), the backward
+    is ``titan::block_ell_swiglu_bwd``; the column indices get no gradient."""
+
+    @staticmethod
+    def forward(ctx, x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual):
+        out, h, gp, uo = swiglu_fwd_with_intermediate(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down,
+                                                      add_residual)
+        ctx.save_for_backward(x, h, gp, uo, v_gate, ci_gate, v_up, ci_up, v_down, ci_down)
+        ctx.add_residual = add_residual
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, h, gp, uo, vg, cg, vu, cu, vd, cd = ctx.saved_tensors
+        dx, dvg, dvu, dvd = swiglu_bwd(grad_out.to(torch.bfloat16).contiguous(), x, gp, uo, h, vg, cg, vu, cu,
+                                       vd, cd, ctx.add_residual)
+        return dx, dvg, None, dvu, None, dvd, None, None
+
+
+def swiglu(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual: bool = False):
+    """SwiGLU FFN forward that autograd can differentiate (through ``titan::block_ell_swiglu_bwd``);
+    without gradients it is ``swiglu_fwd``."""
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (x, v_gate, v_up, v_down)):
+        return _SwiGLUFunction.apply(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual)
+    return swiglu_fwd(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual)
+
+
 def looped_swiglu(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L: int, eps: float = 1e-5):
     """L applications of h <- h + SwiGLU(RMSNorm(h)) with shared weights, in one operator call."""
     _gpu(h, v_gate, v_down)

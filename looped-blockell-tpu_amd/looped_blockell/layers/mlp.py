@@ -9,7 +9,8 @@ Weight layout per projection:
   bias:        [out_features] parameter, zeros (BlockELLLinear only)
 
 ``MLPBlock(use_swiglu=True)`` runs the whole SwiGLU FFN as one fused HIP
-operator (``titan::block_ell_swiglu_fwd``); its projections carry no bias, as
+operator (``titan::block_ell_swiglu_fwd``, differentiable through
+``titan::block_ell_swiglu_bwd``); its projections carry no bias, as
 in the reference's PyTorch mirror (``interop/pt_model.py:865-867``) and its CUDA
 operator (``csrc/block_ell/swiglu_fwd.cuh:75-84``).
 """
@@ -118,7 +119,7 @@ class MLPBlock(nn.Module):
         lead = x.shape[:-1]
         if self.use_swiglu:
             x2 = x.reshape(-1, self.d_model).to(torch.bfloat16).contiguous()
-            out = kernels.swiglu_fwd(x2, *self.swiglu_weights(), add_residual=False).reshape(*lead, self.d_model)
+            out = kernels.swiglu(x2, *self.swiglu_weights(), add_residual=False).reshape(*lead, self.d_model)
         else:
             out = self.fc2(F.gelu(self.fc1(x).float()).to(torch.bfloat16))
         if self.dropout > 0.0 and not deterministic:

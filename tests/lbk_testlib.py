@@ -154,7 +154,7 @@ def abi_looped(h_t, scale_t, g_t, u_t, d_t, L, eps):
     return out
 
 
-def abi_swiglu_bwd(dy_t, x_t, g_t, u_t, h_t, gate_t, up_t, down_t):
+def abi_swiglu_bwd(dy_t, x_t, g_t, u_t, h_t, gate_t, up_t, down_t, add_residual=True):
     """Backward through the C ABI; returns (dx, d_gate_values, d_up_values, d_down_values)."""
     import torch
     A = abi()
@@ -166,6 +166,7 @@ def abi_swiglu_bwd(dy_t, x_t, g_t, u_t, h_t, gate_t, up_t, down_t):
     dx = torch.empty(N, d_model, dtype=torch.bfloat16, device="cuda")
     dvs = [torch.empty_like(w[0]) for w in (gate_t, up_t, down_t)]
     A.check(lib.lbk_swiglu_bwd_bf16(ptr(dy_t), ptr(x_t), ptr(g_t), ptr(u_t), ptr(h_t), N, d_model, C.byref(gb),
-                                    C.byref(ub), C.byref(db), ptr(dx), ptr(dvs[0]), ptr(dvs[1]), ptr(dvs[2]),
+                                    C.byref(ub), C.byref(db), 1 if add_residual else 0, ptr(dx), ptr(dvs[0]),
+                                    ptr(dvs[1]), ptr(dvs[2]),
                                     ptr(ws), wsb, stream()), "swiglu_bwd")
     return dx, dvs[0], dvs[1], dvs[2]

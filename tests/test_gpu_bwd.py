@@ -100,3 +100,56 @@ def test_swiglu_bwd_zero_tokens(gpu):
     dx, dg, du, dd = T.abi_swiglu_bwd(e, e, e2, e2, e2, gw, uw, dw)
     for t in (dg, du, dd):
         assert torch.count_nonzero(t).item() == 0
+
+
+def test_torch_op_matches_abi_and_residual_flag(gpu):
+    """titan::block_ell_swiglu_bwd equals the C ABI bit for bit; without the residual dx lacks grad_out."""
+    from looped_blockell import kernels
+    _say("torch op + residual flag")
+    rng = np.random.default_rng(7)
+    g, u, d, x, dy, gp, uo, h = _inputs(rng, 512, 1024, 32, 0.25, 90, 0.1)
+    G = T.to_gpu_bf16
+    gw, uw, dw = T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d)
+    args = (G(dy), G(x), G(gp), G(uo), G(h), gw[0], gw[1], uw[0], uw[1], dw[0], dw[1])
+    op = kernels.swiglu_bwd(*args)
+    ab = T.abi_swiglu_bwd(args[0], args[1], args[2], args[3], args[4], gw, uw, dw)
+    for a_, b_ in zip(op, ab):
+        assert np.array_equal(T.to_np(a_), T.to_np(b_))
+    nores = kernels.swiglu_bwd(*args, add_residual=False)
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref = O.swiglu_bwd(dy, x, gp, uo, h, f64(g), f64(u), f64(d))
+    rel, absd = T.rel_err(T.to_np(nores[0]), ref[0] - dy)
+    assert rel <= TOL, f"dx without residual: rel {rel} abs {absd}"
+    for a_, b_ in zip(nores[1:], op[1:]):
+        assert np.array_equal(T.to_np(a_), T.to_np(b_))
+
+
+def test_layer_autograd(gpu):
+    """MLPBlock(use_swiglu=True) backward through the HIP operator matches the oracle."""
+    import torch
+    from looped_blockell.layers import MLPBlock
+    _say("layer autograd")
+    torch.manual_seed(3)
+    m = MLPBlock(256, 1024, use_swiglu=True, tile_size=32, density=0.25, device="cuda")
+    m.w_up.alive_mask[2, 1] = False            # a pruned tile gets no gradient
+    x = torch.randn(2, 40, 256, device="cuda").to(torch.bfloat16).requires_grad_(True)
+    y = m(x)
+    dy = torch.randn_like(y)
+    y.backward(dy)
+
+    def w(lin):
+        col = lin.col_indices.cpu().numpy().copy()
+        col[~lin.alive_mask.cpu().numpy()] = -1
+        return lin.values.detach().to(torch.bfloat16).float().cpu().numpy().astype(np.float64), col
+
+    xs = T.to_np(x.detach()).reshape(80, 256).astype(np.float64)
+    wg, wu, wd = w(m.w_gate), w(m.w_up), w(m.w_down)
+    _, h, gp, uo = O.swiglu_fwd(xs, wg, wu, wd)
+    gp, uo, h = (O.bf16_round(a.astype(np.float32)) for a in (gp, uo, h))
+    dys = T.to_np(dy).reshape(80, 256)
+    dx, dvg, dvu, dvd = O.swiglu_bwd(dys, xs, gp, uo, h, wg, wu, wd)
+    dx = dx - dys                               # the layer has no residual
+    assert T.rel_err(T.to_np(x.grad).reshape(80, 256), dx)[0] <= TOL
+    for lin, ref in ((m.w_gate, dvg), (m.w_up, dvu), (m.w_down, dvd)):
+        assert T.rel_err(T.to_np(lin.values.grad), ref)[0] <= TOL
+    assert torch.count_nonzero(m.w_up.values.grad[2, 1]).item() == 0
