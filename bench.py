@@ -9,7 +9,8 @@ forward pass.  The line also carries:
                 on the stream the kernel runs on;
   cpu_baseline  the CPU oracle (numpy gather + matmul restatement of the
                 reference layer) timed on the host cores on the same workload;
-  extra         the other workloads (ternary FFN, looped block L=8, decode).
+  extra         the other workloads (shared gate/up topology, the backward of the
+                headline workload, ternary FFN, looped block L=8, decode).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only-main]
 """
@@ -209,6 +210,30 @@ def bench_bf16_shared(steps, warmup, device):
                 kernel_ms_avg=sum(per) / len(per))
 
 
+def bench_bf16_backward(steps, warmup, device):
+    """Backward of the headline workload (titan::block_ell_swiglu_bwd) from the forward's saved
+    tensors: dh, dx and the three tile gradients, twice the forward's nonzero-block FLOPs."""
+    import torch
+    from looped_blockell import kernels
+    w = WORKLOADS["bf16"]
+    gen = torch.Generator(device=device).manual_seed(w["seed"])
+    g, u, d = make_ffn(w, device, gen)
+    x = torch.randn(w["N"], w["d_model"], generator=gen, device=device).to(torch.bfloat16)
+    dy = torch.randn(w["N"], w["d_model"], generator=gen, device=device).to(torch.bfloat16)
+    _, h, gp, uo = kernels.swiglu_fwd_with_intermediate(x, *g, *u, *d, add_residual=True)
+    out = {}
+
+    def step(i):
+        out["r"] = kernels.swiglu_bwd(dy, x, gp, uo, h, *g, *u, *d)
+
+    ms, per = time_steps(step, steps, warmup)
+    flops = 2 * nonzero_flops(w)
+    assert all(torch.isfinite(t.float()).all() for t in out["r"])
+    return dict(workload="backward of the headline workload (dx and the gate/up/down tile gradients)",
+                ms_per_step=ms, value=flops / (ms * 1e-3) / 1e12, unit="TFLOP/s",
+                frac_of_bf16_peak=flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, kernel_ms_avg=sum(per) / len(per))
+
+
 def bench_ternary(steps, warmup, device):
     import torch
     from looped_blockell import kernels
@@ -317,7 +342,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-main", action="store_true", help="headline workload only (for profiling)")
-    ap.add_argument("--only", default="", help="comma list of extra workloads to run: shared,ternary,looped,decode")
+    ap.add_argument("--only", default="",
+                    help="comma list of extra workloads to run: shared,backward,ternary,looped,decode")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one 256 MiB device-to-device copy (a reference point for HBM byte counters)")
     args = ap.parse_args()
@@ -342,8 +368,9 @@ def main():
     main_res = bench_bf16(args.steps, args.warmup, device)
     extra = {}
     if not args.only_main:
-        todo = [s for s in args.only.split(",") if s] or ["shared", "ternary", "looped", "decode"]
-        fns = dict(shared=bench_bf16_shared, ternary=bench_ternary, looped=bench_looped, decode=bench_decode)
+        todo = [s for s in args.only.split(",") if s] or ["shared", "backward", "ternary", "looped", "decode"]
+        fns = dict(shared=bench_bf16_shared, backward=bench_bf16_backward, ternary=bench_ternary,
+                   looped=bench_looped, decode=bench_decode)
         for name in todo:
             st = max(5, args.steps // (4 if name == "looped" else 1))
             try:

@@ -11,17 +11,20 @@
 //                  (r, k) with col[r,k] = c, in ascending r*K + k (ballot
 //                  compaction, deterministic), for gate, up and down in one launch.
 //   tprod_kernel   out[:, c] = sum over the slots of column block c of
-//                  A[:, r] W[r,k]^T.  A workgroup owns 64 tokens x one column
-//                  block; the raw [B_in, B_out] tile is the MFMA's A operand (row
+//                  A[:, r] W[r,k]^T.  A workgroup owns 64 tokens and four column
+//                  blocks, one per wave (each tile is read once per workgroup);
+//                  the raw [B_in, B_out] tile is the MFMA's A operand (row
 //                  d of the tile holds the 8 consecutive B_out values a lane
 //                  needs), the activation rows the B operand, so each lane ends
-//                  with 4 consecutive output columns of one token.  Epilogue:
+//                  with 4 consecutive output columns of one token; two list
+//                  entries are in flight at a time.  Epilogue:
 //                  the SiLU*mul backward (dh -> dg, du) or the optional + dy (-> dx).
 //   dw_kernel      tile gradients: a workgroup owns one block row, up to 8 of
-//                  its slots (one per wave) and a chunk of tokens; 32-token
-//                  slices of X and G are staged transposed in LDS (the token
-//                  index is the MFMA's k) and every wave accumulates its tile in
-//                  fp32; the chunk's partial tile goes to the workspace.
+//                  its slots (one per wave) and a chunk of tokens; token slices
+//                  of X and G are staged row-major in LDS and read back
+//                  transposed with ds_read_b64_tr_b16 (the token index is the
+//                  MFMA's k); every wave accumulates its tile in fp32 and the
+//                  chunk's partial tile goes to the workspace.
 //   dw_reduce_kernel  sums the chunks' partials in fixed order -> bf16 (dead slots 0).
 // No atomics anywhere: every sum has a fixed order, so the results are deterministic.
 #include "lbk_device.h"
@@ -87,78 +90,112 @@ template <int B, int MODE>
 __global__ __launch_bounds__(256) void tprod_kernel(TProdArgs a) {
   constexpr int CW = B / 16;                 // 16-column groups of a tile
   constexpr int NKS = B >= 32 ? B / 32 : 1;  // 32-deep k-steps
+  constexpr int TQ = 4;                      // 16-token groups of the workgroup's 64 tokens
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = uniform(tid >> 6);
   const int i = lane & 15, g = lane >> 4;
-  const int c = (int)blockIdx.y;
-  const int64_t tn = (int64_t)blockIdx.x * 64 + 16 * w + i;   // this lane's token
-  const int64_t tl = tn < a.N ? tn : a.N - 1;                 // clamped row for the loads
+  const int c = (int)blockIdx.y * 4 + w;     // this wave's output column block
+  if (c >= a.C) return;                      // no barrier in this kernel
+  const int64_t t0 = (int64_t)blockIdx.x * 64;
   // B = 16: a tile row has 16 values, so lanes g >= 2 (k 16..31) read lane g - 2's bytes and
   // carry zeros in the activation operand
   const int gk = (B == 16) ? (g & 1) : g;
   const bool kz = (B == 16) && g >= 2;
-  f32x4 acc[CW];
+  int64_t trow[TQ];                          // clamped token rows of the lane's B fragments
 #pragma unroll
-  for (int m = 0; m < CW; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < TQ; ++q) {
+    const int64_t t = t0 + 16 * q + i;
+    trow[q] = t < a.N ? t : a.N - 1;
+  }
+  f32x4 acc[TQ][CW];
+#pragma unroll
+  for (int q = 0; q < TQ; ++q)
+#pragma unroll
+    for (int m = 0; m < CW; ++m) acc[q][m] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // operands of one list entry: activation fragments of the 64 tokens (B operand) and the
+  // tile rows (A operand)
+  struct Ent {
+    u32x4 bv[NKS][TQ], av[NKS][CW];
+  };
   for (int s = 0; s < a.nsrc; ++s) {
     const TProdSrc S = a.src[s];
     const int cnt = S.cnt[c];
     const int32_t* L = S.list + (int64_t)c * S.cap;
-    const uint16_t* arow = S.a + tl * S.lda + 8 * gk;
+    auto load = [&](int e, Ent& E) {
+      const int r = e / S.K;
+      const uint16_t* tile = S.w + (int64_t)e * B * B + (int64_t)i * B + 8 * gk;
+      const uint16_t* acol = S.a + (int64_t)r * B + 8 * gk;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+        for (int m = 0; m < CW; ++m) E.av[ks][m] = ld16(tile + 16 * m * B + 32 * ks);   // W[16m + i][32ks + 8g ..]
+#pragma unroll
+        for (int q = 0; q < TQ; ++q) E.bv[ks][q] = ld16(acol + trow[q] * S.lda + 32 * ks);
+      }
+    };
+    auto compute = [&](const Ent& E) {
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+        for (int q = 0; q < TQ; ++q) {
+          const u32x4 bv = kz ? u32x4{0, 0, 0, 0} : E.bv[ks][q];
+#pragma unroll
+          for (int m = 0; m < CW; ++m) acc[q][m] = mfma_bf16(E.av[ks][m], bv, acc[q][m]);
+        }
+    };
     for (int j0 = 0; j0 < cnt; j0 += 64) {
       const int lv = (j0 + lane < cnt) ? L[j0 + lane] : 0;   // 64 entries, one per lane
       const int jn = (cnt - j0) < 64 ? (cnt - j0) : 64;
-      for (int jj = 0; jj < jn; ++jj) {
-        const int e = __builtin_amdgcn_readlane(lv, jj);
-        const int r = e / S.K;
-        const uint16_t* tile = S.w + (int64_t)e * B * B + (int64_t)i * B + 8 * gk;
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          const u32x4 bv0 = ld16(arow + (int64_t)r * B + 32 * ks);
-          const u32x4 bv = kz ? u32x4{0, 0, 0, 0} : bv0;
-#pragma unroll
-          for (int m = 0; m < CW; ++m) {
-            const u32x4 av = ld16(tile + 16 * m * B + 32 * ks);   // W[16m + i][32ks + 8g ..]
-            acc[m] = mfma_bf16(av, bv, acc[m]);
-          }
-        }
+      // two entries in flight: every load goes out (entries past the end re-read the last one)
+      auto ent = [&](int jj) { return __builtin_amdgcn_readlane(lv, jj < jn ? jj : jn - 1); };
+      Ent E0, E1;
+      load(ent(0), E0);
+      for (int jj = 0; jj < jn; jj += 2) {
+        load(ent(jj + 1), E1);
+        compute(E0);
+        load(ent(jj + 2), E0);
+        if (jj + 1 < jn) compute(E1);
       }
     }
   }
 
-  // lane (i, g) holds out[token tn][c*B + 16m + 4g + v], v < 4
-  if (tn >= a.N) return;
+  // lane (i, g) of acc[q][m] holds out[token t0 + 16q + i][c*B + 16m + 4g + v], v < 4
 #pragma unroll
-  for (int m = 0; m < CW; ++m) {
-    const int64_t off = tn * a.ldo + (int64_t)c * B + 16 * m + 4 * g;
-    float o[4];
-    if constexpr (MODE == 0) {
-      float gv[4], uv[4], dgv[4], duv[4];
-      load_bf16<4>(a.g + off, gv);
-      load_bf16<4>(a.u + off, uv);
+  for (int q = 0; q < TQ; ++q) {
+    const int64_t tn = t0 + 16 * q + i;
+    if (tn >= a.N) continue;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float dh = acc[m][v];
-        const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-gv[v]));   // sigmoid(g)
-        dgv[v] = dh * uv[v] * (sg + gv[v] * sg * (1.0f - sg));
-        duv[v] = dh * gv[v] * sg;
+    for (int m = 0; m < CW; ++m) {
+      const int64_t off = tn * a.ldo + (int64_t)c * B + 16 * m + 4 * g;
+      float o[4];
+      if constexpr (MODE == 0) {
+        float gv[4], uv[4], dgv[4], duv[4];
+        load_bf16<4>(a.g + off, gv);
+        load_bf16<4>(a.u + off, uv);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float dh = acc[q][m][v];
+          const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-gv[v]));   // sigmoid(g)
+          dgv[v] = dh * uv[v] * (sg + gv[v] * sg * (1.0f - sg));
+          duv[v] = dh * gv[v] * sg;
+        }
+        store_bf16<4>(a.dg + off, dgv);
+        store_bf16<4>(a.du + off, duv);
+      } else {
+        float rv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (a.resid) load_bf16<4>(a.resid + off, rv);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) o[v] = acc[q][m][v] + rv[v];
+        store_bf16<4>(a.out + off, o);
       }
-      store_bf16<4>(a.dg + off, dgv);
-      store_bf16<4>(a.du + off, duv);
-    } else {
-      float rv[4] = {0.f, 0.f, 0.f, 0.f};
-      if (a.resid) load_bf16<4>(a.resid + off, rv);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) o[v] = acc[m][v] + rv[v];
-      store_bf16<4>(a.out + off, o);
     }
   }
 }
 
 int launch_tprod(int B, int mode, const TProdArgs& a, hipStream_t st) {
   if (a.N == 0 || a.C == 0) return 0;
-  const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)a.C);
+  const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)((a.C + 3) / 4));
 #define LBK_TP(BB)                                                                      \
   if (B == BB) {                                                                        \
     if (mode == 0) hipLaunchKernelGGL((tprod_kernel<BB, 0>), grid, dim3(256), 0, st, a); \
@@ -173,12 +210,34 @@ int launch_tprod(int B, int mode, const TProdArgs& a, hipStream_t st) {
 // ---------------------------------------------------------------------------
 // tile gradients
 // ---------------------------------------------------------------------------
-constexpr int DW_TS = 32;   // tokens per staged slice (one MFMA k-step)
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane l receives element l % 4 of the 64-bit
+// blocks read by lanes l / 4, 4 + l / 4, 8 + l / 4 and 12 + l / 4 of the group (measured on
+// gfx950).  So if lane s of a group points at row t0 + s / 4, columns c0 + 4 (s % 4) .. + 3 of a
+// row-major [token][column] slice, lane l gets column c0 + l of tokens t0 .. t0 + 3: two such
+// reads give the 8 consecutive tokens (the MFMA's k) of one column that an operand lane holds.
+__device__ __forceinline__ u32x4 tr_frag(const uint16_t* slice, int rowlen, int t0, int c0, int lane) {
+  const int s = lane & 15, g = lane >> 4;
+  const uint16_t* p = slice + (t0 + 8 * g + (s >> 2)) * rowlen + c0 + 4 * (s & 3);
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * rowlen));
+  const u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
+
+template <int B>
+struct DWShape {
+  static constexpr int TS = B == 64 ? 32 : 64;   // tokens per staged slice
+  static constexpr int ROW = B + 8;              // LDS row length in elements (16 bytes of padding)
+};
 
 template <int B>
 __global__ __launch_bounds__(512) void dw_kernel(DWJobs jobs) {
   constexpr int CW = B / 16;
   constexpr int CPT = B / 8;                 // 16-byte chunks per token row of a tile
+  constexpr int TS = DWShape<B>::TS, ROW = DWShape<B>::ROW;
   int jt = 0;
 #pragma unroll
   for (int u = 1; u < DWJobs::kMax; ++u)
@@ -196,9 +255,9 @@ __global__ __launch_bounds__(512) void dw_kernel(DWJobs jobs) {
   const bool slot = k < J.K;
   const int col = slot ? J.col[(int64_t)r * J.K + k] : -1;
   const bool live = col >= 0 && col < J.C;
-  // LDS, transposed slices: xt[wave][column][token], gt[column][token]
-  __shared__ __attribute__((aligned(16))) uint16_t xt[8][B][DW_TS];
-  __shared__ __attribute__((aligned(16))) uint16_t gt[B][DW_TS];
+  // LDS: row-major token slices, xs[wave][token][column] of X, gs[token][column] of G
+  __shared__ __attribute__((aligned(16))) uint16_t xs[8][TS * ROW];
+  __shared__ __attribute__((aligned(16))) uint16_t gs[TS * ROW];
 
   f32x4 acc[CW][CW];
 #pragma unroll
@@ -210,41 +269,36 @@ __global__ __launch_bounds__(512) void dw_kernel(DWJobs jobs) {
   const int64_t tend = (tbeg + jobs.chunk) < jobs.N ? (tbeg + jobs.chunk) : jobs.N;
   const int64_t xcol = (int64_t)(live ? col : 0) * B;
   const int64_t gcol = (int64_t)r * B;
-  for (int64_t t0 = tbeg; t0 < tend; t0 += DW_TS) {
-    // stage: every chunk (token, 8 columns) is loaded at a clamped row, zeroed beyond N,
-    // and written transposed (8 two-byte stores)
-    for (int q = lane; q < DW_TS * CPT; q += 64) {            // this wave's X slice
+  for (int64_t t0 = tbeg; t0 < tend; t0 += TS) {
+    // stage: each 16-byte chunk (token, 8 columns) is loaded at a clamped row, zeroed beyond
+    // the chunk, and stored as it is
+#pragma unroll
+    for (int q0 = 0; q0 < TS * CPT; q0 += 64) {               // this wave's X slice
+      const int q = q0 + lane;
       const int tt = q / CPT, cc = q - tt * CPT;
       const int64_t t = t0 + tt;
       const u32x4 v0 = ld16(J.x + (t < jobs.N ? t : jobs.N - 1) * J.ldx + xcol + 8 * cc);
-      const u32x4 v = (t < tend) ? v0 : u32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        xt[w][8 * cc + 2 * p][tt] = (uint16_t)(v[p] & 0xffffu);
-        xt[w][8 * cc + 2 * p + 1][tt] = (uint16_t)(v[p] >> 16);
-      }
+      *reinterpret_cast<u32x4*>(&xs[w][tt * ROW + 8 * cc]) = (t < tend) ? v0 : u32x4{0, 0, 0, 0};
     }
-    for (int q = tid; q < DW_TS * CPT; q += 512) {            // the G slice, shared
+    for (int q = tid; q < TS * CPT; q += 512) {               // the G slice, shared
       const int tt = q / CPT, cc = q - tt * CPT;
       const int64_t t = t0 + tt;
       const u32x4 v0 = ld16(J.gy + (t < jobs.N ? t : jobs.N - 1) * J.ldg + gcol + 8 * cc);
-      const u32x4 v = (t < tend) ? v0 : u32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        gt[8 * cc + 2 * p][tt] = (uint16_t)(v[p] & 0xffffu);
-        gt[8 * cc + 2 * p + 1][tt] = (uint16_t)(v[p] >> 16);
-      }
+      *reinterpret_cast<u32x4*>(&gs[tt * ROW + 8 * cc]) = (t < tend) ? v0 : u32x4{0, 0, 0, 0};
     }
     __syncthreads();
-    // dW[d][D] += sum_t X[t][d] G[t][D]: A operand lane (i, g) = X^T[16md + i][8g ..],
-    // B operand lane (n, g) = G^T[16mD + n][8g ..]
+    // dW[d][D] += sum_t X[t][d] G[t][D]: A operand = X^T (lane: column 16md + i, 8 tokens),
+    // B operand = G (lane: column 16mD + n, the same 8 tokens)
 #pragma unroll
-    for (int md = 0; md < CW; ++md) {
-      const u32x4 av = *reinterpret_cast<const u32x4*>(&xt[w][16 * md + i][8 * g]);
+    for (int ks = 0; ks < TS / 32; ++ks) {
+      u32x4 bv[CW];
 #pragma unroll
-      for (int mD = 0; mD < CW; ++mD) {
-        const u32x4 bv = *reinterpret_cast<const u32x4*>(&gt[16 * mD + i][8 * g]);
-        acc[md][mD] = mfma_bf16(av, bv, acc[md][mD]);
+      for (int mD = 0; mD < CW; ++mD) bv[mD] = tr_frag(gs, ROW, 32 * ks, 16 * mD, lane);
+#pragma unroll
+      for (int md = 0; md < CW; ++md) {
+        const u32x4 av = tr_frag(xs[w], ROW, 32 * ks, 16 * md, lane);
+#pragma unroll
+        for (int mD = 0; mD < CW; ++mD) acc[md][mD] = mfma_bf16(av, bv[mD], acc[md][mD]);
       }
     }
     __syncthreads();
@@ -279,7 +333,7 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(DWJobs jobs, int B) {
 }
 
 int launch_dw(int B, const DWJob* jobs, int n, int64_t N, int chunk, hipStream_t st) {
-  if (n < 1 || n > DWJobs::kMax || chunk < DW_TS || chunk % DW_TS) return -2;
+  if (n < 1 || n > DWJobs::kMax || chunk < 64 || chunk % 64) return -2;   // whole slices of 32 and 64 tokens
   DWJobs J{};
   J.n = n;
   J.N = N;
