@@ -19,6 +19,11 @@
 //                  with 4 consecutive output columns of one token; two list
 //                  entries are in flight at a time.  Epilogue:
 //                  the SiLU*mul backward (dh -> dg, du) or the optional + dy (-> dx).
+//   dh_panel_kernel  dh -> dg, du when d_model <= 2048: the dy rows of 64 (32)
+//                  tokens sit in LDS as the forward's XOR-swizzled panel and each
+//                  of 8 waves streams the list entries of its column blocks
+//                  (c = w, w + 8, ...): tile rows from global memory, dy
+//                  fragments from the panel.
 //   dw_kernel      tile gradients: a workgroup owns one block row, up to 8 of
 //                  its slots (one per wave) and a chunk of tokens; token slices
 //                  of X and G are staged row-major in LDS and read back
@@ -86,6 +91,63 @@ int launch_tlist(const TListJob* jobs, int n, hipStream_t st) {
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
+// Tile row that operand lane i loads for 16-row group m (CW = B / 16 groups).  With CW >= 2 the
+// groups interleave in fours, d = 32 (m / 2) + 8 (i / 4) + 4 (m % 2) + i % 4, so that the
+// accumulator lane (n, g) ends with the 8 consecutive output columns 32 p + 8 g .. + 7 of groups
+// m = 2p, 2p + 1 (16-byte epilogue loads and stores); with CW = 1 (B = 16) d = i.
+template <int CW>
+__device__ __forceinline__ int op_row(int i, int m) {
+  if constexpr (CW == 1) return i;
+  else return 32 * (m >> 1) + 8 * (i >> 2) + 4 * (m & 1) + (i & 3);
+}
+
+// epilogue of one token row: the lane's accumulator values v8 (8 consecutive columns starting at
+// col, or 4 for B = 16): SiLU*mul backward (MODE 0) or + residual (MODE 1)
+template <int MODE, int NV>
+__device__ __forceinline__ void tprod_epilogue(const TProdArgs& a, int64_t off, const float (&v)[NV]) {
+  if constexpr (MODE == 0) {
+    float gv[NV], uv[NV], dgv[NV], duv[NV];
+    load_bf16x<NV>(a.g + off, gv);
+    load_bf16x<NV>(a.u + off, uv);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-gv[j]));   // sigmoid(g)
+      dgv[j] = v[j] * uv[j] * (sg + gv[j] * sg * (1.0f - sg));
+      duv[j] = v[j] * gv[j] * sg;
+    }
+    store_bf16x<NV>(a.dg + off, dgv);
+    store_bf16x<NV>(a.du + off, duv);
+  } else {
+    float rv[NV], o[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) rv[j] = 0.f;
+    if (a.resid) load_bf16x<NV>(a.resid + off, rv);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) o[j] = v[j] + rv[j];
+    store_bf16x<NV>(a.out + off, o);
+  }
+}
+
+// lane (i, g) of acc[m] (one 16-token group): columns of output block c of token tn
+template <int MODE, int CW>
+__device__ __forceinline__ void tprod_store(const TProdArgs& a, int64_t tn, int c, int g, const f32x4 (&acc)[CW]) {
+  constexpr int B = 16 * CW;
+  if constexpr (CW == 1) {
+    float v[4] = {acc[0][0], acc[0][1], acc[0][2], acc[0][3]};
+    tprod_epilogue<MODE, 4>(a, tn * a.ldo + (int64_t)c * B + 4 * g, v);
+  } else {
+#pragma unroll
+    for (int p = 0; p < CW / 2; ++p) {
+      float v[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[4 * h + u] = acc[2 * p + h][u];
+      tprod_epilogue<MODE, 8>(a, tn * a.ldo + (int64_t)c * B + 32 * p + 8 * g, v);
+    }
+  }
+}
+
 template <int B, int MODE>
 __global__ __launch_bounds__(256) void tprod_kernel(TProdArgs a) {
   constexpr int CW = B / 16;                 // 16-column groups of a tile
@@ -124,12 +186,12 @@ __global__ __launch_bounds__(256) void tprod_kernel(TProdArgs a) {
     const int32_t* L = S.list + (int64_t)c * S.cap;
     auto load = [&](int e, Ent& E) {
       const int r = e / S.K;
-      const uint16_t* tile = S.w + (int64_t)e * B * B + (int64_t)i * B + 8 * gk;
+      const uint16_t* tile = S.w + (int64_t)e * B * B + 8 * gk;
       const uint16_t* acol = S.a + (int64_t)r * B + 8 * gk;
 #pragma unroll
       for (int ks = 0; ks < NKS; ++ks) {
 #pragma unroll
-        for (int m = 0; m < CW; ++m) E.av[ks][m] = ld16(tile + 16 * m * B + 32 * ks);   // W[16m + i][32ks + 8g ..]
+        for (int m = 0; m < CW; ++m) E.av[ks][m] = ld16(tile + op_row<CW>(i, m) * B + 32 * ks);
 #pragma unroll
         for (int q = 0; q < TQ; ++q) E.bv[ks][q] = ld16(acol + trow[q] * S.lda + 32 * ks);
       }
@@ -160,41 +222,184 @@ __global__ __launch_bounds__(256) void tprod_kernel(TProdArgs a) {
     }
   }
 
-  // lane (i, g) of acc[q][m] holds out[token t0 + 16q + i][c*B + 16m + 4g + v], v < 4
+  // lane (i, g) of acc[q] holds token t0 + 16q + i (columns as op_row arranges them)
 #pragma unroll
   for (int q = 0; q < TQ; ++q) {
     const int64_t tn = t0 + 16 * q + i;
-    if (tn >= a.N) continue;
+    if (tn < a.N) tprod_store<MODE, CW>(a, tn, c, g, acc[q]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dh = dy W_down -> dg, du with the dy rows of the workgroup's tokens in LDS
+// ---------------------------------------------------------------------------
+// The panel layout of the forward's gate/up kernel: token row 16*q + n of the 16*MT rows sits at
+// row slot n*MT + q, and its 16-byte chunk c at chunk c ^ n.
+template <int MT>
+__device__ __forceinline__ uint32_t bpanel_addr(int row, int chunk, int rowb) {
+  const int n = row & 15, q = row >> 4;
+  return (uint32_t)((n * MT + q) * rowb + ((chunk ^ n) << 4));
+}
+
+template <int B, int MT>
+__global__ __launch_bounds__(512, 1) void dh_panel_kernel(TProdArgs a) {
+  constexpr int CW = B / 16;
+  constexpr int NKS = B >= 32 ? B / 32 : 1;
+  constexpr int TM = 16 * MT;
+  constexpr int ROWB = 8192 / MT;            // panel row stride: 2048 B (MT = 4) or 4096 B (MT = 2)
+  extern __shared__ __attribute__((aligned(16))) unsigned char panel[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = uniform(tid >> 6);
+  const int i = lane & 15, g = lane >> 4;
+  const int64_t t0 = (int64_t)blockIdx.x * TM;
+  const TProdSrc S = a.src[0];
+  const int d_model = (int)S.lda;
+
+  // ---- panel: dy rows t0 .. t0 + TM - 1, every load at a clamped address
+  {
+    constexpr int CPR = ROWB / 16;
+    constexpr int PIT = TM * CPR / 512;
+    const int cpr = d_model / 8;
+    u32x4 pv[PIT];
 #pragma unroll
-    for (int m = 0; m < CW; ++m) {
-      const int64_t off = tn * a.ldo + (int64_t)c * B + 16 * m + 4 * g;
-      float o[4];
-      if constexpr (MODE == 0) {
-        float gv[4], uv[4], dgv[4], duv[4];
-        load_bf16<4>(a.g + off, gv);
-        load_bf16<4>(a.u + off, uv);
+    for (int it = 0; it < PIT; ++it) {
+      const int e = tid + 512 * it;
+      const int row = e / CPR, cc = e % CPR;
+      const int64_t t = t0 + row;
+      const bool ok = cc < cpr && t < a.N;
+      pv[it] = ld16(S.a + (ok ? t : t0) * d_model + 8 * (ok ? cc : 0));
+    }
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float dh = acc[q][m][v];
-          const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-gv[v]));   // sigmoid(g)
-          dgv[v] = dh * uv[v] * (sg + gv[v] * sg * (1.0f - sg));
-          duv[v] = dh * gv[v] * sg;
+    for (int it = 0; it < PIT; ++it) {
+      const int e = tid + 512 * it;
+      const int row = e / CPR, cc = e % CPR;
+      const bool ok = cc < cpr && t0 + row < a.N;
+      if (cc < cpr) *reinterpret_cast<u32x4*>(panel + bpanel_addr<MT>(row, cc, ROWB)) = ok ? pv[it] : u32x4{0, 0, 0, 0};
+    }
+  }
+  __syncthreads();
+
+  const int gk = (B == 16) ? (g & 1) : g;
+  const bool kz = (B == 16) && g >= 2;
+  const uint32_t lbase = (uint32_t)(i * MT * ROWB);
+  struct Ent {
+    u32x4 av[NKS][CW];
+    int r;
+  };
+  auto load = [&](int e, Ent& E) {
+    const uint16_t* tile = S.w + (int64_t)e * B * B + 8 * gk;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+      for (int m = 0; m < CW; ++m) E.av[ks][m] = ld16(tile + op_row<CW>(i, m) * B + 32 * ks);
+    E.r = e / S.K;
+  };
+  f32x4 acc[MT][CW];
+  auto compute = [&](const Ent& E) {
+    const int r = uniform(E.r);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const uint32_t pa = lbase + ((((r * (B / 8) + 4 * ks + gk)) ^ i) << 4);
+#pragma unroll
+      for (int q = 0; q < MT; ++q) {
+        const u32x4 bv0 = *reinterpret_cast<const u32x4*>(panel + pa + q * ROWB);   // dy[16q + i][r*B + 32ks + 8g ..]
+        const u32x4 bv = kz ? u32x4{0, 0, 0, 0} : bv0;
+#pragma unroll
+        for (int m = 0; m < CW; ++m) acc[q][m] = mfma_bf16(E.av[ks][m], bv, acc[q][m]);
+      }
+    }
+  };
+
+  // the gate pre-activation and up output at this lane's outputs, fetched before the entries
+  // of a column block so that their latency overlaps its MFMAs (clamped rows, always loaded)
+  constexpr int NV = CW == 1 ? 4 : 8, NP = CW == 1 ? 1 : CW / 2;
+  typedef uint32_t raw_t __attribute__((ext_vector_type(NV / 2)));
+  raw_t graw[MT][NP], uraw[MT][NP];
+  auto col_of = [&](int c, int p) { return (int64_t)c * B + (CW == 1 ? 4 * g : 32 * p + 8 * g); };
+  for (int c = w; c < a.C; c += 8) {
+#pragma unroll
+    for (int q = 0; q < MT; ++q) {
+      const int64_t tn = t0 + 16 * q + i;
+      const int64_t row = (tn < a.N ? tn : a.N - 1) * a.ldo;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        graw[q][p] = *reinterpret_cast<const raw_t*>(a.g + row + col_of(c, p));
+        uraw[q][p] = *reinterpret_cast<const raw_t*>(a.u + row + col_of(c, p));
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < MT; ++q)
+#pragma unroll
+      for (int m = 0; m < CW; ++m) acc[q][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int cnt = S.cnt[c];
+    const int32_t* L = S.list + (int64_t)c * S.cap;
+    for (int j0 = 0; j0 < cnt; j0 += 64) {
+      const int lv = (j0 + lane < cnt) ? L[j0 + lane] : 0;   // 64 entries, one per lane
+      const int jn = (cnt - j0) < 64 ? (cnt - j0) : 64;
+      auto ent = [&](int jj) { return __builtin_amdgcn_readlane(lv, jj < jn ? jj : jn - 1); };
+      Ent E0, E1;
+      load(ent(0), E0);
+      for (int jj = 0; jj < jn; jj += 2) {
+        load(ent(jj + 1), E1);
+        compute(E0);
+        load(ent(jj + 2), E0);
+        if (jj + 1 < jn) compute(E1);
+      }
+    }
+    // epilogue: lane (i, g) of acc[q] holds dh of token t0 + 16q + i (columns as op_row
+    // arranges them): dg = dh * u * silu'(g), du = dh * silu(g)
+#pragma unroll
+    for (int q = 0; q < MT; ++q) {
+      const int64_t tn = t0 + 16 * q + i;
+      if (tn >= a.N) continue;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        float dh[NV], dgv[NV], duv[NV];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) dh[j] = acc[q][CW == 1 ? 0 : 2 * p + j / 4][j % 4];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+          const uint32_t gw = graw[q][p][j / 2], uw = uraw[q][p][j / 2];
+          const float gv = (j & 1) ? bf_hi(gw) : bf_lo(gw), uv = (j & 1) ? bf_hi(uw) : bf_lo(uw);
+          const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-gv));   // sigmoid(g)
+          dgv[j] = dh[j] * uv * (sg + gv * sg * (1.0f - sg));
+          duv[j] = dh[j] * gv * sg;
         }
-        store_bf16<4>(a.dg + off, dgv);
-        store_bf16<4>(a.du + off, duv);
-      } else {
-        float rv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (a.resid) load_bf16<4>(a.resid + off, rv);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) o[v] = acc[q][m][v] + rv[v];
-        store_bf16<4>(a.out + off, o);
+        store_bf16x<NV>(a.dg + tn * a.ldo + col_of(c, p), dgv);
+        store_bf16x<NV>(a.du + tn * a.ldo + col_of(c, p), duv);
       }
     }
   }
 }
 
+// dh through the LDS panel when the dy rows of 16*MT tokens fit (d_model <= 2048, one source)
+template <int B, int MT>
+static int launch_dh_panel_t(const TProdArgs& a, hipStream_t st) {
+  constexpr size_t lds = (size_t)16 * MT * (8192 / MT);
+  auto kern = dh_panel_kernel<B, MT>;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds) != hipSuccess)
+    return -1;
+  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 16 * MT - 1) / (16 * MT))), dim3(512), lds, st, a);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+static int launch_dh_panel(int B, const TProdArgs& a, hipStream_t st) {
+  const int64_t d_model = a.src[0].lda;
+  const int mt = d_model <= 1024 ? 4 : (d_model <= 2048 ? 2 : 0);
+  if (mt == 0 || d_model % 8) return -2;
+#define LBK_DH(BB, MM) if (B == BB && mt == MM) return launch_dh_panel_t<BB, MM>(a, st);
+  LBK_DH(16, 4) LBK_DH(16, 2) LBK_DH(32, 4) LBK_DH(32, 2) LBK_DH(64, 4) LBK_DH(64, 2)
+#undef LBK_DH
+  return -2;
+}
+
 int launch_tprod(int B, int mode, const TProdArgs& a, hipStream_t st) {
   if (a.N == 0 || a.C == 0) return 0;
+  if (mode == 0 && a.nsrc == 1) {
+    const int rc = launch_dh_panel(B, a, st);
+    if (rc != -2) return rc;
+  }
   const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)((a.C + 3) / 4));
 #define LBK_TP(BB)                                                                      \
   if (B == BB) {                                                                        \

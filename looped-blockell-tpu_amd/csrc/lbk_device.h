@@ -198,6 +198,38 @@ __device__ __forceinline__ void store_bf16<4>(uint16_t* p, const float (&v)[4]) 
   *reinterpret_cast<u32x2*>(p) = w;
 }
 
+// Store NV (4 or 8) consecutive bf16 values with one 8- or 16-byte store.
+template <int NV>
+__device__ __forceinline__ void store_bf16x(uint16_t* p, const float (&v)[NV]) {
+  if constexpr (NV == 8) {
+    *reinterpret_cast<u32x4*>(p) = u32x4{pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]), pack2_bf16(v[4], v[5]),
+                                         pack2_bf16(v[6], v[7])};
+  } else {
+    static_assert(NV == 4, "4 or 8 values");
+    *reinterpret_cast<u32x2*>(p) = u32x2{pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3])};
+  }
+}
+
+// Load NV (4 or 8) consecutive bf16 values as floats with one 8- or 16-byte load.
+template <int NV>
+__device__ __forceinline__ void load_bf16x(const uint16_t* p, float (&v)[NV]) {
+  if constexpr (NV == 8) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      v[2 * u] = bf_lo(w[u]);
+      v[2 * u + 1] = bf_hi(w[u]);
+    }
+  } else {
+    static_assert(NV == 4, "4 or 8 values");
+    const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+    v[0] = bf_lo(w[0]);
+    v[1] = bf_hi(w[0]);
+    v[2] = bf_lo(w[1]);
+    v[3] = bf_hi(w[1]);
+  }
+}
+
 // Load CW contiguous bf16 values as floats.
 template <int CW>
 __device__ __forceinline__ void load_bf16(const uint16_t* p, float (&v)[CW]);

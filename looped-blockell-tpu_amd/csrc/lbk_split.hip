@@ -41,18 +41,6 @@ __device__ __forceinline__ u32x4 lds16(const unsigned char* base, uint32_t off) 
 // ROWB apart and fit the ds_read immediate offset), and 16-byte chunk c of it
 // at chunk c ^ i (i = row & 15), which keeps the eight lanes of one LDS read
 // phase on distinct banks.
-// store NV (4 or 8) consecutive bf16 values with one 8- or 16-byte store
-template <int NV>
-__device__ __forceinline__ void store_bf16x(uint16_t* p, const float (&v)[NV]) {
-  if constexpr (NV == 8) {
-    *reinterpret_cast<u32x4*>(p) = u32x4{pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]), pack2_bf16(v[4], v[5]),
-                                         pack2_bf16(v[6], v[7])};
-  } else {
-    static_assert(NV == 4, "4 or 8 values");
-    *reinterpret_cast<u32x2*>(p) = u32x2{pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3])};
-  }
-}
-
 template <int MT>
 __device__ __forceinline__ uint32_t panel_addr(int row, int chunk, int rowb) {
   const int i = row & 15, mt = row >> 4;
