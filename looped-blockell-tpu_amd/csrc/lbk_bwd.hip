@@ -394,10 +394,196 @@ static int launch_dh_panel(int B, const TProdArgs& a, hipStream_t st) {
   return -2;
 }
 
+// ---------------------------------------------------------------------------
+// dx = dg W_gate + du W_up (+ dy) with the activations staged through LDS
+// ---------------------------------------------------------------------------
+// A workgroup owns 64 tokens and every output column block: wave w owns blocks c = w + 8 o
+// (o < OPW).  The columns of dg, then du, pass through LDS 512 at a time (double buffered, the
+// next stage's loads in flight during the current one, as in the forward's down kernel).  A
+// block's list is sorted by slot, hence by the source column block r = e / K, so the entries of
+// a stage are the next run of the list: a cursor per block walks it, 64 entries at a time held
+// one per lane.
+// activation columns per stage: 512 (longer runs of a block's list per stage), 256 for B = 64
+// (its larger accumulators leave no registers for the bigger stage)
+template <int B>
+struct DxStage { static constexpr int COLS = B == 64 ? 256 : 512; };
+
+template <int B, int OPW>
+__global__ __launch_bounds__(512, 1) void dx_stage_kernel(TProdArgs a) {
+  constexpr int CW = B / 16;
+  constexpr int NKS = B >= 32 ? B / 32 : 1;
+  constexpr int MT = 4;
+  constexpr int COLS = DxStage<B>::COLS;
+  constexpr int G = COLS / B;                        // source column blocks per stage
+  constexpr int SROWB = COLS * 2;                    // bytes per token row of a stage
+  constexpr int SBYTES = 64 * SROWB;                 // 64 KB (32 KB for B = 64)
+  constexpr int PER_T = SBYTES / 16 / 512;           // 16-byte chunks per thread per stage
+  extern __shared__ __attribute__((aligned(16))) unsigned char stg[];   // two stages
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = uniform(tid >> 6);
+  const int i = lane & 15, g = lane >> 4;
+  const int64_t t0 = (int64_t)blockIdx.x * 64;
+  const int gk = (B == 16) ? (g & 1) : g;
+  const bool kz = (B == 16) && g >= 2;
+
+  // stages: source s covers ceil(R_s / G) stages; global stage -> (source, first block)
+  const int R0 = (int)(a.src[0].lda / B);
+  const int ns0 = (R0 + G - 1) / G;
+  const int ns1 = a.nsrc > 1 ? ((int)(a.src[1].lda / B) + G - 1) / G : 0;
+  const int nstages = ns0 + ns1;
+
+  u32x4 sreg[PER_T];
+  auto stage_fetch = [&](int s) {
+    const TProdSrc& S = a.src[s < ns0 ? 0 : 1];
+    const int64_t col0 = (int64_t)(s < ns0 ? s : s - ns0) * COLS;
+#pragma unroll
+    for (int u = 0; u < PER_T; ++u) {
+      const int e = tid + 512 * u;
+      const int row = e / (SROWB / 16), cc = e - row * (SROWB / 16);
+      const int64_t t = t0 + row, col = col0 + 8 * cc;
+      const bool ok = t < a.N && col < S.lda;
+      const u32x4 v = ld16(S.a + (ok ? t : t0) * S.lda + (ok ? col : 0));
+      sreg[u] = ok ? v : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto stage_store = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < PER_T; ++u) {
+      const int e = tid + 512 * u;
+      const int row = e / (SROWB / 16), cc = e - row * (SROWB / 16);
+      *reinterpret_cast<u32x4*>(stg + buf * SBYTES + bpanel_addr<MT>(row, cc, SROWB)) = sreg[u];
+    }
+  };
+
+  f32x4 acc[OPW][MT][CW];
+#pragma unroll
+  for (int o = 0; o < OPW; ++o)
+#pragma unroll
+    for (int q = 0; q < MT; ++q)
+#pragma unroll
+      for (int m = 0; m < CW; ++m) acc[o][q][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  struct Ent {
+    u32x4 av[NKS][CW];
+    int r;                                           // source column block
+  };
+  const uint32_t lbase = (uint32_t)(i * MT * SROWB);
+  int cur[OPW];                                      // list cursors of the current source
+
+  stage_fetch(0);
+  stage_store(0);
+  __syncthreads();
+  for (int s = 0; s < nstages; ++s) {
+    const int src = s < ns0 ? 0 : 1;
+    const int st = s < ns0 ? s : s - ns0;
+    const TProdSrc& S = a.src[src];
+    if (st == 0) {
+#pragma unroll
+      for (int o = 0; o < OPW; ++o) cur[o] = 0;
+    }
+    if (s + 1 < nstages) stage_fetch(s + 1);
+    const unsigned char* sb = stg + (s & 1) * SBYTES;
+    const int rlo = st * G, rhi = rlo + G;           // source column blocks of this stage
+    auto load = [&](int e, Ent& E) {
+      const uint16_t* tile = S.w + (int64_t)e * B * B + 8 * gk;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+        for (int m = 0; m < CW; ++m) E.av[ks][m] = ld16(tile + op_row<CW>(i, m) * B + 32 * ks);
+      E.r = e / S.K;
+    };
+#pragma unroll
+    for (int o = 0; o < OPW; ++o) {
+      const int c = w + 8 * o;
+      if (c >= a.C) continue;
+      auto compute = [&](const Ent& E) {
+        const int rb = uniform(E.r) - rlo;           // column block within the stage
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          const uint32_t pa = lbase + (((rb * (B / 8) + 4 * ks + gk) ^ i) << 4);
+#pragma unroll
+          for (int q = 0; q < MT; ++q) {
+            const u32x4 bv0 = *reinterpret_cast<const u32x4*>(sb + pa + q * SROWB);
+            const u32x4 bv = kz ? u32x4{0, 0, 0, 0} : bv0;
+#pragma unroll
+            for (int m = 0; m < CW; ++m) acc[o][q][m] = mfma_bf16(E.av[ks][m], bv, acc[o][q][m]);
+          }
+        }
+      };
+      const int cnt = S.cnt[c];
+      const int32_t* L = S.list + (int64_t)c * S.cap;
+      int jc = cur[o];
+      while (jc < cnt) {
+        const int lv = (jc + lane < cnt) ? L[jc + lane] : 0x7fffffff;   // next 64 entries
+        // entries of this stage: the run from jc whose source block is below rhi
+        const uint64_t m = __ballot(jc + lane < cnt && lv / S.K < rhi);
+        const int n = __builtin_popcountll(m);       // a prefix of the 64 lanes (sorted list)
+        if (n == 0) break;
+        auto ent = [&](int jj) { return __builtin_amdgcn_readlane(lv, jj < n ? jj : n - 1); };
+        Ent E0, E1;
+        load(ent(0), E0);
+        for (int jj = 0; jj < n; jj += 2) {
+          load(ent(jj + 1), E1);
+          compute(E0);
+          load(ent(jj + 2), E0);
+          if (jj + 1 < n) compute(E1);
+        }
+        jc += n;
+        if (n < 64) break;                           // the run ended inside this chunk
+      }
+      cur[o] = jc;
+    }
+    if (s + 1 < nstages) stage_store((s + 1) & 1);
+    __syncthreads();
+  }
+
+  // epilogue: dx = acc (+ dy)
+#pragma unroll
+  for (int o = 0; o < OPW; ++o) {
+    const int c = w + 8 * o;
+    if (c >= a.C) continue;
+#pragma unroll
+    for (int q = 0; q < MT; ++q) {
+      const int64_t tn = t0 + 16 * q + i;
+      if (tn < a.N) tprod_store<1, CW>(a, tn, c, g, acc[o][q]);
+    }
+  }
+}
+
+template <int B, int OPW>
+static int launch_dx_stage_t(const TProdArgs& a, hipStream_t st) {
+  constexpr size_t lds = 2 * (size_t)64 * DxStage<B>::COLS * 2;
+  auto kern = dx_stage_kernel<B, OPW>;
+  if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return -1;
+  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 63) / 64)), dim3(512), lds, st, a);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// staged dx when every output block fits the waves' accumulators (OPW * B / 16 <= 8) and the
+// sources' widths are whole stages of 16-byte chunks
+static int launch_dx_stage(int B, const TProdArgs& a, hipStream_t st) {
+  if (a.nsrc < 1 || a.nsrc > 2) return -2;
+  for (int s = 0; s < a.nsrc; ++s)
+    if (a.src[s].lda % B) return -2;
+  const int opw = (a.C + 7) / 8;
+#define LBK_DX(BB, OO) if (B == BB && opw <= OO) return launch_dx_stage_t<BB, OO>(a, st);
+  if (B == 16) { LBK_DX(16, 1) LBK_DX(16, 2) LBK_DX(16, 4) LBK_DX(16, 8) }
+  if (B == 32) { LBK_DX(32, 1) LBK_DX(32, 2) LBK_DX(32, 4) }
+  if (B == 64) { LBK_DX(64, 1) LBK_DX(64, 2) }
+#undef LBK_DX
+  return -2;
+}
+
 int launch_tprod(int B, int mode, const TProdArgs& a, hipStream_t st) {
   if (a.N == 0 || a.C == 0) return 0;
   if (mode == 0 && a.nsrc == 1) {
     const int rc = launch_dh_panel(B, a, st);
+    if (rc != -2) return rc;
+  }
+  if (mode == 1) {
+    const int rc = launch_dx_stage(B, a, st);
     if (rc != -2) return rc;
   }
   const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)((a.C + 3) / 4));

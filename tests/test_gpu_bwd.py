@@ -1,6 +1,8 @@
 """Parity of the SwiGLU FFN backward (lbk_swiglu_bwd_bf16) against the oracle.
 
-The saved forward tensors (gate_pre_act, up_output, h) are computed by the oracle and rounded
+Cases cover both implementations of each transposed product (LDS panel / staged kernels and the
+per-entry gather kernel they fall back to).  The saved forward tensors (gate_pre_act, up_output, h)
+are computed by the oracle and rounded
 to bf16, then given to both sides; the oracle differentiates in float64.  Bar: max-abs error
 <= 1e-2 of max |reference| for dx and every tile gradient (the kernel rounds dg and du to bf16
 between its products, as the reference operator does).
@@ -41,6 +43,8 @@ BWD_CASES = [
     (512, 1024, 32, 0.25, 130, 0.05),
     (128, 512, 64, 0.5, 70, 0.0),
     (1024, 4096, 32, 0.25, 2100, 0.0),     # two token chunks of the tile gradients, ragged tail
+    (2048, 1024, 32, 0.125, 40, 0.05),     # 64 output blocks: dx through the per-entry gather kernel
+    (4096, 512, 64, 0.25, 20, 0.0),        # d_model > 2048: dh through the per-entry gather kernel too
 ]
 
 
