@@ -10,7 +10,8 @@
 //   tlist_kernel   transposed topology: for every input column block c the slots
 //                  (r, k) with col[r,k] = c, in ascending r*K + k (ballot
 //                  compaction, deterministic), for gate, up and down in one launch.
-//   tprod_kernel   out[:, c] = sum over the slots of column block c of
+//   tprod_kernel   (the general case; the two kernels after it cover the common shapes)
+//                  out[:, c] = sum over the slots of column block c of
 //                  A[:, r] W[r,k]^T.  A workgroup owns 64 tokens and four column
 //                  blocks, one per wave (each tile is read once per workgroup);
 //                  the raw [B_in, B_out] tile is the MFMA's A operand (row
@@ -24,6 +25,9 @@
 //                  of 8 waves streams the list entries of its column blocks
 //                  (c = w, w + 8, ...): tile rows from global memory, dy
 //                  fragments from the panel.
+//   dx_stage_kernel  dx when the output blocks fit 8 waves' accumulators: the dg
+//                  and du columns of 64 tokens pass through LDS 512 at a time and
+//                  a cursor per output block walks its sorted list.
 //   dw_kernel      tile gradients: a workgroup owns one block row, up to 8 of
 //                  its slots (one per wave) and a chunk of tokens; token slices
 //                  of X and G are staged row-major in LDS and read back
