@@ -30,7 +30,8 @@ __all__ = [
     "BlockELLConfig", "k_for_density", "random_topology", "dense_to_block_ell",
     "block_ell_to_dense", "create_block_ell_from_dense", "block_ell_matmul",
     "silu", "swiglu_fwd", "rmsnorm", "looped_swiglu", "block_ell_matmul_t",
-    "block_ell_weight_grad", "swiglu_bwd", "ternary_quantize_blocks",
+    "block_ell_weight_grad", "swiglu_bwd", "alive_slots", "compact_topology", "column_importance",
+    "column_permutation", "apply_permutation", "k_active_macros", "ternary_quantize_blocks",
     "activation_quantize_int8", "encode_ternary", "pack_ternary",
     "unpack_ternary", "ternary_block_partials", "ternary_fixed_point",
     "ternary_matmul", "ternary_swiglu_fwd", "bf16_round",
@@ -311,6 +312,75 @@ def swiglu_bwd(grad_out, x, gate_pre_act, up_output, h, gate, up, down):
 
 
 # --------------------------------------------------------------------------
+# topology transforms (prune-time compaction and d_ff column reorder)
+# --------------------------------------------------------------------------
+
+def alive_slots(col_indices: np.ndarray, alive_mask: np.ndarray, C: int) -> np.ndarray:
+    """Slots that hold a tile: alive and a column in [0, C) (the -1 sentinel marks dead slots,
+    ``looped_blockell/opt/cms.py:229-230``)."""
+    col = np.asarray(col_indices)
+    return np.asarray(alive_mask, bool) & (col >= 0) & (col < C)
+
+
+def compact_topology(values: np.ndarray, col_indices: np.ndarray, alive_mask: np.ndarray):
+    """Pack each row's alive tiles to the front, keep K_new = max(1, max alive per row) slots.
+
+    Restates ``looped_blockell/opt/compaction.py:31-60``: a stable sort of each row by
+    ``~alive`` (alive slots first, both groups in slot order), then truncation.  Returns
+    ``(values[R, K_new, B, B], col[R, K_new], alive[R, K_new], K_new)``.
+    """
+    alive = np.asarray(alive_mask, bool)
+    K_new = max(int(alive.sum(axis=1).max()) if alive.size else 0, 1)
+    order = np.argsort(~alive, axis=1, kind="stable")[:, :K_new]
+    rows = np.arange(alive.shape[0])[:, None]
+    return values[rows, order], col_indices[rows, order], alive[rows, order], K_new
+
+
+def column_importance(fc1_alive, fc2_alive, fc1_col, C_ff: int) -> np.ndarray:
+    """d_ff tile-column importance: alive fc1 tiles whose column index is c (sentinels
+    excluded) plus the alive-tile count of fc2 row c (rows padded or truncated to C_ff).
+    Restates ``looped_blockell/opt/column_reorder.py:33-98``."""
+    imp = np.zeros(C_ff, np.float32)
+    cols = np.asarray(fc1_col).reshape(-1)
+    al = np.asarray(fc1_alive, bool).reshape(-1)
+    ok = cols >= 0
+    np.add.at(imp, np.clip(cols[ok], 0, C_ff - 1), al[ok].astype(np.float32))
+    rc = np.asarray(fc2_alive, bool).sum(axis=1).astype(np.float32)
+    n = min(len(rc), C_ff)
+    imp[:n] += rc[:n]
+    return imp
+
+
+def column_permutation(importance: np.ndarray) -> np.ndarray:
+    """``argsort(-importance)``, stable (ties keep ascending index), int32
+    (``looped_blockell/opt/column_reorder.py:103-114``)."""
+    return np.argsort(-np.asarray(importance, np.float32), kind="stable").astype(np.int32)
+
+
+def apply_permutation(values, col_indices, alive_mask, perm, is_column_dim: bool = True):
+    """``looped_blockell/opt/column_reorder.py:121-177``: column mode remaps
+    ``col -> inv_perm[col]`` (sentinels stay -1; values and mask unchanged); row mode
+    gathers rows ``perm[i]`` of values, col_indices and alive_mask."""
+    perm = np.asarray(perm, np.int64)
+    if is_column_dim:
+        C_ff = perm.shape[0]
+        inv = np.zeros(C_ff, np.int32)
+        inv[perm] = np.arange(C_ff, dtype=np.int32)
+        col = np.asarray(col_indices)
+        new = np.where(col < 0, -1, inv[np.clip(col, 0, C_ff - 1)]).astype(np.int32)
+        return values, new, alive_mask
+    return values[perm], col_indices[perm], alive_mask[perm]
+
+
+def k_active_macros(alive_mask, col_indices, tiles_per_macro: int) -> int:
+    """Macro-block columns needed to cover the largest alive column index
+    (``looped_blockell/opt/column_reorder.py:233-269``); 0 when nothing is alive."""
+    safe = np.where(np.asarray(alive_mask, bool), np.asarray(col_indices), -1)
+    m = int(safe.max()) if safe.size else -1
+    return 0 if m < 0 else int(math.ceil((m + 1) / tiles_per_macro))
+
+
+# --------------------------------------------------------------------------
 # ternary path (weights {-1,0,+1} with one scale per block, int8 activations)
 # --------------------------------------------------------------------------
 
@@ -527,6 +597,12 @@ PINS = {
     "block_ell_weight_grad": "== torch autograd of block_ell_matmul through the dense weight, gathered per tile",
     "swiglu_bwd": "== torch float64 autograd of the dense SwiGLU FFN with residual (x and every tile); "
                   "finite differences on tiny shapes",
+    "alive_slots": "hand-built rows with sentinels, out-of-range columns and masked slots",
+    "compact_topology": "hand-worked rows (order kept, K_new = max alive, all-dead row); product unchanged",
+    "column_importance": "reference tests/test_column_reorder.py:16-29 (shape, >= 0); brute-force loops",
+    "column_permutation": "reference tests/test_column_reorder.py:31-35 known answer; ties in index order",
+    "apply_permutation": "reference tests/test_column_reorder.py:38-69, :99-113; the permuted FFN is unchanged",
+    "k_active_macros": "reference tests/test_column_reorder.py:71-96 known answers; all-dead case",
     "ternary_quantize_blocks": "hand-worked block; round-half-even cases; codes in {-1,0,1}",
     "activation_quantize_int8": "hand-worked rows incl. ties and the -128/127 clamps; bitlinear dequant identity",
     "pack_ternary": "hand-computed words; round trip over all codes",

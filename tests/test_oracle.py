@@ -504,3 +504,111 @@ def test_planted_untransposed_tile_in_backward_is_caught():
     W = O.block_ell_to_dense(values, col, 12, 16)
     wrong = O.block_ell_matmul_t(dy, values.transpose(0, 1, 3, 2), col, 4)
     assert np.abs(wrong - dy @ W).max() > 1e-3
+
+
+# ---------------------------------------------------------------- topology transforms
+
+def test_alive_slots_hand_rows():
+    col = np.array([[0, -1, 3, 4], [2, 2, -1, 1]], np.int32)
+    alive = np.array([[1, 1, 1, 0], [1, 0, 1, 1]], bool)
+    np.testing.assert_array_equal(O.alive_slots(col, alive, 4),
+                                  [[True, False, True, False], [True, False, False, True]])
+
+
+def test_compact_topology_hand_rows():
+    B = 2
+    vals = np.arange(3 * 4 * B * B, dtype=np.float32).reshape(3, 4, B, B)
+    col = np.array([[5, 6, 7, 8], [1, 2, 3, 4], [9, 9, 9, 9]], np.int32)
+    alive = np.array([[0, 1, 0, 1], [1, 1, 1, 0], [0, 0, 0, 0]], bool)
+    v2, c2, a2, K_new = O.compact_topology(vals, col, alive)
+    assert K_new == 3
+    np.testing.assert_array_equal(c2, [[6, 8, 5], [1, 2, 3], [9, 9, 9]])     # alive first, order kept
+    np.testing.assert_array_equal(a2, [[1, 1, 0], [1, 1, 1], [0, 0, 0]])
+    np.testing.assert_array_equal(v2[0, 0], vals[0, 1])
+    np.testing.assert_array_equal(v2[0, 2], vals[0, 0])
+    # compaction keeps the product: dead slots (sentinel) contribute nothing either way
+    g = rng(31)
+    R, C, K, B = 4, 6, 5, 4
+    values = g.standard_normal((R, K, B, B))
+    c = O.random_topology(R, C, K, g)
+    al = g.random((R, K)) < 0.6
+    x = g.standard_normal((3, C * B))
+    eff = np.where(al, c, -1)
+    v3, c3, a3, _ = O.compact_topology(values, c, al)
+    np.testing.assert_allclose(O.block_ell_matmul(x, v3, np.where(a3, c3, -1)),
+                               O.block_ell_matmul(x, values, eff), atol=1e-12)
+    _, _, _, K1 = O.compact_topology(values, c, np.zeros((R, K), bool))
+    assert K1 == 1                                                     # at least one slot
+
+
+def test_column_importance_reference_and_brute():
+    # reference tests/test_column_reorder.py:16-29: shape and non-negativity
+    g = rng(32)
+    R_model, K1, C_ff, K2 = 4, 8, 12, 6
+    fc1_cols = g.integers(0, C_ff, (R_model, K1)).astype(np.int32)
+    fc1_cols[0, 3] = -1
+    fc1_alive = g.random((R_model, K1)) < 0.7
+    fc2_alive = g.random((C_ff, K2)) < 0.5
+    imp = O.column_importance(fc1_alive, fc2_alive, fc1_cols, C_ff)
+    assert imp.shape == (C_ff,) and np.all(imp >= 0)
+    brute = np.zeros(C_ff)
+    for r in range(R_model):
+        for k in range(K1):
+            if fc1_cols[r, k] >= 0 and fc1_alive[r, k]:
+                brute[fc1_cols[r, k]] += 1
+    for c in range(C_ff):
+        brute[c] += fc2_alive[c].sum()
+    np.testing.assert_array_equal(imp, brute)
+
+
+def test_column_permutation_known_answer_and_ties():
+    perm = O.column_permutation(np.array([1.0, 5.0, 3.0, 0.0, 2.0]))   # reference :31-35
+    assert perm[0] == 1 and perm[-1] == 3
+    np.testing.assert_array_equal(O.column_permutation(np.array([2.0, 7.0, 2.0, 7.0])), [1, 3, 0, 2])
+
+
+def test_apply_permutation_reference_cases_and_invariance():
+    # reference :38-55 (column dim, reversed order)
+    col = np.array([[0, 2, 4, 5], [1, 3, 4, 5]], np.int32)
+    alive = np.ones((2, 4), bool)
+    perm = np.array([5, 4, 3, 2, 1, 0], np.int32)
+    _, c2, _ = O.apply_permutation(np.ones((2, 4, 16, 16)), col, alive, perm, True)
+    np.testing.assert_array_equal(c2[0], np.argsort(perm)[col[0]])
+    # reference :57-69 (row dim)
+    g = rng(33)
+    vals = g.standard_normal((4, 3, 16, 16))
+    v2, _, _ = O.apply_permutation(vals, np.arange(12).reshape(4, 3), np.ones((4, 3), bool),
+                                   np.array([3, 1, 0, 2]), False)
+    np.testing.assert_array_equal(v2[0], vals[3])
+    np.testing.assert_array_equal(v2[1], vals[1])
+    # reference :99-113 (sentinels stay -1)
+    cs = np.array([[0, 2, -1, -1], [1, 3, -1, -1]], np.int32)
+    _, c3, _ = O.apply_permutation(None, cs, None, np.arange(8), True)
+    assert np.all(c3[:, 2:] == -1)
+    # permuting d_ff consistently (gate/up rows, down columns) leaves the SwiGLU FFN unchanged
+    B, dm, dff = 4, 8, 16
+    Rf, Cf = dff // B, dff // B
+    gate = (g.standard_normal((Rf, 2, B, B)), O.random_topology(Rf, dm // B, 2, g))
+    up = (g.standard_normal((Rf, 2, B, B)), O.random_topology(Rf, dm // B, 2, g))
+    down = (g.standard_normal((dm // B, 3, B, B)), O.random_topology(dm // B, Cf, 3, g))
+    x = g.standard_normal((3, dm))
+    p = g.permutation(Cf).astype(np.int32)
+    al = lambda w: np.ones(w[1].shape, bool)
+    gv, gc, _ = O.apply_permutation(gate[0], gate[1], al(gate), p, False)
+    uv, uc, _ = O.apply_permutation(up[0], up[1], al(up), p, False)
+    _, dc, _ = O.apply_permutation(down[0], down[1], al(down), p, True)
+    ref, *_ = O.swiglu_fwd(x, gate, up, down)
+    got, *_ = O.swiglu_fwd(x, (gv, gc), (uv, uc), (down[0], dc))
+    np.testing.assert_allclose(got, ref, atol=1e-12)
+
+
+def test_k_active_macros_reference_cases():
+    alive = np.ones((4, 8), bool)
+    col = np.tile(np.arange(8, dtype=np.int32), (4, 1))
+    assert O.k_active_macros(alive, col, 4) == 2                       # reference :71-82
+    alive2 = np.zeros((2, 8), bool)
+    alive2[:, :2] = True
+    col2 = np.full((2, 8), -1, np.int32)
+    col2[:, :2] = [0, 1]
+    assert O.k_active_macros(alive2, col2, 4) == 1                     # reference :84-96
+    assert O.k_active_macros(np.zeros((2, 3), bool), np.zeros((2, 3), np.int32), 4) == 0
