@@ -10,7 +10,8 @@ forward pass.  The line also carries:
   cpu_baseline  the CPU oracle (numpy gather + matmul restatement of the
                 reference layer) timed on the host cores on the same workload;
   extra         the other workloads (shared gate/up topology, the backward of the
-                headline workload, ternary FFN, looped block L=8, decode).
+                headline workload, ternary FFN, looped block L=8, decode, and the
+                prune-time topology transforms on the headline weights).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only-main]
 """
@@ -234,6 +235,41 @@ def bench_bf16_backward(steps, warmup, device):
                 frac_of_bf16_peak=flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, kernel_ms_avg=sum(per) / len(per))
 
 
+def bench_topology(steps, warmup, device):
+    """Prune-time topology transforms on the headline weights (60% of slots alive): the full
+    column reorder (importance, permutation, down column remap, gate rows and their Adam moments
+    gathered), the same row gather for up, then compaction of all three weights.  Copy-bound;
+    two host reads per compaction (K_new) and one for the index are part of the step."""
+    import torch
+    from looped_blockell import opt
+    w = WORKLOADS["bf16"]
+    gen = torch.Generator(device=device).manual_seed(w["seed"])
+    g, u, d = make_ffn(w, device, gen)
+    alive = [torch.rand(t[1].shape, generator=gen, device=device) < 0.6 for t in (g, u, d)]
+    C_ff = w["d_ff"] // w["B"]
+    moments = {"exp_avg": torch.zeros(g[0].shape, dtype=torch.float32, device=device),
+               "exp_avg_sq": torch.zeros(g[0].shape, dtype=torch.float32, device=device)}
+    out = {}
+
+    def step(i):
+        r = opt.full_reorder_step(d[0], d[1], alive[2], g[0], g[1], alive[0], moments, C_ff, 4)
+        uv, uc, ua = opt.apply_permutation_to_block_ell(u[0], u[1], alive[1], opt.compute_permutation(
+            opt.compute_column_importance(alive[2], alive[0], d[1], g[1], C_ff)), is_column_dim=False)
+        out["k"] = [opt.compact_single_layer(r[3], r[4], r[5])[3], opt.compact_single_layer(uv, uc, ua)[3],
+                    opt.compact_single_layer(r[0], r[1], r[2])[3]]
+
+    ms, per = time_steps(step, steps, warmup)
+    vb = lambda t: t[0].numel() * 2
+    kn = out["k"]
+    byts = (2 * vb(g) + 2 * 2 * g[0].numel() * 4 + 2 * vb(u)                  # row gathers (values, moments)
+            + sum(2 * vb(t) * k // t[0].shape[1] for t, k in zip((g, u, d), kn)))   # compaction copies
+    return dict(workload="topology transforms on the headline weights: full column reorder (with Adam "
+                         "moments), up-row gather, compaction of gate/up/down",
+                ms_per_step=ms, value=byts / (ms * 1e-3) / 1e9, unit="GB/s",
+                frac_of_hbm_peak=byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, algorithmic_bytes=byts,
+                k_new=kn, kernel_ms_avg=sum(per) / len(per))
+
+
 def bench_ternary(steps, warmup, device):
     import torch
     from looped_blockell import kernels
@@ -343,7 +379,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-main", action="store_true", help="headline workload only (for profiling)")
     ap.add_argument("--only", default="",
-                    help="comma list of extra workloads to run: shared,backward,ternary,looped,decode")
+                    help="comma list of extra workloads to run: shared,backward,ternary,looped,decode,topology")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one 256 MiB device-to-device copy (a reference point for HBM byte counters)")
     args = ap.parse_args()
@@ -368,9 +404,10 @@ def main():
     main_res = bench_bf16(args.steps, args.warmup, device)
     extra = {}
     if not args.only_main:
-        todo = [s for s in args.only.split(",") if s] or ["shared", "backward", "ternary", "looped", "decode"]
+        todo = [s for s in args.only.split(",") if s] or ["shared", "backward", "ternary", "looped", "decode",
+                                                           "topology"]
         fns = dict(shared=bench_bf16_shared, backward=bench_bf16_backward, ternary=bench_ternary,
-                   looped=bench_looped, decode=bench_decode)
+                   looped=bench_looped, decode=bench_decode, topology=bench_topology)
         for name in todo:
             st = max(5, args.steps // (4 if name == "looped" else 1))
             try:

@@ -228,6 +228,81 @@ int lbk_swiglu_fwd_ternary(const int8_t* xq, const float* sx, int64_t N, int32_t
                            uint16_t* out, uint16_t* h_out, int8_t* hq_out, float* sh_out,
                            void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- prune-time topology transforms (integer and copy work; alive masks are one byte per slot,
+ * nonzero = alive).  Replaces the JAX functions of looped_blockell/opt/compaction.py and
+ * looped_blockell/opt/column_reorder.py on device. */
+
+/*
+ * counts[r] = alive slots of row r, max_count[0] = their maximum (device scalar).
+ * The compacted K is max(1, max_count) (reference looped_blockell/opt/compaction.py:43-45).
+ */
+int lbk_topology_alive_counts(const uint8_t* alive, int32_t R, int32_t K, int32_t* counts,
+                              int32_t* max_count, void* stream);
+
+/*
+ * Packs each row's alive slots to the front (alive first, both groups in slot order) and keeps
+ * the first K_new (1 <= K_new <= K) slots: out_values [R, K_new, B, B], out_col_idx and
+ * out_alive [R, K_new].  Outputs must not overlap the inputs.
+ * Replaces compact_single_layer (reference looped_blockell/opt/compaction.py:31-60).
+ */
+int lbk_topology_compact_bf16(const uint16_t* values, const int32_t* col_idx, const uint8_t* alive,
+                              int32_t R, int32_t K, int32_t B, int32_t K_new, uint16_t* out_values,
+                              int32_t* out_col_idx, uint8_t* out_alive, void* stream);
+
+/*
+ * importance[c] (c < C_ff <= 16384) = alive fc1 slots whose column is c (negative columns
+ * skipped, columns >= C_ff counted at C_ff - 1) + alive slots of fc2 row c.
+ * Replaces compute_column_importance (reference looped_blockell/opt/column_reorder.py:33-98).
+ */
+int lbk_column_importance(const int32_t* fc1_col_idx, const uint8_t* fc1_alive, int32_t R1, int32_t K1,
+                          const uint8_t* fc2_alive, int32_t R2, int32_t K2, int32_t C_ff,
+                          float* importance, void* stream);
+
+/*
+ * perm = stable argsort(-importance) (ties in index order, NaN last), int32 [C_ff].
+ * Replaces compute_permutation (reference looped_blockell/opt/column_reorder.py:103-114).
+ */
+int lbk_column_permutation(const float* importance, int32_t C_ff, int32_t* perm, void* stream);
+
+/*
+ * Applies a d_ff permutation (perm[new] = old): is_column_dim != 0 remaps column indices
+ * through the inverse permutation (sentinels stay -1); tiles and flags are copied to
+ * out_values / out_alive, or left in place when those are NULL (the reference returns them
+ * unchanged).  Otherwise (R == C_ff) output row i is input row perm[i] of values, column
+ * indices and flags.  Outputs must not overlap the inputs.
+ * Replaces apply_permutation_to_block_ell (reference looped_blockell/opt/column_reorder.py:121-177).
+ */
+int lbk_apply_permutation_bf16(const uint16_t* values, const int32_t* col_idx, const uint8_t* alive,
+                               int32_t R, int32_t K, int32_t B, const int32_t* perm, int32_t C_ff,
+                               int32_t is_column_dim, uint16_t* out_values, int32_t* out_col_idx,
+                               uint8_t* out_alive, void* stream);
+
+/*
+ * k_active[0] = ceil((largest alive column + 1) / tiles_per_macro), 0 if nothing is alive.
+ * Replaces compute_k_active_macros (reference looped_blockell/opt/column_reorder.py:233-269).
+ */
+int lbk_k_active_macros(const int32_t* col_idx, const uint8_t* alive, int32_t R, int32_t K,
+                        int32_t tiles_per_macro, int32_t* k_active, void* stream);
+
+/*
+ * dst row i = src row perm[i] for i < n_dst, rows of row_bytes bytes, any element type: the
+ * d_ff row permutation of optimizer moments and other per-row state.
+ * Replaces apply_permutation_to_optimizer's row gather (reference
+ * looped_blockell/opt/column_reorder.py:179-236).
+ */
+int lbk_gather_rows(const void* src, int64_t n_src, int64_t row_bytes, const int32_t* perm, int64_t n_dst,
+                    void* dst, void* stream);
+
+/*
+ * Transposed (CSC) index of a Block-ELL topology: for every column block c < C (<= 16384),
+ * entries[col_ptr[c] .. col_ptr[c+1]) are the slots e = r*K + k with col_idx[e] == c in
+ * ascending order; col_ptr has C + 1 entries, entries up to R*K.  Slots whose column is
+ * outside [0, C) (the -1 sentinel) are left out.  The reference has no such function: it is
+ * the column-major view a transposed product (the backward's dy W, x^T G) walks.
+ */
+int lbk_transposed_index(const int32_t* col_idx, int32_t R, int32_t K, int32_t C, int32_t* col_ptr,
+                         int32_t* entries, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

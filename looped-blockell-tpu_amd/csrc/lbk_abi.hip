@@ -561,4 +561,82 @@ int lbk_swiglu_bwd_bf16(const uint16_t* grad_out, const uint16_t* x, const uint1
   return LBK_OK;
 }
 
+// ---- topology transforms
+int lbk_topology_alive_counts(const uint8_t* alive, int32_t R, int32_t K, int32_t* counts, int32_t* max_count,
+                              void* stream) {
+  if (R < 0 || K < 0) return LBK_ERR_ARG;
+  if (!max_count || (R > 0 && (!counts || (K > 0 && !alive)))) return LBK_ERR_NULL;
+  return launch_topo_count(alive, R, K, counts, max_count, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+int lbk_topology_compact_bf16(const uint16_t* values, const int32_t* col_idx, const uint8_t* alive, int32_t R,
+                              int32_t K, int32_t B, int32_t K_new, uint16_t* out_values, int32_t* out_col_idx,
+                              uint8_t* out_alive, void* stream) {
+  if (!tile_ok(B)) return LBK_ERR_TILE;
+  if (R < 0 || K < 1 || K_new < 1 || K_new > K) return LBK_ERR_ARG;
+  if (R == 0) return LBK_OK;
+  if (!values || !col_idx || !alive || !out_values || !out_col_idx || !out_alive) return LBK_ERR_NULL;
+  if (!a16(values) || !a16(out_values)) return LBK_ERR_ALIGN;
+  return launch_topo_compact(values, col_idx, alive, R, K, B, K_new, out_values, out_col_idx, out_alive,
+                             S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+int lbk_column_importance(const int32_t* fc1_col_idx, const uint8_t* fc1_alive, int32_t R1, int32_t K1,
+                          const uint8_t* fc2_alive, int32_t R2, int32_t K2, int32_t C_ff, float* importance,
+                          void* stream) {
+  if (R1 < 0 || K1 < 0 || R2 < 0 || K2 < 0 || C_ff < 1 || C_ff > 16384) return LBK_ERR_ARG;
+  if (!importance || ((int64_t)R1 * K1 > 0 && (!fc1_col_idx || !fc1_alive)) || ((int64_t)R2 * K2 > 0 && !fc2_alive))
+    return LBK_ERR_NULL;
+  return launch_topo_importance(fc1_col_idx, fc1_alive, (int64_t)R1 * K1, fc2_alive, R2, K2, C_ff, importance,
+                                S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+int lbk_column_permutation(const float* importance, int32_t C_ff, int32_t* perm, void* stream) {
+  if (C_ff < 1 || C_ff > 16384) return LBK_ERR_ARG;
+  if (!importance || !perm) return LBK_ERR_NULL;
+  return launch_topo_perm(importance, C_ff, perm, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+int lbk_apply_permutation_bf16(const uint16_t* values, const int32_t* col_idx, const uint8_t* alive, int32_t R,
+                               int32_t K, int32_t B, const int32_t* perm, int32_t C_ff, int32_t is_column_dim,
+                               uint16_t* out_values, int32_t* out_col_idx, uint8_t* out_alive, void* stream) {
+  if (!tile_ok(B)) return LBK_ERR_TILE;
+  if (R < 0 || K < 0 || C_ff < 1 || C_ff > 16384) return LBK_ERR_ARG;
+  if (!is_column_dim && R != C_ff) return LBK_ERR_SHAPE;
+  if ((int64_t)R * K == 0) return LBK_OK;
+  if (!col_idx || !perm || !out_col_idx) return LBK_ERR_NULL;
+  // column mode leaves tiles and flags in place when out_values / out_alive are null
+  if (!is_column_dim && (!out_values || !out_alive)) return LBK_ERR_NULL;
+  if ((out_values && !values) || (out_alive && !alive)) return LBK_ERR_NULL;
+  if (out_values && (!a16(values) || !a16(out_values))) return LBK_ERR_ALIGN;
+  return launch_topo_apply(values, col_idx, alive, R, K, B, perm, C_ff, is_column_dim ? 1 : 0, out_values,
+                           out_col_idx, out_alive, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+int lbk_k_active_macros(const int32_t* col_idx, const uint8_t* alive, int32_t R, int32_t K, int32_t tiles_per_macro,
+                        int32_t* k_active, void* stream) {
+  if (R < 0 || K < 0 || tiles_per_macro < 1) return LBK_ERR_ARG;
+  if (!k_active || ((int64_t)R * K > 0 && (!col_idx || !alive))) return LBK_ERR_NULL;
+  return launch_topo_kactive(col_idx, alive, (int64_t)R * K, tiles_per_macro, k_active, S(stream)) == 0
+             ? LBK_OK
+             : LBK_ERR_LAUNCH;
+}
+
+int lbk_gather_rows(const void* src, int64_t n_src, int64_t row_bytes, const int32_t* perm, int64_t n_dst,
+                    void* dst, void* stream) {
+  if (n_src < 0 || n_dst < 0 || row_bytes < 0 || n_src > INT32_MAX || n_dst > INT32_MAX) return LBK_ERR_ARG;
+  if (n_dst == 0 || row_bytes == 0) return LBK_OK;
+  if (n_src == 0) return LBK_ERR_SHAPE;
+  if (!src || !perm || !dst) return LBK_ERR_NULL;
+  return launch_topo_gather(src, row_bytes, perm, (int)n_src, (int)n_dst, dst, S(stream)) == 0 ? LBK_OK
+                                                                                                : LBK_ERR_LAUNCH;
+}
+
+int lbk_transposed_index(const int32_t* col_idx, int32_t R, int32_t K, int32_t C, int32_t* col_ptr,
+                         int32_t* entries, void* stream) {
+  if (R < 0 || K < 0 || C < 1 || C > 16384 || (int64_t)R * K > INT32_MAX) return LBK_ERR_ARG;
+  if (!col_ptr || ((int64_t)R * K > 0 && (!col_idx || !entries))) return LBK_ERR_NULL;
+  return launch_topo_csc(col_idx, R, K, C, col_ptr, entries, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
 }  // extern "C"

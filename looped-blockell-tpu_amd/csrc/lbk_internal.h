@@ -200,6 +200,21 @@ struct DWJobs {
 constexpr int DW_CHUNK = 2048;   // tokens per partial tile
 int launch_dw(int B, const DWJob* jobs, int n, int64_t N, int chunk, hipStream_t st);
 
+// ---- topology transforms (lbk_topo.hip)
+int launch_topo_count(const uint8_t* alive, int R, int K, int32_t* counts, int32_t* mx, hipStream_t st);
+int launch_topo_compact(const uint16_t* values, const int32_t* col, const uint8_t* alive, int R, int K, int B,
+                        int K_new, uint16_t* ov, int32_t* oc, uint8_t* oa, hipStream_t st);
+int launch_topo_importance(const int32_t* c1, const uint8_t* a1, int64_t n1, const uint8_t* a2, int R2, int K2,
+                           int C_ff, float* imp, hipStream_t st);
+int launch_topo_perm(const float* imp, int C, int32_t* perm, hipStream_t st);
+int launch_topo_apply(const uint16_t* values, const int32_t* col, const uint8_t* alive, int R, int K, int B,
+                      const int32_t* perm, int C_ff, int column, uint16_t* ov, int32_t* oc, uint8_t* oa,
+                      hipStream_t st);
+int launch_topo_kactive(const int32_t* col, const uint8_t* alive, int64_t n, int tpm, int32_t* out, hipStream_t st);
+int launch_topo_gather(const void* src, int64_t row_bytes, const int32_t* perm, int n_src, int n_dst, void* dst,
+                       hipStream_t st);
+int launch_topo_csc(const int32_t* col, int R, int K, int C, int32_t* col_ptr, int32_t* entries, hipStream_t st);
+
 int launch_check_columns(const int32_t* col, int64_t count, int C, int32_t* bad, hipStream_t st);
 
 }  // namespace lbk

@@ -51,6 +51,14 @@ SIGNATURES = {
     "lbk_status_string": (C.c_char_p, [C.c_int]),
     "lbk_version": (C.c_int, []),
     "lbk_check_columns": (C.c_int, [_P, _I64, _I32, _P, _P]),
+    "lbk_topology_alive_counts": (C.c_int, [_P, _I32, _I32, _P, _P, _P]),
+    "lbk_topology_compact_bf16": (C.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _P, _P, _P, _P]),
+    "lbk_column_importance": (C.c_int, [_P, _P, _I32, _I32, _P, _I32, _I32, _I32, _P, _P]),
+    "lbk_column_permutation": (C.c_int, [_P, _I32, _P, _P]),
+    "lbk_apply_permutation_bf16": (C.c_int, [_P, _P, _P, _I32, _I32, _I32, _P, _I32, _I32, _P, _P, _P, _P]),
+    "lbk_k_active_macros": (C.c_int, [_P, _P, _I32, _I32, _I32, _P, _P]),
+    "lbk_gather_rows": (C.c_int, [_P, _I64, _I64, _P, _I64, _P, _P]),
+    "lbk_transposed_index": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P]),
     "lbk_block_ell_matmul_bf16": (C.c_int, [_P, _I64, _I32, _I64, _PB, _P, _P, _I64, _P]),
     "lbk_swiglu_workspace_bytes": (_SZ, [_I64, _I32, _PB, _PB, _PB, C.c_int]),
     "lbk_swiglu_fwd_bf16": (C.c_int, [_P, _I64, _I32, _PB, _PB, _PB, C.c_int, _P, _P, _P, _P, _P, _SZ, _P]),

@@ -28,6 +28,7 @@ import numpy as np
 
 __all__ = [
     "BlockELLConfig", "k_for_density", "random_topology", "dense_to_block_ell",
+    "permute_optimizer_rows", "transposed_index",
     "block_ell_to_dense", "create_block_ell_from_dense", "block_ell_matmul",
     "silu", "swiglu_fwd", "rmsnorm", "looped_swiglu", "block_ell_matmul_t",
     "block_ell_weight_grad", "swiglu_bwd", "alive_slots", "compact_topology", "column_importance",
@@ -380,6 +381,39 @@ def k_active_macros(alive_mask, col_indices, tiles_per_macro: int) -> int:
     return 0 if m < 0 else int(math.ceil((m + 1) / tiles_per_macro))
 
 
+def permute_optimizer_rows(state, perm, is_column_dim: bool = True):
+    """``looped_blockell/opt/column_reorder.py:179-236``: in row mode every array leaf whose
+    first dimension is C_ff = len(perm) is gathered ``leaf[perm]``; column mode and other leaves
+    are returned unchanged.  ``state`` is a nested dict / list / tuple of arrays."""
+    perm = np.asarray(perm, np.int64)
+
+    def leaf(x):
+        if isinstance(x, dict):
+            return {k: leaf(v) for k, v in x.items()}
+        if isinstance(x, (list, tuple)):
+            return type(x)(leaf(v) for v in x)
+        if isinstance(x, np.ndarray) and not is_column_dim and x.ndim >= 1 and x.shape[0] == perm.shape[0]:
+            return x[perm]
+        return x
+
+    return leaf(state)
+
+
+def transposed_index(col_indices, C: int):
+    """Column-major (CSC) view of a topology: ``col_ptr[C + 1]`` and the slots ``e = r*K + k``
+    of each column block in ascending order, sentinel (-1) and out-of-range slots left out.
+    No reference counterpart: the index a transposed product walks (the backward's ``dy W``
+    gathers, ``looped_blockell/layers/block_ell.py:149-182`` read column-wise)."""
+    col = np.asarray(col_indices).reshape(-1)
+    ok = (col >= 0) & (col < C)
+    e = np.nonzero(ok)[0]
+    order = np.argsort(col[e], kind="stable")
+    counts = np.bincount(col[e], minlength=C)[:C]
+    col_ptr = np.zeros(C + 1, np.int32)
+    col_ptr[1:] = np.cumsum(counts)
+    return col_ptr, e[order].astype(np.int32)
+
+
 # --------------------------------------------------------------------------
 # ternary path (weights {-1,0,+1} with one scale per block, int8 activations)
 # --------------------------------------------------------------------------
@@ -603,6 +637,8 @@ PINS = {
     "column_permutation": "reference tests/test_column_reorder.py:31-35 known answer; ties in index order",
     "apply_permutation": "reference tests/test_column_reorder.py:38-69, :99-113; the permuted FFN is unchanged",
     "k_active_macros": "reference tests/test_column_reorder.py:71-96 known answers; all-dead case",
+    "permute_optimizer_rows": "hand-built moment trees: rows of C_ff-leading leaves permuted, other leaves and column mode untouched",
+    "transposed_index": "brute force per column on tiny topologies; every valid slot listed once; sentinels left out",
     "ternary_quantize_blocks": "hand-worked block; round-half-even cases; codes in {-1,0,1}",
     "activation_quantize_int8": "hand-worked rows incl. ties and the -128/127 clamps; bitlinear dequant identity",
     "pack_ternary": "hand-computed words; round trip over all codes",

@@ -612,3 +612,37 @@ def test_k_active_macros_reference_cases():
     col2[:, :2] = [0, 1]
     assert O.k_active_macros(alive2, col2, 4) == 1                     # reference :84-96
     assert O.k_active_macros(np.zeros((2, 3), bool), np.zeros((2, 3), np.int32), 4) == 0
+
+
+def test_permute_optimizer_rows_hand_tree():
+    perm = np.array([2, 0, 1], np.int32)
+    mu = np.arange(3 * 2, dtype=np.float32).reshape(3, 2)
+    other = np.arange(4, dtype=np.float32)                      # first dim != C_ff: untouched
+    state = {"count": 7, "mu": mu, "nested": [mu * 10, other], "t": (mu,)}
+    out = O.permute_optimizer_rows(state, perm, is_column_dim=False)
+    np.testing.assert_array_equal(out["mu"], [[4, 5], [0, 1], [2, 3]])
+    np.testing.assert_array_equal(out["nested"][0], [[40, 50], [0, 10], [20, 30]])
+    assert out["nested"][1] is other and out["count"] == 7 and isinstance(out["t"], tuple)
+    same = O.permute_optimizer_rows(state, perm, is_column_dim=True)
+    assert same["mu"] is mu                                      # column mode: moments stay put
+
+
+def _csc_brute(col, C):
+    flat = col.reshape(-1)
+    lists = [[e for e in range(flat.size) if flat[e] == c] for c in range(C)]
+    ptr = np.cumsum([0] + [len(l) for l in lists])
+    return ptr, [e for l in lists for e in l]
+
+
+def test_transposed_index_brute_force():
+    rng = np.random.default_rng(3)
+    for R, K, C in [(1, 1, 1), (3, 4, 5), (7, 3, 2), (10, 9, 40)]:
+        col = rng.integers(-1, C + 2, size=(R, K)).astype(np.int32)
+        ptr, ent = O.transposed_index(col, C)
+        bp, be = _csc_brute(col, C)
+        np.testing.assert_array_equal(ptr, bp)
+        np.testing.assert_array_equal(ent, be)
+        valid = ((col >= 0) & (col < C)).sum()
+        assert ptr[-1] == valid and len(set(ent.tolist())) == valid
+    ptr, ent = O.transposed_index(np.full((2, 3), -1, np.int32), 4)
+    assert ptr.tolist() == [0, 0, 0, 0, 0] and ent.size == 0
