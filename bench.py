@@ -270,6 +270,35 @@ def bench_topology(steps, warmup, device):
                 k_new=kn, kernel_ms_avg=sum(per) / len(per))
 
 
+def bench_formats(steps, warmup, device):
+    """The dense <-> Block-ELL bridge at the headline shapes: dense bf16 gate/up [4096, 1024] and
+    down [1024, 4096] -> top-25 % blocks per row by Frobenius norm + tile gather (the layer API's
+    create_block_ell_from_dense), then back to dense.  Copy-bound."""
+    import torch
+    from looped_blockell.layers import block_ell_to_dense, create_block_ell_from_dense
+    w = WORKLOADS["bf16"]
+    gen = torch.Generator(device=device).manual_seed(w["seed"])
+    dm, dff, B = w["d_model"], w["d_ff"], w["B"]
+    dense = [torch.randn(s, generator=gen, device=device).to(torch.bfloat16) for s in ((dff, dm), (dff, dm), (dm, dff))]
+    out = {}
+
+    def step(i):
+        es = [create_block_ell_from_dense(d, tile_size=B, density=w["density"]) for d in dense]
+        out["d"] = [block_ell_to_dense(e) for e in es]
+
+    ms, per = time_steps(step, steps, warmup)
+    full = sum(d.numel() * 2 for d in dense)
+    # norms read every dense block; the gather reads and writes the kept quarter; to-dense
+    # reads the tiles and writes every dense block
+    byts = full + 2 * w["density"] * full + w["density"] * full + full
+    assert all(torch.isfinite(d.float()).all() for d in out["d"])
+    return dict(workload="dense <-> Block-ELL bridge: top-25% block selection + gather, and back to dense, for "
+                         "gate/up [4096,1024] and down [1024,4096] bf16",
+                ms_per_step=ms, value=byts / (ms * 1e-3) / 1e9, unit="GB/s",
+                frac_of_hbm_peak=byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, algorithmic_bytes=byts,
+                kernel_ms_avg=sum(per) / len(per))
+
+
 def bench_ternary(steps, warmup, device):
     import torch
     from looped_blockell import kernels
@@ -379,7 +408,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-main", action="store_true", help="headline workload only (for profiling)")
     ap.add_argument("--only", default="",
-                    help="comma list of extra workloads to run: shared,backward,ternary,looped,decode,topology")
+                    help="comma list of extra workloads to run: shared,backward,ternary,looped,decode,topology,"
+                         "formats")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one 256 MiB device-to-device copy (a reference point for HBM byte counters)")
     args = ap.parse_args()
@@ -405,9 +435,9 @@ def main():
     extra = {}
     if not args.only_main:
         todo = [s for s in args.only.split(",") if s] or ["shared", "backward", "ternary", "looped", "decode",
-                                                           "topology"]
+                                                           "topology", "formats"]
         fns = dict(shared=bench_bf16_shared, backward=bench_bf16_backward, ternary=bench_ternary,
-                   looped=bench_looped, decode=bench_decode, topology=bench_topology)
+                   looped=bench_looped, decode=bench_decode, topology=bench_topology, formats=bench_formats)
         for name in todo:
             st = max(5, args.steps // (4 if name == "looped" else 1))
             try:

@@ -303,6 +303,47 @@ int lbk_gather_rows(const void* src, int64_t n_src, int64_t row_bytes, const int
 int lbk_transposed_index(const int32_t* col_idx, int32_t R, int32_t K, int32_t C, int32_t* col_ptr,
                          int32_t* entries, void* stream);
 
+/* ---- storage-format bridges (copies move bits: elem_bytes 2 = bf16, 4 = fp32) ---- */
+
+/*
+ * Dense [R*B, C*B] row-major (leading dimension ld >= C*B elements) -> Block-ELL values
+ * [R, K, B_in, B_out]: values[r,k] = transpose of dense block (r, col_idx[r,k]); a zero tile
+ * where the column is outside [0, C).  With col_idx[r,k] = k and K = C this is the density-1
+ * checkpoint conversion.
+ * Replaces _dense_to_block_ell (reference interop/convert_checkpoint.py:114-131) and the
+ * gather of create_block_ell_from_dense (reference looped_blockell/layers/block_ell.py:108-111).
+ */
+int lbk_dense_to_block_ell(const void* dense, int64_t ld, int32_t elem_bytes, int32_t R, int32_t C,
+                           int32_t B, const int32_t* col_idx, int32_t K, void* values, void* stream);
+
+/*
+ * Block-ELL -> dense [R*B, C*B] (leading dimension ld): every block (r, c) gets the transposed
+ * tile of the last slot of row r whose column is c (later slots overwrite earlier ones), or
+ * zeros; sentinel slots write nothing.
+ * Replaces _block_ell_to_dense (reference interop/convert_checkpoint.py:134-148) and
+ * block_ell_to_dense (reference looped_blockell/layers/block_ell.py:118-146).
+ */
+int lbk_block_ell_to_dense(const void* values, const int32_t* col_idx, int32_t R, int32_t K,
+                           int32_t B, int32_t C, int32_t elem_bytes, void* dense, int64_t ld,
+                           void* stream);
+
+/*
+ * Per block row, the K (1 <= K <= C <= 16384) columns whose dense blocks have the largest
+ * Frobenius norm (fp32; ties to the smaller column), written in ascending order to
+ * col_idx_out [R, K].  dense and its rows (ld * elem_bytes) must be 16-byte aligned.
+ * Replaces the top-K selection of create_block_ell_from_dense (reference
+ * looped_blockell/layers/block_ell.py:100-106).
+ */
+int lbk_block_ell_topk_columns(const void* dense, int64_t ld, int32_t elem_bytes, int32_t R, int32_t C,
+                               int32_t B, int32_t K, int32_t* col_idx_out, void* stream);
+
+/*
+ * bad_count[0] = number of 2-bit fields holding the unused code 0b10 in n_words packed ternary
+ * words (0 for a valid file).  The packed ternary format has no reference counterpart: it is
+ * this library's storage format, checked when a file is loaded.
+ */
+int lbk_ternary_check_codes(const uint32_t* words, int64_t n_words, int32_t* bad_count, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,7 +24,7 @@ PKG = os.path.join(HERE, "looped_blockell")
 LIB = os.path.join(PKG, "liblbk.so")
 EXT = os.path.join(PKG, "_titan_ext.so")
 
-HIP_SOURCES = ["lbk_bf16.hip", "lbk_split.hip", "lbk_decode.hip", "lbk_ternary.hip", "lbk_tsplit.hip", "lbk_bwd.hip", "lbk_topo.hip",
+HIP_SOURCES = ["lbk_bf16.hip", "lbk_split.hip", "lbk_decode.hip", "lbk_ternary.hip", "lbk_tsplit.hip", "lbk_bwd.hip", "lbk_topo.hip", "lbk_format.hip",
                "lbk_abi.hip"]
 ARCH = os.environ.get("LBK_OFFLOAD_ARCH", "gfx950")
 

@@ -639,4 +639,48 @@ int lbk_transposed_index(const int32_t* col_idx, int32_t R, int32_t K, int32_t C
   return launch_topo_csc(col_idx, R, K, C, col_ptr, entries, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
 }
 
+static bool elem_ok(int e, const void* p) {
+  return (e == 2 || e == 4) && (reinterpret_cast<uintptr_t>(p) % (uintptr_t)e) == 0;
+}
+
+int lbk_dense_to_block_ell(const void* dense, int64_t ld, int32_t elem_bytes, int32_t R, int32_t C, int32_t B,
+                           const int32_t* col_idx, int32_t K, void* values, void* stream) {
+  if (!tile_ok(B)) return LBK_ERR_TILE;
+  if (R < 0 || C < 1 || K < 0 || R > 65535 || ld < (int64_t)C * B) return LBK_ERR_ARG;
+  if ((int64_t)R * K == 0) return LBK_OK;
+  if (!dense || !col_idx || !values) return LBK_ERR_NULL;
+  if (!elem_ok(elem_bytes, dense) || !elem_ok(elem_bytes, values)) return LBK_ERR_ALIGN;
+  return launch_fmt_from_dense(dense, ld, elem_bytes, R, C, B, col_idx, K, values, S(stream)) == 0
+             ? LBK_OK
+             : LBK_ERR_LAUNCH;
+}
+
+int lbk_block_ell_to_dense(const void* values, const int32_t* col_idx, int32_t R, int32_t K, int32_t B, int32_t C,
+                           int32_t elem_bytes, void* dense, int64_t ld, void* stream) {
+  if (!tile_ok(B)) return LBK_ERR_TILE;
+  if (R < 0 || C < 0 || K < 0 || R > 65535 || ld < (int64_t)C * B) return LBK_ERR_ARG;
+  if ((int64_t)R * C == 0) return LBK_OK;
+  if (!dense || (K > 0 && (!values || !col_idx))) return LBK_ERR_NULL;
+  if (!elem_ok(elem_bytes, dense) || (K > 0 && !elem_ok(elem_bytes, values))) return LBK_ERR_ALIGN;
+  return launch_fmt_to_dense(values, col_idx, R, K, B, C, elem_bytes, dense, ld, S(stream)) == 0 ? LBK_OK
+                                                                                                : LBK_ERR_LAUNCH;
+}
+
+int lbk_block_ell_topk_columns(const void* dense, int64_t ld, int32_t elem_bytes, int32_t R, int32_t C, int32_t B,
+                               int32_t K, int32_t* col_idx_out, void* stream) {
+  if (!tile_ok(B)) return LBK_ERR_TILE;
+  if (R < 0 || C < 1 || C > 16384 || K < 1 || K > C || ld < (int64_t)C * B) return LBK_ERR_ARG;
+  if (R == 0) return LBK_OK;
+  if (!dense || !col_idx_out) return LBK_ERR_NULL;
+  // the norms read 16-byte chunks: rows and the base must be 16-byte aligned
+  if (!elem_ok(elem_bytes, dense) || !a16(dense) || (ld * elem_bytes) % 16) return LBK_ERR_ALIGN;
+  return launch_fmt_topk(dense, ld, elem_bytes, R, C, B, K, col_idx_out, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+int lbk_ternary_check_codes(const uint32_t* words, int64_t n_words, int32_t* bad_count, void* stream) {
+  if (n_words < 0) return LBK_ERR_ARG;
+  if (!bad_count || (n_words > 0 && !words)) return LBK_ERR_NULL;
+  return launch_fmt_ternary_check(words, n_words, bad_count, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
 }  // extern "C"

@@ -215,6 +215,15 @@ int launch_topo_gather(const void* src, int64_t row_bytes, const int32_t* perm, 
                        hipStream_t st);
 int launch_topo_csc(const int32_t* col, int R, int K, int C, int32_t* col_ptr, int32_t* entries, hipStream_t st);
 
+// storage-format bridges (lbk_format.hip); elem_bytes 2 = bf16, 4 = fp32
+int launch_fmt_from_dense(const void* dense, int64_t ld, int elem_bytes, int R, int C, int B, const int32_t* col,
+                          int K, void* values, hipStream_t st);
+int launch_fmt_to_dense(const void* values, const int32_t* col, int R, int K, int B, int C, int elem_bytes,
+                        void* dense, int64_t ld, hipStream_t st);
+int launch_fmt_topk(const void* dense, int64_t ld, int elem_bytes, int R, int C, int B, int K, int32_t* col_out,
+                    hipStream_t st);
+int launch_fmt_ternary_check(const uint32_t* words, int64_t n, int32_t* bad, hipStream_t st);
+
 int launch_check_columns(const int32_t* col, int64_t count, int C, int32_t* bad, hipStream_t st);
 
 }  // namespace lbk

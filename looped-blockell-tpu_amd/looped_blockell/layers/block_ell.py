@@ -7,8 +7,9 @@ Block-ELL stores a sparse weight as
   col_indices: [R, K] int32  input column block of each tile (-1 = dead slot)
 Layout convention: the weight is [out_features, in_features] = [R*B, C*B].
 
-``block_ell_matmul`` runs on the GPU through the HIP kernels (``titan::block_ell_matmul``);
-format helpers (topology, dense conversion) are plain torch code usable on any device.
+``block_ell_matmul`` and the dense conversions run on the GPU through the HIP kernels
+(``titan::block_ell_matmul``, ``lbk_block_ell_topk_columns``, ``lbk_dense_to_block_ell``,
+``lbk_block_ell_to_dense``); ``create_random_topology`` is torch RNG code usable on any device.
 """
 
 from __future__ import annotations
@@ -95,32 +96,24 @@ def create_block_ell_from_dense(dense: torch.Tensor, tile_size: int = 16, densit
 
     Reference ``block_ell.py:79-115``: ``K = max(1, int(C * density))``, indices sorted.
     """
+    from ..interop import gather_tiles, topk_columns
     out_f, in_f = dense.shape
     B = tile_size
     if out_f % B or in_f % B:
         raise ValueError(f"Dimensions ({out_f}, {in_f}) must be divisible by tile_size {B}")
     R, C = out_f // B, in_f // B
     K = max(1, int(C * density))
-    blocks = dense.reshape(R, B, C, B).permute(0, 2, 3, 1)            # [R, C, B_in, B_out]
-    norms = blocks.float().pow(2).sum(dim=(2, 3)).sqrt()
-    top = torch.argsort(-norms, dim=1, stable=True)[:, :K]
-    cols = torch.sort(top, dim=1).values
-    values = torch.gather(blocks, 1, cols[:, :, None, None].expand(R, K, B, B)).contiguous()
-    return BlockELLTensor(values=values, col_indices=cols.to(torch.int32),
-                          config=BlockELLConfig(R=R, C=C, K=K, B=B))
+    cols = topk_columns(dense, B, K)                                   # ascending, ties to the smaller column
+    values = gather_tiles(dense, cols, B)                              # [R, K, B_in, B_out]
+    return BlockELLTensor(values=values, col_indices=cols, config=BlockELLConfig(R=R, C=C, K=K, B=B))
 
 
 def block_ell_to_dense(block_ell: BlockELLTensor) -> torch.Tensor:
-    """Scatter to dense [out, in]; each [B_in, B_out] tile lands transposed (reference ``block_ell.py:118-146``)."""
+    """Scatter to dense [out, in]; each [B_in, B_out] tile lands transposed (reference
+    ``block_ell.py:118-146``; the last slot naming a column wins, ``-1`` slots write nothing)."""
+    from ..interop import block_ell_to_dense as _to_dense
     cfg = block_ell.config
-    R, K, B, C = cfg.R, cfg.K, cfg.B, cfg.C
-    vals = block_ell.values
-    dense = torch.zeros(R, C, B, B, dtype=vals.dtype, device=vals.device)         # [R, C, B_out, B_in]
-    col = block_ell.col_indices.long()
-    alive = col >= 0
-    r_idx = torch.arange(R, device=vals.device)[:, None].expand(R, K)[alive]
-    dense[r_idx, col[alive]] = vals[alive].transpose(-1, -2)
-    return dense.permute(0, 2, 1, 3).reshape(R * B, C * B)
+    return _to_dense(block_ell.values, block_ell.col_indices, cfg.out_features, cfg.in_features)
 
 
 def block_ell_matmul(x: torch.Tensor, block_ell: BlockELLTensor, bias: torch.Tensor | None = None) -> torch.Tensor:

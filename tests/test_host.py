@@ -194,17 +194,41 @@ def test_layer_config_and_topology():
     assert torch.equal(col, create_random_topology(16, 8, 3, 0))
 
 
-def test_layer_dense_round_trip_matches_oracle():
+def test_layer_dense_conversions_refuse_cpu_tensors():
+    """The dense bridge runs on the HIP kernels only: CPU tensors are refused, never converted
+    by a CPU fallback (the GPU parity lives in test_gpu_format.py)."""
     from looped_blockell.layers import block_ell_to_dense, create_block_ell_from_dense
+    from looped_blockell.layers.block_ell import BlockELLConfig, BlockELLTensor
     w = torch.randn(64, 128, generator=torch.Generator().manual_seed(3))
-    e = create_block_ell_from_dense(w, tile_size=16, density=1.0)
-    assert torch.allclose(block_ell_to_dense(e), w)
-    e = create_block_ell_from_dense(w, tile_size=16, density=0.5)
-    v, c, cfg = O.create_block_ell_from_dense(w.numpy(), 16, 0.5)
-    np.testing.assert_array_equal(e.col_indices.numpy(), c)
-    np.testing.assert_array_equal(e.values.numpy(), v)
-    dense = block_ell_to_dense(e).numpy()
-    np.testing.assert_array_equal(dense, O.block_ell_to_dense(v, c, 64, 128))
+    with pytest.raises(RuntimeError, match="GPU"):
+        create_block_ell_from_dense(w, tile_size=16, density=1.0)
+    e = BlockELLTensor(torch.zeros(4, 8, 16, 16), torch.zeros(4, 8, dtype=torch.int32), BlockELLConfig(4, 8, 8, 16))
+    with pytest.raises(RuntimeError, match="GPU"):
+        block_ell_to_dense(e)
+
+
+def test_ternary_file_layout_on_host(tmp_path):
+    """save_ternary writes the documented header and the packed words unchanged: the words of
+    the oracle's packing round-trip through the file and unpack to the same codes."""
+    import json
+    from safetensors import safe_open
+    from looped_blockell.interop import TERNARY_FORMAT, save_ternary
+    rng = np.random.default_rng(4)
+    t = rng.integers(-1, 2, size=(3, 2, 32, 32)).astype(np.int8)
+    words = O.pack_ternary(t).view(np.int32)
+    scales = rng.random((3, 2)).astype(np.float32)
+    cols = np.array([[0, 2], [1, -1], [3, 0]], np.int32)
+    path = str(tmp_path / "w.safetensors")
+    save_ternary(path, {"core.0.w_gate": (torch.from_numpy(words), torch.from_numpy(scales), torch.from_numpy(cols))},
+                 in_features={"core.0.w_gate": 128}, metadata={"step": 7})
+    with safe_open(path, framework="pt", device="cpu") as f:
+        meta = f.metadata()
+        assert meta["format"] == TERNARY_FORMAT and meta["version"] == "1" and meta["user.step"] == "7"
+        assert json.loads(meta["weights"]) == ["core.0.w_gate"] and json.loads(meta["B"]) == {"core.0.w_gate": 32}
+        back = f.get_tensor("core.0.w_gate.packed").numpy()
+        np.testing.assert_array_equal(f.get_tensor("core.0.w_gate.col_indices").numpy(), cols)
+        np.testing.assert_array_equal(f.get_tensor("core.0.w_gate.scales").numpy(), scales)
+    np.testing.assert_array_equal(O.unpack_ternary(back.view(np.uint32)), t)
 
 
 def test_blockell_linear_topology_rules():
