@@ -10,7 +10,7 @@ forward pass.  The line also carries:
   cpu_baseline  the CPU oracle (numpy gather + matmul restatement of the
                 reference layer) timed on the host cores on the same workload;
   extra         the other workloads (shared gate/up topology, the backward of the
-                headline workload, ternary FFN, looped block L=8, decode, and the
+                headline workload and of one of its products, ternary FFN, looped block L=8, decode, and the
                 prune-time topology transforms on the headline weights).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only-main]
@@ -299,6 +299,31 @@ def bench_formats(steps, warmup, device):
                 kernel_ms_avg=sum(per) / len(per))
 
 
+def bench_matmul_backward(steps, warmup, device):
+    """Backward of one Block-ELL product at the headline gate shape (x [16384, 1024] -> [16384, 4096],
+    B=32, 25 %): dx = dy W and the tile gradients (titan::block_ell_matmul_bwd), 2x the product's
+    nonzero-block FLOPs."""
+    import torch
+    from looped_blockell import kernels
+    w = WORKLOADS["bf16"]
+    gen = torch.Generator(device=device).manual_seed(w["seed"])
+    Rf, Rm, Cm, Cf, Kg, Kd = geometry(w)
+    vals, cols = make_bell(Rf, Cm, Kg, w["B"], gen, device)
+    x = torch.randn(w["N"], w["d_model"], generator=gen, device=device).to(torch.bfloat16)
+    dy = torch.randn(w["N"], w["d_ff"], generator=gen, device=device).to(torch.bfloat16)
+    out = {}
+
+    def step(i):
+        out["r"] = kernels.block_ell_matmul_bwd(dy, x, vals, cols)
+
+    ms, per = time_steps(step, steps, warmup)
+    flops = 2 * 2 * w["N"] * w["B"] ** 2 * Rf * Kg
+    assert all(torch.isfinite(t.float()).all() for t in out["r"])
+    return dict(workload="backward of one Block-ELL product, x [16384,1024] -> [16384,4096], B=32, density 0.25",
+                ms_per_step=ms, value=flops / (ms * 1e-3) / 1e12, unit="TFLOP/s",
+                frac_of_bf16_peak=flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, kernel_ms_avg=sum(per) / len(per))
+
+
 def bench_ternary(steps, warmup, device):
     import torch
     from looped_blockell import kernels
@@ -408,8 +433,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-main", action="store_true", help="headline workload only (for profiling)")
     ap.add_argument("--only", default="",
-                    help="comma list of extra workloads to run: shared,backward,ternary,looped,decode,topology,"
-                         "formats")
+                    help="comma list of extra workloads to run: shared,backward,matmul_backward,ternary,looped,"
+                         "decode,topology,formats")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one 256 MiB device-to-device copy (a reference point for HBM byte counters)")
     args = ap.parse_args()
@@ -434,10 +459,11 @@ def main():
     main_res = bench_bf16(args.steps, args.warmup, device)
     extra = {}
     if not args.only_main:
-        todo = [s for s in args.only.split(",") if s] or ["shared", "backward", "ternary", "looped", "decode",
-                                                           "topology", "formats"]
-        fns = dict(shared=bench_bf16_shared, backward=bench_bf16_backward, ternary=bench_ternary,
-                   looped=bench_looped, decode=bench_decode, topology=bench_topology, formats=bench_formats)
+        todo = [s for s in args.only.split(",") if s] or ["shared", "backward", "matmul_backward", "ternary", "looped",
+                                                           "decode", "topology", "formats"]
+        fns = dict(shared=bench_bf16_shared, backward=bench_bf16_backward, matmul_backward=bench_matmul_backward,
+                   ternary=bench_ternary, looped=bench_looped, decode=bench_decode, topology=bench_topology,
+                   formats=bench_formats)
         for name in todo:
             st = max(5, args.steps // (4 if name == "looped" else 1))
             try:

@@ -228,6 +228,19 @@ int lbk_swiglu_fwd_ternary(const int8_t* xq, const float* sx, int64_t N, int32_t
                            uint16_t* out, uint16_t* h_out, int8_t* hq_out, float* sh_out,
                            void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Backward of the Block-ELL product y = x W^T (bias excluded): dx = grad_out W (tile [B_in, B_out]
+ * of slot (r, k) sends grad_out[:, r] back to column block col[r,k]) and, per tile,
+ * d_values[r,k] = x[:, col]^T grad_out[:, r] (zero for dead slots).  grad_out [N, R*B],
+ * x [N, in_features] (needed only for d_values), either output may be NULL.  Deterministic
+ * (fixed summation order, no atomics).  The reference differentiates block_ell_matmul with JAX
+ * autodiff (looped_blockell/layers/block_ell.py:149-182, tests/test_block_ell.py:57-72).
+ */
+size_t lbk_block_ell_matmul_bwd_workspace_bytes(int64_t N, int32_t in_features, const lbk_bell* w);
+int lbk_block_ell_matmul_bwd_bf16(const uint16_t* grad_out, const uint16_t* x, int64_t N, int32_t in_features,
+                                  const lbk_bell* w, uint16_t* dx, uint16_t* d_values, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+
 /* ---- prune-time topology transforms (integer and copy work; alive masks are one byte per slot,
  * nonzero = alive).  Replaces the JAX functions of looped_blockell/opt/compaction.py and
  * looped_blockell/opt/column_reorder.py on device. */

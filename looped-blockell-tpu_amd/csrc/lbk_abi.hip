@@ -561,6 +561,61 @@ int lbk_swiglu_bwd_bf16(const uint16_t* grad_out, const uint16_t* x, const uint1
   return LBK_OK;
 }
 
+size_t lbk_block_ell_matmul_bwd_workspace_bytes(int64_t N, int32_t in_features, const lbk_bell* w) {
+  if (!w || N < 0 || in_features <= 0 || !tile_ok(w->B) || in_features % w->B) return 0;
+  const int C = in_features / w->B;
+  return tlist_bytes(w, C) + align256((size_t)dw_chunks(N) * w->R * w->K * w->B * w->B * 4);
+}
+
+int lbk_block_ell_matmul_bwd_bf16(const uint16_t* grad_out, const uint16_t* x, int64_t N, int32_t in_features,
+                                  const lbk_bell* w, uint16_t* dx, uint16_t* d_values, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  int st;
+  if ((st = check_bell(w))) return st;
+  if (N < 0 || in_features <= 0) return LBK_ERR_ARG;
+  const int B = w->B;
+  if (in_features % B) return LBK_ERR_SHAPE;
+  const int C = in_features / B;
+  const int64_t nt = (int64_t)w->R * w->K, out_f = (int64_t)w->R * B;
+  if (d_values && !a16(d_values)) return LBK_ERR_ALIGN;
+  if (nt > 0 && !a16(w->values)) return LBK_ERR_ALIGN;
+  if (N > 0 && (dx || d_values)) {
+    if (!grad_out || (d_values && !x)) return LBK_ERR_NULL;
+    if (!a16(grad_out) || (x && !a16(x)) || (dx && !a16(dx)) || in_features % 8) return LBK_ERR_ALIGN;
+  }
+  const size_t need = lbk_block_ell_matmul_bwd_workspace_bytes(N, in_features, w);
+  if (!workspace || workspace_bytes < need) return LBK_ERR_WORKSPACE;
+  if (!a16(workspace)) return LBK_ERR_ALIGN;
+  hipStream_t s = S(stream);
+  char* p = static_cast<char*>(workspace);
+  auto take = [&](size_t bytes) {
+    char* q = p;
+    p += align256(bytes);
+    return q;
+  };
+  TListJob lj{};
+  lj.col = w->col_idx; lj.R = w->R; lj.K = w->K; lj.C = C;
+  lj.cnt = reinterpret_cast<int32_t*>(take((size_t)C * 4));
+  lj.list = reinterpret_cast<int32_t*>(take((size_t)C * w->R * w->K * 4));
+  float* part = reinterpret_cast<float*>(p);
+  if (dx && N > 0) {
+    // dx = dy W: out[:, c] = sum over the slots of column block c of dy[:, r] W[r,k]^T (with no
+    // tiles at all the product kernel writes zeros)
+    if (nt > 0 && launch_tlist(&lj, 1, s)) return LBK_ERR_LAUNCH;
+    TProdArgs a{};
+    a.nsrc = 0;
+    if (nt > 0) a.src[a.nsrc++] = TProdSrc{grad_out, out_f, w->values, w->K, lj.cnt, lj.list, nt};
+    a.N = N; a.C = C; a.ldo = in_features;
+    a.out = dx;
+    if (launch_tprod(B, 1, a, s)) return LBK_ERR_LAUNCH;
+  }
+  if (d_values && nt > 0) {
+    DWJob dj{x, in_features, grad_out, out_f, w->col_idx, w->R, w->K, C, part, d_values};
+    if (launch_dw(B, &dj, 1, N, DW_CHUNK, s)) return LBK_ERR_LAUNCH;
+  }
+  return LBK_OK;
+}
+
 // ---- topology transforms
 int lbk_topology_alive_counts(const uint8_t* alive, int32_t R, int32_t K, int32_t* counts, int32_t* max_count,
                               void* stream) {

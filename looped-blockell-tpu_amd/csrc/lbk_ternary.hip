@@ -300,8 +300,14 @@ int launch_ternary(int B, int mode, const TernaryLaunch& a, hipStream_t st) {
   return -2;
 }
 
+// clears the counter with a kernel (a memset node recorded into a captured graph is avoided)
+__global__ __launch_bounds__(64) void zero_counter_kernel(int32_t* __restrict__ p) {
+  if (threadIdx.x == 0) p[0] = 0;
+}
+
 int launch_check_columns(const int32_t* col, int64_t count, int C, int32_t* bad, hipStream_t st) {
-  if (hipMemsetAsync(bad, 0, sizeof(int32_t), st) != hipSuccess) return -1;
+  hipLaunchKernelGGL(zero_counter_kernel, dim3(1), dim3(64), 0, st, bad);
+  if (hipGetLastError() != hipSuccess) return -1;
   if (count == 0) return 0;
   hipLaunchKernelGGL(check_columns_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st, col, count, C,
                      bad);

@@ -152,6 +152,29 @@ at::Tensor block_ell_matmul(const at::Tensor& x_, const at::Tensor& v_, const at
   return y;
 }
 
+// backward of block_ell_matmul (bias gradient excluded): (dx, d_values)
+std::tuple<at::Tensor, at::Tensor> block_ell_matmul_bwd(const at::Tensor& dy_, const at::Tensor& x_,
+                                                        const at::Tensor& v_, const at::Tensor& c_) {
+  const char* op = "block_ell_matmul_bwd";
+  at::Tensor v = v_, c = c_;
+  at::Tensor x = check_x2d(x_, op);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  lbk_bell w = make_bell(v, c, op, "weight");
+  TORCH_CHECK(x.size(1) % w.B == 0, "titan::block_ell_matmul_bwd: in_features ", x.size(1),
+              " not a multiple of B=", w.B);
+  const int64_t N = x.size(0), out_f = (int64_t)w.R * w.B;
+  at::Tensor dy = check_x2d(dy_, op);
+  TORCH_CHECK(dy.size(0) == N && dy.size(1) == out_f, "titan::block_ell_matmul_bwd: grad_out must be [", N, ", ",
+              out_f, "], got ", dy.sizes());
+  at::Tensor dx = at::empty({N, x.size(1)}, x.options());
+  at::Tensor dv = at::empty_like(v);
+  const size_t wsb = lbk_block_ell_matmul_bwd_workspace_bytes(N, (int32_t)x.size(1), &w);
+  at::Tensor ws = workspace(wsb, x);
+  LBK_CALL("block_ell_matmul_bwd", lbk_block_ell_matmul_bwd_bf16(bf(dy), bf(x), N, (int32_t)x.size(1), &w, bfm(dx),
+                                                                 bfm(dv), ws.data_ptr(), wsb, cur_stream(x)));
+  return {dx, dv};
+}
+
 // ------------------------------------------------------------------ norm / loop
 at::Tensor rmsnorm(const at::Tensor& x_, const at::Tensor& scale_, double eps) {
   at::Tensor x = check_x2d(x_, "rmsnorm");
@@ -430,6 +453,7 @@ TORCH_LIBRARY(titan, m) {
         "Tensor[] down_values, Tensor[] down_col_idx) -> Tensor");
   // ops beyond the reference's set
   m.def("block_ell_matmul(Tensor x, Tensor values, Tensor col_indices, Tensor? bias=None) -> Tensor");
+  m.def("block_ell_matmul_bwd(Tensor grad_out, Tensor x, Tensor values, Tensor col_indices) -> (Tensor, Tensor)");
   m.def("block_ell_swiglu_bwd_ex(Tensor grad_out, Tensor x, Tensor gate_pre_act, Tensor up_out, Tensor h, "
         "Tensor v_gate, Tensor ci_gate, Tensor v_up, Tensor ci_up, Tensor v_down, Tensor ci_down, "
         "bool add_residual) -> (Tensor, Tensor, Tensor, Tensor)");
@@ -459,6 +483,7 @@ TORCH_LIBRARY_IMPL(titan, CUDA, m) {
   m.impl("pin_weights_l2", &pin_weights_l2);
   m.impl("persistent_mlp_step", &persistent_mlp_step);
   m.impl("block_ell_matmul", &block_ell_matmul);
+  m.impl("block_ell_matmul_bwd", &block_ell_matmul_bwd);
   m.impl("looped_swiglu", &looped_swiglu);
   m.impl("rmsnorm", &rmsnorm);
   m.impl("diagonal_injection", &diagonal_injection);
@@ -507,6 +532,9 @@ TORCH_LIBRARY_IMPL(titan, Meta, m) {
   m.impl("block_ell_matmul", [](const at::Tensor& x, const at::Tensor& v, const at::Tensor&,
                                 const c10::optional<at::Tensor>&) {
     return at::empty({x.size(0), v.size(0) * v.size(2)}, x.options());
+  });
+  m.impl("block_ell_matmul_bwd", [](const at::Tensor&, const at::Tensor& x, const at::Tensor& v, const at::Tensor&) {
+    return std::make_tuple(at::empty_like(x), at::empty_like(v));
   });
   m.impl("looped_swiglu", [](const at::Tensor& h, const at::Tensor&, const at::Tensor&, const at::Tensor&,
                              const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t,

@@ -59,6 +59,8 @@ SIGNATURES = {
     "lbk_k_active_macros": (C.c_int, [_P, _P, _I32, _I32, _I32, _P, _P]),
     "lbk_gather_rows": (C.c_int, [_P, _I64, _I64, _P, _I64, _P, _P]),
     "lbk_transposed_index": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P]),
+    "lbk_block_ell_matmul_bwd_workspace_bytes": (C.c_size_t, [_I64, _I32, _PB]),
+    "lbk_block_ell_matmul_bwd_bf16": (C.c_int, [_P, _P, _I64, _I32, _PB, _P, _P, _P, C.c_size_t, _P]),
     "lbk_dense_to_block_ell": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _P, _I32, _P, _P]),
     "lbk_block_ell_to_dense": (C.c_int, [_P, _P, _I32, _I32, _I32, _I32, _I32, _P, _I64, _P]),
     "lbk_block_ell_topk_columns": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P]),

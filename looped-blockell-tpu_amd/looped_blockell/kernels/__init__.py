@@ -50,12 +50,46 @@ def _gpu(*ts):
 
 # ---------------------------------------------------------------- bf16 path
 
+def block_ell_matmul_bwd(grad_out, x, values, col_indices):
+    """``titan::block_ell_matmul_bwd``: ``(dx, d_values)`` of ``y = x W^T``; dead slots get zero
+    tile gradients."""
+    _gpu(grad_out, x, values, col_indices)
+    return ops().block_ell_matmul_bwd(grad_out, x, values, col_indices)
+
+
+class _BlockELLMatmulFunction(torch.autograd.Function):
+    """Differentiable Block-ELL product: the backward is ``titan::block_ell_matmul_bwd`` (dx and
+    the tile gradients) plus the bias gradient (the column sums of grad_out); the column
+    indices get no gradient."""
+
+    @staticmethod
+    def forward(ctx, x2, values, col_indices, bias):
+        y = ops().block_ell_matmul(x2, values, col_indices, bias)
+        ctx.save_for_backward(x2, values, col_indices)
+        ctx.has_bias = bias is not None
+        ctx.bias_dtype = bias.dtype if bias is not None else None
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x2, values, col_indices = ctx.saved_tensors
+        dy = gy.to(torch.bfloat16).contiguous()
+        dx, dv = ops().block_ell_matmul_bwd(dy, x2, values, col_indices)
+        db = gy.float().sum(0).to(ctx.bias_dtype) if ctx.has_bias and ctx.needs_input_grad[3] else None
+        return dx, dv, None, db
+
+
 def block_ell_matmul(x: torch.Tensor, values: torch.Tensor, col_indices: torch.Tensor,
                      bias: torch.Tensor | None = None) -> torch.Tensor:
-    """x [..., C*B] -> [..., R*B] through the Block-ELL weight (tiles [B_in, B_out])."""
+    """x [..., C*B] -> [..., R*B] through the Block-ELL weight (tiles [B_in, B_out]);
+    differentiable in x, values and bias (``titan::block_ell_matmul_bwd``)."""
     _gpu(x, values, col_indices)
     lead = x.shape[:-1]
-    y = ops().block_ell_matmul(x.reshape(-1, x.shape[-1]).to(torch.bfloat16), values, col_indices, bias)
+    x2 = x.reshape(-1, x.shape[-1]).to(torch.bfloat16).contiguous()
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, values, bias)):
+        y = _BlockELLMatmulFunction.apply(x2, values, col_indices, bias)
+    else:
+        y = ops().block_ell_matmul(x2, values, col_indices, bias)
     return y.reshape(*lead, y.shape[-1])
 
 

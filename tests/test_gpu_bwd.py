@@ -8,6 +8,8 @@ to bf16, then given to both sides; the oracle differentiates in float64.  Bar: m
 between its products, as the reference operator does).
 """
 
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -157,3 +159,136 @@ def test_layer_autograd(gpu):
     for lin, ref in ((m.w_gate, dvg), (m.w_up, dvu), (m.w_down, dvd)):
         assert T.rel_err(T.to_np(lin.values.grad), ref)[0] <= TOL
     assert torch.count_nonzero(m.w_up.values.grad[2, 1]).item() == 0
+
+
+# ------------------------------------------------------------------ block_ell_matmul backward
+
+MM_CASES = [
+    # (out_features, in_features, B, density, N, sentinel_frac)
+    (256, 512, 32, 0.25, 130, 0.1),
+    (128, 256, 16, 0.5, 77, 0.0),
+    (512, 256, 64, 0.25, 40, 0.05),
+    (1024, 4096, 32, 0.25, 2100, 0.0),      # two token chunks of the tile gradients
+    (256, 2048, 16, 0.125, 33, 0.0),       # 128 output blocks: dx through the per-entry gather kernel
+]
+
+
+def _abi_matmul_bwd(dy_t, x_t, w_t, want_dx=True, want_dv=True):
+    import torch
+    A = T.abi()
+    lib = A.load()
+    vals_t, col_t = w_t
+    N, F = x_t.shape
+    wb = T.bell_struct(vals_t, col_t)
+    wsb = lib.lbk_block_ell_matmul_bwd_workspace_bytes(N, F, C.byref(wb))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
+    dx = torch.empty(N, F, dtype=torch.bfloat16, device="cuda") if want_dx else None
+    dv = torch.empty_like(vals_t) if want_dv else None
+    A.check(lib.lbk_block_ell_matmul_bwd_bf16(T.ptr(dy_t), T.ptr(x_t), N, F, C.byref(wb), T.ptr(dx), T.ptr(dv),
+                                              T.ptr(ws), wsb, T.stream()), "block_ell_matmul_bwd")
+    return dx, dv
+
+
+@pytest.mark.parametrize("case", MM_CASES)
+def test_block_ell_matmul_bwd_parity(gpu, case):
+    out_f, in_f, B, dens, N, sf = case
+    _say(f"matmul bwd {case}")
+    rng = np.random.default_rng(abs(hash(case)) % 2 ** 31)
+    R, Cb = out_f // B, in_f // B
+    vals, col = T.bell_weight(rng, R, Cb, O.k_for_density(Cb, dens), B)
+    col[rng.random(col.shape) < sf] = -1
+    x, dy = T.act(rng, N, in_f), T.act(rng, N, out_f)
+    dx, dv = _abi_matmul_bwd(T.to_gpu_bf16(dy), T.to_gpu_bf16(x), T.gpu_weight((vals, col)))
+    rdx = O.block_ell_matmul_t(dy.astype(np.float64), vals.astype(np.float64), col, Cb)
+    rdv = O.block_ell_weight_grad(x.astype(np.float64), dy.astype(np.float64), col, B)
+    for got, ref, name in ((dx, rdx, "dx"), (dv, rdv, "d_values")):
+        rel, ab = T.rel_err(T.to_np(got), ref)
+        assert rel <= TOL, f"{name}: rel {rel} abs {ab}"
+    assert np.all(T.to_np(dv)[col < 0] == 0)
+
+
+def test_block_ell_matmul_bwd_optional_outputs_and_no_tiles(gpu):
+    """Either output may be skipped; a weight whose slots are all dead gives dx = 0."""
+    import torch
+    _say("matmul bwd optional outputs")
+    rng = np.random.default_rng(8)
+    vals, col = T.bell_weight(rng, 8, 8, 4, 16)
+    x, dy = T.act(rng, 50, 128), T.act(rng, 50, 128)
+    w = T.gpu_weight((vals, col))
+    dx, dv = _abi_matmul_bwd(T.to_gpu_bf16(dy), T.to_gpu_bf16(x), w)
+    dx2, none = _abi_matmul_bwd(T.to_gpu_bf16(dy), T.to_gpu_bf16(x), w, want_dv=False)
+    none2, dv2 = _abi_matmul_bwd(T.to_gpu_bf16(dy), T.to_gpu_bf16(x), w, want_dx=False)
+    assert none is None and none2 is None
+    assert torch.equal(dx, dx2) and torch.equal(dv, dv2)
+    dead = (w[0], torch.full_like(w[1], -1))
+    dx3, dv3 = _abi_matmul_bwd(T.to_gpu_bf16(dy), T.to_gpu_bf16(x), dead)
+    assert torch.count_nonzero(dx3).item() == 0 and torch.count_nonzero(dv3).item() == 0
+
+
+def test_block_ell_linear_autograd_matches_dense_fp32(gpu):
+    """BlockELLLinear (bias, one pruned tile) trained through titan::block_ell_matmul_bwd: the
+    gradients of x, the tiles and the bias match a dense float32 torch reference; the
+    reference's gradient-flow test (non-zero tile gradients of the right shape) holds."""
+    import torch
+    from looped_blockell.layers import BlockELLLinear
+    _say("BlockELLLinear autograd")
+    torch.manual_seed(4)
+    lin = BlockELLLinear(96, 128, tile_size=16, density=0.5, device="cuda")
+    with torch.no_grad():
+        lin.bias.copy_(torch.randn(96, device="cuda") * 0.1)
+    lin.alive_mask[1, 2] = False
+    x = torch.randn(3, 7, 128, device="cuda").requires_grad_(True)
+    y = lin(x)
+    gy = torch.randn_like(y.float())
+    y.float().backward(gy)
+    # dense fp32 reference on the same bf16-rounded operands
+    vals = lin.values.detach().to(torch.bfloat16).float().cpu().numpy()
+    col = lin.effective_col_indices().cpu().numpy()
+    W = torch.from_numpy(O.block_ell_to_dense(vals, col, 96, 128)).requires_grad_(True)
+    xr = x.detach().to(torch.bfloat16).float().cpu().requires_grad_(True)
+    br = lin.bias.detach().float().cpu().requires_grad_(True)
+    yr = xr @ W.T + br
+    gyr = gy.to(torch.bfloat16).float().cpu()
+    yr.backward(gyr)
+    assert T.rel_err(T.to_np(y.detach().float()), yr.detach().numpy())[0] <= TOL
+    assert T.rel_err(T.to_np(x.grad), xr.grad.numpy())[0] <= TOL
+    assert T.rel_err(T.to_np(lin.bias.grad), br.grad.numpy())[0] <= TOL
+    ref_tiles = O.dense_to_block_ell(W.grad.numpy(), 16)[0]                  # [R, C, B_in, B_out]
+    got = T.to_np(lin.values.grad)
+    for r in range(lin.R):
+        for k in range(lin.K):
+            c = col[r, k]
+            ref = ref_tiles[r, c] if c >= 0 else np.zeros((16, 16), np.float32)
+            assert T.rel_err(got[r, k], ref)[1] <= TOL * max(np.abs(ref_tiles).max(), 1e-30)
+    assert lin.values.grad.shape == lin.values.shape and torch.count_nonzero(lin.values.grad).item() > 0
+    assert torch.count_nonzero(lin.values.grad[1, 2]).item() == 0
+
+
+def test_gelu_mlpblock_backward_runs(gpu):
+    """MLPBlock(use_swiglu=False): both Block-ELL products are differentiable; the gradients of
+    x match a float32 torch recomputation with the same tiles."""
+    import torch
+    import torch.nn.functional as F
+    from looped_blockell.layers import MLPBlock
+    _say("GELU MLPBlock autograd")
+    torch.manual_seed(6)
+    m = MLPBlock(128, 256, use_swiglu=False, tile_size=32, density=0.5, device="cuda")
+    x = torch.randn(40, 128, device="cuda").to(torch.bfloat16).requires_grad_(True)
+    y = m(x)
+    gy = torch.randn_like(y.float())
+    y.float().backward(gy)
+
+    def dense(lin):
+        v = lin.values.detach().to(torch.bfloat16).float().cpu().numpy()
+        return torch.from_numpy(O.block_ell_to_dense(v, lin.effective_col_indices().cpu().numpy(), lin.out_features,
+                                                     lin.in_features))
+
+    W1, W2 = dense(m.fc1), dense(m.fc2)
+    xr = x.detach().float().cpu().requires_grad_(True)
+    h = F.gelu(xr @ W1.T + m.fc1.bias.detach().float().cpu())
+    yr = h.to(torch.bfloat16).float() @ W2.T + m.fc2.bias.detach().float().cpu()
+    yr.backward(gy.to(torch.bfloat16).float().cpu())
+    assert T.rel_err(T.to_np(x.grad), xr.grad.numpy())[0] <= 3 * TOL
+    for lin in (m.fc1, m.fc2):
+        assert lin.values.grad is not None and torch.count_nonzero(lin.values.grad).item() > 0
+        assert lin.bias.grad is not None
