@@ -292,3 +292,65 @@ def test_gelu_mlpblock_backward_runs(gpu):
     for lin in (m.fc1, m.fc2):
         assert lin.values.grad is not None and torch.count_nonzero(lin.values.grad).item() > 0
         assert lin.bias.grad is not None
+
+
+def test_swiglu_bwd_full_size_sampled(gpu):
+    """The headline shape (d_model 1024, d_ff 4096, B 32, 25 %, 16384 tokens), saved tensors from
+    the GPU forward: dx checked on sampled token rows (a row of dx depends only on that row), the
+    tile gradients on sampled tiles (each a sum over all 16384 tokens, recomputed in float64 from
+    the same saved tensors); two calls agree bit for bit."""
+    import torch
+    _say("full size d_model=1024 d_ff=4096 B=32 N=16384 (sampled)")
+    rng = np.random.default_rng(2024)
+    d_model, d_ff, B, N = 1024, 4096, 32, 16384
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25)
+    x, dy = T.act(rng, N, d_model), T.act(rng, N, d_model)
+    gw, uw, dw = T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d)
+    x_t, dy_t = T.to_gpu_bf16(x), T.to_gpu_bf16(dy)
+    _, h_t, gp_t, uo_t = T.abi_swiglu(x_t, gw, uw, dw, add_residual=True, intermediates=True)
+    got = T.abi_swiglu_bwd(dy_t, x_t, gp_t, uo_t, h_t, gw, uw, dw)
+    again = T.abi_swiglu_bwd(dy_t, x_t, gp_t, uo_t, h_t, gw, uw, dw)
+    for a_, b_ in zip(got, again):
+        assert torch.equal(a_, b_)
+    gp, uo, h = (T.to_np(t) for t in (gp_t, uo_t, h_t))
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    # dx on sampled rows
+    rows = np.sort(rng.choice(N, 96, replace=False))
+    rdx = O.swiglu_bwd(dy[rows], x[rows], gp[rows], uo[rows], h[rows], f64(g), f64(u), f64(d))[0]
+    rel, ab = T.rel_err(T.to_np(got[0])[rows], rdx)
+    assert rel <= TOL, f"dx rows: rel {rel} abs {ab}"
+    # tile gradients on sampled tiles
+    Wd, dcol = d[0].astype(np.float64), d[1]
+
+    def dh_block(r):            # dh[:, r-th d_ff block] = sum over down slots reading it of dy[:, rm] Wd^T
+        out = np.zeros((N, B))
+        for rm, kk in zip(*np.nonzero(dcol == r)):
+            out += dy[:, rm * B:(rm + 1) * B].astype(np.float64) @ Wd[rm, kk].T
+        return out
+
+    def check(name, got_t, col, ref_tile):
+        R, K = col.shape
+        picks = [(int(r), int(k)) for r, k in zip(rng.integers(0, R, 12), rng.integers(0, K, 12))]
+        gt = T.to_np(got_t)
+        refs = [ref_tile(r, k) for r, k in picks]
+        den = max(np.abs(np.stack(refs)).max(), 1e-30)
+        for (r, k), ref in zip(picks, refs):
+            err = np.abs(gt[r, k] - ref).max() / den
+            assert err <= TOL, f"{name} tile ({r},{k}): rel {err}"
+
+    def gate_up_tile(which):
+        def tile(r, k):
+            c = (g if which == "gate" else u)[1][r, k]
+            dh = dh_block(r)
+            gg = gp[:, r * B:(r + 1) * B].astype(np.float64)
+            uu = uo[:, r * B:(r + 1) * B].astype(np.float64)
+            s = 1.0 / (1.0 + np.exp(-gg))
+            gy = dh * uu * (s + gg * s * (1.0 - s)) if which == "gate" else dh * gg * s
+            return x[:, c * B:(c + 1) * B].astype(np.float64).T @ gy
+        return tile
+
+    check("d_gate", got[1], g[1], gate_up_tile("gate"))
+    check("d_up", got[2], u[1], gate_up_tile("up"))
+    check("d_down", got[3], dcol,
+          lambda r, k: h[:, dcol[r, k] * B:(dcol[r, k] + 1) * B].astype(np.float64).T
+          @ dy[:, r * B:(r + 1) * B].astype(np.float64))
