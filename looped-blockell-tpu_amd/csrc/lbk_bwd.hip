@@ -341,13 +341,18 @@ __global__ __launch_bounds__(512, 1) void dh_panel_kernel(TProdArgs a) {
       const int lv = (j0 + lane < cnt) ? L[j0 + lane] : 0;   // 64 entries, one per lane
       const int jn = (cnt - j0) < 64 ? (cnt - j0) : 64;
       auto ent = [&](int jj) { return __builtin_amdgcn_readlane(lv, jj < jn ? jj : jn - 1); };
-      Ent E0, E1;
-      load(ent(0), E0);
-      for (int jj = 0; jj < jn; jj += 2) {
-        load(ent(jj + 1), E1);
-        compute(E0);
-        load(ent(jj + 2), E0);
-        if (jj + 1 < jn) compute(E1);
+      // a DHR-entry ring: DHR - 1 tile loads in flight ahead of the MFMAs (positions past the
+      // end reload the last entry and are not computed)
+      constexpr int DHR = B == 64 ? 2 : 6;
+      Ent E[DHR];
+#pragma unroll
+      for (int k = 0; k < DHR - 1; ++k) load(ent(k), E[k]);
+      for (int jj = 0; jj < jn; jj += DHR) {
+#pragma unroll
+        for (int k = 0; k < DHR; ++k) {
+          load(ent(jj + k + DHR - 1), E[(k + DHR - 1) % DHR]);
+          if (k == 0 || jj + k < jn) compute(E[k]);
+        }
       }
     }
     // epilogue: lane (i, g) of acc[q] holds dh of token t0 + 16q + i (columns as op_row
