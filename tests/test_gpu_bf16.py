@@ -60,10 +60,10 @@ def test_matmul_out_of_range_column_is_skipped(gpu):
 
 SWIGLU_CASES = [
     # (d_model, d_ff, B, density, N, sentinel_frac)   panel path unless noted
-    (256, 1024, 16, 0.25, 512, 0.0),      # config-1 geometry
+    (256, 1024, 16, 0.25, 512, 0.0),      # the small CPU-runnable geometry
     (256, 1024, 16, 0.25, 77, 0.1),       # ragged N, dead slots
     (512, 1024, 32, 0.25, 130, 0.0),
-    (1024, 4096, 32, 0.25, 200, 0.05),    # config-2 geometry, small N
+    (1024, 4096, 32, 0.25, 200, 0.05),    # the headline geometry, small N
     (128, 512, 64, 0.5, 70, 0.0),         # B = 64 -> general two-kernel path
     (2048, 1024, 32, 0.125, 40, 0.0),     # d_model > 1024: 32-token gate/up panels, 64 down rows
     (2048, 2048, 16, 0.125, 100, 0.05),   # 128 down rows: 16 row groups per token block
@@ -183,11 +183,12 @@ def test_swiglu_zero_k(gpu):
     assert not T.to_np(h).any()
 
 
-def test_swiglu_full_config2_sampled_rows(gpu):
-    """Config 2 at full size (N=16384); rows are independent, so sampled rows are checked."""
+def test_swiglu_full_headline_sampled_rows(gpu):
+    """The headline FFN (d_model 1024, d_ff 4096, B 32, density 0.25) at its full 16384 tokens; rows are
+    independent, so sampled rows are checked."""
     rng = np.random.default_rng(1002)
     d_model, d_ff, B, N = 1024, 4096, 32, 16384
-    _say("swiglu config-2 full size")
+    _say("swiglu d1024 ff4096 B32 N16384 full size")
     g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25)
     x = T.act(rng, N, d_model)
     out, *_ = T.abi_swiglu(T.to_gpu_bf16(x), T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d))
@@ -214,7 +215,7 @@ def test_swiglu_deterministic(gpu):
 LOOP_CASES = [
     # (d_model, d_ff, B, density, N, L)
     (256, 1024, 16, 0.25, 100, 3),
-    (1024, 4096, 32, 0.25, 130, 8),       # config-4 geometry
+    (1024, 4096, 32, 0.25, 130, 8),       # the looped-block geometry
     (128, 512, 64, 0.5, 40, 2),           # general path (per-iteration launches)
     (2048, 2048, 32, 0.125, 70, 2),       # 64 down rows: 8 row groups per token block
 ]
@@ -236,11 +237,12 @@ def test_looped_parity(gpu, case):
     assert rel <= TOL, f"rel {rel} abs {ab}"
 
 
-def test_looped_config4_sampled_rows(gpu):
-    """Config 4 at full size (32 x 512 tokens, L = 8, norm scale ones); sampled rows vs the oracle."""
+def test_looped_full_size_sampled_rows(gpu):
+    """The looped block at full size (32 x 512 tokens, d_model 1024, d_ff 4096, B 32, L = 8, norm scale
+    ones); sampled rows vs the oracle."""
     rng = np.random.default_rng(1004)
     d_model, d_ff, B, N, L = 1024, 4096, 32, 32 * 512, 8
-    _say("looped config-4 full size")
+    _say("looped L8 d1024 ff4096 B32 N16384 full size")
     g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25)
     h = T.act(rng, N, d_model)
     scale = np.ones(d_model, np.float32)
@@ -325,11 +327,11 @@ def test_decode_duplicates_and_workspace_reuse(gpu):
     assert np.array_equal(outs[0], outs[2])
 
 
-def test_decode_config5_full(gpu):
-    """Config 5 geometry: 16 tokens, d_model 4096, d_ff 14336, B 64, density 0.10."""
+def test_decode_full_geometry(gpu):
+    """The decode geometry: 16 tokens, d_model 4096, d_ff 14336, B 64, density 0.10."""
     rng = np.random.default_rng(1005)
     d_model, d_ff, B, N = 4096, 14336, 64, 16
-    _say("decode config-5 full size")
+    _say("decode N16 d4096 ff14336 B64 full size")
     g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.10)
     x = T.act(rng, N, d_model)
     out, *_ = T.abi_swiglu(T.to_gpu_bf16(x), T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d))

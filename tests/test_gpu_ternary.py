@@ -115,7 +115,7 @@ TERN_CASES = [
     (512, 2048, 64, 0.125, 100),
     (256, 1024, 32, 0.25, 65),
     (128, 512, 16, 0.25, 33),
-    (2048, 8192, 64, 0.125, 64),    # config-3 geometry, small N
+    (2048, 8192, 64, 0.125, 64),    # the ternary headline geometry, small N
 ]
 
 
@@ -227,10 +227,11 @@ def test_ternary_swiglu_split_extreme(gpu):
     assert np.array_equal(T.to_np(out), O.bf16_round(yd))
 
 
-def test_ternary_config3_full_sampled_rows(gpu):
-    """Config 3 at full size (N=8192); bit-exact checks on sampled rows."""
+def test_ternary_full_size_sampled_rows(gpu):
+    """The ternary FFN at full size (8192 tokens, d_model 2048, d_ff 8192, B 64); bit-exact checks on
+    sampled rows."""
     from looped_blockell import kernels
-    _say("ternary config-3 full size")
+    _say("ternary d2048 ff8192 B64 N8192 full size")
     rng = np.random.default_rng(1003)
     d_model, d_ff, B, N = 2048, 8192, 64, 8192
     g = tern_weight(rng, d_ff // B, d_model // B, 4, B)
