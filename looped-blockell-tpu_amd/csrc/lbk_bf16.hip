@@ -233,16 +233,53 @@ __global__ __launch_bounds__(256) void pack_bf16_kernel(const uint16_t* __restri
   pack_bf16_dword<B>(values, col, ntiles, C, ndw, packed, (int64_t)blockIdx.x * 256 + threadIdx.x, 0);
 }
 
-// several weights in one launch: workgroups [first[t], first[t + 1]) pack weight t
+// several weights in one launch, one wave per tile (the R*K tiles of weight t and its zero
+// tile are workgroups [first[t], first[t + 1])): the raw tile is read with 16-byte loads into
+// LDS, then each lane gathers its fragment dwords from there and writes them as 16-byte chunks
+// (chunk index (ks, m) is 64 consecutive u32x4 across the wave)
 template <int B>
-__global__ __launch_bounds__(256) void pack_bf16_multi_kernel(PackJobs jobs) {
+__global__ __launch_bounds__(64) void pack_bf16_multi_kernel(PackJobs jobs) {
+  constexpr int CW = TileShape<B>::CW, NKS = TileShape<B>::NKS;
+  constexpr int LANES = PackedTile<B>::LANES, U32X4 = PackedTile<B>::U32X4;
+  constexpr int RAW = B * B / 8;                     // 16-byte chunks of a raw tile
+  __shared__ __attribute__((aligned(16))) uint16_t s[B * B];
   int t = 0;
 #pragma unroll
   for (int u = 1; u < PackJobs::kMax; ++u)
     if (u < jobs.n && (int64_t)blockIdx.x >= jobs.first[u]) t = u;
   const PackJob& J = jobs.job[t];
-  pack_bf16_dword<B>(J.values, J.col, J.ntiles, J.C, J.ndw, J.packed,
-                     ((int64_t)blockIdx.x - jobs.first[t]) * 256 + threadIdx.x, J.gu_layout);
+  const int64_t tile = (int64_t)blockIdx.x - jobs.first[t];
+  const int lane = threadIdx.x;
+  u32x4* out = reinterpret_cast<u32x4*>(J.packed) + tile * U32X4;
+  const int c0 = tile < J.ntiles ? J.col[tile] : -1;
+  if (c0 < 0 || c0 >= J.C) {                         // dead slot or the appended zero tile
+    for (int q = lane; q < U32X4; q += 64) out[q] = u32x4{0, 0, 0, 0};
+    return;
+  }
+  if ((reinterpret_cast<uintptr_t>(J.values) & 15u) == 0) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(J.values + tile * B * B);
+    for (int q = lane; q < RAW; q += 64) reinterpret_cast<u32x4*>(s)[q] = src[q];
+  } else {                                           // 8-byte aligned values (the ABI's minimum)
+    const u32x2* src = reinterpret_cast<const u32x2*>(J.values + tile * B * B);
+    for (int q = lane; q < 2 * RAW; q += 64) reinterpret_cast<u32x2*>(s)[q] = src[q];
+  }
+  __syncthreads();
+  if (lane >= LANES) return;
+  const int j = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+    for (int m = 0; m < CW; ++m) {
+      // gate/up layout (B = 32): column 8 (j / 4) + 4 m + j % 4, so that the product with the
+      // tile as the A operand leaves 8 consecutive columns of one token in each lane
+      const int c = (B == 32 && J.gu_layout) ? 8 * (j >> 2) + 4 * m + (j & 3) : CW * j + m;
+      const int k0 = 32 * ks + 8 * g;
+      u32x4 v;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        v[u] = (uint32_t)s[(k0 + 2 * u) * B + c] | ((uint32_t)s[(k0 + 2 * u + 1) * B + c] << 16);
+      out[(ks * CW + m) * LANES + lane] = v;
+    }
 }
 
 size_t packed_bf16_bytes(int64_t ntiles, int B) {
@@ -263,13 +300,13 @@ int launch_pack_bf16_multi(const PackJob* jobs, int n, int B, hipStream_t st) {
     J.job[t] = jobs[t];
     J.job[t].ndw = (int64_t)(packed_bf16_bytes(jobs[t].ntiles, B) / 4);
     J.first[t] = blocks;
-    blocks += (J.job[t].ndw + 255) / 256;
+    blocks += jobs[t].ntiles + 1;                    // one wave per tile, plus the zero tile
   }
   if (blocks == 0 || blocks > 0x7fffffff) return -2;
   const dim3 grid((unsigned)blocks);
-  if (B == 16) hipLaunchKernelGGL(pack_bf16_multi_kernel<16>, grid, dim3(256), 0, st, J);
-  else if (B == 32) hipLaunchKernelGGL(pack_bf16_multi_kernel<32>, grid, dim3(256), 0, st, J);
-  else if (B == 64) hipLaunchKernelGGL(pack_bf16_multi_kernel<64>, grid, dim3(256), 0, st, J);
+  if (B == 16) hipLaunchKernelGGL(pack_bf16_multi_kernel<16>, grid, dim3(64), 0, st, J);
+  else if (B == 32) hipLaunchKernelGGL(pack_bf16_multi_kernel<32>, grid, dim3(64), 0, st, J);
+  else if (B == 64) hipLaunchKernelGGL(pack_bf16_multi_kernel<64>, grid, dim3(64), 0, st, J);
   else return -2;
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
