@@ -1,5 +1,6 @@
 // lbk_internal.h — launcher interfaces shared between the kernel files and the C ABI.
 #pragma once
+#include <atomic>
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -30,6 +31,18 @@ int launch_pack_bf16(const uint16_t* values, const int32_t* col, int64_t ntiles,
                      hipStream_t st);
 size_t packed_bf16_bytes(int64_t ntiles, int B);   // includes the appended zero tile
 // up to three weights packed by one launch (ndw is filled in by the launcher)
+// Raises a kernel's dynamic LDS limit once per device: the attribute belongs to the device that
+// is current at the call (the device of the stream the kernel is then launched on).
+inline int set_lds_limit_once(const void* kern, int bytes, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  const uint64_t bit = (dev >= 0 && dev < 64) ? (1ull << dev) : 0ull;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return 0;
+  if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) return -1;
+  done.fetch_or(bit, std::memory_order_release);
+  return 0;
+}
+
 struct PackJob {
   const uint16_t* values; const int32_t* col; int64_t ntiles; int C; uint32_t* packed; int64_t ndw;
   int gu_layout;   // 1: column order of the gate/up kernel's swapped product (B = 32)

@@ -650,12 +650,8 @@ bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int 
 template <int B, int MT, bool NORM, bool INTER, bool SHARED>
 static int launch_gu_t(const GUArgs& a, hipStream_t st) {
   auto kern = gu_kernel<B, MT, NORM, INTER, SHARED>;
-  static bool configured = false;
-  if (!configured) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 163840) != hipSuccess)
-      return -1;
-    configured = true;
-  }
+  static std::atomic<uint64_t> configured{0};
+  if (set_lds_limit_once((const void*)kern, 163840, configured)) return -1;
   const int TM = 16 * MT;
   const size_t lds = gu_lds(a.R_ff, a.Kg, MT);
   hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + TM - 1) / TM)), dim3(512), lds, st, a);

@@ -661,13 +661,8 @@ int tgu_slices(int64_t N) {
 int launch_tgu(const TGUArgs& a, hipStream_t st) {
   if (a.N == 0) return 0;
   auto kern = tgu_kernel<4>;
-  static bool configured = false;
-  if (!configured) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 163840 - 256) !=
-        hipSuccess)
-      return -1;
-    configured = true;
-  }
+  static std::atomic<uint64_t> configured{0};
+  if (set_lds_limit_once((const void*)kern, 163840 - 256, configured)) return -1;
   const size_t lds = tgu_lds((a.R_ff + a.H - 1) / a.H, a.K);
   const int64_t blocks = (a.N + 63) / 64;
   hipLaunchKernelGGL(kern, dim3((unsigned)(blocks * a.H)), dim3(512), lds, st, a);
@@ -676,13 +671,8 @@ int launch_tgu(const TGUArgs& a, hipStream_t st) {
 
 int launch_tdn(const TDNArgs& a, hipStream_t st) {
   if (a.N == 0) return 0;
-  static bool configured = false;
-  if (!configured) {
-    if (hipFuncSetAttribute((const void*)tdn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 163840 - 256) !=
-        hipSuccess)
-      return -1;
-    configured = true;
-  }
+  static std::atomic<uint64_t> configured{0};
+  if (set_lds_limit_once((const void*)tdn_kernel, 163840 - 256, configured)) return -1;
   const size_t lds = tdn_lds(a.d_ff, a.R_m, a.Kd);
   hipLaunchKernelGGL(tdn_kernel, dim3((unsigned)((a.N + 15) / 16)), dim3(512), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
