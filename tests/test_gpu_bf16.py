@@ -85,6 +85,35 @@ def test_swiglu_parity(gpu, case, resid):
     assert rel <= TOL, f"rel {rel} abs {ab}"
 
 
+def _offset_bf16(a, elems):
+    """A bf16 GPU copy of `a` that starts `elems` elements (2 bytes each) into a larger buffer."""
+    import torch
+    flat = T.to_gpu_bf16(np.asarray(a, np.float32).reshape(-1))
+    buf = torch.zeros(flat.numel() + elems, dtype=torch.bfloat16, device=flat.device)
+    buf[elems:] = flat
+    return buf[elems:].view(*np.shape(a))
+
+
+@pytest.mark.parametrize("case", [(256, 1024, 16, 0.25, 60), (1024, 4096, 32, 0.25, 70)])
+def test_swiglu_weights_8_byte_aligned(gpu, case):
+    """Weight values only 8-byte aligned (the ABI's minimum): the packing kernel's 8-byte loads."""
+    d_model, d_ff, B, dens, N = case
+    _say(f"swiglu 8-byte aligned weights {case}")
+    rng = np.random.default_rng(31 + B)
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, dens, sentinel_frac=0.05)
+    x = T.act(rng, N, d_model)
+    w = [(_offset_bf16(v, 4), T.to_gpu(c.astype(np.int32))) for v, c in (g, u, d)]
+    assert all(t[0].data_ptr() % 16 == 8 for t in w)
+    out, *_ = T.abi_swiglu(T.to_gpu_bf16(x), *w, add_residual=True)
+    f64 = lambda w_: (w_[0].astype(np.float64), w_[1])
+    ref, *_ = O.swiglu_fwd(x.astype(np.float64), f64(g), f64(u), f64(d), add_residual=True)
+    rel, ab = T.rel_err(T.to_np(out), ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+    aligned, *_ = T.abi_swiglu(T.to_gpu_bf16(x), T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d),
+                               add_residual=True)
+    assert np.array_equal(T.to_np(out), T.to_np(aligned))     # same packed tiles, same result
+
+
 @pytest.mark.parametrize("case", [(256, 1024, 16, 0.25, 100), (1024, 4096, 32, 0.25, 64), (128, 256, 64, 1.0, 33)])
 def test_swiglu_with_intermediates(gpu, case):
     d_model, d_ff, B, dens, N = case
