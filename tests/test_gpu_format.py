@@ -76,12 +76,13 @@ def test_gather_tiles_sentinel_and_range(gpu):
             np.testing.assert_array_equal(got[r, k], ref)
 
 
-@pytest.mark.parametrize("dt,density", [("bf16", 0.5), ("fp32", 0.25), ("bf16", 1.0)])
-def test_create_block_ell_from_dense_parity(gpu, dt, density):
+@pytest.mark.parametrize("dt,density,B", [("bf16", 0.5, 32), ("fp32", 0.25, 32), ("bf16", 1.0, 32),
+                                          ("bf16", 0.25, 16), ("fp32", 0.5, 64)])
+def test_create_block_ell_from_dense_parity(gpu, dt, density, B):
     from looped_blockell.layers import block_ell_to_dense, create_block_ell_from_dense
-    _say(f"create_block_ell_from_dense {dt} density={density}")
-    rng = np.random.default_rng(int(density * 100))
-    B, out_f, in_f = 32, 128, 512
+    _say(f"create_block_ell_from_dense {dt} density={density} B={B}")
+    rng = np.random.default_rng(int(density * 100) + B)
+    out_f, in_f = 4 * B, 16 * B
     w = _dense(rng, out_f, in_f, dt)
     # equal-norm blocks: row 0 holds copies of one block (ties go to the smaller column)
     w[:B, B:2 * B] = w[:B, 3 * B:4 * B] = w[:B, 5 * B:6 * B] = w[:B, 0:B]
