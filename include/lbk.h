@@ -228,6 +228,34 @@ int lbk_swiglu_fwd_ternary(const int8_t* xq, const float* sx, int64_t N, int32_t
                            uint16_t* out, uint16_t* h_out, int8_t* hq_out, float* sh_out,
                            void* workspace, size_t workspace_bytes, void* stream);
 
+/* Optional exports of the ternary SwiGLU's accumulators before scaling (each pointer may be
+ * NULL; all 16-byte aligned, row-major, row stride = the feature count):
+ *   acc_gate, acc_up [N, d_ff] int32: sum_k m[r,k] * P[n,r,k,j] of the gate / up products
+ *   acc_down         [N, d_model] int32: the same sum of the down product (over hq)
+ *   gate_pre, up_pre [N, d_ff] fp32: f32(f32(acc) * 2^-e[r]) * sx[n], the pre-activations
+ *                    that enter silu(g) * u
+ * P is the exact int32 block partial of lbk_ternary_matmul and m, e its fixed point. */
+typedef struct lbk_ternary_acc {
+    int32_t* acc_gate;
+    int32_t* acc_up;
+    int32_t* acc_down;
+    float* gate_pre;
+    float* up_pre;
+} lbk_ternary_acc;
+
+/*
+ * lbk_swiglu_fwd_ternary with the accumulator exports of *acc (acc may be NULL, which is
+ * lbk_swiglu_fwd_ternary itself).  The same kernels run: the exports are extra stores in the
+ * epilogues.  Replaces the int32 accumulate-then-scale contract of BitLinear (reference
+ * bonsai-test/bitlinear.py:34-69, :132-138) with the group = one B x B block.
+ */
+int lbk_swiglu_fwd_ternary_acc(const int8_t* xq, const float* sx, int64_t N, int32_t d_model,
+                               const lbk_bell_ternary* gate, const lbk_bell_ternary* up,
+                               const lbk_bell_ternary* down, const uint16_t* x_resid,
+                               uint16_t* out, uint16_t* h_out, int8_t* hq_out, float* sh_out,
+                               const lbk_ternary_acc* acc, void* workspace, size_t workspace_bytes,
+                               void* stream);
+
 /*
  * Backward of the Block-ELL product y = x W^T (bias excluded): dx = grad_out W (tile [B_in, B_out]
  * of slot (r, k) sends grad_out[:, r] back to column block col[r,k]) and, per tile,

@@ -60,14 +60,17 @@ def hipcc() -> str:
 
 
 def build_lib() -> str:
+    from concurrent.futures import ThreadPoolExecutor
+
     objdir = os.path.join(HERE, "_build")
     os.makedirs(objdir, exist_ok=True)
-    objs = []
-    for src in HIP_SOURCES:
-        obj = os.path.join(objdir, src.replace(".hip", ".o"))
-        _run([hipcc(), *HIP_FLAGS, *FILE_FLAGS.get(src, []), f"-I{INCLUDE}", f"-I{CSRC}", "-c",
-              os.path.join(CSRC, src), "-o", obj])
-        objs.append(obj)
+    objs = [os.path.join(objdir, src.replace(".hip", ".o")) for src in HIP_SOURCES]
+    cmds = [[hipcc(), *HIP_FLAGS, *FILE_FLAGS.get(src, []), f"-I{INCLUDE}", f"-I{CSRC}", "-c",
+             os.path.join(CSRC, src), "-o", obj] for src, obj in zip(HIP_SOURCES, objs)]
+    jobs = max(1, min(len(cmds), int(os.environ.get("LBK_BUILD_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(jobs) as pool:
+        for fut in [pool.submit(_run, c) for c in cmds]:
+            fut.result()
     tmp = LIB + ".tmp"
     _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, LIB)

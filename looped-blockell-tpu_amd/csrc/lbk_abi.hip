@@ -386,6 +386,15 @@ int lbk_swiglu_fwd_ternary(const int8_t* xq, const float* sx, int64_t N, int32_t
                            const lbk_bell_ternary* gate, const lbk_bell_ternary* up, const lbk_bell_ternary* down,
                            const uint16_t* x_resid, uint16_t* out, uint16_t* h_out, int8_t* hq_out,
                            float* sh_out, void* workspace, size_t workspace_bytes, void* stream) {
+  return lbk_swiglu_fwd_ternary_acc(xq, sx, N, d_model, gate, up, down, x_resid, out, h_out, hq_out, sh_out, nullptr,
+                                    workspace, workspace_bytes, stream);
+}
+
+int lbk_swiglu_fwd_ternary_acc(const int8_t* xq, const float* sx, int64_t N, int32_t d_model,
+                               const lbk_bell_ternary* gate, const lbk_bell_ternary* up,
+                               const lbk_bell_ternary* down, const uint16_t* x_resid, uint16_t* out,
+                               uint16_t* h_out, int8_t* hq_out, float* sh_out, const lbk_ternary_acc* acc,
+                               void* workspace, size_t workspace_bytes, void* stream) {
   int st;
   if ((st = check_tern(gate)) || (st = check_tern(up)) || (st = check_tern(down))) return st;
   int64_t d_ff = 0;
@@ -394,6 +403,17 @@ int lbk_swiglu_fwd_ternary(const int8_t* xq, const float* sx, int64_t N, int32_t
   if (N == 0) return LBK_OK;
   if (!xq || !sx || !out) return LBK_ERR_NULL;
   if (!a16(xq) || !a16(out)) return LBK_ERR_ALIGN;
+  // the down kernels read the residual with vector loads
+  if (x_resid && !a16(x_resid)) return LBK_ERR_ALIGN;
+  lbk_ternary_acc ax{};
+  if (acc) {
+    ax = *acc;
+    // gate and up accumulators (and pre-activations) come as pairs
+    if (!ax.acc_gate != !ax.acc_up || !ax.gate_pre != !ax.up_pre) return LBK_ERR_NULL;
+    for (const void* p : {(const void*)ax.acc_gate, (const void*)ax.acc_up, (const void*)ax.acc_down,
+                          (const void*)ax.gate_pre, (const void*)ax.up_pre})
+      if (p && !a16(p)) return LBK_ERR_ALIGN;
+  }
   char* ws = static_cast<char*>(workspace);
   hipStream_t s = S(stream);
 
@@ -421,10 +441,11 @@ int lbk_swiglu_fwd_ternary(const int8_t* xq, const float* sx, int64_t N, int32_t
     g.xq = xq; g.sx = sx; g.N = N; g.d_model = d_model;
     g.cg = gate->col_idx; g.cu = up->col_idx; g.K = gate->K;
     g.R_ff = gate->R; g.H = tgu_slices(N); g.h = h; g.hmax = hmax;
+    g.acc_g = ax.acc_gate; g.acc_u = ax.acc_up; g.g_pre = ax.gate_pre; g.u_pre = ax.up_pre;
     if (launch_tgu(g, s) != 0) return LBK_ERR_LAUNCH;
     d.h = h; d.hmax = hmax; d.H = g.H; d.N = N; d.d_ff = (int)d_ff; d.d_model = d_model;
     d.cd = down->col_idx; d.Kd = down->K; d.R_m = down->R; d.C_d = gate->R;
-    d.resid = x_resid; d.out = out; d.hq_out = hq_out; d.sh_out = sh_out;
+    d.resid = x_resid; d.out = out; d.hq_out = hq_out; d.sh_out = sh_out; d.acc_d = ax.acc_down;
     if (launch_tdn(d, s) != 0) return LBK_ERR_LAUNCH;
     return LBK_OK;
   }
@@ -445,12 +466,13 @@ int lbk_swiglu_fwd_ternary(const int8_t* xq, const float* sx, int64_t N, int32_t
   a.p0 = gate->packed; a.s0 = gate->scales; a.c0 = gate->col_idx; a.K0 = gate->K;
   a.p1 = up->packed; a.s1 = up->scales; a.c1 = up->col_idx; a.K1 = up->K;
   a.R = gate->R; a.y = h;
+  a.acc0 = ax.acc_gate; a.acc1 = ax.acc_up; a.pre0 = ax.gate_pre; a.pre1 = ax.up_pre;
   if (launch_ternary(gate->B, 1, a, s) != 0) return LBK_ERR_LAUNCH;
   if (launch_quantize_act(h, N, (int)d_ff, d_ff, hq, sh, s) != 0) return LBK_ERR_LAUNCH;
   TernaryLaunch d{};
   d.xq = hq; d.sx = sh; d.N = N; d.C = gate->R;
   d.p0 = down->packed; d.s0 = down->scales; d.c0 = down->col_idx; d.K0 = down->K;
-  d.R = down->R; d.resid = x_resid; d.y = out;
+  d.R = down->R; d.resid = x_resid; d.y = out; d.acc0 = ax.acc_down;
   if (launch_ternary(gate->B, 0, d, s) != 0) return LBK_ERR_LAUNCH;
   return LBK_OK;
 }

@@ -123,6 +123,9 @@ struct TernaryLaunch {
   const uint16_t* resid;      // [N, R*B] bf16, optional (product mode)
   uint16_t* y;                // [N, R*B] bf16
   int32_t* partials;          // [N, R, K0, B] int32, optional (product mode)
+  // optional accumulators before scaling, [N, R*B]: acc = sum_k m * P of weight 0 (and of
+  // weight 1 in gate/up mode), pre = f32(f32(acc) * 2^-e) * sx
+  int32_t* acc0; int32_t* acc1; float* pre0; float* pre1;
 };
 // mode: 0 = product, 1 = gate/up with SiLU*mul (y = h bf16)
 int launch_ternary(int B, int mode, const TernaryLaunch& a, hipStream_t st);
@@ -138,6 +141,8 @@ struct TGUArgs {
   int H;                    // block-row slices per token block
   uint16_t* h;              // [N, d_ff] bf16
   float* hmax;              // [H, N] max |h| of each slice
+  // optional [N, d_ff]: integer accumulators sum_k m * P and pre-activations f32(f32(acc) * 2^-e) * sx
+  int32_t* acc_g; int32_t* acc_u; float* g_pre; float* u_pre;
 };
 struct TDNArgs {
   const uint16_t* h; const float* hmax; int H; int64_t N; int d_ff; int d_model;
@@ -147,6 +152,7 @@ struct TDNArgs {
   uint16_t* out;            // [N, d_model]
   int8_t* hq_out;           // optional [N, d_ff]
   float* sh_out;            // optional [N]
+  int32_t* acc_d;           // optional [N, d_model]: integer accumulators sum_k m * P
 };
 size_t tprep_bytes(int64_t ntiles, int R);
 struct TPrepWeight {

@@ -233,16 +233,27 @@ __global__ __launch_bounds__(256) void ternary_rowblock_kernel(TernaryLaunch a) 
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       const int64_t oc = (int64_t)r * B + 16 * m + i;
+      const int64_t yo = t * (int64_t)a.R * B + oc;
       float o;
       if constexpr (MODE == 1) {
         const float gv = __fmul_rn(__fmul_rn((float)acc[0][m][v], mult[0]), s_tok);
         const float uv = __fmul_rn(__fmul_rn((float)acc[1][m][v], mult[1]), s_tok);
+        if (a.acc0) {
+          a.acc0[yo] = acc[0][m][v];
+          a.acc1[yo] = acc[1][m][v];
+        }
+        if (a.pre0) {
+          a.pre0[yo] = gv;
+          a.pre1[yo] = uv;
+        }
         o = silu_f(gv) * uv;
       } else {
         o = __fmul_rn(__fmul_rn((float)acc[0][m][v], mult[0]), s_tok);
-        if (a.resid) o += bf2f(a.resid[t * (int64_t)a.R * B + oc]);
+        if (a.acc0) a.acc0[yo] = acc[0][m][v];
+        if (a.pre0) a.pre0[yo] = o;
+        if (a.resid) o += bf2f(a.resid[yo]);
       }
-      a.y[t * (int64_t)a.R * B + oc] = f2bf(o);
+      a.y[yo] = f2bf(o);
     }
   }
 }

@@ -377,6 +377,23 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
           hmax[mt][v >> 1] = __builtin_elementwise_max(hmax[mt][v >> 1],
                                                        (v & 1) ? u16x2{0, tm} : u16x2{tm, 0});
           if (t < a.N) *reinterpret_cast<u32x2*>(a.h + t * d_ff + col0) = u32x2{p01, p23};
+          // optional export of the integer accumulators and the fp32 pre-activations
+          if (a.acc_g && t < a.N) {
+            *reinterpret_cast<i32x4*>(a.acc_g + t * d_ff + col0) =
+                i32x4{ag[mt][0][v], ag[mt][1][v], ag[mt][2][v], ag[mt][3][v]};
+            *reinterpret_cast<i32x4*>(a.acc_u + t * d_ff + col0) =
+                i32x4{au[mt][0][v], au[mt][1][v], au[mt][2][v], au[mt][3][v]};
+          }
+          if (a.g_pre && t < a.N) {
+            float gp[4], up[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              gp[q] = __fmul_rn(__fmul_rn((float)ag[mt][q][v], fg), sxv);
+              up[q] = __fmul_rn(__fmul_rn((float)au[mt][q][v], fu), sxv);
+            }
+            *reinterpret_cast<float4*>(a.g_pre + t * d_ff + col0) = make_float4(gp[0], gp[1], gp[2], gp[3]);
+            *reinterpret_cast<float4*>(a.u_pre + t * d_ff + col0) = make_float4(up[0], up[1], up[2], up[3]);
+          }
         }
     }
   }
@@ -586,6 +603,7 @@ __global__ __launch_bounds__(512, 1) void tdn_kernel(TDNArgs a) {
       if (t >= a.N) continue;
       const float shv = s_sh[4 * g + v];
       const int64_t off = t * a.d_model + (int64_t)rm * 64 + 4 * i;
+      if (a.acc_d) *reinterpret_cast<i32x4*>(a.acc_d + off) = i32x4{acc[0][v], acc[1][v], acc[2][v], acc[3][v]};
       float o[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) o[q] = __fmul_rn(__fmul_rn((float)acc[q][v], fd), shv);

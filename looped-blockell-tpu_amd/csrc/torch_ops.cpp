@@ -315,8 +315,11 @@ std::tuple<at::Tensor, at::Tensor> ternary_matmul(const at::Tensor& xq_, const a
 std::vector<at::Tensor> tern_swiglu_impl(const at::Tensor& xq_, const at::Tensor& sx_, at::Tensor pg, at::Tensor sg,
                                          at::Tensor cg, at::Tensor pu, at::Tensor su, at::Tensor cu, at::Tensor pd,
                                          at::Tensor sd, at::Tensor cd, const c10::optional<at::Tensor>& x_resid,
-                                         bool inter) {
-  const char* op = inter ? "block_ell_swiglu_fwd_ternary_with_intermediate" : "block_ell_swiglu_fwd_ternary";
+                                         bool inter, bool accs = false) {
+  const char* op = accs    ? "block_ell_swiglu_fwd_ternary_accumulators"
+                   : inter ? "block_ell_swiglu_fwd_ternary_with_intermediate"
+                           : "block_ell_swiglu_fwd_ternary";
+  inter = inter || accs;
   at::Tensor xq = check_int8_x(xq_, sx_, op);
   at::Tensor sx = sx_.contiguous();
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(xq.device());
@@ -349,11 +352,23 @@ std::vector<at::Tensor> tern_swiglu_impl(const at::Tensor& xq_, const at::Tensor
     res.push_back(tq);
     res.push_back(ts);
   }
+  lbk_ternary_acc acc{};
+  if (accs) {
+    at::Tensor ag = at::empty({N, d_ff}, xq.options().dtype(at::kInt));
+    at::Tensor au = at::empty({N, d_ff}, xq.options().dtype(at::kInt));
+    at::Tensor ad = at::empty({N, d_model}, xq.options().dtype(at::kInt));
+    at::Tensor gp = at::empty({N, d_ff}, xq.options().dtype(at::kFloat));
+    at::Tensor up = at::empty({N, d_ff}, xq.options().dtype(at::kFloat));
+    acc = lbk_ternary_acc{ag.data_ptr<int32_t>(), au.data_ptr<int32_t>(), ad.data_ptr<int32_t>(),
+                          gp.data_ptr<float>(), up.data_ptr<float>()};
+    for (const at::Tensor& t : {ag, au, ad, gp, up}) res.push_back(t);
+  }
   wsb = lbk_ternary_swiglu_workspace_bytes(N, (int32_t)d_model, &g, &u, &d);
   if (wsb) ws = workspace(wsb, xq);
   LBK_CALL("block_ell_swiglu_fwd_ternary",
-           lbk_swiglu_fwd_ternary(xq.data_ptr<int8_t>(), sx.data_ptr<float>(), N, (int32_t)d_model, &g, &u, &d, xrp,
-                                  bfm(out), h, hq, sh, wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(xq)));
+           lbk_swiglu_fwd_ternary_acc(xq.data_ptr<int8_t>(), sx.data_ptr<float>(), N, (int32_t)d_model, &g, &u, &d,
+                                      xrp, bfm(out), h, hq, sh, accs ? &acc : nullptr,
+                                      wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(xq)));
   return res;
 }
 
@@ -370,6 +385,16 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> tern_swiglu_inter(
     const at::Tensor& cd, const c10::optional<at::Tensor>& x_resid) {
   auto r = tern_swiglu_impl(xq, sx, pg, sg, cg, pu, su, cu, pd, sd, cd, x_resid, true);
   return {r[0], r[1], r[2], r[3]};
+}
+
+// out, h, hq, sh, acc_gate, acc_up, acc_down, gate_pre, up_pre
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor>
+tern_swiglu_accs(const at::Tensor& xq, const at::Tensor& sx, const at::Tensor& pg, const at::Tensor& sg,
+                 const at::Tensor& cg, const at::Tensor& pu, const at::Tensor& su, const at::Tensor& cu,
+                 const at::Tensor& pd, const at::Tensor& sd, const at::Tensor& cd,
+                 const c10::optional<at::Tensor>& x_resid) {
+  auto r = tern_swiglu_impl(xq, sx, pg, sg, cg, pu, su, cu, pd, sd, cd, x_resid, true, true);
+  return {r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7], r[8]};
 }
 
 at::Tensor check_columns(const at::Tensor& c_, int64_t C) {
@@ -472,6 +497,9 @@ TORCH_LIBRARY(titan, m) {
   m.def("block_ell_swiglu_fwd_ternary_with_intermediate(Tensor xq, Tensor sx, Tensor p_gate, Tensor s_gate, "
         "Tensor ci_gate, Tensor p_up, Tensor s_up, Tensor ci_up, Tensor p_down, Tensor s_down, Tensor ci_down, "
         "Tensor? x_resid=None) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("block_ell_swiglu_fwd_ternary_accumulators(Tensor xq, Tensor sx, Tensor p_gate, Tensor s_gate, "
+        "Tensor ci_gate, Tensor p_up, Tensor s_up, Tensor ci_up, Tensor p_down, Tensor s_down, Tensor ci_down, "
+        "Tensor? x_resid=None) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
   m.def("check_columns(Tensor col_indices, int C) -> Tensor");
 }
 
@@ -493,6 +521,7 @@ TORCH_LIBRARY_IMPL(titan, CUDA, m) {
   m.impl("ternary_matmul", &ternary_matmul);
   m.impl("block_ell_swiglu_fwd_ternary", &tern_swiglu);
   m.impl("block_ell_swiglu_fwd_ternary_with_intermediate", &tern_swiglu_inter);
+  m.impl("block_ell_swiglu_fwd_ternary_accumulators", &tern_swiglu_accs);
   m.impl("check_columns", &check_columns);
 }
 
@@ -575,6 +604,18 @@ TORCH_LIBRARY_IMPL(titan, Meta, m) {
                                   at::empty({N, d_ff}, xq.options().dtype(at::kBFloat16)),
                                   at::empty({N, d_ff}, xq.options().dtype(at::kChar)),
                                   at::empty({N}, xq.options().dtype(at::kFloat)));
+         });
+  m.impl("block_ell_swiglu_fwd_ternary_accumulators",
+         [](const at::Tensor& xq, const at::Tensor&, const at::Tensor& pg, const at::Tensor&, const at::Tensor&,
+            const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+            const at::Tensor&, const c10::optional<at::Tensor>&) {
+           const int64_t N = xq.size(0), d_ff = pg.size(0) * pg.size(2);
+           auto o = xq.options();
+           return std::make_tuple(at::empty(xq.sizes(), o.dtype(at::kBFloat16)), at::empty({N, d_ff}, o.dtype(at::kBFloat16)),
+                                  at::empty({N, d_ff}, o.dtype(at::kChar)), at::empty({N}, o.dtype(at::kFloat)),
+                                  at::empty({N, d_ff}, o.dtype(at::kInt)), at::empty({N, d_ff}, o.dtype(at::kInt)),
+                                  at::empty(xq.sizes(), o.dtype(at::kInt)), at::empty({N, d_ff}, o.dtype(at::kFloat)),
+                                  at::empty({N, d_ff}, o.dtype(at::kFloat)));
          });
   m.impl("check_columns", [](const at::Tensor& c, int64_t) { return at::empty({}, c.options()); });
 }

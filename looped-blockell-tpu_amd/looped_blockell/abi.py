@@ -39,6 +39,13 @@ class BellTernary(C.Structure):
                 ("R", C.c_int32), ("K", C.c_int32), ("B", C.c_int32)]
 
 
+class TernaryAcc(C.Structure):
+    """``lbk_ternary_acc``: optional accumulator exports of the ternary SwiGLU (device pointers)."""
+
+    _fields_ = [("acc_gate", C.c_void_p), ("acc_up", C.c_void_p), ("acc_down", C.c_void_p),
+                ("gate_pre", C.c_void_p), ("up_pre", C.c_void_p)]
+
+
 # (name, restype, argtypes) for every entry point of include/lbk.h
 _P = C.c_void_p
 _I64 = C.c_int64
@@ -81,6 +88,8 @@ SIGNATURES = {
     "lbk_ternary_matmul": (C.c_int, [_P, _P, _I64, _I32, _PT, _P, _P, _P]),
     "lbk_ternary_swiglu_workspace_bytes": (_SZ, [_I64, _I32, _PT, _PT, _PT]),
     "lbk_swiglu_fwd_ternary": (C.c_int, [_P, _P, _I64, _I32, _PT, _PT, _PT, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "lbk_swiglu_fwd_ternary_acc": (C.c_int, [_P, _P, _I64, _I32, _PT, _PT, _PT, _P, _P, _P, _P, _P,
+                                             C.POINTER(TernaryAcc), _P, _SZ, _P]),
 }
 
 _lib = None

@@ -221,3 +221,15 @@ def ternary_swiglu_fwd_with_intermediate(xq, sx, gate, up, down, x_resid=None):
     """Returns (out, h bf16, hq int8, sh fp32)."""
     _gpu(xq)
     return ops().block_ell_swiglu_fwd_ternary_with_intermediate(xq, sx, *gate, *up, *down, x_resid)
+
+
+def ternary_swiglu_fwd_accumulators(xq, sx, gate, up, down, x_resid=None):
+    """The ternary SwiGLU with its accumulators before scaling exported.
+
+    Returns ``(out, h, hq, sh, acc_gate, acc_up, acc_down, gate_pre, up_pre)``: the int32
+    ``sum_k m[r,k] * P`` of the gate and up products ([N, d_ff]) and of the down product
+    ([N, d_model]), and the fp32 pre-activations ``f32(f32(acc) * 2^-e) * sx`` that enter
+    ``silu(g) * u`` — the integer accumulate-then-scale of BitLinear
+    (reference ``bonsai-test/bitlinear.py:34-69``) with one scale per block."""
+    _gpu(xq)
+    return ops().block_ell_swiglu_fwd_ternary_accumulators(xq, sx, *gate, *up, *down, x_resid)

@@ -32,6 +32,31 @@ def tern_weight(rng, R, C_, K, B, sentinel_frac=0.0):
     return t, s, col
 
 
+def check_accumulators(res, xq, sx, g, u, d, rows=None):
+    """Bit-exact checks of the exported accumulators of ternary_swiglu_fwd_accumulators: the int32
+    sums sum_k m*P of gate and up given xq, their fp32 pre-activations, the down sums given the
+    kernel's own hq; h within TOL of silu(g)*u.  Only ``rows`` are copied back when given."""
+    import torch
+    if rows is not None:
+        idx = torch.as_tensor(rows, device=res[0].device)
+        res = [t[idx] for t in res]
+    out, h, hq, sh, ag, au, ad, gp, up = (T.to_np(t) for t in res)
+    n = xq.shape[0]
+    gf, acc_g = O.ternary_matmul(xq, sx, *g, exact_scales=False)
+    uf, acc_u = O.ternary_matmul(xq, sx, *u, exact_scales=False)
+    assert np.array_equal(ag, acc_g.reshape(n, -1)), "gate int32 accumulators"
+    assert np.array_equal(au, acc_u.reshape(n, -1)), "up int32 accumulators"
+    assert np.array_equal(gp.view(np.uint32), gf.astype(np.float32).view(np.uint32)), "gate pre-activations"
+    assert np.array_equal(up.view(np.uint32), uf.astype(np.float32).view(np.uint32)), "up pre-activations"
+    assert np.abs(acc_g).max() > 0 and np.abs(acc_u).max() > 0
+    yd, acc_d = O.ternary_matmul(hq, sh, *d, exact_scales=False)
+    assert np.array_equal(ad, acc_d.reshape(n, -1)), "down int32 accumulators"
+    # h = silu(g) * u from the kernel's own (bit-exact) pre-activations, device exp / rcp
+    href = O.bf16_round(O.silu(gp.astype(np.float64)) * up)
+    assert T.rel_err(h, href)[0] <= TOL
+    return out, h, hq, sh, yd
+
+
 def gpu_tern(w):
     import torch
     t, s, col = w
@@ -133,9 +158,9 @@ def test_ternary_swiglu(gpu, case, resid):
     x = T.act(rng, N, d_model)
     xq, sx = O.activation_quantize_int8(x)
     xg = T.to_gpu_bf16(x)
-    out, h, hq, sh = kernels.ternary_swiglu_fwd_with_intermediate(
+    res = kernels.ternary_swiglu_fwd_accumulators(
         T.to_gpu(xq), T.to_gpu(sx), gpu_tern(g), gpu_tern(u), gpu_tern(d), xg if resid else None)
-    out, h, hq, sh = T.to_np(out), T.to_np(h), T.to_np(hq), T.to_np(sh)
+    out, h, hq, sh, _ = check_accumulators(res, xq, sx, g, u, d)
     # h re-quantisation is bit-exact given the kernel's h
     hq_ref, sh_ref = O.activation_quantize_int8(h)
     assert np.array_equal(hq, hq_ref) and np.array_equal(sh, sh_ref)
@@ -188,6 +213,10 @@ def test_ternary_swiglu_split(gpu, case):
     out_ws = kernels.ternary_swiglu_fwd(*args)
     out, h, hq, sh, out_ws = T.to_np(out), T.to_np(h), T.to_np(hq), T.to_np(sh), T.to_np(out_ws)
     assert np.array_equal(out, out_ws)
+    # the same kernels with the accumulator exports: identical outputs, bit-exact accumulators
+    res = kernels.ternary_swiglu_fwd_accumulators(*args)
+    out_a, h_a, hq_a, sh_a, _ = check_accumulators(res, xq, sx, g, u, d)
+    assert np.array_equal(out_a, out) and np.array_equal(h_a, h) and np.array_equal(hq_a, hq)
     hq_ref, sh_ref = O.activation_quantize_int8(h)
     assert np.array_equal(hq, hq_ref) and np.array_equal(sh, sh_ref)
     gf, _ = O.ternary_matmul(xq, sx, *g, exact_scales=False)
@@ -240,13 +269,18 @@ def test_ternary_full_size_sampled_rows(gpu):
     x = T.act(rng, N, d_model)
     xg = T.to_gpu_bf16(x)
     xq_t, sx_t = kernels.quantize_act_int8(xg)
-    out, h, hq, sh = kernels.ternary_swiglu_fwd_with_intermediate(xq_t, sx_t, gpu_tern(g), gpu_tern(u),
-                                                                  gpu_tern(d))
+    res = kernels.ternary_swiglu_fwd_accumulators(xq_t, sx_t, gpu_tern(g), gpu_tern(u), gpu_tern(d))
+    out_plain = kernels.ternary_swiglu_fwd(xq_t, sx_t, gpu_tern(g), gpu_tern(u), gpu_tern(d))
+    import torch
+    assert torch.equal(out_plain, res[0])
     rows = np.sort(rng.choice(N, 256, replace=False))
     xq, sx = O.activation_quantize_int8(x[rows])
     assert np.array_equal(T.to_np(xq_t)[rows], xq) and np.array_equal(T.to_np(sx_t)[rows], sx)
-    hq_r, sh_r = T.to_np(hq)[rows], T.to_np(sh)[rows]
-    yd, _ = O.ternary_matmul(hq_r, sh_r, *d, exact_scales=False)
-    assert np.array_equal(T.to_np(out)[rows], O.bf16_round(yd))
+    # int32 accumulators of gate, up (given xq) and down (given the kernel's hq) bit-exact, the fp32
+    # pre-activations bit-exact, on the sampled rows
+    out, h, hq_r, sh_r, yd = check_accumulators(res, xq, sx, g, u, d, rows=rows)
+    assert np.array_equal(out, O.bf16_round(yd))
+    hq_ref, sh_ref = O.activation_quantize_int8(h)
+    assert np.array_equal(hq_r, hq_ref) and np.array_equal(sh_r, sh_ref)
     ref = O.ternary_swiglu_fwd(x[rows], g, u, d, exact_scales=True, h_round=O.bf16_round)
-    assert T.rel_err(T.to_np(out)[rows], ref["out"])[0] <= TOL
+    assert T.rel_err(out, ref["out"])[0] <= TOL
