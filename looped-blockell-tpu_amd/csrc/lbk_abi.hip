@@ -192,7 +192,8 @@ static int swiglu_split(const uint16_t* x, const float* xf, const float* norm_sc
 static constexpr int64_t kDecodeMaxTokens = 16;
 
 static bool use_decode(int64_t N, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, bool inter) {
-  return !inter && N <= kDecodeMaxTokens && decode_supported(gate->K, up->K, down->K);
+  // the decode kernels read down tiles (and the prefetch reads them) with 16-byte loads
+  return !inter && N <= kDecodeMaxTokens && decode_supported(gate->K, up->K, down->K) && a16(down->values);
 }
 
 size_t lbk_swiglu_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,

@@ -61,7 +61,75 @@ __device__ __forceinline__ void load_a_rows(const uint16_t* base, int64_t ld, in
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// gate/up: h row block r = blockIdx.x
+// down-tile prefetch share of a gate/up workgroup
+// ---------------------------------------------------------------------------
+// The down kernel's workgroups for down row rm run on XCD rm % 8 (see decode_dn_kernel).
+// The gate/up launch has 8 * S workgroups, S on each XCD (workgroup b on XCD b % 8); those
+// of XCD x read the tiles of the down rows rm = x (mod 8) once, so that the down kernel
+// finds them in the memory-side cache (and in the XCD's L2 where it is kept), and the
+// down weights stream from HBM while the gate/up phase runs.  Work is balanced in tiles:
+// a workgroup with a gate/up row (Kg + Ku tiles) takes fewer down tiles than one without.
+// Returns the XOR of what was read (consumed by the caller so the loads stay).
+template <int B, int PF>
+__device__ __forceinline__ uint32_t prefetch_down_share(const DecodeArgs& a, int b, int S, int tid) {
+  constexpr int CPT = B * B / 8;          // 16-byte chunks per tile
+  constexpr int TPR = 512 / CPT;          // tiles covered by one 512-thread round
+  const int x = b & 7, s = b >> 3;
+  const int n_gu = a.R_ff > x ? min(S, (a.R_ff - x + 7) / 8) : 0;
+  const int rows_x = a.R_m > x ? (a.R_m - x + 7) / 8 : 0;
+  const int D = rows_x * a.Kd;                                  // down tiles read on this XCD
+  const int gu_t = a.Kg + a.Ku;
+  const int T = (n_gu * gu_t + D + S - 1) / S;                 // tiles per workgroup
+  const int cg = T > gu_t ? T - gu_t : 0;                       // down share of a gate/up workgroup
+  const int j0 = s < n_gu ? s * cg : n_gu * cg + (s - n_gu) * T;
+  const int j1 = min(D, j0 + (s < n_gu ? cg : T));
+  const bool any = j1 > j0;
+  // the last workgroup of the XCD also reads the column indices of the XCD's down rows (first,
+  // so that nothing waits for it behind the tiles)
+  int cv = 0;
+  if (s == S - 1 && tid < D) {
+    const int rr = tid / a.Kd;
+    cv = a.cd[(int64_t)(x + 8 * rr) * a.Kd + (tid - rr * a.Kd)];
+  }
+  // PF rounds, all requested before any is consumed and none under a branch (a share shorter
+  // than PF re-reads its last tile, an empty one tile 0; a longer one is left to the down
+  // kernel's own loads: this is only a prefetch)
+  const int jt = tid / CPT, ch = tid % CPT;
+  u32x4 v[PF];
+  if constexpr (TPR == 1) {
+    // one tile per round, a uniform walk over (row, slot) with no division inside
+    int rr = any ? j0 / a.Kd : 0;
+    int kk = any ? j0 - rr * a.Kd : 0;
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int64_t e = any ? (int64_t)(x + 8 * rr) * a.Kd + kk : 0;
+      v[u] = *reinterpret_cast<const u32x4*>(a.vd + e * B * B + 8 * ch);
+      const bool adv = j0 + u + 1 < j1;
+      const int kn = kk + 1 == a.Kd ? 0 : kk + 1;
+      rr = adv && kn == 0 ? rr + 1 : rr;
+      kk = adv ? kn : kk;
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      int j = j0 + TPR * u + jt;
+      j = j < j1 ? j : j1 - 1;
+      const int rr = any ? j / a.Kd : 0;
+      const int64_t e = any ? (int64_t)(x + 8 * rr) * a.Kd + (j - rr * a.Kd) : 0;
+      v[u] = *reinterpret_cast<const u32x4*>(a.vd + e * B * B + 8 * ch);
+    }
+  }
+  uint32_t acc = (uint32_t)cv;
+#pragma unroll
+  for (int u = 0; u < PF; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+  return acc;
+}
+
+// workgroups of the gate/up launch per XCD: at least one per CU, a multiple of the 8 XCDs
+__host__ __device__ inline int decode_gu_per_xcd(int R_ff) { return ((R_ff > 256 ? R_ff : 256) + 7) / 8; }
+
+// ---------------------------------------------------------------------------
+// gate/up: h row block r = blockIdx.x (workgroups r >= R_ff only prefetch)
 // ---------------------------------------------------------------------------
 template <int B>
 __global__ __launch_bounds__(512, 1) void decode_gu_kernel(DecodeArgs a) {
@@ -73,6 +141,11 @@ __global__ __launch_bounds__(512, 1) void decode_gu_kernel(DecodeArgs a) {
   const int w = uniform(tid >> 6);
   const int i = lane & 15, g = lane >> 4;
   const int r = (int)blockIdx.x;
+  if (r >= a.R_ff) {
+    const uint32_t pf = prefetch_down_share<B, 16>(a, r, decode_gu_per_xcd(a.R_ff), tid);
+    if (pf == 0x9e3779b9u && a.N < 0) a.h[0] = 0;               // never true: keeps the loads
+    return;
+  }
   const int C_in = a.d_model / B;
   const int64_t d_ff = (int64_t)a.R_ff * B;
   // waves 0-3: gate slots k = (w & 3) + 4j, waves 4-7: up slots, j < 2.  The same loads in
@@ -84,12 +157,20 @@ __global__ __launch_bounds__(512, 1) void decode_gu_kernel(DecodeArgs a) {
   const int k0 = w & 3, k1 = k0 + 4;
   const bool use0 = k0 < Km, use1 = k1 < Km;
   const int64_t e0 = (int64_t)r * Km + (use0 ? k0 : 0), e1 = (int64_t)r * Km + (use1 ? k1 : 0);
-  const int c0 = use0 ? cm[e0] : -1, c1 = use1 ? cm[e1] : -1;
-  const bool ok0 = c0 >= 0 && c0 < C_in, ok1 = c1 >= 0 && c1 < C_in;
+  // Request order (a wave's loads return in order): the two column indices (one vector
+  // load), this workgroup's tiles (their addresses need no index), its share of the down
+  // tiles, then the x fragments the indices select.
+  const int cl = cm[lane == 1 ? e1 : e0];
+  asm volatile("" ::: "memory");
   WRaw<B> t0, t1;
   u32x4 a0[NKS], a1[NKS];
   load_wraw<B>(vm + e0 * B * B, lane, t0);
   load_wraw<B>(vm + e1 * B * B, lane, t1);
+  asm volatile("" ::: "memory");
+  const uint32_t pf = prefetch_down_share<B, 4>(a, r, decode_gu_per_xcd(a.R_ff), tid);
+  asm volatile("" ::: "memory");
+  const int c0 = use0 ? __builtin_amdgcn_readlane(cl, 0) : -1, c1 = use1 ? __builtin_amdgcn_readlane(cl, 1) : -1;
+  const bool ok0 = c0 >= 0 && c0 < C_in, ok1 = c1 >= 0 && c1 < C_in;
   load_a_rows<B>(a.x + (int64_t)(ok0 ? c0 : 0) * B, a.d_model, ok0 ? a.N : 0, i, g, a0);
   load_a_rows<B>(a.x + (int64_t)(ok1 ? c1 : 0) * B, a.d_model, ok1 ? a.N : 0, i, g, a1);
   f32x4 acc[CW];
@@ -115,6 +196,7 @@ __global__ __launch_bounds__(512, 1) void decode_gu_kernel(DecodeArgs a) {
       if (tk < a.N) a.h[(int64_t)tk * d_ff + col] = f2bf(silu_f(gs[v]) * us[v]);
     }
   }
+  if (pf == 0x9e3779b9u && a.N < 0) a.h[0] = 0;                 // never true: keeps the loads
 }
 
 // ---------------------------------------------------------------------------
@@ -141,19 +223,28 @@ __global__ __launch_bounds__(512, 1) void decode_dn_kernel(DecodeArgs a) {
   const int drow = lane >> 1;
   u32x4 dq[DEC_DS][NKS], av[DEC_DS][NKS];
   int dc[DEC_DS];
+  // Request order (a wave's loads return in order): the column indices (one vector load, lane
+  // j holding slot w + 8j's), the tiles, whose addresses need no index, then the h fragments
+  // the indices select, issued as soon as the indices are back.
+  const int kl = w + 8 * (lane < DEC_DS ? lane : 0);
+  const int cl = a.cd[(int64_t)rm * a.Kd + (kl < a.Kd ? kl : 0)];
+  asm volatile("" ::: "memory");
 #pragma unroll
   for (int j = 0; j < DEC_DS; ++j) {
     const int k = w + 8 * j;
-    const bool live = k < a.Kd;
-    const int64_t e = (int64_t)rm * a.Kd + (live ? k : 0);
-    const int c = live ? a.cd[e] : -1;
-    dc[j] = (c >= 0 && c < a.R_ff) ? c : -1;
+    const int64_t e = (int64_t)rm * a.Kd + (k < a.Kd ? k : 0);
     const uint16_t* tile = a.vd + e * B * B + 16 * q + 8 * (lane & 1);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
       const int row = 32 * ks + drow;
       dq[j][ks] = *reinterpret_cast<const u32x4*>(tile + (int64_t)(row < B ? row : 0) * B);
     }
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int j = 0; j < DEC_DS; ++j) {
+    const int c = (w + 8 * j < a.Kd) ? __builtin_amdgcn_readlane(cl, j) : -1;
+    dc[j] = (c >= 0 && c < a.R_ff) ? c : -1;
     load_a_rows<B>(a.h + (int64_t)(dc[j] >= 0 ? dc[j] : 0) * B, d_ff, dc[j] >= 0 ? a.N : 0, i, g, av[j]);
   }
   // each (tile, k-step) of 32 rows x 16 columns goes through this wave's LDS buffer to become
@@ -206,7 +297,8 @@ bool decode_supported(int Kg, int Ku, int Kd) {
 int launch_decode(int B, const DecodeArgs& a, hipStream_t st) {
   if (a.N == 0) return 0;
   if (!decode_supported(a.Kg, a.Ku, a.Kd) || a.R_ff <= 0 || a.R_m <= 0) return -2;
-  const unsigned g1 = (unsigned)a.R_ff, g2 = 8u * (unsigned)(B / 16) * (unsigned)((a.R_m + 7) / 8);
+  const unsigned g1 = 8u * (unsigned)decode_gu_per_xcd(a.R_ff);
+  const unsigned g2 = 8u * (unsigned)(B / 16) * (unsigned)((a.R_m + 7) / 8);
   switch (B) {
     case 16:
       hipLaunchKernelGGL(decode_gu_kernel<16>, dim3(g1), dim3(512), 0, st, a);
