@@ -171,6 +171,26 @@ int lbk_looped_swiglu_bf16(const uint16_t* h_in, int64_t N, int32_t d_model,
                            void* stream);
 
 /*
+ * The looped block of lbk_looped_swiglu_bf16 in one persistent launch (after the weight
+ * packing): workgroup b owns token block b (64 tokens) for all L iterations, so nothing is
+ * exchanged between workgroups and no grid-wide barrier is needed.  Per iteration it
+ * RMS-normalises its fp32 state rows into an LDS panel, runs the gate/up tiles (h of its
+ * tokens to the workspace), then the down tiles with h staged back through LDS, and adds the
+ * result to its state.  Same workspace (lbk_looped_workspace_bytes) and same results as the
+ * two-kernel path of lbk_looped_swiglu_bf16 (the same tiles, summed in the same order).
+ * Takes B in {16, 32}, d_model a multiple of 128 and at most 1024, gate and up with the same
+ * K, K_down <= 63 and a 16-byte aligned norm_scale; LBK_ERR_SHAPE otherwise.
+ * Replaces the persistent core loop of the reference's design notes
+ * (Ai-notes/05-02-2026/CUDA-Kernel-Spec/spec.md:184-243: "persistent_core_loop", MLP path
+ * only) over the host loop of persistent_mlp_step (csrc/loop/persistent_core.cu:315-335).
+ */
+int lbk_looped_swiglu_persistent_bf16(const uint16_t* h_in, int64_t N, int32_t d_model,
+                                      const float* norm_scale, float eps, int32_t L,
+                                      const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                                      uint16_t* h_out, void* workspace, size_t workspace_bytes,
+                                      void* stream);
+
+/*
  * Per-token absmax int8 quantisation of bf16 activations:
  *   absmax = max(max|x|, 1e-8); q = clamp(rint(x * (128/absmax)), -128, 127);
  *   sx = absmax / 128 (the dequantisation multiplier).

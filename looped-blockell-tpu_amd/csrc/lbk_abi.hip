@@ -330,6 +330,48 @@ int lbk_looped_swiglu_bf16(const uint16_t* h_in, int64_t N, int32_t d_model, con
   return LBK_OK;
 }
 
+int lbk_looped_swiglu_persistent_bf16(const uint16_t* h_in, int64_t N, int32_t d_model, const float* norm_scale,
+                                      float eps, int32_t L, const lbk_bell* gate, const lbk_bell* up,
+                                      const lbk_bell* down, uint16_t* h_out, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  int st;
+  if ((st = check_bell(gate)) || (st = check_bell(up)) || (st = check_bell(down))) return st;
+  int64_t d_ff = 0;
+  if ((st = check_ffn(gate, up, down, d_model, &d_ff))) return st;
+  if (N < 0 || L < 0 || !(eps >= 0.f)) return LBK_ERR_ARG;
+  if (!looped_persistent_supported(gate->B, d_model, gate->R, down->R, gate->K, up->K, down->K)) return LBK_ERR_SHAPE;
+  if (N == 0) return LBK_OK;
+  if (!h_in || !h_out || !norm_scale) return LBK_ERR_NULL;
+  if (!a16(h_in) || !a16(h_out) || !a16(norm_scale)) return LBK_ERR_ALIGN;
+  hipStream_t s = S(stream);
+  if (L == 0) {
+    if (h_out != h_in &&
+        hipMemcpyAsync(h_out, h_in, (size_t)N * d_model * 2, hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return LBK_ERR_LAUNCH;
+    return LBK_OK;
+  }
+  const size_t sbytes = align256((size_t)N * d_model * 4), hbytes = align256((size_t)N * d_ff * 2);
+  const size_t pbytes = packed_ffn_bytes(gate, up, down);
+  if (!workspace || workspace_bytes < sbytes + hbytes + pbytes) return LBK_ERR_WORKSPACE;
+  if (!a16(workspace)) return LBK_ERR_ALIGN;
+  char* ws = static_cast<char*>(workspace);
+  float* state = reinterpret_cast<float*>(ws);
+  uint16_t* h = reinterpret_cast<uint16_t*>(ws + sbytes);
+  PackedFFN pk{};
+  if ((st = pack_ffn(gate, up, down, ws + sbytes + hbytes, &pk, s))) return st;
+  LoopArgs la{};
+  la.gu.xf = state; la.gu.N = N; la.gu.d_model = d_model; la.gu.norm_scale = norm_scale; la.gu.eps = eps;
+  la.gu.pg = pk.g; la.gu.cg = gate->col_idx; la.gu.Kg = gate->K;
+  la.gu.pu = pk.u; la.gu.cu = up->col_idx; la.gu.Ku = up->K;
+  la.gu.R_ff = gate->R; la.gu.h = h;
+  la.dn.h = h; la.dn.N = N; la.dn.d_ff = d_ff; la.dn.d_model = d_model;
+  la.dn.pd = pk.d; la.dn.cd = down->col_idx; la.dn.Kd = down->K;
+  la.dn.R_m = down->R; la.dn.C_d = gate->R; la.dn.state = state; la.dn.out = h_out;
+  la.h_in = h_in; la.L = L;
+  // h_out may alias h_in: the kernel reads a token block's h_in rows before any write to them
+  return launch_looped(gate->B, la, s) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
 int lbk_quantize_act_int8(const uint16_t* x, int64_t N, int32_t F, int64_t ldx, int8_t* xq, float* sx,
                           void* stream) {
   if (N < 0 || F <= 0 || ldx < F) return LBK_ERR_ARG;

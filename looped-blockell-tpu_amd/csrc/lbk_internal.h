@@ -85,6 +85,16 @@ struct DNArgs {
   int nrg;                  // row groups per token block (set by the launcher)
 };
 bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd);
+// looped block in one launch: gate/up (RMSNorm of the fp32 state) and down per token block
+// for all L iterations; gu.xf == dn.state == the fp32 state, gu.h == dn.h
+struct LoopArgs {
+  GUArgs gu;
+  DNArgs dn;                 // dn.out: bf16 result, written by the last iteration
+  const uint16_t* h_in;      // [N, d_model] bf16 initial state
+  int L;
+};
+bool looped_persistent_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd);
+int launch_looped(int B, const LoopArgs& a, hipStream_t st);
 int launch_gu(int B, bool norm, const GUArgs& a, hipStream_t st);
 int launch_dn(int B, const DNArgs& a, hipStream_t st);
 int launch_bf16_to_f32(const uint16_t* x, int64_t n, float* y, hipStream_t st);

@@ -202,7 +202,8 @@ at::Tensor diagonal_injection(const at::Tensor& h_, const at::Tensor& e_, const 
 }
 
 at::Tensor looped_impl(const at::Tensor& h, const at::Tensor& scale_, at::Tensor vg, at::Tensor cg, at::Tensor vu,
-                       at::Tensor cu, at::Tensor vd, at::Tensor cd, int64_t L, double eps, const char* op) {
+                       at::Tensor cu, at::Tensor vd, at::Tensor cd, int64_t L, double eps, const char* op,
+                       bool persistent = false) {
   at::Tensor x = check_x2d(h, op);
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
   lbk_bell g = make_bell(vg, cg, op, "gate"), u = make_bell(vu, cu, op, "up"), d = make_bell(vd, cd, op, "down");
@@ -212,10 +213,16 @@ at::Tensor looped_impl(const at::Tensor& h, const at::Tensor& scale_, at::Tensor
   at::Tensor out = at::empty_like(x);
   const size_t wsb = lbk_looped_workspace_bytes(x.size(0), (int32_t)x.size(1), &g, &u, &d);
   at::Tensor ws = wsb ? workspace(wsb, x) : at::Tensor();
-  LBK_CALL("looped_swiglu", lbk_looped_swiglu_bf16(bf(x), x.size(0), (int32_t)x.size(1), s.data_ptr<float>(),
-                                                   (float)eps, (int32_t)L, &g, &u, &d, bfm(out),
-                                                   wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(x)));
+  auto fn = persistent ? lbk_looped_swiglu_persistent_bf16 : lbk_looped_swiglu_bf16;
+  LBK_CALL("looped_swiglu", fn(bf(x), x.size(0), (int32_t)x.size(1), s.data_ptr<float>(), (float)eps, (int32_t)L,
+                               &g, &u, &d, bfm(out), wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(x)));
   return out;
+}
+
+at::Tensor looped_swiglu_persistent(const at::Tensor& h, const at::Tensor& scale, const at::Tensor& vg,
+                                    const at::Tensor& cg, const at::Tensor& vu, const at::Tensor& cu,
+                                    const at::Tensor& vd, const at::Tensor& cd, int64_t L, double eps) {
+  return looped_impl(h, scale, vg, cg, vu, cu, vd, cd, L, eps, "looped_swiglu_persistent", true);
 }
 
 at::Tensor looped_swiglu(const at::Tensor& h, const at::Tensor& scale, const at::Tensor& vg, const at::Tensor& cg,
@@ -484,6 +491,8 @@ TORCH_LIBRARY(titan, m) {
         "bool add_residual) -> (Tensor, Tensor, Tensor, Tensor)");
   m.def("looped_swiglu(Tensor h, Tensor norm_scale, Tensor v_gate, Tensor ci_gate, Tensor v_up, Tensor ci_up, "
         "Tensor v_down, Tensor ci_down, int L, float eps=1e-05) -> Tensor");
+  m.def("looped_swiglu_persistent(Tensor h, Tensor norm_scale, Tensor v_gate, Tensor ci_gate, Tensor v_up, "
+        "Tensor ci_up, Tensor v_down, Tensor ci_down, int L, float eps=1e-05) -> Tensor");
   m.def("rmsnorm(Tensor x, Tensor scale, float eps=1e-05) -> Tensor");
   m.def("diagonal_injection(Tensor h, Tensor e, Tensor log_A, Tensor log_dt) -> Tensor");
   m.def("quantize_act_int8(Tensor x) -> (Tensor, Tensor)");
@@ -513,6 +522,7 @@ TORCH_LIBRARY_IMPL(titan, CUDA, m) {
   m.impl("block_ell_matmul", &block_ell_matmul);
   m.impl("block_ell_matmul_bwd", &block_ell_matmul_bwd);
   m.impl("looped_swiglu", &looped_swiglu);
+  m.impl("looped_swiglu_persistent", &looped_swiglu_persistent);
   m.impl("rmsnorm", &rmsnorm);
   m.impl("diagonal_injection", &diagonal_injection);
   m.impl("quantize_act_int8", &quantize_act_int8);
@@ -566,6 +576,9 @@ TORCH_LIBRARY_IMPL(titan, Meta, m) {
     return std::make_tuple(at::empty_like(x), at::empty_like(v));
   });
   m.impl("looped_swiglu", [](const at::Tensor& h, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+                             const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t,
+                             double) { return at::empty_like(h); });
+  m.impl("looped_swiglu_persistent", [](const at::Tensor& h, const at::Tensor&, const at::Tensor&, const at::Tensor&,
                              const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t,
                              double) { return at::empty_like(h); });
   m.impl("rmsnorm", [](const at::Tensor& x, const at::Tensor&, double) { return at::empty_like(x); });

@@ -154,6 +154,14 @@ def looped_swiglu(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, 
     return ops().looped_swiglu(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L, eps)
 
 
+def looped_swiglu_persistent(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L: int,
+                             eps: float = 1e-5):
+    """``looped_swiglu`` in one persistent launch: each workgroup owns a 64-token block for all L
+    iterations (same tiles, same summation order, same result as the two-kernel path)."""
+    _gpu(h, v_gate, v_down)
+    return ops().looped_swiglu_persistent(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L, eps)
+
+
 def rmsnorm(x, scale, eps: float = 1e-5):
     _gpu(x)
     return ops().rmsnorm(x, scale, eps)

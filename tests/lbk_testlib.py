@@ -139,18 +139,20 @@ def abi_swiglu(x_t, g_t, u_t, d_t, add_residual=False, intermediates=False):
     return out, h, gp, uo
 
 
-def abi_looped(h_t, scale_t, g_t, u_t, d_t, L, eps):
+def abi_looped(h_t, scale_t, g_t, u_t, d_t, L, eps, persistent=False, out=None):
+    """The looped block through the C ABI: lbk_looped_swiglu_bf16, or with persistent=True the
+    one-launch lbk_looped_swiglu_persistent_bf16 (same workspace)."""
     import torch
     A = abi()
     lib = A.load()
     N, dm = h_t.shape
     gb, ub, db = bell_struct(*g_t), bell_struct(*u_t), bell_struct(*d_t)
-    out = torch.empty_like(h_t)
+    out = torch.empty_like(h_t) if out is None else out
     wsb = lib.lbk_looped_workspace_bytes(N, dm, C.byref(gb), C.byref(ub), C.byref(db))
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=h_t.device)
-    A.check(lib.lbk_looped_swiglu_bf16(ptr(h_t), N, dm, ptr(scale_t), C.c_float(eps), L, C.byref(gb), C.byref(ub),
-                                       C.byref(db), ptr(out), ptr(ws) if wsb else C.c_void_p(0), wsb, stream()),
-            "looped")
+    fn = lib.lbk_looped_swiglu_persistent_bf16 if persistent else lib.lbk_looped_swiglu_bf16
+    A.check(fn(ptr(h_t), N, dm, ptr(scale_t), C.c_float(eps), L, C.byref(gb), C.byref(ub), C.byref(db), ptr(out),
+               ptr(ws) if wsb else C.c_void_p(0), wsb, stream()), "looped_persistent" if persistent else "looped")
     return out
 
 

@@ -284,6 +284,77 @@ def test_looped_full_size_sampled_rows(gpu):
     assert rel <= TOL, f"rel {rel} abs {ab}"
 
 
+PERSISTENT_CASES = [
+    # (d_model, d_ff, B, density, N, L, shared gate/up topology)
+    (256, 1024, 16, 0.25, 100, 3, False),
+    (1024, 4096, 32, 0.25, 130, 8, False),      # the looped-block geometry, ragged token tail
+    (1024, 4096, 32, 0.25, 64, 2, True),
+    (512, 2048, 32, 0.5, 1, 1, False),
+    (384, 1536, 32, 0.25, 200, 4, False),       # 12 down rows: a partial row group
+]
+
+
+@pytest.mark.parametrize("case", PERSISTENT_CASES)
+def test_looped_persistent_matches_two_kernel_path(gpu, case):
+    """The one-launch persistent looped block runs the same tiles in the same order as the
+    per-iteration gate/up + down launches: bit-identical outputs; both within TOL of the oracle."""
+    d_model, d_ff, B, dens, N, L, shared = case
+    _say(f"looped persistent {case}")
+    rng = np.random.default_rng(abs(hash(case)) % 2 ** 31)
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, dens, sentinel_frac=0.05)
+    if shared:
+        u = (u[0], g[1].copy())
+    h = T.act(rng, N, d_model)
+    scale = (1.0 + 0.1 * rng.standard_normal(d_model)).astype(np.float32)
+    ws = [T.gpu_weight(w) for w in (g, u, d)]
+    if shared:
+        ws[1] = (ws[1][0], ws[0][1])   # one index buffer: the shared-topology kernels
+    ht, st = T.to_gpu_bf16(h), T.to_gpu(scale)
+    two = T.to_np(T.abi_looped(ht, st, *ws, L, 1e-5))
+    one = T.to_np(T.abi_looped(ht, st, *ws, L, 1e-5, persistent=True))
+    assert np.array_equal(one, two)
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref = O.looped_swiglu(h.astype(np.float64), scale.astype(np.float64), f64(g), f64(u), f64(d), L=L, eps=1e-5)
+    rel, ab = T.rel_err(one, ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
+def test_looped_persistent_full_size_and_in_place(gpu):
+    """The persistent looped block at full size (32 x 512 tokens, L = 8) on sampled rows, and
+    called in place (h_out = h_in)."""
+    import torch
+    rng = np.random.default_rng(1004)
+    d_model, d_ff, B, N, L = 1024, 4096, 32, 32 * 512, 8
+    _say("looped persistent L8 d1024 ff4096 B32 N16384 full size")
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25)
+    h = T.act(rng, N, d_model)
+    scale = np.ones(d_model, np.float32)
+    ws = [T.gpu_weight(w) for w in (g, u, d)]
+    ht, st = T.to_gpu_bf16(h), T.to_gpu(scale)
+    two = T.abi_looped(ht, st, *ws, L, 1e-5)
+    inplace = ht.clone()
+    T.abi_looped(inplace, st, *ws, L, 1e-5, persistent=True, out=inplace)
+    assert torch.equal(inplace, two)
+    rows = np.sort(rng.choice(N, 128, replace=False))
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref = O.looped_swiglu(h[rows].astype(np.float64), scale.astype(np.float64), f64(g), f64(u), f64(d), L=L)
+    rel, ab = T.rel_err(T.to_np(inplace)[rows], ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
+def test_looped_persistent_rejects_other_shapes(gpu):
+    """Shapes outside the persistent kernel's (B = 64, d_model > 1024) are refused, not run."""
+    import ctypes
+    A = T.abi()
+    rng = np.random.default_rng(5)
+    for (dm, dff, B) in [(128, 512, 64), (2048, 2048, 32)]:
+        g, u, d = T.ffn_weights(rng, dm, dff, B, 0.25)
+        ws = [T.gpu_weight(w) for w in (g, u, d)]
+        with pytest.raises(RuntimeError, match="inconsistent shapes"):
+            T.abi_looped(T.to_gpu_bf16(T.act(rng, 8, dm)), T.to_gpu(np.ones(dm, np.float32)), *ws, 2, 1e-5,
+                         persistent=True)
+
+
 def test_looped_L0_and_L1(gpu):
     rng = np.random.default_rng(9)
     g, u, d = T.ffn_weights(rng, 256, 1024, 16, 0.25)
