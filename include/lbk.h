@@ -171,13 +171,31 @@ int lbk_looped_swiglu_bf16(const uint16_t* h_in, int64_t N, int32_t d_model,
                            void* stream);
 
 /*
+ * lbk_looped_swiglu_bf16 as separate launches per iteration: the weight packing and an fp32
+ * copy of h_in once, then a gate/up launch (RMSNorm of the state in its prologue) and a down
+ * launch (state += product) per iteration, or, for shapes outside the two-kernel path, RMSNorm
+ * and the row-block kernels per iteration with the state rounded to bf16 each time.  Same
+ * workspace.  lbk_looped_swiglu_bf16 takes this path where the persistent launch
+ * (lbk_looped_swiglu_persistent_bf16) does not take the shape.
+ */
+int lbk_looped_swiglu_launches_bf16(const uint16_t* h_in, int64_t N, int32_t d_model,
+                                    const float* norm_scale, float eps, int32_t L,
+                                    const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                                    uint16_t* h_out, void* workspace, size_t workspace_bytes,
+                                    void* stream);
+
+/*
  * The looped block of lbk_looped_swiglu_bf16 in one persistent launch (after the weight
  * packing): workgroup b owns token block b (64 tokens) for all L iterations, so nothing is
- * exchanged between workgroups and no grid-wide barrier is needed.  Per iteration it
- * RMS-normalises its fp32 state rows into an LDS panel, runs the gate/up tiles (h of its
- * tokens to the workspace), then the down tiles with h staged back through LDS, and adds the
- * result to its state.  Same workspace (lbk_looped_workspace_bytes) and same results as the
- * two-kernel path of lbk_looped_swiglu_bf16 (the same tiles, summed in the same order).
+ * exchanged between workgroups and no grid-wide barrier is needed.  Per iteration it runs
+ * the gate/up tiles on an LDS panel of its RMS-normalised fp32 state rows (h of its tokens
+ * to the workspace), then the down tiles with h staged back through LDS; the down phase adds
+ * the result to the state and, when one workgroup covers every down row (d_model / B <= 32),
+ * writes the next iteration's normalised panel itself, so the gate/up phase reads the state
+ * only in the first iteration.  Same workspace (lbk_looped_workspace_bytes); the same tiles
+ * in the same order as lbk_looped_swiglu_launches_bf16 (results agree to bf16 rounding: the
+ * sums of squares of the norm are taken in another order).  lbk_looped_swiglu_bf16 uses it
+ * for every shape it takes.
  * Takes B in {16, 32}, d_model a multiple of 128 and at most 1024, gate and up with the same
  * K, K_down <= 63 and a 16-byte aligned norm_scale; LBK_ERR_SHAPE otherwise.
  * Replaces the persistent core loop of the reference's design notes

@@ -286,6 +286,20 @@ size_t lbk_looped_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* ga
 int lbk_looped_swiglu_bf16(const uint16_t* h_in, int64_t N, int32_t d_model, const float* norm_scale, float eps,
                            int32_t L, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
                            uint16_t* h_out, void* workspace, size_t workspace_bytes, void* stream) {
+  // the persistent launch where it takes the shape (measured faster at the looped-block
+  // geometry), the per-iteration launches otherwise
+  if (gate && up && down && norm_scale && a16(norm_scale) &&
+      looped_persistent_supported(gate->B, d_model, gate->R, down->R, gate->K, up->K, down->K))
+    return lbk_looped_swiglu_persistent_bf16(h_in, N, d_model, norm_scale, eps, L, gate, up, down, h_out, workspace,
+                                             workspace_bytes, stream);
+  return lbk_looped_swiglu_launches_bf16(h_in, N, d_model, norm_scale, eps, L, gate, up, down, h_out, workspace,
+                                         workspace_bytes, stream);
+}
+
+int lbk_looped_swiglu_launches_bf16(const uint16_t* h_in, int64_t N, int32_t d_model, const float* norm_scale,
+                                    float eps, int32_t L, const lbk_bell* gate, const lbk_bell* up,
+                                    const lbk_bell* down, uint16_t* h_out, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
   int st;
   if ((st = check_bell(gate)) || (st = check_bell(up)) || (st = check_bell(down))) return st;
   int64_t d_ff = 0;

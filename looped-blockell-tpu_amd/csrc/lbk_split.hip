@@ -67,7 +67,9 @@ struct GUPanel { static constexpr int ROWB = 8192 / MT; };
 // gate/up of token block tb (16 * MT tokens) by one workgroup of 512 threads; smem holds the
 // panel and the column table (gu_lds bytes).  Waves without rows return after the panel
 // barrier, so a caller that synchronises afterwards must do so after the call.
-template <int B, int MT, bool NORM, bool INTER, bool SHARED>
+// READY: the panel and the column table are already in LDS (the looped kernel's down phase
+// wrote the next iteration's normalised rows; the table stays from the first iteration).
+template <int B, int MT, bool NORM, bool INTER, bool SHARED, bool READY = false>
 __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned char* smem, int tid) {
   constexpr int CW = TileShape<B>::CW;
   constexpr int TM = 16 * MT;
@@ -191,7 +193,9 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
 
   // ---- input panel: all of this thread's loads are issued before any store,
   // and the first ring positions' weight loads go out before the barrier
-  if constexpr (!NORM) {
+  if constexpr (READY) {
+    if (nrows > 0) prefetch_ring();
+  } else if constexpr (!NORM) {
     constexpr int CPR = ROWB / 16;                 // chunk capacity of a panel row
     constexpr int PIT = TM * CPR / 512;            // chunks per thread
     const int cpr = d_model / 8;
@@ -435,9 +439,14 @@ __device__ __forceinline__ void dn_build(FetchList<RPW>& L, int c0, int ncb, con
 // down projection of token block tb for the down rows of row group rg (NW * RPW rows) by one
 // workgroup of NW waves; dn_smem holds two h stages (2 * 16 * MT * DN_STAGE_COLS * 2 bytes).
 // Every wave reaches every barrier (a workgroup whose tokens are all past N returns at once).
-template <int B, int MT, int RPW, int NW>
+// NORMOUT (fp32 state mode, all down rows in this one group): the epilogue also writes the
+// RMSNorm of the new state rows (norm_scale, eps), as bf16, into the gate/up panel at the start
+// of dn_smem (row stride GUPanel<MT>::ROWB), for the next iteration's gate/up phase; red holds
+// (NW + 1) * 16 * MT floats for the per-token sums of squares.
+template <int B, int MT, int RPW, int NW, bool NORMOUT = false>
 __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, unsigned char* dn_smem,
-                                        uint16_t* out, int tid) {
+                                        uint16_t* out, int tid, const float* norm_scale = nullptr,
+                                        float eps = 0.f, float* red = nullptr) {
   constexpr int CW = TileShape<B>::CW;
   constexpr int TM = 16 * MT;
   constexpr int G = DnStage<B>::G;
@@ -579,6 +588,83 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
     __syncthreads();
   }
 
+  if constexpr (NORMOUT) {
+    // ---- epilogue with the next iteration's normalised panel: new state = acc + state
+    // (written back, kept in acc), per-token sums of squares over the lanes, the waves, then
+    // bf16(state * rs * scale) into the panel
+    constexpr int ROWB = GUPanel<MT>::ROWB;
+    float ssq[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) ssq[mt][v] = 0.f;
+#pragma unroll
+    for (int rho = 0; rho < RPW; ++rho) {
+      const int rm = row0 + w * RPW + rho;
+      if (rm >= a.R_m) continue;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int64_t t = t0 + 16 * mt + 4 * g + v;
+          const bool ok = t < a.N;
+          const int64_t off = (ok ? t : t0) * d_model + rm * B + CW * i;
+          float o[CW];
+#pragma unroll
+          for (int m = 0; m < CW; ++m) {
+            o[m] = acc[rho][mt][m][v] + (ok ? a.state[off + m] : 0.f);
+            acc[rho][mt][m][v] = o[m];
+            ssq[mt][v] += o[m] * o[m];
+          }
+          if (ok) {
+#pragma unroll
+            for (int m = 0; m < CW; ++m) a.state[off + m] = o[m];
+            if (out) store_bf16<CW>(out + off, o);
+          }
+        }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) ssq[mt][v] += __shfl_xor(ssq[mt][v], o, 64);
+        if (i == 0) red[w * TM + 16 * mt + 4 * g + v] = ssq[mt][v];
+      }
+    __syncthreads();
+    if (tid < TM) {
+      float ss = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) ss += red[ww * TM + tid];
+      red[NW * TM + tid] = 1.0f / sqrtf(ss / (float)d_model + eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rho = 0; rho < RPW; ++rho) {
+      const int rm = row0 + w * RPW + rho;
+      if (rm >= a.R_m) continue;
+      const int col = rm * B + CW * i;
+      float sc[CW];
+#pragma unroll
+      for (int m = 0; m < CW; ++m) sc[m] = norm_scale[col + m];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = 16 * mt + 4 * g + v;
+          const float rs = red[NW * TM + row];
+          unsigned char* dst = dn_smem + panel_addr<MT>(row, col / 8, ROWB) + 2 * (col % 8);
+          if constexpr (CW == 2) {
+            *reinterpret_cast<uint32_t*>(dst) =
+                pack2_bf16(acc[rho][mt][0][v] * rs * sc[0], acc[rho][mt][1][v] * rs * sc[1]);
+          } else {
+            *reinterpret_cast<uint16_t*>(dst) = f2bf(acc[rho][mt][0][v] * rs * sc[0]);
+          }
+        }
+    }
+    return;
+  }
+
   // ---- epilogue: + residual (bf16) or + fp32 state; store bf16 (and the state)
 #pragma unroll
   for (int rho = 0; rho < RPW; ++rho) {
@@ -629,6 +715,12 @@ __global__ __launch_bounds__(64 * DN_WAVES, (RPW == 1 && DN_WAVES == 8) ? 2 : 1)
 // ===========================================================================
 // looped block in one persistent launch
 // ===========================================================================
+// LDS of the looped kernel: gate/up panel (or the two down stages) | column table | per-token
+// sums of squares of the down phase's normalisation (9 * 16 * MT floats)
+template <int MT>
+__host__ __device__ inline size_t looped_red_offset(int R_ff, int K) {
+  return (size_t)16 * MT * GUPanel<MT>::ROWB + (((size_t)R_ff * K * 8 + 255) & ~(size_t)255);
+}
 // looped_kernel<B, MT, SHARED, RPW>: workgroup tb owns token block tb (16 * MT tokens) for
 // all L applications of h <- h + SwiGLU(RMSNorm(h)): it copies its rows of h_in into the fp32
 // state, then per iteration runs the gate/up tile (RMSNorm of its state rows into the LDS
@@ -661,6 +753,10 @@ __global__ __launch_bounds__(512, 1) void looped_kernel(LoopArgs la) {
   }
   __syncthreads();
   const int nrg = (la.dn.R_m + 8 * RPW - 1) / (8 * RPW);
+  // with every down row in one group, the down phase writes the next iteration's normalised
+  // panel itself (the gate/up phase then reads neither the state nor the column indices again)
+  const bool fuse = nrg == 1;
+  float* red = reinterpret_cast<float*>(smem + looped_red_offset<MT>(la.gu.R_ff, la.gu.Kg));
   for (int l = 0; l < la.L; ++l) {
     // The thread and token-block indices pass through an opaque copy in every phase:
     // otherwise the compiler hoists the phases' address arithmetic (derived from them) out
@@ -668,14 +764,18 @@ __global__ __launch_bounds__(512, 1) void looped_kernel(LoopArgs la) {
     int tg = tid;
     int64_t tbg = tb;
     asm volatile("" : "+v"(tg), "+s"(tbg));
-    gu_tile<B, MT, true, false, SHARED>(la.gu, tbg, smem, tg);
+    if (fuse && l > 0) gu_tile<B, MT, true, false, SHARED, true>(la.gu, tbg, smem, tg);
+    else gu_tile<B, MT, true, false, SHARED>(la.gu, tbg, smem, tg);
     __syncthreads();
     uint16_t* out = l == la.L - 1 ? la.dn.out : nullptr;
     for (int rg = 0; rg < nrg; ++rg) {
       int td = tid;
       int64_t tbd = tb;
       asm volatile("" : "+v"(td), "+s"(tbd));
-      dn_tile<B, MT, RPW, 8>(la.dn, tbd, rg, smem, out, td);
+      if (fuse && l < la.L - 1)
+        dn_tile<B, MT, RPW, 8, true>(la.dn, tbd, rg, smem, out, td, la.gu.norm_scale, la.gu.eps, red);
+      else
+        dn_tile<B, MT, RPW, 8>(la.dn, tbd, rg, smem, out, td);
       __syncthreads();
     }
   }
@@ -782,7 +882,10 @@ static int launch_looped_t(const LoopArgs& a, hipStream_t st) {
   const int TM = 16 * MT;
   const size_t dn_lds = 2 * (size_t)TM * DN_STAGE_COLS * 2;
   const size_t g_lds = gu_lds(a.gu.R_ff, a.gu.Kg, MT);
-  const size_t lds = g_lds > dn_lds ? g_lds : dn_lds;
+  size_t lds = g_lds > dn_lds ? g_lds : dn_lds;
+  const size_t r_end = looped_red_offset<MT>(a.gu.R_ff, a.gu.Kg) + (size_t)9 * TM * 4;
+  lds = lds > r_end ? lds : r_end;
+  if (lds > 163840) return -2;
   hipLaunchKernelGGL(kern, dim3((unsigned)((a.gu.N + TM - 1) / TM)), dim3(512), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
@@ -790,7 +893,8 @@ static int launch_looped_t(const LoopArgs& a, hipStream_t st) {
 // The persistent looped block takes the shapes of the two-kernel path with MT = 4
 // (d_model <= 1024): its LDS holds either the gate/up panel or the two down stages.
 bool looped_persistent_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd) {
-  return split_supported(B, d_model, R_ff, R_m, Kg, Ku, Kd) && gu_mt(d_model) == 4;
+  return split_supported(B, d_model, R_ff, R_m, Kg, Ku, Kd) && gu_mt(d_model) == 4 &&
+         looped_red_offset<4>(R_ff, Kg) + (size_t)9 * 64 * 4 <= 163840;
 }
 
 int launch_looped(int B, const LoopArgs& a, hipStream_t st) {

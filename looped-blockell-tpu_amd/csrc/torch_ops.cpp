@@ -203,7 +203,7 @@ at::Tensor diagonal_injection(const at::Tensor& h_, const at::Tensor& e_, const 
 
 at::Tensor looped_impl(const at::Tensor& h, const at::Tensor& scale_, at::Tensor vg, at::Tensor cg, at::Tensor vu,
                        at::Tensor cu, at::Tensor vd, at::Tensor cd, int64_t L, double eps, const char* op,
-                       bool persistent = false) {
+                       int path = 0) {
   at::Tensor x = check_x2d(h, op);
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
   lbk_bell g = make_bell(vg, cg, op, "gate"), u = make_bell(vu, cu, op, "up"), d = make_bell(vd, cd, op, "down");
@@ -213,7 +213,9 @@ at::Tensor looped_impl(const at::Tensor& h, const at::Tensor& scale_, at::Tensor
   at::Tensor out = at::empty_like(x);
   const size_t wsb = lbk_looped_workspace_bytes(x.size(0), (int32_t)x.size(1), &g, &u, &d);
   at::Tensor ws = wsb ? workspace(wsb, x) : at::Tensor();
-  auto fn = persistent ? lbk_looped_swiglu_persistent_bf16 : lbk_looped_swiglu_bf16;
+  // path 0: the library's choice, 1: one persistent launch, 2: launches per iteration
+  auto fn = path == 1 ? lbk_looped_swiglu_persistent_bf16
+                      : (path == 2 ? lbk_looped_swiglu_launches_bf16 : lbk_looped_swiglu_bf16);
   LBK_CALL("looped_swiglu", fn(bf(x), x.size(0), (int32_t)x.size(1), s.data_ptr<float>(), (float)eps, (int32_t)L,
                                &g, &u, &d, bfm(out), wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(x)));
   return out;
@@ -222,7 +224,13 @@ at::Tensor looped_impl(const at::Tensor& h, const at::Tensor& scale_, at::Tensor
 at::Tensor looped_swiglu_persistent(const at::Tensor& h, const at::Tensor& scale, const at::Tensor& vg,
                                     const at::Tensor& cg, const at::Tensor& vu, const at::Tensor& cu,
                                     const at::Tensor& vd, const at::Tensor& cd, int64_t L, double eps) {
-  return looped_impl(h, scale, vg, cg, vu, cu, vd, cd, L, eps, "looped_swiglu_persistent", true);
+  return looped_impl(h, scale, vg, cg, vu, cu, vd, cd, L, eps, "looped_swiglu_persistent", 1);
+}
+
+at::Tensor looped_swiglu_launches(const at::Tensor& h, const at::Tensor& scale, const at::Tensor& vg,
+                                  const at::Tensor& cg, const at::Tensor& vu, const at::Tensor& cu,
+                                  const at::Tensor& vd, const at::Tensor& cd, int64_t L, double eps) {
+  return looped_impl(h, scale, vg, cg, vu, cu, vd, cd, L, eps, "looped_swiglu_launches", 2);
 }
 
 at::Tensor looped_swiglu(const at::Tensor& h, const at::Tensor& scale, const at::Tensor& vg, const at::Tensor& cg,
@@ -493,6 +501,8 @@ TORCH_LIBRARY(titan, m) {
         "Tensor v_down, Tensor ci_down, int L, float eps=1e-05) -> Tensor");
   m.def("looped_swiglu_persistent(Tensor h, Tensor norm_scale, Tensor v_gate, Tensor ci_gate, Tensor v_up, "
         "Tensor ci_up, Tensor v_down, Tensor ci_down, int L, float eps=1e-05) -> Tensor");
+  m.def("looped_swiglu_launches(Tensor h, Tensor norm_scale, Tensor v_gate, Tensor ci_gate, Tensor v_up, "
+        "Tensor ci_up, Tensor v_down, Tensor ci_down, int L, float eps=1e-05) -> Tensor");
   m.def("rmsnorm(Tensor x, Tensor scale, float eps=1e-05) -> Tensor");
   m.def("diagonal_injection(Tensor h, Tensor e, Tensor log_A, Tensor log_dt) -> Tensor");
   m.def("quantize_act_int8(Tensor x) -> (Tensor, Tensor)");
@@ -523,6 +533,7 @@ TORCH_LIBRARY_IMPL(titan, CUDA, m) {
   m.impl("block_ell_matmul_bwd", &block_ell_matmul_bwd);
   m.impl("looped_swiglu", &looped_swiglu);
   m.impl("looped_swiglu_persistent", &looped_swiglu_persistent);
+  m.impl("looped_swiglu_launches", &looped_swiglu_launches);
   m.impl("rmsnorm", &rmsnorm);
   m.impl("diagonal_injection", &diagonal_injection);
   m.impl("quantize_act_int8", &quantize_act_int8);
@@ -579,6 +590,9 @@ TORCH_LIBRARY_IMPL(titan, Meta, m) {
                              const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t,
                              double) { return at::empty_like(h); });
   m.impl("looped_swiglu_persistent", [](const at::Tensor& h, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+                             const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t,
+                             double) { return at::empty_like(h); });
+  m.impl("looped_swiglu_launches", [](const at::Tensor& h, const at::Tensor&, const at::Tensor&, const at::Tensor&,
                              const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t,
                              double) { return at::empty_like(h); });
   m.impl("rmsnorm", [](const at::Tensor& x, const at::Tensor&, double) { return at::empty_like(x); });

@@ -84,6 +84,7 @@ SIGNATURES = {
     "lbk_looped_swiglu_bf16": (C.c_int, [_P, _I64, _I32, _P, _F, _I32, _PB, _PB, _PB, _P, _P, _SZ, _P]),
     "lbk_looped_swiglu_persistent_bf16": (C.c_int, [_P, _I64, _I32, _P, _F, _I32, _PB, _PB, _PB, _P, _P, _SZ,
                                                     _P]),
+    "lbk_looped_swiglu_launches_bf16": (C.c_int, [_P, _I64, _I32, _P, _F, _I32, _PB, _PB, _PB, _P, _P, _SZ, _P]),
     "lbk_quantize_act_int8": (C.c_int, [_P, _I64, _I32, _I64, _P, _P, _P]),
     "lbk_pack_ternary": (C.c_int, [_P, _I32, _I32, _I32, _P, _P]),
     "lbk_ternary_quantize_weights_bf16": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P]),

@@ -149,7 +149,8 @@ def swiglu(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual: bool 
 
 
 def looped_swiglu(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L: int, eps: float = 1e-5):
-    """L applications of h <- h + SwiGLU(RMSNorm(h)) with shared weights, in one operator call."""
+    """L applications of h <- h + SwiGLU(RMSNorm(h)) with shared weights, in one operator call (one
+    persistent launch where the shape allows, per-iteration launches otherwise)."""
     _gpu(h, v_gate, v_down)
     return ops().looped_swiglu(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L, eps)
 
@@ -160,6 +161,14 @@ def looped_swiglu_persistent(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down
     iterations (same tiles, same summation order, same result as the two-kernel path)."""
     _gpu(h, v_gate, v_down)
     return ops().looped_swiglu_persistent(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L, eps)
+
+
+def looped_swiglu_launches(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L: int,
+                           eps: float = 1e-5):
+    """``looped_swiglu`` as a gate/up and a down launch per iteration (the path the library takes
+    for shapes outside the persistent kernel's)."""
+    _gpu(h, v_gate, v_down)
+    return ops().looped_swiglu_launches(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L, eps)
 
 
 def rmsnorm(x, scale, eps: float = 1e-5):

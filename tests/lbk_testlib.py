@@ -139,9 +139,10 @@ def abi_swiglu(x_t, g_t, u_t, d_t, add_residual=False, intermediates=False):
     return out, h, gp, uo
 
 
-def abi_looped(h_t, scale_t, g_t, u_t, d_t, L, eps, persistent=False, out=None):
-    """The looped block through the C ABI: lbk_looped_swiglu_bf16, or with persistent=True the
-    one-launch lbk_looped_swiglu_persistent_bf16 (same workspace)."""
+def abi_looped(h_t, scale_t, g_t, u_t, d_t, L, eps, persistent=False, out=None, launches=False):
+    """The looped block through the C ABI: lbk_looped_swiglu_bf16 (the library's choice of path),
+    with persistent=True the one-launch lbk_looped_swiglu_persistent_bf16, with launches=True the
+    per-iteration launches of lbk_looped_swiglu_launches_bf16 (one workspace size for all)."""
     import torch
     A = abi()
     lib = A.load()
@@ -150,7 +151,8 @@ def abi_looped(h_t, scale_t, g_t, u_t, d_t, L, eps, persistent=False, out=None):
     out = torch.empty_like(h_t) if out is None else out
     wsb = lib.lbk_looped_workspace_bytes(N, dm, C.byref(gb), C.byref(ub), C.byref(db))
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=h_t.device)
-    fn = lib.lbk_looped_swiglu_persistent_bf16 if persistent else lib.lbk_looped_swiglu_bf16
+    fn = (lib.lbk_looped_swiglu_persistent_bf16 if persistent else
+          lib.lbk_looped_swiglu_launches_bf16 if launches else lib.lbk_looped_swiglu_bf16)
     A.check(fn(ptr(h_t), N, dm, ptr(scale_t), C.c_float(eps), L, C.byref(gb), C.byref(ub), C.byref(db), ptr(out),
                ptr(ws) if wsb else C.c_void_p(0), wsb, stream()), "looped_persistent" if persistent else "looped")
     return out

@@ -291,13 +291,17 @@ PERSISTENT_CASES = [
     (1024, 4096, 32, 0.25, 64, 2, True),
     (512, 2048, 32, 0.5, 1, 1, False),
     (384, 1536, 32, 0.25, 200, 4, False),       # 12 down rows: a partial row group
+    (1024, 2048, 16, 0.25, 70, 3, False),       # 64 down rows: two row groups, norm not fused
 ]
 
 
 @pytest.mark.parametrize("case", PERSISTENT_CASES)
 def test_looped_persistent_matches_two_kernel_path(gpu, case):
     """The one-launch persistent looped block runs the same tiles in the same order as the
-    per-iteration gate/up + down launches: bit-identical outputs; both within TOL of the oracle."""
+    per-iteration gate/up + down launches; its down phase computes the next iteration's RMSNorm
+    (per-token sums of squares in another order), so the two agree to bf16 rounding, and both
+    are within TOL of the oracle.  With one iteration, or two row groups (norm not fused), they
+    are bit-identical."""
     d_model, d_ff, B, dens, N, L, shared = case
     _say(f"looped persistent {case}")
     rng = np.random.default_rng(abs(hash(case)) % 2 ** 31)
@@ -310,9 +314,13 @@ def test_looped_persistent_matches_two_kernel_path(gpu, case):
     if shared:
         ws[1] = (ws[1][0], ws[0][1])   # one index buffer: the shared-topology kernels
     ht, st = T.to_gpu_bf16(h), T.to_gpu(scale)
-    two = T.to_np(T.abi_looped(ht, st, *ws, L, 1e-5))
+    two = T.to_np(T.abi_looped(ht, st, *ws, L, 1e-5, launches=True))
     one = T.to_np(T.abi_looped(ht, st, *ws, L, 1e-5, persistent=True))
-    assert np.array_equal(one, two)
+    assert np.array_equal(one, T.to_np(T.abi_looped(ht, st, *ws, L, 1e-5)))   # the default path
+    if L == 1 or d_model // B > 32:
+        assert np.array_equal(one, two)
+    else:
+        assert T.rel_err(one, two)[0] <= TOL
     f64 = lambda w: (w[0].astype(np.float64), w[1])
     ref = O.looped_swiglu(h.astype(np.float64), scale.astype(np.float64), f64(g), f64(u), f64(d), L=L, eps=1e-5)
     rel, ab = T.rel_err(one, ref)
@@ -331,10 +339,12 @@ def test_looped_persistent_full_size_and_in_place(gpu):
     scale = np.ones(d_model, np.float32)
     ws = [T.gpu_weight(w) for w in (g, u, d)]
     ht, st = T.to_gpu_bf16(h), T.to_gpu(scale)
-    two = T.abi_looped(ht, st, *ws, L, 1e-5)
+    two = T.abi_looped(ht, st, *ws, L, 1e-5, launches=True)
     inplace = ht.clone()
     T.abi_looped(inplace, st, *ws, L, 1e-5, persistent=True, out=inplace)
-    assert torch.equal(inplace, two)
+    again = T.abi_looped(ht, st, *ws, L, 1e-5, persistent=True)
+    assert torch.equal(inplace, again)                       # in place == out of place, deterministic
+    assert T.rel_err(T.to_np(inplace), T.to_np(two))[0] <= TOL
     rows = np.sort(rng.choice(N, 128, replace=False))
     f64 = lambda w: (w[0].astype(np.float64), w[1])
     ref = O.looped_swiglu(h[rows].astype(np.float64), scale.astype(np.float64), f64(g), f64(u), f64(d), L=L)
