@@ -38,8 +38,12 @@ enum {
     LBK_ERR_WORKSPACE = 5,     /* workspace missing or smaller than required */
     LBK_ERR_LAUNCH = 6,        /* HIP reported an error launching a kernel */
     LBK_ERR_ARG = 7,           /* other invalid argument (N < 0, L < 0, eps < 0 ...) */
-    LBK_ERR_COLUMN = 8         /* reserved: column index >= C found by lbk_check_columns */
+    LBK_ERR_COLUMN = 8,        /* reserved: column index >= C found by lbk_check_columns */
+    LBK_ERR_TOO_LARGE = 9      /* the geometry needs more than the no-alloc entry point's fixed scratch */
 };
+
+/* Size of the fixed device scratch array behind lbk_swiglu_fwd_bf16_noalloc (per GPU). */
+#define LBK_NOALLOC_SCRATCH_BYTES (4u << 20)
 
 /* One Block-ELL weight with bf16 tiles. */
 typedef struct lbk_bell {
@@ -104,6 +108,22 @@ int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model,
                         int add_residual, uint16_t* out,
                         uint16_t* h_out, uint16_t* gate_pre_out, uint16_t* up_out,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * lbk_swiglu_fwd_bf16 (no optional outputs) for callers that cannot allocate: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.  No counterpart in the
+ * reference.  Instead of a workspace it uses a fixed array of LBK_NOALLOC_SCRATCH_BYTES (4 MiB)
+ * in device memory, one per GPU, held until the process ends; the call itself allocates and
+ * frees nothing.  Geometries whose workspace (lbk_swiglu_workspace_bytes with
+ * want_intermediates = 0) exceeds the array return LBK_ERR_TOO_LARGE without launching
+ * anything: decode shapes fit (16 tokens at d_ff = 14336 need 459 KB).  All calls on one GPU
+ * share its array: calls that overlap in time on one GPU race.  Same kernels, same results as
+ * lbk_swiglu_fwd_bf16.
+ */
+size_t lbk_noalloc_scratch_bytes(void);
+int lbk_swiglu_fwd_bf16_noalloc(const uint16_t* x, int64_t N, int32_t d_model,
+                                const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                                int add_residual, uint16_t* out, void* stream);
 
 /*
  * Workspace bytes needed by lbk_swiglu_bwd_bf16 for this geometry: the transposed

@@ -25,7 +25,7 @@ LIB = os.path.join(PKG, "liblbk.so")
 EXT = os.path.join(PKG, "_titan_ext.so")
 
 HIP_SOURCES = ["lbk_bf16.hip", "lbk_split.hip", "lbk_decode.hip", "lbk_ternary.hip", "lbk_tsplit.hip", "lbk_bwd.hip", "lbk_topo.hip", "lbk_format.hip",
-               "lbk_abi.hip"]
+               "lbk_abi.hip", "lbk_noalloc.hip"]
 ARCH = os.environ.get("LBK_OFFLOAD_ARCH", "gfx950")
 
 # Packed-fp32 VALU forms are kept out of the generated code.

@@ -105,6 +105,7 @@ const char* lbk_status_string(int s) {
     case LBK_ERR_LAUNCH: return "HIP kernel launch failed";
     case LBK_ERR_ARG: return "invalid argument";
     case LBK_ERR_COLUMN: return "column index out of range";
+    case LBK_ERR_TOO_LARGE: return "geometry needs more than the no-alloc entry point's fixed scratch";
     default: return "unknown status";
   }
 }

@@ -23,6 +23,7 @@ LBK_ERR_WORKSPACE = 5
 LBK_ERR_LAUNCH = 6
 LBK_ERR_ARG = 7
 LBK_ERR_COLUMN = 8
+LBK_ERR_TOO_LARGE = 9
 
 
 class Bell(C.Structure):
@@ -75,6 +76,8 @@ SIGNATURES = {
     "lbk_block_ell_matmul_bf16": (C.c_int, [_P, _I64, _I32, _I64, _PB, _P, _P, _I64, _P]),
     "lbk_swiglu_workspace_bytes": (_SZ, [_I64, _I32, _PB, _PB, _PB, C.c_int]),
     "lbk_swiglu_fwd_bf16": (C.c_int, [_P, _I64, _I32, _PB, _PB, _PB, C.c_int, _P, _P, _P, _P, _P, _SZ, _P]),
+    "lbk_noalloc_scratch_bytes": (_SZ, []),
+    "lbk_swiglu_fwd_bf16_noalloc": (C.c_int, [_P, _I64, _I32, _PB, _PB, _PB, C.c_int, _P, _P]),
     "lbk_swiglu_bwd_workspace_bytes": (_SZ, [_I64, _I32, _PB, _PB, _PB]),
     "lbk_swiglu_bwd_bf16": (C.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _PB, _PB, _PB, C.c_int, _P, _P, _P, _P, _P,
                                       _SZ, _P]),
