@@ -494,51 +494,55 @@ __global__ __launch_bounds__(512, 1) void tdn_kernel(TDNArgs a) {
 #pragma unroll
   for (int sl = 0; sl < TD_RING; ++sl) meta(P[sl]);
 
-  // ---- panel: the 16 h rows quantised to int8.  A unit is 16 values (32 bytes of h);
-  // batches of 8 units per thread are loaded before any is converted.
+  // ---- panel: the 16 h rows quantised to int8.  A unit is 16 values (32 bytes of h) of one
+  // row; thread tid takes the units cc = tid, tid + 512, ... of every row (no index division),
+  // rows in batches of 8 whose loads are all issued before any is converted.  Quantisation
+  // per value: q = clamp(rint(h * scale), -128, 127) computed as med3(h * scale, -128, 127) +
+  // 1.5 * 2^23 (the add rounds to the nearest integer, ties to even, and leaves the int8 two's
+  // complement in the low byte of the float); bytes of four values merged with two v_perm.
   {
     constexpr int UB = 8;
-    const int upr = d_ff / 16;          // units per row
-    const int units = TM * upr;
-    for (int base = tid; base < units; base += 512 * UB) {
-      u32x4 hv[UB][2];
+    const int upr = d_ff / 16;          // units per row (a multiple of 16)
+    for (int cc = tid; cc < upr; cc += 512) {
+#pragma unroll 1
+      for (int rb = 0; rb < TM; rb += UB) {
+        u32x4 hv[UB][2];
 #pragma unroll
-      for (int b = 0; b < UB; ++b) {
-        int e = base + 512 * b;
-        e = e < units ? e : units - 1;
-        const int row = e / upr, cc = e - row * upr;
-        int64_t t = t0 + row;
-        t = t < a.N ? t : a.N - 1;
-        const u32x4* hp = reinterpret_cast<const u32x4*>(a.h + t * (int64_t)d_ff + 16 * cc);
-        hv[b][0] = hp[0];
-        hv[b][1] = hp[1];
-      }
-#pragma unroll
-      for (int b = 0; b < UB; ++b) {
-        const int eb = base + 512 * b;
-        const int e = eb < units ? eb : units - 1;   // a clamped unit rewrites the last unit's own bytes
-        const int row = e / upr, cc = e - row * upr;
-        const int64_t t = t0 + row;
-        const float sc = s_scale[row];
-        u32x4 q = {0, 0, 0, 0};
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const uint32_t wv = hv[b][u >> 2][u & 3];
-          const float lo = fminf(fmaxf(rintf(__fmul_rn(bf_lo(wv), sc)), -128.f), 127.f);
-          const float hi = fminf(fmaxf(rintf(__fmul_rn(bf_hi(wv), sc)), -128.f), 127.f);
-          const uint32_t pair = ((uint32_t)((int)lo) & 0xffu) | (((uint32_t)((int)hi) & 0xffu) << 8);
-          q[u >> 1] |= pair << (16 * (u & 1));
+        for (int b = 0; b < UB; ++b) {
+          int64_t t = t0 + rb + b;
+          t = t < a.N ? t : a.N - 1;
+          const u32x4* hp = reinterpret_cast<const u32x4*>(a.h + t * (int64_t)d_ff + 16 * cc);
+          hv[b][0] = hp[0];
+          hv[b][1] = hp[1];
         }
-        if (t >= a.N) q = u32x4{0, 0, 0, 0};
-        if (a.hq_out && t < a.N && eb < units)
-          *reinterpret_cast<u32x4*>(a.hq_out + t * (int64_t)d_ff + 16 * cc) = q;
-        // -sum(hq) of each 64-wide block: its 4 chunks sit in 4 adjacent lanes, all of which
-        // are in range or all clamped (units and the chunks per row are multiples of 4)
-        int sm = sum16_i8(q);
-        sm += __shfl_xor(sm, 1, 64);
-        sm += __shfl_xor(sm, 2, 64);
-        if ((cc & 3) == 0 && eb < units) rsum[(cc >> 2) * TM + row] = -sm;
-        *reinterpret_cast<u32x4*>(smem + tpanel_addr<1>(row, cc, rowb)) = q;
+#pragma unroll
+        for (int b = 0; b < UB; ++b) {
+          const int row = rb + b;
+          const int64_t t = t0 + row;
+          const float sc = s_scale[row];
+          u32x4 q;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            // dword d of the result: values 4d .. 4d + 3 (bf16 pairs hv[.][d / 2][2 (d % 2)], + 1)
+            const uint32_t w0 = hv[b][d >> 1][2 * (d & 1)], w1 = hv[b][d >> 1][2 * (d & 1) + 1];
+            const float v0 = __builtin_amdgcn_fmed3f(__fmul_rn(bf_lo(w0), sc), -128.f, 127.f) + 12582912.0f;
+            const float v1 = __builtin_amdgcn_fmed3f(__fmul_rn(bf_hi(w0), sc), -128.f, 127.f) + 12582912.0f;
+            const float v2 = __builtin_amdgcn_fmed3f(__fmul_rn(bf_lo(w1), sc), -128.f, 127.f) + 12582912.0f;
+            const float v3 = __builtin_amdgcn_fmed3f(__fmul_rn(bf_hi(w1), sc), -128.f, 127.f) + 12582912.0f;
+            const uint32_t lo = __builtin_amdgcn_perm(__float_as_uint(v1), __float_as_uint(v0), 0x0c0c0400u);
+            const uint32_t hi = __builtin_amdgcn_perm(__float_as_uint(v3), __float_as_uint(v2), 0x04000c0cu);
+            q[d] = lo | hi;
+          }
+          if (t >= a.N) q = u32x4{0, 0, 0, 0};
+          if (a.hq_out && t < a.N) *reinterpret_cast<u32x4*>(a.hq_out + t * (int64_t)d_ff + 16 * cc) = q;
+          // -sum(hq) of each 64-wide block: its 4 units sit in 4 adjacent lanes, all of which
+          // take part (upr is a multiple of 16, so a 4-lane group is in or out as a whole)
+          int sm = sum16_i8(q);
+          sm += __shfl_xor(sm, 1, 64);
+          sm += __shfl_xor(sm, 2, 64);
+          if ((cc & 3) == 0) rsum[(cc >> 2) * TM + row] = -sm;
+          *reinterpret_cast<u32x4*>(smem + tpanel_addr<1>(row, cc, rowb)) = q;
+        }
       }
     }
   }
