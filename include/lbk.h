@@ -126,6 +126,21 @@ int lbk_swiglu_fwd_bf16_noalloc(const uint16_t* x, int64_t N, int32_t d_model,
                                 int add_residual, uint16_t* out, void* stream);
 
 /*
+ * lbk_swiglu_fwd_bf16 with the projections' biases (each fp32, optional):
+ *   out = W_down(silu(W_gate x + b_gate) * (W_up x + b_up)) + b_down  (+ x if add_residual)
+ * b_gate, b_up [d_ff], b_down [d_model]; gate_pre_out / up_out then hold W_gate x + b_gate and
+ * W_up x + b_up.  The biases are added in fp32 in the kernels' epilogues.  Replaces the biased
+ * BlockELLLinear projections of the reference's SwiGLU MLPBlock
+ * (looped_blockell/layers/mlp.py:56-60, :82, :119-145).  Same workspace as lbk_swiglu_fwd_bf16.
+ */
+int lbk_swiglu_fwd_bias_bf16(const uint16_t* x, int64_t N, int32_t d_model,
+                             const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                             const float* b_gate, const float* b_up, const float* b_down,
+                             int add_residual, uint16_t* out,
+                             uint16_t* h_out, uint16_t* gate_pre_out, uint16_t* up_out,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Workspace bytes needed by lbk_swiglu_bwd_bf16 for this geometry: the transposed
  * column lists of the three weights, dg and du [N, d_ff] bf16, and fp32 partial
  * tile gradients (one set per 2048 tokens).
@@ -155,12 +170,44 @@ int lbk_swiglu_bwd_bf16(const uint16_t* grad_out, const uint16_t* x, const uint1
                         uint16_t* d_down_values, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * lbk_swiglu_bwd_bf16 plus the bias gradients of lbk_swiglu_fwd_bias_bf16 (each optional, fp32):
+ * d_b_gate = column sums of dg, d_b_up = of du [d_ff], d_b_down = of grad_out [d_model],
+ * summed per 64-row group and the groups in a fixed order (deterministic).  gate_pre_act and
+ * up_output are the forward's biased pre-activations.  Its workspace
+ * (lbk_swiglu_bwd_bias_workspace_bytes) adds the column-sum partials when a bias gradient is
+ * asked for.
+ */
+size_t lbk_swiglu_bwd_bias_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate,
+                                           const lbk_bell* up, const lbk_bell* down);
+int lbk_swiglu_bwd_bias_bf16(const uint16_t* grad_out, const uint16_t* x, const uint16_t* gate_pre_act,
+                             const uint16_t* up_output, const uint16_t* h, int64_t N, int32_t d_model,
+                             const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                             int add_residual, uint16_t* dx, uint16_t* d_gate_values,
+                             uint16_t* d_up_values, uint16_t* d_down_values, float* d_b_gate,
+                             float* d_b_up, float* d_b_down, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/*
  * out = x / sqrt(mean(x^2) + eps) * scale, rows of length d (bf16 in/out, fp32 math).
  * Replaces rmsnorm_cuda (reference csrc/loop/persistent_core.cuh:76-92) with the
  * layer-API semantics of looped_blockell/layers/norms.py:14-15.
  */
 int lbk_rmsnorm_bf16(const uint16_t* x, int64_t N, int32_t d, const float* scale, float eps,
                      uint16_t* out, void* stream);
+
+/*
+ * Backward of lbk_rmsnorm_bf16 for an output gradient dy [N, d] (bf16):
+ *   dx     [N, d] bf16 = rs * scale * dy - x * rs^3 * mean(scale * dy * x)
+ *   dscale [d] fp32    = sum over rows of dy * x * rs,   rs = 1 / sqrt(mean(x^2) + eps)
+ * fp32 arithmetic; dscale is summed per 64-row group into the workspace
+ * (lbk_rmsnorm_bwd_workspace_bytes) and the groups in a fixed order: deterministic.
+ * The reference differentiates its Flax RMSNorm with JAX autodiff
+ * (looped_blockell/layers/norms.py:8-15).
+ */
+size_t lbk_rmsnorm_bwd_workspace_bytes(int64_t N, int32_t d);
+int lbk_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* dy, int64_t N, int32_t d, const float* scale,
+                         float eps, uint16_t* dx, float* dscale, void* workspace, size_t workspace_bytes,
+                         void* stream);
 
 /*
  * h_out = h + e-injection: decay*h + dt*e with dt = softplus(log_dt),
@@ -189,6 +236,19 @@ int lbk_looped_swiglu_bf16(const uint16_t* h_in, int64_t N, int32_t d_model,
                            const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
                            uint16_t* h_out, void* workspace, size_t workspace_bytes,
                            void* stream);
+
+/*
+ * lbk_looped_swiglu_bf16 with the projections' biases (as lbk_swiglu_fwd_bias_bf16; each
+ * optional): h <- h + (W_down(silu(W_gate n + b_gate) * (W_up n + b_up)) + b_down),
+ * n = RMSNorm(h).  The looped block of the reference's MLPBlock with its biased projections
+ * (looped_blockell/layers/mlp.py:56-60, looped_blockell/layers/transformer_block.py:83-84).
+ */
+int lbk_looped_swiglu_bias_bf16(const uint16_t* h_in, int64_t N, int32_t d_model,
+                                const float* norm_scale, float eps, int32_t L,
+                                const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                                const float* b_gate, const float* b_up, const float* b_down,
+                                uint16_t* h_out, void* workspace, size_t workspace_bytes,
+                                void* stream);
 
 /*
  * lbk_looped_swiglu_bf16 as separate launches per iteration: the weight packing and an fp32

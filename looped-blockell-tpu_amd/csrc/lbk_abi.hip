@@ -49,9 +49,16 @@ int check_ffn(const W* gate, const W* up, const W* down, int32_t d_model, int64_
   return LBK_OK;
 }
 
+// optional fp32 biases of the three projections (gate/up [d_ff], down [d_model])
+struct Biases {
+  const float* g;
+  const float* u;
+  const float* d;
+};
+
 int swiglu_general(const uint16_t* x, int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
                    const lbk_bell* down, const uint16_t* resid, uint16_t* out, uint16_t* h,
-                   uint16_t* gate_pre, uint16_t* up_out, hipStream_t st) {
+                   uint16_t* gate_pre, uint16_t* up_out, hipStream_t st, Biases bs = {}) {
   const int B = gate->B;
   const int64_t d_ff = (int64_t)gate->R * B;
   RowblockLaunch a{};
@@ -59,12 +66,13 @@ int swiglu_general(const uint16_t* x, int64_t N, int32_t d_model, const lbk_bell
   a.v0 = gate->values; a.c0 = gate->col_idx; a.K0 = gate->K;
   a.v1 = up->values; a.c1 = up->col_idx; a.K1 = up->K;
   a.y = h; a.ldy = d_ff; a.aux0 = gate_pre; a.aux1 = up_out; a.ldaux = d_ff;
+  a.bias = bs.g; a.bias1 = bs.u;
   if (launch_rowblock(B, 1, a, st) != 0) return LBK_ERR_LAUNCH;
   RowblockLaunch d{};
   d.x = h; d.N = N; d.ldx = d_ff; d.C = gate->R; d.R = down->R;
   d.v0 = down->values; d.c0 = down->col_idx; d.K0 = down->K;
   d.resid = resid; d.ldr = d_model;
-  d.y = out; d.ldy = d_model;
+  d.y = out; d.ldy = d_model; d.bias = bs.d;
   if (launch_rowblock(B, 2, d, st) != 0) return LBK_ERR_LAUNCH;
   return LBK_OK;
 }
@@ -173,19 +181,19 @@ static int pack_ffn(const lbk_bell* gate, const lbk_bell* up, const lbk_bell* do
 static int swiglu_split(const uint16_t* x, const float* xf, const float* norm_scale, float eps, int64_t N,
                         int32_t d_model, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
                         const PackedFFN& pk, const uint16_t* resid, float* state, uint16_t* out, uint16_t* h,
-                        uint16_t* gate_pre, uint16_t* up_out, hipStream_t st) {
+                        uint16_t* gate_pre, uint16_t* up_out, hipStream_t st, Biases bs = {}) {
   GUArgs g{};
   g.x = x; g.xf = xf; g.N = N; g.d_model = d_model; g.norm_scale = norm_scale; g.eps = eps;
   g.pg = pk.g; g.cg = gate->col_idx; g.Kg = gate->K;
   g.pu = pk.u; g.cu = up->col_idx; g.Ku = up->K;
   g.R_ff = gate->R;
-  g.h = h; g.gpre = gate_pre; g.uout = up_out;
+  g.h = h; g.gpre = gate_pre; g.uout = up_out; g.bg = bs.g; g.bu = bs.u;
   if (launch_gu(gate->B, xf != nullptr, g, st) != 0) return LBK_ERR_LAUNCH;
   DNArgs d{};
   d.h = h; d.N = N; d.d_ff = (int64_t)gate->R * gate->B; d.d_model = d_model;
   d.pd = pk.d; d.cd = down->col_idx; d.Kd = down->K;
   d.R_m = down->R; d.C_d = gate->R;
-  d.resid = resid; d.state = state; d.out = out;
+  d.resid = resid; d.state = state; d.out = out; d.bd = bs.d;
   return launch_dn(gate->B, d, st) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
 }
 
@@ -212,6 +220,16 @@ int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk
                         const lbk_bell* down, int add_residual, uint16_t* out, uint16_t* h_out,
                         uint16_t* gate_pre_out, uint16_t* up_out, void* workspace, size_t workspace_bytes,
                         void* stream) {
+  return lbk_swiglu_fwd_bias_bf16(x, N, d_model, gate, up, down, nullptr, nullptr, nullptr, add_residual, out, h_out,
+                                  gate_pre_out, up_out, workspace, workspace_bytes, stream);
+}
+
+int lbk_swiglu_fwd_bias_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk_bell* gate,
+                             const lbk_bell* up, const lbk_bell* down, const float* b_gate, const float* b_up,
+                             const float* b_down, int add_residual, uint16_t* out, uint16_t* h_out,
+                             uint16_t* gate_pre_out, uint16_t* up_out, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  const Biases bs{b_gate, b_up, b_down};
   int st;
   if ((st = check_bell(gate)) || (st = check_bell(up)) || (st = check_bell(down))) return st;
   int64_t d_ff = 0;
@@ -239,6 +257,7 @@ int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk
     a.resid = add_residual ? x : nullptr;
     a.out = out;
     a.h = hbuf;
+    a.bg = bs.g; a.bu = bs.u; a.bd = bs.d;
     return launch_decode(gate->B, a, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
   }
   const bool split = use_split(gate, up, down, d_model);
@@ -255,9 +274,10 @@ int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk
     PackedFFN pk{};
     if ((st = pack_ffn(gate, up, down, ws, &pk, s))) return st;
     return swiglu_split(x, nullptr, nullptr, 0.f, N, d_model, gate, up, down, pk, add_residual ? x : nullptr,
-                        nullptr, out, h, gate_pre_out, up_out, s);
+                        nullptr, out, h, gate_pre_out, up_out, s, bs);
   }
-  return swiglu_general(x, N, d_model, gate, up, down, add_residual ? x : nullptr, out, h, gate_pre_out, up_out, s);
+  return swiglu_general(x, N, d_model, gate, up, down, add_residual ? x : nullptr, out, h, gate_pre_out, up_out, s,
+                        bs);
 }
 
 int lbk_rmsnorm_bf16(const uint16_t* x, int64_t N, int32_t d, const float* scale, float eps, uint16_t* out,
@@ -266,6 +286,23 @@ int lbk_rmsnorm_bf16(const uint16_t* x, int64_t N, int32_t d, const float* scale
   if (N == 0) return LBK_OK;
   if (!x || !scale || !out) return LBK_ERR_NULL;
   return launch_rmsnorm(x, N, d, scale, eps, out, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+size_t lbk_rmsnorm_bwd_workspace_bytes(int64_t N, int32_t d) {
+  if (N < 0 || d <= 0) return 0;
+  return align256(rmsnorm_bwd_bytes(N, d));
+}
+
+int lbk_rmsnorm_bwd_bf16(const uint16_t* x, const uint16_t* dy, int64_t N, int32_t d, const float* scale, float eps,
+                         uint16_t* dx, float* dscale, void* workspace, size_t workspace_bytes, void* stream) {
+  if (N < 0 || d <= 0 || !(eps >= 0.f)) return LBK_ERR_ARG;
+  if (!scale || !dscale) return LBK_ERR_NULL;
+  if (N > 0 && (!x || !dy || !dx)) return LBK_ERR_NULL;
+  const size_t need = lbk_rmsnorm_bwd_workspace_bytes(N, d);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return LBK_ERR_WORKSPACE;
+  return launch_rmsnorm_bwd(x, dy, N, d, scale, eps, dx, dscale, static_cast<float*>(workspace), S(stream)) == 0
+             ? LBK_OK
+             : LBK_ERR_LAUNCH;
 }
 
 int lbk_diagonal_injection_bf16(const uint16_t* h, const uint16_t* e, const float* log_A, const float* log_dt,
@@ -284,23 +321,46 @@ size_t lbk_looped_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* ga
          (use_split(gate, up, down, d_model) ? packed_ffn_bytes(gate, up, down) : 0);
 }
 
+static int looped_persistent(const uint16_t* h_in, int64_t N, int32_t d_model, const float* norm_scale, float eps,
+                             int32_t L, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                             uint16_t* h_out, void* workspace, size_t workspace_bytes, void* stream, Biases bs);
+static int looped_launches(const uint16_t* h_in, int64_t N, int32_t d_model, const float* norm_scale, float eps,
+                           int32_t L, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                           uint16_t* h_out, void* workspace, size_t workspace_bytes, void* stream, Biases bs);
+
 int lbk_looped_swiglu_bf16(const uint16_t* h_in, int64_t N, int32_t d_model, const float* norm_scale, float eps,
                            int32_t L, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
                            uint16_t* h_out, void* workspace, size_t workspace_bytes, void* stream) {
+  return lbk_looped_swiglu_bias_bf16(h_in, N, d_model, norm_scale, eps, L, gate, up, down, nullptr, nullptr, nullptr,
+                                     h_out, workspace, workspace_bytes, stream);
+}
+
+int lbk_looped_swiglu_bias_bf16(const uint16_t* h_in, int64_t N, int32_t d_model, const float* norm_scale,
+                                float eps, int32_t L, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                                const float* b_gate, const float* b_up, const float* b_down, uint16_t* h_out,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  const Biases bs{b_gate, b_up, b_down};
   // the persistent launch where it takes the shape (measured faster at the looped-block
   // geometry), the per-iteration launches otherwise
   if (gate && up && down && norm_scale && a16(norm_scale) &&
       looped_persistent_supported(gate->B, d_model, gate->R, down->R, gate->K, up->K, down->K))
-    return lbk_looped_swiglu_persistent_bf16(h_in, N, d_model, norm_scale, eps, L, gate, up, down, h_out, workspace,
-                                             workspace_bytes, stream);
-  return lbk_looped_swiglu_launches_bf16(h_in, N, d_model, norm_scale, eps, L, gate, up, down, h_out, workspace,
-                                         workspace_bytes, stream);
+    return looped_persistent(h_in, N, d_model, norm_scale, eps, L, gate, up, down, h_out, workspace, workspace_bytes,
+                             stream, bs);
+  return looped_launches(h_in, N, d_model, norm_scale, eps, L, gate, up, down, h_out, workspace, workspace_bytes,
+                         stream, bs);
 }
 
 int lbk_looped_swiglu_launches_bf16(const uint16_t* h_in, int64_t N, int32_t d_model, const float* norm_scale,
                                     float eps, int32_t L, const lbk_bell* gate, const lbk_bell* up,
                                     const lbk_bell* down, uint16_t* h_out, void* workspace, size_t workspace_bytes,
                                     void* stream) {
+  return looped_launches(h_in, N, d_model, norm_scale, eps, L, gate, up, down, h_out, workspace, workspace_bytes,
+                         stream, Biases{});
+}
+
+static int looped_launches(const uint16_t* h_in, int64_t N, int32_t d_model, const float* norm_scale, float eps,
+                           int32_t L, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                           uint16_t* h_out, void* workspace, size_t workspace_bytes, void* stream, Biases bs) {
   int st;
   if ((st = check_bell(gate)) || (st = check_bell(up)) || (st = check_bell(down))) return st;
   int64_t d_ff = 0;
@@ -331,7 +391,7 @@ int lbk_looped_swiglu_launches_bf16(const uint16_t* h_in, int64_t N, int32_t d_m
     if (launch_bf16_to_f32(h_in, N * d_model, state, s) != 0) return LBK_ERR_LAUNCH;
     for (int l = 0; l < L; ++l)
       if ((st = swiglu_split(nullptr, state, norm_scale, eps, N, d_model, gate, up, down, pk, nullptr, state,
-                             l == L - 1 ? h_out : nullptr, h, nullptr, nullptr, s)))
+                             l == L - 1 ? h_out : nullptr, h, nullptr, nullptr, s, bs)))
         return st;
     return LBK_OK;
   }
@@ -339,7 +399,7 @@ int lbk_looped_swiglu_launches_bf16(const uint16_t* h_in, int64_t N, int32_t d_m
   const uint16_t* cur = h_in;
   for (int l = 0; l < L; ++l) {
     if (launch_rmsnorm(cur, N, d_model, norm_scale, eps, normed, s) != 0) return LBK_ERR_LAUNCH;
-    if ((st = swiglu_general(normed, N, d_model, gate, up, down, cur, h_out, h, nullptr, nullptr, s))) return st;
+    if ((st = swiglu_general(normed, N, d_model, gate, up, down, cur, h_out, h, nullptr, nullptr, s, bs))) return st;
     cur = h_out;
   }
   return LBK_OK;
@@ -349,6 +409,13 @@ int lbk_looped_swiglu_persistent_bf16(const uint16_t* h_in, int64_t N, int32_t d
                                       float eps, int32_t L, const lbk_bell* gate, const lbk_bell* up,
                                       const lbk_bell* down, uint16_t* h_out, void* workspace,
                                       size_t workspace_bytes, void* stream) {
+  return looped_persistent(h_in, N, d_model, norm_scale, eps, L, gate, up, down, h_out, workspace, workspace_bytes,
+                           stream, Biases{});
+}
+
+static int looped_persistent(const uint16_t* h_in, int64_t N, int32_t d_model, const float* norm_scale, float eps,
+                             int32_t L, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                             uint16_t* h_out, void* workspace, size_t workspace_bytes, void* stream, Biases bs) {
   int st;
   if ((st = check_bell(gate)) || (st = check_bell(up)) || (st = check_bell(down))) return st;
   int64_t d_ff = 0;
@@ -378,10 +445,10 @@ int lbk_looped_swiglu_persistent_bf16(const uint16_t* h_in, int64_t N, int32_t d
   la.gu.xf = state; la.gu.N = N; la.gu.d_model = d_model; la.gu.norm_scale = norm_scale; la.gu.eps = eps;
   la.gu.pg = pk.g; la.gu.cg = gate->col_idx; la.gu.Kg = gate->K;
   la.gu.pu = pk.u; la.gu.cu = up->col_idx; la.gu.Ku = up->K;
-  la.gu.R_ff = gate->R; la.gu.h = h;
+  la.gu.R_ff = gate->R; la.gu.h = h; la.gu.bg = bs.g; la.gu.bu = bs.u;
   la.dn.h = h; la.dn.N = N; la.dn.d_ff = d_ff; la.dn.d_model = d_model;
   la.dn.pd = pk.d; la.dn.cd = down->col_idx; la.dn.Kd = down->K;
-  la.dn.R_m = down->R; la.dn.C_d = gate->R; la.dn.state = state; la.dn.out = h_out;
+  la.dn.R_m = down->R; la.dn.C_d = gate->R; la.dn.state = state; la.dn.out = h_out; la.dn.bd = bs.d;
   la.h_in = h_in; la.L = L;
   // h_out may alias h_in: the kernel reads a token block's h_in rows before any write to them
   return launch_looped(gate->B, la, s) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
@@ -553,11 +620,31 @@ size_t lbk_swiglu_bwd_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell
          2 * align256((size_t)N * d_ff * 2) + align256((size_t)dw_chunks(N) * tiles * B * B * 4);
 }
 
+size_t lbk_swiglu_bwd_bias_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
+                                           const lbk_bell* down) {
+  const size_t base = lbk_swiglu_bwd_workspace_bytes(N, d_model, gate, up, down);
+  if (!base) return 0;
+  const int64_t d_ff = (int64_t)gate->R * gate->B;
+  return base + align256(colsum_bytes(N, (int)(d_ff > d_model ? d_ff : d_model)));
+}
+
 int lbk_swiglu_bwd_bf16(const uint16_t* grad_out, const uint16_t* x, const uint16_t* gate_pre_act,
                         const uint16_t* up_output, const uint16_t* h, int64_t N, int32_t d_model,
                         const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, int add_residual,
                         uint16_t* dx, uint16_t* d_gate_values, uint16_t* d_up_values, uint16_t* d_down_values,
                         void* workspace, size_t workspace_bytes, void* stream) {
+  return lbk_swiglu_bwd_bias_bf16(grad_out, x, gate_pre_act, up_output, h, N, d_model, gate, up, down, add_residual,
+                                  dx, d_gate_values, d_up_values, d_down_values, nullptr, nullptr, nullptr,
+                                  workspace, workspace_bytes, stream);
+}
+
+int lbk_swiglu_bwd_bias_bf16(const uint16_t* grad_out, const uint16_t* x, const uint16_t* gate_pre_act,
+                             const uint16_t* up_output, const uint16_t* h, int64_t N, int32_t d_model,
+                             const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, int add_residual,
+                             uint16_t* dx, uint16_t* d_gate_values, uint16_t* d_up_values,
+                             uint16_t* d_down_values, float* d_b_gate, float* d_b_up, float* d_b_down,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  const bool want_db = d_b_gate || d_b_up || d_b_down;
   int st;
   if ((st = check_bell(gate)) || (st = check_bell(up)) || (st = check_bell(down))) return st;
   int64_t d_ff = 0;
@@ -577,7 +664,8 @@ int lbk_swiglu_bwd_bf16(const uint16_t* grad_out, const uint16_t* x, const uint1
   }
   for (const lbk_bell* w : {gate, up, down})
     if ((int64_t)w->R * w->K > 0 && !a16(w->values)) return LBK_ERR_ALIGN;
-  const size_t need = lbk_swiglu_bwd_workspace_bytes(N, d_model, gate, up, down);
+  const size_t need = want_db ? lbk_swiglu_bwd_bias_workspace_bytes(N, d_model, gate, up, down)
+                              : lbk_swiglu_bwd_workspace_bytes(N, d_model, gate, up, down);
   if (!workspace || workspace_bytes < need) return LBK_ERR_WORKSPACE;
   if (!a16(workspace)) return LBK_ERR_ALIGN;
   hipStream_t s = S(stream);
@@ -638,6 +726,14 @@ int lbk_swiglu_bwd_bf16(const uint16_t* grad_out, const uint16_t* x, const uint1
   add(x, d_model, du, d_ff, up, C_in, d_up_values);
   add(h, d_ff, grad_out, d_model, down, C_d, d_down_values);
   if (nj && launch_dw(B, dj, nj, N, DW_CHUNK, s)) return LBK_ERR_LAUNCH;
+  // bias gradients: column sums of dg, du and grad_out (the partials after the tile partials)
+  if (want_db) {
+    float* cpart = reinterpret_cast<float*>(reinterpret_cast<char*>(part) + align256((size_t)nch * (
+        (size_t)gate->R * gate->K + (size_t)up->R * up->K + (size_t)down->R * down->K) * B * B * 4));
+    if (d_b_gate && launch_colsum(dg, N, (int)d_ff, d_ff, cpart, d_b_gate, s)) return LBK_ERR_LAUNCH;
+    if (d_b_up && launch_colsum(du, N, (int)d_ff, d_ff, cpart, d_b_up, s)) return LBK_ERR_LAUNCH;
+    if (d_b_down && launch_colsum(grad_out, N, d_model, d_model, cpart, d_b_down, s)) return LBK_ERR_LAUNCH;
+  }
   return LBK_OK;
 }
 

@@ -8,8 +8,8 @@
 //    memory (16-byte loads of the gathered column block), weight fragments from
 //    transposing loads.  Works for any geometry (B in {16,32,64}, any K, dead
 //    slots, ragged N).  MODE selects the epilogue: plain product (+bias),
-//    gate/up with SiLU*mul (+ optional pre-activation outputs), or down
-//    projection (+ residual).
+//    gate/up with SiLU*mul (+ biases, + optional pre-activation outputs), or down
+//    projection (+ bias, + residual).
 //
 #include "lbk_device.h"
 #include "lbk_internal.h"
@@ -28,8 +28,10 @@ __global__ __launch_bounds__(256) void rowblock_kernel(
     const uint16_t* __restrict__ x, int64_t N, int64_t ldx, int C,
     const uint16_t* __restrict__ v0, const int32_t* __restrict__ c0, int K0,
     const uint16_t* __restrict__ v1, const int32_t* __restrict__ c1, int K1,
-    const float* __restrict__ bias, const uint16_t* __restrict__ resid, int64_t ldr,
-    uint16_t* __restrict__ y, int64_t ldy, uint16_t* __restrict__ aux0, uint16_t* __restrict__ aux1,
+    // resid and y may be the same buffer (the general looped path updates its state in place;
+    // each element is read before the thread that reads it writes it), so neither is restrict
+    const float* __restrict__ bias, const float* __restrict__ bias1, const uint16_t* resid, int64_t ldr,
+    uint16_t* y, int64_t ldy, uint16_t* __restrict__ aux0, uint16_t* __restrict__ aux1,
     int64_t ldaux) {
   constexpr int NKS = TileShape<B>::NKS, CW = TileShape<B>::CW;
   constexpr int NL = (MODE == MODE_GATEUP) ? 2 : 1;
@@ -83,8 +85,8 @@ __global__ __launch_bounds__(256) void rowblock_kernel(
       float gv[CW], uv[CW];
 #pragma unroll
       for (int m = 0; m < CW; ++m) {
-        gv[m] = acc[0][m][v];
-        uv[m] = acc[1][m][v];
+        gv[m] = acc[0][m][v] + (bias ? bias[ocol + m] : 0.f);
+        uv[m] = acc[1][m][v] + (bias1 ? bias1[ocol + m] : 0.f);
         o[m] = silu_f(gv[m]) * uv[m];
       }
       if (aux0) store_bf16<CW>(aux0 + t * ldaux + ocol, gv);
@@ -92,11 +94,9 @@ __global__ __launch_bounds__(256) void rowblock_kernel(
     } else {
 #pragma unroll
       for (int m = 0; m < CW; ++m) o[m] = acc[0][m][v];
-      if constexpr (MODE == MODE_LINEAR) {
-        if (bias) {
+      if (bias) {
 #pragma unroll
-          for (int m = 0; m < CW; ++m) o[m] += bias[ocol + m];
-        }
+        for (int m = 0; m < CW; ++m) o[m] += bias[ocol + m];
       }
       if constexpr (MODE == MODE_DOWN) {
         if (resid) {
@@ -134,9 +134,117 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
   for (int c = lane; c < d; c += 64) orow[c] = f2bf(bf2f(xr[c]) * rs * scale[c]);
 }
 
-__global__ __launch_bounds__(256) void injection_kernel(const uint16_t* __restrict__ h, const uint16_t* __restrict__ e,
+// Backward of out = x * rs * scale, rs = 1 / sqrt(mean(x^2) + eps), per row of length d:
+//   dx     = rs * scale * dy - x * rs^3 * mean(scale * dy * x)
+//   dscale = sum over rows of dy * x * rs
+// A workgroup owns RMS_BWD_ROWS consecutive rows: its four waves first reduce each row's
+// sum of squares and sum(scale * dy * x) (rows w, w + 4, ...), then every thread walks its
+// columns c = tid, tid + 256, ... over the rows, writing dx and keeping its dscale partial,
+// stored per workgroup ([gridDim, d] fp32) and summed over the workgroups in a fixed order by
+// rmsnorm_dscale_kernel: deterministic.
+constexpr int RMS_BWD_ROWS = 64;
+
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ dy, int64_t N, int d,
+                                                          const float* __restrict__ scale, float eps,
+                                                          uint16_t* __restrict__ dx, float* __restrict__ part) {
+  __shared__ float s_rs[RMS_BWD_ROWS], s_coef[RMS_BWD_ROWS];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t r0 = (int64_t)blockIdx.x * RMS_BWD_ROWS;
+  const int nrows = (int)(N - r0 < RMS_BWD_ROWS ? N - r0 : RMS_BWD_ROWS);
+  for (int rr = w; rr < nrows; rr += 4) {
+    const uint16_t* xr = x + (r0 + rr) * d;
+    const uint16_t* gr = dy + (r0 + rr) * d;
+    float ss = 0.f, dot = 0.f;
+    for (int c = lane; c < d; c += 64) {
+      const float xv = bf2f(xr[c]);
+      ss += xv * xv;
+      dot += scale[c] * bf2f(gr[c]) * xv;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      ss += __shfl_xor(ss, o, 64);
+      dot += __shfl_xor(dot, o, 64);
+    }
+    if (lane == 0) {
+      const float rs = 1.0f / sqrtf(ss / (float)d + eps);
+      s_rs[rr] = rs;
+      s_coef[rr] = rs * rs * rs * (dot / (float)d);
+    }
+  }
+  __syncthreads();
+  for (int c = tid; c < d; c += 256) {
+    const float sc = scale[c];
+    float ds = 0.f;
+    for (int rr = 0; rr < nrows; ++rr) {
+      const int64_t off = (r0 + rr) * d + c;
+      const float xv = bf2f(x[off]), gv = bf2f(dy[off]);
+      const float rs = s_rs[rr];
+      dx[off] = f2bf(rs * sc * gv - xv * s_coef[rr]);
+      ds += gv * xv * rs;
+    }
+    part[(int64_t)blockIdx.x * d + c] = ds;
+  }
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_dscale_kernel(const float* __restrict__ part, int nblk, int d,
+                                                             float* __restrict__ dscale) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= d) return;
+  float s = 0.f;
+  for (int b = 0; b < nblk; ++b) s += part[(int64_t)b * d + c];
+  dscale[c] = s;
+}
+
+// Column sums of a bf16 matrix [N, C] (row stride lda) in fp32 (bias gradients): workgroup b
+// sums rows [64 b, 64 b + 64) of its columns c = tid, tid + 256, ... into part[b, c], then
+// rmsnorm_dscale_kernel sums the workgroups in order: deterministic.
+__global__ __launch_bounds__(256) void colsum_part_kernel(const uint16_t* __restrict__ a, int64_t N, int C,
+                                                          int64_t lda, float* __restrict__ part) {
+  const int64_t r0 = (int64_t)blockIdx.x * RMS_BWD_ROWS;
+  const int nrows = (int)(N - r0 < RMS_BWD_ROWS ? N - r0 : RMS_BWD_ROWS);
+  for (int c = threadIdx.x; c < C; c += 256) {
+    float s = 0.f;
+    for (int rr = 0; rr < nrows; ++rr) s += bf2f(a[(r0 + rr) * lda + c]);
+    part[(int64_t)blockIdx.x * C + c] = s;
+  }
+}
+
+size_t colsum_bytes(int64_t N, int C) { return (size_t)((N + RMS_BWD_ROWS - 1) / RMS_BWD_ROWS) * (size_t)C * 4; }
+
+int launch_colsum(const uint16_t* a, int64_t N, int C, int64_t lda, float* part, float* out, hipStream_t st) {
+  const int64_t nblk = (N + RMS_BWD_ROWS - 1) / RMS_BWD_ROWS;
+  if (nblk > 0x7fffffff || C <= 0) return -2;
+  if (nblk > 0) {
+    hipLaunchKernelGGL(colsum_part_kernel, dim3((unsigned)nblk), dim3(256), 0, st, a, N, C, lda, part);
+    if (hipGetLastError() != hipSuccess) return -1;
+  }
+  hipLaunchKernelGGL(rmsnorm_dscale_kernel, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, st, part, (int)nblk, C,
+                     out);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+size_t rmsnorm_bwd_bytes(int64_t N, int d) {
+  return (size_t)((N + RMS_BWD_ROWS - 1) / RMS_BWD_ROWS) * (size_t)d * 4;
+}
+
+int launch_rmsnorm_bwd(const uint16_t* x, const uint16_t* dy, int64_t N, int d, const float* scale, float eps,
+                       uint16_t* dx, float* dscale, float* part, hipStream_t st) {
+  const int64_t nblk = (N + RMS_BWD_ROWS - 1) / RMS_BWD_ROWS;
+  if (nblk > 0x7fffffff) return -2;
+  if (nblk > 0) {
+    hipLaunchKernelGGL(rmsnorm_bwd_kernel, dim3((unsigned)nblk), dim3(256), 0, st, x, dy, N, d, scale, eps, dx, part);
+    if (hipGetLastError() != hipSuccess) return -1;
+  }
+  hipLaunchKernelGGL(rmsnorm_dscale_kernel, dim3((unsigned)((d + 255) / 256)), dim3(256), 0, st, part, (int)nblk, d,
+                     dscale);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// out may alias h (lbk_diagonal_injection_bf16 allows it): neither is restrict
+__global__ __launch_bounds__(256) void injection_kernel(const uint16_t* h, const uint16_t* __restrict__ e,
                                                         const float* __restrict__ log_A, const float* __restrict__ log_dt,
-                                                        int64_t total, int d, uint16_t* __restrict__ out) {
+                                                        int64_t total, int d, uint16_t* out) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= total) return;
   const int c = (int)(idx % d);
@@ -154,7 +262,7 @@ template <int B, int MODE>
 static int launch_rowblock_t(const RowblockLaunch& a, hipStream_t st) {
   dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)a.R);
   hipLaunchKernelGGL((rowblock_kernel<B, MODE>), grid, dim3(256), 0, st, a.x, a.N, a.ldx, a.C, a.v0, a.c0, a.K0,
-                     a.v1, a.c1, a.K1, a.bias, a.resid, a.ldr, a.y, a.ldy, a.aux0, a.aux1, a.ldaux);
+                     a.v1, a.c1, a.K1, a.bias, a.bias1, a.resid, a.ldr, a.y, a.ldy, a.aux0, a.aux1, a.ldaux);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

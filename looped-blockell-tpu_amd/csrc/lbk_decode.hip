@@ -190,10 +190,11 @@ __global__ __launch_bounds__(512, 1) void decode_gu_kernel(DecodeArgs a) {
       us += red[4 + ww][m][l];
     }
     const int col = r * B + CW * (l & 15) + m;
+    const float bgc = a.bg ? a.bg[col] : 0.f, buc = a.bu ? a.bu[col] : 0.f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int tk = 4 * (l >> 4) + v;
-      if (tk < a.N) a.h[(int64_t)tk * d_ff + col] = f2bf(silu_f(gs[v]) * us[v]);
+      if (tk < a.N) a.h[(int64_t)tk * d_ff + col] = f2bf(silu_f(gs[v] + bgc) * (us[v] + buc));
     }
   }
   if (pf == 0x9e3779b9u && a.N < 0) a.h[0] = 0;                 // never true: keeps the loads
@@ -279,7 +280,7 @@ __global__ __launch_bounds__(512, 1) void decode_dn_kernel(DecodeArgs a) {
     for (int v = 0; v < 4; ++v) {
       const int tk = 4 * (l >> 4) + v;
       if (tk < a.N) {
-        float o = ps[v];
+        float o = ps[v] + (a.bd ? a.bd[col] : 0.f);
         if (a.resid) o += bf2f(a.resid[(int64_t)tk * a.d_model + col]);
         a.out[(int64_t)tk * a.d_model + col] = f2bf(o);
       }

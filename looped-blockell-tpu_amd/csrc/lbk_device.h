@@ -1,7 +1,7 @@
 // lbk_device.h — device-side building blocks shared by the gfx950 kernels.
 //
-// MFMA fragment conventions (v_mfma_f32_16x16x32_bf16, checked on the GPU by
-// tests/test_gpu_lanes.py):
+// MFMA fragment conventions (v_mfma_f32_16x16x32_bf16; every kernel's GPU parity test
+// exercises them end to end):
 //   A (16 x 32, M x K): lane l holds row l%16, k = 8*(l/16) .. +7  (8 bf16)
 //   B (32 x 16, K x N): lane l holds col l%16, k = 8*(l/16) .. +7
 //   C (16 x 16):        lane l holds col l%16, rows 4*(l/16) + v, v = 0..3

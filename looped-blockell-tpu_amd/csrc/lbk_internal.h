@@ -16,7 +16,8 @@ struct RowblockLaunch {
   int R;               // block rows (output features / B)
   const uint16_t* v0; const int32_t* c0; int K0;   // weight (gate for MODE 1)
   const uint16_t* v1; const int32_t* c1; int K1;   // up weight (MODE 1 only)
-  const float* bias;                                // MODE 0, optional
+  const float* bias;                                // optional: the product's (MODE 0, 2) or gate's (MODE 1)
+  const float* bias1;                               // optional: up's bias (MODE 1)
   const uint16_t* resid; int64_t ldr;              // MODE 2, optional
   uint16_t* y; int64_t ldy;
   uint16_t* aux0; uint16_t* aux1; int64_t ldaux;    // MODE 1 optional pre-activations
@@ -70,6 +71,7 @@ struct GUArgs {
   uint16_t* h;              // [N, d_ff] silu(g) * u
   uint16_t* gpre;           // [N, d_ff] optional gate pre-activation
   uint16_t* uout;           // [N, d_ff] optional up output
+  const float* bg; const float* bu;   // optional [d_ff] gate / up biases (added before SiLU*mul)
 };
 struct DNArgs {
   const uint16_t* h;        // [N, d_ff]
@@ -83,6 +85,7 @@ struct DNArgs {
   float* state;             // optional fp32 state [N, d_model]: read as residual, written back
   uint16_t* out;            // optional bf16 output [N, d_model]
   int nrg;                  // row groups per token block (set by the launcher)
+  const float* bd;          // optional [d_model] down bias
 };
 bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd);
 // looped block in one launch: gate/up (RMSNorm of the fp32 state) and down per token block
@@ -110,12 +113,19 @@ struct DecodeArgs {
   const uint16_t* resid;     // optional [N, d_model]
   uint16_t* out;             // [N, d_model]
   uint16_t* h;               // [N, d_ff] workspace (or the caller's h)
+  const float* bg; const float* bu; const float* bd;   // optional biases
 };
 bool decode_supported(int Kg, int Ku, int Kd);
 int launch_decode(int B, const DecodeArgs& a, hipStream_t st);
 
 int launch_rmsnorm(const uint16_t* x, int64_t N, int d, const float* scale, float eps, uint16_t* out,
                    hipStream_t st);
+size_t rmsnorm_bwd_bytes(int64_t N, int d);   // fp32 dscale partials of the workgroups
+// fp32 column sums out[C] of a bf16 [N, C] matrix (deterministic: per-64-row partials in part)
+size_t colsum_bytes(int64_t N, int C);
+int launch_colsum(const uint16_t* a, int64_t N, int C, int64_t lda, float* part, float* out, hipStream_t st);
+int launch_rmsnorm_bwd(const uint16_t* x, const uint16_t* dy, int64_t N, int d, const float* scale, float eps,
+                       uint16_t* dx, float* dscale, float* part, hipStream_t st);
 int launch_injection(const uint16_t* h, const uint16_t* e, const float* log_A, const float* log_dt, int64_t N,
                      int d, uint16_t* out, hipStream_t st);
 

@@ -321,6 +321,13 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
     // 4 * CW consecutive columns it holds of one token with one store
     const int r = w + 8 * n;
     const int64_t col0 = (int64_t)r * B + 4 * CW * g;
+    // biases of this lane's 4 * CW columns (zero without)
+    float bgv[4 * CW], buv[4 * CW];
+#pragma unroll
+    for (int q = 0; q < 4 * CW; ++q) {
+      bgv[q] = a.bg ? a.bg[col0 + q] : 0.f;
+      buv[q] = a.bu ? a.bu[col0 + q] : 0.f;
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int64_t t = t0 + 16 * mt + i;
@@ -329,8 +336,8 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
       for (int m = 0; m < CW; ++m)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          gv[4 * m + v] = ag[mt][m][v];
-          uv[4 * m + v] = au[mt][m][v];
+          gv[4 * m + v] = ag[mt][m][v] + bgv[4 * m + v];
+          uv[4 * m + v] = au[mt][m][v] + buv[4 * m + v];
           o[4 * m + v] = silu_f(gv[4 * m + v]) * uv[4 * m + v];
         }
       if (t < a.N) {
@@ -612,7 +619,7 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
           float o[CW];
 #pragma unroll
           for (int m = 0; m < CW; ++m) {
-            o[m] = acc[rho][mt][m][v] + (ok ? a.state[off + m] : 0.f);
+            o[m] = ok ? acc[rho][mt][m][v] + (a.bd ? a.bd[rm * B + CW * i + m] : 0.f) + a.state[off + m] : 0.f;
             acc[rho][mt][m][v] = o[m];
             ssq[mt][v] += o[m] * o[m];
           }
@@ -679,7 +686,7 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
         const int64_t off = t * d_model + rm * B + CW * i;
         float o[CW];
 #pragma unroll
-        for (int m = 0; m < CW; ++m) o[m] = acc[rho][mt][m][v];
+        for (int m = 0; m < CW; ++m) o[m] = acc[rho][mt][m][v] + (a.bd ? a.bd[rm * B + CW * i + m] : 0.f);
         if (a.state) {
 #pragma unroll
           for (int m = 0; m < CW; ++m) {

@@ -12,6 +12,7 @@
 #include <ATen/ATen.h>
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <torch/csrc/autograd/autograd_not_implemented_fallback.h>
 #include <torch/library.h>
 
 #include <vector>
@@ -85,10 +86,24 @@ at::Tensor workspace(size_t bytes, const at::Tensor& like) {
 }
 
 // ------------------------------------------------------------------ bf16 SwiGLU
+// optional fp32 bias of `n` elements on x's device (made contiguous), or undefined
+at::Tensor opt_bias(const c10::optional<at::Tensor>& b, int64_t n, const at::Tensor& x, const char* op,
+                    const char* name) {
+  if (!b.has_value() || !b->defined()) return at::Tensor();
+  check_gpu(*b, op, name);
+  TORCH_CHECK(b->numel() == n, "titan::", op, ": ", name, " must have ", n, " elements, got ", b->numel());
+  return b->to(x.device(), at::kFloat).contiguous();
+}
+const float* fptr(const at::Tensor& t) { return t.defined() ? t.data_ptr<float>() : nullptr; }
+
 std::vector<at::Tensor> swiglu_impl(const at::Tensor& x_, at::Tensor vg, at::Tensor cg, at::Tensor vu,
                                     at::Tensor cu, at::Tensor vd, at::Tensor cd, bool add_residual,
-                                    bool intermediates) {
-  const char* op = intermediates ? "block_ell_swiglu_fwd_with_intermediate" : "block_ell_swiglu_fwd";
+                                    bool intermediates, const c10::optional<at::Tensor>& bg_ = c10::nullopt,
+                                    const c10::optional<at::Tensor>& bu_ = c10::nullopt,
+                                    const c10::optional<at::Tensor>& bd_ = c10::nullopt,
+                                    const char* opname = nullptr) {
+  const char* op = opname ? opname
+                          : (intermediates ? "block_ell_swiglu_fwd_with_intermediate" : "block_ell_swiglu_fwd");
   at::Tensor x = check_x2d(x_, op);
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
   lbk_bell g = make_bell(vg, cg, op, "gate"), u = make_bell(vu, cu, op, "up"), d = make_bell(vd, cd, op, "down");
@@ -110,12 +125,30 @@ std::vector<at::Tensor> swiglu_impl(const at::Tensor& x_, at::Tensor vg, at::Ten
     res.push_back(tg);
     res.push_back(tu);
   }
+  const at::Tensor bg = opt_bias(bg_, d_ff, x, op, "b_gate"), bu = opt_bias(bu_, d_ff, x, op, "b_up"),
+                   bd = opt_bias(bd_, d_model, x, op, "b_down");
   const size_t wsb = lbk_swiglu_workspace_bytes(N, (int32_t)d_model, &g, &u, &d, intermediates ? 1 : 0);
   at::Tensor ws = wsb ? workspace(wsb, x) : at::Tensor();
   LBK_CALL("block_ell_swiglu_fwd",
-           lbk_swiglu_fwd_bf16(bf(x), N, (int32_t)d_model, &g, &u, &d, add_residual ? 1 : 0, bfm(out), h, gp, uo,
-                               wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(x)));
+           lbk_swiglu_fwd_bias_bf16(bf(x), N, (int32_t)d_model, &g, &u, &d, fptr(bg), fptr(bu), fptr(bd),
+                                    add_residual ? 1 : 0, bfm(out), h, gp, uo, wsb ? ws.data_ptr() : nullptr, wsb,
+                                    cur_stream(x)));
   return res;
+}
+
+// SwiGLU with the projections' biases: (out, h, gate_pre_act, up_out); the intermediates are
+// empty tensors unless asked for
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> swiglu_fwd_bias(
+    const at::Tensor& x, const at::Tensor& vg, const at::Tensor& cg, const c10::optional<at::Tensor>& bg,
+    const at::Tensor& vu, const at::Tensor& cu, const c10::optional<at::Tensor>& bu, const at::Tensor& vd,
+    const at::Tensor& cd, const c10::optional<at::Tensor>& bd, bool add_residual, bool intermediates) {
+  auto r = swiglu_impl(x, vg, cg, vu, cu, vd, cd, add_residual, intermediates, bg, bu, bd,
+                       "block_ell_swiglu_fwd_bias");
+  if (!intermediates) {
+    at::Tensor e = at::empty({0}, x.options());
+    return {r[0], e, e, e};
+  }
+  return {r[0], r[1], r[2], r[3]};
 }
 
 at::Tensor swiglu_fwd(const at::Tensor& x, const at::Tensor& vg, const at::Tensor& cg, const at::Tensor& vu,
@@ -187,6 +220,24 @@ at::Tensor rmsnorm(const at::Tensor& x_, const at::Tensor& scale_, double eps) {
   return out;
 }
 
+std::tuple<at::Tensor, at::Tensor> rmsnorm_bwd(const at::Tensor& dy_, const at::Tensor& x_, const at::Tensor& scale_,
+                                               double eps) {
+  at::Tensor x = check_x2d(x_, "rmsnorm_bwd");
+  at::Tensor dy = check_x2d(dy_, "rmsnorm_bwd");
+  TORCH_CHECK(dy.sizes() == x.sizes(), "titan::rmsnorm_bwd: grad_out must match x");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  at::Tensor s = scale_.to(x.device(), at::kFloat).contiguous();
+  TORCH_CHECK(s.numel() == x.size(1), "titan::rmsnorm_bwd: scale must have d elements");
+  at::Tensor dx = at::empty_like(x);
+  at::Tensor ds = at::empty({x.size(1)}, x.options().dtype(at::kFloat));
+  const size_t wsb = lbk_rmsnorm_bwd_workspace_bytes(x.size(0), (int32_t)x.size(1));
+  at::Tensor ws = workspace(wsb, x);
+  LBK_CALL("rmsnorm_bwd", lbk_rmsnorm_bwd_bf16(bf(x), bf(dy), x.size(0), (int32_t)x.size(1), s.data_ptr<float>(),
+                                               (float)eps, bfm(dx), ds.data_ptr<float>(), ws.data_ptr(), wsb,
+                                               cur_stream(x)));
+  return {dx, ds};
+}
+
 at::Tensor diagonal_injection(const at::Tensor& h_, const at::Tensor& e_, const at::Tensor& log_A,
                               const at::Tensor& log_dt) {
   at::Tensor h = check_x2d(h_, "diagonal_injection");
@@ -218,6 +269,31 @@ at::Tensor looped_impl(const at::Tensor& h, const at::Tensor& scale_, at::Tensor
                       : (path == 2 ? lbk_looped_swiglu_launches_bf16 : lbk_looped_swiglu_bf16);
   LBK_CALL("looped_swiglu", fn(bf(x), x.size(0), (int32_t)x.size(1), s.data_ptr<float>(), (float)eps, (int32_t)L,
                                &g, &u, &d, bfm(out), wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(x)));
+  return out;
+}
+
+at::Tensor looped_swiglu_bias(const at::Tensor& h_, const at::Tensor& scale_, const at::Tensor& vg_,
+                              const at::Tensor& cg_, const c10::optional<at::Tensor>& bg_, const at::Tensor& vu_,
+                              const at::Tensor& cu_, const c10::optional<at::Tensor>& bu_, const at::Tensor& vd_,
+                              const at::Tensor& cd_, const c10::optional<at::Tensor>& bd_, int64_t L, double eps) {
+  const char* op = "looped_swiglu_bias";
+  at::Tensor x = check_x2d(h_, op);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  at::Tensor vg = vg_, cg = cg_, vu = vu_, cu = cu_, vd = vd_, cd = cd_;
+  lbk_bell g = make_bell(vg, cg, op, "gate"), u = make_bell(vu, cu, op, "up"), d = make_bell(vd, cd, op, "down");
+  at::Tensor s = scale_.to(x.device(), at::kFloat).contiguous();
+  TORCH_CHECK(s.numel() == x.size(1), "titan::", op, ": norm scale must have d_model elements");
+  TORCH_CHECK(L >= 0, "titan::", op, ": L must be >= 0");
+  const int64_t d_ff = (int64_t)g.R * g.B;
+  const at::Tensor bg = opt_bias(bg_, d_ff, x, op, "b_gate"), bu = opt_bias(bu_, d_ff, x, op, "b_up"),
+                   bd = opt_bias(bd_, x.size(1), x, op, "b_down");
+  at::Tensor out = at::empty_like(x);
+  const size_t wsb = lbk_looped_workspace_bytes(x.size(0), (int32_t)x.size(1), &g, &u, &d);
+  at::Tensor ws = wsb ? workspace(wsb, x) : at::Tensor();
+  LBK_CALL("looped_swiglu_bias",
+           lbk_looped_swiglu_bias_bf16(bf(x), x.size(0), (int32_t)x.size(1), s.data_ptr<float>(), (float)eps,
+                                       (int32_t)L, &g, &u, &d, fptr(bg), fptr(bu), fptr(bd), bfm(out),
+                                       wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(x)));
   return out;
 }
 
@@ -453,6 +529,40 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> swiglu_bwd_impl(
   return {dx, dvg, dvu, dvd};
 }
 
+// backward with the bias gradients (fp32 column sums of dg, du and grad_out)
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> swiglu_bwd_bias(
+    const at::Tensor& dy_, const at::Tensor& x_, const at::Tensor& gp_, const at::Tensor& uo_, const at::Tensor& h_,
+    const at::Tensor& vg_, const at::Tensor& cg_, const at::Tensor& vu_, const at::Tensor& cu_, const at::Tensor& vd_,
+    const at::Tensor& cd_, bool add_residual) {
+  const char* op = "block_ell_swiglu_bwd_bias";
+  at::Tensor vg = vg_, cg = cg_, vu = vu_, cu = cu_, vd = vd_, cd = cd_;
+  at::Tensor x = check_x2d(x_, op);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  lbk_bell g = make_bell(vg, cg, op, "gate"), u = make_bell(vu, cu, op, "up"), d = make_bell(vd, cd, op, "down");
+  const int64_t N = x.size(0), d_model = x.size(1);
+  const int64_t d_ff = (int64_t)g.R * g.B;
+  auto act = [&](const at::Tensor& t, int64_t cols, const char* name) {
+    check_gpu(t, op, name);
+    TORCH_CHECK(t.scalar_type() == at::kBFloat16, "titan::", op, ": ", name, " must be bf16");
+    TORCH_CHECK(t.dim() == 2 && t.size(0) == N && t.size(1) == cols, "titan::", op, ": ", name, " must be [", N,
+                ", ", cols, "], got ", t.sizes());
+    return t.contiguous();
+  };
+  at::Tensor dy = act(dy_, d_model, "grad_out"), gp = act(gp_, d_ff, "gate_pre_act"),
+             uo = act(uo_, d_ff, "up_output"), h = act(h_, d_ff, "h");
+  at::Tensor dx = at::empty({N, d_model}, x.options());
+  at::Tensor dvg = at::empty_like(vg), dvu = at::empty_like(vu), dvd = at::empty_like(vd);
+  at::Tensor dbg = at::empty({d_ff}, x.options().dtype(at::kFloat)), dbu = at::empty({d_ff}, x.options().dtype(at::kFloat)),
+             dbd = at::empty({d_model}, x.options().dtype(at::kFloat));
+  const size_t wsb = lbk_swiglu_bwd_bias_workspace_bytes(N, (int32_t)d_model, &g, &u, &d);
+  at::Tensor ws = workspace(wsb, x);
+  LBK_CALL("block_ell_swiglu_bwd_bias",
+           lbk_swiglu_bwd_bias_bf16(bf(dy), bf(x), bf(gp), bf(uo), bf(h), N, (int32_t)d_model, &g, &u, &d,
+                                    add_residual ? 1 : 0, bfm(dx), bfm(dvg), bfm(dvu), bfm(dvd), dbg.data_ptr<float>(),
+                                    dbu.data_ptr<float>(), dbd.data_ptr<float>(), ws.data_ptr(), wsb, cur_stream(x)));
+  return {dx, dvg, dvu, dvd, dbg, dbu, dbd};
+}
+
 // the reference operator: dx always includes grad_out (the forward's residual)
 std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> swiglu_bwd(
     const at::Tensor& dy, const at::Tensor& x, const at::Tensor& gp, const at::Tensor& uo, const at::Tensor& h,
@@ -494,6 +604,15 @@ TORCH_LIBRARY(titan, m) {
   // ops beyond the reference's set
   m.def("block_ell_matmul(Tensor x, Tensor values, Tensor col_indices, Tensor? bias=None) -> Tensor");
   m.def("block_ell_matmul_bwd(Tensor grad_out, Tensor x, Tensor values, Tensor col_indices) -> (Tensor, Tensor)");
+  m.def("block_ell_swiglu_fwd_bias(Tensor x, Tensor v_gate, Tensor ci_gate, Tensor? b_gate, Tensor v_up, "
+        "Tensor ci_up, Tensor? b_up, Tensor v_down, Tensor ci_down, Tensor? b_down, bool add_residual, "
+        "bool intermediates=False) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("block_ell_swiglu_bwd_bias(Tensor grad_out, Tensor x, Tensor gate_pre_act, Tensor up_out, Tensor h, "
+        "Tensor v_gate, Tensor ci_gate, Tensor v_up, Tensor ci_up, Tensor v_down, Tensor ci_down, "
+        "bool add_residual) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
+  m.def("looped_swiglu_bias(Tensor h, Tensor norm_scale, Tensor v_gate, Tensor ci_gate, Tensor? b_gate, "
+        "Tensor v_up, Tensor ci_up, Tensor? b_up, Tensor v_down, Tensor ci_down, Tensor? b_down, int L, "
+        "float eps=1e-05) -> Tensor");
   m.def("block_ell_swiglu_bwd_ex(Tensor grad_out, Tensor x, Tensor gate_pre_act, Tensor up_out, Tensor h, "
         "Tensor v_gate, Tensor ci_gate, Tensor v_up, Tensor ci_up, Tensor v_down, Tensor ci_down, "
         "bool add_residual) -> (Tensor, Tensor, Tensor, Tensor)");
@@ -504,6 +623,7 @@ TORCH_LIBRARY(titan, m) {
   m.def("looped_swiglu_launches(Tensor h, Tensor norm_scale, Tensor v_gate, Tensor ci_gate, Tensor v_up, "
         "Tensor ci_up, Tensor v_down, Tensor ci_down, int L, float eps=1e-05) -> Tensor");
   m.def("rmsnorm(Tensor x, Tensor scale, float eps=1e-05) -> Tensor");
+  m.def("rmsnorm_bwd(Tensor grad_out, Tensor x, Tensor scale, float eps=1e-05) -> (Tensor, Tensor)");
   m.def("diagonal_injection(Tensor h, Tensor e, Tensor log_A, Tensor log_dt) -> Tensor");
   m.def("quantize_act_int8(Tensor x) -> (Tensor, Tensor)");
   m.def("pack_ternary(Tensor t) -> Tensor");
@@ -527,6 +647,9 @@ TORCH_LIBRARY_IMPL(titan, CUDA, m) {
   m.impl("block_ell_swiglu_fwd_with_intermediate", &swiglu_fwd_inter);
   m.impl("block_ell_swiglu_bwd", &swiglu_bwd);
   m.impl("block_ell_swiglu_bwd_ex", &swiglu_bwd_ex);
+  m.impl("block_ell_swiglu_fwd_bias", &swiglu_fwd_bias);
+  m.impl("block_ell_swiglu_bwd_bias", &swiglu_bwd_bias);
+  m.impl("looped_swiglu_bias", &looped_swiglu_bias);
   m.impl("pin_weights_l2", &pin_weights_l2);
   m.impl("persistent_mlp_step", &persistent_mlp_step);
   m.impl("block_ell_matmul", &block_ell_matmul);
@@ -535,6 +658,7 @@ TORCH_LIBRARY_IMPL(titan, CUDA, m) {
   m.impl("looped_swiglu_persistent", &looped_swiglu_persistent);
   m.impl("looped_swiglu_launches", &looped_swiglu_launches);
   m.impl("rmsnorm", &rmsnorm);
+  m.impl("rmsnorm_bwd", &rmsnorm_bwd);
   m.impl("diagonal_injection", &diagonal_injection);
   m.impl("quantize_act_int8", &quantize_act_int8);
   m.impl("pack_ternary", &pack_ternary);
@@ -547,6 +671,22 @@ TORCH_LIBRARY_IMPL(titan, CUDA, m) {
 }
 
 TORCH_LIBRARY_IMPL(titan, CompositeExplicitAutograd, m) { m.impl("unpin_weights_l2", &unpin_weights_l2); }
+
+// No operator here has an autograd formula of its own (the differentiable ones are wrapped by
+// torch.autograd.Function in looped_blockell.kernels, which call them with grad mode off).
+// Outputs of an op called on inputs that require grad get a node that raises on backward,
+// instead of silently carrying no gradient.
+TORCH_LIBRARY_IMPL(titan, Autograd, m) {
+  for (const char* name :
+       {"block_ell_swiglu_fwd", "block_ell_swiglu_fwd_with_intermediate", "block_ell_swiglu_bwd",
+        "persistent_mlp_step", "block_ell_matmul", "block_ell_matmul_bwd", "block_ell_swiglu_bwd_ex",
+        "looped_swiglu", "looped_swiglu_persistent", "looped_swiglu_launches", "rmsnorm", "rmsnorm_bwd",
+        "block_ell_swiglu_fwd_bias", "block_ell_swiglu_bwd_bias", "looped_swiglu_bias",
+        "diagonal_injection", "quantize_act_int8", "pack_ternary", "ternary_quantize_weights", "ternary_matmul",
+        "block_ell_swiglu_fwd_ternary", "block_ell_swiglu_fwd_ternary_with_intermediate",
+        "block_ell_swiglu_fwd_ternary_accumulators"})
+    m.impl(name, torch::autograd::autogradNotImplementedFallback());
+}
 
 // Meta (shape-only) implementations, as the reference provides for FakeTensor tracing
 // (csrc/block_ell/block_ell_ops.cpp:179-237, csrc/loop/loop_ops.cpp:125-156).
@@ -574,6 +714,28 @@ TORCH_LIBRARY_IMPL(titan, Meta, m) {
             const at::Tensor&, bool) {
            return std::make_tuple(at::empty_like(x), at::empty_like(vg), at::empty_like(vu), at::empty_like(vd));
          });
+  m.impl("block_ell_swiglu_fwd_bias",
+         [](const at::Tensor& x, const at::Tensor& vg, const at::Tensor&, const c10::optional<at::Tensor>&,
+            const at::Tensor&, const at::Tensor&, const c10::optional<at::Tensor>&, const at::Tensor&,
+            const at::Tensor&, const c10::optional<at::Tensor>&, bool, bool inter) {
+           const int64_t N = x.size(0), d_ff = vg.size(0) * vg.size(2);
+           auto mk = [&]() { return inter ? at::empty({N, d_ff}, x.options()) : at::empty({0}, x.options()); };
+           return std::make_tuple(at::empty_like(x), mk(), mk(), mk());
+         });
+  m.impl("block_ell_swiglu_bwd_bias",
+         [](const at::Tensor&, const at::Tensor& x, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+            const at::Tensor& vg, const at::Tensor&, const at::Tensor& vu, const at::Tensor&, const at::Tensor& vd,
+            const at::Tensor&, bool) {
+           const int64_t d_ff = vg.size(0) * vg.size(2);
+           auto f = x.options().dtype(at::kFloat);
+           return std::make_tuple(at::empty_like(x), at::empty_like(vg), at::empty_like(vu), at::empty_like(vd),
+                                  at::empty({d_ff}, f), at::empty({d_ff}, f), at::empty({x.size(1)}, f));
+         });
+  m.impl("looped_swiglu_bias",
+         [](const at::Tensor& h, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+            const c10::optional<at::Tensor>&, const at::Tensor&, const at::Tensor&, const c10::optional<at::Tensor>&,
+            const at::Tensor&, const at::Tensor&, const c10::optional<at::Tensor>&, int64_t,
+            double) { return at::empty_like(h); });
   m.impl("pin_weights_l2", [](at::TensorList) {});
   m.impl("persistent_mlp_step",
          [](const at::Tensor& h, const at::Tensor&, const at::Tensor&, const at::Tensor&, at::TensorList,
@@ -596,6 +758,9 @@ TORCH_LIBRARY_IMPL(titan, Meta, m) {
                              const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t,
                              double) { return at::empty_like(h); });
   m.impl("rmsnorm", [](const at::Tensor& x, const at::Tensor&, double) { return at::empty_like(x); });
+  m.impl("rmsnorm_bwd", [](const at::Tensor&, const at::Tensor& x, const at::Tensor&, double) {
+    return std::make_tuple(at::empty_like(x), at::empty({x.size(1)}, x.options().dtype(at::kFloat)));
+  });
   m.impl("diagonal_injection", [](const at::Tensor& h, const at::Tensor&, const at::Tensor&, const at::Tensor&) {
     return at::empty_like(h);
   });

@@ -78,13 +78,22 @@ SIGNATURES = {
     "lbk_swiglu_fwd_bf16": (C.c_int, [_P, _I64, _I32, _PB, _PB, _PB, C.c_int, _P, _P, _P, _P, _P, _SZ, _P]),
     "lbk_noalloc_scratch_bytes": (_SZ, []),
     "lbk_swiglu_fwd_bf16_noalloc": (C.c_int, [_P, _I64, _I32, _PB, _PB, _PB, C.c_int, _P, _P]),
+    "lbk_swiglu_fwd_bias_bf16": (C.c_int, [_P, _I64, _I32, _PB, _PB, _PB, _P, _P, _P, C.c_int, _P, _P, _P, _P, _P,
+                                           _SZ, _P]),
     "lbk_swiglu_bwd_workspace_bytes": (_SZ, [_I64, _I32, _PB, _PB, _PB]),
+    "lbk_swiglu_bwd_bias_workspace_bytes": (_SZ, [_I64, _I32, _PB, _PB, _PB]),
+    "lbk_swiglu_bwd_bias_bf16": (C.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _PB, _PB, _PB, C.c_int, _P, _P, _P, _P,
+                                           _P, _P, _P, _P, _SZ, _P]),
     "lbk_swiglu_bwd_bf16": (C.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _PB, _PB, _PB, C.c_int, _P, _P, _P, _P, _P,
                                       _SZ, _P]),
     "lbk_rmsnorm_bf16": (C.c_int, [_P, _I64, _I32, _P, _F, _P, _P]),
+    "lbk_rmsnorm_bwd_workspace_bytes": (_SZ, [_I64, _I32]),
+    "lbk_rmsnorm_bwd_bf16": (C.c_int, [_P, _P, _I64, _I32, _P, _F, _P, _P, _P, _SZ, _P]),
     "lbk_diagonal_injection_bf16": (C.c_int, [_P, _P, _P, _P, _I64, _I32, _P, _P]),
     "lbk_looped_workspace_bytes": (_SZ, [_I64, _I32, _PB, _PB, _PB]),
     "lbk_looped_swiglu_bf16": (C.c_int, [_P, _I64, _I32, _P, _F, _I32, _PB, _PB, _PB, _P, _P, _SZ, _P]),
+    "lbk_looped_swiglu_bias_bf16": (C.c_int, [_P, _I64, _I32, _P, _F, _I32, _PB, _PB, _PB, _P, _P, _P, _P, _P, _SZ,
+                                              _P]),
     "lbk_looped_swiglu_persistent_bf16": (C.c_int, [_P, _I64, _I32, _P, _F, _I32, _PB, _PB, _PB, _P, _P, _SZ,
                                                     _P]),
     "lbk_looped_swiglu_launches_bf16": (C.c_int, [_P, _I64, _I32, _P, _F, _I32, _PB, _PB, _PB, _P, _P, _SZ, _P]),

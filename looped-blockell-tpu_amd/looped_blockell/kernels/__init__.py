@@ -140,10 +140,46 @@ class _SwiGLUFunction(torch.autograd.Function):
         return dx, dvg, None, dvu, None, dvd, None, None
 
 
-def swiglu(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual: bool = False):
-    """SwiGLU FFN forward that autograd can differentiate (through ``titan::block_ell_swiglu_bwd``);
-    without gradients it is ``swiglu_fwd``."""
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (x, v_gate, v_up, v_down)):
+class _SwiGLUBiasFunction(torch.autograd.Function):
+    """Differentiable SwiGLU FFN with the projections' biases: forward
+    ``titan::block_ell_swiglu_fwd_bias``, backward ``titan::block_ell_swiglu_bwd_bias`` (tile and
+    bias gradients); the column indices get no gradient."""
+
+    @staticmethod
+    def forward(ctx, x, v_gate, ci_gate, b_gate, v_up, ci_up, b_up, v_down, ci_down, b_down, add_residual):
+        out, h, gp, uo = ops().block_ell_swiglu_fwd_bias(x, v_gate, ci_gate, b_gate, v_up, ci_up, b_up, v_down,
+                                                          ci_down, b_down, add_residual, True)
+        ctx.save_for_backward(x, h, gp, uo, v_gate, ci_gate, v_up, ci_up, v_down, ci_down)
+        ctx.add_residual = add_residual
+        ctx.bias_dtypes = tuple(b.dtype if b is not None else None for b in (b_gate, b_up, b_down))
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, h, gp, uo, vg, cg, vu, cu, vd, cd = ctx.saved_tensors
+        dx, dvg, dvu, dvd, dbg, dbu, dbd = ops().block_ell_swiglu_bwd_bias(
+            grad_out.to(torch.bfloat16).contiguous(), x, gp, uo, h, vg, cg, vu, cu, vd, cd, ctx.add_residual)
+        db = [d.to(t) if t is not None else None for d, t in zip((dbg, dbu, dbd), ctx.bias_dtypes)]
+        return dx, dvg, None, db[0], dvu, None, db[1], dvd, None, db[2], None
+
+
+def swiglu(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual: bool = False,
+           b_gate=None, b_up=None, b_down=None):
+    """SwiGLU FFN forward that autograd can differentiate (through ``titan::block_ell_swiglu_bwd``,
+    or ``..._bwd_bias`` with biases); without gradients it is ``swiglu_fwd`` (or
+    ``titan::block_ell_swiglu_fwd_bias``).  ``b_gate``/``b_up`` [d_ff] and ``b_down`` [d_model]
+    are optional biases of the three projections."""
+    biased = any(b is not None for b in (b_gate, b_up, b_down))
+    grad = torch.is_grad_enabled() and any(t is not None and t.requires_grad
+                                           for t in (x, v_gate, v_up, v_down, b_gate, b_up, b_down))
+    if biased:
+        _gpu(x, v_gate, v_down)
+        if grad:
+            return _SwiGLUBiasFunction.apply(x, v_gate, ci_gate, b_gate, v_up, ci_up, b_up, v_down, ci_down, b_down,
+                                             add_residual)
+        return ops().block_ell_swiglu_fwd_bias(x, v_gate, ci_gate, b_gate, v_up, ci_up, b_up, v_down, ci_down,
+                                               b_down, add_residual, False)[0]
+    if grad:
         return _SwiGLUFunction.apply(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual)
     return swiglu_fwd(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual)
 
@@ -153,6 +189,14 @@ def looped_swiglu(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, 
     persistent launch where the shape allows, per-iteration launches otherwise)."""
     _gpu(h, v_gate, v_down)
     return ops().looped_swiglu(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L, eps)
+
+
+def looped_swiglu_bias(h, norm_scale, v_gate, ci_gate, b_gate, v_up, ci_up, b_up, v_down, ci_down, b_down,
+                       L: int, eps: float = 1e-5):
+    """``looped_swiglu`` with the projections' (optional) biases, as ``swiglu``'s."""
+    _gpu(h, v_gate, v_down)
+    return ops().looped_swiglu_bias(h, norm_scale, v_gate, ci_gate, b_gate, v_up, ci_up, b_up, v_down, ci_down,
+                                    b_down, L, eps)
 
 
 def looped_swiglu_persistent(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L: int,
@@ -171,9 +215,36 @@ def looped_swiglu_launches(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, 
     return ops().looped_swiglu_launches(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L, eps)
 
 
+class _RMSNormFunction(torch.autograd.Function):
+    """Differentiable RMSNorm: the backward is ``titan::rmsnorm_bwd`` (dx and the scale gradient,
+    deterministic)."""
+
+    @staticmethod
+    def forward(ctx, x, scale, eps):
+        ctx.save_for_backward(x, scale)
+        ctx.eps = eps
+        return ops().rmsnorm(x, scale, eps)
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, scale = ctx.saved_tensors
+        dx, ds = ops().rmsnorm_bwd(gy.to(torch.bfloat16).contiguous(), x, scale, ctx.eps)
+        return dx, ds.to(scale.dtype), None
+
+
 def rmsnorm(x, scale, eps: float = 1e-5):
+    """``x / sqrt(mean(x^2) + eps) * scale`` over rows of a 2-D bf16 x; differentiable in x and
+    scale (``titan::rmsnorm_bwd``)."""
     _gpu(x)
+    if torch.is_grad_enabled() and (x.requires_grad or scale.requires_grad):
+        return _RMSNormFunction.apply(x, scale, eps)
     return ops().rmsnorm(x, scale, eps)
+
+
+def rmsnorm_bwd(grad_out, x, scale, eps: float = 1e-5):
+    """``titan::rmsnorm_bwd``: ``(dx bf16, dscale fp32)``."""
+    _gpu(grad_out, x)
+    return ops().rmsnorm_bwd(grad_out, x, scale, eps)
 
 
 def diagonal_injection(h, e, log_A, log_dt):

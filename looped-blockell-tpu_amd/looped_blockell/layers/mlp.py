@@ -9,10 +9,13 @@ Weight layout per projection:
   bias:        [out_features] parameter, zeros (BlockELLLinear only)
 
 ``MLPBlock(use_swiglu=True)`` runs the whole SwiGLU FFN as one fused HIP
-operator (``titan::block_ell_swiglu_fwd``, differentiable through
-``titan::block_ell_swiglu_bwd``); its projections carry no bias, as
-in the reference's PyTorch mirror (``interop/pt_model.py:865-867``) and its CUDA
-operator (``csrc/block_ell/swiglu_fwd.cuh:75-84``).
+operator (``titan::block_ell_swiglu_fwd_bias``, differentiable through
+``titan::block_ell_swiglu_bwd_bias``); each projection carries a zero-initialised
+trainable bias, as every ``BlockELLLinear`` of the reference's Flax module does
+(``mlp.py:56-60``, ``:82``), added in fp32 in the kernels' epilogues.  ``bias=False``
+gives the bias-free form of the reference's PyTorch mirror (``interop/pt_model.py:865-867``)
+and CUDA operator (``csrc/block_ell/swiglu_fwd.cuh:75-84``).  The GELU form uses the tanh
+approximation, ``jax.nn.gelu``'s default (``mlp.py:156``).
 """
 
 from __future__ import annotations
@@ -87,14 +90,15 @@ class MLPBlock(nn.Module):
     """
 
     def __init__(self, d_model: int, d_ff: int, use_swiglu: bool = False, dropout: float = 0.0,
-                 tile_size: int = 16, density: float = 1.0, dtype: torch.dtype = torch.bfloat16, device=None):
+                 tile_size: int = 16, density: float = 1.0, dtype: torch.dtype = torch.bfloat16, device=None,
+                 bias: bool = True):
         super().__init__()
         self.d_model, self.d_ff, self.use_swiglu, self.dropout = d_model, d_ff, use_swiglu, dropout
         kw = dict(tile_size=tile_size, density=density, dtype=dtype, device=device)
         if use_swiglu:
-            self.w_gate = BlockELLLinear(d_ff, d_model, bias=False, **kw)
-            self.w_up = BlockELLLinear(d_ff, d_model, bias=False, **kw)
-            self.w_down = BlockELLLinear(d_model, d_ff, bias=False, **kw)
+            self.w_gate = BlockELLLinear(d_ff, d_model, bias=bias, **kw)
+            self.w_up = BlockELLLinear(d_ff, d_model, bias=bias, **kw)
+            self.w_down = BlockELLLinear(d_model, d_ff, bias=bias, **kw)
         else:
             self.fc1 = BlockELLLinear(d_ff, d_model, **kw)
             self.fc2 = BlockELLLinear(d_model, d_ff, **kw)
@@ -115,13 +119,19 @@ class MLPBlock(nn.Module):
         return (self.w_gate.kernel_values(), cg, self.w_up.kernel_values(), cu,
                 self.w_down.kernel_values(), self.w_down.effective_col_indices())
 
+    def swiglu_biases(self):
+        """(b_gate, b_up, b_down): the projections' biases (None where a projection has none)."""
+        return self.w_gate.bias, self.w_up.bias, self.w_down.bias
+
     def forward(self, x: torch.Tensor, deterministic: bool = True) -> torch.Tensor:
         lead = x.shape[:-1]
         if self.use_swiglu:
             x2 = x.reshape(-1, self.d_model).to(torch.bfloat16).contiguous()
-            out = kernels.swiglu(x2, *self.swiglu_weights(), add_residual=False).reshape(*lead, self.d_model)
+            bg, bu, bd = self.swiglu_biases()
+            out = kernels.swiglu(x2, *self.swiglu_weights(), add_residual=False, b_gate=bg, b_up=bu,
+                                 b_down=bd).reshape(*lead, self.d_model)
         else:
-            out = self.fc2(F.gelu(self.fc1(x).float()).to(torch.bfloat16))
+            out = self.fc2(F.gelu(self.fc1(x).float(), approximate="tanh").to(torch.bfloat16))
         if self.dropout > 0.0 and not deterministic:
             out = F.dropout(out, p=self.dropout, training=True)
         return out

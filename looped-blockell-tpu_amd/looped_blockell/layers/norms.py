@@ -21,6 +21,7 @@ class RMSNorm(nn.Module):
         self.scale = nn.Parameter(torch.ones(dim, device=device))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """Differentiable in x and scale (``titan::rmsnorm_bwd``)."""
         lead = x.shape[:-1]
         y = kernels.rmsnorm(x.reshape(-1, x.shape[-1]).to(torch.bfloat16).contiguous(), self.scale, self.eps)
         return y.reshape(*lead, x.shape[-1])

@@ -30,7 +30,8 @@ __all__ = [
     "BlockELLConfig", "k_for_density", "random_topology", "dense_to_block_ell",
     "permute_optimizer_rows", "transposed_index",
     "block_ell_to_dense", "create_block_ell_from_dense", "block_ell_matmul",
-    "silu", "swiglu_fwd", "rmsnorm", "looped_swiglu", "block_ell_matmul_t",
+    "silu", "swiglu_fwd", "gelu_tanh", "gelu_mlp_fwd", "rmsnorm", "rmsnorm_bwd", "looped_swiglu",
+    "block_ell_matmul_t", "swiglu_bias_grads",
     "block_ell_weight_grad", "swiglu_bwd", "alive_slots", "compact_topology", "column_importance",
     "column_permutation", "apply_permutation", "k_active_macros", "ternary_quantize_blocks",
     "activation_quantize_int8", "encode_ternary", "pack_ternary",
@@ -189,25 +190,54 @@ def silu(z: np.ndarray) -> np.ndarray:
     return z / (1.0 + np.exp(-z))
 
 
-def swiglu_fwd(x, gate, up, down, add_residual: bool = False, h_round=None):
-    """``out = W_down(silu(W_gate x) * W_up x) (+ x)``.
+def swiglu_fwd(x, gate, up, down, add_residual: bool = False, h_round=None, biases=None):
+    """``out = W_down(silu(W_gate x + b_g) * (W_up x + b_u)) + b_d (+ x)``.
 
-    Restates ``looped_blockell/layers/mlp.py:119-145`` (SwiGLU branch) and the
+    Restates ``looped_blockell/layers/mlp.py:119-145`` (SwiGLU branch, whose three
+    ``BlockELLLinear`` projections each add a bias, ``:56-60``, ``:82``) and the
     reference operator's optional residual epilogue
     (``csrc/block_ell/swiglu_fwd.cuh:60-84``).  ``gate``/``up``/``down`` are
-    ``(values, col_indices)`` pairs.  ``h_round`` optionally rounds the hidden
+    ``(values, col_indices)`` pairs; ``biases`` is ``None`` or ``(b_g, b_u, b_d)`` with
+    ``None`` entries for absent biases.  ``h_round`` optionally rounds the hidden
     state (e.g. to bf16) before the down projection.
     Returns ``(out, h, gate_pre_act, up_output)``.
     """
+    bg, bu, bd = biases if biases is not None else (None, None, None)
     g = block_ell_matmul(x, *gate)
     u = block_ell_matmul(x, *up)
+    if bg is not None:
+        g = g + bg
+    if bu is not None:
+        u = u + bu
     h = silu(g) * u
     if h_round is not None:
         h = h_round(h)
     out = block_ell_matmul(h, *down)
+    if bd is not None:
+        out = out + bd
     if add_residual:
         out = out + x
     return out, h, g, u
+
+
+def gelu_tanh(z: np.ndarray) -> np.ndarray:
+    """``jax.nn.gelu`` with its default ``approximate=True`` (the GELU MLP of
+    ``looped_blockell/layers/mlp.py:156``):
+    ``0.5 z (1 + tanh(sqrt(2/pi) (z + 0.044715 z^3)))``."""
+    z = np.asarray(z)
+    return 0.5 * z * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (z + 0.044715 * z ** 3)))
+
+
+def gelu_mlp_fwd(x, fc1, fc2, b1=None, b2=None):
+    """The GELU branch of ``MLPBlock`` (``looped_blockell/layers/mlp.py:146-164``):
+    ``fc2(gelu_tanh(fc1(x) + b1)) + b2``; ``fc1``/``fc2`` are ``(values, col_indices)``."""
+    a = block_ell_matmul(x, *fc1)
+    if b1 is not None:
+        a = a + b1
+    y = block_ell_matmul(gelu_tanh(a), *fc2)
+    if b2 is not None:
+        y = y + b2
+    return y
 
 
 def rmsnorm(x: np.ndarray, scale: np.ndarray, eps: float = 1e-5) -> np.ndarray:
@@ -216,15 +246,31 @@ def rmsnorm(x: np.ndarray, scale: np.ndarray, eps: float = 1e-5) -> np.ndarray:
     return x / np.sqrt(ms + eps) * scale
 
 
-def looped_swiglu(h, norm_scale, gate, up, down, L: int, eps: float = 1e-5, state_round=None):
+def rmsnorm_bwd(x: np.ndarray, scale: np.ndarray, dy: np.ndarray, eps: float = 1e-5):
+    """Gradients of :func:`rmsnorm` for an output gradient ``dy`` (the chain rule of
+    ``looped_blockell/layers/norms.py:14-15``, which the reference differentiates with JAX):
+    ``dx = rs * scale * dy - x * rs^3 * mean(scale * dy * x)``, ``dscale = sum_rows dy * x * rs``
+    with ``rs = 1 / sqrt(mean(x^2) + eps)``.  Returns ``(dx, dscale)``."""
+    x = np.asarray(x, dtype=np.float64)
+    dy = np.asarray(dy, dtype=np.float64)
+    scale = np.asarray(scale, dtype=np.float64)
+    rs = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    dot = np.mean(scale * dy * x, axis=-1, keepdims=True)
+    dx = rs * scale * dy - x * rs ** 3 * dot
+    dscale = np.sum((dy * x * rs).reshape(-1, x.shape[-1]), axis=0)
+    return dx, dscale
+
+
+def looped_swiglu(h, norm_scale, gate, up, down, L: int, eps: float = 1e-5, state_round=None, biases=None):
     """L applications of the pre-norm residual FFN block with shared weights.
 
     ``h <- h + SwiGLU(RMSNorm(h))`` (``looped_blockell/layers/transformer_block.py:84``;
-    the MLP part of ``csrc/loop/persistent_core.cu:315-335``).  ``state_round``
-    optionally rounds the carried state after each iteration (e.g. to bf16).
+    the MLP part of ``csrc/loop/persistent_core.cu:315-335``), the SwiGLU with the optional
+    ``biases`` of :func:`swiglu_fwd`.  ``state_round`` optionally rounds the carried state
+    after each iteration (e.g. to bf16).
     """
     for _ in range(L):
-        y, *_ = swiglu_fwd(rmsnorm(h, norm_scale, eps), gate, up, down)
+        y, *_ = swiglu_fwd(rmsnorm(h, norm_scale, eps), gate, up, down, biases=biases)
         h = h + y
         if state_round is not None:
             h = state_round(h)
@@ -310,6 +356,23 @@ def swiglu_bwd(grad_out, x, gate_pre_act, up_output, h, gate, up, down):
     d_uv = block_ell_weight_grad(xd, du, up[1], B)
     d_dv = block_ell_weight_grad(np.asarray(h, dtype=np.float64), dy, dcol, B)
     return dx, d_gv, d_uv, d_dv
+
+
+def swiglu_bias_grads(grad_out, gate_pre_act, up_output, down):
+    """Bias gradients of the biased SwiGLU of :func:`swiglu_fwd`: the column sums of
+    ``dg``, ``du`` (as in :func:`swiglu_bwd`, from the biased pre-activations) and of
+    ``grad_out``.  Returns ``(d_b_gate, d_b_up, d_b_down)``."""
+    dvals, dcol = down
+    B = dvals.shape[2]
+    d_ff = gate_pre_act.shape[-1]
+    g = np.asarray(gate_pre_act, dtype=np.float64)
+    u = np.asarray(up_output, dtype=np.float64)
+    dy = np.asarray(grad_out, dtype=np.float64)
+    dh = block_ell_matmul_t(dy, dvals.astype(np.float64), dcol, d_ff // B)
+    s = 1.0 / (1.0 + np.exp(-g))
+    dg = dh * u * (s + g * s * (1.0 - s))
+    du = dh * g * s
+    return dg.sum(0), du.sum(0), dy.sum(0)
 
 
 # --------------------------------------------------------------------------
@@ -624,7 +687,11 @@ PINS = {
     "block_ell_matmul": "== x @ W.T of block_ell_to_dense (tests/test_block_ell.py:42-54); brute-force loops; "
                         "identity tiles; sentinel contributes 0; linearity",
     "silu": "closed form values (silu(0)=0, silu(z)-silu(-z)=z)",
-    "swiglu_fwd": "brute-force dense SwiGLU on tiny shapes; residual adds x exactly",
+    "swiglu_fwd": "brute-force dense SwiGLU on tiny shapes, with and without biases; residual adds x exactly",
+    "gelu_tanh": "closed forms (0, odd part z/2, large |z|) and torch's tanh-approximate GELU in float64",
+    "gelu_mlp_fwd": "brute-force dense fc1 -> tanh GELU -> fc2 with biases",
+    "rmsnorm_bwd": "torch float64 autograd of the closed-form RMSNorm (x and scale); finite differences",
+    "swiglu_bias_grads": "torch float64 autograd of the dense biased SwiGLU FFN (the three bias gradients)",
     "rmsnorm": "constant-vector closed form; unit-RMS invariance; scale linearity",
     "looped_swiglu": "L=0 identity; L=1 equals one block; L=2 equals composition",
     "block_ell_matmul_t": "== dy @ W of block_ell_to_dense; adjoint identity <A x, y> = <x, A^T y>; sentinel 0",

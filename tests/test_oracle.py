@@ -197,6 +197,97 @@ def test_swiglu_brute_dense():
     np.testing.assert_allclose(out - out0, x, atol=1e-12)
 
 
+def test_swiglu_biases_brute_dense():
+    """The biased SwiGLU (each projection adds its bias, reference mlp.py:82) against dense math;
+    a planted mistake (the up bias added after the product) is caught."""
+    g = rng(81)
+    B, dm, dff = 4, 12, 16
+    Cm, Cf, Rf, Rm = dm // B, dff // B, dff // B, dm // B
+    gate = (g.standard_normal((Rf, 2, B, B)), O.random_topology(Rf, Cm, 2, g))
+    up = (g.standard_normal((Rf, 2, B, B)), O.random_topology(Rf, Cm, 2, g))
+    down = (g.standard_normal((Rm, 3, B, B)), O.random_topology(Rm, Cf, 3, g))
+    bg, bu, bd = g.standard_normal(dff), g.standard_normal(dff), g.standard_normal(dm)
+    x = g.standard_normal((5, dm))
+    Wg, Wu, Wd = (O.block_ell_to_dense(*gate, dff, dm), O.block_ell_to_dense(*up, dff, dm),
+                  O.block_ell_to_dense(*down, dm, dff))
+    a, b = x @ Wg.T + bg, x @ Wu.T + bu
+    h = a / (1 + np.exp(-a)) * b
+    out, h2, g2, u2 = O.swiglu_fwd(x, gate, up, down, add_residual=True, biases=(bg, bu, bd))
+    np.testing.assert_allclose(out, h @ Wd.T + bd + x, atol=1e-10)
+    np.testing.assert_allclose(g2, a, atol=1e-12)
+    np.testing.assert_allclose(u2, b, atol=1e-12)
+    wrong = (a / (1 + np.exp(-a)) * (x @ Wu.T) + bu) @ Wd.T + bd + x
+    assert np.abs(wrong - out).max() > 1e-3
+    # only some biases
+    out_g, *_ = O.swiglu_fwd(x, gate, up, down, biases=(bg, None, None))
+    np.testing.assert_allclose(out_g, (a / (1 + np.exp(-a)) * (x @ Wu.T)) @ Wd.T, atol=1e-10)
+
+
+def test_gelu_tanh_closed_forms_and_torch():
+    torch = pytest.importorskip("torch")
+    assert O.gelu_tanh(np.array(0.0)) == 0.0
+    z = np.linspace(-6, 6, 49)
+    np.testing.assert_allclose(O.gelu_tanh(z) - O.gelu_tanh(-z), z, atol=1e-12)   # odd part is z/2
+    np.testing.assert_allclose(O.gelu_tanh(np.array([30.0, -30.0])), [30.0, 0.0], atol=1e-12)
+    ref = torch.nn.functional.gelu(torch.tensor(z, dtype=torch.float64), approximate="tanh").numpy()
+    np.testing.assert_allclose(O.gelu_tanh(z), ref, atol=1e-14)
+    exact = torch.nn.functional.gelu(torch.tensor(z, dtype=torch.float64)).numpy()
+    assert np.abs(O.gelu_tanh(z) - exact).max() > 1e-5          # the tanh form, not the erf form
+
+
+def test_gelu_mlp_brute_dense():
+    g = rng(82)
+    B, dm, dff = 4, 8, 16
+    fc1 = (g.standard_normal((dff // B, 2, B, B)), O.random_topology(dff // B, dm // B, 2, g))
+    fc2 = (g.standard_normal((dm // B, 3, B, B)), O.random_topology(dm // B, dff // B, 3, g))
+    b1, b2 = g.standard_normal(dff), g.standard_normal(dm)
+    x = g.standard_normal((3, dm))
+    W1, W2 = O.block_ell_to_dense(*fc1, dff, dm), O.block_ell_to_dense(*fc2, dm, dff)
+    a = x @ W1.T + b1
+    gel = 0.5 * a * (1 + np.tanh(math.sqrt(2 / math.pi) * (a + 0.044715 * a ** 3)))
+    np.testing.assert_allclose(O.gelu_mlp_fwd(x, fc1, fc2, b1, b2), gel @ W2.T + b2, atol=1e-10)
+
+
+def test_rmsnorm_bwd_matches_autograd_and_fd():
+    torch = pytest.importorskip("torch")
+    g = rng(83)
+    x = g.standard_normal((6, 16))
+    s = 1.0 + 0.3 * g.standard_normal(16)
+    dy = g.standard_normal((6, 16))
+    xt = torch.tensor(x, requires_grad=True)
+    st = torch.tensor(s, requires_grad=True)
+    y = xt / torch.sqrt((xt * xt).mean(-1, keepdim=True) + 1e-5) * st
+    (y * torch.tensor(dy)).sum().backward()
+    dx, ds = O.rmsnorm_bwd(x, s, dy, eps=1e-5)
+    np.testing.assert_allclose(dx, xt.grad.numpy(), atol=1e-12)
+    np.testing.assert_allclose(ds, st.grad.numpy(), atol=1e-12)
+    e = 1e-6
+    xp, xm = x.copy(), x.copy()
+    xp[2, 5] += e
+    xm[2, 5] -= e
+    fd = (np.sum(O.rmsnorm(xp, s) * dy) - np.sum(O.rmsnorm(xm, s) * dy)) / (2 * e)
+    assert abs(fd - dx[2, 5]) < 1e-6
+
+
+def test_swiglu_bias_grads_match_autograd():
+    torch = pytest.importorskip("torch")
+    B, dm, dff = 4, 12, 16
+    gate, up, down, x, dy = _bwd_case(84, B, dm, dff)
+    g = rng(85)
+    bg, bu, bd = g.standard_normal(dff), g.standard_normal(dff), g.standard_normal(dm)
+    T = lambda a, grad=False: torch.tensor(a, dtype=torch.float64, requires_grad=grad)
+    xt = T(x)
+    bgt, but, bdt = T(bg, True), T(bu, True), T(bd, True)
+    a = xt @ T(_dense_sum(*gate, dff, dm)).T + bgt
+    b = xt @ T(_dense_sum(*up, dff, dm)).T + but
+    out = (torch.nn.functional.silu(a) * b) @ T(_dense_sum(*down, dm, dff)).T + bdt + xt
+    (out * T(dy)).sum().backward()
+    dbg, dbu, dbd = O.swiglu_bias_grads(dy, a.detach().numpy(), b.detach().numpy(), down)
+    np.testing.assert_allclose(dbg, bgt.grad.numpy(), atol=1e-10)
+    np.testing.assert_allclose(dbu, but.grad.numpy(), atol=1e-10)
+    np.testing.assert_allclose(dbd, bdt.grad.numpy(), atol=1e-10)
+
+
 def test_rmsnorm_closed_forms():
     x = np.full((2, 8), 3.0)
     np.testing.assert_allclose(O.rmsnorm(x, np.ones(8), eps=0.0), np.ones((2, 8)), atol=1e-15)
