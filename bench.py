@@ -7,8 +7,10 @@ over nonzero blocks (plus tokens/s), inputs resident in HBM, one step = one
 forward pass.  The line also carries:
   roofline      the dominant kernel's achieved vs peak, timed with HIP events
                 on the stream the kernel runs on;
-  cpu_baseline  the CPU oracle (numpy gather + matmul restatement of the
-                reference layer) timed on the host cores on the same workload;
+  cpu_baseline  a PyTorch CPU float32 restatement of the reference layer (its
+                gather + einsum, chunked over tokens), median of 3 runs on the
+                host cores, on the same workload (bounded token samples for the
+                ternary and looped lines, each named in its "sample");
   extra         the other workloads (shared gate/up topology, the backward of the
                 headline workload and of one of its products, ternary FFN, looped block L=8, decode, and the
                 prune-time topology transforms on the headline weights).
@@ -21,6 +23,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -335,19 +338,29 @@ def bench_ternary(steps, warmup, device):
     u = make_ternary(Rf, Cm, Kg, B, gen, device)
     d = make_ternary(Rm, Cf, Kd, B, gen, device)
     x = torch.randn(w["N"], w["d_model"], generator=gen, device=device).to(torch.bfloat16)
-    xq, sx = kernels.quantize_act_int8(x)
 
     def step(i):
+        # TernaryMLPBlock.forward: per-token int8 quantisation of x, then the ternary FFN
+        xq, sx = kernels.quantize_act_int8(x)
         kernels.ternary_swiglu_fwd(xq, sx, g, u, d)
 
     ms, per = time_steps(step, steps, warmup)
     ops = nonzero_flops(w)
     tops = ops / (ms * 1e-3) / 1e12
+    xq, sx = kernels.quantize_act_int8(x)
+
+    def step_q(i):
+        kernels.ternary_swiglu_fwd(xq, sx, g, u, d)
+
+    ms_q, per_q = time_steps(step_q, steps, warmup)
     return dict(workload="ternary 2-bit weights / int8 activations SwiGLU FFN, d_model=2048 d_ff=8192 B=64 "
-                         "density=0.125 N=8192 (forward from xq, sx)",
+                         "density=0.125 N=8192 (forward from bf16 x: activation quantisation + FFN)",
                 ms_per_step=ms, value=tops, unit="TOP/s", tokens_per_s=w["N"] / (ms * 1e-3),
                 frac_of_int8_peak=tops / PEAK_INT8_TOPS, algorithmic_ops=ops,
-                algorithmic_bytes=algorithmic_bytes(w, ternary=True))
+                algorithmic_bytes=algorithmic_bytes(w, ternary=True), kernel_ms_avg=sum(per) / len(per),
+                from_quantized=dict(workload="the same FFN from already-quantised xq, sx",
+                                    ms_per_step=ms_q, value=ops / (ms_q * 1e-3) / 1e12, unit="TOP/s",
+                                    kernel_ms_avg=sum(per_q) / len(per_q)))
 
 
 def bench_looped(steps, warmup, device):
@@ -438,35 +451,111 @@ def bench_decode(steps, warmup, device):
                 eager_kernel_ms_avg=sum(per) / len(per))
 
 
-def cpu_baseline():
-    """The oracle (numpy, float32) on the headline workload's full token count."""
-    import numpy as np
-    from oracle import oracle as O
+def _cpu_info():
+    """Threads this process may use for the CPU baseline, and the host CPU model."""
+    cores = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        cores = min(cores, int(env))
+    model = "unknown"
     try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:
-        threads = len(os.sched_getaffinity(0))
-    w = WORKLOADS["bf16"]
-    Rf, Rm, Cm, Cf, Kg, Kd = geometry(w)
-    B = w["B"]
-    rng = np.random.default_rng(w["seed"])
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return cores, model
 
-    def bw(R, C, K):
-        return (rng.standard_normal((R, K, B, B)) * 0.02).astype(np.float32), O.random_topology(R, C, K, rng)
 
-    g, u, d = bw(Rf, Cm, Kg), bw(Rf, Cm, Kg), bw(Rm, Cf, Kd)
-    n = w["N"]
-    x = rng.standard_normal((n, w["d_model"])).astype(np.float32)
-    O.swiglu_fwd(x[:256], g, u, d)  # warm-up
-    t0 = time.perf_counter()
-    O.swiglu_fwd(x, g, u, d)
-    dt = time.perf_counter() - t0
-    flops = nonzero_flops(dict(w, N=n))
-    return dict(value=flops / dt / 1e12, unit="TFLOP/s", tokens_per_s=n / dt, seconds=dt, cores=threads,
-                kind="port",
-                sample=f"headline workload, all {n} tokens, float32 numpy oracle "
-                       "(gather + batched matmul restatement of the reference layer)")
+def _cpu_median(fn, reps):
+    """One untimed warm-up, then the median wall time of `reps` runs."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return median(ts), ts
+
+
+def _cpu_bell(rng, R, C, K, B, std=0.02):
+    import torch
+    from oracle import oracle as O
+    v = torch.from_numpy((rng.standard_normal((R, K, B, B)) * std).astype("float32"))
+    return v, torch.from_numpy(O.random_topology(R, C, K, rng))
+
+
+def cpu_baselines(reps=3):
+    """The PyTorch CPU float32 restatement of the reference layer (gather + einsum, chunked over
+    1024 tokens) on the host cores: the headline workload in full and bounded token samples of the
+    ternary, looped and decode workloads.  Median of `reps` runs after one warm-up each."""
+    import numpy as np
+    import torch
+    from oracle import torch_cpu as TC
+    cores, model = _cpu_info()
+    torch.set_num_threads(cores)
+    common = dict(cores=cores, kind="port", cpu_model=model, reps=reps,
+                  implementation="PyTorch CPU float32 restatement of looped_blockell/layers/block_ell.py:149-182 "
+                                 "composed as looped_blockell/layers/mlp.py:119-145, 1024-token chunks")
+    res = {}
+    with torch.inference_mode():
+        # headline: all 16384 tokens
+        w = WORKLOADS["bf16"]
+        Rf, Rm, Cm, Cf, Kg, Kd = geometry(w)
+        B = w["B"]
+        rng = np.random.default_rng(w["seed"])
+        g, u, d = _cpu_bell(rng, Rf, Cm, Kg, B), _cpu_bell(rng, Rf, Cm, Kg, B), _cpu_bell(rng, Rm, Cf, Kd, B)
+        x = torch.from_numpy(rng.standard_normal((w["N"], w["d_model"])).astype("float32"))
+        dt, ts = _cpu_median(lambda: TC.swiglu_fwd(x, g, u, d), reps)
+        res["bf16"] = dict(common, value=nonzero_flops(w) / dt / 1e12, unit="TFLOP/s", tokens_per_s=w["N"] / dt,
+                           seconds_median=dt, seconds=ts,
+                           sample=f"headline workload, all {w['N']} tokens, float32")
+        # ternary: a 1024-token sample of the 8192
+        w = dict(WORKLOADS["ternary"], N=1024)
+        Rf, Rm, Cm, Cf, Kg, Kd = geometry(w)
+        B = w["B"]
+        rng = np.random.default_rng(w["seed"])
+
+        def tern(R, C, K):
+            from oracle import oracle as O
+            t = torch.from_numpy(rng.integers(-1, 2, size=(R, K, B, B)).astype("float32"))
+            s = torch.from_numpy((0.015 + 0.002 * rng.random((R, K))).astype("float32"))
+            return t, s, torch.from_numpy(O.random_topology(R, C, K, rng))
+
+        tg, tu, td = tern(Rf, Cm, Kg), tern(Rf, Cm, Kg), tern(Rm, Cf, Kd)
+        x = torch.from_numpy(rng.standard_normal((w["N"], w["d_model"])).astype("float32"))
+        dt, ts = _cpu_median(lambda: TC.ternary_swiglu_fwd(x, tg, tu, td), reps)
+        res["ternary"] = dict(common, value=nonzero_flops(w) / dt / 1e12, unit="TOP/s", tokens_per_s=w["N"] / dt,
+                              seconds_median=dt, seconds=ts,
+                              sample="ternary workload on 1024 of its 8192 tokens (int8 activations, exact "
+                                     "integer partials in float32, per-block fp32 scales)")
+        # looped: a 2048-token sample of the 32x512, all L = 8 iterations
+        w = dict(WORKLOADS["looped"], N=2048)
+        Rf, Rm, Cm, Cf, Kg, Kd = geometry(w)
+        B = w["B"]
+        rng = np.random.default_rng(w["seed"])
+        g, u, d = _cpu_bell(rng, Rf, Cm, Kg, B), _cpu_bell(rng, Rf, Cm, Kg, B), _cpu_bell(rng, Rm, Cf, Kd, B)
+        h = torch.from_numpy(rng.standard_normal((w["N"], w["d_model"])).astype("float32"))
+        scale = torch.ones(w["d_model"])
+        dt, ts = _cpu_median(lambda: TC.looped_swiglu(h, scale, g, u, d, L=w["L"]), reps)
+        res["looped"] = dict(common, value=nonzero_flops(w) / dt / 1e12, unit="TFLOP/s", tokens_per_s=w["N"] / dt,
+                             seconds_median=dt, seconds=ts,
+                             sample="looped block (L = 8) on 2048 of its 16384 tokens, float32 state")
+        # decode: the full 16-token step
+        w = WORKLOADS["decode"]
+        Rf, Rm, Cm, Cf, Kg, Kd = geometry(w)
+        B = w["B"]
+        rng = np.random.default_rng(w["seed"])
+        g, u, d = _cpu_bell(rng, Rf, Cm, Kg, B), _cpu_bell(rng, Rf, Cm, Kg, B), _cpu_bell(rng, Rm, Cf, Kd, B)
+        x = torch.from_numpy(rng.standard_normal((w["N"], w["d_model"])).astype("float32"))
+        dt, ts = _cpu_median(lambda: TC.swiglu_fwd(x, g, u, d), max(reps, 5))
+        res["decode"] = dict(common, value=algorithmic_bytes(w) / dt / 1e9, unit="GB/s (bf16-equivalent bytes)",
+                             ms_per_step=dt * 1e3, seconds_median=dt, seconds=ts, reps=max(reps, 5),
+                             sample="decode workload, the full 16-token step on one weight copy (float32 weights "
+                                    "in host memory; GB/s counts the bf16 weight bytes the GPU streams)")
+    return res
 
 
 def main():
@@ -516,7 +605,11 @@ def main():
                 extra[name] = dict(error=f"{type(e).__name__}: {e}")
     cpu = None
     if not args.no_cpu and not args.only_main:
-        cpu = cpu_baseline()
+        cpus = cpu_baselines()
+        cpu = cpus.pop("bf16")
+        for name, c in cpus.items():
+            if name in extra and "error" not in extra[name]:
+                extra[name]["cpu_baseline"] = c
 
     w = WORKLOADS["bf16"]
     line = {

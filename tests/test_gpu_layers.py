@@ -113,6 +113,39 @@ def test_persistent_mlp_step_matches_reference_semantics(gpu):
     kernels.unpin_weights_l2()
 
 
+def test_persistent_mlp_step_rounding(gpu):
+    """The rounding persistent_mlp_step uses, pinned: per core block the residual add happens in
+    fp32 and the state is rounded to bf16 once (= titan::looped_swiglu with L = 1, eps 1e-6, bit for
+    bit), where the reference rounds mlp_out to bf16 and adds in bf16 (csrc/loop/persistent_core.cu:
+    317-334); the two differ by at most a couple of bf16 ulps of the state."""
+    from looped_blockell import kernels
+    rng = np.random.default_rng(24)
+    d_model, d_ff, B, N = 256, 1024, 16, 64
+    blocks = [T.ffn_weights(rng, d_model, d_ff, B, 0.25) for _ in range(2)]
+    scales = [(1 + 0.1 * rng.standard_normal(d_model)).astype(np.float32) for _ in range(2)]
+    h, e = T.act(rng, N, d_model), T.act(rng, N, d_model)
+    la = (0.2 * rng.standard_normal(d_model)).astype(np.float32)
+    ld = (0.2 * rng.standard_normal(d_model)).astype(np.float32)
+    gw = [[T.gpu_weight(w) for w in blk] for blk in blocks]
+    st = [T.to_gpu_bf16(s) for s in scales]
+    out = kernels.persistent_mlp_step(
+        T.to_gpu_bf16(h), T.to_gpu_bf16(e), T.to_gpu(la), T.to_gpu(ld), st,
+        [b[0][0] for b in gw], [b[0][1] for b in gw], [b[1][0] for b in gw], [b[1][1] for b in gw],
+        [b[2][0] for b in gw], [b[2][1] for b in gw])
+    cur = kernels.diagonal_injection(T.to_gpu_bf16(h), T.to_gpu_bf16(e), T.to_gpu(la), T.to_gpu(ld))
+    for b, s in zip(gw, st):
+        cur = kernels.looped_swiglu(cur, s, b[0][0], b[0][1], b[1][0], b[1][1], b[2][0], b[2][1], L=1, eps=1e-6)
+    assert torch.equal(out, cur)
+    # the reference's double rounding, evaluated from the same injected state on the CPU
+    x0 = T.to_np(kernels.diagonal_injection(T.to_gpu_bf16(h), T.to_gpu_bf16(e), T.to_gpu(la), T.to_gpu(ld)))
+    ref = x0.astype(np.float64)
+    for blk, s in zip(blocks, scales):
+        normed = O.bf16_round(O.rmsnorm(ref, O.bf16_round(s).astype(np.float64), 1e-6).astype(np.float32))
+        mlp = O.bf16_round(O.swiglu_fwd(normed.astype(np.float64), *(f64(w) for w in blk))[0].astype(np.float32))
+        ref = O.bf16_round((mlp.astype(np.float64) + ref).astype(np.float32)).astype(np.float64)
+    assert T.rel_err(T.to_np(out), ref)[0] <= TOL
+
+
 def test_looped_layer(gpu):
     from looped_blockell.layers import LoopedSwiGLU
     torch.manual_seed(2)

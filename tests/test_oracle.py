@@ -737,3 +737,60 @@ def test_transposed_index_brute_force():
         assert ptr[-1] == valid and len(set(ent.tolist())) == valid
     ptr, ent = O.transposed_index(np.full((2, 3), -1, np.int32), 4)
     assert ptr.tolist() == [0, 0, 0, 0, 0] and ent.size == 0
+
+
+# ---------------------------------------------------------------- PyTorch CPU restatement (the CPU baseline)
+
+def _tw(r, R, C, K, B, sentinel=False):
+    v = (r.standard_normal((R, K, B, B)) * 0.05).astype(np.float32)
+    col = O.random_topology(R, C, K, r)
+    if sentinel:
+        col[0, -1] = -1
+    return v, col
+
+
+def test_torch_cpu_swiglu_and_loop_match_oracle():
+    import torch
+    from oracle import torch_cpu as TC
+    r = rng(41)
+    B, dm, dff = 16, 64, 256
+    g, u, d = _tw(r, dff // B, dm // B, 2, B, True), _tw(r, dff // B, dm // B, 2, B), _tw(r, dm // B, dff // B, 4, B)
+    x = r.standard_normal((2 * TC.CHUNK + 37, dm)).astype(np.float32)     # several chunks, ragged tail
+    tt = lambda w: (torch.from_numpy(w[0]), torch.from_numpy(w[1]))
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    got = TC.swiglu_fwd(torch.from_numpy(x), tt(g), tt(u), tt(d), add_residual=True).numpy()
+    want, *_ = O.swiglu_fwd(x.astype(np.float64), f64(g), f64(u), f64(d), add_residual=True)
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+    scale = (1 + 0.1 * r.standard_normal(dm)).astype(np.float32)
+    h = x[:300]
+    got = TC.looped_swiglu(torch.from_numpy(h), torch.from_numpy(scale), tt(g), tt(u), tt(d), L=3).numpy()
+    want = O.looped_swiglu(h.astype(np.float64), scale.astype(np.float64), f64(g), f64(u), f64(d), L=3)
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+
+
+def test_torch_cpu_ternary_matches_oracle():
+    import torch
+    from oracle import torch_cpu as TC
+    r = rng(42)
+    B, dm, dff, n = 64, 256, 512, 70
+    def tw(R, C, K, sentinel=False):
+        t = r.integers(-1, 2, size=(R, K, B, B)).astype(np.int8)
+        s = (0.01 + 0.01 * r.random((R, K))).astype(np.float32)
+        col = O.random_topology(R, C, K, r)
+        if sentinel:
+            col[1, 0] = -1
+        return t, s, col
+    g, u, d = tw(dff // B, dm // B, 2, True), tw(dff // B, dm // B, 2), tw(dm // B, dff // B, 4)
+    tt = lambda w: (torch.from_numpy(w[0].astype(np.float32)), torch.from_numpy(w[1]), torch.from_numpy(w[2]))
+    x = r.standard_normal((n, dm)).astype(np.float32)
+    q, sx = TC.activation_quantize_int8(torch.from_numpy(x))
+    q_ref, sx_ref = O.activation_quantize_int8(x)
+    assert np.array_equal(q.numpy().astype(np.int8), q_ref) and np.array_equal(sx.numpy(), sx_ref)
+    got = TC.ternary_matmul(q, sx, *tt(g)).numpy()
+    want, _ = O.ternary_matmul(q_ref, sx_ref, *g)
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+    got = TC.ternary_swiglu_fwd(torch.from_numpy(x), tt(g), tt(u), tt(d)).numpy()
+    res = O.ternary_swiglu_fwd(x, g, u, d)
+    # h is re-quantised: a float32 vs float64 h can flip a rounding of hq, which moves the output by
+    # one int8 step of one token's hidden value times a weight, far below the tolerance used here
+    assert np.abs(got - res["out"]).max() <= 1e-3 * np.abs(res["out"]).max()
