@@ -141,6 +141,42 @@ int lbk_swiglu_fwd_bias_bf16(const uint16_t* x, int64_t N, int32_t d_model,
                              void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Weights packed once, forwards without the per-call pack.  The two-kernel path reads the
+ * gate/up/down tiles in a fragment-major packed copy that lbk_swiglu_fwd_bf16 rebuilds on
+ * every call; a caller whose weights do not change between forwards (inference, a decode
+ * loop) builds it once with lbk_swiglu_prepack_bf16 into a buffer of
+ * lbk_swiglu_prepacked_bytes and passes it to lbk_swiglu_fwd_prepacked_bf16.  The packed
+ * copy reflects values and col_idx at the time of the prepack (dead and out-of-range slots
+ * become zero tiles): pack again after either changes.  lbk_swiglu_prepacked_bytes returns 0
+ * for geometries that read the tiles directly (no packed form); the prepack is then a no-op
+ * and the forward ignores the buffer.  No counterpart in the reference, whose kernel reads
+ * the tiles in place (csrc/block_ell/swiglu_fwd.cu:273-284); this layout's packing is the
+ * part of titan::block_ell_swiglu_fwd (csrc/block_ell/block_ell_ops.cpp:51-63) that a caller
+ * with fixed weights can hoist out of the loop.
+ */
+size_t lbk_swiglu_prepacked_bytes(int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
+                                  const lbk_bell* down);
+int lbk_swiglu_prepack_bf16(int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
+                            const lbk_bell* down, void* packed, size_t packed_bytes, void* stream);
+
+/*
+ * lbk_swiglu_fwd_bias_bf16 from a prepacked copy (biases optional, as there).  gate/up/down
+ * still describe the weights (col_idx, R, K, B; values are read on the decode and general
+ * paths).  The workspace holds h [N, d_ff] bf16 unless h_out is given:
+ * lbk_swiglu_prepacked_workspace_bytes.  Same kernels and results as lbk_swiglu_fwd_bias_bf16.
+ */
+size_t lbk_swiglu_prepacked_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate,
+                                            const lbk_bell* up, const lbk_bell* down,
+                                            int want_intermediates);
+int lbk_swiglu_fwd_prepacked_bf16(const uint16_t* x, int64_t N, int32_t d_model,
+                                  const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                                  const void* packed, size_t packed_bytes,
+                                  const float* b_gate, const float* b_up, const float* b_down,
+                                  int add_residual, uint16_t* out,
+                                  uint16_t* h_out, uint16_t* gate_pre_out, uint16_t* up_out,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Workspace bytes needed by lbk_swiglu_bwd_bf16 for this geometry: the transposed
  * column lists of the three weights, dg and du [N, d_ff] bf16, and fp32 partial
  * tile gradients (one set per 2048 tokens).

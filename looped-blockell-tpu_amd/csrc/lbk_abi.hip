@@ -224,12 +224,13 @@ int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk
                                   gate_pre_out, up_out, workspace, workspace_bytes, stream);
 }
 
-int lbk_swiglu_fwd_bias_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk_bell* gate,
-                             const lbk_bell* up, const lbk_bell* down, const float* b_gate, const float* b_up,
-                             const float* b_down, int add_residual, uint16_t* out, uint16_t* h_out,
-                             uint16_t* gate_pre_out, uint16_t* up_out, void* workspace, size_t workspace_bytes,
-                             void* stream) {
-  const Biases bs{b_gate, b_up, b_down};
+// The forward behind lbk_swiglu_fwd_bias_bf16 and lbk_swiglu_fwd_prepacked_bf16: `prepacked`
+// (may be null) holds the packed tiles of lbk_swiglu_prepack_bf16, otherwise the two-kernel
+// path packs into the workspace.
+static int swiglu_fwd_impl(const uint16_t* x, int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
+                           const lbk_bell* down, const char* prepacked, size_t prepacked_bytes, Biases bs,
+                           int add_residual, uint16_t* out, uint16_t* h_out, uint16_t* gate_pre_out,
+                           uint16_t* up_out, void* workspace, size_t workspace_bytes, hipStream_t s) {
   int st;
   if ((st = check_bell(gate)) || (st = check_bell(up)) || (st = check_bell(down))) return st;
   int64_t d_ff = 0;
@@ -258,26 +259,89 @@ int lbk_swiglu_fwd_bias_bf16(const uint16_t* x, int64_t N, int32_t d_model, cons
     a.out = out;
     a.h = hbuf;
     a.bg = bs.g; a.bu = bs.u; a.bd = bs.d;
-    return launch_decode(gate->B, a, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+    return launch_decode(gate->B, a, s) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
   }
   const bool split = use_split(gate, up, down, d_model);
   const size_t pbytes = split ? packed_ffn_bytes(gate, up, down) : 0;
+  if (split && prepacked) {
+    if (prepacked_bytes < pbytes) return LBK_ERR_WORKSPACE;
+    if (!a16(prepacked)) return LBK_ERR_ALIGN;
+  }
+  const size_t own = (split && !prepacked) ? pbytes : 0;     // packed tiles built by this call
   const size_t hbytes = h_out ? 0 : align256((size_t)N * d_ff * 2);
-  if (pbytes + hbytes > 0) {
-    if (!workspace || workspace_bytes < pbytes + hbytes) return LBK_ERR_WORKSPACE;
+  if (own + hbytes > 0) {
+    if (!workspace || workspace_bytes < own + hbytes) return LBK_ERR_WORKSPACE;
     if (!a16(workspace)) return LBK_ERR_ALIGN;
   }
   char* ws = static_cast<char*>(workspace);
-  uint16_t* h = h_out ? h_out : reinterpret_cast<uint16_t*>(ws + pbytes);
-  hipStream_t s = S(stream);
+  uint16_t* h = h_out ? h_out : reinterpret_cast<uint16_t*>(ws + own);
   if (split) {
     PackedFFN pk{};
-    if ((st = pack_ffn(gate, up, down, ws, &pk, s))) return st;
+    if (prepacked) {
+      const int B = gate->B;
+      pk.g = prepacked;
+      pk.u = prepacked + align256(packed_bf16_bytes((int64_t)gate->R * gate->K, B));
+      pk.d = static_cast<const char*>(pk.u) + align256(packed_bf16_bytes((int64_t)up->R * up->K, B));
+      pk.bytes = pbytes;
+    } else if ((st = pack_ffn(gate, up, down, ws, &pk, s))) {
+      return st;
+    }
     return swiglu_split(x, nullptr, nullptr, 0.f, N, d_model, gate, up, down, pk, add_residual ? x : nullptr,
                         nullptr, out, h, gate_pre_out, up_out, s, bs);
   }
   return swiglu_general(x, N, d_model, gate, up, down, add_residual ? x : nullptr, out, h, gate_pre_out, up_out, s,
                         bs);
+}
+
+int lbk_swiglu_fwd_bias_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk_bell* gate,
+                             const lbk_bell* up, const lbk_bell* down, const float* b_gate, const float* b_up,
+                             const float* b_down, int add_residual, uint16_t* out, uint16_t* h_out,
+                             uint16_t* gate_pre_out, uint16_t* up_out, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  return swiglu_fwd_impl(x, N, d_model, gate, up, down, nullptr, 0, Biases{b_gate, b_up, b_down}, add_residual, out,
+                         h_out, gate_pre_out, up_out, workspace, workspace_bytes, S(stream));
+}
+
+size_t lbk_swiglu_prepacked_bytes(int32_t d_model, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down) {
+  if (!gate || !up || !down || d_model <= 0) return 0;
+  if (check_bell(gate) || check_bell(up) || check_bell(down)) return 0;
+  int64_t d_ff = 0;
+  if (check_ffn(gate, up, down, d_model, &d_ff)) return 0;
+  return use_split(gate, up, down, d_model) ? packed_ffn_bytes(gate, up, down) : 0;
+}
+
+int lbk_swiglu_prepack_bf16(int32_t d_model, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
+                            void* packed, size_t packed_bytes, void* stream) {
+  int st;
+  if ((st = check_bell(gate)) || (st = check_bell(up)) || (st = check_bell(down))) return st;
+  int64_t d_ff = 0;
+  if ((st = check_ffn(gate, up, down, d_model, &d_ff))) return st;
+  if (!use_split(gate, up, down, d_model)) return LBK_OK;        // no packed form for this geometry
+  if (!packed || packed_bytes < packed_ffn_bytes(gate, up, down)) return LBK_ERR_WORKSPACE;
+  if (!a16(packed)) return LBK_ERR_ALIGN;
+  PackedFFN pk{};
+  return pack_ffn(gate, up, down, static_cast<char*>(packed), &pk, S(stream));
+}
+
+size_t lbk_swiglu_prepacked_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
+                                            const lbk_bell* down, int want_intermediates) {
+  if (!gate || !up || !down || N <= 0) return 0;
+  if (use_decode(N, gate, up, down, want_intermediates != 0)) return align256((size_t)N * gate->R * gate->B * 2);
+  if (!use_split(gate, up, down, d_model)) return lbk_swiglu_workspace_bytes(N, d_model, gate, up, down,
+                                                                             want_intermediates);
+  return want_intermediates ? 0 : align256((size_t)N * gate->R * gate->B * 2);
+}
+
+int lbk_swiglu_fwd_prepacked_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk_bell* gate,
+                                  const lbk_bell* up, const lbk_bell* down, const void* packed, size_t packed_bytes,
+                                  const float* b_gate, const float* b_up, const float* b_down, int add_residual,
+                                  uint16_t* out, uint16_t* h_out, uint16_t* gate_pre_out, uint16_t* up_out,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  if (!gate || !up || !down) return LBK_ERR_NULL;
+  if (use_split(gate, up, down, d_model) && !packed && N > 0) return LBK_ERR_NULL;
+  return swiglu_fwd_impl(x, N, d_model, gate, up, down, static_cast<const char*>(packed), packed_bytes,
+                         Biases{b_gate, b_up, b_down}, add_residual, out, h_out, gate_pre_out, up_out, workspace,
+                         workspace_bytes, S(stream));
 }
 
 int lbk_rmsnorm_bf16(const uint16_t* x, int64_t N, int32_t d, const float* scale, float eps, uint16_t* out,

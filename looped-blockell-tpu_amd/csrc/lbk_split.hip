@@ -69,7 +69,9 @@ struct GUPanel { static constexpr int ROWB = 8192 / MT; };
 // barrier, so a caller that synchronises afterwards must do so after the call.
 // READY: the panel and the column table are already in LDS (the looped kernel's down phase
 // wrote the next iteration's normalised rows; the table stays from the first iteration).
-template <int B, int MT, bool NORM, bool INTER, bool SHARED, bool READY = false>
+// BIAS: add a.bg / a.bu (either may be null) to the pre-activations; without it the epilogue
+// has no bias code at all.
+template <int B, int MT, bool NORM, bool INTER, bool SHARED, bool READY = false, bool BIAS = false>
 __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned char* smem, int tid) {
   constexpr int CW = TileShape<B>::CW;
   constexpr int TM = 16 * MT;
@@ -321,12 +323,14 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
     // 4 * CW consecutive columns it holds of one token with one store
     const int r = w + 8 * n;
     const int64_t col0 = (int64_t)r * B + 4 * CW * g;
-    // biases of this lane's 4 * CW columns (zero without)
+    // biases of this lane's 4 * CW columns
     float bgv[4 * CW], buv[4 * CW];
+    if constexpr (BIAS) {
 #pragma unroll
-    for (int q = 0; q < 4 * CW; ++q) {
-      bgv[q] = a.bg ? a.bg[col0 + q] : 0.f;
-      buv[q] = a.bu ? a.bu[col0 + q] : 0.f;
+      for (int q = 0; q < 4 * CW; ++q) {
+        bgv[q] = a.bg ? a.bg[col0 + q] : 0.f;
+        buv[q] = a.bu ? a.bu[col0 + q] : 0.f;
+      }
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -336,8 +340,12 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
       for (int m = 0; m < CW; ++m)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          gv[4 * m + v] = ag[mt][m][v] + bgv[4 * m + v];
-          uv[4 * m + v] = au[mt][m][v] + buv[4 * m + v];
+          gv[4 * m + v] = ag[mt][m][v];
+          uv[4 * m + v] = au[mt][m][v];
+          if constexpr (BIAS) {
+            gv[4 * m + v] += bgv[4 * m + v];
+            uv[4 * m + v] += buv[4 * m + v];
+          }
           o[4 * m + v] = silu_f(gv[4 * m + v]) * uv[4 * m + v];
         }
       if (t < a.N) {
@@ -351,10 +359,10 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
   }
 }
 
-template <int B, int MT, bool NORM, bool INTER, bool SHARED>
+template <int B, int MT, bool NORM, bool INTER, bool SHARED, bool BIAS>
 __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  gu_tile<B, MT, NORM, INTER, SHARED>(a, (int64_t)blockIdx.x, smem, (int)threadIdx.x);
+  gu_tile<B, MT, NORM, INTER, SHARED, false, BIAS>(a, (int64_t)blockIdx.x, smem, (int)threadIdx.x);
 }
 
 // ===========================================================================
@@ -450,7 +458,7 @@ __device__ __forceinline__ void dn_build(FetchList<RPW>& L, int c0, int ncb, con
 // RMSNorm of the new state rows (norm_scale, eps), as bf16, into the gate/up panel at the start
 // of dn_smem (row stride GUPanel<MT>::ROWB), for the next iteration's gate/up phase; red holds
 // (NW + 1) * 16 * MT floats for the per-token sums of squares.
-template <int B, int MT, int RPW, int NW, bool NORMOUT = false>
+template <int B, int MT, int RPW, int NW, bool NORMOUT = false, bool BIAS = false>
 __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, unsigned char* dn_smem,
                                         uint16_t* out, int tid, const float* norm_scale = nullptr,
                                         float eps = 0.f, float* red = nullptr) {
@@ -619,7 +627,9 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
           float o[CW];
 #pragma unroll
           for (int m = 0; m < CW; ++m) {
-            o[m] = ok ? acc[rho][mt][m][v] + (a.bd ? a.bd[rm * B + CW * i + m] : 0.f) + a.state[off + m] : 0.f;
+            float av = acc[rho][mt][m][v];
+            if constexpr (BIAS) av += a.bd[rm * B + CW * i + m];
+            o[m] = ok ? av + a.state[off + m] : 0.f;
             acc[rho][mt][m][v] = o[m];
             ssq[mt][v] += o[m] * o[m];
           }
@@ -686,7 +696,10 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
         const int64_t off = t * d_model + rm * B + CW * i;
         float o[CW];
 #pragma unroll
-        for (int m = 0; m < CW; ++m) o[m] = acc[rho][mt][m][v] + (a.bd ? a.bd[rm * B + CW * i + m] : 0.f);
+        for (int m = 0; m < CW; ++m) {
+          o[m] = acc[rho][mt][m][v];
+          if constexpr (BIAS) o[m] += a.bd[rm * B + CW * i + m];
+        }
         if (a.state) {
 #pragma unroll
           for (int m = 0; m < CW; ++m) {
@@ -704,7 +717,7 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
   }
 }
 
-template <int B, int MT, int RPW>
+template <int B, int MT, int RPW, bool BIAS>
 __global__ __launch_bounds__(64 * DN_WAVES, (RPW == 1 && DN_WAVES == 8) ? 2 : 1) void dn_kernel(DNArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char dn_smem[];   // two stages
   // workgroup -> (token block, row group).  With several row groups, the groups of one token
@@ -716,7 +729,7 @@ __global__ __launch_bounds__(64 * DN_WAVES, (RPW == 1 && DN_WAVES == 8) ? 2 : 1)
     rg = rest % a.nrg;
     tb = 8 * (rest / a.nrg) + (b & 7);
   }
-  dn_tile<B, MT, RPW, DN_WAVES>(a, tb, rg, dn_smem, a.out, (int)threadIdx.x);
+  dn_tile<B, MT, RPW, DN_WAVES, false, BIAS>(a, tb, rg, dn_smem, a.out, (int)threadIdx.x);
 }
 
 // ===========================================================================
@@ -737,7 +750,7 @@ __host__ __device__ inline size_t looped_red_offset(int R_ff, int K) {
 // needed; the weights are read by every workgroup in every iteration (the packed tiles stay
 // in L2 / the memory-side cache across iterations).  The last iteration also writes the
 // bf16 output.
-template <int B, int MT, bool SHARED, int RPW>
+template <int B, int MT, bool SHARED, int RPW, bool BIAS>
 __global__ __launch_bounds__(512, 1) void looped_kernel(LoopArgs la) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int TM = 16 * MT;
@@ -771,8 +784,8 @@ __global__ __launch_bounds__(512, 1) void looped_kernel(LoopArgs la) {
     int tg = tid;
     int64_t tbg = tb;
     asm volatile("" : "+v"(tg), "+s"(tbg));
-    if (fuse && l > 0) gu_tile<B, MT, true, false, SHARED, true>(la.gu, tbg, smem, tg);
-    else gu_tile<B, MT, true, false, SHARED>(la.gu, tbg, smem, tg);
+    if (fuse && l > 0) gu_tile<B, MT, true, false, SHARED, true, BIAS>(la.gu, tbg, smem, tg);
+    else gu_tile<B, MT, true, false, SHARED, false, BIAS>(la.gu, tbg, smem, tg);
     __syncthreads();
     uint16_t* out = l == la.L - 1 ? la.dn.out : nullptr;
     for (int rg = 0; rg < nrg; ++rg) {
@@ -780,9 +793,9 @@ __global__ __launch_bounds__(512, 1) void looped_kernel(LoopArgs la) {
       int64_t tbd = tb;
       asm volatile("" : "+v"(td), "+s"(tbd));
       if (fuse && l < la.L - 1)
-        dn_tile<B, MT, RPW, 8, true>(la.dn, tbd, rg, smem, out, td, la.gu.norm_scale, la.gu.eps, red);
+        dn_tile<B, MT, RPW, 8, true, BIAS>(la.dn, tbd, rg, smem, out, td, la.gu.norm_scale, la.gu.eps, red);
       else
-        dn_tile<B, MT, RPW, 8>(la.dn, tbd, rg, smem, out, td);
+        dn_tile<B, MT, RPW, 8, false, BIAS>(la.dn, tbd, rg, smem, out, td);
       __syncthreads();
     }
   }
@@ -824,15 +837,22 @@ bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int 
   return true;
 }
 
-template <int B, int MT, bool NORM, bool INTER, bool SHARED>
-static int launch_gu_t(const GUArgs& a, hipStream_t st) {
-  auto kern = gu_kernel<B, MT, NORM, INTER, SHARED>;
+template <int B, int MT, bool NORM, bool INTER, bool SHARED, bool BIAS>
+static int launch_gu_b(const GUArgs& a, hipStream_t st) {
+  auto kern = gu_kernel<B, MT, NORM, INTER, SHARED, BIAS>;
   static std::atomic<uint64_t> configured{0};
   if (set_lds_limit_once((const void*)kern, 163840, configured)) return -1;
   const int TM = 16 * MT;
   const size_t lds = gu_lds(a.R_ff, a.Kg, MT);
   hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + TM - 1) / TM)), dim3(512), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// the bias-free kernels carry no bias code (a bias is an epilogue add and two loads per column)
+template <int B, int MT, bool NORM, bool INTER, bool SHARED>
+static int launch_gu_t(const GUArgs& a, hipStream_t st) {
+  return (a.bg || a.bu) ? launch_gu_b<B, MT, NORM, INTER, SHARED, true>(a, st)
+                        : launch_gu_b<B, MT, NORM, INTER, SHARED, false>(a, st);
 }
 
 int launch_gu(int B, bool norm, const GUArgs& a, hipStream_t st) {
@@ -864,7 +884,7 @@ static int launch_dn_t(const DNArgs& a0, hipStream_t st) {
   const int64_t ntb = (a.N + TM - 1) / TM;
   a.nrg = (a.R_m + DN_WAVES * RPW - 1) / (DN_WAVES * RPW);
   const int64_t grid = a.nrg == 1 ? ntb : 8 * a.nrg * ((ntb + 7) / 8);
-  auto kern = dn_kernel<B, MT, RPW>;
+  auto kern = a.bd ? dn_kernel<B, MT, RPW, true> : dn_kernel<B, MT, RPW, false>;
   if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return -1;
@@ -881,9 +901,9 @@ int launch_dn(int B, const DNArgs& a, hipStream_t st) {
   return -2;
 }
 
-template <int B, int MT, bool SHARED, int RPW>
-static int launch_looped_t(const LoopArgs& a, hipStream_t st) {
-  auto kern = looped_kernel<B, MT, SHARED, RPW>;
+template <int B, int MT, bool SHARED, int RPW, bool BIAS>
+static int launch_looped_b(const LoopArgs& a, hipStream_t st) {
+  auto kern = looped_kernel<B, MT, SHARED, RPW, BIAS>;
   static std::atomic<uint64_t> configured{0};
   if (set_lds_limit_once((const void*)kern, 163840, configured)) return -1;
   const int TM = 16 * MT;
@@ -895,6 +915,12 @@ static int launch_looped_t(const LoopArgs& a, hipStream_t st) {
   if (lds > 163840) return -2;
   hipLaunchKernelGGL(kern, dim3((unsigned)((a.gu.N + TM - 1) / TM)), dim3(512), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+template <int B, int MT, bool SHARED, int RPW>
+static int launch_looped_t(const LoopArgs& a, hipStream_t st) {
+  return (a.gu.bg || a.gu.bu || a.dn.bd) ? launch_looped_b<B, MT, SHARED, RPW, true>(a, st)
+                                         : launch_looped_b<B, MT, SHARED, RPW, false>(a, st);
 }
 
 // The persistent looped block takes the shapes of the two-kernel path with MT = 4

@@ -101,7 +101,7 @@ std::vector<at::Tensor> swiglu_impl(const at::Tensor& x_, at::Tensor vg, at::Ten
                                     bool intermediates, const c10::optional<at::Tensor>& bg_ = c10::nullopt,
                                     const c10::optional<at::Tensor>& bu_ = c10::nullopt,
                                     const c10::optional<at::Tensor>& bd_ = c10::nullopt,
-                                    const char* opname = nullptr) {
+                                    const char* opname = nullptr, const at::Tensor* packed = nullptr) {
   const char* op = opname ? opname
                           : (intermediates ? "block_ell_swiglu_fwd_with_intermediate" : "block_ell_swiglu_fwd");
   at::Tensor x = check_x2d(x_, op);
@@ -127,6 +127,22 @@ std::vector<at::Tensor> swiglu_impl(const at::Tensor& x_, at::Tensor vg, at::Ten
   }
   const at::Tensor bg = opt_bias(bg_, d_ff, x, op, "b_gate"), bu = opt_bias(bu_, d_ff, x, op, "b_up"),
                    bd = opt_bias(bd_, d_model, x, op, "b_down");
+  if (packed) {
+    check_gpu(*packed, op, "packed");
+    TORCH_CHECK(packed->scalar_type() == at::kByte && packed->dim() == 1 && packed->is_contiguous(), "titan::", op,
+                ": packed must be the contiguous uint8 tensor of block_ell_swiglu_prepack");
+    const size_t need = lbk_swiglu_prepacked_bytes((int32_t)d_model, &g, &u, &d);
+    TORCH_CHECK((size_t)packed->numel() >= need, "titan::", op, ": packed holds ", packed->numel(),
+                " bytes, this geometry needs ", need, " (pack these weights with block_ell_swiglu_prepack)");
+    const size_t wsb = lbk_swiglu_prepacked_workspace_bytes(N, (int32_t)d_model, &g, &u, &d, intermediates ? 1 : 0);
+    at::Tensor ws = wsb ? workspace(wsb, x) : at::Tensor();
+    LBK_CALL("block_ell_swiglu_fwd_prepacked",
+             lbk_swiglu_fwd_prepacked_bf16(bf(x), N, (int32_t)d_model, &g, &u, &d,
+                                           need ? packed->data_ptr() : nullptr, (size_t)packed->numel(), fptr(bg),
+                                           fptr(bu), fptr(bd), add_residual ? 1 : 0, bfm(out), h, gp, uo,
+                                           wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(x)));
+    return res;
+  }
   const size_t wsb = lbk_swiglu_workspace_bytes(N, (int32_t)d_model, &g, &u, &d, intermediates ? 1 : 0);
   at::Tensor ws = wsb ? workspace(wsb, x) : at::Tensor();
   LBK_CALL("block_ell_swiglu_fwd",
@@ -149,6 +165,33 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> swiglu_fwd_bias(
     return {r[0], e, e, e};
   }
   return {r[0], r[1], r[2], r[3]};
+}
+
+// The fragment-major packed copy of gate/up/down that the two-kernel forward reads, built once
+// (uint8; empty when the geometry has no packed form): block_ell_swiglu_fwd_prepacked then
+// skips the per-call pack.  It reflects the values and column indices at the time of the call.
+at::Tensor swiglu_prepack(const at::Tensor& vg_, const at::Tensor& cg_, const at::Tensor& vu_, const at::Tensor& cu_,
+                          const at::Tensor& vd_, const at::Tensor& cd_) {
+  const char* op = "block_ell_swiglu_prepack";
+  at::Tensor vg = vg_, cg = cg_, vu = vu_, cu = cu_, vd = vd_, cd = cd_;
+  check_gpu(vg, op, "gate");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(vg.device());
+  lbk_bell g = make_bell(vg, cg, op, "gate"), u = make_bell(vu, cu, op, "up"), d = make_bell(vd, cd, op, "down");
+  const int32_t d_model = d.R * d.B;
+  const size_t bytes = lbk_swiglu_prepacked_bytes(d_model, &g, &u, &d);
+  at::Tensor packed = at::empty({(int64_t)bytes}, vg.options().dtype(at::kByte));
+  if (bytes)
+    LBK_CALL("block_ell_swiglu_prepack",
+             lbk_swiglu_prepack_bf16(d_model, &g, &u, &d, packed.data_ptr(), bytes, cur_stream(vg)));
+  return packed;
+}
+
+at::Tensor swiglu_fwd_prepacked(const at::Tensor& x, const at::Tensor& packed, const at::Tensor& vg,
+                                const at::Tensor& cg, const c10::optional<at::Tensor>& bg, const at::Tensor& vu,
+                                const at::Tensor& cu, const c10::optional<at::Tensor>& bu, const at::Tensor& vd,
+                                const at::Tensor& cd, const c10::optional<at::Tensor>& bd, bool add_residual) {
+  return swiglu_impl(x, vg, cg, vu, cu, vd, cd, add_residual, false, bg, bu, bd, "block_ell_swiglu_fwd_prepacked",
+                     &packed)[0];
 }
 
 at::Tensor swiglu_fwd(const at::Tensor& x, const at::Tensor& vg, const at::Tensor& cg, const at::Tensor& vu,
@@ -607,6 +650,11 @@ TORCH_LIBRARY(titan, m) {
   m.def("block_ell_swiglu_fwd_bias(Tensor x, Tensor v_gate, Tensor ci_gate, Tensor? b_gate, Tensor v_up, "
         "Tensor ci_up, Tensor? b_up, Tensor v_down, Tensor ci_down, Tensor? b_down, bool add_residual, "
         "bool intermediates=False) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("block_ell_swiglu_prepack(Tensor v_gate, Tensor ci_gate, Tensor v_up, Tensor ci_up, Tensor v_down, "
+        "Tensor ci_down) -> Tensor");
+  m.def("block_ell_swiglu_fwd_prepacked(Tensor x, Tensor packed, Tensor v_gate, Tensor ci_gate, Tensor? b_gate, "
+        "Tensor v_up, Tensor ci_up, Tensor? b_up, Tensor v_down, Tensor ci_down, Tensor? b_down, "
+        "bool add_residual) -> Tensor");
   m.def("block_ell_swiglu_bwd_bias(Tensor grad_out, Tensor x, Tensor gate_pre_act, Tensor up_out, Tensor h, "
         "Tensor v_gate, Tensor ci_gate, Tensor v_up, Tensor ci_up, Tensor v_down, Tensor ci_down, "
         "bool add_residual) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
@@ -649,6 +697,8 @@ TORCH_LIBRARY_IMPL(titan, CUDA, m) {
   m.impl("block_ell_swiglu_bwd_ex", &swiglu_bwd_ex);
   m.impl("block_ell_swiglu_fwd_bias", &swiglu_fwd_bias);
   m.impl("block_ell_swiglu_bwd_bias", &swiglu_bwd_bias);
+  m.impl("block_ell_swiglu_prepack", &swiglu_prepack);
+  m.impl("block_ell_swiglu_fwd_prepacked", &swiglu_fwd_prepacked);
   m.impl("looped_swiglu_bias", &looped_swiglu_bias);
   m.impl("pin_weights_l2", &pin_weights_l2);
   m.impl("persistent_mlp_step", &persistent_mlp_step);
@@ -682,7 +732,7 @@ TORCH_LIBRARY_IMPL(titan, Autograd, m) {
         "persistent_mlp_step", "block_ell_matmul", "block_ell_matmul_bwd", "block_ell_swiglu_bwd_ex",
         "looped_swiglu", "looped_swiglu_persistent", "looped_swiglu_launches", "rmsnorm", "rmsnorm_bwd",
         "block_ell_swiglu_fwd_bias", "block_ell_swiglu_bwd_bias", "looped_swiglu_bias",
-        "diagonal_injection", "quantize_act_int8", "pack_ternary", "ternary_quantize_weights", "ternary_matmul",
+        "block_ell_swiglu_prepack", "block_ell_swiglu_fwd_prepacked", "diagonal_injection", "quantize_act_int8", "pack_ternary", "ternary_quantize_weights", "ternary_matmul",
         "block_ell_swiglu_fwd_ternary", "block_ell_swiglu_fwd_ternary_with_intermediate",
         "block_ell_swiglu_fwd_ternary_accumulators"})
     m.impl(name, torch::autograd::autogradNotImplementedFallback());
@@ -731,6 +781,10 @@ TORCH_LIBRARY_IMPL(titan, Meta, m) {
            return std::make_tuple(at::empty_like(x), at::empty_like(vg), at::empty_like(vu), at::empty_like(vd),
                                   at::empty({d_ff}, f), at::empty({d_ff}, f), at::empty({x.size(1)}, f));
          });
+  m.impl("block_ell_swiglu_fwd_prepacked",
+         [](const at::Tensor& x, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+            const c10::optional<at::Tensor>&, const at::Tensor&, const at::Tensor&, const c10::optional<at::Tensor>&,
+            const at::Tensor&, const at::Tensor&, const c10::optional<at::Tensor>&, bool) { return at::empty_like(x); });
   m.impl("looped_swiglu_bias",
          [](const at::Tensor& h, const at::Tensor&, const at::Tensor&, const at::Tensor&,
             const c10::optional<at::Tensor>&, const at::Tensor&, const at::Tensor&, const c10::optional<at::Tensor>&,

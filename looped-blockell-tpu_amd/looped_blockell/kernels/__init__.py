@@ -184,6 +184,23 @@ def swiglu(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual: bool 
     return swiglu_fwd(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual)
 
 
+def swiglu_prepack(v_gate, ci_gate, v_up, ci_up, v_down, ci_down):
+    """``titan::block_ell_swiglu_prepack``: the packed tile copy the two-kernel forward reads,
+    built once for weights that stay fixed across forwards (uint8; empty when the geometry has
+    no packed form).  Pack again after the values or the column indices change."""
+    _gpu(v_gate, v_down)
+    return ops().block_ell_swiglu_prepack(v_gate, ci_gate, v_up, ci_up, v_down, ci_down)
+
+
+def swiglu_fwd_prepacked(x, packed, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual: bool = False,
+                         b_gate=None, b_up=None, b_down=None):
+    """SwiGLU forward (optional biases) from a ``swiglu_prepack`` copy: the gate/up and down
+    launches only; same result as ``swiglu_fwd`` / ``titan::block_ell_swiglu_fwd_bias``."""
+    _gpu(x, v_gate, v_down)
+    return ops().block_ell_swiglu_fwd_prepacked(x, packed, v_gate, ci_gate, b_gate, v_up, ci_up, b_up, v_down,
+                                                ci_down, b_down, add_residual)
+
+
 def looped_swiglu(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L: int, eps: float = 1e-5):
     """L applications of h <- h + SwiGLU(RMSNorm(h)) with shared weights, in one operator call (one
     persistent launch where the shape allows, per-iteration launches otherwise)."""

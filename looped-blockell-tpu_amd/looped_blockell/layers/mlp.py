@@ -16,6 +16,14 @@ trainable bias, as every ``BlockELLLinear`` of the reference's Flax module does
 gives the bias-free form of the reference's PyTorch mirror (``interop/pt_model.py:865-867``)
 and CUDA operator (``csrc/block_ell/swiglu_fwd.cuh:75-84``).  The GELU form uses the tanh
 approximation, ``jax.nn.gelu``'s default (``mlp.py:156``).
+
+Forwards that need no gradient (``torch.no_grad()`` / ``torch.inference_mode()``) run from
+weights prepared once per weight version: the bf16 tiles and their fragment-major packed copy
+(``titan::block_ell_swiglu_prepack``) are cached on the module and rebuilt when a value tensor,
+a column-index buffer or an alive mask changes (tensor version counters), so such a forward is
+the gate/up and down launches only.  Writes through ``.data`` bypass the version counter: call
+``release_inference_cache()`` after them.  The cache holds about two bytes per weight element
+twice (bf16 tiles, packed tiles); ``release_inference_cache()`` drops it.
 """
 
 from __future__ import annotations
@@ -68,8 +76,11 @@ class BlockELLLinear(nn.Module):
         key = (self.col_indices.data_ptr(), self.col_indices._version, self.alive_mask.data_ptr(),
                self.alive_mask._version)
         if self._eff_cache is None or self._eff_cache[0] != key:
-            eff = torch.where(self.alive_mask, self.col_indices, torch.full_like(self.col_indices, -1))
-            self._eff_cache = (key, eff.to(torch.int32).contiguous())
+            # an ordinary tensor even when built under inference mode: a later forward with
+            # gradients saves it for the backward
+            with torch.inference_mode(False):
+                eff = torch.where(self.alive_mask, self.col_indices, torch.full_like(self.col_indices, -1))
+                self._eff_cache = (key, eff.to(torch.int32).contiguous())
         return self._eff_cache[1]
 
     def kernel_values(self) -> torch.Tensor:
@@ -102,6 +113,7 @@ class MLPBlock(nn.Module):
         else:
             self.fc1 = BlockELLLinear(d_ff, d_model, **kw)
             self.fc2 = BlockELLLinear(d_model, d_ff, **kw)
+        self._frozen = None
 
     def swiglu_weights(self):
         """(v_gate, ci_gate, v_up, ci_up, v_down, ci_down) in kernel form.
@@ -119,6 +131,21 @@ class MLPBlock(nn.Module):
         return (self.w_gate.kernel_values(), cg, self.w_up.kernel_values(), cu,
                 self.w_down.kernel_values(), self.w_down.effective_col_indices())
 
+    def _frozen_swiglu(self):
+        """(kernel-form weights, packed copy), rebuilt when any weight's version changes."""
+        lins = (self.w_gate, self.w_up, self.w_down)
+        for lin in lins:
+            lin.effective_col_indices()                  # refreshes each topology key
+        key = tuple((lin.values.data_ptr(), lin.values._version, lin._eff_cache[0]) for lin in lins)
+        if self._frozen is None or self._frozen[0] != key:
+            w = self.swiglu_weights()
+            self._frozen = (key, w, kernels.swiglu_prepack(*w))
+        return self._frozen[1], self._frozen[2]
+
+    def release_inference_cache(self) -> None:
+        """Drop the cached bf16 and packed weights of gradient-free forwards."""
+        self._frozen = None
+
     def swiglu_biases(self):
         """(b_gate, b_up, b_down): the projections' biases (None where a projection has none)."""
         return self.w_gate.bias, self.w_up.bias, self.w_down.bias
@@ -128,8 +155,13 @@ class MLPBlock(nn.Module):
         if self.use_swiglu:
             x2 = x.reshape(-1, self.d_model).to(torch.bfloat16).contiguous()
             bg, bu, bd = self.swiglu_biases()
-            out = kernels.swiglu(x2, *self.swiglu_weights(), add_residual=False, b_gate=bg, b_up=bu,
-                                 b_down=bd).reshape(*lead, self.d_model)
+            grad = torch.is_grad_enabled() and (x2.requires_grad or any(p.requires_grad for p in self.parameters()))
+            if grad:
+                out = kernels.swiglu(x2, *self.swiglu_weights(), add_residual=False, b_gate=bg, b_up=bu, b_down=bd)
+            else:
+                w, packed = self._frozen_swiglu()
+                out = kernels.swiglu_fwd_prepacked(x2, packed, *w, add_residual=False, b_gate=bg, b_up=bu, b_down=bd)
+            out = out.reshape(*lead, self.d_model)
         else:
             out = self.fc2(F.gelu(self.fc1(x).float(), approximate="tanh").to(torch.bfloat16))
         if self.dropout > 0.0 and not deterministic:
