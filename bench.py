@@ -15,7 +15,8 @@ forward pass.  The line also carries:
                 headline workload and of one of its products, ternary FFN, looped block L=8, decode, and the
                 prune-time topology transforms on the headline weights).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only-main]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only-main | --skip-main]
+                      [--only shared,backward,...] [--copy-calibration]
 """
 
 from __future__ import annotations
@@ -197,8 +198,8 @@ def bench_bf16(steps, warmup, device):
         kernel_ms_avg=kern_ms, kernel_ms_median=median(per),
         roofline=dict(bound="mfma", achieved=achieved, peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
                       frac=achieved / PEAK_BF16_TFLOPS, traffic=profiled_traffic(TRAFFIC_PROFILE_BF16),
-                      traffic_source=os.path.relpath(TRAFFIC_PROFILE_BF16, ROOT) + " (FETCH_SIZE/WRITE_SIZE, "
-                                     "calibrated on a 256 MiB copy)",
+                      traffic_source=os.path.relpath(TRAFFIC_PROFILE_BF16, ROOT) + " (2 x FETCH_SIZE + WRITE_SIZE "
+                                     "of the two launches, the factors a copy of known size reads)",
                       kernel="SwiGLU forward launch pair gu_kernel<32,4,false,false,false,false> + "
                              "dn_kernel<32,4,1,false>, timed together with HIP events around each step",
                       algorithmic_flops_per_launch=flops,
@@ -587,6 +588,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-main", action="store_true", help="headline workload only (for profiling)")
+    ap.add_argument("--skip-main", action="store_true",
+                    help="skip the headline workload (profiling one extra workload on its own; the line's "
+                         "headline fields are then null)")
     ap.add_argument("--only", default="",
                     help="comma list of extra workloads to run: shared,backward,matmul_backward,ternary,looped,"
                          "decode,topology,formats")
@@ -611,7 +615,8 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    main_res = bench_bf16(args.steps, args.warmup, device)
+    empty = dict(value=None, ms_per_step=None, tokens_per_s=None, kernel_ms_avg=None, roofline=None, with_pack=None)
+    main_res = empty if args.skip_main else bench_bf16(args.steps, args.warmup, device)
     extra = {}
     if not args.only_main:
         todo = [s for s in args.only.split(",") if s] or ["shared", "backward", "matmul_backward", "ternary", "looped",
