@@ -373,8 +373,8 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
 // DN_STAGE_COLS h columns of the workgroup's tokens
 constexpr int DN_WAVES = 16;
 constexpr int DN_STAGE_COLS = 512;
-template <int B>
-struct DnStage { static constexpr int G = DN_STAGE_COLS / B; };
+template <int B, int SC>
+struct DnStage { static constexpr int G = SC / B; };
 
 // Per-wave fetch list of one stage: position q (lane q % 64 of v[q / 64]) holds
 // desc = tile << 6 | cb -- the packed down tile (row * Kd + slot) and its column
@@ -458,13 +458,13 @@ __device__ __forceinline__ void dn_build(FetchList<RPW>& L, int c0, int ncb, con
 // RMSNorm of the new state rows (norm_scale, eps), as bf16, into the gate/up panel at the start
 // of dn_smem (row stride GUPanel<MT>::ROWB), for the next iteration's gate/up phase; red holds
 // (NW + 1) * 16 * MT floats for the per-token sums of squares.
-template <int B, int MT, int RPW, int NW, bool NORMOUT = false, bool BIAS = false>
+template <int B, int MT, int RPW, int NW, bool NORMOUT = false, bool BIAS = false, int SC = DN_STAGE_COLS>
 __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, unsigned char* dn_smem,
                                         uint16_t* out, int tid, const float* norm_scale = nullptr,
                                         float eps = 0.f, float* red = nullptr) {
   constexpr int CW = TileShape<B>::CW;
   constexpr int TM = 16 * MT;
-  constexpr int G = DnStage<B>::G;
+  constexpr int G = DnStage<B, SC>::G;
   constexpr int SROWB = G * B * 2;                   // bytes per token row of a stage (512)
   constexpr int SBYTES = TM * SROWB;                 // bytes per stage
   constexpr int CHUNKS = SBYTES / 16;                // 16-byte chunks per stage
@@ -717,8 +717,8 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
   }
 }
 
-template <int B, int MT, int RPW, bool BIAS>
-__global__ __launch_bounds__(64 * DN_WAVES, (RPW == 1 && DN_WAVES == 8) ? 2 : 1) void dn_kernel(DNArgs a) {
+template <int B, int MT, int RPW, int NW, int SC, bool BIAS>
+__global__ __launch_bounds__(64 * NW, 1) void dn_kernel(DNArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char dn_smem[];   // two stages
   // workgroup -> (token block, row group).  With several row groups, the groups of one token
   // block get workgroup ids that agree mod 8, i.e. one XCD (workgroups are dealt to the 8
@@ -729,7 +729,7 @@ __global__ __launch_bounds__(64 * DN_WAVES, (RPW == 1 && DN_WAVES == 8) ? 2 : 1)
     rg = rest % a.nrg;
     tb = 8 * (rest / a.nrg) + (b & 7);
   }
-  dn_tile<B, MT, RPW, DN_WAVES, false, BIAS>(a, tb, rg, dn_smem, a.out, (int)threadIdx.x);
+  dn_tile<B, MT, RPW, NW, false, BIAS, SC>(a, tb, rg, dn_smem, a.out, (int)threadIdx.x);
 }
 
 // ===========================================================================
@@ -876,28 +876,31 @@ int launch_gu(int B, bool norm, const GUArgs& a, hipStream_t st) {
   return -2;
 }
 
-template <int B, int MT, int RPW>
+template <int B, int MT, int RPW, int NW, int SC>
 static int launch_dn_t(const DNArgs& a0, hipStream_t st) {
   const int TM = 16 * MT;
-  constexpr size_t lds = 2 * (size_t)TM * DN_STAGE_COLS * 2;   // two stages
+  constexpr size_t lds = 2 * (size_t)TM * SC * 2;   // two stages
   DNArgs a = a0;
   const int64_t ntb = (a.N + TM - 1) / TM;
-  a.nrg = (a.R_m + DN_WAVES * RPW - 1) / (DN_WAVES * RPW);
+  a.nrg = (a.R_m + NW * RPW - 1) / (NW * RPW);
   const int64_t grid = a.nrg == 1 ? ntb : 8 * a.nrg * ((ntb + 7) / 8);
-  auto kern = a.bd ? dn_kernel<B, MT, RPW, true> : dn_kernel<B, MT, RPW, false>;
+  auto kern = a.bd ? dn_kernel<B, MT, RPW, NW, SC, true> : dn_kernel<B, MT, RPW, NW, SC, false>;
   if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return -1;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * DN_WAVES), lds, st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * NW), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 // One down row per wave (a workgroup covers DN_WAVES rows; the row groups of one token block
-// share an XCD): few accumulator registers per wave, four waves per SIMD.
+// share an XCD): few accumulator registers per wave, four waves per SIMD.  (128-token
+// workgroups, which halve the weight bytes each CU streams, measured slower at the headline
+// geometry: 154 us with 8 waves of two rows and 256-column stages, 161 us with 16 waves of one
+// row, against 144 us; the smaller stages add padding and per-stage imbalance.)
 int launch_dn(int B, const DNArgs& a, hipStream_t st) {
   if (a.N == 0) return 0;
-  if (B == 16) return launch_dn_t<16, 4, 1>(a, st);
-  if (B == 32) return launch_dn_t<32, 4, 1>(a, st);
+  if (B == 16) return launch_dn_t<16, 4, 1, DN_WAVES, DN_STAGE_COLS>(a, st);
+  if (B == 32) return launch_dn_t<32, 4, 1, DN_WAVES, DN_STAGE_COLS>(a, st);
   return -2;
 }
 
