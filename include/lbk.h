@@ -256,6 +256,22 @@ int lbk_diagonal_injection_bf16(const uint16_t* h, const uint16_t* e, const floa
                                 void* stream);
 
 /*
+ * Backward of lbk_diagonal_injection_bf16 for an output gradient grad_out [N, d] (bf16):
+ *   dh = decay * grad_out, de = dt * grad_out            (bf16, each optional)
+ *   d_log_A[c]  = -sum_n grad_out * h * decay * dt * A    (fp32, optional; A = exp(log_A))
+ *   d_log_dt[c] = sum_n grad_out * (e - h * decay * A) * sigmoid(log_dt)   (fp32, optional)
+ * The sums run per 64 rows, then over those partials in a fixed order (deterministic); the
+ * workspace (lbk_diagonal_injection_bwd_workspace_bytes) holds the partials.  The gradients of
+ * the reference's PyTorch DiagonalInjection (interop/pt_model.py:923-935) under autograd; the
+ * reference's CUDA operator has no backward.
+ */
+size_t lbk_diagonal_injection_bwd_workspace_bytes(int64_t N, int32_t d);
+int lbk_diagonal_injection_bwd_bf16(const uint16_t* grad_out, const uint16_t* h, const uint16_t* e,
+                                    const float* log_A, const float* log_dt, int64_t N, int32_t d,
+                                    uint16_t* dh, uint16_t* de, float* d_log_A, float* d_log_dt,
+                                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Looped pre-norm FFN block with shared weights, applied L times:
  *   h <- h + SwiGLU(RMSNorm(h; norm_scale, eps))
  * h_in, h_out: [N, d_model] bf16 (may alias).  On the two-kernel path the

@@ -377,6 +377,26 @@ int lbk_diagonal_injection_bf16(const uint16_t* h, const uint16_t* e, const floa
   return launch_injection(h, e, log_A, log_dt, N, d, h_out, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
 }
 
+size_t lbk_diagonal_injection_bwd_workspace_bytes(int64_t N, int32_t d) {
+  if (N < 0 || d <= 0) return 0;
+  return align256(injection_bwd_bytes(N, d));
+}
+
+int lbk_diagonal_injection_bwd_bf16(const uint16_t* grad_out, const uint16_t* h, const uint16_t* e,
+                                    const float* log_A, const float* log_dt, int64_t N, int32_t d, uint16_t* dh,
+                                    uint16_t* de, float* d_log_A, float* d_log_dt, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  if (N < 0 || d <= 0) return LBK_ERR_ARG;
+  if (!log_A || !log_dt) return LBK_ERR_NULL;
+  if (N > 0 && (!grad_out || !h || !e)) return LBK_ERR_NULL;
+  const size_t need = lbk_diagonal_injection_bwd_workspace_bytes(N, d);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return LBK_ERR_WORKSPACE;
+  return launch_injection_bwd(grad_out, h, e, log_A, log_dt, N, d, dh, de, d_log_A, d_log_dt,
+                              static_cast<float*>(workspace), S(stream)) == 0
+             ? LBK_OK
+             : LBK_ERR_LAUNCH;
+}
+
 size_t lbk_looped_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
                                   const lbk_bell* down) {
   if (!gate || !up || !down || N <= 0 || d_model <= 0) return 0;

@@ -255,6 +255,59 @@ __global__ __launch_bounds__(256) void injection_kernel(const uint16_t* h, const
   out[idx] = f2bf(decay * bf2f(h[idx]) + dt * bf2f(e[idx]));
 }
 
+// Backward of the injection, one workgroup per 64 rows: dh = decay * g, de = dt * g (either may
+// be skipped), and per column the partial sums over the block's rows of g * h and g * e, which
+// injection_param_grad_kernel adds in a fixed order into the parameter gradients.
+__global__ __launch_bounds__(256) void injection_bwd_kernel(const uint16_t* __restrict__ g,
+                                                            const uint16_t* __restrict__ h,
+                                                            const uint16_t* __restrict__ e,
+                                                            const float* __restrict__ log_A,
+                                                            const float* __restrict__ log_dt, int64_t N, int d,
+                                                            uint16_t* __restrict__ dh, uint16_t* __restrict__ de,
+                                                            float* __restrict__ part) {
+  const int64_t r0 = (int64_t)blockIdx.x * RMS_BWD_ROWS;
+  const int nrows = (int)(N - r0 < RMS_BWD_ROWS ? N - r0 : RMS_BWD_ROWS);
+  for (int c = threadIdx.x; c < d; c += 256) {
+    const float ld = log_dt[c];
+    const float dt = ld > 20.f ? ld : log1pf(expf(ld));
+    const float decay = expf(-dt * expf(log_A[c]));
+    float sgh = 0.f, sge = 0.f;
+    for (int rr = 0; rr < nrows; ++rr) {
+      const int64_t idx = (r0 + rr) * d + c;
+      const float gv = bf2f(g[idx]);
+      sgh += gv * bf2f(h[idx]);
+      sge += gv * bf2f(e[idx]);
+      if (dh) dh[idx] = f2bf(decay * gv);
+      if (de) de[idx] = f2bf(dt * gv);
+    }
+    part[((int64_t)blockIdx.x * 2) * d + c] = sgh;
+    part[((int64_t)blockIdx.x * 2 + 1) * d + c] = sge;
+  }
+}
+
+// d log_A = -S_gh * decay * dt * A, d log_dt = (S_ge - S_gh * decay * A) * sigmoid(log_dt), with the
+// column sums S over the nblk row blocks added in block order
+__global__ __launch_bounds__(256) void injection_param_grad_kernel(const float* __restrict__ part, int nblk, int d,
+                                                                   const float* __restrict__ log_A,
+                                                                   const float* __restrict__ log_dt,
+                                                                   float* __restrict__ d_log_A,
+                                                                   float* __restrict__ d_log_dt) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= d) return;
+  float sgh = 0.f, sge = 0.f;
+  for (int b = 0; b < nblk; ++b) {
+    sgh += part[((int64_t)b * 2) * d + c];
+    sge += part[((int64_t)b * 2 + 1) * d + c];
+  }
+  const float ld = log_dt[c];
+  const float dt = ld > 20.f ? ld : log1pf(expf(ld));
+  const float A = expf(log_A[c]);
+  const float decay = expf(-dt * A);
+  const float sig = 1.0f / (1.0f + expf(-ld));
+  if (d_log_A) d_log_A[c] = -sgh * decay * dt * A;
+  if (d_log_dt) d_log_dt[c] = (sge - sgh * decay * A) * sig;
+}
+
 // ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
@@ -286,6 +339,26 @@ int launch_rmsnorm(const uint16_t* x, int64_t N, int d, const float* scale, floa
                    hipStream_t st) {
   if (N == 0) return 0;
   hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, x, N, d, scale, eps, out);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+size_t injection_bwd_bytes(int64_t N, int d) {
+  return (size_t)((N + RMS_BWD_ROWS - 1) / RMS_BWD_ROWS) * 2 * (size_t)d * 4;
+}
+
+int launch_injection_bwd(const uint16_t* g, const uint16_t* h, const uint16_t* e, const float* log_A,
+                         const float* log_dt, int64_t N, int d, uint16_t* dh, uint16_t* de, float* d_log_A,
+                         float* d_log_dt, float* part, hipStream_t st) {
+  const int64_t nblk = (N + RMS_BWD_ROWS - 1) / RMS_BWD_ROWS;
+  if (nblk > 0x7fffffff || d <= 0) return -2;
+  if (nblk > 0) {
+    hipLaunchKernelGGL(injection_bwd_kernel, dim3((unsigned)nblk), dim3(256), 0, st, g, h, e, log_A, log_dt, N, d,
+                       dh, de, part);
+    if (hipGetLastError() != hipSuccess) return -1;
+  }
+  if (d_log_A || d_log_dt)
+    hipLaunchKernelGGL(injection_param_grad_kernel, dim3((unsigned)((d + 255) / 256)), dim3(256), 0, st, part,
+                       (int)nblk, d, log_A, log_dt, d_log_A, d_log_dt);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

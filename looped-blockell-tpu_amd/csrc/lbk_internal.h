@@ -128,6 +128,10 @@ int launch_rmsnorm_bwd(const uint16_t* x, const uint16_t* dy, int64_t N, int d, 
                        uint16_t* dx, float* dscale, float* part, hipStream_t st);
 int launch_injection(const uint16_t* h, const uint16_t* e, const float* log_A, const float* log_dt, int64_t N,
                      int d, uint16_t* out, hipStream_t st);
+size_t injection_bwd_bytes(int64_t N, int d);   // fp32 column partials (two per row block)
+int launch_injection_bwd(const uint16_t* g, const uint16_t* h, const uint16_t* e, const float* log_A,
+                         const float* log_dt, int64_t N, int d, uint16_t* dh, uint16_t* de, float* d_log_A,
+                         float* d_log_dt, float* part, hipStream_t st);
 
 // ---- ternary / int8
 int launch_quantize_act(const uint16_t* x, int64_t N, int F, int64_t ldx, int8_t* xq, float* sx, hipStream_t st);

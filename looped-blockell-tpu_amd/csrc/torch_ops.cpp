@@ -295,6 +295,29 @@ at::Tensor diagonal_injection(const at::Tensor& h_, const at::Tensor& e_, const 
   return out;
 }
 
+// (dh, de, d_log_A, d_log_dt) of diagonal_injection for grad_out
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> diagonal_injection_bwd(
+    const at::Tensor& dy_, const at::Tensor& h_, const at::Tensor& e_, const at::Tensor& log_A,
+    const at::Tensor& log_dt) {
+  const char* op = "diagonal_injection_bwd";
+  at::Tensor dy = check_x2d(dy_, op), h = check_x2d(h_, op), e = check_x2d(e_, op);
+  TORCH_CHECK(e.sizes() == h.sizes() && dy.sizes() == h.sizes(), "titan::diagonal_injection_bwd: grad_out, h and e "
+              "must have one shape");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(h.device());
+  at::Tensor la = log_A.to(h.device(), at::kFloat).contiguous(), ld = log_dt.to(h.device(), at::kFloat).contiguous();
+  TORCH_CHECK(la.numel() == h.size(1) && ld.numel() == h.size(1),
+              "titan::diagonal_injection_bwd: log_A/log_dt must be [d_model]");
+  at::Tensor dh = at::empty_like(h), de = at::empty_like(h);
+  at::Tensor dla = at::empty({h.size(1)}, h.options().dtype(at::kFloat)), dld = at::empty_like(dla);
+  const size_t wsb = lbk_diagonal_injection_bwd_workspace_bytes(h.size(0), (int32_t)h.size(1));
+  at::Tensor ws = workspace(wsb, h);
+  LBK_CALL("diagonal_injection_bwd",
+           lbk_diagonal_injection_bwd_bf16(bf(dy), bf(h), bf(e), la.data_ptr<float>(), ld.data_ptr<float>(), h.size(0),
+                                           (int32_t)h.size(1), bfm(dh), bfm(de), dla.data_ptr<float>(),
+                                           dld.data_ptr<float>(), ws.data_ptr(), wsb, cur_stream(h)));
+  return {dh, de, dla, dld};
+}
+
 at::Tensor looped_impl(const at::Tensor& h, const at::Tensor& scale_, at::Tensor vg, at::Tensor cg, at::Tensor vu,
                        at::Tensor cu, at::Tensor vd, at::Tensor cd, int64_t L, double eps, const char* op,
                        int path = 0) {
@@ -673,6 +696,8 @@ TORCH_LIBRARY(titan, m) {
   m.def("rmsnorm(Tensor x, Tensor scale, float eps=1e-05) -> Tensor");
   m.def("rmsnorm_bwd(Tensor grad_out, Tensor x, Tensor scale, float eps=1e-05) -> (Tensor, Tensor)");
   m.def("diagonal_injection(Tensor h, Tensor e, Tensor log_A, Tensor log_dt) -> Tensor");
+  m.def("diagonal_injection_bwd(Tensor grad_out, Tensor h, Tensor e, Tensor log_A, Tensor log_dt) "
+        "-> (Tensor, Tensor, Tensor, Tensor)");
   m.def("quantize_act_int8(Tensor x) -> (Tensor, Tensor)");
   m.def("pack_ternary(Tensor t) -> Tensor");
   m.def("ternary_quantize_weights(Tensor values) -> (Tensor, Tensor)");
@@ -710,6 +735,7 @@ TORCH_LIBRARY_IMPL(titan, CUDA, m) {
   m.impl("rmsnorm", &rmsnorm);
   m.impl("rmsnorm_bwd", &rmsnorm_bwd);
   m.impl("diagonal_injection", &diagonal_injection);
+  m.impl("diagonal_injection_bwd", &diagonal_injection_bwd);
   m.impl("quantize_act_int8", &quantize_act_int8);
   m.impl("pack_ternary", &pack_ternary);
   m.impl("ternary_quantize_weights", &ternary_quantize_weights);
@@ -732,7 +758,8 @@ TORCH_LIBRARY_IMPL(titan, Autograd, m) {
         "persistent_mlp_step", "block_ell_matmul", "block_ell_matmul_bwd", "block_ell_swiglu_bwd_ex",
         "looped_swiglu", "looped_swiglu_persistent", "looped_swiglu_launches", "rmsnorm", "rmsnorm_bwd",
         "block_ell_swiglu_fwd_bias", "block_ell_swiglu_bwd_bias", "looped_swiglu_bias",
-        "block_ell_swiglu_prepack", "block_ell_swiglu_fwd_prepacked", "diagonal_injection", "quantize_act_int8", "pack_ternary", "ternary_quantize_weights", "ternary_matmul",
+        "block_ell_swiglu_prepack", "block_ell_swiglu_fwd_prepacked", "diagonal_injection", "diagonal_injection_bwd",
+        "quantize_act_int8", "pack_ternary", "ternary_quantize_weights", "ternary_matmul",
         "block_ell_swiglu_fwd_ternary", "block_ell_swiglu_fwd_ternary_with_intermediate",
         "block_ell_swiglu_fwd_ternary_accumulators"})
     m.impl(name, torch::autograd::autogradNotImplementedFallback());
@@ -814,6 +841,11 @@ TORCH_LIBRARY_IMPL(titan, Meta, m) {
   m.impl("rmsnorm", [](const at::Tensor& x, const at::Tensor&, double) { return at::empty_like(x); });
   m.impl("rmsnorm_bwd", [](const at::Tensor&, const at::Tensor& x, const at::Tensor&, double) {
     return std::make_tuple(at::empty_like(x), at::empty({x.size(1)}, x.options().dtype(at::kFloat)));
+  });
+  m.impl("diagonal_injection_bwd", [](const at::Tensor&, const at::Tensor& h, const at::Tensor&, const at::Tensor&,
+                                      const at::Tensor&) {
+    auto f = h.options().dtype(at::kFloat);
+    return std::make_tuple(at::empty_like(h), at::empty_like(h), at::empty({h.size(1)}, f), at::empty({h.size(1)}, f));
   });
   m.impl("diagonal_injection", [](const at::Tensor& h, const at::Tensor&, const at::Tensor&, const at::Tensor&) {
     return at::empty_like(h);

@@ -80,6 +80,8 @@ SIGNATURES = {
     "lbk_swiglu_fwd_bf16_noalloc": (C.c_int, [_P, _I64, _I32, _PB, _PB, _PB, C.c_int, _P, _P]),
     "lbk_swiglu_fwd_bias_bf16": (C.c_int, [_P, _I64, _I32, _PB, _PB, _PB, _P, _P, _P, C.c_int, _P, _P, _P, _P, _P,
                                            _SZ, _P]),
+    "lbk_diagonal_injection_bwd_workspace_bytes": (_SZ, [_I64, _I32]),
+    "lbk_diagonal_injection_bwd_bf16": (C.c_int, [_P, _P, _P, _P, _P, _I64, _I32, _P, _P, _P, _P, _P, _SZ, _P]),
     "lbk_swiglu_prepacked_bytes": (_SZ, [_I32, _PB, _PB, _PB]),
     "lbk_swiglu_prepack_bf16": (C.c_int, [_I32, _PB, _PB, _PB, _P, _SZ, _P]),
     "lbk_swiglu_prepacked_workspace_bytes": (_SZ, [_I64, _I32, _PB, _PB, _PB, C.c_int]),

@@ -264,8 +264,28 @@ def rmsnorm_bwd(grad_out, x, scale, eps: float = 1e-5):
     return ops().rmsnorm_bwd(grad_out, x, scale, eps)
 
 
+class _InjectionFunction(torch.autograd.Function):
+    """Differentiable diagonal injection: the backward is ``titan::diagonal_injection_bwd`` (dh, de
+    and the deterministic per-feature gradients of log_A and log_dt)."""
+
+    @staticmethod
+    def forward(ctx, h, e, log_A, log_dt):
+        ctx.save_for_backward(h, e, log_A, log_dt)
+        return ops().diagonal_injection(h, e, log_A, log_dt)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        h, e, log_A, log_dt = ctx.saved_tensors
+        dh, de, dla, dld = ops().diagonal_injection_bwd(grad_out.to(torch.bfloat16).contiguous(), h, e, log_A, log_dt)
+        return dh, de, dla.to(log_A.dtype), dld.to(log_dt.dtype)
+
+
 def diagonal_injection(h, e, log_A, log_dt):
+    """``decay * h + dt * e`` per feature (``titan::diagonal_injection``), differentiable in all four
+    inputs when gradients are enabled."""
     _gpu(h, e)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (h, e, log_A, log_dt)):
+        return _InjectionFunction.apply(h, e, log_A, log_dt)
     return ops().diagonal_injection(h, e, log_A, log_dt)
 
 

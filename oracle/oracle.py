@@ -31,6 +31,7 @@ __all__ = [
     "permute_optimizer_rows", "transposed_index",
     "block_ell_to_dense", "create_block_ell_from_dense", "block_ell_matmul",
     "silu", "swiglu_fwd", "gelu_tanh", "gelu_mlp_fwd", "rmsnorm", "rmsnorm_bwd", "looped_swiglu",
+    "diagonal_injection", "diagonal_injection_bwd",
     "block_ell_matmul_t", "swiglu_bias_grads",
     "block_ell_weight_grad", "swiglu_bwd", "alive_slots", "compact_topology", "column_importance",
     "column_permutation", "apply_permutation", "k_active_macros", "ternary_quantize_blocks",
@@ -259,6 +260,31 @@ def rmsnorm_bwd(x: np.ndarray, scale: np.ndarray, dy: np.ndarray, eps: float = 1
     dx = rs * scale * dy - x * rs ** 3 * dot
     dscale = np.sum((dy * x * rs).reshape(-1, x.shape[-1]), axis=0)
     return dx, dscale
+
+
+def diagonal_injection(h, e, log_A, log_dt):
+    """``decay * h + dt * e`` with ``dt = softplus(log_dt)``, ``decay = exp(-dt * exp(log_A))``
+    per feature (``interop/pt_model.py:923-935``, ``DiagonalInjection.forward``)."""
+    dt = np.log1p(np.exp(np.asarray(log_dt, dtype=np.float64)))
+    decay = np.exp(-dt * np.exp(np.asarray(log_A, dtype=np.float64)))
+    return decay * h + dt * e
+
+
+def diagonal_injection_bwd(h, e, log_A, log_dt, dy):
+    """Gradients of :func:`diagonal_injection` for an output gradient ``dy`` (the chain rule of
+    ``interop/pt_model.py:931-935``): ``dh = decay * dy``, ``de = dt * dy``,
+    ``dlog_A = -sum_n dy * h * decay * dt * A`` and
+    ``dlog_dt = sum_n dy * (e - h * decay * A) * sigmoid(log_dt)`` with ``A = exp(log_A)``.
+    Returns ``(dh, de, dlog_A, dlog_dt)``."""
+    la = np.asarray(log_A, dtype=np.float64)
+    ld = np.asarray(log_dt, dtype=np.float64)
+    A = np.exp(la)
+    dt = np.log1p(np.exp(ld))
+    decay = np.exp(-dt * A)
+    sig = 1.0 / (1.0 + np.exp(-ld))
+    sgh = np.sum(dy * h, axis=0)
+    sge = np.sum(dy * e, axis=0)
+    return decay * dy, dt * dy, -sgh * decay * dt * A, (sge - sgh * decay * A) * sig
 
 
 def looped_swiglu(h, norm_scale, gate, up, down, L: int, eps: float = 1e-5, state_round=None, biases=None):
@@ -694,6 +720,9 @@ PINS = {
     "swiglu_bias_grads": "torch float64 autograd of the dense biased SwiGLU FFN (the three bias gradients)",
     "rmsnorm": "constant-vector closed form; unit-RMS invariance; scale linearity",
     "looped_swiglu": "L=0 identity; L=1 equals one block; L=2 equals composition",
+    "diagonal_injection": "closed forms: log_A = -inf keeps h, log_dt = log(e - 1) gives dt = 1; torch's "
+                          "DiagonalInjection formula in float64",
+    "diagonal_injection_bwd": "torch float64 autograd of the injection (h, e, log_A, log_dt); finite differences",
     "block_ell_matmul_t": "== dy @ W of block_ell_to_dense; adjoint identity <A x, y> = <x, A^T y>; sentinel 0",
     "block_ell_weight_grad": "== torch autograd of block_ell_matmul through the dense weight, gathered per tile",
     "swiglu_bwd": "== torch float64 autograd of the dense SwiGLU FFN with residual (x and every tile); "

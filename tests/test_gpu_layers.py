@@ -242,3 +242,42 @@ def test_graph_capture_replays(gpu, shape):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, ref), f"replay {rep} differs"
+
+
+def test_diagonal_injection_backward(gpu):
+    """Gradients of the injection (h, e, log_A, log_dt) through the autograd wrapper against the
+    float64 oracle; the C ABI entry with optional outputs; bit-identical repeated calls."""
+    import ctypes as C
+    from looped_blockell import kernels
+    rng = np.random.default_rng(61)
+    N, d = 130, 384                      # three 64-row blocks, the last ragged
+    h, e, dy = T.act(rng, N, d), T.act(rng, N, d), T.act(rng, N, d)
+    la = (0.3 * rng.standard_normal(d)).astype(np.float32)
+    ld = (0.5 * rng.standard_normal(d)).astype(np.float32)
+    th, te = T.to_gpu_bf16(h).requires_grad_(True), T.to_gpu_bf16(e).requires_grad_(True)
+    tla, tld = T.to_gpu(la).requires_grad_(True), T.to_gpu(ld).requires_grad_(True)
+    out = kernels.diagonal_injection(th, te, tla, tld)
+    out.backward(T.to_gpu_bf16(dy))
+    ref = O.diagonal_injection_bwd(h.astype(np.float64), e.astype(np.float64), la.astype(np.float64),
+                                   ld.astype(np.float64), dy.astype(np.float64))
+    for got, want, tol in ((th.grad, ref[0], TOL), (te.grad, ref[1], TOL), (tla.grad, ref[2], 1e-4),
+                           (tld.grad, ref[3], 1e-4)):
+        assert T.rel_err(T.to_np(got), want)[0] <= tol
+    # through the C ABI: only the parameter gradients, twice, bit-identical
+    A = T.abi()
+    lib = A.load()
+    wsb = lib.lbk_diagonal_injection_bwd_workspace_bytes(N, d)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    res = []
+    tdy = T.to_gpu_bf16(dy)
+    for _ in range(2):
+        g1, g2 = torch.empty(d, device="cuda"), torch.empty(d, device="cuda")
+        A.check(lib.lbk_diagonal_injection_bwd_bf16(T.ptr(tdy), T.ptr(th.detach()), T.ptr(te.detach()),
+                                                    T.ptr(tla.detach()), T.ptr(tld.detach()), N, d, None, None,
+                                                    T.ptr(g1), T.ptr(g2), T.ptr(ws), wsb, T.stream()), "inj_bwd")
+        torch.cuda.synchronize()
+        res.append((g1, g2))
+    assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
+    assert torch.equal(res[0][0], tla.grad) and torch.equal(res[0][1], tld.grad)
+    assert lib.lbk_diagonal_injection_bwd_bf16(None, None, None, T.ptr(tla.detach()), T.ptr(tld.detach()), N, d,
+                                               None, None, None, None, T.ptr(ws), wsb, T.stream()) == A.LBK_ERR_NULL

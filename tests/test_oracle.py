@@ -794,3 +794,47 @@ def test_torch_cpu_ternary_matches_oracle():
     # h is re-quantised: a float32 vs float64 h can flip a rounding of hq, which moves the output by
     # one int8 step of one token's hidden value times a weight, far below the tolerance used here
     assert np.abs(got - res["out"]).max() <= 1e-3 * np.abs(res["out"]).max()
+
+
+# ---------------------------------------------------------------- diagonal injection
+
+def test_diagonal_injection_closed_forms_and_torch():
+    import torch
+    r = rng(51)
+    n, d = 7, 12
+    h, e = r.standard_normal((n, d)), r.standard_normal((n, d))
+    la, ld = 0.3 * r.standard_normal(d), 0.5 * r.standard_normal(d)
+    # log_A -> -inf: A -> 0, decay -> 1; log_dt = log(e - 1): dt = 1 exactly
+    out = O.diagonal_injection(h, e, np.full(d, -np.inf), np.full(d, math.log(math.e - 1)))
+    np.testing.assert_allclose(out, h + e, rtol=1e-12, atol=1e-12)
+    # the reference's PyTorch formula (interop/pt_model.py:931-935), in float64
+    tl, td = torch.tensor(la), torch.tensor(ld)
+    A = -torch.exp(tl)
+    dt = torch.nn.functional.softplus(td)
+    ref = (torch.exp(dt * A) * torch.tensor(h) + dt * torch.tensor(e)).numpy()
+    np.testing.assert_allclose(O.diagonal_injection(h, e, la, ld), ref, rtol=1e-12, atol=1e-12)
+
+
+def test_diagonal_injection_bwd_autograd_and_finite_differences():
+    import torch
+    r = rng(52)
+    n, d = 9, 10
+    h, e, dy = r.standard_normal((n, d)), r.standard_normal((n, d)), r.standard_normal((n, d))
+    la, ld = 0.3 * r.standard_normal(d), 0.5 * r.standard_normal(d)
+    th, te, tla, tld = (torch.tensor(a, requires_grad=True) for a in (h, e, la, ld))
+    A = -torch.exp(tla)
+    dt = torch.nn.functional.softplus(tld)
+    out = torch.exp(dt * A) * th + dt * te
+    out.backward(torch.tensor(dy))
+    got = O.diagonal_injection_bwd(h, e, la, ld, dy)
+    for g, t in zip(got, (th, te, tla, tld)):
+        np.testing.assert_allclose(g, t.grad.numpy(), rtol=1e-10, atol=1e-12)
+    eps = 1e-6
+    for j in (0, 4, 9):
+        for which in (2, 3):
+            p = [la.copy(), ld.copy()]
+            p[which - 2][j] += eps
+            up = np.sum(dy * O.diagonal_injection(h, e, *p))
+            p[which - 2][j] -= 2 * eps
+            dn = np.sum(dy * O.diagonal_injection(h, e, *p))
+            assert abs((up - dn) / (2 * eps) - got[which][j]) < 1e-6
