@@ -427,6 +427,33 @@ int lbk_swiglu_fwd_ternary_acc(const int8_t* xq, const float* sx, int64_t N, int
                                void* stream);
 
 /*
+ * Ternary weights prepared once.  The B = 64 two-kernel ternary path re-encodes the packed
+ * tiles per call (fragment-major words in the t + 1 encoding, the per-row fixed-point scales);
+ * a caller whose weights stay fixed builds them once with lbk_ternary_prepare into a buffer of
+ * lbk_ternary_prepared_bytes and passes it to lbk_swiglu_fwd_ternary_prepared (same kernels,
+ * same results as lbk_swiglu_fwd_ternary_acc; acc may be NULL; the workspace then holds only
+ * the h maxima and h: lbk_ternary_prepared_workspace_bytes).  The buffer reflects packed,
+ * scales and col_idx at the time of the call: prepare again after any of them changes.
+ * lbk_ternary_prepared_bytes returns 0 for geometries without a prepared form (the prepare is a
+ * no-op and the forward ignores the buffer).  No counterpart in the reference, which has no
+ * ternary Block-ELL kernel (bonsai-test/bitlinear.py:132-138 dequantises and runs F.linear).
+ */
+size_t lbk_ternary_prepared_bytes(int32_t d_model, const lbk_bell_ternary* gate,
+                                  const lbk_bell_ternary* up, const lbk_bell_ternary* down);
+int lbk_ternary_prepare(int32_t d_model, const lbk_bell_ternary* gate, const lbk_bell_ternary* up,
+                        const lbk_bell_ternary* down, void* prepared, size_t prepared_bytes,
+                        void* stream);
+size_t lbk_ternary_prepared_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell_ternary* gate,
+                                            const lbk_bell_ternary* up, const lbk_bell_ternary* down);
+int lbk_swiglu_fwd_ternary_prepared(const int8_t* xq, const float* sx, int64_t N, int32_t d_model,
+                                    const lbk_bell_ternary* gate, const lbk_bell_ternary* up,
+                                    const lbk_bell_ternary* down, const void* prepared,
+                                    size_t prepared_bytes, const uint16_t* x_resid, uint16_t* out,
+                                    uint16_t* h_out, int8_t* hq_out, float* sh_out,
+                                    const lbk_ternary_acc* acc, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+
+/*
  * Backward of the Block-ELL product y = x W^T (bias excluded): dx = grad_out W (tile [B_in, B_out]
  * of slot (r, k) sends grad_out[:, r] back to column block col[r,k]) and, per tile,
  * d_values[r,k] = x[:, col]^T grad_out[:, r] (zero for dead slots).  grad_out [N, R*B],

@@ -599,11 +599,21 @@ int lbk_swiglu_fwd_ternary(const int8_t* xq, const float* sx, int64_t N, int32_t
                                     workspace, workspace_bytes, stream);
 }
 
-int lbk_swiglu_fwd_ternary_acc(const int8_t* xq, const float* sx, int64_t N, int32_t d_model,
-                               const lbk_bell_ternary* gate, const lbk_bell_ternary* up,
-                               const lbk_bell_ternary* down, const uint16_t* x_resid, uint16_t* out,
-                               uint16_t* h_out, int8_t* hq_out, float* sh_out, const lbk_ternary_acc* acc,
-                               void* workspace, size_t workspace_bytes, void* stream) {
+// prepared weights of the B = 64 two-kernel path: gate | up | down regions of tprep_bytes each
+static size_t tern_prepared_bytes(const lbk_bell_ternary* gate, const lbk_bell_ternary* up,
+                                  const lbk_bell_ternary* down) {
+  const TernSplitLayout L = tern_split_layout(1, gate, up, down);
+  return L.pg + L.pu + L.pd;
+}
+
+// The ternary forward behind lbk_swiglu_fwd_ternary_acc and lbk_swiglu_fwd_ternary_prepared:
+// `prepared` (may be null) holds the weights of lbk_ternary_prepare, otherwise the two-kernel
+// path prepares them into the workspace.
+static int tern_fwd_impl(const int8_t* xq, const float* sx, int64_t N, int32_t d_model, const lbk_bell_ternary* gate,
+                         const lbk_bell_ternary* up, const lbk_bell_ternary* down, const char* prepared,
+                         size_t prepared_bytes, const uint16_t* x_resid, uint16_t* out, uint16_t* h_out,
+                         int8_t* hq_out, float* sh_out, const lbk_ternary_acc* acc, void* workspace,
+                         size_t workspace_bytes, hipStream_t s) {
   int st;
   if ((st = check_tern(gate)) || (st = check_tern(up)) || (st = check_tern(down))) return st;
   int64_t d_ff = 0;
@@ -624,13 +634,20 @@ int lbk_swiglu_fwd_ternary_acc(const int8_t* xq, const float* sx, int64_t N, int
       if (p && !a16(p)) return LBK_ERR_ALIGN;
   }
   char* ws = static_cast<char*>(workspace);
-  hipStream_t s = S(stream);
 
   if (tern_split(N, d_model, gate, up, down)) {
     const TernSplitLayout L = tern_split_layout(N, gate, up, down);
-    if (!ws || workspace_bytes < L.total) return LBK_ERR_WORKSPACE;
+    // [prepared gate | up | down (unless given)] [per-slice maxima of h] [h]
+    const size_t pbytes = L.pg + L.pu + L.pd;
+    if (prepared) {
+      if (prepared_bytes < pbytes) return LBK_ERR_WORKSPACE;
+      if (!a16(prepared)) return LBK_ERR_ALIGN;
+    }
+    const size_t own = prepared ? 0 : pbytes;
+    if (!ws || workspace_bytes < L.total - pbytes + own) return LBK_ERR_WORKSPACE;
     if (!a16(ws)) return LBK_ERR_ALIGN;
-    uint16_t* h = h_out ? h_out : reinterpret_cast<uint16_t*>(ws + L.pg + L.pu + L.pd + L.hmax);
+    char* pb = prepared ? const_cast<char*>(prepared) : ws;
+    uint16_t* h = h_out ? h_out : reinterpret_cast<uint16_t*>(ws + own + L.hmax);
     if (!a16(h) || (hq_out && !a16(hq_out))) return LBK_ERR_ALIGN;
     const int C_in = d_model / gate->B;
     TGUArgs g{};
@@ -638,15 +655,15 @@ int lbk_swiglu_fwd_ternary_acc(const int8_t* xq, const float* sx, int64_t N, int
     const TPrepWeight pw[3] = {{gate->packed, gate->scales, gate->col_idx, gate->R, gate->K, C_in},
                                {up->packed, up->scales, up->col_idx, up->R, up->K, C_in},
                                {down->packed, down->scales, down->col_idx, down->R, down->K, gate->R}};
-    void* const po[3] = {ws, ws + L.pg, ws + L.pg + L.pu};
+    void* const po[3] = {pb, pb + L.pg, pb + L.pg + L.pu};
     const tu32x4* ptw[3];
     const int32_t* pm[3];
     const float* pr[3];
-    if (launch_tprep(pw, po, ptw, pm, pr, s) != 0) return LBK_ERR_LAUNCH;
+    if (launch_tprep(pw, po, ptw, pm, pr, s, prepared == nullptr) != 0) return LBK_ERR_LAUNCH;
     g.twg = ptw[0]; g.mg = pm[0]; g.rmg = pr[0];
     g.twu = ptw[1]; g.mu = pm[1]; g.rmu = pr[1];
     d.twd = ptw[2]; d.md = pm[2]; d.rmd = pr[2];
-    float* hmax = reinterpret_cast<float*>(ws + L.pg + L.pu + L.pd);
+    float* hmax = reinterpret_cast<float*>(ws + own);
     g.xq = xq; g.sx = sx; g.N = N; g.d_model = d_model;
     g.cg = gate->col_idx; g.cu = up->col_idx; g.K = gate->K;
     g.R_ff = gate->R; g.H = tgu_slices(N); g.h = h; g.hmax = hmax;
@@ -684,6 +701,65 @@ int lbk_swiglu_fwd_ternary_acc(const int8_t* xq, const float* sx, int64_t N, int
   d.R = down->R; d.resid = x_resid; d.y = out; d.acc0 = ax.acc_down;
   if (launch_ternary(gate->B, 0, d, s) != 0) return LBK_ERR_LAUNCH;
   return LBK_OK;
+}
+
+int lbk_swiglu_fwd_ternary_acc(const int8_t* xq, const float* sx, int64_t N, int32_t d_model,
+                               const lbk_bell_ternary* gate, const lbk_bell_ternary* up,
+                               const lbk_bell_ternary* down, const uint16_t* x_resid, uint16_t* out,
+                               uint16_t* h_out, int8_t* hq_out, float* sh_out, const lbk_ternary_acc* acc,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  return tern_fwd_impl(xq, sx, N, d_model, gate, up, down, nullptr, 0, x_resid, out, h_out, hq_out, sh_out, acc,
+                       workspace, workspace_bytes, S(stream));
+}
+
+size_t lbk_ternary_prepared_bytes(int32_t d_model, const lbk_bell_ternary* gate, const lbk_bell_ternary* up,
+                                  const lbk_bell_ternary* down) {
+  if (!gate || !up || !down) return 0;
+  if (check_tern(gate) || check_tern(up) || check_tern(down)) return 0;
+  int64_t d_ff = 0;
+  if (check_ffn(gate, up, down, d_model, &d_ff)) return 0;
+  return tern_split(1, d_model, gate, up, down) ? tern_prepared_bytes(gate, up, down) : 0;
+}
+
+int lbk_ternary_prepare(int32_t d_model, const lbk_bell_ternary* gate, const lbk_bell_ternary* up,
+                        const lbk_bell_ternary* down, void* prepared, size_t prepared_bytes, void* stream) {
+  int st;
+  if ((st = check_tern(gate)) || (st = check_tern(up)) || (st = check_tern(down))) return st;
+  int64_t d_ff = 0;
+  if ((st = check_ffn(gate, up, down, d_model, &d_ff))) return st;
+  if (!tern_split(1, d_model, gate, up, down)) return LBK_OK;        // no prepared form for this geometry
+  const TernSplitLayout L = tern_split_layout(1, gate, up, down);
+  if (!prepared || prepared_bytes < L.pg + L.pu + L.pd) return LBK_ERR_WORKSPACE;
+  if (!a16(prepared)) return LBK_ERR_ALIGN;
+  char* pb = static_cast<char*>(prepared);
+  const int C_in = d_model / gate->B;
+  const TPrepWeight pw[3] = {{gate->packed, gate->scales, gate->col_idx, gate->R, gate->K, C_in},
+                             {up->packed, up->scales, up->col_idx, up->R, up->K, C_in},
+                             {down->packed, down->scales, down->col_idx, down->R, down->K, gate->R}};
+  void* const po[3] = {pb, pb + L.pg, pb + L.pg + L.pu};
+  const tu32x4* ptw[3];
+  const int32_t* pm[3];
+  const float* pr[3];
+  return launch_tprep(pw, po, ptw, pm, pr, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+size_t lbk_ternary_prepared_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell_ternary* gate,
+                                            const lbk_bell_ternary* up, const lbk_bell_ternary* down) {
+  const size_t all = lbk_ternary_swiglu_workspace_bytes(N, d_model, gate, up, down);
+  if (all == 0 || !tern_split(N, d_model, gate, up, down)) return all;
+  return all - tern_prepared_bytes(gate, up, down);
+}
+
+int lbk_swiglu_fwd_ternary_prepared(const int8_t* xq, const float* sx, int64_t N, int32_t d_model,
+                                    const lbk_bell_ternary* gate, const lbk_bell_ternary* up,
+                                    const lbk_bell_ternary* down, const void* prepared, size_t prepared_bytes,
+                                    const uint16_t* x_resid, uint16_t* out, uint16_t* h_out, int8_t* hq_out,
+                                    float* sh_out, const lbk_ternary_acc* acc, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  if (!gate || !up || !down) return LBK_ERR_NULL;
+  if (N > 0 && !prepared && tern_split(N, d_model, gate, up, down)) return LBK_ERR_NULL;
+  return tern_fwd_impl(xq, sx, N, d_model, gate, up, down, static_cast<const char*>(prepared), prepared_bytes,
+                       x_resid, out, h_out, hq_out, sh_out, acc, workspace, workspace_bytes, S(stream));
 }
 
 // ---- backward of the SwiGLU FFN

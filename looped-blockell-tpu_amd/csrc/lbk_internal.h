@@ -190,9 +190,11 @@ struct TPrepJobs {
   TPrepJob job[3];
   int64_t first[3];   // first workgroup of each weight
 };
-// prepares gate, up and down (w[0..2]) into out[0..2] (tprep_bytes each) in one launch
+// prepares gate, up and down (w[0..2]) into out[0..2] (tprep_bytes each) in one launch; with
+// run = false only the pointers into out are returned (weights prepared earlier)
 int launch_tprep(const TPrepWeight (&w)[3], void* const (&out)[3], const tu32x4* (&tw)[3],
-                 const int32_t* (&mval)[3], const float* (&rmul)[3], hipStream_t st);
+                 const int32_t* (&mval)[3], const float* (&rmul)[3], hipStream_t st,
+                 bool run = true);
 bool tsplit_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd);
 int tgu_slices(int64_t N);
 int launch_tgu(const TGUArgs& a, hipStream_t st);

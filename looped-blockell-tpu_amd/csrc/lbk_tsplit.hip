@@ -632,7 +632,7 @@ size_t tprep_bytes(int64_t ntiles, int R) {
 }
 
 int launch_tprep(const TPrepWeight (&w)[3], void* const (&out)[3], const u32x4* (&tw)[3],
-                 const int32_t* (&mval)[3], const float* (&rmul)[3], hipStream_t st) {
+                 const int32_t* (&mval)[3], const float* (&rmul)[3], hipStream_t st, bool run) {
   auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
   TPrepJobs J{};
   int64_t blocks = 0;
@@ -652,6 +652,7 @@ int launch_tprep(const TPrepWeight (&w)[3], void* const (&out)[3], const u32x4* 
     blocks += nt + 1;
   }
   if (blocks > 0x7fffffff) return -2;
+  if (!run) return 0;
   hipLaunchKernelGGL(tprep_kernel, dim3((unsigned)blocks), dim3(64), 0, st, J);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -472,10 +472,11 @@ std::tuple<at::Tensor, at::Tensor> ternary_matmul(const at::Tensor& xq_, const a
 std::vector<at::Tensor> tern_swiglu_impl(const at::Tensor& xq_, const at::Tensor& sx_, at::Tensor pg, at::Tensor sg,
                                          at::Tensor cg, at::Tensor pu, at::Tensor su, at::Tensor cu, at::Tensor pd,
                                          at::Tensor sd, at::Tensor cd, const c10::optional<at::Tensor>& x_resid,
-                                         bool inter, bool accs = false) {
-  const char* op = accs    ? "block_ell_swiglu_fwd_ternary_accumulators"
-                   : inter ? "block_ell_swiglu_fwd_ternary_with_intermediate"
-                           : "block_ell_swiglu_fwd_ternary";
+                                         bool inter, bool accs = false, const at::Tensor* prepared = nullptr) {
+  const char* op = prepared ? "block_ell_swiglu_fwd_ternary_prepared"
+                   : accs   ? "block_ell_swiglu_fwd_ternary_accumulators"
+                   : inter  ? "block_ell_swiglu_fwd_ternary_with_intermediate"
+                            : "block_ell_swiglu_fwd_ternary";
   inter = inter || accs;
   at::Tensor xq = check_int8_x(xq_, sx_, op);
   at::Tensor sx = sx_.contiguous();
@@ -520,6 +521,22 @@ std::vector<at::Tensor> tern_swiglu_impl(const at::Tensor& xq_, const at::Tensor
                           gp.data_ptr<float>(), up.data_ptr<float>()};
     for (const at::Tensor& t : {ag, au, ad, gp, up}) res.push_back(t);
   }
+  if (prepared) {
+    check_gpu(*prepared, op, "prepared");
+    TORCH_CHECK(prepared->scalar_type() == at::kByte && prepared->dim() == 1 && prepared->is_contiguous(), "titan::",
+                op, ": prepared must be the contiguous uint8 tensor of ternary_prepare");
+    const size_t need = lbk_ternary_prepared_bytes((int32_t)d_model, &g, &u, &d);
+    TORCH_CHECK((size_t)prepared->numel() >= need, "titan::", op, ": prepared holds ", prepared->numel(),
+                " bytes, this geometry needs ", need, " (prepare these weights with ternary_prepare)");
+    wsb = lbk_ternary_prepared_workspace_bytes(N, (int32_t)d_model, &g, &u, &d);
+    if (wsb) ws = workspace(wsb, xq);
+    LBK_CALL("block_ell_swiglu_fwd_ternary_prepared",
+             lbk_swiglu_fwd_ternary_prepared(xq.data_ptr<int8_t>(), sx.data_ptr<float>(), N, (int32_t)d_model, &g, &u,
+                                             &d, need ? prepared->data_ptr() : nullptr, (size_t)prepared->numel(), xrp,
+                                             bfm(out), h, hq, sh, accs ? &acc : nullptr,
+                                             wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(xq)));
+    return res;
+  }
   wsb = lbk_ternary_swiglu_workspace_bytes(N, (int32_t)d_model, &g, &u, &d);
   if (wsb) ws = workspace(wsb, xq);
   LBK_CALL("block_ell_swiglu_fwd_ternary",
@@ -552,6 +569,33 @@ tern_swiglu_accs(const at::Tensor& xq, const at::Tensor& sx, const at::Tensor& p
                  const c10::optional<at::Tensor>& x_resid) {
   auto r = tern_swiglu_impl(xq, sx, pg, sg, cg, pu, su, cu, pd, sd, cd, x_resid, true, true);
   return {r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7], r[8]};
+}
+
+// The B = 64 ternary path's prepared weights (uint8; empty when the geometry has none), built once
+// for weights that stay fixed; block_ell_swiglu_fwd_ternary_prepared then skips the per-call
+// preparation.  They reflect packed, scales and col_indices at the time of the call.
+at::Tensor ternary_prepare(const at::Tensor& pg_, const at::Tensor& sg_, const at::Tensor& cg_, const at::Tensor& pu_,
+                           const at::Tensor& su_, const at::Tensor& cu_, const at::Tensor& pd_, const at::Tensor& sd_,
+                           const at::Tensor& cd_) {
+  const char* op = "ternary_prepare";
+  at::Tensor pg = pg_, sg = sg_, cg = cg_, pu = pu_, su = su_, cu = cu_, pd = pd_, sd = sd_, cd = cd_;
+  check_gpu(pg, op, "gate");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pg.device());
+  lbk_bell_ternary g = make_tern(pg, sg, cg, op, "gate"), u = make_tern(pu, su, cu, op, "up"),
+                   d = make_tern(pd, sd, cd, op, "down");
+  const int32_t d_model = d.R * d.B;
+  const size_t bytes = lbk_ternary_prepared_bytes(d_model, &g, &u, &d);
+  at::Tensor prepared = at::empty({(int64_t)bytes}, pg.options().dtype(at::kByte));
+  if (bytes) LBK_CALL("ternary_prepare", lbk_ternary_prepare(d_model, &g, &u, &d, prepared.data_ptr(), bytes,
+                                                             cur_stream(pg)));
+  return prepared;
+}
+
+at::Tensor tern_swiglu_prepared(const at::Tensor& xq, const at::Tensor& sx, const at::Tensor& prepared,
+                                const at::Tensor& pg, const at::Tensor& sg, const at::Tensor& cg, const at::Tensor& pu,
+                                const at::Tensor& su, const at::Tensor& cu, const at::Tensor& pd, const at::Tensor& sd,
+                                const at::Tensor& cd, const c10::optional<at::Tensor>& x_resid) {
+  return tern_swiglu_impl(xq, sx, pg, sg, cg, pu, su, cu, pd, sd, cd, x_resid, false, false, &prepared)[0];
 }
 
 at::Tensor check_columns(const at::Tensor& c_, int64_t C) {
@@ -713,6 +757,11 @@ TORCH_LIBRARY(titan, m) {
         "Tensor ci_gate, Tensor p_up, Tensor s_up, Tensor ci_up, Tensor p_down, Tensor s_down, Tensor ci_down, "
         "Tensor? x_resid=None) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
   m.def("check_columns(Tensor col_indices, int C) -> Tensor");
+  m.def("ternary_prepare(Tensor p_gate, Tensor s_gate, Tensor ci_gate, Tensor p_up, Tensor s_up, Tensor ci_up, "
+        "Tensor p_down, Tensor s_down, Tensor ci_down) -> Tensor");
+  m.def("block_ell_swiglu_fwd_ternary_prepared(Tensor xq, Tensor sx, Tensor prepared, Tensor p_gate, Tensor s_gate, "
+        "Tensor ci_gate, Tensor p_up, Tensor s_up, Tensor ci_up, Tensor p_down, Tensor s_down, Tensor ci_down, "
+        "Tensor? x_resid=None) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(titan, CUDA, m) {
@@ -744,6 +793,8 @@ TORCH_LIBRARY_IMPL(titan, CUDA, m) {
   m.impl("block_ell_swiglu_fwd_ternary_with_intermediate", &tern_swiglu_inter);
   m.impl("block_ell_swiglu_fwd_ternary_accumulators", &tern_swiglu_accs);
   m.impl("check_columns", &check_columns);
+  m.impl("ternary_prepare", &ternary_prepare);
+  m.impl("block_ell_swiglu_fwd_ternary_prepared", &tern_swiglu_prepared);
 }
 
 TORCH_LIBRARY_IMPL(titan, CompositeExplicitAutograd, m) { m.impl("unpin_weights_l2", &unpin_weights_l2); }
@@ -761,7 +812,7 @@ TORCH_LIBRARY_IMPL(titan, Autograd, m) {
         "block_ell_swiglu_prepack", "block_ell_swiglu_fwd_prepacked", "diagonal_injection", "diagonal_injection_bwd",
         "quantize_act_int8", "pack_ternary", "ternary_quantize_weights", "ternary_matmul",
         "block_ell_swiglu_fwd_ternary", "block_ell_swiglu_fwd_ternary_with_intermediate",
-        "block_ell_swiglu_fwd_ternary_accumulators"})
+        "block_ell_swiglu_fwd_ternary_accumulators", "ternary_prepare", "block_ell_swiglu_fwd_ternary_prepared"})
     m.impl(name, torch::autograd::autogradNotImplementedFallback());
 }
 
@@ -871,6 +922,12 @@ TORCH_LIBRARY_IMPL(titan, Meta, m) {
          [](const at::Tensor& xq, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
             const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
             const at::Tensor&, const c10::optional<at::Tensor>&) {
+           return at::empty(xq.sizes(), xq.options().dtype(at::kBFloat16));
+         });
+  m.impl("block_ell_swiglu_fwd_ternary_prepared",
+         [](const at::Tensor& xq, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+            const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+            const at::Tensor&, const at::Tensor&, const c10::optional<at::Tensor>&) {
            return at::empty(xq.sizes(), xq.options().dtype(at::kBFloat16));
          });
   m.impl("block_ell_swiglu_fwd_ternary_with_intermediate",

@@ -112,6 +112,11 @@ SIGNATURES = {
     "lbk_swiglu_fwd_ternary": (C.c_int, [_P, _P, _I64, _I32, _PT, _PT, _PT, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "lbk_swiglu_fwd_ternary_acc": (C.c_int, [_P, _P, _I64, _I32, _PT, _PT, _PT, _P, _P, _P, _P, _P,
                                              C.POINTER(TernaryAcc), _P, _SZ, _P]),
+    "lbk_ternary_prepared_bytes": (_SZ, [_I32, _PT, _PT, _PT]),
+    "lbk_ternary_prepare": (C.c_int, [_I32, _PT, _PT, _PT, _P, _SZ, _P]),
+    "lbk_ternary_prepared_workspace_bytes": (_SZ, [_I64, _I32, _PT, _PT, _PT]),
+    "lbk_swiglu_fwd_ternary_prepared": (C.c_int, [_P, _P, _I64, _I32, _PT, _PT, _PT, _P, _SZ, _P, _P, _P, _P, _P,
+                                                  C.POINTER(TernaryAcc), _P, _SZ, _P]),
 }
 
 _lib = None

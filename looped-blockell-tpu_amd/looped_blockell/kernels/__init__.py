@@ -342,6 +342,20 @@ def ternary_swiglu_fwd(xq, sx, gate, up, down, x_resid=None):
     return ops().block_ell_swiglu_fwd_ternary(xq, sx, *gate, *up, *down, x_resid)
 
 
+def ternary_prepare(gate, up, down):
+    """``titan::ternary_prepare``: the prepared weights of the B = 64 ternary kernels, built once for
+    (packed, scales, col_indices) triples that stay fixed (uint8; empty when the geometry has no
+    prepared form).  Prepare again after any of them changes."""
+    _gpu(gate[0])
+    return ops().ternary_prepare(*gate, *up, *down)
+
+
+def ternary_swiglu_fwd_prepared(xq, sx, prepared, gate, up, down, x_resid=None):
+    """``ternary_swiglu_fwd`` from a ``ternary_prepare`` buffer (same kernels, same result)."""
+    _gpu(xq)
+    return ops().block_ell_swiglu_fwd_ternary_prepared(xq, sx, prepared, *gate, *up, *down, x_resid)
+
+
 def ternary_swiglu_fwd_with_intermediate(xq, sx, gate, up, down, x_resid=None):
     """Returns (out, h bf16, hq int8, sh fp32)."""
     _gpu(xq)

@@ -41,11 +41,30 @@ class TernaryBlockELLWeight(nn.Module):
 
 
 class TernaryMLPBlock(nn.Module):
-    """SwiGLU FFN with ternary gate/up/down weights; forward quantises x per token."""
+    """SwiGLU FFN with ternary gate/up/down weights; forward quantises x per token.
+
+    The kernels' prepared form of the three weights (``titan::ternary_prepare``) is cached on the
+    module and rebuilt when a packed, scales or col_indices buffer changes (tensor version
+    counters; writes through ``.data`` bypass them: call ``release_prepared()`` after those)."""
 
     def __init__(self, gate: TernaryBlockELLWeight, up: TernaryBlockELLWeight, down: TernaryBlockELLWeight):
         super().__init__()
         self.w_gate, self.w_up, self.w_down = gate, up, down
+        self._prepared = None
+
+    def prepared(self):
+        """The cached prepared weights, rebuilt when any weight buffer's version changes."""
+        bufs = [t for w in (self.w_gate, self.w_up, self.w_down) for t in w.triple()]
+        key = tuple((t.data_ptr(), t._version) for t in bufs)
+        if self._prepared is None or self._prepared[0] != key:
+            with torch.inference_mode(False):
+                self._prepared = (key, kernels.ternary_prepare(self.w_gate.triple(), self.w_up.triple(),
+                                                               self.w_down.triple()))
+        return self._prepared[1]
+
+    def release_prepared(self) -> None:
+        """Drop the cached prepared weights."""
+        self._prepared = None
 
     @classmethod
     def random(cls, d_model: int, d_ff: int, tile_size: int, density: float, device, seed: int = 0):
@@ -66,6 +85,6 @@ class TernaryMLPBlock(nn.Module):
         lead, d = x.shape[:-1], x.shape[-1]
         x2 = x.reshape(-1, d).to(torch.bfloat16).contiguous()
         xq, sx = kernels.quantize_act_int8(x2)
-        out = kernels.ternary_swiglu_fwd(xq, sx, self.w_gate.triple(), self.w_up.triple(), self.w_down.triple(),
-                                         x2 if add_residual else None)
+        out = kernels.ternary_swiglu_fwd_prepared(xq, sx, self.prepared(), self.w_gate.triple(), self.w_up.triple(),
+                                                  self.w_down.triple(), x2 if add_residual else None)
         return out.reshape(*lead, d)

@@ -284,3 +284,80 @@ def test_ternary_full_size_sampled_rows(gpu):
     assert np.array_equal(hq_r, hq_ref) and np.array_equal(sh_r, sh_ref)
     ref = O.ternary_swiglu_fwd(x[rows], g, u, d, exact_scales=True, h_round=O.bf16_round)
     assert T.rel_err(out, ref["out"])[0] <= TOL
+
+
+@pytest.mark.parametrize("case", [
+    # (d_model, d_ff, B, Kg, Kd, token counts, sentinel_frac)
+    (512, 2048, 64, 2, 7, (300, 17), 0.1),      # the B = 64 two-kernel path: prepared weights
+    (256, 1024, 32, 2, 8, (77, 5), 0.0),         # row-block path: no prepared form
+])
+def test_ternary_prepared_matches_per_call_preparation(gpu, case):
+    """lbk_ternary_prepare + lbk_swiglu_fwd_ternary_prepared against lbk_swiglu_fwd_ternary_acc (the
+    same kernels, bit-identical outputs and accumulators) on two calls in a row reusing one prepared
+    buffer; then the operator pair and TernaryMLPBlock's cache."""
+    import torch
+    from looped_blockell import kernels
+    d_model, d_ff, B, Kg, Kd, ns, frac = case
+    _say(f"ternary prepared {case}")
+    A = T.abi()
+    lib = A.load()
+    rng = np.random.default_rng(900 + B)
+    g = tern_weight(rng, d_ff // B, d_model // B, Kg, B, sentinel_frac=frac)
+    u = tern_weight(rng, d_ff // B, d_model // B, Kg, B, sentinel_frac=frac)
+    d = tern_weight(rng, d_model // B, d_ff // B, Kd, B, sentinel_frac=frac)
+    tw = [gpu_tern(w) for w in (g, u, d)]
+    gs, us, ds = (T.tern_struct(*w) for w in tw)
+    pb = lib.lbk_ternary_prepared_bytes(d_model, C.byref(gs), C.byref(us), C.byref(ds))
+    assert (pb > 0) == (B == 64)
+    prep = torch.empty(max(pb, 1), dtype=torch.uint8, device="cuda")
+    A.check(lib.lbk_ternary_prepare(d_model, C.byref(gs), C.byref(us), C.byref(ds), T.ptr(prep), pb, T.stream()),
+            "ternary_prepare")
+    for n in ns:
+        x = T.act(rng, n, d_model)
+        xq, sx = O.activation_quantize_int8(x)
+        txq, tsx, txr = T.to_gpu(xq), T.to_gpu(sx), T.to_gpu_bf16(x)
+        outs = []
+        for prepared in (False, True):
+            o = torch.empty(n, d_model, dtype=torch.bfloat16, device="cuda")
+            h = torch.empty(n, d_ff, dtype=torch.bfloat16, device="cuda")
+            accs = [torch.empty(n, f, dtype=dt, device="cuda") for f, dt in
+                    ((d_ff, torch.int32), (d_ff, torch.int32), (d_model, torch.int32), (d_ff, torch.float32),
+                     (d_ff, torch.float32))]
+            acc = A.TernaryAcc(*(T.ptr(t) for t in accs))
+            if prepared:
+                wsb = lib.lbk_ternary_prepared_workspace_bytes(n, d_model, C.byref(gs), C.byref(us), C.byref(ds))
+                ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
+                st = lib.lbk_swiglu_fwd_ternary_prepared(T.ptr(txq), T.ptr(tsx), n, d_model, C.byref(gs), C.byref(us),
+                                                         C.byref(ds), T.ptr(prep) if pb else None, pb, T.ptr(txr),
+                                                         T.ptr(o), T.ptr(h), None, None, C.byref(acc), T.ptr(ws), wsb,
+                                                         T.stream())
+            else:
+                wsb = lib.lbk_ternary_swiglu_workspace_bytes(n, d_model, C.byref(gs), C.byref(us), C.byref(ds))
+                ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
+                st = lib.lbk_swiglu_fwd_ternary_acc(T.ptr(txq), T.ptr(tsx), n, d_model, C.byref(gs), C.byref(us),
+                                                    C.byref(ds), T.ptr(txr), T.ptr(o), T.ptr(h), None, None,
+                                                    C.byref(acc), T.ptr(ws), wsb, T.stream())
+            A.check(st, "ternary forward")
+            torch.cuda.synchronize()
+            outs.append([o, h] + accs)
+        for a, b in zip(*outs):
+            assert torch.equal(a, b)
+        ref = O.ternary_swiglu_fwd(x, g, u, d, add_residual=True, exact_scales=True, h_round=O.bf16_round)
+        assert T.rel_err(T.to_np(outs[1][0]), ref["out"])[0] <= TOL
+    if pb:
+        small = torch.empty(pb - 256, dtype=torch.uint8, device="cuda")
+        assert lib.lbk_ternary_prepare(d_model, C.byref(gs), C.byref(us), C.byref(ds), T.ptr(small), small.numel(),
+                                       T.stream()) == A.LBK_ERR_WORKSPACE
+    # operators and the layer cache
+    from looped_blockell.layers.ternary import TernaryBlockELLWeight, TernaryMLPBlock
+    wts = [TernaryBlockELLWeight(*w) for w in tw]
+    m = TernaryMLPBlock(*wts)
+    x = T.to_gpu_bf16(T.act(rng, 40, d_model))
+    xq, sx = kernels.quantize_act_int8(x)
+    y = m(x)
+    assert torch.equal(y, kernels.ternary_swiglu_fwd(xq, sx, *[w.triple() for w in wts]))
+    with torch.no_grad():
+        wts[2].scales.mul_(2.0)                      # new version: the cache is rebuilt
+    y2 = m(x)
+    assert torch.equal(y2, kernels.ternary_swiglu_fwd(xq, sx, *[w.triple() for w in wts]))
+    assert not torch.equal(y2, y)
