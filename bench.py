@@ -12,8 +12,8 @@ forward pass.  The line also carries:
                 host cores, on the same workload (bounded token samples for the
                 ternary and looped lines, each named in its "sample");
   extra         the other workloads (shared gate/up topology, the backward of the
-                headline workload and of one of its products, ternary FFN, looped block L=8, decode, and the
-                prune-time topology transforms on the headline weights).
+                headline workload, the plain Block-ELL product and its backward, ternary FFN, looped block
+                L=8, decode, and the prune-time topology transforms on the headline weights).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only-main | --skip-main]
                       [--only shared,backward,...] [--copy-calibration]
@@ -325,6 +325,34 @@ def bench_formats(steps, warmup, device):
                 kernel_ms_avg=sum(per) / len(per))
 
 
+def bench_matmul(steps, warmup, device):
+    """The layer API's plain Block-ELL product (block_ell_matmul / BlockELLLinear, with a bias) at
+    the headline workload's gate shape [16384, 1024] -> [16384, 4096] and down shape
+    [16384, 4096] -> [16384, 1024], B=32, density 0.25."""
+    import torch
+    from looped_blockell import kernels
+    w = WORKLOADS["bf16"]
+    gen = torch.Generator(device=device).manual_seed(w["seed"] + 7)
+    Rf, Rm, Cm, Cf, Kg, Kd = geometry(w)
+    B, N = w["B"], w["N"]
+    res = {}
+    for name, (R, C, K, fin) in dict(gate_shape=(Rf, Cm, Kg, w["d_model"]), down_shape=(Rm, Cf, Kd, w["d_ff"])).items():
+        v, c = make_bell(R, C, K, B, gen, device)
+        x = torch.randn(N, fin, generator=gen, device=device).to(torch.bfloat16)
+        bias = torch.randn(R * B, generator=gen, device=device) * 0.01
+        ms, per = time_steps(lambda i: kernels.block_ell_matmul(x, v, c, bias), steps, warmup)
+        flops = 2.0 * N * B * B * R * K
+        res[name] = dict(ms_per_step=ms, value=flops / (ms * 1e-3) / 1e12, unit="TFLOP/s",
+                         frac_of_bf16_peak=flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                         kernel_ms_avg=sum(per) / len(per))
+    g = res["gate_shape"]
+    return dict(workload="block_ell_matmul forward with bias (weights packed per call), gate shape 1024 -> 4096 "
+                         "and down shape 4096 -> 1024, 16384 tokens, B=32, density 0.25",
+                ms_per_step=g["ms_per_step"], value=g["value"], unit="TFLOP/s",
+                frac_of_bf16_peak=g["frac_of_bf16_peak"], kernel_ms_avg=g["kernel_ms_avg"],
+                down_shape=res["down_shape"])
+
+
 def bench_matmul_backward(steps, warmup, device):
     """Backward of one Block-ELL product at the headline gate shape (x [16384, 1024] -> [16384, 4096],
     B=32, 25 %): dx = dy W and the tile gradients (titan::block_ell_matmul_bwd), 2x the product's
@@ -605,8 +633,8 @@ def main():
                     help="skip the headline workload (profiling one extra workload on its own; the line's "
                          "headline fields are then null)")
     ap.add_argument("--only", default="",
-                    help="comma list of extra workloads to run: shared,backward,matmul_backward,ternary,looped,"
-                         "decode,topology,formats")
+                    help="comma list of extra workloads to run: shared,backward,matmul,matmul_backward,ternary,"
+                         "looped,decode,topology,formats")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one 256 MiB device-to-device copy (a reference point for HBM byte counters)")
     args = ap.parse_args()
@@ -632,9 +660,10 @@ def main():
     main_res = empty if args.skip_main else bench_bf16(args.steps, args.warmup, device)
     extra = {}
     if not args.only_main:
-        todo = [s for s in args.only.split(",") if s] or ["shared", "backward", "matmul_backward", "ternary", "looped",
-                                                           "decode", "topology", "formats"]
-        fns = dict(shared=bench_bf16_shared, backward=bench_bf16_backward, matmul_backward=bench_matmul_backward,
+        todo = [s for s in args.only.split(",") if s] or ["shared", "backward", "matmul", "matmul_backward", "ternary",
+                                                           "looped", "decode", "topology", "formats"]
+        fns = dict(shared=bench_bf16_shared, backward=bench_bf16_backward, matmul=bench_matmul,
+                   matmul_backward=bench_matmul_backward,
                    ternary=bench_ternary, looped=bench_looped, decode=bench_decode, topology=bench_topology,
                    formats=bench_formats)
         for name in todo:

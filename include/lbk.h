@@ -88,6 +88,20 @@ int lbk_block_ell_matmul_bf16(const uint16_t* x, int64_t N, int32_t in_features,
                               void* stream);
 
 /*
+ * lbk_block_ell_matmul_bf16 for contiguous rows (ldx = in_features, ldy = R*B) with a workspace:
+ * the tiles are packed into it (fragment-major) and the product runs on the SwiGLU kernels'
+ * machinery -- the gate/up kernel's gate stream over an LDS panel of x when in_features is a
+ * multiple of 128 up to 2048, the down kernel (x staged through LDS 512 columns at a time) for
+ * wider inputs -- for B in {16, 32}; other shapes take the row-block kernel and need no
+ * workspace (lbk_block_ell_matmul_workspace_bytes returns 0).  Same contract and result
+ * (within float32 summation order) as lbk_block_ell_matmul_bf16.
+ */
+size_t lbk_block_ell_matmul_workspace_bytes(int64_t N, int32_t in_features, const lbk_bell* w);
+int lbk_block_ell_matmul_ws_bf16(const uint16_t* x, int64_t N, int32_t in_features, const lbk_bell* w,
+                                 const float* bias, uint16_t* y, void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
+/*
  * Workspace bytes needed by lbk_swiglu_fwd_bf16 for this geometry: packed
  * copies of the gate/up/down tiles (two-kernel path) plus the hidden state h
  * [N, d_ff] bf16 unless want_intermediates (then the caller passes h_out).

@@ -143,6 +143,61 @@ int lbk_block_ell_matmul_bf16(const uint16_t* x, int64_t N, int32_t in_features,
   return launch_rowblock(w->B, 0, a, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
 }
 
+// The plain product on packed tiles: the gate/up kernel's gate stream over an LDS panel of x
+// (in_features <= 2048) or the down kernel (x staged 512 columns at a time); row-block kernel
+// otherwise.
+enum MatmulPath { MM_ROWBLOCK = 0, MM_LIN = 1, MM_STAGED = 2 };
+
+static MatmulPath matmul_path(int32_t in_features, const lbk_bell* w) {
+  if (w->B != 16 && w->B != 32) return MM_ROWBLOCK;
+  if (lin_supported(w->B, in_features, w->R, w->K)) return MM_LIN;
+  if (w->K >= 1 && w->K <= 63 && w->R >= 1 && in_features % 8 == 0) return MM_STAGED;
+  return MM_ROWBLOCK;
+}
+
+size_t lbk_block_ell_matmul_workspace_bytes(int64_t N, int32_t in_features, const lbk_bell* w) {
+  if (!w || N <= 0 || in_features <= 0 || check_bell(w) || in_features % w->B) return 0;
+  if (matmul_path(in_features, w) == MM_ROWBLOCK) return 0;
+  return align256(packed_bf16_bytes((int64_t)w->R * w->K, w->B));
+}
+
+int lbk_block_ell_matmul_ws_bf16(const uint16_t* x, int64_t N, int32_t in_features, const lbk_bell* w,
+                                 const float* bias, uint16_t* y, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  int st = check_bell(w);
+  if (st) return st;
+  if (N < 0) return LBK_ERR_ARG;
+  if (in_features <= 0 || in_features % w->B) return LBK_ERR_SHAPE;
+  if (N == 0) return LBK_OK;
+  if (!x || !y) return LBK_ERR_NULL;
+  const int64_t out_f = (int64_t)w->R * w->B;
+  if (!a16(x) || (in_features % 8) || !a16(y) || (out_f % 8)) return LBK_ERR_ALIGN;
+  const MatmulPath path = matmul_path(in_features, w);
+  if (path == MM_ROWBLOCK)
+    return lbk_block_ell_matmul_bf16(x, N, in_features, in_features, w, bias, y, out_f, stream);
+  const size_t need = lbk_block_ell_matmul_workspace_bytes(N, in_features, w);
+  if (!workspace || workspace_bytes < need) return LBK_ERR_WORKSPACE;
+  if (!a16(workspace)) return LBK_ERR_ALIGN;
+  hipStream_t s = S(stream);
+  const int C_in = in_features / w->B;
+  PackJob job{w->values, w->col_idx, (int64_t)w->R * w->K, C_in, static_cast<uint32_t*>(workspace), 0,
+              path == MM_LIN ? 1 : 0};
+  if (launch_pack_bf16_multi(&job, 1, w->B, s) != 0) return LBK_ERR_LAUNCH;
+  if (path == MM_LIN) {
+    GUArgs g{};
+    g.x = x; g.N = N; g.d_model = in_features;
+    g.pg = workspace; g.cg = w->col_idx; g.Kg = w->K;
+    g.R_ff = w->R; g.h = y; g.bg = bias;
+    return launch_lin(w->B, g, s) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+  }
+  DNArgs d{};
+  d.h = x; d.N = N; d.d_ff = in_features; d.d_model = (int)out_f;
+  d.pd = workspace; d.cd = w->col_idx; d.Kd = w->K;
+  d.R_m = w->R; d.C_d = C_in;
+  d.out = y; d.bd = bias;
+  return launch_dn(w->B, d, s) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
 static bool use_split(const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, int32_t d_model) {
   return split_supported(gate->B, d_model, gate->R, down->R, gate->K, up->K, down->K);
 }

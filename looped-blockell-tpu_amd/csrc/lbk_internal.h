@@ -88,6 +88,10 @@ struct DNArgs {
   const float* bd;          // optional [d_model] down bias
 };
 bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd);
+// plain product y[N, R*B] = x[N, in] W (+ bias in a.bg) on packed tiles (a.pg, a.cg, a.Kg, a.R_ff,
+// a.d_model = in, output in a.h with row stride R*B): the gate/up kernel's gate stream alone
+bool lin_supported(int B, int in_features, int R, int K);
+int launch_lin(int B, const GUArgs& a, hipStream_t st);
 // looped block in one launch: gate/up (RMSNorm of the fp32 state) and down per token block
 // for all L iterations; gu.xf == dn.state == the fp32 state, gu.h == dn.h
 struct LoopArgs {

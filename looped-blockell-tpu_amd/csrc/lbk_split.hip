@@ -71,7 +71,9 @@ struct GUPanel { static constexpr int ROWB = 8192 / MT; };
 // wrote the next iteration's normalised rows; the table stays from the first iteration).
 // BIAS: add a.bg / a.bu (either may be null) to the pre-activations; without it the epilogue
 // has no bias code at all.
-template <int B, int MT, bool NORM, bool INTER, bool SHARED, bool READY = false, bool BIAS = false>
+// LIN: one plain product y = x W (+ a.bg) into a.h: the gate stream only (the caller passes
+// the gate's weights and columns for up too, with SHARED), no SiLU.
+template <int B, int MT, bool NORM, bool INTER, bool SHARED, bool READY = false, bool BIAS = false, bool LIN = false>
 __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned char* smem, int tid) {
   constexpr int CW = TileShape<B>::CW;
   constexpr int TM = 16 * MT;
@@ -130,7 +132,7 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
     const bool live = rn < nrows && rk < K;
     const int64_t e = live ? (int64_t)(w + 8 * rn) * K + rk : ztile;
     load_pfrag<B>(pg + e * PackedTile<B>::U32X4, lane, S.g);
-    load_pfrag<B>(pu + e * PackedTile<B>::U32X4, lane, S.u);
+    if constexpr (!LIN) load_pfrag<B>(pu + e * PackedTile<B>::U32X4, lane, S.u);
     S.cg = live ? (int)e : -1;   // position index until fetch_c replaces it by columns
   };
   auto fetch_c = [&](GUSlot<B>& S) {
@@ -187,10 +189,12 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int m = 0; m < CW; ++m) ag[mt][m] = mfma_bf16(S.g[0][m], A.g[mt], ag[mt][m]);
+    if constexpr (!LIN) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int m = 0; m < CW; ++m) au[mt][m] = mfma_bf16(S.u[0][m], SHARED ? A.g[mt] : A.u[mt], au[mt][m]);
+        for (int m = 0; m < CW; ++m) au[mt][m] = mfma_bf16(S.u[0][m], SHARED ? A.g[mt] : A.u[mt], au[mt][m]);
+    }
   };
 
   // ---- input panel: all of this thread's loads are issued before any store,
@@ -346,7 +350,7 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
             gv[4 * m + v] += bgv[4 * m + v];
             uv[4 * m + v] += buv[4 * m + v];
           }
-          o[4 * m + v] = silu_f(gv[4 * m + v]) * uv[4 * m + v];
+          o[4 * m + v] = LIN ? gv[4 * m + v] : silu_f(gv[4 * m + v]) * uv[4 * m + v];
         }
       if (t < a.N) {
         store_bf16x<4 * CW>(a.h + t * d_ff + col0, o);
@@ -363,6 +367,14 @@ template <int B, int MT, bool NORM, bool INTER, bool SHARED, bool BIAS>
 __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   gu_tile<B, MT, NORM, INTER, SHARED, false, BIAS>(a, (int64_t)blockIdx.x, smem, (int)threadIdx.x);
+}
+
+// plain Block-ELL product y = x W (+ bias) over an LDS panel of x (the gate/up kernel's gate
+// stream alone)
+template <int B, int MT, bool BIAS>
+__global__ __launch_bounds__(512, 1) void lin_kernel(GUArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  gu_tile<B, MT, false, false, true, false, BIAS, true>(a, (int64_t)blockIdx.x, smem, (int)threadIdx.x);
 }
 
 // ===========================================================================
@@ -873,6 +885,39 @@ int launch_gu(int B, bool norm, const GUArgs& a, hipStream_t st) {
   LBK_GU(16, 4) LBK_GU(16, 2) LBK_GU(32, 4) LBK_GU(32, 2)
 #undef LBK_GU
 #undef LBK_GU2
+  return -2;
+}
+
+template <int B, int MT, bool BIAS>
+static int launch_lin_t(const GUArgs& a, hipStream_t st) {
+  auto kern = lin_kernel<B, MT, BIAS>;
+  static std::atomic<uint64_t> configured{0};
+  if (set_lds_limit_once((const void*)kern, 163840, configured)) return -1;
+  const int TM = 16 * MT;
+  const size_t lds = gu_lds(a.R_ff, a.Kg, MT);
+  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + TM - 1) / TM)), dim3(512), lds, st, a);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+bool lin_supported(int B, int in_features, int R, int K) {
+  if (B != 16 && B != 32) return false;
+  if (K < 1 || in_features % 128) return false;
+  const int mt = gu_mt(in_features);
+  if (mt == 0 || gu_lds(R, K, mt) > 163840 || (int64_t)R * K > 512 * GU_CT_MAX) return false;
+  return (R * B) % 8 == 0;
+}
+
+int launch_lin(int B, const GUArgs& a0, hipStream_t st) {
+  if (a0.N == 0) return 0;
+  GUArgs a = a0;   // the up operands are the gate's (never read as weights)
+  a.pu = a.pg;
+  a.cu = a.cg;
+  a.Ku = a.Kg;
+  const int mt = gu_mt(a.d_model);
+#define LBK_LIN(BB, MM)                                                                     \
+  if (B == BB && mt == MM) return a.bg ? launch_lin_t<BB, MM, true>(a, st) : launch_lin_t<BB, MM, false>(a, st);
+  LBK_LIN(16, 4) LBK_LIN(16, 2) LBK_LIN(32, 4) LBK_LIN(32, 2)
+#undef LBK_LIN
   return -2;
 }
 

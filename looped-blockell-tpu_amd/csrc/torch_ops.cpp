@@ -215,16 +215,12 @@ at::Tensor block_ell_matmul(const at::Tensor& x_, const at::Tensor& v_, const at
   lbk_bell w = make_bell(v, c, op, "weight");
   TORCH_CHECK(x.size(1) % w.B == 0, "titan::block_ell_matmul: in_features ", x.size(1), " not a multiple of B=", w.B);
   const int64_t N = x.size(0), out_f = (int64_t)w.R * w.B;
-  at::Tensor b;
-  const float* bp = nullptr;
-  if (bias.has_value() && bias->defined()) {
-    b = bias->to(at::kFloat).contiguous();
-    TORCH_CHECK(b.numel() == out_f, "titan::block_ell_matmul: bias must have out_features elements");
-    bp = b.data_ptr<float>();
-  }
+  const at::Tensor b = opt_bias(bias, out_f, x, op, "bias");
   at::Tensor y = at::empty({N, out_f}, x.options());
-  LBK_CALL("block_ell_matmul", lbk_block_ell_matmul_bf16(bf(x), N, (int32_t)x.size(1), x.size(1), &w, bp, bfm(y),
-                                                         out_f, cur_stream(x)));
+  const size_t wsb = lbk_block_ell_matmul_workspace_bytes(N, (int32_t)x.size(1), &w);
+  at::Tensor ws = wsb ? workspace(wsb, x) : at::Tensor();
+  LBK_CALL("block_ell_matmul", lbk_block_ell_matmul_ws_bf16(bf(x), N, (int32_t)x.size(1), &w, fptr(b), bfm(y),
+                                                            wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(x)));
   return y;
 }
 

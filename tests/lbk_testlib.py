@@ -120,6 +120,23 @@ def abi_matmul(x_t, w_t, bias_t=None):
     return y
 
 
+def abi_matmul_ws(x_t, w_t, bias_t=None):
+    """lbk_block_ell_matmul_ws_bf16 (packed tiles on the SwiGLU kernels where the shape allows)."""
+    import torch
+    A = abi()
+    lib = A.load()
+    vals_t, col_t = w_t
+    N, F = x_t.shape
+    R, K, B, _ = vals_t.shape
+    y = torch.empty(N, R * B, dtype=torch.bfloat16, device=x_t.device)
+    wb = bell_struct(vals_t, col_t)
+    wsb = lib.lbk_block_ell_matmul_workspace_bytes(N, F, C.byref(wb))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x_t.device)
+    A.check(lib.lbk_block_ell_matmul_ws_bf16(ptr(x_t), N, F, C.byref(wb), ptr(bias_t), ptr(y), ptr(ws), wsb,
+                                             stream()), "matmul_ws")
+    return y, wsb
+
+
 def abi_swiglu(x_t, g_t, u_t, d_t, add_residual=False, intermediates=False):
     import torch
     A = abi()

@@ -34,6 +34,42 @@ def test_matmul_parity(gpu, B, N):
     assert rel <= TOL, f"rel {rel} abs {ab}"
 
 
+@pytest.mark.parametrize("case", [
+    # (in_features, out_features, B, K, N, path)
+    (256, 512, 16, 4, 77, "panel"),
+    (1024, 4096, 32, 8, 200, "panel"),          # the headline gate shape
+    (2048, 1024, 32, 8, 70, "panel"),           # 32-token panels
+    (4096, 1024, 32, 32, 130, "staged"),        # the headline down shape
+    (96, 64, 32, 2, 33, "staged"),              # in_features not a multiple of 128
+    (4096, 512, 16, 40, 17, "staged"),
+    (256, 256, 64, 2, 40, "row-block"),         # B = 64
+])
+def test_matmul_ws_paths(gpu, case):
+    """The workspace entry's three paths against the oracle and the row-block entry, with a bias,
+    dead slots and out-of-range columns."""
+    fin, fout, B, K, N, path = case
+    _say(f"matmul_ws {case}")
+    rng = np.random.default_rng(fin + fout + B + N)
+    R, C_ = fout // B, fin // B
+    vals, col = T.bell_weight(rng, R, C_, K, B)
+    col[0, 0] = -1
+    col[R - 1, K - 1] = C_ + 3                   # out of range: skipped
+    x = T.act(rng, N, fin)
+    bias = (0.1 * rng.standard_normal(fout)).astype(np.float32)
+    wt = (T.to_gpu_bf16(vals), T.to_gpu(col))
+    y, wsb = T.abi_matmul_ws(T.to_gpu_bf16(x), wt, T.to_gpu(bias))
+    assert (wsb > 0) == (path != "row-block")
+    col_ref = col.copy()
+    col_ref[col_ref >= C_] = -1
+    ref = O.block_ell_matmul(x.astype(np.float64), vals.astype(np.float64), col_ref) + bias
+    rel, ab = T.rel_err(T.to_np(y), ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+    y_rb = T.abi_matmul(T.to_gpu_bf16(x), wt, T.to_gpu(bias))
+    assert T.rel_err(T.to_np(y), T.to_np(y_rb).astype(np.float64))[0] <= TOL
+    y2, _ = T.abi_matmul_ws(T.to_gpu_bf16(x), wt, None)      # no bias
+    assert T.rel_err(T.to_np(y2), ref - bias)[0] <= TOL
+
+
 def test_matmul_density_one_equals_dense(gpu):
     # reference tests/test_block_ell.py:42-54 on the GPU: Block-ELL at density 1.0 == x @ W.T
     rng = np.random.default_rng(7)
