@@ -102,6 +102,20 @@ int lbk_block_ell_matmul_ws_bf16(const uint16_t* x, int64_t N, int32_t in_featur
                                  void* stream);
 
 /*
+ * The same product on tiles packed once (weights fixed across calls): lbk_block_ell_matmul_prepack_bf16
+ * fills a buffer of lbk_block_ell_matmul_prepacked_bytes (0: the shape has no packed form, the
+ * prepack is a no-op and the product takes the row-block kernel), reflecting values and col_idx
+ * at the time of the call; lbk_block_ell_matmul_prepacked_bf16 then needs no workspace.  No
+ * counterpart in the reference (its JAX product has no weight preparation).
+ */
+size_t lbk_block_ell_matmul_prepacked_bytes(int32_t in_features, const lbk_bell* w);
+int lbk_block_ell_matmul_prepack_bf16(int32_t in_features, const lbk_bell* w, void* packed, size_t packed_bytes,
+                                      void* stream);
+int lbk_block_ell_matmul_prepacked_bf16(const uint16_t* x, int64_t N, int32_t in_features, const lbk_bell* w,
+                                        const void* packed, size_t packed_bytes, const float* bias, uint16_t* y,
+                                        void* stream);
+
+/*
  * Workspace bytes needed by lbk_swiglu_fwd_bf16 for this geometry: packed
  * copies of the gate/up/down tiles (two-kernel path) plus the hidden state h
  * [N, d_ff] bf16 unless want_intermediates (then the caller passes h_out).

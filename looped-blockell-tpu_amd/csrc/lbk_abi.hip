@@ -161,9 +161,10 @@ size_t lbk_block_ell_matmul_workspace_bytes(int64_t N, int32_t in_features, cons
   return align256(packed_bf16_bytes((int64_t)w->R * w->K, w->B));
 }
 
-int lbk_block_ell_matmul_ws_bf16(const uint16_t* x, int64_t N, int32_t in_features, const lbk_bell* w,
-                                 const float* bias, uint16_t* y, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
+// the product on tiles already packed (packed != null) or packed into the workspace
+static int matmul_impl(const uint16_t* x, int64_t N, int32_t in_features, const lbk_bell* w, const void* packed,
+                       size_t packed_bytes, const float* bias, uint16_t* y, void* workspace, size_t workspace_bytes,
+                       hipStream_t s) {
   int st = check_bell(w);
   if (st) return st;
   if (N < 0) return LBK_ERR_ARG;
@@ -174,28 +175,67 @@ int lbk_block_ell_matmul_ws_bf16(const uint16_t* x, int64_t N, int32_t in_featur
   if (!a16(x) || (in_features % 8) || !a16(y) || (out_f % 8)) return LBK_ERR_ALIGN;
   const MatmulPath path = matmul_path(in_features, w);
   if (path == MM_ROWBLOCK)
-    return lbk_block_ell_matmul_bf16(x, N, in_features, in_features, w, bias, y, out_f, stream);
-  const size_t need = lbk_block_ell_matmul_workspace_bytes(N, in_features, w);
-  if (!workspace || workspace_bytes < need) return LBK_ERR_WORKSPACE;
-  if (!a16(workspace)) return LBK_ERR_ALIGN;
-  hipStream_t s = S(stream);
+    return lbk_block_ell_matmul_bf16(x, N, in_features, in_features, w, bias, y, out_f, s);
+  const size_t need = align256(packed_bf16_bytes((int64_t)w->R * w->K, w->B));
+  const void* pk = packed;
+  if (pk) {
+    if (packed_bytes < need) return LBK_ERR_WORKSPACE;
+    if (!a16(pk)) return LBK_ERR_ALIGN;
+  } else {
+    if (!workspace || workspace_bytes < need) return LBK_ERR_WORKSPACE;
+    if (!a16(workspace)) return LBK_ERR_ALIGN;
+    const int C_in = in_features / w->B;
+    PackJob job{w->values, w->col_idx, (int64_t)w->R * w->K, C_in, static_cast<uint32_t*>(workspace), 0,
+                path == MM_LIN ? 1 : 0};
+    if (launch_pack_bf16_multi(&job, 1, w->B, s) != 0) return LBK_ERR_LAUNCH;
+    pk = workspace;
+  }
   const int C_in = in_features / w->B;
-  PackJob job{w->values, w->col_idx, (int64_t)w->R * w->K, C_in, static_cast<uint32_t*>(workspace), 0,
-              path == MM_LIN ? 1 : 0};
-  if (launch_pack_bf16_multi(&job, 1, w->B, s) != 0) return LBK_ERR_LAUNCH;
   if (path == MM_LIN) {
     GUArgs g{};
     g.x = x; g.N = N; g.d_model = in_features;
-    g.pg = workspace; g.cg = w->col_idx; g.Kg = w->K;
+    g.pg = pk; g.cg = w->col_idx; g.Kg = w->K;
     g.R_ff = w->R; g.h = y; g.bg = bias;
     return launch_lin(w->B, g, s) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
   }
   DNArgs d{};
   d.h = x; d.N = N; d.d_ff = in_features; d.d_model = (int)out_f;
-  d.pd = workspace; d.cd = w->col_idx; d.Kd = w->K;
+  d.pd = pk; d.cd = w->col_idx; d.Kd = w->K;
   d.R_m = w->R; d.C_d = C_in;
   d.out = y; d.bd = bias;
   return launch_dn(w->B, d, s) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+int lbk_block_ell_matmul_ws_bf16(const uint16_t* x, int64_t N, int32_t in_features, const lbk_bell* w,
+                                 const float* bias, uint16_t* y, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  return matmul_impl(x, N, in_features, w, nullptr, 0, bias, y, workspace, workspace_bytes, S(stream));
+}
+
+size_t lbk_block_ell_matmul_prepacked_bytes(int32_t in_features, const lbk_bell* w) {
+  return lbk_block_ell_matmul_workspace_bytes(1, in_features, w);
+}
+
+int lbk_block_ell_matmul_prepack_bf16(int32_t in_features, const lbk_bell* w, void* packed, size_t packed_bytes,
+                                      void* stream) {
+  int st = check_bell(w);
+  if (st) return st;
+  if (in_features <= 0 || in_features % w->B) return LBK_ERR_SHAPE;
+  const MatmulPath path = matmul_path(in_features, w);
+  if (path == MM_ROWBLOCK) return LBK_OK;        // no packed form for this geometry
+  if (!packed || packed_bytes < lbk_block_ell_matmul_prepacked_bytes(in_features, w)) return LBK_ERR_WORKSPACE;
+  if (!a16(packed)) return LBK_ERR_ALIGN;
+  PackJob job{w->values, w->col_idx, (int64_t)w->R * w->K, in_features / w->B, static_cast<uint32_t*>(packed), 0,
+              path == MM_LIN ? 1 : 0};
+  return launch_pack_bf16_multi(&job, 1, w->B, S(stream)) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+int lbk_block_ell_matmul_prepacked_bf16(const uint16_t* x, int64_t N, int32_t in_features, const lbk_bell* w,
+                                        const void* packed, size_t packed_bytes, const float* bias, uint16_t* y,
+                                        void* stream) {
+  if (!w) return LBK_ERR_NULL;
+  if (N > 0 && !packed && lbk_block_ell_matmul_prepacked_bytes(in_features, w) > 0) return LBK_ERR_NULL;
+  return matmul_impl(x, N, in_features, w, packed, packed_bytes, bias, y, nullptr, 0, S(stream));
 }
 
 static bool use_split(const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, int32_t d_model) {

@@ -224,6 +224,48 @@ at::Tensor block_ell_matmul(const at::Tensor& x_, const at::Tensor& v_, const at
   return y;
 }
 
+// block_ell_matmul's packed tiles for weights fixed across calls (uint8; empty when the shape takes
+// the row-block kernel), and the product from them
+at::Tensor block_ell_matmul_prepack(const at::Tensor& v_, const at::Tensor& c_, int64_t in_features) {
+  const char* op = "block_ell_matmul_prepack";
+  at::Tensor v = v_, c = c_;
+  check_gpu(v, op, "values");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(v.device());
+  lbk_bell w = make_bell(v, c, op, "weight");
+  TORCH_CHECK(in_features > 0 && in_features % w.B == 0, "titan::block_ell_matmul_prepack: in_features ",
+              in_features, " not a positive multiple of B=", w.B);
+  const size_t bytes = lbk_block_ell_matmul_prepacked_bytes((int32_t)in_features, &w);
+  at::Tensor packed = at::empty({(int64_t)bytes}, v.options().dtype(at::kByte));
+  if (bytes)
+    LBK_CALL("block_ell_matmul_prepack",
+             lbk_block_ell_matmul_prepack_bf16((int32_t)in_features, &w, packed.data_ptr(), bytes, cur_stream(v)));
+  return packed;
+}
+
+at::Tensor block_ell_matmul_prepacked(const at::Tensor& x_, const at::Tensor& packed, const at::Tensor& v_,
+                                      const at::Tensor& c_, const c10::optional<at::Tensor>& bias) {
+  const char* op = "block_ell_matmul_prepacked";
+  at::Tensor v = v_, c = c_;
+  at::Tensor x = check_x2d(x_, op);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  lbk_bell w = make_bell(v, c, op, "weight");
+  TORCH_CHECK(x.size(1) % w.B == 0, "titan::block_ell_matmul_prepacked: in_features ", x.size(1),
+              " not a multiple of B=", w.B);
+  check_gpu(packed, op, "packed");
+  TORCH_CHECK(packed.scalar_type() == at::kByte && packed.dim() == 1 && packed.is_contiguous(),
+              "titan::block_ell_matmul_prepacked: packed must be the uint8 tensor of block_ell_matmul_prepack");
+  const size_t need = lbk_block_ell_matmul_prepacked_bytes((int32_t)x.size(1), &w);
+  TORCH_CHECK((size_t)packed.numel() >= need, "titan::block_ell_matmul_prepacked: packed holds ", packed.numel(),
+              " bytes, this shape needs ", need);
+  const int64_t N = x.size(0), out_f = (int64_t)w.R * w.B;
+  const at::Tensor b = opt_bias(bias, out_f, x, op, "bias");
+  at::Tensor y = at::empty({N, out_f}, x.options());
+  LBK_CALL("block_ell_matmul_prepacked",
+           lbk_block_ell_matmul_prepacked_bf16(bf(x), N, (int32_t)x.size(1), &w, need ? packed.data_ptr() : nullptr,
+                                               (size_t)packed.numel(), fptr(b), bfm(y), cur_stream(x)));
+  return y;
+}
+
 // backward of block_ell_matmul (bias gradient excluded): (dx, d_values)
 std::tuple<at::Tensor, at::Tensor> block_ell_matmul_bwd(const at::Tensor& dy_, const at::Tensor& x_,
                                                         const at::Tensor& v_, const at::Tensor& c_) {
@@ -710,6 +752,9 @@ TORCH_LIBRARY(titan, m) {
   // ops beyond the reference's set
   m.def("block_ell_matmul(Tensor x, Tensor values, Tensor col_indices, Tensor? bias=None) -> Tensor");
   m.def("block_ell_matmul_bwd(Tensor grad_out, Tensor x, Tensor values, Tensor col_indices) -> (Tensor, Tensor)");
+  m.def("block_ell_matmul_prepack(Tensor values, Tensor col_indices, int in_features) -> Tensor");
+  m.def("block_ell_matmul_prepacked(Tensor x, Tensor packed, Tensor values, Tensor col_indices, Tensor? bias=None) "
+        "-> Tensor");
   m.def("block_ell_swiglu_fwd_bias(Tensor x, Tensor v_gate, Tensor ci_gate, Tensor? b_gate, Tensor v_up, "
         "Tensor ci_up, Tensor? b_up, Tensor v_down, Tensor ci_down, Tensor? b_down, bool add_residual, "
         "bool intermediates=False) -> (Tensor, Tensor, Tensor, Tensor)");
@@ -774,6 +819,8 @@ TORCH_LIBRARY_IMPL(titan, CUDA, m) {
   m.impl("persistent_mlp_step", &persistent_mlp_step);
   m.impl("block_ell_matmul", &block_ell_matmul);
   m.impl("block_ell_matmul_bwd", &block_ell_matmul_bwd);
+  m.impl("block_ell_matmul_prepack", &block_ell_matmul_prepack);
+  m.impl("block_ell_matmul_prepacked", &block_ell_matmul_prepacked);
   m.impl("looped_swiglu", &looped_swiglu);
   m.impl("looped_swiglu_persistent", &looped_swiglu_persistent);
   m.impl("looped_swiglu_launches", &looped_swiglu_launches);
@@ -803,6 +850,7 @@ TORCH_LIBRARY_IMPL(titan, Autograd, m) {
   for (const char* name :
        {"block_ell_swiglu_fwd", "block_ell_swiglu_fwd_with_intermediate", "block_ell_swiglu_bwd",
         "persistent_mlp_step", "block_ell_matmul", "block_ell_matmul_bwd", "block_ell_swiglu_bwd_ex",
+        "block_ell_matmul_prepack", "block_ell_matmul_prepacked",
         "looped_swiglu", "looped_swiglu_persistent", "looped_swiglu_launches", "rmsnorm", "rmsnorm_bwd",
         "block_ell_swiglu_fwd_bias", "block_ell_swiglu_bwd_bias", "looped_swiglu_bias",
         "block_ell_swiglu_prepack", "block_ell_swiglu_fwd_prepacked", "diagonal_injection", "diagonal_injection_bwd",
@@ -871,6 +919,10 @@ TORCH_LIBRARY_IMPL(titan, Meta, m) {
             at::TensorList) { return at::empty_like(h); });
   m.impl("block_ell_matmul", [](const at::Tensor& x, const at::Tensor& v, const at::Tensor&,
                                 const c10::optional<at::Tensor>&) {
+    return at::empty({x.size(0), v.size(0) * v.size(2)}, x.options());
+  });
+  m.impl("block_ell_matmul_prepacked", [](const at::Tensor& x, const at::Tensor&, const at::Tensor& v, const at::Tensor&,
+                                          const c10::optional<at::Tensor>&) {
     return at::empty({x.size(0), v.size(0) * v.size(2)}, x.options());
   });
   m.impl("block_ell_matmul_bwd", [](const at::Tensor&, const at::Tensor& x, const at::Tensor& v, const at::Tensor&) {

@@ -76,6 +76,9 @@ SIGNATURES = {
     "lbk_block_ell_matmul_bf16": (C.c_int, [_P, _I64, _I32, _I64, _PB, _P, _P, _I64, _P]),
     "lbk_block_ell_matmul_workspace_bytes": (_SZ, [_I64, _I32, _PB]),
     "lbk_block_ell_matmul_ws_bf16": (C.c_int, [_P, _I64, _I32, _PB, _P, _P, _P, _SZ, _P]),
+    "lbk_block_ell_matmul_prepacked_bytes": (_SZ, [_I32, _PB]),
+    "lbk_block_ell_matmul_prepack_bf16": (C.c_int, [_I32, _PB, _P, _SZ, _P]),
+    "lbk_block_ell_matmul_prepacked_bf16": (C.c_int, [_P, _I64, _I32, _PB, _P, _SZ, _P, _P, _P]),
     "lbk_swiglu_workspace_bytes": (_SZ, [_I64, _I32, _PB, _PB, _PB, C.c_int]),
     "lbk_swiglu_fwd_bf16": (C.c_int, [_P, _I64, _I32, _PB, _PB, _PB, C.c_int, _P, _P, _P, _P, _P, _SZ, _P]),
     "lbk_noalloc_scratch_bytes": (_SZ, []),

@@ -184,6 +184,19 @@ def swiglu(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual: bool 
     return swiglu_fwd(x, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, add_residual)
 
 
+def block_ell_matmul_prepack(values, col_indices, in_features: int):
+    """``titan::block_ell_matmul_prepack``: the packed tiles ``block_ell_matmul`` reads, built once
+    for weights that stay fixed (uint8; empty when the shape takes the row-block kernel)."""
+    _gpu(values)
+    return ops().block_ell_matmul_prepack(values, col_indices, int(in_features))
+
+
+def block_ell_matmul_prepacked(x, packed, values, col_indices, bias=None):
+    """``block_ell_matmul`` (no gradient) from a ``block_ell_matmul_prepack`` copy."""
+    _gpu(x, values)
+    return ops().block_ell_matmul_prepacked(x, packed, values, col_indices, bias)
+
+
 def swiglu_prepack(v_gate, ci_gate, v_up, ci_up, v_down, ci_down):
     """``titan::block_ell_swiglu_prepack``: the packed tile copy the two-kernel forward reads,
     built once for weights that stay fixed across forwards (uint8; empty when the geometry has

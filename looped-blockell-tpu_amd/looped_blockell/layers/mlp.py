@@ -19,7 +19,8 @@ approximation, ``jax.nn.gelu``'s default (``mlp.py:156``).
 
 Forwards that need no gradient (``torch.no_grad()`` / ``torch.inference_mode()``) run from
 weights prepared once per weight version: the bf16 tiles and their fragment-major packed copy
-(``titan::block_ell_swiglu_prepack``) are cached on the module and rebuilt when a value tensor,
+(``titan::block_ell_swiglu_prepack``, ``titan::block_ell_matmul_prepack`` for ``BlockELLLinear``)
+are cached on the module and rebuilt when a value tensor,
 a column-index buffer or an alive mask changes (tensor version counters), so such a forward is
 the gate/up and down launches only.  Writes through ``.data`` bypass the version counter: call
 ``release_inference_cache()`` after them.  The cache holds about two bytes per weight element
@@ -60,6 +61,7 @@ class BlockELLLinear(nn.Module):
         self.register_buffer("col_indices", self._init_topology().to(device))
         self.register_buffer("alive_mask", torch.ones(self.R, self.K, dtype=torch.bool, device=device))
         self._eff_cache = None
+        self._frozen = None
 
     def _init_topology(self) -> torch.Tensor:
         if self.density >= 1.0:
@@ -89,8 +91,30 @@ class BlockELLLinear(nn.Module):
     def as_block_ell(self) -> BlockELLTensor:
         return BlockELLTensor(self.kernel_values(), self.effective_col_indices(), self.config)
 
+    def _frozen_weight(self):
+        """(bf16 tiles, effective columns, packed copy), rebuilt when the values or the topology change."""
+        cols = self.effective_col_indices()
+        key = (self.values.data_ptr(), self.values._version, self._eff_cache[0])
+        if self._frozen is None or self._frozen[0] != key:
+            with torch.inference_mode(False):
+                v = self.kernel_values()
+                self._frozen = (key, v, cols, kernels.block_ell_matmul_prepack(v, cols, self.in_features))
+        return self._frozen[1:]
+
+    def release_inference_cache(self) -> None:
+        """Drop the cached bf16 and packed tiles of gradient-free forwards."""
+        self._frozen = None
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return kernels.block_ell_matmul(x, self.kernel_values(), self.effective_col_indices(), self.bias)
+        grad = torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
+        if grad:
+            return kernels.block_ell_matmul(x, self.kernel_values(), self.effective_col_indices(), self.bias)
+        # weights fixed across gradient-free forwards: bf16 tiles and their packed copy cached
+        v, cols, packed = self._frozen_weight()
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, x.shape[-1]).to(torch.bfloat16).contiguous()
+        y = kernels.block_ell_matmul_prepacked(x2, packed, v, cols, self.bias)
+        return y.reshape(*lead, y.shape[-1])
 
 
 class MLPBlock(nn.Module):

@@ -141,3 +141,61 @@ def test_mlpblock_inference_cache_follows_weight_versions(gpu):
 def _interleave(w, b):
     vg, cg, vu, cu, vd, cd = w
     return vg, cg, b[0], vu, cu, b[1], vd, cd, b[2]
+
+
+@pytest.mark.parametrize("case", [
+    # (in_features, out_features, B, K, N)
+    (1024, 4096, 32, 8, 150),      # panel path
+    (4096, 512, 32, 12, 90),       # staged path
+    (256, 256, 64, 2, 33),         # row-block (no packed form)
+])
+def test_matmul_prepacked_matches_ws_entry(gpu, case):
+    fin, fout, B, K, N = case
+    print(f"matmul prepacked {case}", flush=True)
+    A = T.abi()
+    lib = A.load()
+    rng = np.random.default_rng(fin + fout + 3)
+    vals, col = T.bell_weight(rng, fout // B, fin // B, K, B, sentinel=[(0, 0)])
+    wt = (T.to_gpu_bf16(vals), T.to_gpu(col))
+    wb = T.bell_struct(*wt)
+    pb = lib.lbk_block_ell_matmul_prepacked_bytes(fin, C.byref(wb))
+    assert (pb > 0) == (B != 64)
+    packed = torch.empty(max(pb, 1), dtype=torch.uint8, device="cuda")
+    A.check(lib.lbk_block_ell_matmul_prepack_bf16(fin, C.byref(wb), T.ptr(packed), pb, T.stream()), "prepack")
+    bias = T.to_gpu((0.1 * rng.standard_normal(fout)).astype(np.float32))
+    for n in (N, 7):
+        x = T.to_gpu_bf16(T.act(rng, n, fin))
+        want, _ = T.abi_matmul_ws(x, wt, bias)
+        got = torch.empty(n, fout, dtype=torch.bfloat16, device="cuda")
+        A.check(lib.lbk_block_ell_matmul_prepacked_bf16(T.ptr(x), n, fin, C.byref(wb), T.ptr(packed) if pb else None,
+                                                        pb, T.ptr(bias), T.ptr(got), T.stream()), "prepacked")
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+
+
+def test_linear_inference_cache(gpu):
+    from looped_blockell.layers import BlockELLLinear, MLPBlock
+    torch.manual_seed(9)
+    lin = BlockELLLinear(1024, 512, tile_size=32, density=0.25, device="cuda")
+    with torch.no_grad():
+        lin.bias.copy_(torch.randn_like(lin.bias) * 0.1)
+    x = torch.randn(3, 50, 512, device="cuda").to(torch.bfloat16)
+    y_grad = lin(x)                                   # autograd path, packs per call
+    with torch.no_grad():
+        y0 = lin(x)
+        assert lin._frozen is not None
+        assert torch.equal(y0, y_grad.detach())
+        lin.values.mul_(0.5)
+        y1 = lin(x)
+    assert torch.equal(y1, lin(x).detach()) and not torch.equal(y1, y0)
+    lin.alive_mask[0, 0] = False
+    with torch.inference_mode():
+        y2 = lin(x)
+    assert torch.equal(y2, lin(x).detach()) and not torch.equal(y2, y1)
+    lin.release_inference_cache()
+    assert lin._frozen is None
+    # the GELU MLPBlock runs its two projections from the cached copies
+    m = MLPBlock(512, 1024, use_swiglu=False, tile_size=32, density=0.5, device="cuda")
+    with torch.no_grad():
+        ym = m(x)
+    assert m.fc1._frozen is not None and torch.equal(ym, m(x).detach())
