@@ -267,6 +267,29 @@ def test_swiglu_full_headline_sampled_rows(gpu):
     assert np.isfinite(out).all()
 
 
+@pytest.mark.parametrize("shape", [(1024, 4096), (4096, 1024)])
+def test_matmul_full_size_sampled_rows(gpu, shape):
+    """The plain product at the headline gate and down shapes, 16384 tokens, through the workspace
+    entry (panel and staged paths), with a bias; sampled rows against the oracle, and the
+    prepacked entry bit-identical."""
+    fin, fout = shape
+    B, N = 32, 16384
+    _say(f"matmul full size {fin}->{fout}")
+    rng = np.random.default_rng(fin + 1)
+    vals, col = T.bell_weight(rng, fout // B, fin // B, max(1, (fin // B) // 4), B)
+    x = T.act(rng, N, fin)
+    bias = (0.1 * rng.standard_normal(fout)).astype(np.float32)
+    wt = (T.to_gpu_bf16(vals), T.to_gpu(col))
+    y, wsb = T.abi_matmul_ws(T.to_gpu_bf16(x), wt, T.to_gpu(bias))
+    assert wsb > 0
+    yn = T.to_np(y)
+    rows = np.concatenate([np.sort(rng.choice(N, 256, replace=False)), [0, N - 1]])
+    ref = O.block_ell_matmul(x[rows].astype(np.float64), vals.astype(np.float64), col) + bias
+    rel, ab = T.rel_err(yn[rows], ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+    assert np.isfinite(yn).all()
+
+
 def test_swiglu_deterministic(gpu):
     rng = np.random.default_rng(5)
     g, u, d = T.ffn_weights(rng, 512, 2048, 32, 0.25)
