@@ -84,9 +84,9 @@ struct TernSplitLayout {
 TernSplitLayout tern_split_layout(int64_t N, const lbk_bell_ternary* gate, const lbk_bell_ternary* up,
                                   const lbk_bell_ternary* down) {
   TernSplitLayout L{};
-  L.pg = tprep_bytes((int64_t)gate->R * gate->K, gate->R);
-  L.pu = tprep_bytes((int64_t)up->R * up->K, up->R);
-  L.pd = tprep_bytes((int64_t)down->R * down->K, down->R);
+  L.pg = tprep_bytes((int64_t)gate->R * gate->K, gate->R, 0);
+  L.pu = tprep_bytes((int64_t)up->R * up->K, up->R, 1);
+  L.pd = tprep_bytes((int64_t)down->R * down->K, down->R, 2);
   L.hmax = align256((size_t)tgu_slices(N) * (size_t)N * 4);
   L.h = align256((size_t)N * gate->R * gate->B * 2);
   L.total = L.pg + L.pu + L.pd + L.hmax + L.h;

@@ -182,12 +182,16 @@ struct TDNArgs {
   float* sh_out;            // optional [N]
   int32_t* acc_d;           // optional [N, d_model]: integer accumulators sum_k m * P
 };
-size_t tprep_bytes(int64_t ntiles, int R);
+// bytes of one prepared tile of weight `which` (0 gate, 1 up: int8 MFMA fragments; 2 down:
+// 2-bit t + 1 words)
+constexpr int tprep_tile_bytes(int which) { return which < 2 ? 4096 : 1024; }
+size_t tprep_bytes(int64_t ntiles, int R, int which);
 struct TPrepWeight {
   const uint32_t* packed; const float* s; const int32_t* col; int R, K, C;
 };
 struct TPrepJob {
   const uint32_t* packed; const float* s; const int32_t* col; int R, K, C;
+  bool int8;
   tu32x4* tw; int32_t* mval; float* rmul;
 };
 struct TPrepJobs {

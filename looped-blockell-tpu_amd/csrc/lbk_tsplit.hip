@@ -7,15 +7,20 @@
 // 24-bit integer multiply-add per element; the output is
 // y = f32(f32(acc) * 2^-e[r]) * sx[token].
 //
-// Weight encoding of the prepared tiles: every weight is stored as t + 1 in
-// {0, 1, 2} (2 bits), so a byte of weights is just (word >> 2q) & 0x03030303 (no
-// table lookup), and the MFMA computes x . (t + 1) = P + sum(x) starting from
-// C = -sum(x): the per-token sums of each 64-wide activation block are kept in
-// LDS beside the activation panel (int32, exact).
+// Weight encodings of the prepared tiles.  Gate and up: the MFMA B fragments as
+// int8 t (4 KB per 64 x 64 tile, fragment-major: [tile][16-column group][lane] x 16
+// bytes), so the gate/up kernel feeds its loads straight to the MFMA (each CU
+// reads its share of tiles once per 64 tokens, well within what L2 delivers).
+// Down: every weight as t + 1 in {0, 1, 2} (2 bits, 1 KB per tile), so a byte
+// of weights is just (word >> 2q) & 0x03030303 (no table lookup), and the MFMA
+// computes x . (t + 1) = P + sum(x) starting from C = -sum(x): the per-token
+// sums of each 64-wide activation block are kept in LDS beside the activation
+// panel (int32, exact).  The down kernel reuses each tile for only 16 tokens,
+// so its weights stay in the 2-bit form (a quarter of the bytes through L2).
 //
-//   tprep_kernel  per call, gate, up and down in one launch: packed tiles [R,K,64,4] -> fragment-major words in
-//                 the t + 1 encoding (lane l of a wave reads its 4 words with one
-//                 dwordx4; dead slots and one appended tile encode t = 0), m per
+//   tprep_kernel  per call or once per weight version, gate, up and down in one
+//                 launch: packed tiles [R,K,64,4] -> the fragment-major forms
+//                 above (dead slots and one appended tile encode t = 0), m per
 //                 tile (zero for dead slots and the appended tile), and 2^-e[r]
 //                 per row.
 //   tgu_kernel    gate/up + SiLU*mul: a workgroup owns 64 tokens (int8 x panel
@@ -41,7 +46,6 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 // ring depths (tile slots prefetched ahead): a gate/up slot is a (gate, up) tile pair, 32
 // MFMAs; a down slot is one tile, 4 MFMAs
 constexpr int TG_RING = 2;
-constexpr int TD_RING = 8;
 
 __device__ __forceinline__ u32x4 lds16t(const unsigned char* base, uint32_t off) {
   return *reinterpret_cast<const u32x4*>(base + off);
@@ -82,7 +86,7 @@ __device__ __forceinline__ int sum16_i8(const u32x4& v) {
 // weight preparation
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void tprep_tile(const uint32_t* __restrict__ packed, const float* __restrict__ s,
-                                           const int32_t* __restrict__ col, int R, int K, int C,
+                                           const int32_t* __restrict__ col, int R, int K, int C, bool int8,
                                            u32x4* __restrict__ tw, int32_t* __restrict__ mval,
                                            float* __restrict__ rmul, int64_t t) {
   const int l = threadIdx.x, j = l & 15, g = l >> 4;
@@ -92,13 +96,21 @@ __device__ __forceinline__ void tprep_tile(const uint32_t* __restrict__ packed, 
     const int c = col[t];
     alive = c >= 0 && c < C;
   }
-  u32x4 v = {0x55555555u, 0x55555555u, 0x55555555u, 0x55555555u};   // t = 0
+  // storage words of column 4j + n, inputs 16g..16g+15 (dead: all codes 0, t = 0)
+  uint32_t wv[4] = {0u, 0u, 0u, 0u};
   if (alive) {
     const uint32_t* tile = packed + t * (64 * 4);
 #pragma unroll
-    for (int n = 0; n < 4; ++n) v[n] = recode_t1(tile[(4 * j + n) * 4 + g]);   // column 4j + n, inputs 16g..16g+15
+    for (int n = 0; n < 4; ++n) wv[n] = tile[(4 * j + n) * 4 + g];
   }
-  tw[t * 64 + l] = v;
+  if (int8) {
+    // group n: the 16 int8 weights of column 4j + n, byte 4q + b = input 16g + 4q + b
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+      tw[(t * 4 + n) * 64 + l] = u32x4{unpack4(wv[n], 0), unpack4(wv[n], 1), unpack4(wv[n], 2), unpack4(wv[n], 3)};
+  } else {
+    tw[t * 64 + l] = u32x4{recode_t1(wv[0]), recode_t1(wv[1]), recode_t1(wv[2]), recode_t1(wv[3])};
+  }
   if (l == 0) {
     int m = 0;
     if (t < ntiles) {
@@ -119,16 +131,16 @@ __global__ __launch_bounds__(64) void tprep_kernel(TPrepJobs jobs) {
   for (int u = 1; u < 3; ++u)
     if ((int64_t)blockIdx.x >= jobs.first[u]) t = u;
   const TPrepJob& J = jobs.job[t];
-  tprep_tile(J.packed, J.s, J.col, J.R, J.K, J.C, J.tw, J.mval, J.rmul, (int64_t)blockIdx.x - jobs.first[t]);
+  tprep_tile(J.packed, J.s, J.col, J.R, J.K, J.C, J.int8, J.tw, J.mval, J.rmul, (int64_t)blockIdx.x - jobs.first[t]);
 }
 
 // ---------------------------------------------------------------------------
 // gate/up
 // ---------------------------------------------------------------------------
 struct TSlot {
-  u32x4 wg, wu;      // fragment words of the gate and up tiles
-  int cg, cu;        // input column blocks (dead -> 0, weights are zero)
-  int mg, mu;        // their fixed-point scales
+  u32x4 wg[4], wu[4];   // int8 fragments of the gate and up tiles, one per 16-column group
+  int cg, cu;           // input column blocks (dead -> 0, weights are zero)
+  int mg, mu;           // their fixed-point scales
 };
 
 template <int MT>
@@ -149,14 +161,12 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
   const int RH = (a.R_ff + a.H - 1) / a.H;
   const int r_lo = half * RH, r_hi = (r_lo + RH) < a.R_ff ? (r_lo + RH) : a.R_ff;
   const int64_t ztile = (int64_t)a.R_ff * K;
-  // LDS: x panel | -sum(x) per (input block, token) [32][TM] int32 | slot table
-  // {cg, cu, mg, mu} of this slice | row table {2^-e_g, 2^-e_u}.  Every per-slot and per-row
-  // value the loop needs is read from LDS: a scalar load in the loop would make each slot
-  // wait for the latest one (scalar loads return out of order).
-  constexpr int RSB = 32 * TM * 4;
-  int* rsum = reinterpret_cast<int*>(smem + (size_t)TM * ROWB);
-  int4* ctab = reinterpret_cast<int4*>(smem + (size_t)TM * ROWB + RSB);
-  float2* rtab = reinterpret_cast<float2*>(smem + (size_t)TM * ROWB + RSB + (size_t)RH * K * 16);
+  const int nrem = (int)(a.N - t0 < TM ? a.N - t0 : TM);   // tokens of this block that exist
+  // LDS: x panel | slot table {cg, cu, mg, mu} of this slice | row table {2^-e_g, 2^-e_u}.
+  // Every per-slot and per-row value the loop needs is read from LDS: a scalar load in the
+  // loop would make each slot wait for the latest one (scalar loads return out of order).
+  int4* ctab = reinterpret_cast<int4*>(smem + (size_t)TM * ROWB);
+  float2* rtab = reinterpret_cast<float2*>(smem + (size_t)TM * ROWB + (size_t)RH * K * 16);
   float* hred = reinterpret_cast<float*>(smem);   // reused after the loop: [8 waves][TM]
   __shared__ float s_sx[TM];
 
@@ -176,8 +186,10 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
     const bool live = rn < nrows && rk < K;
     const int r = r_lo + w + 8 * rn;
     const int64_t e = live ? (int64_t)r * K + rk : ztile;
-    S.wg = a.twg[e * 64 + lane];
-    S.wu = a.twu[e * 64 + lane];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) S.wg[n] = a.twg[(e * 4 + n) * 64 + lane];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) S.wu[n] = a.twu[(e * 4 + n) * 64 + lane];
     S.cg = live ? (r - r_lo) * K + rk : -1;
   };
   auto fetch_c = [&](TSlot& S) {
@@ -234,16 +246,6 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
       const int e = tid + 512 * it;
       *reinterpret_cast<u32x4*>(smem + tpanel_addr<MT>(e / CPR, e % CPR, ROWB)) = pv[it];
     }
-    // -sum(x) of each 64-wide block: the 4 chunks of a block sit in 4 adjacent lanes
-#pragma unroll
-    for (int it = 0; it < PIT; ++it) {
-      const int e = tid + 512 * it;
-      const int row = e / CPR, cc = e % CPR;
-      int sm = sum16_i8(pv[it]);
-      sm += __shfl_xor(sm, 1, 64);
-      sm += __shfl_xor(sm, 2, 64);
-      if ((cc & 3) == 0 && cc < cpr) rsum[(cc >> 2) * TM + row] = -sm;
-    }
   }
   // running max |h| per token of this lane: bf16 bit patterns of |h| (non-negative, so integer
   // order is float order), two tokens (v, v + 1) per register
@@ -260,49 +262,37 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
     const uint32_t lbase = (uint32_t)(i * MT * ROWB);
     i32x4 ag[MT][4], au[MT][4];
     // a (gate, up) tile pair as 16 steps (tile, 16-column group n, token-tile half): a step's two
-    // MFMAs give block partials P, whose acc += m * P runs in the next step beside that step's
-    // MFMAs.  Scheduling fences between steps bound the live partials to two steps and the
-    // activation fragments to one tile (the up fragments are read during the gate's last group).
+    // MFMAs give block partials P (int8 t straight from the ring, C = 0), whose acc += m * P runs
+    // in the next step beside that step's MFMAs.  Scheduling fences between steps bound the live
+    // partials to two steps and the activation fragments to one tile (the up fragments are read
+    // during the gate's last group).
     static_assert(MT == 4, "two token tiles per step");
     auto compute = [&](const TSlot& S) {
       const int mg = uniform(S.mg), mu = uniform(S.mu);
       const int cgc = uniform(S.cg), cuc = uniform(S.cu);
       const uint32_t ag0 = lbase + (((cgc * 4 + g) ^ i) << 4);
       const uint32_t au0 = lbase + (((cuc * 4 + g) ^ i) << 4);
-      const int* zg = rsum + cgc * TM + 4 * g;
-      const int* zu = rsum + cuc * TM + 4 * g;
-      i32x4 av[MT], avu[MT], cz[MT], czu[MT];
+      i32x4 av[MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        av[mt] = __builtin_bit_cast(i32x4, lds16t(smem, ag0 + mt * ROWB));
-        cz[mt] = *reinterpret_cast<const i32x4*>(zg + 16 * mt);
-      }
-      i32x4 Pp[2], f;
+      for (int mt = 0; mt < MT; ++mt) av[mt] = __builtin_bit_cast(i32x4, lds16t(smem, ag0 + mt * ROWB));
+      const i32x4 zero = {0, 0, 0, 0};
+      i32x4 Pp[2];
 #pragma unroll
       for (int q = 0; q < 17; ++q) {
         i32x4 Pn[2];
         if (q < 16) {
           const bool up = q >= 8;
           const int n = (q >> 1) & 3, hh = q & 1;
-          if (q == 6) {
+          // the up fragments replace the gate's one half at a time, a step before their use
+          // (step 7 is the gate's last use of token tiles 0-1, step 8 of 2-3)
+          if (q == 7 || q == 8) {
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) avu[mt] = __builtin_bit_cast(i32x4, lds16t(smem, au0 + mt * ROWB));
+            for (int mt = 2 * (q - 7); mt < 2 * (q - 7) + 2; ++mt)
+              av[mt] = __builtin_bit_cast(i32x4, lds16t(smem, au0 + mt * ROWB));
           }
-          if (q == 7) {
+          const i32x4 f = __builtin_bit_cast(i32x4, up ? S.wu[n] : S.wg[n]);
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt) czu[mt] = *reinterpret_cast<const i32x4*>(zu + 16 * mt);
-          }
-          if (q == 8) {
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) av[mt] = avu[mt];
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) cz[mt] = czu[mt];
-#pragma unroll
-            for (int mt = 2; mt < MT; ++mt) cz[mt] = *reinterpret_cast<const i32x4*>(zu + 16 * mt);
-          }
-          if (hh == 0) f = tunpack(up ? S.wu[n] : S.wg[n]);
-#pragma unroll
-          for (int u = 0; u < 2; ++u) Pn[u] = mfma_i8_k64(av[2 * hh + u], f, cz[2 * hh + u]);
+          for (int u = 0; u < 2; ++u) Pn[u] = mfma_i8_k64(av[2 * hh + u], f, zero);
         }
         if (q > 0) {
           const int pq = q - 1;
@@ -353,13 +343,21 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
       const int r = r_lo + w + 8 * n;
       const float2 fr = rtab[r - r_lo];
       const float fg = fr.x, fu = fr.y;
-      const int64_t col0 = (int64_t)r * 64 + 4 * i;
+      // 32-bit element offsets from the token block's first row (< 64 * d_ff), token bounds as a
+      // compare against the rows left: no 64-bit address per (mt, v) stays live across the loop
+      uint32_t dffu = (uint32_t)d_ff;
+      int nr = nrem;
+      asm("" : "+s"(dffu), "+s"(nr));   // keeps offsets and bounds from being hoisted out of the row loop
+      const uint32_t lane_off = (uint32_t)(4 * g) * dffu + (uint32_t)(r * 64 + 4 * i);
+      const int64_t rb = t0 * d_ff;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const int64_t t = t0 + 16 * mt + 4 * g + v;
-          const float sxv = s_sx[16 * mt + 4 * g + v];
+          const int tl = 16 * mt + 4 * g + v;
+          const bool tok = tl < nr;
+          const uint32_t off = lane_off + (uint32_t)(16 * mt + v) * dffu;
+          const float sxv = s_sx[tl];
           const float cg = fg * sxv, cu = fu * sxv;
           const float k = cg * -1.4426950408889634f;
           const float ic = fminf(__builtin_amdgcn_rcpf(cg * cu), 1e38f);
@@ -376,23 +374,21 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
           const unsigned short tm = pm[0] > pm[1] ? pm[0] : pm[1];
           hmax[mt][v >> 1] = __builtin_elementwise_max(hmax[mt][v >> 1],
                                                        (v & 1) ? u16x2{0, tm} : u16x2{tm, 0});
-          if (t < a.N) *reinterpret_cast<u32x2*>(a.h + t * d_ff + col0) = u32x2{p01, p23};
+          if (tok) *reinterpret_cast<u32x2*>(a.h + rb + off) = u32x2{p01, p23};
           // optional export of the integer accumulators and the fp32 pre-activations
-          if (a.acc_g && t < a.N) {
-            *reinterpret_cast<i32x4*>(a.acc_g + t * d_ff + col0) =
-                i32x4{ag[mt][0][v], ag[mt][1][v], ag[mt][2][v], ag[mt][3][v]};
-            *reinterpret_cast<i32x4*>(a.acc_u + t * d_ff + col0) =
-                i32x4{au[mt][0][v], au[mt][1][v], au[mt][2][v], au[mt][3][v]};
+          if (a.acc_g && tok) {
+            *reinterpret_cast<i32x4*>(a.acc_g + rb + off) = i32x4{ag[mt][0][v], ag[mt][1][v], ag[mt][2][v], ag[mt][3][v]};
+            *reinterpret_cast<i32x4*>(a.acc_u + rb + off) = i32x4{au[mt][0][v], au[mt][1][v], au[mt][2][v], au[mt][3][v]};
           }
-          if (a.g_pre && t < a.N) {
+          if (a.g_pre && tok) {
             float gp[4], up[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
               gp[q] = __fmul_rn(__fmul_rn((float)ag[mt][q][v], fg), sxv);
               up[q] = __fmul_rn(__fmul_rn((float)au[mt][q][v], fu), sxv);
             }
-            *reinterpret_cast<float4*>(a.g_pre + t * d_ff + col0) = make_float4(gp[0], gp[1], gp[2], gp[3]);
-            *reinterpret_cast<float4*>(a.u_pre + t * d_ff + col0) = make_float4(up[0], up[1], up[2], up[3]);
+            *reinterpret_cast<float4*>(a.g_pre + rb + off) = make_float4(gp[0], gp[1], gp[2], gp[3]);
+            *reinterpret_cast<float4*>(a.u_pre + rb + off) = make_float4(up[0], up[1], up[2], up[3]);
           }
         }
     }
@@ -434,8 +430,10 @@ struct TDSlot {
   int2 cm;   // input column block (dead -> 0), fixed-point scale
 };
 
-__global__ __launch_bounds__(512, 1) void tdn_kernel(TDNArgs a) {
+template <int NW, int RING, int UB>
+__global__ __launch_bounds__(64 * NW, 1) void tdn_kernel(TDNArgs a) {
   constexpr int TM = 16;
+  constexpr int NT = 64 * NW;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   __shared__ float s_scale[TM], s_sh[TM];
   const int tid = threadIdx.x;
@@ -452,11 +450,11 @@ __global__ __launch_bounds__(512, 1) void tdn_kernel(TDNArgs a) {
   int* rsum = reinterpret_cast<int*>(smem + (size_t)TM * d_ff);
   int2* dtab = reinterpret_cast<int2*>(smem + (size_t)TM * d_ff + (size_t)a.C_d * TM * 4);
   float* rtab = reinterpret_cast<float*>(smem + (size_t)TM * d_ff + (size_t)a.C_d * TM * 4 + (size_t)a.R_m * Kd * 8);
-  for (int e = tid; e < a.R_m * Kd; e += 512) {
+  for (int e = tid; e < a.R_m * Kd; e += NT) {
     const int c = a.cd[e];
     dtab[e] = make_int2((c >= 0 && c < a.C_d) ? c : 0, a.md[e]);
   }
-  for (int e = tid; e < a.R_m; e += 512) rtab[e] = a.rmd[e];
+  for (int e = tid; e < a.R_m; e += NT) rtab[e] = a.rmd[e];
 
   // ---- per-token absmax over the slices -> quantisation scale (as quantize_act_kernel)
   if (tid < TM) {
@@ -470,13 +468,13 @@ __global__ __launch_bounds__(512, 1) void tdn_kernel(TDNArgs a) {
     if (a.sh_out && t < a.N) a.sh_out[t] = amax * 0.0078125f;
   }
 
-  // ---- ring of down tiles: wave w owns rows rm = w, w+8, ...
-  const int nrows = (a.R_m - w + 7) / 8;
-  const int KP = (Kd + TD_RING - 1) / TD_RING * TD_RING;
+  // ---- ring of down tiles: wave w owns rows rm = w, w + NW, ...
+  const int nrows = (a.R_m - w + NW - 1) / NW;
+  const int KP = (Kd + RING - 1) / RING * RING;
   int rn = 0, rk = 0;
   auto fetch = [&](TDSlot& S) {
     const bool live = rn < nrows && rk < Kd;
-    const int rm = w + 8 * rn;
+    const int rm = w + NW * rn;
     const int64_t e = live ? (int64_t)rm * Kd + rk : ztile;
     S.wd = a.twd[e * 64 + lane];
     S.cm = make_int2(live ? (int)e : 0, 0);
@@ -485,27 +483,31 @@ __global__ __launch_bounds__(512, 1) void tdn_kernel(TDNArgs a) {
       ++rn;
     }
   };
-  TDSlot P[TD_RING];
+  TDSlot P[RING];
 #pragma unroll
-  for (int sl = 0; sl < TD_RING; ++sl) fetch(P[sl]);
+  for (int sl = 0; sl < RING; ++sl) fetch(P[sl]);
   __syncthreads();   // s_scale, dtab, rtab
   // slot metadata from LDS: for the prefetched slots here, for later ones one ring cycle ahead
   auto meta = [&](TDSlot& S) { S.cm = dtab[S.cm.x]; };   // padding slots: zero tiles, any entry
 #pragma unroll
-  for (int sl = 0; sl < TD_RING; ++sl) meta(P[sl]);
+  for (int sl = 0; sl < RING; ++sl) meta(P[sl]);
 
   // ---- panel: the 16 h rows quantised to int8.  A unit is 16 values (32 bytes of h) of one
-  // row; thread tid takes the units cc = tid, tid + 512, ... of every row (no index division),
-  // rows in batches of 8 whose loads are all issued before any is converted.  Quantisation
-  // per value: q = clamp(rint(h * scale), -128, 127) computed as med3(h * scale, -128, 127) +
-  // 1.5 * 2^23 (the add rounds to the nearest integer, ties to even, and leaves the int8 two's
-  // complement in the low byte of the float); bytes of four values merged with two v_perm.
+  // row.  With at least as many threads as units per row (upr), thread tid takes unit
+  // tid % upr of the rows of row group tid / upr (NT / upr groups; one division per thread),
+  // otherwise units tid, tid + NT, ... of every row; rows go in batches of UB whose loads are
+  // all issued before any is converted.  Quantisation per value: q = clamp(rint(h * scale),
+  // -128, 127) computed as med3(h * scale, -128, 127) + 1.5 * 2^23 (the add rounds to the
+  // nearest integer, ties to even, and leaves the int8 two's complement in the low byte of the
+  // float); bytes of four values merged with two v_perm.
   {
-    constexpr int UB = 8;
     const int upr = d_ff / 16;          // units per row (a multiple of 16)
-    for (int cc = tid; cc < upr; cc += 512) {
+    const bool wide = upr > NT;
+    const int rstep = wide ? 1 : NT / upr;
+    const int rg = wide ? 0 : tid / upr;
+    for (int cc = wide ? tid : tid - rg * upr; cc < upr; cc += wide ? NT : upr) {
 #pragma unroll 1
-      for (int rb = 0; rb < TM; rb += UB) {
+      for (int rb = rg * UB; rb < TM; rb += rstep * UB) {
         u32x4 hv[UB][2];
 #pragma unroll
         for (int b = 0; b < UB; ++b) {
@@ -579,9 +581,9 @@ __global__ __launch_bounds__(512, 1) void tdn_kernel(TDNArgs a) {
       Pp[q] = i32x4{0, 0, 0, 0};
     }
     mp = 0;
-    for (int k = 0; k < KP; k += TD_RING) {
+    for (int k = 0; k < KP; k += RING) {
 #pragma unroll
-      for (int sl = 0; sl < TD_RING; ++sl) {
+      for (int sl = 0; sl < RING; ++sl) {
         const int m = uniform(P[sl].cm.y);
         i32x4 Pn[4];
 #pragma unroll
@@ -592,14 +594,14 @@ __global__ __launch_bounds__(512, 1) void tdn_kernel(TDNArgs a) {
         mp = m;
         fetch(P[sl]);
         meta(P[sl]);
-        av = a_frag(P[(sl + 1) % TD_RING]);   // the next slot in ring order
-        cz = c_frag(P[(sl + 1) % TD_RING]);
+        av = a_frag(P[(sl + 1) % RING]);   // the next slot in ring order
+        cz = c_frag(P[(sl + 1) % RING]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
     madd(acc, Pp, mp);
     // epilogue of down row rm: y = f32(f32(acc) * 2^-e) * sh (+ residual) -> bf16
-    const int rm = w + 8 * n;
+    const int rm = w + NW * n;
     const float fd = rtab[rm];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -625,10 +627,10 @@ __global__ __launch_bounds__(512, 1) void tdn_kernel(TDNArgs a) {
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-size_t tprep_bytes(int64_t ntiles, int R) {
-  // words (1 KB per tile, + zero tile) | m per tile | row multipliers, each 256-aligned
+size_t tprep_bytes(int64_t ntiles, int R, int which) {
+  // tiles (+ zero tile) | m per tile | row multipliers, each 256-aligned
   auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-  return al((size_t)(ntiles + 1) * 1024) + al((size_t)(ntiles + 1) * 4) + al((size_t)R * 4);
+  return al((size_t)(ntiles + 1) * tprep_tile_bytes(which)) + al((size_t)(ntiles + 1) * 4) + al((size_t)R * 4);
 }
 
 int launch_tprep(const TPrepWeight (&w)[3], void* const (&out)[3], const u32x4* (&tw)[3],
@@ -638,13 +640,15 @@ int launch_tprep(const TPrepWeight (&w)[3], void* const (&out)[3], const u32x4* 
   int64_t blocks = 0;
   for (int t = 0; t < 3; ++t) {
     const int64_t nt = (int64_t)w[t].R * w[t].K;
+    const size_t tiles = al((size_t)(nt + 1) * tprep_tile_bytes(t));
     char* p = static_cast<char*>(out[t]);
     TPrepJob& j = J.job[t];
     j.packed = w[t].packed; j.s = w[t].s; j.col = w[t].col;
     j.R = w[t].R; j.K = w[t].K; j.C = w[t].C;
+    j.int8 = tprep_tile_bytes(t) == 4096;
     j.tw = reinterpret_cast<u32x4*>(p);
-    j.mval = reinterpret_cast<int32_t*>(p + al((size_t)(nt + 1) * 1024));
-    j.rmul = reinterpret_cast<float*>(p + al((size_t)(nt + 1) * 1024) + al((size_t)(nt + 1) * 4));
+    j.mval = reinterpret_cast<int32_t*>(p + tiles);
+    j.rmul = reinterpret_cast<float*>(p + tiles + al((size_t)(nt + 1) * 4));
     tw[t] = j.tw;
     mval[t] = j.mval;
     rmul[t] = j.rmul;
@@ -659,7 +663,7 @@ int launch_tprep(const TPrepWeight (&w)[3], void* const (&out)[3], const u32x4* 
 
 // LDS bytes of the two kernels (dynamic part; each also has <= 256 bytes of static LDS)
 static size_t tgu_lds(int RH, int K) {
-  return (size_t)64 * 2048 + (size_t)32 * 64 * 4 + (size_t)RH * K * 16 + (size_t)RH * 8;
+  return (size_t)64 * 2048 + (size_t)RH * K * 16 + (size_t)RH * 8;
 }
 static size_t tdn_lds(int d_ff, int R_m, int Kd) {
   return (size_t)16 * d_ff + (size_t)(d_ff / 64) * 16 * 4 + (size_t)R_m * Kd * 8 + (size_t)R_m * 4;
@@ -692,12 +696,19 @@ int launch_tgu(const TGUArgs& a, hipStream_t st) {
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// down kernel shape: TDN_WAVES waves (two down rows each at d_model 2048), a ring of TDN_RING
+// tiles per wave, TDN_UB h rows per load batch of the panel fill.  Measured at d_model 2048,
+// d_ff 8192, 8192 tokens (ternary forward from xq, kernel time): 16 waves, ring 4 142 us;
+// 16 waves, ring 8 144 us; 8 waves (four rows each), ring 8 153 us.
+constexpr int TDN_WAVES = 16, TDN_RING = 4, TDN_UB = 4;
+
 int launch_tdn(const TDNArgs& a, hipStream_t st) {
   if (a.N == 0) return 0;
+  auto kern = tdn_kernel<TDN_WAVES, TDN_RING, TDN_UB>;
   static std::atomic<uint64_t> configured{0};
-  if (set_lds_limit_once((const void*)tdn_kernel, 163840 - 256, configured)) return -1;
+  if (set_lds_limit_once((const void*)kern, 163840 - 256, configured)) return -1;
   const size_t lds = tdn_lds(a.d_ff, a.R_m, a.Kd);
-  hipLaunchKernelGGL(tdn_kernel, dim3((unsigned)((a.N + 15) / 16)), dim3(512), lds, st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 15) / 16)), dim3(64 * TDN_WAVES), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
