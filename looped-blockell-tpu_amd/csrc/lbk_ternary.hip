@@ -26,6 +26,28 @@ namespace lbk {
 // ---------------------------------------------------------------------------
 // per-token absmax int8 quantisation: one wave per row
 // ---------------------------------------------------------------------------
+// one wave per row: rows of at most 512 * QA_REG values are read once into registers (all loads
+// issued before the reduction), longer rows in two passes
+constexpr int QA_REG = 8;
+
+__device__ __forceinline__ u32x2 quantize8(const u32x4& v, float scale) {
+  uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const float a = fminf(fmaxf(rintf(__fmul_rn(bf_lo(v[u]), scale)), -128.f), 127.f);
+    const float b = fminf(fmaxf(rintf(__fmul_rn(bf_hi(v[u]), scale)), -128.f), 127.f);
+    const uint32_t qa = (uint32_t)((int)a) & 0xffu, qb = (uint32_t)((int)b) & 0xffu;
+    packed[u >> 1] |= (qa | (qb << 8)) << (16 * (u & 1));
+  }
+  return u32x2{packed[0], packed[1]};
+}
+
+__device__ __forceinline__ float absmax8(const u32x4& v, float amax) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) amax = fmaxf(amax, fmaxf(fabsf(bf_lo(v[u])), fabsf(bf_hi(v[u]))));
+  return amax;
+}
+
 __global__ __launch_bounds__(256) void quantize_act_kernel(const uint16_t* __restrict__ x, int64_t N, int F,
                                                            int64_t ldx, int8_t* __restrict__ xq,
                                                            float* __restrict__ sx) {
@@ -33,28 +55,34 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const uint16_t* __res
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= N) return;
   const uint16_t* xr = x + row * ldx;
-  float amax = 0.f;
-  for (int c = 8 * lane; c < F; c += 512) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + c);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) amax = fmaxf(amax, fmaxf(fabsf(bf_lo(v[u])), fabsf(bf_hi(v[u]))));
-  }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-  amax = fmaxf(amax, 1e-8f);
-  const float scale = __fdiv_rn(128.0f, amax);
   int8_t* qr = xq + row * (int64_t)F;
-  for (int c = 8 * lane; c < F; c += 512) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + c);
-    uint32_t packed[2] = {0u, 0u};
+  float amax = 0.f;
+  if (F <= 512 * QA_REG) {
+    u32x4 v[QA_REG];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float a = fminf(fmaxf(rintf(__fmul_rn(bf_lo(v[u]), scale)), -128.f), 127.f);
-      const float b = fminf(fmaxf(rintf(__fmul_rn(bf_hi(v[u]), scale)), -128.f), 127.f);
-      const uint32_t qa = (uint32_t)((int)a) & 0xffu, qb = (uint32_t)((int)b) & 0xffu;
-      packed[u >> 1] |= (qa | (qb << 8)) << (16 * (u & 1));
+    for (int u = 0; u < QA_REG; ++u) {
+      const int c = 8 * lane + 512 * u;
+      v[u] = c < F ? *reinterpret_cast<const u32x4*>(xr + c) : u32x4{0, 0, 0, 0};
     }
-    *reinterpret_cast<u32x2*>(qr + c) = u32x2{packed[0], packed[1]};
+#pragma unroll
+    for (int u = 0; u < QA_REG; ++u) amax = absmax8(v[u], amax);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    amax = fmaxf(amax, 1e-8f);
+    const float scale = __fdiv_rn(128.0f, amax);
+#pragma unroll
+    for (int u = 0; u < QA_REG; ++u) {
+      const int c = 8 * lane + 512 * u;
+      if (c < F) *reinterpret_cast<u32x2*>(qr + c) = quantize8(v[u], scale);
+    }
+  } else {
+    for (int c = 8 * lane; c < F; c += 512) amax = absmax8(*reinterpret_cast<const u32x4*>(xr + c), amax);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    amax = fmaxf(amax, 1e-8f);
+    const float scale = __fdiv_rn(128.0f, amax);
+    for (int c = 8 * lane; c < F; c += 512)
+      *reinterpret_cast<u32x2*>(qr + c) = quantize8(*reinterpret_cast<const u32x4*>(xr + c), scale);
   }
   if (lane == 0) sx[row] = amax * 0.0078125f;
 }

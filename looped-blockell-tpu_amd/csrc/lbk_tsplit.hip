@@ -162,11 +162,14 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
   const int r_lo = half * RH, r_hi = (r_lo + RH) < a.R_ff ? (r_lo + RH) : a.R_ff;
   const int64_t ztile = (int64_t)a.R_ff * K;
   const int nrem = (int)(a.N - t0 < TM ? a.N - t0 : TM);   // tokens of this block that exist
-  // LDS: x panel | slot table {cg, cu, mg, mu} of this slice | row table {2^-e_g, 2^-e_u}.
+  // LDS: x panel | slot table {cg, cu, mg, mu} of this slice | row table {2^-e_g, 2^-e_u} |
+  // per-token epilogue factors.
   // Every per-slot and per-row value the loop needs is read from LDS: a scalar load in the
   // loop would make each slot wait for the latest one (scalar loads return out of order).
   int4* ctab = reinterpret_cast<int4*>(smem + (size_t)TM * ROWB);
   float2* rtab = reinterpret_cast<float2*>(smem + (size_t)TM * ROWB + (size_t)RH * K * 16);
+  // per token: (-log2(e) * sx, 1 / sx^2) for the epilogue
+  float2* s_tf = reinterpret_cast<float2*>(smem + (size_t)TM * ROWB + (size_t)RH * K * 16 + (size_t)RH * 8);
   float* hred = reinterpret_cast<float*>(smem);   // reused after the loop: [8 waves][TM]
   __shared__ float s_sx[TM];
 
@@ -224,7 +227,7 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
   // unconditional (clamped addresses, zero selected afterwards) so that each store below waits
   // only for its own load
   const int64_t tsx = t0 + (tid & 63);
-  const float sxv = a.sx[tsx < a.N ? tsx : a.N - 1];
+  const float sx_own = a.sx[tsx < a.N ? tsx : a.N - 1];
   {
     constexpr int CPR = ROWB / 16;
     constexpr int PIT = TM * CPR / 512;
@@ -240,7 +243,11 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
       pv[it] = (cc < cpr && t < a.N) ? v : u32x4{0, 0, 0, 0};
     }
     prefetch_ring();
-    if (w == 0) s_sx[tid] = tsx < a.N ? sxv : 0.f;
+    if (w == 0) {
+      const float sv = tsx < a.N ? sx_own : 0.f;
+      s_sx[tid] = sv;
+      s_tf[tid] = make_float2(sv * -1.4426950408889634f, __builtin_amdgcn_rcpf(sv * sv));
+    }
 #pragma unroll
     for (int it = 0; it < PIT; ++it) {
       const int e = tid + 512 * it;
@@ -350,6 +357,7 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
       asm("" : "+s"(dffu), "+s"(nr));   // keeps offsets and bounds from being hoisted out of the row loop
       const uint32_t lane_off = (uint32_t)(4 * g) * dffu + (uint32_t)(r * 64 + 4 * i);
       const int64_t rb = t0 * d_ff;
+      const float ifgu = __builtin_amdgcn_rcpf(fg * fu);   // a power of two
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -357,10 +365,11 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
           const int tl = 16 * mt + 4 * g + v;
           const bool tok = tl < nr;
           const uint32_t off = lane_off + (uint32_t)(16 * mt + v) * dffu;
-          const float sxv = s_sx[tl];
-          const float cg = fg * sxv, cu = fu * sxv;
-          const float k = cg * -1.4426950408889634f;
-          const float ic = fminf(__builtin_amdgcn_rcpf(cg * cu), 1e38f);
+          // with cg = 2^-e_g * sx, cu = 2^-e_u * sx: k = -log2(e) * cg, 1 / (cg * cu) =
+          // 2^(e_g + e_u) / sx^2, from per-token factors and the row's power of two
+          const float2 tf = s_tf[tl];
+          const float k = fg * tf.x;
+          const float ic = fminf(tf.y * ifgu, 1e38f);
           float hv[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
@@ -381,6 +390,7 @@ __global__ __launch_bounds__(512, 1) void tgu_kernel(TGUArgs a) {
             *reinterpret_cast<i32x4*>(a.acc_u + rb + off) = i32x4{au[mt][0][v], au[mt][1][v], au[mt][2][v], au[mt][3][v]};
           }
           if (a.g_pre && tok) {
+            const float sxv = s_sx[tl];
             float gp[4], up[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -663,7 +673,7 @@ int launch_tprep(const TPrepWeight (&w)[3], void* const (&out)[3], const u32x4* 
 
 // LDS bytes of the two kernels (dynamic part; each also has <= 256 bytes of static LDS)
 static size_t tgu_lds(int RH, int K) {
-  return (size_t)64 * 2048 + (size_t)RH * K * 16 + (size_t)RH * 8;
+  return (size_t)64 * 2048 + (size_t)RH * K * 16 + (size_t)RH * 8 + (size_t)64 * 8;
 }
 static size_t tdn_lds(int d_ff, int R_m, int Kd) {
   return (size_t)16 * d_ff + (size_t)(d_ff / 64) * 16 * 4 + (size_t)R_m * Kd * 8 + (size_t)R_m * 4;
