@@ -466,6 +466,32 @@ __global__ __launch_bounds__(64 * NW, 1) void tdn_kernel(TDNArgs a) {
   }
   for (int e = tid; e < a.R_m; e += NT) rtab[e] = a.rmd[e];
 
+  // ---- panel fill, part 1: this thread's first batch of h rows is requested before anything
+  // else (the scales it needs come later).  A unit is 16 values (32 bytes of h) of one row.
+  // With at least as many threads as units per row (upr), thread tid takes unit tid % upr of
+  // the rows of row group tid / upr (NT / upr groups; one division per thread), otherwise units
+  // tid, tid + NT, ... of every row; rows go in batches of UB whose loads are all issued before
+  // any is converted.
+  const int upr = d_ff / 16;          // units per row (a multiple of 16)
+  const bool wide = upr > NT;
+  const int rstep = wide ? 1 : NT / upr;
+  const int rg = wide ? 0 : tid / upr;
+  const int cc0 = wide ? tid : tid - rg * upr;
+  const int ccstep = wide ? NT : upr;
+  u32x4 hv[UB][2];
+  auto load_batch = [&](int cc, int rb) {
+#pragma unroll
+    for (int b = 0; b < UB; ++b) {
+      int64_t t = t0 + rb + b;
+      t = t < a.N ? t : a.N - 1;
+      const u32x4* hp = reinterpret_cast<const u32x4*>(a.h + t * (int64_t)d_ff + 16 * cc);
+      hv[b][0] = hp[0];
+      hv[b][1] = hp[1];
+    }
+  };
+  const bool first = cc0 < upr && rg * UB < TM;
+  if (first) load_batch(cc0, rg * UB);
+
   // ---- per-token absmax over the slices -> quantisation scale (as quantize_act_kernel)
   if (tid < TM) {
     const int64_t t = t0 + tid;
@@ -502,31 +528,15 @@ __global__ __launch_bounds__(64 * NW, 1) void tdn_kernel(TDNArgs a) {
 #pragma unroll
   for (int sl = 0; sl < RING; ++sl) meta(P[sl]);
 
-  // ---- panel: the 16 h rows quantised to int8.  A unit is 16 values (32 bytes of h) of one
-  // row.  With at least as many threads as units per row (upr), thread tid takes unit
-  // tid % upr of the rows of row group tid / upr (NT / upr groups; one division per thread),
-  // otherwise units tid, tid + NT, ... of every row; rows go in batches of UB whose loads are
-  // all issued before any is converted.  Quantisation per value: q = clamp(rint(h * scale),
-  // -128, 127) computed as med3(h * scale, -128, 127) + 1.5 * 2^23 (the add rounds to the
-  // nearest integer, ties to even, and leaves the int8 two's complement in the low byte of the
-  // float); bytes of four values merged with two v_perm.
+  // ---- panel fill, part 2: the 16 h rows quantised to int8.  Quantisation per value: q =
+  // clamp(rint(h * scale), -128, 127) computed as med3(h * scale, -128, 127) + 1.5 * 2^23 (the
+  // add rounds to the nearest integer, ties to even, and leaves the int8 two's complement in
+  // the low byte of the float); bytes of four values merged with two v_perm.
   {
-    const int upr = d_ff / 16;          // units per row (a multiple of 16)
-    const bool wide = upr > NT;
-    const int rstep = wide ? 1 : NT / upr;
-    const int rg = wide ? 0 : tid / upr;
-    for (int cc = wide ? tid : tid - rg * upr; cc < upr; cc += wide ? NT : upr) {
+    for (int cc = cc0; cc < upr; cc += ccstep) {
 #pragma unroll 1
       for (int rb = rg * UB; rb < TM; rb += rstep * UB) {
-        u32x4 hv[UB][2];
-#pragma unroll
-        for (int b = 0; b < UB; ++b) {
-          int64_t t = t0 + rb + b;
-          t = t < a.N ? t : a.N - 1;
-          const u32x4* hp = reinterpret_cast<const u32x4*>(a.h + t * (int64_t)d_ff + 16 * cc);
-          hv[b][0] = hp[0];
-          hv[b][1] = hp[1];
-        }
+        if (cc != cc0 || rb != rg * UB) load_batch(cc, rb);
 #pragma unroll
         for (int b = 0; b < UB; ++b) {
           const int row = rb + b;
