@@ -158,8 +158,9 @@ __global__ __launch_bounds__(512, 1) void decode_gu_kernel(DecodeArgs a) {
   const bool use0 = k0 < Km, use1 = k1 < Km;
   const int64_t e0 = (int64_t)r * Km + (use0 ? k0 : 0), e1 = (int64_t)r * Km + (use1 ? k1 : 0);
   // Request order (a wave's loads return in order): the two column indices (one vector
-  // load), this workgroup's tiles (their addresses need no index), its share of the down
-  // tiles, then the x fragments the indices select.
+  // load), this workgroup's tiles (their addresses need no index), the x fragments the indices
+  // select (issued once the indices are back), then its share of the down tiles, which nothing
+  // waits for until the end, so the MFMAs, the reduction and the h stores run while it streams.
   const int cl = cm[lane == 1 ? e1 : e0];
   asm volatile("" ::: "memory");
   WRaw<B> t0, t1;
@@ -167,12 +168,13 @@ __global__ __launch_bounds__(512, 1) void decode_gu_kernel(DecodeArgs a) {
   load_wraw<B>(vm + e0 * B * B, lane, t0);
   load_wraw<B>(vm + e1 * B * B, lane, t1);
   asm volatile("" ::: "memory");
-  const uint32_t pf = prefetch_down_share<B, 4>(a, r, decode_gu_per_xcd(a.R_ff), tid);
-  asm volatile("" ::: "memory");
   const int c0 = use0 ? __builtin_amdgcn_readlane(cl, 0) : -1, c1 = use1 ? __builtin_amdgcn_readlane(cl, 1) : -1;
   const bool ok0 = c0 >= 0 && c0 < C_in, ok1 = c1 >= 0 && c1 < C_in;
   load_a_rows<B>(a.x + (int64_t)(ok0 ? c0 : 0) * B, a.d_model, ok0 ? a.N : 0, i, g, a0);
   load_a_rows<B>(a.x + (int64_t)(ok1 ? c1 : 0) * B, a.d_model, ok1 ? a.N : 0, i, g, a1);
+  asm volatile("" ::: "memory");
+  const uint32_t pf = prefetch_down_share<B, 4>(a, r, decode_gu_per_xcd(a.R_ff), tid);
+  asm volatile("" ::: "memory");
   f32x4 acc[CW];
 #pragma unroll
   for (int m = 0; m < CW; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
