@@ -260,13 +260,8 @@ __global__ __launch_bounds__(512, 1) void decode_dn_kernel(DecodeArgs a) {
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
       *reinterpret_cast<u32x4*>(xw + drow * 16 + 8 * (lane & 1)) = dq[j][ks];
-      const int n = lane & 15;
-      u32x4 f;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int r0 = 8 * g + 2 * u;
-        f[u] = (uint32_t)xw[r0 * 16 + n] | ((uint32_t)xw[(r0 + 1) * 16 + n] << 16);
-      }
+      // rows 8g .. 8g + 7 of column n = lane & 15, by two transposing 64-bit reads
+      const u32x4 f = tr_frag(xw, 16, 0, 0, lane);
       acc = mfma_bf16(av[j][ks], f, acc);
     }
   }

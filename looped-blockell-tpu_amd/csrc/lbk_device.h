@@ -250,4 +250,22 @@ __device__ __forceinline__ void load_bf16<4>(const uint16_t* p, float (&v)[4]) {
   v[3] = bf_hi(w[1]);
 }
 
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane l receives element l % 4 of the 64-bit
+// blocks read by lanes l / 4, 4 + l / 4, 8 + l / 4 and 12 + l / 4 of the group (measured on
+// gfx950).  So if lane s of a group points at row t0 + s / 4, columns c0 + 4 (s % 4) .. + 3 of a
+// row-major [row][column] bf16 slice in LDS, lane l gets column c0 + l of rows t0 .. t0 + 3: two
+// such reads give the 8 consecutive rows (the MFMA's k) of one column that an operand lane
+// holds (lane group g takes rows t0 + 8 g .. t0 + 8 g + 7).
+__device__ __forceinline__ u32x4 tr_frag(const uint16_t* slice, int rowlen, int t0, int c0, int lane) {
+  const int s = lane & 15, g = lane >> 4;
+  const uint16_t* p = slice + (t0 + 8 * g + (s >> 2)) * rowlen + c0 + 4 * (s & 3);
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * rowlen));
+  const u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
+
 }  // namespace lbk
