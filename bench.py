@@ -114,15 +114,16 @@ def make_ternary(R, C, K, B, gen, device):
     return kernels.pack_ternary(t), s, cols
 
 
-def time_steps(step, steps, warmup, step_events=True):
+def time_steps(step, steps, warmup, step_events=False):
     """Run `warmup` untimed steps (more if they take under WARMUP_S), then exactly `steps` timed ones.
 
     Returns (ms_per_step from the host clock between two synchronisations,
-    list of per-step durations from HIP events on the current stream).  With
-    step_events=False the timed steps run back to back with no event between
-    them (a recorded event separates two launches on the GPU, which costs a
-    short kernel several microseconds), and the per-step durations come from
-    a second, untimed pass of the same steps.
+    list of per-step durations from HIP events on the current stream).  The
+    timed steps run back to back with no event between them (a recorded event
+    separates two launches on the GPU, which costs a short kernel several
+    microseconds), and the per-step durations come from a second, untimed pass
+    of the same steps with an event pair around each; with step_events=True
+    the timed pass itself carries the events.
     """
     import torch
     # untimed warm-up: `warmup` steps, continued until the GPU has been busy for WARMUP_S (its
@@ -472,7 +473,7 @@ def bench_decode(steps, warmup, device):
         g, u, d = copies[i % len(copies)]
         kernels.swiglu_fwd(x, *g, *u, *d, add_residual=False)
 
-    eager_ms, per = time_steps(step, steps, warmup, step_events=False)
+    eager_ms, per = time_steps(step, steps, warmup)
 
     # The forward is a ~10 us weight stream, so host submission (python, the op's checks, two
     # launches) is as long as the GPU work: a decode loop runs it from a HIP graph.  One graph
