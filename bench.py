@@ -202,7 +202,7 @@ def bench_bf16(steps, warmup, device):
                       traffic_source=os.path.relpath(TRAFFIC_PROFILE_BF16, ROOT) + " (2 x FETCH_SIZE + WRITE_SIZE "
                                      "of the two launches, the factors a copy of known size reads)",
                       kernel="SwiGLU forward launch pair gu_kernel<32,4,false,false,false,false> + "
-                             "dn_kernel<32,4,1,false>, timed together with HIP events around each step",
+                             "dn_kernel<32,4,1,16,512,false>, timed together with HIP events around each step",
                       algorithmic_flops_per_launch=flops,
                       algorithmic_bytes_per_launch=algorithmic_bytes(w)),
         with_pack=dict(workload="the same forward packing the weights on every call (titan::block_ell_swiglu_fwd: "
