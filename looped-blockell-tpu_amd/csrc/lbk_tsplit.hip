@@ -489,7 +489,9 @@ __global__ __launch_bounds__(64 * NW, 1) void tdn_kernel(TDNArgs a) {
       hv[b][1] = hp[1];
     }
   };
-  const bool first = cc0 < upr && rg * UB < TM;
+  // threads past the last whole row group (when upr does not divide NT) stay idle
+  const bool filler = rg < rstep;
+  const bool first = filler && cc0 < upr && rg * UB < TM;
   if (first) load_batch(cc0, rg * UB);
 
   // ---- per-token absmax over the slices -> quantisation scale (as quantize_act_kernel)
@@ -533,7 +535,7 @@ __global__ __launch_bounds__(64 * NW, 1) void tdn_kernel(TDNArgs a) {
   // add rounds to the nearest integer, ties to even, and leaves the int8 two's complement in
   // the low byte of the float); bytes of four values merged with two v_perm.
   {
-    for (int cc = cc0; cc < upr; cc += ccstep) {
+    for (int cc = filler ? cc0 : upr; cc < upr; cc += ccstep) {
 #pragma unroll 1
       for (int rb = rg * UB; rb < TM; rb += rstep * UB) {
         if (cc != cc0 || rb != rg * UB) load_batch(cc, rb);

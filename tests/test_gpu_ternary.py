@@ -190,6 +190,8 @@ SPLIT_CASES = [
     (512, 2048, 2, 7, 8192 + 3, 0.1),
     (256, 512, 4, 8, 16384 + 37, 0.0),
     (2048, 4096, 5, 3, 200, 0.3),
+    (1024, 6144, 4, 12, 300, 0.1),    # 384 panel units per token row: 1024 threads in 2 whole row groups
+    (512, 9216, 2, 9, 70, 0.0),       # 576 units: one row group, 448 threads idle in the fill
 ]
 
 
@@ -209,6 +211,7 @@ def test_ternary_swiglu_split(gpu, case):
     xq, sx = O.activation_quantize_int8(x)
     xg = T.to_gpu_bf16(x)
     args = (T.to_gpu(xq), T.to_gpu(sx), gpu_tern(g), gpu_tern(u), gpu_tern(d), xg)
+    assert kernels.ternary_prepare(*args[2:5]).numel() > 0, "geometry outside the two-kernel path"
     out, h, hq, sh = kernels.ternary_swiglu_fwd_with_intermediate(*args)
     out_ws = kernels.ternary_swiglu_fwd(*args)
     out, h, hq, sh, out_ws = T.to_np(out), T.to_np(h), T.to_np(hq), T.to_np(sh), T.to_np(out_ws)
