@@ -25,9 +25,11 @@
 //                  of 8 waves streams the list entries of its column blocks
 //                  (c = w, w + 8, ...): tile rows from global memory, dy
 //                  fragments from the panel.
-//   dx_stage_kernel  dx when the output blocks fit 8 waves' accumulators: the dg
-//                  and du columns of 64 tokens pass through LDS 512 at a time and
-//                  a cursor per output block walks its sorted list.
+//   dx_stage_kernel  dx when the output blocks fit the waves' accumulators (16
+//                  waves where they fit 128 VGPRs, else 8): the dg and du columns
+//                  of 64 tokens pass through LDS 512 at a time, and a cursor per
+//                  output block walks its sorted list, whose first 64 entries
+//                  stay in a register.
 //   dw_kernel      tile gradients: a workgroup owns one block row, up to 8 of
 //                  its slots (one per wave) and a chunk of tokens; token slices
 //                  of X and G are staged row-major in LDS and read back
@@ -417,8 +419,9 @@ static int launch_dh_panel(int B, const TProdArgs& a, hipStream_t st) {
 template <int B>
 struct DxStage { static constexpr int COLS = B == 64 ? 256 : 512; };
 
-template <int B, int OPW>
-__global__ __launch_bounds__(512, 1) void dx_stage_kernel(TProdArgs a) {
+template <int B, int OPW, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void dx_stage_kernel(TProdArgs a) {
+  constexpr int NT = 64 * NW;
   constexpr int CW = B / 16;
   constexpr int NKS = B >= 32 ? B / 32 : 1;
   constexpr int MT = 4;
@@ -426,7 +429,7 @@ __global__ __launch_bounds__(512, 1) void dx_stage_kernel(TProdArgs a) {
   constexpr int G = COLS / B;                        // source column blocks per stage
   constexpr int SROWB = COLS * 2;                    // bytes per token row of a stage
   constexpr int SBYTES = 64 * SROWB;                 // 64 KB (32 KB for B = 64)
-  constexpr int PER_T = SBYTES / 16 / 512;           // 16-byte chunks per thread per stage
+  constexpr int PER_T = SBYTES / 16 / NT;            // 16-byte chunks per thread per stage
   extern __shared__ __attribute__((aligned(16))) unsigned char stg[];   // two stages
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = uniform(tid >> 6);
@@ -447,7 +450,7 @@ __global__ __launch_bounds__(512, 1) void dx_stage_kernel(TProdArgs a) {
     const int64_t col0 = (int64_t)(s < ns0 ? s : s - ns0) * COLS;
 #pragma unroll
     for (int u = 0; u < PER_T; ++u) {
-      const int e = tid + 512 * u;
+      const int e = tid + NT * u;
       const int row = e / (SROWB / 16), cc = e - row * (SROWB / 16);
       const int64_t t = t0 + row, col = col0 + 8 * cc;
       const bool ok = t < a.N && col < S.lda;
@@ -458,7 +461,7 @@ __global__ __launch_bounds__(512, 1) void dx_stage_kernel(TProdArgs a) {
   auto stage_store = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < PER_T; ++u) {
-      const int e = tid + 512 * u;
+      const int e = tid + NT * u;
       const int row = e / (SROWB / 16), cc = e - row * (SROWB / 16);
       *reinterpret_cast<u32x4*>(stg + buf * SBYTES + bpanel_addr<MT>(row, cc, SROWB)) = sreg[u];
     }
@@ -478,6 +481,7 @@ __global__ __launch_bounds__(512, 1) void dx_stage_kernel(TProdArgs a) {
   };
   const uint32_t lbase = (uint32_t)(i * MT * SROWB);
   int cur[OPW];                                      // list cursors of the current source
+  int lvr[OPW];                                      // first 64 list entries of each output block
 
   stage_fetch(0);
   stage_store(0);
@@ -487,8 +491,15 @@ __global__ __launch_bounds__(512, 1) void dx_stage_kernel(TProdArgs a) {
     const int st = s < ns0 ? s : s - ns0;
     const TProdSrc& S = a.src[src];
     if (st == 0) {
+      // a new source: each output block's first 64 list entries into a register (lane j holds
+      // entry j), so that a stage finds its run with a ballot instead of a global load
 #pragma unroll
-      for (int o = 0; o < OPW; ++o) cur[o] = 0;
+      for (int o = 0; o < OPW; ++o) {
+        cur[o] = 0;
+        const int c = w + NW * o;
+        const int cnt = c < a.C ? S.cnt[c] : 0;
+        lvr[o] = lane < cnt ? S.list[(int64_t)c * S.cap + lane] : 0x7fffffff;
+      }
     }
     if (s + 1 < nstages) stage_fetch(s + 1);
     const unsigned char* sb = stg + (s & 1) * SBYTES;
@@ -503,7 +514,7 @@ __global__ __launch_bounds__(512, 1) void dx_stage_kernel(TProdArgs a) {
     };
 #pragma unroll
     for (int o = 0; o < OPW; ++o) {
-      const int c = w + 8 * o;
+      const int c = w + NW * o;
       if (c >= a.C) continue;
       auto compute = [&](const Ent& E) {
         const int rb = uniform(E.r) - rlo;           // column block within the stage
@@ -523,12 +534,17 @@ __global__ __launch_bounds__(512, 1) void dx_stage_kernel(TProdArgs a) {
       const int32_t* L = S.list + (int64_t)c * S.cap;
       int jc = cur[o];
       while (jc < cnt) {
-        const int lv = (jc + lane < cnt) ? L[jc + lane] : 0x7fffffff;   // next 64 entries
-        // entries of this stage: the run from jc whose source block is below rhi
-        const uint64_t m = __ballot(jc + lane < cnt && lv / S.K < rhi);
-        const int n = __builtin_popcountll(m);       // a prefix of the 64 lanes (sorted list)
+        // entries of this stage: the run from jc whose source block is below rhi.  Within the
+        // first 64 entries they come from the register (lanes jc .. jc + n - 1), beyond them
+        // from the next 64 entries loaded here (lanes 0 .. n - 1)
+        const bool inreg = jc < 64;
+        const int lv = inreg ? lvr[o] : ((jc + lane < cnt) ? L[jc + lane] : 0x7fffffff);
+        const int base = inreg ? jc : 0;
+        const int lim = inreg ? (cnt < 64 ? cnt : 64) : cnt - jc;
+        const uint64_t m = __ballot(lane >= base && lane < lim && lv / S.K < rhi);
+        const int n = __builtin_popcountll(m);       // a contiguous run of lanes (sorted list)
         if (n == 0) break;
-        auto ent = [&](int jj) { return __builtin_amdgcn_readlane(lv, jj < n ? jj : n - 1); };
+        auto ent = [&](int jj) { return __builtin_amdgcn_readlane(lv, base + (jj < n ? jj : n - 1)); };
         Ent E0, E1;
         load(ent(0), E0);
         for (int jj = 0; jj < n; jj += 2) {
@@ -538,7 +554,7 @@ __global__ __launch_bounds__(512, 1) void dx_stage_kernel(TProdArgs a) {
           if (jj + 1 < n) compute(E1);
         }
         jc += n;
-        if (n < 64) break;                           // the run ended inside this chunk
+        if (base + n < 64) break;                    // the run ended inside this chunk
       }
       cur[o] = jc;
     }
@@ -549,7 +565,7 @@ __global__ __launch_bounds__(512, 1) void dx_stage_kernel(TProdArgs a) {
   // epilogue: dx = acc (+ dy)
 #pragma unroll
   for (int o = 0; o < OPW; ++o) {
-    const int c = w + 8 * o;
+    const int c = w + NW * o;
     if (c >= a.C) continue;
 #pragma unroll
     for (int q = 0; q < MT; ++q) {
@@ -559,14 +575,14 @@ __global__ __launch_bounds__(512, 1) void dx_stage_kernel(TProdArgs a) {
   }
 }
 
-template <int B, int OPW>
+template <int B, int OPW, int NW>
 static int launch_dx_stage_t(const TProdArgs& a, hipStream_t st) {
   constexpr size_t lds = 2 * (size_t)64 * DxStage<B>::COLS * 2;
-  auto kern = dx_stage_kernel<B, OPW>;
+  auto kern = dx_stage_kernel<B, OPW, NW>;
   if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return -1;
-  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 63) / 64)), dim3(512), lds, st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 63) / 64)), dim3(64 * NW), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -576,8 +592,17 @@ static int launch_dx_stage(int B, const TProdArgs& a, hipStream_t st) {
   if (a.nsrc < 1 || a.nsrc > 2) return -2;
   for (int s = 0; s < a.nsrc; ++s)
     if (a.src[s].lda % B) return -2;
+  // 16 waves (four per SIMD to hide the tile loads) when their accumulators fit 128 VGPRs:
+  // headline backward 0.785 -> 0.740 ms, B = 16 at d_model 512 / 1024 0.497 -> 0.447 and
+  // 2.10 -> 1.95 ms against 8 waves; B = 64 keeps 8 waves (16 would spill)
+  const int o16 = (a.C + 15) / 16;
+  if (B == 16 && o16 <= 1) return launch_dx_stage_t<16, 1, 16>(a, st);
+  if (B == 16 && o16 <= 2) return launch_dx_stage_t<16, 2, 16>(a, st);
+  if (B == 16 && o16 <= 4) return launch_dx_stage_t<16, 4, 16>(a, st);
+  if (B == 32 && o16 <= 1) return launch_dx_stage_t<32, 1, 16>(a, st);
+  if (B == 32 && o16 <= 2) return launch_dx_stage_t<32, 2, 16>(a, st);
   const int opw = (a.C + 7) / 8;
-#define LBK_DX(BB, OO) if (B == BB && opw <= OO) return launch_dx_stage_t<BB, OO>(a, st);
+#define LBK_DX(BB, OO) if (B == BB && opw <= OO) return launch_dx_stage_t<BB, OO, 8>(a, st);
   if (B == 16) { LBK_DX(16, 1) LBK_DX(16, 2) LBK_DX(16, 4) LBK_DX(16, 8) }
   if (B == 32) { LBK_DX(32, 1) LBK_DX(32, 2) LBK_DX(32, 4) }
   if (B == 64) { LBK_DX(64, 1) LBK_DX(64, 2) }

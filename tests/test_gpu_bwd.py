@@ -42,6 +42,8 @@ def _run(g, u, d, x, dy, gp, uo, h):
 BWD_CASES = [
     # (d_model, d_ff, B, density, N, sentinel_frac)
     (256, 1024, 16, 0.25, 100, 0.1),
+    (512, 1024, 16, 0.125, 90, 0.05),      # 32 output blocks: dx with 16 waves of two blocks
+    (1024, 512, 16, 0.125, 70, 0.0),       # 64 output blocks: 16 waves of four
     (512, 1024, 32, 0.25, 130, 0.05),
     (128, 512, 64, 0.5, 70, 0.0),
     (1024, 4096, 32, 0.25, 2100, 0.0),     # two token chunks of the tile gradients, ragged tail
