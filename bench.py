@@ -506,12 +506,17 @@ def bench_decode(steps, warmup, device):
     torch.cuda.synchronize()
     graph_kernel_ms = sum(a.elapsed_time(b) for a, b in ev) / (reps * len(copies))
     byts = algorithmic_bytes(w)
-    gbs = byts / (ms * 1e-3) / 1e9
+    # the line reports the faster of the two ways a decode loop runs the forward (both measured
+    # on the host clock over whole steps; when the host keeps up, eager submission skips the
+    # graph's per-node overhead)
+    best, mode = (eager_ms, "eager launches") if eager_ms < ms else (ms, "HIP graph replay")
+    gbs = byts / (best * 1e-3) / 1e9
     return dict(workload="decode SwiGLU FFN, 16 tokens, d_model=4096 d_ff=14336 B=64 density=0.10, "
-                         f"{w['copies']} rotating weight copies, forwards replayed from a HIP graph",
-                ms_per_step=ms, value=gbs, unit="GB/s", frac_of_hbm_peak=gbs / PEAK_HBM_GBS,
-                tflops=nonzero_flops(w) / (ms * 1e-3) / 1e12, algorithmic_bytes=byts,
-                steps=reps * len(copies), graph_ms_per_step_events=graph_kernel_ms,
+                         f"{w['copies']} rotating weight copies",
+                mode=mode, ms_per_step=best, value=gbs, unit="GB/s", frac_of_hbm_peak=gbs / PEAK_HBM_GBS,
+                tflops=nonzero_flops(w) / (best * 1e-3) / 1e12, algorithmic_bytes=byts,
+                graph_ms_per_step=ms, graph_gbs=byts / (ms * 1e-3) / 1e9, graph_steps=reps * len(copies),
+                graph_ms_per_step_events=graph_kernel_ms,
                 eager_ms_per_step=eager_ms, eager_gbs=byts / (eager_ms * 1e-3) / 1e9,
                 eager_kernel_ms_avg=sum(per) / len(per))
 
