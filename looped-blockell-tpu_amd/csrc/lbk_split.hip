@@ -3,7 +3,8 @@
 // gu_kernel<B, MT, NORM, INTER>: a workgroup owns 16*MT tokens.  Their input
 // rows sit in LDS as an XOR-swizzled panel (optionally RMSNorm-ed on the way in
 // from an fp32 state), next to a table of the gate/up column indices.  Eight
-// waves (two per SIMD) each stream their own d_ff block rows (r = w, w+8, ...):
+// waves (two per SIMD; twelve with a shallower ring on the plain B = 32 path,
+// gu_kernel_w12) each stream their own d_ff block rows (r = w, w+8, ...):
 // gate and up tiles are consumed in (gate k, up k) pairs from a GU_RING-deep
 // register ring that runs across row boundaries.  The weight tile is the A
 // operand of the MFMA, so the accumulators hold h transposed and every lane
@@ -64,7 +65,7 @@ constexpr int GU_CT_MAX = 8;
 template <int MT>
 struct GUPanel { static constexpr int ROWB = 8192 / MT; };
 
-// gate/up of token block tb (16 * MT tokens) by one workgroup of 512 threads; smem holds the
+// gate/up of token block tb (16 * MT tokens) by one workgroup of 64 * NW threads; smem holds the
 // panel and the column table (gu_lds bytes).  Waves without rows return after the panel
 // barrier, so a caller that synchronises afterwards must do so after the call.
 // READY: the panel and the column table are already in LDS (the looped kernel's down phase
@@ -73,12 +74,17 @@ struct GUPanel { static constexpr int ROWB = 8192 / MT; };
 // has no bias code at all.
 // LIN: one plain product y = x W (+ a.bg) into a.h: the gate stream only (the caller passes
 // the gate's weights and columns for up too, with SHARED), no SiLU.
-template <int B, int MT, bool NORM, bool INTER, bool SHARED, bool READY = false, bool BIAS = false, bool LIN = false>
+// NW, RING: waves of the workgroup and ring depth (12 waves with a 2-deep ring for the plain
+// x-panel path, where three waves per SIMD fit the register budget).
+template <int B, int MT, bool NORM, bool INTER, bool SHARED, bool READY = false, bool BIAS = false, bool LIN = false,
+          int NW = 8, int RING = GU_RING>
 __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned char* smem, int tid) {
   constexpr int CW = TileShape<B>::CW;
   constexpr int TM = 16 * MT;
   constexpr int ROWB = GUPanel<MT>::ROWB;
   static_assert(TileShape<B>::NKS == 1, "gate/up kernel handles B <= 32");
+  constexpr int NT = 64 * NW;
+  static_assert(NW == 8 || (!NORM && !READY), "the normalising and looped paths run 8 waves");
   const int d_model = a.d_model;
   const int lane = tid & 63;
   const int w = uniform(tid >> 6);
@@ -98,7 +104,7 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
   auto ctab_fetch = [&]() {
 #pragma unroll
     for (int u = 0; u < GU_CT_MAX; ++u) {
-      const int e = tid + 512 * u;
+      const int e = tid + NT * u;
       const int ec = e < nct ? e : 0;
       ctv[u] = make_int2(a.cg[ec], a.cu[ec]);
     }
@@ -106,7 +112,7 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
   auto ctab_store = [&]() {
 #pragma unroll
     for (int u = 0; u < GU_CT_MAX; ++u) {
-      const int e = tid + 512 * u;
+      const int e = tid + NT * u;
       int cg = ctv[u].x, cu = ctv[u].y;
       cg = (cg >= 0 && cg < cin) ? cg : 0;
       cu = (cu >= 0 && cu < cin) ? cu : 0;
@@ -114,14 +120,14 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
     }
   };
 
-  // ---- stream this wave's rows r = w + 8n through a GU_RING-slot ring of
+  // ---- stream this wave's rows r = w + NW n through a RING-slot ring of
   // (gate, up) tile pairs.  Each row takes KP positions, K rounded up to a
-  // multiple of GU_RING (padding positions read the zero tile), so slot s of the
+  // multiple of RING (padding positions read the zero tile), so slot s of the
   // ring always holds position s of a group; every position issues the same
-  // loads, so the compiler's memory-counter waits stay exact and GU_RING - 1
+  // loads, so the compiler's memory-counter waits stay exact and RING - 1
   // positions stay in flight across row boundaries.
-  const int nrows = (a.R_ff - w + 7) / 8;   // may be <= 0: such a wave only helps fill the panel
-  const int KP = (K + GU_RING - 1) / GU_RING * GU_RING;
+  const int nrows = (a.R_ff - w + NW - 1) / NW;   // may be <= 0: such a wave only helps fill the panel
+  const int KP = (K + RING - 1) / RING * RING;
   const u32x4* pg = static_cast<const u32x4*>(a.pg);
   const u32x4* pu = static_cast<const u32x4*>(a.pu);
   const uint32_t lbase = (uint32_t)(i * MT * ROWB);   // this lane's first panel row
@@ -130,7 +136,7 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
   // weight loads of the next position (the column table is not needed yet)
   auto fetch_w = [&](GUSlot<B>& S) {
     const bool live = rn < nrows && rk < K;
-    const int64_t e = live ? (int64_t)(w + 8 * rn) * K + rk : ztile;
+    const int64_t e = live ? (int64_t)(w + NW * rn) * K + rk : ztile;
     load_pfrag<B>(pg + e * PackedTile<B>::U32X4, lane, S.g);
     if constexpr (!LIN) load_pfrag<B>(pu + e * PackedTile<B>::U32X4, lane, S.u);
     S.cg = live ? (int)e : -1;   // position index until fetch_c replaces it by columns
@@ -148,11 +154,11 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
     fetch_w(S);
     fetch_c(S);
   };
-  GUSlot<B> P[GU_RING];
+  GUSlot<B> P[RING];
   auto prefetch_ring = [&]() {
     int sn = 0, sk = 0;
 #pragma unroll
-    for (int sl = 0; sl < GU_RING; ++sl) {
+    for (int sl = 0; sl < RING; ++sl) {
       rn = sn;
       rk = sk;
       fetch_w(P[sl]);
@@ -203,14 +209,16 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
     if (nrows > 0) prefetch_ring();
   } else if constexpr (!NORM) {
     constexpr int CPR = ROWB / 16;                 // chunk capacity of a panel row
-    constexpr int PIT = TM * CPR / 512;            // chunks per thread
+    constexpr int NCH = TM * CPR;                  // chunks of the panel
+    constexpr int PIT = (NCH + NT - 1) / NT;       // chunks per thread
     const int cpr = d_model / 8;
     // every load at a clamped address (row t0, chunk 0 stand in for the padding), so no
     // load sits under a branch and the waits before the stores stay exact
     u32x4 pv[PIT];
 #pragma unroll
     for (int it = 0; it < PIT; ++it) {
-      const int e = tid + 512 * it;
+      const int e0 = tid + NT * it;
+      const int e = (NCH % NT == 0 || e0 < NCH) ? e0 : 0;
       const int row = e / CPR, cc = e % CPR;
       const int64_t t = t0 + row;
       const bool ok = cc < cpr && t < a.N;
@@ -221,10 +229,10 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
     ctab_store();
 #pragma unroll
     for (int it = 0; it < PIT; ++it) {
-      const int e = tid + 512 * it;
+      const int e = tid + NT * it;
       const int row = e / CPR, cc = e % CPR;
       const bool ok = cc < cpr && t0 + row < a.N;
-      if (cc < cpr) *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, cc, ROWB)) = ok ? pv[it] : u32x4{0, 0, 0, 0};
+      if ((NCH % NT == 0 || e < NCH) && cc < cpr) *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, cc, ROWB)) = ok ? pv[it] : u32x4{0, 0, 0, 0};
     }
   } else {
     // fp32 state rows -> RMSNorm -> bf16 panel; wave w owns rows w, w+8, ...;
@@ -290,12 +298,12 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
   __syncthreads();
   if (nrows <= 0) return;
 #pragma unroll
-  for (int sl = 0; sl < GU_RING; ++sl) fetch_c(P[sl]);
+  for (int sl = 0; sl < RING; ++sl) fetch_c(P[sl]);
 
   // The A fragments of position p + 1 are read from the panel while position p's MFMAs
-  // run (two register sets, alternating with the slot parity; GU_RING is even), so the
+  // run (two register sets, alternating with the slot parity; RING is even), so the
   // LDS latency stays off the MFMA chain.
-  static_assert(GU_RING % 2 == 0, "A-fragment double buffer alternates with the slot parity");
+  static_assert(RING % 2 == 0, "A-fragment double buffer alternates with the slot parity");
   AFrags A0, A1;
   load_a(P[0], A0);
   __builtin_amdgcn_sched_barrier(0);
@@ -309,14 +317,14 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
       }
     // the scheduling barriers keep each slot's use after the previous slot's
     // refill, so the wait before it covers only that slot's loads
-    for (int k = 0; k < KP; k += GU_RING) {
+    for (int k = 0; k < KP; k += RING) {
 #pragma unroll
-      for (int sl = 0; sl < GU_RING; ++sl) {
+      for (int sl = 0; sl < RING; ++sl) {
         if (sl % 2 == 0) {
-          load_a(P[(sl + 1) % GU_RING], A1);
+          load_a(P[(sl + 1) % RING], A1);
           compute(P[sl], A0);
         } else {
-          load_a(P[(sl + 1) % GU_RING], A0);
+          load_a(P[(sl + 1) % RING], A0);
           compute(P[sl], A1);
         }
         fetch(P[sl]);
@@ -325,7 +333,7 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
     }
     // epilogue of row r: h = silu(g) * u (and the pre-activations); each lane stores the
     // 4 * CW consecutive columns it holds of one token with one store
-    const int r = w + 8 * n;
+    const int r = w + NW * n;
     const int64_t col0 = (int64_t)r * B + 4 * CW * g;
     // biases of this lane's 4 * CW columns
     float bgv[4 * CW], buv[4 * CW];
@@ -367,6 +375,15 @@ template <int B, int MT, bool NORM, bool INTER, bool SHARED, bool BIAS>
 __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   gu_tile<B, MT, NORM, INTER, SHARED, false, BIAS>(a, (int64_t)blockIdx.x, smem, (int)threadIdx.x);
+}
+
+// the plain x-panel gate/up (no norm, no exported pre-activations, no biases) with 12 waves
+// and a 2-deep ring: 161 VGPRs fit three waves per SIMD, and the extra waves hide more of
+// the panel-read and weight-load latency than the shallower ring gives up
+template <int B, int MT, bool SHARED>
+__global__ __launch_bounds__(768, 1) void gu_kernel_w12(GUArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  gu_tile<B, MT, false, false, SHARED, false, false, false, 12, 2>(a, (int64_t)blockIdx.x, smem, (int)threadIdx.x);
 }
 
 // plain Block-ELL product y = x W (+ bias) over an LDS panel of x (the gate/up kernel's gate
@@ -874,6 +891,13 @@ int launch_gu(int B, bool norm, const GUArgs& a, hipStream_t st) {
   // gate and up passing the same column-index buffer share their topology (the reference
   // layer initialises both from the same seed)
   const bool shared = a.cg == a.cu;
+  if (B == 32 && mt == 4 && !norm && !inter && !shared && !a.bg && !a.bu) {
+    auto kern = gu_kernel_w12<32, 4, false>;
+    static std::atomic<uint64_t> configured{0};
+    if (set_lds_limit_once((const void*)kern, 163840, configured)) return -1;
+    hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 63) / 64)), dim3(768), gu_lds(a.R_ff, a.Kg, 4), st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+  }
 #define LBK_GU2(BB, MM, SH)                                                                          \
   if (norm) return launch_gu_t<BB, MM, true, false, SH>(a, st);                                     \
   return inter ? launch_gu_t<BB, MM, false, true, SH>(a, st) : launch_gu_t<BB, MM, false, false, SH>(a, st);
