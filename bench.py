@@ -201,7 +201,7 @@ def bench_bf16(steps, warmup, device):
                       frac=achieved / PEAK_BF16_TFLOPS, traffic=profiled_traffic(TRAFFIC_PROFILE_BF16),
                       traffic_source=os.path.relpath(TRAFFIC_PROFILE_BF16, ROOT) + " (2 x FETCH_SIZE + WRITE_SIZE "
                                      "of the two launches, the factors a copy of known size reads)",
-                      kernel="SwiGLU forward launch pair gu_kernel<32,4,false,false,false,false> + "
+                      kernel="SwiGLU forward launch pair gu_kernel_w12<32,4,false> + "
                              "dn_kernel<32,4,1,16,512,false>, timed together with HIP events around each step",
                       algorithmic_flops_per_launch=flops,
                       algorithmic_bytes_per_launch=algorithmic_bytes(w)),
