@@ -72,6 +72,7 @@ struct GUArgs {
   uint16_t* gpre;           // [N, d_ff] optional gate pre-activation
   uint16_t* uout;           // [N, d_ff] optional up output
   const float* bg; const float* bu;   // optional [d_ff] gate / up biases (added before SiLU*mul)
+  int H;                    // row slices per token block (set by the launcher)
 };
 struct DNArgs {
   const uint16_t* h;        // [N, d_ff]

@@ -65,8 +65,8 @@ constexpr int GU_CT_MAX = 8;
 template <int MT>
 struct GUPanel { static constexpr int ROWB = 8192 / MT; };
 
-// gate/up of token block tb (16 * MT tokens) by one workgroup of 64 * NW threads; smem holds the
-// panel and the column table (gu_lds bytes).  Waves without rows return after the panel
+// gate/up of token block tb (16 * MT tokens), h rows r_lo .. r_lo + nrs - 1, by one workgroup of
+// 64 * NW threads; smem holds the panel and the slice's column table (gu_lds bytes).  Waves without rows return after the panel
 // barrier, so a caller that synchronises afterwards must do so after the call.
 // READY: the panel and the column table are already in LDS (the looped kernel's down phase
 // wrote the next iteration's normalised rows; the table stays from the first iteration).
@@ -78,7 +78,8 @@ struct GUPanel { static constexpr int ROWB = 8192 / MT; };
 // x-panel path, where three waves per SIMD fit the register budget).
 template <int B, int MT, bool NORM, bool INTER, bool SHARED, bool READY = false, bool BIAS = false, bool LIN = false,
           int NW = 8, int RING = GU_RING>
-__device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned char* smem, int tid) {
+__device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, int nrs, unsigned char* smem,
+                                        int tid) {
   constexpr int CW = TileShape<B>::CW;
   constexpr int TM = 16 * MT;
   constexpr int ROWB = GUPanel<MT>::ROWB;
@@ -94,18 +95,19 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
   const int64_t d_ff = (int64_t)a.R_ff * B;
   const int K = a.Kg;                        // == a.Ku >= 1
   const int64_t ztile = (int64_t)a.R_ff * K; // index of the packed zero tile
-  // column table after the panel: (gate col, up col) per (row, slot); dead -> 0
+  // column table after the panel: (gate col, up col) per (row of the slice, slot); dead -> 0
   int2* ctab = reinterpret_cast<int2*>(smem + (size_t)TM * ROWB);
 
   // ---- column table (at most GU_CT_MAX entries per thread): loads at clamped addresses,
   // all issued with the panel loads, stored after them
-  const int nct = a.R_ff * K;
+  const int nct = nrs * K;
+  const int64_t cbase = (int64_t)r_lo * K;
   int2 ctv[GU_CT_MAX];
   auto ctab_fetch = [&]() {
 #pragma unroll
     for (int u = 0; u < GU_CT_MAX; ++u) {
       const int e = tid + NT * u;
-      const int ec = e < nct ? e : 0;
+      const int64_t ec = cbase + (e < nct ? e : 0);
       ctv[u] = make_int2(a.cg[ec], a.cu[ec]);
     }
   };
@@ -120,13 +122,13 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
     }
   };
 
-  // ---- stream this wave's rows r = w + NW n through a RING-slot ring of
+  // ---- stream this wave's rows r = r_lo + w + NW n through a RING-slot ring of
   // (gate, up) tile pairs.  Each row takes KP positions, K rounded up to a
   // multiple of RING (padding positions read the zero tile), so slot s of the
   // ring always holds position s of a group; every position issues the same
   // loads, so the compiler's memory-counter waits stay exact and RING - 1
   // positions stay in flight across row boundaries.
-  const int nrows = (a.R_ff - w + NW - 1) / NW;   // may be <= 0: such a wave only helps fill the panel
+  const int nrows = (nrs - w + NW - 1) / NW;   // may be <= 0: such a wave only helps fill the panel
   const int KP = (K + RING - 1) / RING * RING;
   const u32x4* pg = static_cast<const u32x4*>(a.pg);
   const u32x4* pu = static_cast<const u32x4*>(a.pu);
@@ -136,10 +138,11 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
   // weight loads of the next position (the column table is not needed yet)
   auto fetch_w = [&](GUSlot<B>& S) {
     const bool live = rn < nrows && rk < K;
-    const int64_t e = live ? (int64_t)(w + NW * rn) * K + rk : ztile;
+    const int el = (w + NW * rn) * K + rk;   // entry of the slice's column table
+    const int64_t e = live ? cbase + el : ztile;
     load_pfrag<B>(pg + e * PackedTile<B>::U32X4, lane, S.g);
     if constexpr (!LIN) load_pfrag<B>(pu + e * PackedTile<B>::U32X4, lane, S.u);
-    S.cg = live ? (int)e : -1;   // position index until fetch_c replaces it by columns
+    S.cg = live ? el : -1;   // table entry until fetch_c replaces it by columns
   };
   auto fetch_c = [&](GUSlot<B>& S) {
     const int2 c = ctab[S.cg >= 0 ? S.cg : 0];
@@ -333,7 +336,7 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
     }
     // epilogue of row r: h = silu(g) * u (and the pre-activations); each lane stores the
     // 4 * CW consecutive columns it holds of one token with one store
-    const int r = w + NW * n;
+    const int r = r_lo + w + NW * n;
     const int64_t col0 = (int64_t)r * B + 4 * CW * g;
     // biases of this lane's 4 * CW columns
     float bgv[4 * CW], buv[4 * CW];
@@ -371,10 +374,24 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, unsigned ch
   }
 }
 
+// workgroup b -> (token block b / H, row slice b % H); the slices' rows split R_ff evenly, and
+// with H a multiple of 8 every workgroup of one slice runs on the same XCD (workgroups are dealt
+// to the 8 XCDs round robin), so each XCD's L2 holds the weights of its slices only
+__device__ __forceinline__ void gu_slice(const GUArgs& a, int64_t& tb, int& r_lo, int& nrs) {
+  const int64_t b = blockIdx.x;
+  const int H = a.H, hs = (int)(b % H);
+  tb = b / H;
+  r_lo = (int)((int64_t)hs * a.R_ff / H);
+  nrs = (int)((int64_t)(hs + 1) * a.R_ff / H) - r_lo;
+}
+
 template <int B, int MT, bool NORM, bool INTER, bool SHARED, bool BIAS>
 __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  gu_tile<B, MT, NORM, INTER, SHARED, false, BIAS>(a, (int64_t)blockIdx.x, smem, (int)threadIdx.x);
+  int64_t tb;
+  int r_lo, nrs;
+  gu_slice(a, tb, r_lo, nrs);
+  gu_tile<B, MT, NORM, INTER, SHARED, false, BIAS>(a, tb, r_lo, nrs, smem, (int)threadIdx.x);
 }
 
 // the plain x-panel gate/up (no norm, no exported pre-activations, no biases) with 12 waves
@@ -383,7 +400,8 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
 template <int B, int MT, bool SHARED>
 __global__ __launch_bounds__(768, 1) void gu_kernel_w12(GUArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  gu_tile<B, MT, false, false, SHARED, false, false, false, 12, 2>(a, (int64_t)blockIdx.x, smem, (int)threadIdx.x);
+  gu_tile<B, MT, false, false, SHARED, false, false, false, 12, 2>(a, (int64_t)blockIdx.x, 0, a.R_ff, smem,
+                                                                   (int)threadIdx.x);
 }
 
 // plain Block-ELL product y = x W (+ bias) over an LDS panel of x (the gate/up kernel's gate
@@ -391,7 +409,10 @@ __global__ __launch_bounds__(768, 1) void gu_kernel_w12(GUArgs a) {
 template <int B, int MT, bool BIAS>
 __global__ __launch_bounds__(512, 1) void lin_kernel(GUArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  gu_tile<B, MT, false, false, true, false, BIAS, true>(a, (int64_t)blockIdx.x, smem, (int)threadIdx.x);
+  int64_t tb;
+  int r_lo, nrs;
+  gu_slice(a, tb, r_lo, nrs);
+  gu_tile<B, MT, false, false, true, false, BIAS, true>(a, tb, r_lo, nrs, smem, (int)threadIdx.x);
 }
 
 // ===========================================================================
@@ -813,8 +834,8 @@ __global__ __launch_bounds__(512, 1) void looped_kernel(LoopArgs la) {
     int tg = tid;
     int64_t tbg = tb;
     asm volatile("" : "+v"(tg), "+s"(tbg));
-    if (fuse && l > 0) gu_tile<B, MT, true, false, SHARED, true, BIAS>(la.gu, tbg, smem, tg);
-    else gu_tile<B, MT, true, false, SHARED, false, BIAS>(la.gu, tbg, smem, tg);
+    if (fuse && l > 0) gu_tile<B, MT, true, false, SHARED, true, BIAS>(la.gu, tbg, 0, la.gu.R_ff, smem, tg);
+    else gu_tile<B, MT, true, false, SHARED, false, BIAS>(la.gu, tbg, 0, la.gu.R_ff, smem, tg);
     __syncthreads();
     uint16_t* out = l == la.L - 1 ? la.dn.out : nullptr;
     for (int rg = 0; rg < nrg; ++rg) {
@@ -854,6 +875,18 @@ static size_t gu_lds(int R_ff, int K, int mt) {
   return (size_t)16 * mt * (8192 / mt) + (size_t)R_ff * K * 8;   // panel (128 KB) + column table
 }
 
+// Row slices per token block for the gate/up kernels: with fewer token blocks than CUs, each
+// block's h rows are split so that about 256 workgroups run (a workgroup streams the weights of
+// its rows only), keeping at least 8 rows (one per wave) per slice; above 4 slices the count is
+// a multiple of 8, so that one slice's workgroups share an XCD.
+static int gu_slices(int64_t ntb, int R_ff) {
+  if (ntb >= 256) return 1;
+  const int hmax = R_ff / 8 > 1 ? R_ff / 8 : 1;
+  int H = (int)((256 + ntb - 1) / ntb);
+  if (H > 4) H = (H + 7) / 8 * 8;
+  return H < hmax ? H : hmax;
+}
+
 bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd) {
   if (B != 16 && B != 32) return false;
   if (Kg != Ku || Kg < 1) return false;               // gate and up stream in lockstep
@@ -873,7 +906,7 @@ static int launch_gu_b(const GUArgs& a, hipStream_t st) {
   if (set_lds_limit_once((const void*)kern, 163840, configured)) return -1;
   const int TM = 16 * MT;
   const size_t lds = gu_lds(a.R_ff, a.Kg, MT);
-  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + TM - 1) / TM)), dim3(512), lds, st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + TM - 1) / TM * a.H)), dim3(512), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -884,14 +917,17 @@ static int launch_gu_t(const GUArgs& a, hipStream_t st) {
                         : launch_gu_b<B, MT, NORM, INTER, SHARED, false>(a, st);
 }
 
-int launch_gu(int B, bool norm, const GUArgs& a, hipStream_t st) {
-  if (a.N == 0) return 0;
-  const int mt = gu_mt(a.d_model);
+int launch_gu(int B, bool norm, const GUArgs& a0, hipStream_t st) {
+  if (a0.N == 0) return 0;
+  const int mt = gu_mt(a0.d_model);
+  if (mt == 0) return -2;
+  GUArgs a = a0;
+  a.H = gu_slices((a.N + 16 * mt - 1) / (16 * mt), a.R_ff);
   const bool inter = a.gpre || a.uout;
   // gate and up passing the same column-index buffer share their topology (the reference
   // layer initialises both from the same seed)
   const bool shared = a.cg == a.cu;
-  if (B == 32 && mt == 4 && !norm && !inter && !shared && !a.bg && !a.bu) {
+  if (B == 32 && mt == 4 && a.H == 1 && !norm && !inter && !shared && !a.bg && !a.bu) {
     auto kern = gu_kernel_w12<32, 4, false>;
     static std::atomic<uint64_t> configured{0};
     if (set_lds_limit_once((const void*)kern, 163840, configured)) return -1;
@@ -919,7 +955,7 @@ static int launch_lin_t(const GUArgs& a, hipStream_t st) {
   if (set_lds_limit_once((const void*)kern, 163840, configured)) return -1;
   const int TM = 16 * MT;
   const size_t lds = gu_lds(a.R_ff, a.Kg, MT);
-  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + TM - 1) / TM)), dim3(512), lds, st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + TM - 1) / TM * a.H)), dim3(512), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -938,6 +974,8 @@ int launch_lin(int B, const GUArgs& a0, hipStream_t st) {
   a.cu = a.cg;
   a.Ku = a.Kg;
   const int mt = gu_mt(a.d_model);
+  if (mt == 0) return -2;
+  a.H = gu_slices((a.N + 16 * mt - 1) / (16 * mt), a.R_ff);
 #define LBK_LIN(BB, MM)                                                                     \
   if (B == BB && mt == MM) return a.bg ? launch_lin_t<BB, MM, true>(a, st) : launch_lin_t<BB, MM, false>(a, st);
   LBK_LIN(16, 4) LBK_LIN(16, 2) LBK_LIN(32, 4) LBK_LIN(32, 2)
@@ -968,6 +1006,12 @@ static int launch_dn_t(const DNArgs& a0, hipStream_t st) {
 // row, against 144 us; the smaller stages add padding and per-stage imbalance.)
 int launch_dn(int B, const DNArgs& a, hipStream_t st) {
   if (a.N == 0) return 0;
+  // Fewer token blocks than the 16-row groups need to fill the CUs: 4-wave workgroups of four
+  // rows with 256-column stages (four times the workgroups, each with a quarter of the weights)
+  if ((a.N + 63) / 64 * ((a.R_m + 15) / 16) < 256) {
+    if (B == 16) return launch_dn_t<16, 4, 1, 4, 256>(a, st);
+    if (B == 32) return launch_dn_t<32, 4, 1, 4, 256>(a, st);
+  }
   if (B == 16) return launch_dn_t<16, 4, 1, DN_WAVES, DN_STAGE_COLS>(a, st);
   if (B == 32) return launch_dn_t<32, 4, 1, DN_WAVES, DN_STAGE_COLS>(a, st);
   return -2;

@@ -100,6 +100,7 @@ SWIGLU_CASES = [
     (256, 1024, 16, 0.25, 77, 0.1),       # ragged N, dead slots
     (512, 1024, 32, 0.25, 130, 0.0),
     (512, 256, 32, 0.5, 90, 0.1),         # 8 h rows: fewer than the 12 gate/up waves
+    (256, 1408, 32, 0.25, 100, 0.05),     # 44 h rows in 5 uneven row slices (few token blocks)
     (1024, 4096, 32, 0.25, 200, 0.05),    # the headline geometry, small N
     (128, 512, 64, 0.5, 70, 0.0),         # B = 64 -> general two-kernel path
     (2048, 1024, 32, 0.125, 40, 0.0),     # d_model > 1024: 32-token gate/up panels, 64 down rows
