@@ -522,6 +522,7 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
   constexpr int PER_T = (CHUNKS + NT - 1) / NT;      // chunks per thread per stage
   static_assert(TileShape<B>::NKS == 1, "down kernel handles B <= 32");
   static_assert(SROWB % 256 == 0, "stage rows must cover multiples of 16 chunks");
+  static_assert(G <= 64, "a list entry holds the column block of its stage in 6 bits");
 
   const int lane = tid & 63;
   const int w = uniform(tid >> 6);
@@ -1006,11 +1007,19 @@ static int launch_dn_t(const DNArgs& a0, hipStream_t st) {
 // row, against 144 us; the smaller stages add padding and per-stage imbalance.)
 int launch_dn(int B, const DNArgs& a, hipStream_t st) {
   if (a.N == 0) return 0;
-  // Fewer token blocks than the 16-row groups need to fill the CUs: 4-wave workgroups of four
-  // rows with 256-column stages (four times the workgroups, each with a quarter of the weights)
+  // Fewer 64-token blocks than the 16-row groups need to fill the CUs: smaller workgroups with
+  // longer stages, so that more of them run and each walks fewer stages -- 16 tokens and 4 rows
+  // per workgroup with 2048-column stages (1024 for B = 16) while they number at most 128, else
+  // 32 tokens and 8 rows with 1024-column stages.  Measured at d_model 1024, d_ff 4096, B = 32
+  // (forward per N = 64 / 256 / 1024 / 2048 / 4096): 20.0 / 21.0 / 28.6 / 37.3 / 62.3 us, against
+  // 38.4 / 40.3 / 44.4 / 50.9 / 61.9 with 64 tokens and 4 rows at 256-column stages.
   if ((a.N + 63) / 64 * ((a.R_m + 15) / 16) < 256) {
-    if (B == 16) return launch_dn_t<16, 4, 1, 4, 256>(a, st);
-    if (B == 32) return launch_dn_t<32, 4, 1, 4, 256>(a, st);
+    if ((a.N + 15) / 16 * ((a.R_m + 3) / 4) <= 128) {
+      if (B == 16) return launch_dn_t<16, 1, 1, 4, 1024>(a, st);
+      if (B == 32) return launch_dn_t<32, 1, 1, 4, 2048>(a, st);
+    }
+    if (B == 16) return launch_dn_t<16, 2, 1, 8, 1024>(a, st);
+    if (B == 32) return launch_dn_t<32, 2, 1, 8, 1024>(a, st);
   }
   if (B == 16) return launch_dn_t<16, 4, 1, DN_WAVES, DN_STAGE_COLS>(a, st);
   if (B == 32) return launch_dn_t<32, 4, 1, DN_WAVES, DN_STAGE_COLS>(a, st);
