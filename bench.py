@@ -194,6 +194,15 @@ def bench_bf16(steps, warmup, device):
         out["y2"] = kernels.swiglu_fwd(x, *args, add_residual=False)
 
     ms_p, per_p = time_steps(step_pack, steps, warmup)
+
+    # the same forward on fewer tokens (the first N rows of x): fewer token blocks than CUs, so
+    # the gate/up rows are split over workgroups and the down kernel takes smaller workgroups
+    by_tokens = {}
+    for n in (64, 1024, 4096):
+        xs = x[:n].contiguous()
+        ms_n, _ = time_steps(lambda i: kernels.swiglu_fwd_prepacked(xs, packed, *args, add_residual=False),
+                             steps, warmup)
+        by_tokens[str(n)] = dict(ms_per_step=ms_n, value=nonzero_flops(dict(w, N=n)) / (ms_n * 1e-3) / 1e12)
     res = dict(
         ms_per_step=ms, value=flops / (ms * 1e-3) / 1e12, tokens_per_s=w["N"] / (ms * 1e-3),
         kernel_ms_avg=kern_ms, kernel_ms_median=median(per),
@@ -205,6 +214,8 @@ def bench_bf16(steps, warmup, device):
                              "dn_kernel<32,4,1,16,512,false>, timed together with HIP events around each step",
                       algorithmic_flops_per_launch=flops,
                       algorithmic_bytes_per_launch=algorithmic_bytes(w)),
+        fewer_tokens=dict(workload="the same forward (weights packed once) on the first N tokens", unit="TFLOP/s",
+                          by_tokens=by_tokens),
         with_pack=dict(workload="the same forward packing the weights on every call (titan::block_ell_swiglu_fwd: "
                                 "pack_bf16_multi_kernel + gu_kernel + dn_kernel)",
                        ms_per_step=ms_p, value=flops / (ms_p * 1e-3) / 1e12, unit="TFLOP/s",
@@ -438,7 +449,7 @@ def bench_looped(steps, warmup, device):
     scale = torch.ones(w["d_model"], device=device)
 
     def step(i):
-        kernels.looped_swiglu(h, scale, *g, *u, *d, L=w["L"], eps=1e-5)
+        kernels.looped_swiglu_persistent(h, scale, *g, *u, *d, L=w["L"], eps=1e-5)
 
     ms, per = time_steps(step, steps, warmup)
     flops = nonzero_flops(w)
@@ -449,6 +460,17 @@ def bench_looped(steps, warmup, device):
 
     ms_l, per_l = time_steps(step_l, steps, warmup)
     tf_l = flops / (ms_l * 1e-3) / 1e12
+
+    # fewer tokens: the persistent launch has one workgroup per 64 tokens, the per-iteration
+    # kernels split the weight rows over many
+    small = {}
+    for n in (64, 1024, 4096):
+        hs = h[:n].contiguous()
+        ms_p, _ = time_steps(lambda i: kernels.looped_swiglu_persistent(hs, scale, *g, *u, *d, L=w["L"], eps=1e-5),
+                             steps, warmup)
+        ms_s, _ = time_steps(lambda i: kernels.looped_swiglu_launches(hs, scale, *g, *u, *d, L=w["L"], eps=1e-5),
+                             steps, warmup)
+        small[str(n)] = dict(persistent_ms=ms_p, launches_ms=ms_s)
     return dict(workload="looped RMSNorm -> SwiGLU -> residual, L=8 shared weights, d_model=1024 d_ff=4096 B=32 "
                          "density=0.25 N=32x512 (weight packing + one persistent launch: a workgroup owns a "
                          "64-token block for all L iterations)",
@@ -456,9 +478,11 @@ def bench_looped(steps, warmup, device):
                 token_iterations_per_s=w["N"] * w["L"] / (ms * 1e-3), frac_of_bf16_peak=tf / PEAK_BF16_TFLOPS,
                 kernel_ms_avg=sum(per) / len(per),
                 launches=dict(workload="the same looped block as weight packing + an fp32 copy + 2L launches "
-                                       "(gate/up and down per iteration)",
+                                       "(gate/up and down per iteration; the default of titan::looped_swiglu)",
                               ms_per_step=ms_l, value=tf_l, unit="TFLOP/s", frac_of_bf16_peak=tf_l / PEAK_BF16_TFLOPS,
-                              kernel_ms_avg=sum(per_l) / len(per_l)))
+                              kernel_ms_avg=sum(per_l) / len(per_l)),
+                fewer_tokens=dict(workload="the same looped block (L=8) on the first N tokens, ms per call",
+                                  by_tokens=small))
 
 
 def bench_decode(steps, warmup, device):
@@ -662,7 +686,8 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    empty = dict(value=None, ms_per_step=None, tokens_per_s=None, kernel_ms_avg=None, roofline=None, with_pack=None)
+    empty = dict(value=None, ms_per_step=None, tokens_per_s=None, kernel_ms_avg=None, roofline=None, with_pack=None,
+                 fewer_tokens=None)
     main_res = empty if args.skip_main else bench_bf16(args.steps, args.warmup, device)
     extra = {}
     if not args.only_main:
@@ -708,6 +733,7 @@ def main():
         "kernel_ms_avg": main_res["kernel_ms_avg"],
         "roofline": main_res["roofline"],
         "with_pack": main_res["with_pack"],
+        "fewer_tokens": main_res.get("fewer_tokens"),
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -215,8 +215,9 @@ def swiglu_fwd_prepacked(x, packed, v_gate, ci_gate, v_up, ci_up, v_down, ci_dow
 
 
 def looped_swiglu(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L: int, eps: float = 1e-5):
-    """L applications of h <- h + SwiGLU(RMSNorm(h)) with shared weights, in one operator call (one
-    persistent launch where the shape allows, per-iteration launches otherwise)."""
+    """L applications of h <- h + SwiGLU(RMSNorm(h)) with shared weights, in one operator call (the
+    per-iteration launches, faster than the persistent launch of ``looped_swiglu_persistent`` at
+    every token count measured)."""
     _gpu(h, v_gate, v_down)
     return ops().looped_swiglu(h, norm_scale, v_gate, ci_gate, v_up, ci_up, v_down, ci_down, L, eps)
 

@@ -377,7 +377,7 @@ def test_looped_persistent_matches_two_kernel_path(gpu, case):
     ht, st = T.to_gpu_bf16(h), T.to_gpu(scale)
     two = T.to_np(T.abi_looped(ht, st, *ws, L, 1e-5, launches=True))
     one = T.to_np(T.abi_looped(ht, st, *ws, L, 1e-5, persistent=True))
-    assert np.array_equal(one, T.to_np(T.abi_looped(ht, st, *ws, L, 1e-5)))   # the default path
+    assert np.array_equal(two, T.to_np(T.abi_looped(ht, st, *ws, L, 1e-5)))   # the default path
     if L == 1 or d_model // B > 32:
         assert np.array_equal(one, two)
     else:
