@@ -49,6 +49,7 @@ def profiled_traffic(path):
         pass
     return None
 WARMUP_S = 0.3
+FEWER_TOKENS = [64, 1024, 4096]   # token counts of the headline and looped workloads' fewer-token runs
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_INT8_TOPS = 5000.0       # MI355X dense int8 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
@@ -198,7 +199,7 @@ def bench_bf16(steps, warmup, device):
     # the same forward on fewer tokens (the first N rows of x): fewer token blocks than CUs, so
     # the gate/up rows are split over workgroups and the down kernel takes smaller workgroups
     by_tokens = {}
-    for n in (64, 1024, 4096):
+    for n in FEWER_TOKENS:
         xs = x[:n].contiguous()
         ms_n, _ = time_steps(lambda i: kernels.swiglu_fwd_prepacked(xs, packed, *args, add_residual=False),
                              steps, warmup)
@@ -464,7 +465,7 @@ def bench_looped(steps, warmup, device):
     # fewer tokens: the persistent launch has one workgroup per 64 tokens, the per-iteration
     # kernels split the weight rows over many
     small = {}
-    for n in (64, 1024, 4096):
+    for n in FEWER_TOKENS:
         hs = h[:n].contiguous()
         ms_p, _ = time_steps(lambda i: kernels.looped_swiglu_persistent(hs, scale, *g, *u, *d, L=w["L"], eps=1e-5),
                              steps, warmup)
@@ -665,9 +666,13 @@ def main():
     ap.add_argument("--only", default="",
                     help="comma list of extra workloads to run: shared,backward,matmul,matmul_backward,ternary,"
                          "looped,decode,topology,formats")
+    ap.add_argument("--no-fewer-tokens", action="store_true",
+                    help="skip the fewer-token runs of the headline and looped workloads (profiling: the kernel "
+                         "statistics then hold the named workload's launches only)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one 256 MiB device-to-device copy (a reference point for HBM byte counters)")
     args = ap.parse_args()
+    FEWER_TOKENS[:] = [] if args.no_fewer_tokens else FEWER_TOKENS
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the Block-ELL FFN path is single-GPU; "
               "no multi-GPU figure is produced). Run with --gpus 1.", file=sys.stderr)

@@ -3,8 +3,9 @@
 // gu_kernel<B, MT, NORM, INTER>: a workgroup owns 16*MT tokens.  Their input
 // rows sit in LDS as an XOR-swizzled panel (optionally RMSNorm-ed on the way in
 // from an fp32 state), next to a table of the gate/up column indices.  Eight
-// waves (two per SIMD; twelve with a shallower ring on the plain B = 32 path,
-// gu_kernel_w12) each stream their own d_ff block rows (r = w, w+8, ...):
+// waves (two per SIMD; twelve with a shallower ring, gu_kernel_w12, at B = 32 with distinct
+// gate/up topologies, no exports and no biases) each stream their own d_ff block rows (r = w,
+// w+8, ...):
 // gate and up tiles are consumed in (gate k, up k) pairs from a GU_RING-deep
 // register ring that runs across row boundaries.  The weight tile is the A
 // operand of the MFMA, so the accumulators hold h transposed and every lane
@@ -85,7 +86,7 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
   constexpr int ROWB = GUPanel<MT>::ROWB;
   static_assert(TileShape<B>::NKS == 1, "gate/up kernel handles B <= 32");
   constexpr int NT = 64 * NW;
-  static_assert(NW == 8 || (!NORM && !READY), "the normalising and looped paths run 8 waves");
+  static_assert(NW == 8 || !READY, "the looped kernel's gate/up phase runs 8 waves");
   const int d_model = a.d_model;
   const int lane = tid & 63;
   const int w = uniform(tid >> 6);
@@ -238,63 +239,89 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
       if ((NCH % NT == 0 || e < NCH) && cc < cpr) *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, cc, ROWB)) = ok ? pv[it] : u32x4{0, 0, 0, 0};
     }
   } else {
-    // fp32 state rows -> RMSNorm -> bf16 panel; wave w owns rows w, w+8, ...;
+    // fp32 state rows -> RMSNorm -> bf16 panel; wave w owns rows w, w+NW, ...;
     // lane holds 8 contiguous values per 512-column step of each row
-    constexpr int RW = TM / 8;                     // rows per wave
+    constexpr int RW = (TM + NW - 1) / NW;         // rows per wave
     constexpr int SPR = ROWB / 1024;               // 512-column steps of the widest row
-    f32x4 xv[RW][SPR][2];
+    // rows in registers at once: all of a wave's rows with 8 waves (their loads go out with the
+    // other prologue loads), two at a time with more waves (a smaller register budget)
+    constexpr int RB = NW == 8 ? RW : 2;
+    f32x4 xv[RB][SPR][2];
+    auto load_rows = [&](int rr0) {
 #pragma unroll
-    for (int rr = 0; rr < RW; ++rr) {
-      const int64_t t = t0 + w + 8 * rr;
+      for (int b = 0; b < RB; ++b) {
+        const int row = w + NW * (rr0 + b);
+        const bool rok = (TM % NW == 0 || row < TM) && rr0 + b < RW;
+        const int64_t t = t0 + row;
 #pragma unroll
-      for (int j = 0; j < SPR; ++j) {
-        const int col = 8 * lane + 512 * j;
-        // clamped address (row t0, column 0) for padding, zeroed after the load
-        const bool ok = col < d_model && t < a.N;
-        const float* src = a.xf + (ok ? t : t0) * d_model + (ok ? col : 0);
-        const f32x4 v0 = *reinterpret_cast<const f32x4*>(src);
-        const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + 4);
-        xv[rr][j][0] = ok ? v0 : f32x4{0.f, 0.f, 0.f, 0.f};
-        xv[rr][j][1] = ok ? v1 : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < SPR; ++j) {
+          const int col = 8 * lane + 512 * j;
+          // clamped address (row t0, column 0) for padding, zeroed after the load
+          const bool ok = rok && col < d_model && t < a.N;
+          const float* src = a.xf + (ok ? t : t0) * d_model + (ok ? col : 0);
+          const f32x4 v0 = *reinterpret_cast<const f32x4*>(src);
+          const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + 4);
+          xv[b][j][0] = ok ? v0 : f32x4{0.f, 0.f, 0.f, 0.f};
+          xv[b][j][1] = ok ? v1 : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
       }
-    }
+    };
     // the norm scale of this lane's columns, loaded once for all rows
     f32x4 sc[SPR][2];
-#pragma unroll
-    for (int j = 0; j < SPR; ++j) {
-      const int col = 8 * lane + 512 * j;
-      const float* src = a.norm_scale + (col < d_model ? col : 0);
-      sc[j][0] = *reinterpret_cast<const f32x4*>(src);
-      sc[j][1] = *reinterpret_cast<const f32x4*>(src + 4);
-    }
-    ctab_fetch();
-    if (nrows > 0) prefetch_ring();
-    ctab_store();
-#pragma unroll
-    for (int rr = 0; rr < RW; ++rr) {
-      const int row = w + 8 * rr;
-      float ss = 0.f;
-#pragma unroll
-      for (int j = 0; j < SPR; ++j)
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) ss += xv[rr][j][h2][q] * xv[rr][j][h2][q];
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-      const float rs = 1.0f / sqrtf(ss / (float)d_model + a.eps);
+    auto load_scale = [&]() {
 #pragma unroll
       for (int j = 0; j < SPR; ++j) {
         const int col = 8 * lane + 512 * j;
-        // col < ROWB / 2 always: the padding columns of the panel row get zeros (no branch)
-        const f32x4 s0 = sc[j][0], s1 = sc[j][1];
-        const f32x4 v0 = xv[rr][j][0], v1 = xv[rr][j][1];
-        const u32x4 o = {pack2_bf16(v0[0] * rs * s0[0], v0[1] * rs * s0[1]),
-                         pack2_bf16(v0[2] * rs * s0[2], v0[3] * rs * s0[3]),
-                         pack2_bf16(v1[0] * rs * s1[0], v1[1] * rs * s1[1]),
-                         pack2_bf16(v1[2] * rs * s1[2], v1[3] * rs * s1[3])};
-        *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, col / 8, ROWB)) =
-            col < d_model ? o : u32x4{0, 0, 0, 0};
+        const float* src = a.norm_scale + (col < d_model ? col : 0);
+        sc[j][0] = *reinterpret_cast<const f32x4*>(src);
+        sc[j][1] = *reinterpret_cast<const f32x4*>(src + 4);
+      }
+    };
+    auto norm_rows = [&](int rr0) {
+#pragma unroll
+      for (int b = 0; b < RB; ++b) {
+        const int row = w + NW * (rr0 + b);
+        if (rr0 + b >= RW || (TM % NW != 0 && row >= TM)) break;
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < SPR; ++j)
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ss += xv[b][j][h2][q] * xv[b][j][h2][q];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        const float rs = 1.0f / sqrtf(ss / (float)d_model + a.eps);
+#pragma unroll
+        for (int j = 0; j < SPR; ++j) {
+          const int col = 8 * lane + 512 * j;
+          // col < ROWB / 2 always: the padding columns of the panel row get zeros (no branch)
+          const f32x4 s0 = sc[j][0], s1 = sc[j][1];
+          const f32x4 v0 = xv[b][j][0], v1 = xv[b][j][1];
+          const u32x4 o = {pack2_bf16(v0[0] * rs * s0[0], v0[1] * rs * s0[1]),
+                           pack2_bf16(v0[2] * rs * s0[2], v0[3] * rs * s0[3]),
+                           pack2_bf16(v1[0] * rs * s1[0], v1[1] * rs * s1[1]),
+                           pack2_bf16(v1[2] * rs * s1[2], v1[3] * rs * s1[3])};
+          *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, col / 8, ROWB)) =
+              col < d_model ? o : u32x4{0, 0, 0, 0};
+        }
+      }
+    };
+    if constexpr (RB == RW) {
+      load_rows(0);
+      load_scale();
+      ctab_fetch();
+      if (nrows > 0) prefetch_ring();
+      ctab_store();
+      norm_rows(0);
+    } else {
+      load_scale();
+      ctab_fetch();
+      if (nrows > 0) prefetch_ring();
+      ctab_store();
+      for (int rr0 = 0; rr0 < RW; rr0 += RB) {
+        load_rows(rr0);
+        norm_rows(rr0);
       }
     }
   }
@@ -394,14 +421,15 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
   gu_tile<B, MT, NORM, INTER, SHARED, false, BIAS>(a, tb, r_lo, nrs, smem, (int)threadIdx.x);
 }
 
-// the plain x-panel gate/up (no norm, no exported pre-activations, no biases) with 12 waves
-// and a 2-deep ring: 161 VGPRs fit three waves per SIMD, and the extra waves hide more of
-// the panel-read and weight-load latency than the shallower ring gives up
-template <int B, int MT, bool SHARED>
+// gate/up with distinct gate/up topologies, without exported pre-activations or biases, one row
+// slice, with 12 waves and a 2-deep
+// ring: at most 168 VGPRs fit three waves per SIMD, and the extra waves hide more of the
+// panel-read and weight-load latency than the shallower ring gives up
+template <int B, int MT, bool NORM>
 __global__ __launch_bounds__(768, 1) void gu_kernel_w12(GUArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  gu_tile<B, MT, false, false, SHARED, false, false, false, 12, 2>(a, (int64_t)blockIdx.x, 0, a.R_ff, smem,
-                                                                   (int)threadIdx.x);
+  gu_tile<B, MT, NORM, false, false, false, false, false, 12, 2>(a, (int64_t)blockIdx.x, 0, a.R_ff, smem,
+                                                                 (int)threadIdx.x);
 }
 
 // plain Block-ELL product y = x W (+ bias) over an LDS panel of x (the gate/up kernel's gate
@@ -911,6 +939,15 @@ static int launch_gu_b(const GUArgs& a, hipStream_t st) {
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+template <int B, int MT, bool NORM>
+static int launch_gu_w12(const GUArgs& a, hipStream_t st) {
+  auto kern = gu_kernel_w12<B, MT, NORM>;
+  static std::atomic<uint64_t> configured{0};
+  if (set_lds_limit_once((const void*)kern, 163840, configured)) return -1;
+  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 16 * MT - 1) / (16 * MT))), dim3(768), gu_lds(a.R_ff, a.Kg, MT), st, a);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // the bias-free kernels carry no bias code (a bias is an epilogue add and two loads per column)
 template <int B, int MT, bool NORM, bool INTER, bool SHARED>
 static int launch_gu_t(const GUArgs& a, hipStream_t st) {
@@ -928,13 +965,12 @@ int launch_gu(int B, bool norm, const GUArgs& a0, hipStream_t st) {
   // gate and up passing the same column-index buffer share their topology (the reference
   // layer initialises both from the same seed)
   const bool shared = a.cg == a.cu;
-  if (B == 32 && mt == 4 && a.H == 1 && !norm && !inter && !shared && !a.bg && !a.bu) {
-    auto kern = gu_kernel_w12<32, 4, false>;
-    static std::atomic<uint64_t> configured{0};
-    if (set_lds_limit_once((const void*)kern, 163840, configured)) return -1;
-    hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 63) / 64)), dim3(768), gu_lds(a.R_ff, a.Kg, 4), st, a);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
-  }
+  // 12 waves for distinct gate/up topologies at B = 32 with one row slice, no exports and no
+  // biases (interleaved runs: headline forward 0.1455 -> 0.1434 ms, looped launches at L = 8
+  // 1.305 -> 1.283 ms with the normalising kernel; with a shared topology 8 waves measured as
+  // fast or faster, 0.1378 against 0.1381-0.1429 ms)
+  if (B == 32 && mt == 4 && a.H == 1 && !inter && !shared && !a.bg && !a.bu)
+    return norm ? launch_gu_w12<32, 4, true>(a, st) : launch_gu_w12<32, 4, false>(a, st);
 #define LBK_GU2(BB, MM, SH)                                                                          \
   if (norm) return launch_gu_t<BB, MM, true, false, SH>(a, st);                                     \
   return inter ? launch_gu_t<BB, MM, false, true, SH>(a, st) : launch_gu_t<BB, MM, false, false, SH>(a, st);
