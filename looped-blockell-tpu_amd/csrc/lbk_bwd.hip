@@ -722,6 +722,149 @@ __global__ __launch_bounds__(512) void dw_kernel(DWJobs jobs) {
       for (int v = 0; v < 4; ++v) part[(16 * md + 4 * g + v) * B + 16 * mD + i] = acc[md][mD][v];
 }
 
+// The B = 32 tile gradient with the token slices double-buffered in LDS and filled by direct
+// global->LDS loads (global_load_lds_dwordx4), so slice s + 1 streams in while slice s is
+// multiplied.  The slices are unpadded 64-byte rows whose 16-byte chunk c of row t sits at chunk
+// c ^ ((t & 8) >> 2): the transposed reads of a half-wave (rows t..t+3 and t+8..t+11, two
+// chunks each) then cover all 64 banks once.  A load instruction fills 1 KB (16 rows) in place:
+// lane l of instruction j brings the chunk whose swizzled position is 64 j + l.  The waits are
+// explicit (s_waitcnt vmcnt with the next slice's loads still in flight) and the barriers carry
+// no fence, which would wait for those loads too.
+namespace {
+constexpr int DWD_TS = 64;   // tokens per slice
+
+__device__ __forceinline__ int dwd_swz(int row) { return (row & 8) >> 2; }
+
+// transposed operand of a swizzled [64][32] bf16 slice: lane (s, g) gets column c0 + 4 (s & 3) ..
+// + 3 of rows t0 + 8 g + s / 4 and + 4 (as tr_frag on a plain row-major slice)
+__device__ __forceinline__ u32x4 dwd_frag(const uint16_t* slice, int t0, int c0, int lane) {
+  const int s = lane & 15, g = lane >> 4;
+  const int row = t0 + 8 * g + (s >> 2);
+  const int col = c0 + 4 * (s & 3);
+  const uint16_t* p = slice + row * 32 + 8 * ((col >> 3) ^ dwd_swz(row)) + (col & 7);
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * 32));   // rows + 4: same swizzle
+  const u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
+
+// 1 KB of a slice (instruction j: rows 16 j .. 16 j + 15) from rows t0.. of a [N, ld] matrix,
+// columns col0 .. col0 + 31, rows at or past N read from row N - 1
+__device__ __forceinline__ void dwd_load(const uint16_t* src, int64_t ld, int64_t col0, int64_t t0, int64_t N,
+                                         uint16_t* slice, int j, int lane) {
+  const int P = 64 * j + lane;
+  const int row = P >> 2;
+  const int c = (P & 3) ^ dwd_swz(row);
+  const int64_t t = t0 + row < N ? t0 + row : N - 1;
+  // issued from inline assembly, so the compiler counts no load of its own here and inserts no
+  // wait for these LDS writes before the reads of the other buffer; the kernel waits explicitly
+  const uint32_t lds = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void*)(slice + 512 * j)));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src + t * ld + col0 + 8 * c),
+               "s"(lds) : "memory", "m0");
+}
+
+// barrier without a fence: this wave's LDS reads have returned, its loads in flight stay so
+__device__ __forceinline__ void dwd_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+}  // namespace
+
+__global__ __launch_bounds__(512) void dw_dma_kernel(DWJobs jobs) {
+  constexpr int B = 32, CW = 2, TS = DWD_TS;
+  int jt = 0;
+#pragma unroll
+  for (int u = 1; u < DWJobs::kMax; ++u)
+    if (u < jobs.n && (int64_t)blockIdx.x >= jobs.first[u]) jt = u;
+  const DWJob& J = jobs.job[jt];
+  const int64_t b = (int64_t)blockIdx.x - jobs.first[jt];
+  const int KG = (J.K + 7) / 8;
+  const int ch = (int)(b % jobs.nchunk);
+  const int rg = (int)(b / jobs.nchunk);
+  const int r = rg / KG, kg = rg - r * KG;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = uniform(tid >> 6);
+  const int i = lane & 15, g = lane >> 4;
+  const int k = 8 * kg + w;
+  const bool slot = k < J.K;
+  const int col = slot ? J.col[(int64_t)r * J.K + k] : -1;
+  const bool live = col >= 0 && col < J.C;
+  __shared__ __attribute__((aligned(16))) uint16_t xs0[8][TS * B], xs1[8][TS * B];
+  __shared__ __attribute__((aligned(16))) uint16_t gs0[TS * B], gs1[TS * B];
+
+  f32x4 acc[CW][CW];
+#pragma unroll
+  for (int md = 0; md < CW; ++md)
+#pragma unroll
+    for (int mD = 0; mD < CW; ++mD) acc[md][mD] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t N = jobs.N;
+  const int64_t tbeg = (int64_t)ch * jobs.chunk;
+  const int64_t tend = (tbeg + jobs.chunk) < N ? (tbeg + jobs.chunk) : N;
+  const int ns = tbeg < tend ? (int)((tend - tbeg + TS - 1) / TS) : 0;
+  const int64_t xcol = (int64_t)(live ? col : 0) * B;
+  const int64_t gcol = (int64_t)r * B;
+  // a slice into one buffer pair: four instructions of this wave's X slice, one of the shared
+  // G slice for waves 0-3
+  auto issue = [&](int s, uint16_t* xd, uint16_t* gd) {
+    const int64_t t0 = tbeg + (int64_t)s * TS;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dwd_load(J.x, J.ldx, xcol, t0, N, xd, j, lane);
+    if (w < 4) dwd_load(J.gy, J.ldg, gcol, t0, N, gd, w, lane);
+  };
+  // slice s from (xb, gb) while slice s + 1 streams into (xn, gn); the loop below passes the
+  // buffers as the fixed arrays, so the compiler sees that the reads and the loads in flight
+  // touch different memory and puts no wait of its own before the reads
+  auto step = [&](int s, uint16_t* xb, uint16_t* gb, uint16_t* xn, uint16_t* gn) {
+    const int64_t t0 = tbeg + (int64_t)s * TS;
+    if (s + 1 < ns) {
+      issue(s + 1, xn, gn);
+      // this wave's loads of slice s are done once only slice s + 1's (5 or 4) are in flight
+      if (w < 4) __builtin_amdgcn_s_waitcnt(0x0F70 | 5);
+      else __builtin_amdgcn_s_waitcnt(0x0F70 | 4);
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+    }
+    dwd_barrier();
+    if (t0 + TS > tend) {
+      // the last slice of the data: rows at or past tend hold clamped copies; zero them
+      const int valid = (int)(tend - t0);
+      for (int q = lane; q < TS * 4; q += 64)
+        if (q / 4 >= valid) *reinterpret_cast<u32x4*>(xb + 8 * q) = u32x4{0, 0, 0, 0};
+      for (int q = tid; q < TS * 4; q += 512)
+        if (q / 4 >= valid) *reinterpret_cast<u32x4*>(gb + 8 * q) = u32x4{0, 0, 0, 0};
+      __syncthreads();
+    }
+    // dW[d][D] += sum_t X[t][d] G[t][D] (operands as in dw_kernel)
+#pragma unroll
+    for (int ks = 0; ks < TS / 32; ++ks) {
+      u32x4 bv[CW];
+#pragma unroll
+      for (int mD = 0; mD < CW; ++mD) bv[mD] = dwd_frag(gb, 32 * ks, 16 * mD, lane);
+#pragma unroll
+      for (int md = 0; md < CW; ++md) {
+        const u32x4 av = dwd_frag(xb, 32 * ks, 16 * md, lane);
+#pragma unroll
+        for (int mD = 0; mD < CW; ++mD) acc[md][mD] = mfma_bf16(av, bv[mD], acc[md][mD]);
+      }
+    }
+    // every wave's reads of this buffer pair have returned before slice s + 2 is loaded into it
+    dwd_barrier();
+  };
+  if (ns > 0) issue(0, xs0[w], gs0);
+  for (int s = 0; s < ns; s += 2) {
+    step(s, xs0[w], gs0, xs1[w], gs1);
+    if (s + 1 < ns) step(s + 1, xs1[w], gs1, xs0[w], gs0);
+  }
+  if (!live) return;
+  float* part = J.part + ((int64_t)ch * J.R * J.K + (int64_t)r * J.K + k) * B * B;
+#pragma unroll
+  for (int md = 0; md < CW; ++md)
+#pragma unroll
+    for (int mD = 0; mD < CW; ++mD)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) part[(16 * md + 4 * g + v) * B + 16 * mD + i] = acc[md][mD][v];
+}
+
 // dW[e] = sum over chunks of the partial tiles (fixed order), bf16; dead slots -> 0
 __global__ __launch_bounds__(256) void dw_reduce_kernel(DWJobs jobs, int B) {
   int jt = 0;
@@ -757,7 +900,7 @@ int launch_dw(int B, const DWJob* jobs, int n, int64_t N, int chunk, hipStream_t
   }
   if (blocks > 0) {
     if (B == 16) hipLaunchKernelGGL(dw_kernel<16>, dim3((unsigned)blocks), dim3(512), 0, st, J);
-    else if (B == 32) hipLaunchKernelGGL(dw_kernel<32>, dim3((unsigned)blocks), dim3(512), 0, st, J);
+    else if (B == 32) hipLaunchKernelGGL(dw_dma_kernel, dim3((unsigned)blocks), dim3(512), 0, st, J);
     else if (B == 64) hipLaunchKernelGGL(dw_kernel<64>, dim3((unsigned)blocks), dim3(512), 0, st, J);
     else return -2;
     if (hipGetLastError() != hipSuccess) return -1;
