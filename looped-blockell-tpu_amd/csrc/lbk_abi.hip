@@ -87,7 +87,7 @@ TernSplitLayout tern_split_layout(int64_t N, const lbk_bell_ternary* gate, const
   L.pg = tprep_bytes((int64_t)gate->R * gate->K, gate->R, 0);
   L.pu = tprep_bytes((int64_t)up->R * up->K, up->R, 1);
   L.pd = tprep_bytes((int64_t)down->R * down->K, down->R, 2);
-  L.hmax = align256((size_t)tgu_slices(N) * (size_t)N * 4);
+  L.hmax = align256((size_t)tgu_slices(N, gate->R) * (size_t)N * 4);
   L.h = align256((size_t)N * gate->R * gate->B * 2);
   L.total = L.pg + L.pu + L.pd + L.hmax + L.h;
   return L;
@@ -758,7 +758,7 @@ static int tern_fwd_impl(const int8_t* xq, const float* sx, int64_t N, int32_t d
     float* hmax = reinterpret_cast<float*>(ws + own);
     g.xq = xq; g.sx = sx; g.N = N; g.d_model = d_model;
     g.cg = gate->col_idx; g.cu = up->col_idx; g.K = gate->K;
-    g.R_ff = gate->R; g.H = tgu_slices(N); g.h = h; g.hmax = hmax;
+    g.R_ff = gate->R; g.H = tgu_slices(N, gate->R); g.h = h; g.hmax = hmax;
     g.acc_g = ax.acc_gate; g.acc_u = ax.acc_up; g.g_pre = ax.gate_pre; g.u_pre = ax.up_pre;
     if (launch_tgu(g, s) != 0) return LBK_ERR_LAUNCH;
     d.h = h; d.hmax = hmax; d.H = g.H; d.N = N; d.d_ff = (int)d_ff; d.d_model = d_model;

@@ -182,6 +182,7 @@ struct TDNArgs {
   int8_t* hq_out;           // optional [N, d_ff]
   float* sh_out;            // optional [N]
   int32_t* acc_d;           // optional [N, d_model]: integer accumulators sum_k m * P
+  int G;                    // down row groups per token block (set by the launcher)
 };
 // bytes of one prepared tile of weight `which` (0 gate, 1 up: int8 MFMA fragments; 2 down:
 // 2-bit t + 1 words)
@@ -205,7 +206,7 @@ int launch_tprep(const TPrepWeight (&w)[3], void* const (&out)[3], const tu32x4*
                  const int32_t* (&mval)[3], const float* (&rmul)[3], hipStream_t st,
                  bool run = true);
 bool tsplit_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd);
-int tgu_slices(int64_t N);
+int tgu_slices(int64_t N, int R_ff);
 int launch_tgu(const TGUArgs& a, hipStream_t st);
 int launch_tdn(const TDNArgs& a, hipStream_t st);
 

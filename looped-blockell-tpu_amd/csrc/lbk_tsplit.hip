@@ -450,7 +450,9 @@ __global__ __launch_bounds__(64 * NW, 1) void tdn_kernel(TDNArgs a) {
   const int lane = tid & 63;
   const int w = uniform(tid >> 6);
   const int i = lane & 15, g = lane >> 4;
-  const int64_t t0 = (int64_t)blockIdx.x * TM;
+  // workgroup -> (16-token block, row group grp of G: down rows grp, grp + G, ...)
+  const int grp = (int)(blockIdx.x % (unsigned)a.G);
+  const int64_t t0 = (int64_t)(blockIdx.x / (unsigned)a.G) * TM;
   const int d_ff = a.d_ff;
   const int rowb = d_ff;   // int8 panel row stride (a multiple of 256)
   const int Kd = a.Kd;
@@ -503,16 +505,17 @@ __global__ __launch_bounds__(64 * NW, 1) void tdn_kernel(TDNArgs a) {
     amax = fmaxf(amax, 1e-8f);
     s_scale[tid] = __fdiv_rn(128.0f, amax);
     s_sh[tid] = amax * 0.0078125f;
-    if (a.sh_out && t < a.N) a.sh_out[t] = amax * 0.0078125f;
+    if (a.sh_out && grp == 0 && t < a.N) a.sh_out[t] = amax * 0.0078125f;
   }
 
-  // ---- ring of down tiles: wave w owns rows rm = w, w + NW, ...
-  const int nrows = (a.R_m - w + NW - 1) / NW;
+  // ---- ring of down tiles: wave w owns rows rm = grp + G (w + NW n)
+  const int rows_g = (a.R_m - grp + a.G - 1) / a.G;
+  const int nrows = (rows_g - w + NW - 1) / NW;
   const int KP = (Kd + RING - 1) / RING * RING;
   int rn = 0, rk = 0;
   auto fetch = [&](TDSlot& S) {
     const bool live = rn < nrows && rk < Kd;
-    const int rm = w + NW * rn;
+    const int rm = grp + a.G * (w + NW * rn);
     const int64_t e = live ? (int64_t)rm * Kd + rk : ztile;
     S.wd = a.twd[e * 64 + lane];
     S.cm = make_int2(live ? (int)e : 0, 0);
@@ -558,7 +561,7 @@ __global__ __launch_bounds__(64 * NW, 1) void tdn_kernel(TDNArgs a) {
             q[d] = lo | hi;
           }
           if (t >= a.N) q = u32x4{0, 0, 0, 0};
-          if (a.hq_out && t < a.N) *reinterpret_cast<u32x4*>(a.hq_out + t * (int64_t)d_ff + 16 * cc) = q;
+          if (a.hq_out && grp == 0 && t < a.N) *reinterpret_cast<u32x4*>(a.hq_out + t * (int64_t)d_ff + 16 * cc) = q;
           // -sum(hq) of each 64-wide block: its 4 units sit in 4 adjacent lanes, all of which
           // take part (upr is a multiple of 16, so a 4-lane group is in or out as a whole)
           int sm = sum16_i8(q);
@@ -623,7 +626,7 @@ __global__ __launch_bounds__(64 * NW, 1) void tdn_kernel(TDNArgs a) {
     }
     madd(acc, Pp, mp);
     // epilogue of down row rm: y = f32(f32(acc) * 2^-e) * sh (+ residual) -> bf16
-    const int rm = w + NW * n;
+    const int rm = grp + a.G * (w + NW * n);
     const float fd = rtab[rm];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -702,9 +705,14 @@ bool tsplit_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int
   return true;
 }
 
-int tgu_slices(int64_t N) {
+// row slices per 64-token block: about 256 workgroups in all, at least 8 rows (one per wave) per
+// slice
+int tgu_slices(int64_t N, int R_ff) {
   const int64_t blocks = (N + 63) / 64;
-  return blocks >= 256 ? 1 : (blocks >= 128 ? 2 : 4);
+  if (blocks >= 256) return 1;
+  const int hmax = R_ff / 8 > 1 ? R_ff / 8 : 1;
+  const int H = (int)((256 + blocks - 1) / blocks);
+  return H < hmax ? H : hmax;
 }
 
 int launch_tgu(const TGUArgs& a, hipStream_t st) {
@@ -724,13 +732,19 @@ int launch_tgu(const TGUArgs& a, hipStream_t st) {
 // 16 waves, ring 8 144 us; 8 waves (four rows each), ring 8 153 us.
 constexpr int TDN_WAVES = 16, TDN_RING = 4, TDN_UB = 4;
 
-int launch_tdn(const TDNArgs& a, hipStream_t st) {
-  if (a.N == 0) return 0;
+int launch_tdn(const TDNArgs& a0, hipStream_t st) {
+  if (a0.N == 0) return 0;
   auto kern = tdn_kernel<TDN_WAVES, TDN_RING, TDN_UB>;
   static std::atomic<uint64_t> configured{0};
   if (set_lds_limit_once((const void*)kern, 163840 - 256, configured)) return -1;
-  const size_t lds = tdn_lds(a.d_ff, a.R_m, a.Kd);
-  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 15) / 16)), dim3(64 * TDN_WAVES), lds, st, a);
+  const size_t lds = tdn_lds(a0.d_ff, a0.R_m, a0.Kd);
+  // with fewer than 256 token blocks, the down rows are dealt to G row groups (each workgroup
+  // quantises the block's h rows itself and runs every G-th row), at least 4 rows per group
+  TDNArgs a = a0;
+  const int64_t blocks = (a.N + 15) / 16;
+  const int gmax = a.R_m / 4 > 1 ? a.R_m / 4 : 1;
+  a.G = blocks >= 256 ? 1 : (int)std::min<int64_t>((256 + blocks - 1) / blocks, gmax);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(blocks * a.G)), dim3(64 * TDN_WAVES), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
