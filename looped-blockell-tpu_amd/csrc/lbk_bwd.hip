@@ -257,7 +257,9 @@ __global__ __launch_bounds__(512, 1) void dh_panel_kernel(TProdArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = uniform(tid >> 6);
   const int i = lane & 15, g = lane >> 4;
-  const int64_t t0 = (int64_t)blockIdx.x * TM;
+  // workgroup -> (token block, slice sl of nsl: column blocks sl + nsl (w + 8 j))
+  const int sl = (int)(blockIdx.x % (unsigned)a.nsl);
+  const int64_t t0 = (int64_t)(blockIdx.x / (unsigned)a.nsl) * TM;
   const TProdSrc S = a.src[0];
   const int d_model = (int)S.lda;
 
@@ -322,7 +324,7 @@ __global__ __launch_bounds__(512, 1) void dh_panel_kernel(TProdArgs a) {
   typedef uint32_t raw_t __attribute__((ext_vector_type(NV / 2)));
   raw_t graw[MT][NP], uraw[MT][NP];
   auto col_of = [&](int c, int p) { return (int64_t)c * B + (CW == 1 ? 4 * g : 32 * p + 8 * g); };
-  for (int c = w; c < a.C; c += 8) {
+  for (int c = sl + a.nsl * w; c < a.C; c += 8 * a.nsl) {
 #pragma unroll
     for (int q = 0; q < MT; ++q) {
       const int64_t tn = t0 + 16 * q + i;
@@ -384,14 +386,20 @@ __global__ __launch_bounds__(512, 1) void dh_panel_kernel(TProdArgs a) {
 }
 
 // dh through the LDS panel when the dy rows of 16*MT tokens fit (d_model <= 2048, one source)
+// With fewer token blocks than CUs, the column blocks are split over nsl workgroups per token
+// block (about 256 workgroups, at least one column block per wave), each loading the dy panel.
 template <int B, int MT>
-static int launch_dh_panel_t(const TProdArgs& a, hipStream_t st) {
+static int launch_dh_panel_t(const TProdArgs& a0, hipStream_t st) {
   constexpr size_t lds = (size_t)16 * MT * (8192 / MT);
   auto kern = dh_panel_kernel<B, MT>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)lds) != hipSuccess)
     return -1;
-  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 16 * MT - 1) / (16 * MT))), dim3(512), lds, st, a);
+  TProdArgs a = a0;
+  const int64_t ntb = (a.N + 16 * MT - 1) / (16 * MT);
+  const int smax = a.C / 8 > 1 ? a.C / 8 : 1;
+  a.nsl = ntb >= 256 ? 1 : (int)std::min<int64_t>((256 + ntb - 1) / ntb, smax);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(ntb * a.nsl)), dim3(512), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -434,7 +442,9 @@ __global__ __launch_bounds__(64 * NW, 1) void dx_stage_kernel(TProdArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = uniform(tid >> 6);
   const int i = lane & 15, g = lane >> 4;
-  const int64_t t0 = (int64_t)blockIdx.x * 64;
+  // workgroup -> (64-token block, slice sl of nsl: output blocks sl + nsl (w + NW o))
+  const int sl = (int)(blockIdx.x % (unsigned)a.nsl);
+  const int64_t t0 = (int64_t)(blockIdx.x / (unsigned)a.nsl) * 64;
   const int gk = (B == 16) ? (g & 1) : g;
   const bool kz = (B == 16) && g >= 2;
 
@@ -496,7 +506,7 @@ __global__ __launch_bounds__(64 * NW, 1) void dx_stage_kernel(TProdArgs a) {
 #pragma unroll
       for (int o = 0; o < OPW; ++o) {
         cur[o] = 0;
-        const int c = w + NW * o;
+        const int c = sl + a.nsl * (w + NW * o);
         const int cnt = c < a.C ? S.cnt[c] : 0;
         lvr[o] = lane < cnt ? S.list[(int64_t)c * S.cap + lane] : 0x7fffffff;
       }
@@ -514,7 +524,7 @@ __global__ __launch_bounds__(64 * NW, 1) void dx_stage_kernel(TProdArgs a) {
     };
 #pragma unroll
     for (int o = 0; o < OPW; ++o) {
-      const int c = w + NW * o;
+      const int c = sl + a.nsl * (w + NW * o);
       if (c >= a.C) continue;
       auto compute = [&](const Ent& E) {
         const int rb = uniform(E.r) - rlo;           // column block within the stage
@@ -565,7 +575,7 @@ __global__ __launch_bounds__(64 * NW, 1) void dx_stage_kernel(TProdArgs a) {
   // epilogue: dx = acc (+ dy)
 #pragma unroll
   for (int o = 0; o < OPW; ++o) {
-    const int c = w + NW * o;
+    const int c = sl + a.nsl * (w + NW * o);
     if (c >= a.C) continue;
 #pragma unroll
     for (int q = 0; q < MT; ++q) {
@@ -582,26 +592,33 @@ static int launch_dx_stage_t(const TProdArgs& a, hipStream_t st) {
   if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return -1;
-  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 63) / 64)), dim3(64 * NW), lds, st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 63) / 64 * a.nsl)), dim3(64 * NW), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 // staged dx when every output block fits the waves' accumulators (OPW * B / 16 <= 8) and the
 // sources' widths are whole stages of 16-byte chunks
-static int launch_dx_stage(int B, const TProdArgs& a, hipStream_t st) {
-  if (a.nsrc < 1 || a.nsrc > 2) return -2;
-  for (int s = 0; s < a.nsrc; ++s)
-    if (a.src[s].lda % B) return -2;
+static int launch_dx_stage(int B, const TProdArgs& a0, hipStream_t st) {
+  if (a0.nsrc < 1 || a0.nsrc > 2) return -2;
+  for (int s = 0; s < a0.nsrc; ++s)
+    if (a0.src[s].lda % B) return -2;
+  // With fewer 64-token blocks than CUs, the output blocks are split over nsl workgroups per
+  // token block so that each wave owns one (each workgroup stages all the activation columns).
+  TProdArgs a = a0;
+  const int64_t ntb = (a.N + 63) / 64;
+  const int per_wg = B == 64 ? 8 : 16;
+  a.nsl = ntb >= 256 ? 1 : (a.C + per_wg - 1) / per_wg;
+  const int cs = (a.C + a.nsl - 1) / a.nsl;        // output blocks per slice
   // 16 waves (four per SIMD to hide the tile loads) when their accumulators fit 128 VGPRs:
   // headline backward 0.785 -> 0.740 ms, B = 16 at d_model 512 / 1024 0.497 -> 0.447 and
   // 2.10 -> 1.95 ms against 8 waves; B = 64 keeps 8 waves (16 would spill)
-  const int o16 = (a.C + 15) / 16;
+  const int o16 = (cs + 15) / 16;
   if (B == 16 && o16 <= 1) return launch_dx_stage_t<16, 1, 16>(a, st);
   if (B == 16 && o16 <= 2) return launch_dx_stage_t<16, 2, 16>(a, st);
   if (B == 16 && o16 <= 4) return launch_dx_stage_t<16, 4, 16>(a, st);
   if (B == 32 && o16 <= 1) return launch_dx_stage_t<32, 1, 16>(a, st);
   if (B == 32 && o16 <= 2) return launch_dx_stage_t<32, 2, 16>(a, st);
-  const int opw = (a.C + 7) / 8;
+  const int opw = (cs + 7) / 8;
 #define LBK_DX(BB, OO) if (B == BB && opw <= OO) return launch_dx_stage_t<BB, OO, 8>(a, st);
   if (B == 16) { LBK_DX(16, 1) LBK_DX(16, 2) LBK_DX(16, 4) LBK_DX(16, 8) }
   if (B == 32) { LBK_DX(32, 1) LBK_DX(32, 2) LBK_DX(32, 4) }

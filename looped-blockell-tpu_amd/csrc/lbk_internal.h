@@ -235,6 +235,7 @@ struct TProdArgs {
   int64_t N; int C; int64_t ldo;    // output [N, C*B], row stride ldo (also of g, u, resid)
   const uint16_t* g; const uint16_t* u; uint16_t* dg; uint16_t* du;   // mode 0
   const uint16_t* resid; uint16_t* out;                               // mode 1 (resid optional)
+  int nsl;                          // output column slices per token block (set by the launcher)
 };
 // mode 0: dh -> dg, du (SiLU*mul backward); mode 1: out = product + resid
 int launch_tprod(int B, int mode, const TProdArgs& a, hipStream_t st);
