@@ -269,9 +269,17 @@ def bench_bf16_backward(steps, warmup, device):
     ms, per = time_steps(step, steps, warmup)
     flops = 2 * nonzero_flops(w)
     assert all(torch.isfinite(t.float()).all() for t in out["r"])
+    # the same backward on the first N tokens
+    by_tokens = {}
+    for n in FEWER_TOKENS:
+        sl = [t[:n].contiguous() for t in (dy, x, gp, uo, h)]
+        ms_n, _ = time_steps(lambda i: kernels.swiglu_bwd(*sl, *g, *u, *d), steps, warmup)
+        by_tokens[str(n)] = dict(ms_per_step=ms_n, value=2 * nonzero_flops(dict(w, N=n)) / (ms_n * 1e-3) / 1e12)
     return dict(workload="backward of the headline workload (dx and the gate/up/down tile gradients)",
                 ms_per_step=ms, value=flops / (ms * 1e-3) / 1e12, unit="TFLOP/s",
-                frac_of_bf16_peak=flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, kernel_ms_avg=sum(per) / len(per))
+                frac_of_bf16_peak=flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, kernel_ms_avg=sum(per) / len(per),
+                fewer_tokens=dict(workload="the same backward on the first N tokens", unit="TFLOP/s",
+                                  by_tokens=by_tokens))
 
 
 def bench_topology(steps, warmup, device):
