@@ -36,7 +36,7 @@ class LoopedSwiGLU(nn.Module):
             # training: the L applications one by one through the differentiable RMSNorm and
             # SwiGLU (titan::rmsnorm_bwd, titan::block_ell_swiglu_bwd_bias), as the reference's
             # scan is differentiated (looped_blockell/looping/looped_model.py:342-350); the
-            # carried state stays in fp32 as in the one-launch path
+            # carried state stays in fp32 as in the operator path
             hf = h2.float()
             for _ in range(self.L):
                 hf = hf + self.mlp(self.norm(hf.to(torch.bfloat16))).float()
