@@ -4,8 +4,9 @@ The MLP half of the reference's core block applied L times:
 ``h <- h + MLPBlock(RMSNorm(h))`` (reference ``looped_blockell/layers/transformer_block.py:83-84``,
 the core loop ``looped_blockell/looping/looped_model.py:293-350`` and the MLP path of
 ``csrc/loop/persistent_core.cu:315-335``), one operator call
-(``titan::looped_swiglu``): the weights are packed once and one persistent launch runs the
-L applications with the carried state in fp32.  With gradients required the applications
+(``titan::looped_swiglu``): the weights are packed once, then a gate/up and a down launch per
+application with the carried state in fp32 (``titan::looped_swiglu_persistent`` runs all L in
+one launch).  With gradients required the applications
 run one by one through the differentiable RMSNorm and SwiGLU instead.
 """
 
