@@ -33,7 +33,7 @@ namespace lbk {
 
 namespace {
 
-constexpr int DEC_DS = 3;   // down slots per wave: Kd <= 8 * DEC_DS
+constexpr int DEC_DS_MAX = 4;   // down slots per wave: Kd <= 8 * DEC_DS_MAX
 
 template <int B>
 __device__ __forceinline__ void mfma_tile(const u32x4 (&a)[TileShape<B>::NKS], const WRaw<B>& wt,
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(512, 1) void decode_gu_kernel(DecodeArgs a) {
 // down: output columns 16q .. 16q + 15 of down row rm; the B / 16 units of a row
 // are workgroups 8 * (B / 16 * (rm / 8) + q) + rm % 8
 // ---------------------------------------------------------------------------
-template <int B>
+template <int B, int DEC_DS>
 __global__ __launch_bounds__(512, 1) void decode_dn_kernel(DecodeArgs a) {
   constexpr int CW = TileShape<B>::CW;   // = B / 16
   constexpr int NKS = TileShape<B>::NKS;
@@ -286,10 +286,10 @@ __global__ __launch_bounds__(512, 1) void decode_dn_kernel(DecodeArgs a) {
 }
 
 // Whether the decode kernels take this shape: at most 8 gate and 8 up slots per h
-// row, 1 .. 8 * DEC_DS down slots (empty slot lists excluded: unused slots read
+// row, 1 .. 8 * DEC_DS_MAX down slots (empty slot lists excluded: unused slots read
 // each weight's first tile).
 bool decode_supported(int Kg, int Ku, int Kd) {
-  return Kg >= 1 && Ku >= 1 && Kd >= 1 && Kg <= 8 && Ku <= 8 && Kd <= 8 * DEC_DS;
+  return Kg >= 1 && Ku >= 1 && Kd >= 1 && Kg <= 8 && Ku <= 8 && Kd <= 8 * DEC_DS_MAX;
 }
 
 int launch_decode(int B, const DecodeArgs& a, hipStream_t st) {
@@ -297,21 +297,22 @@ int launch_decode(int B, const DecodeArgs& a, hipStream_t st) {
   if (!decode_supported(a.Kg, a.Ku, a.Kd) || a.R_ff <= 0 || a.R_m <= 0) return -2;
   const unsigned g1 = 8u * (unsigned)decode_gu_per_xcd(a.R_ff);
   const unsigned g2 = 8u * (unsigned)(B / 16) * (unsigned)((a.R_m + 7) / 8);
+  // three down slots per wave up to Kd = 24, four beyond (a fourth slot of dead loads costs
+  // the shorter lists time)
+  const bool ds4 = a.Kd > 24;
+#define LBK_DEC(BB)                                                                                  \
+  case BB:                                                                                           \
+    hipLaunchKernelGGL(decode_gu_kernel<BB>, dim3(g1), dim3(512), 0, st, a);                         \
+    if (ds4) hipLaunchKernelGGL((decode_dn_kernel<BB, 4>), dim3(g2), dim3(512), 0, st, a);           \
+    else hipLaunchKernelGGL((decode_dn_kernel<BB, 3>), dim3(g2), dim3(512), 0, st, a);               \
+    break;
   switch (B) {
-    case 16:
-      hipLaunchKernelGGL(decode_gu_kernel<16>, dim3(g1), dim3(512), 0, st, a);
-      hipLaunchKernelGGL(decode_dn_kernel<16>, dim3(g2), dim3(512), 0, st, a);
-      break;
-    case 32:
-      hipLaunchKernelGGL(decode_gu_kernel<32>, dim3(g1), dim3(512), 0, st, a);
-      hipLaunchKernelGGL(decode_dn_kernel<32>, dim3(g2), dim3(512), 0, st, a);
-      break;
-    case 64:
-      hipLaunchKernelGGL(decode_gu_kernel<64>, dim3(g1), dim3(512), 0, st, a);
-      hipLaunchKernelGGL(decode_dn_kernel<64>, dim3(g2), dim3(512), 0, st, a);
-      break;
+    LBK_DEC(16)
+    LBK_DEC(32)
+    LBK_DEC(64)
     default: return -2;
   }
+#undef LBK_DEC
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
