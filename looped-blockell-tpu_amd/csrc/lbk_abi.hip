@@ -292,8 +292,8 @@ static int swiglu_split(const uint16_t* x, const float* xf, const float* norm_sc
   return launch_dn(gate->B, d, st) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
 }
 
-// ---- decode shape (N <= 16): gate/up and down kernels of lbk_decode.hip
-static constexpr int64_t kDecodeMaxTokens = 16;
+// ---- decode shape (N <= 64): gate/up and down kernels of lbk_decode.hip
+static constexpr int64_t kDecodeMaxTokens = 64;
 
 static bool use_decode(int64_t N, const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down, bool inter) {
   // the decode kernels read down tiles (and the prefetch reads them) with 16-byte loads
@@ -336,6 +336,14 @@ static int swiglu_fwd_impl(const uint16_t* x, int64_t N, int32_t d_model, const 
   if (!a16(x) || !a16(out) || (d_model % 8)) return LBK_ERR_ALIGN;
   for (const void* p : {(const void*)h_out, (const void*)gate_pre_out, (const void*)up_out})
     if (p && !a16(p)) return LBK_ERR_ALIGN;
+  const bool split = use_split(gate, up, down, d_model);
+  const size_t pbytes = split ? packed_ffn_bytes(gate, up, down) : 0;
+  // a packed copy is checked whatever path the token count selects (the decode kernels read the
+  // raw tiles and do not use it)
+  if (split && prepacked) {
+    if (prepacked_bytes < pbytes) return LBK_ERR_WORKSPACE;
+    if (!a16(prepacked)) return LBK_ERR_ALIGN;
+  }
   if (use_decode(N, gate, up, down, gate_pre_out || up_out)) {
     uint16_t* hbuf = h_out;
     if (!hbuf) {
@@ -355,12 +363,6 @@ static int swiglu_fwd_impl(const uint16_t* x, int64_t N, int32_t d_model, const 
     a.h = hbuf;
     a.bg = bs.g; a.bu = bs.u; a.bd = bs.d;
     return launch_decode(gate->B, a, s) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
-  }
-  const bool split = use_split(gate, up, down, d_model);
-  const size_t pbytes = split ? packed_ffn_bytes(gate, up, down) : 0;
-  if (split && prepacked) {
-    if (prepacked_bytes < pbytes) return LBK_ERR_WORKSPACE;
-    if (!a16(prepacked)) return LBK_ERR_ALIGN;
   }
   const size_t own = (split && !prepacked) ? pbytes : 0;     // packed tiles built by this call
   const size_t hbytes = h_out ? 0 : align256((size_t)N * d_ff * 2);

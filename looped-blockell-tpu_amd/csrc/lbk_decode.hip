@@ -1,4 +1,5 @@
-// lbk_decode.hip — decode-shaped SwiGLU FFN (N <= 16 tokens), gfx950.
+// lbk_decode.hip — decode-shaped SwiGLU FFN (N <= 64 tokens, in one, two or four
+// 16-token tiles), gfx950.
 //
 // With 16 tokens every weight byte feeds 16 MACs, so the forward is a stream of
 // the weights through HBM: every CU should keep its share of the bytes in
@@ -131,11 +132,11 @@ __host__ __device__ inline int decode_gu_per_xcd(int R_ff) { return ((R_ff > 256
 // ---------------------------------------------------------------------------
 // gate/up: h row block r = blockIdx.x (workgroups r >= R_ff only prefetch)
 // ---------------------------------------------------------------------------
-template <int B>
+template <int B, int MT>
 __global__ __launch_bounds__(512, 1) void decode_gu_kernel(DecodeArgs a) {
   constexpr int CW = TileShape<B>::CW;
   constexpr int NKS = TileShape<B>::NKS;
-  __shared__ f32x4 red[8][CW][64];
+  __shared__ f32x4 red[8][CW][64];   // one 16-token tile at a time
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = uniform(tid >> 6);
@@ -164,39 +165,55 @@ __global__ __launch_bounds__(512, 1) void decode_gu_kernel(DecodeArgs a) {
   const int cl = cm[lane == 1 ? e1 : e0];
   asm volatile("" ::: "memory");
   WRaw<B> t0, t1;
-  u32x4 a0[NKS], a1[NKS];
+  u32x4 a0[MT][NKS], a1[MT][NKS];
   load_wraw<B>(vm + e0 * B * B, lane, t0);
   load_wraw<B>(vm + e1 * B * B, lane, t1);
   asm volatile("" ::: "memory");
   const int c0 = use0 ? __builtin_amdgcn_readlane(cl, 0) : -1, c1 = use1 ? __builtin_amdgcn_readlane(cl, 1) : -1;
   const bool ok0 = c0 >= 0 && c0 < C_in, ok1 = c1 >= 0 && c1 < C_in;
-  load_a_rows<B>(a.x + (int64_t)(ok0 ? c0 : 0) * B, a.d_model, ok0 ? a.N : 0, i, g, a0);
-  load_a_rows<B>(a.x + (int64_t)(ok1 ? c1 : 0) * B, a.d_model, ok1 ? a.N : 0, i, g, a1);
+  // 16-token tile mt: rows 16 mt .. of x (a tile past N reads row 0 and zeroes it)
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int nt = a.N - 16 * mt;
+    const uint16_t* xt = a.x + (nt > 0 ? (int64_t)16 * mt * a.d_model : 0);
+    load_a_rows<B>(xt + (int64_t)(ok0 ? c0 : 0) * B, a.d_model, ok0 && nt > 0 ? nt : 0, i, g, a0[mt]);
+    load_a_rows<B>(xt + (int64_t)(ok1 ? c1 : 0) * B, a.d_model, ok1 && nt > 0 ? nt : 0, i, g, a1[mt]);
+  }
   asm volatile("" ::: "memory");
   const uint32_t pf = prefetch_down_share<B, 4>(a, r, decode_gu_per_xcd(a.R_ff), tid);
   asm volatile("" ::: "memory");
-  f32x4 acc[CW];
+  f32x4 acc[MT][CW];
 #pragma unroll
-  for (int m = 0; m < CW; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (use0) mfma_tile<B>(a0, t0, acc);
-  if (use1) mfma_tile<B>(a1, t1, acc);
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-  for (int m = 0; m < CW; ++m) red[w][m][lane] = acc[m];
-  __syncthreads();
-  if (tid < 64 * CW) {
-    const int m = tid >> 6, l = tid & 63;
-    f32x4 gs = red[0][m][l], us = red[4][m][l];
+    for (int m = 0; m < CW; ++m) acc[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ww = 1; ww < 4; ++ww) {
-      gs += red[ww][m][l];
-      us += red[4 + ww][m][l];
-    }
-    const int col = r * B + CW * (l & 15) + m;
-    const float bgc = a.bg ? a.bg[col] : 0.f, buc = a.bu ? a.bu[col] : 0.f;
+  for (int mt = 0; mt < MT; ++mt) {
+    if (use0) mfma_tile<B>(a0[mt], t0, acc[mt]);
+    if (use1) mfma_tile<B>(a1[mt], t1, acc[mt]);
+  }
+  // the eight waves' sums meet in LDS, one 16-token tile at a time
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int tk = 4 * (l >> 4) + v;
-      if (tk < a.N) a.h[(int64_t)tk * d_ff + col] = f2bf(silu_f(gs[v] + bgc) * (us[v] + buc));
+  for (int mt = 0; mt < MT; ++mt) {
+    if (mt > 0) __syncthreads();   // the previous tile's sums have been read
+#pragma unroll
+    for (int m = 0; m < CW; ++m) red[w][m][lane] = acc[mt][m];
+    __syncthreads();
+    if (tid < 64 * CW) {
+      const int m = tid >> 6, l = tid & 63;
+      f32x4 gs = red[0][m][l], us = red[4][m][l];
+#pragma unroll
+      for (int ww = 1; ww < 4; ++ww) {
+        gs += red[ww][m][l];
+        us += red[4 + ww][m][l];
+      }
+      const int col = r * B + CW * (l & 15) + m;
+      const float bgc = a.bg ? a.bg[col] : 0.f, buc = a.bu ? a.bu[col] : 0.f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int tk = 16 * mt + 4 * (l >> 4) + v;
+        if (tk < a.N) a.h[(int64_t)tk * d_ff + col] = f2bf(silu_f(gs[v] + bgc) * (us[v] + buc));
+      }
     }
   }
   if (pf == 0x9e3779b9u && a.N < 0) a.h[0] = 0;                 // never true: keeps the loads
@@ -206,11 +223,11 @@ __global__ __launch_bounds__(512, 1) void decode_gu_kernel(DecodeArgs a) {
 // down: output columns 16q .. 16q + 15 of down row rm; the B / 16 units of a row
 // are workgroups 8 * (B / 16 * (rm / 8) + q) + rm % 8
 // ---------------------------------------------------------------------------
-template <int B, int DEC_DS>
+template <int B, int DEC_DS, int MT>
 __global__ __launch_bounds__(512, 1) void decode_dn_kernel(DecodeArgs a) {
   constexpr int CW = TileShape<B>::CW;   // = B / 16
   constexpr int NKS = TileShape<B>::NKS;
-  __shared__ f32x4 red[8][64];
+  __shared__ f32x4 red[8][MT][64];
   __shared__ __attribute__((aligned(16))) uint16_t xs[8][32 * 16];   // per-wave transpose buffer
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -224,7 +241,7 @@ __global__ __launch_bounds__(512, 1) void decode_dn_kernel(DecodeArgs a) {
   // Lane l reads row 32 ks + l / 2, columns 16q + 8 (l & 1) .. + 7 of each of its tiles; the
   // same loads in every wave (an unused slot reads the row's first tile).
   const int drow = lane >> 1;
-  u32x4 dq[DEC_DS][NKS], av[DEC_DS][NKS];
+  u32x4 dq[DEC_DS][NKS], av[DEC_DS][MT][NKS];
   int dc[DEC_DS];
   // Request order (a wave's loads return in order): the column indices (one vector load, lane
   // j holding slot w + 8j's), the tiles, whose addresses need no index, then the h fragments
@@ -248,11 +265,20 @@ __global__ __launch_bounds__(512, 1) void decode_dn_kernel(DecodeArgs a) {
   for (int j = 0; j < DEC_DS; ++j) {
     const int c = (w + 8 * j < a.Kd) ? __builtin_amdgcn_readlane(cl, j) : -1;
     dc[j] = (c >= 0 && c < a.R_ff) ? c : -1;
-    load_a_rows<B>(a.h + (int64_t)(dc[j] >= 0 ? dc[j] : 0) * B, d_ff, dc[j] >= 0 ? a.N : 0, i, g, av[j]);
+    // 16-token tile mt: rows 16 mt .. of h (a tile past N reads row 0 and zeroes it)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int nt = a.N - 16 * mt;
+      const uint16_t* ht = a.h + (nt > 0 ? (int64_t)16 * mt * d_ff : 0);
+      load_a_rows<B>(ht + (int64_t)(dc[j] >= 0 ? dc[j] : 0) * B, d_ff, dc[j] >= 0 && nt > 0 ? nt : 0, i, g,
+                     av[j][mt]);
+    }
   }
   // each (tile, k-step) of 32 rows x 16 columns goes through this wave's LDS buffer to become
   // the B fragment of lane (n, g): rows 8g .. 8g + 7 of column n
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   uint16_t* xw = xs[w];
 #pragma unroll
   for (int j = 0; j < DEC_DS; ++j) {
@@ -262,20 +288,22 @@ __global__ __launch_bounds__(512, 1) void decode_dn_kernel(DecodeArgs a) {
       *reinterpret_cast<u32x4*>(xw + drow * 16 + 8 * (lane & 1)) = dq[j][ks];
       // rows 8g .. 8g + 7 of column n = lane & 15, by two transposing 64-bit reads
       const u32x4 f = tr_frag(xw, 16, 0, 0, lane);
-      acc = mfma_bf16(av[j][ks], f, acc);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma_bf16(av[j][mt][ks], f, acc[mt]);
     }
   }
-  red[w][lane] = acc;
-  __syncthreads();
-  if (tid < 64) {
-    const int l = tid;
-    f32x4 ps = red[0][l];
 #pragma unroll
-    for (int ww = 1; ww < 8; ++ww) ps += red[ww][l];
+  for (int mt = 0; mt < MT; ++mt) red[w][mt][lane] = acc[mt];
+  __syncthreads();
+  if (tid < 64 * MT) {
+    const int mt = tid >> 6, l = tid & 63;
+    f32x4 ps = red[0][mt][l];
+#pragma unroll
+    for (int ww = 1; ww < 8; ++ww) ps += red[ww][mt][l];
     const int col = rm * B + 16 * q + (l & 15);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const int tk = 4 * (l >> 4) + v;
+      const int tk = 16 * mt + 4 * (l >> 4) + v;
       if (tk < a.N) {
         float o = ps[v] + (a.bd ? a.bd[col] : 0.f);
         if (a.resid) o += bf2f(a.resid[(int64_t)tk * a.d_model + col]);
@@ -298,13 +326,18 @@ int launch_decode(int B, const DecodeArgs& a, hipStream_t st) {
   const unsigned g1 = 8u * (unsigned)decode_gu_per_xcd(a.R_ff);
   const unsigned g2 = 8u * (unsigned)(B / 16) * (unsigned)((a.R_m + 7) / 8);
   // three down slots per wave up to Kd = 24, four beyond (a fourth slot of dead loads costs
-  // the shorter lists time)
+  // the shorter lists time); one, two or four 16-token tiles
   const bool ds4 = a.Kd > 24;
+  const int mt = a.N <= 16 ? 1 : (a.N <= 32 ? 2 : 4);
+#define LBK_DEC_MT(BB, MM)                                                                           \
+  if (mt == MM) {                                                                                    \
+    hipLaunchKernelGGL((decode_gu_kernel<BB, MM>), dim3(g1), dim3(512), 0, st, a);                   \
+    if (ds4) hipLaunchKernelGGL((decode_dn_kernel<BB, 4, MM>), dim3(g2), dim3(512), 0, st, a);       \
+    else hipLaunchKernelGGL((decode_dn_kernel<BB, 3, MM>), dim3(g2), dim3(512), 0, st, a);           \
+  }
 #define LBK_DEC(BB)                                                                                  \
   case BB:                                                                                           \
-    hipLaunchKernelGGL(decode_gu_kernel<BB>, dim3(g1), dim3(512), 0, st, a);                         \
-    if (ds4) hipLaunchKernelGGL((decode_dn_kernel<BB, 4>), dim3(g2), dim3(512), 0, st, a);           \
-    else hipLaunchKernelGGL((decode_dn_kernel<BB, 3>), dim3(g2), dim3(512), 0, st, a);               \
+    LBK_DEC_MT(BB, 1) LBK_DEC_MT(BB, 2) LBK_DEC_MT(BB, 4)                                            \
     break;
   switch (B) {
     LBK_DEC(16)
@@ -313,6 +346,7 @@ int launch_decode(int B, const DecodeArgs& a, hipStream_t st) {
     default: return -2;
   }
 #undef LBK_DEC
+#undef LBK_DEC_MT
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -441,7 +441,7 @@ def test_looped_L0_and_L1(gpu):
 
 
 DECODE_CASES = [
-    # (d_model, d_ff, B, density, N, sentinel_frac)   N <= 16: the decode kernels
+    # (d_model, d_ff, B, density, N, sentinel_frac)   N <= 64: the decode kernels
     # (at most 32 down slots per row)
     (256, 1024, 16, 0.25, 16, 0.0),
     (512, 1024, 32, 0.25, 5, 0.1),
@@ -450,6 +450,10 @@ DECODE_CASES = [
     (128, 512, 64, 1.0, 9, 0.0),
     (256, 2048, 16, 0.25, 8, 0.1),      # 32 down slots per row: four slots per wave
     (1024, 4096, 32, 0.25, 16, 0.05),   # the headline geometry at 16 tokens (32 down slots)
+    (1024, 4096, 32, 0.25, 64, 0.0),    # four 16-token tiles
+    (512, 1024, 32, 0.25, 33, 0.1),     # three tiles' worth: four tiles, the last ones partial
+    (256, 1024, 16, 0.25, 20, 0.05),    # two tiles
+    (1024, 3072, 64, 0.125, 47, 0.1),   # B = 64, four tiles
     (256, 4096, 16, 0.25, 8, 0.1),      # 64 down slots per row: beyond the kernels' 32, other path
 ]
 
