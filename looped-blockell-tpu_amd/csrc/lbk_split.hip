@@ -433,14 +433,18 @@ __global__ __launch_bounds__(768, 1) void gu_kernel_w12(GUArgs a) {
 }
 
 // plain Block-ELL product y = x W (+ bias) over an LDS panel of x (the gate/up kernel's gate
-// stream alone)
+// stream alone).  With one stream the accumulators and fragments fit 16 waves at a 2-deep ring
+// (at most 92 VGPRs); at the headline gate shape (16384 x 1024 -> 4096, B = 32) a call with
+// per-call packing took 0.0535 ms against 0.0615 with 8 waves and a 4-deep ring (12 waves:
+// 0.0551 with a 2-deep ring, 0.0535 with a 4-deep one)
+constexpr int LIN_WAVES = 16;
 template <int B, int MT, bool BIAS>
-__global__ __launch_bounds__(512, 1) void lin_kernel(GUArgs a) {
+__global__ __launch_bounds__(64 * LIN_WAVES, 1) void lin_kernel(GUArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   int64_t tb;
   int r_lo, nrs;
   gu_slice(a, tb, r_lo, nrs);
-  gu_tile<B, MT, false, false, true, false, BIAS, true>(a, tb, r_lo, nrs, smem, (int)threadIdx.x);
+  gu_tile<B, MT, false, false, true, false, BIAS, true, LIN_WAVES, 2>(a, tb, r_lo, nrs, smem, (int)threadIdx.x);
 }
 
 // ===========================================================================
@@ -992,7 +996,7 @@ static int launch_lin_t(const GUArgs& a, hipStream_t st) {
   if (set_lds_limit_once((const void*)kern, 163840, configured)) return -1;
   const int TM = 16 * MT;
   const size_t lds = gu_lds(a.R_ff, a.Kg, MT);
-  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + TM - 1) / TM * a.H)), dim3(512), lds, st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + TM - 1) / TM * a.H)), dim3(64 * LIN_WAVES), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
