@@ -923,7 +923,7 @@ static int gu_slices(int64_t ntb, int R_ff) {
 bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd) {
   if (B != 16 && B != 32) return false;
   if (Kg != Ku || Kg < 1) return false;               // gate and up stream in lockstep
-  if (Kd > 63) return false;                          // one lane per slot; <= 4 * 64 hit-list entries
+  if (Kd > 64) return false;                          // one lane per slot of a down row
   if (d_model % 128) return false;                    // swizzled panel rows
   const int mt = gu_mt(d_model);
   if (mt == 0 || gu_lds(R_ff, Kg, mt) > 163840 || (int64_t)R_ff * Kg > 512 * GU_CT_MAX) return false;
@@ -1091,7 +1091,8 @@ static int launch_looped_t(const LoopArgs& a, hipStream_t st) {
 // The persistent looped block takes the shapes of the two-kernel path with MT = 4
 // (d_model <= 1024): its LDS holds either the gate/up panel or the two down stages.
 bool looped_persistent_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd) {
-  return split_supported(B, d_model, R_ff, R_m, Kg, Ku, Kd) && gu_mt(d_model) == 4 &&
+  // four down rows per wave: a stage's hit list holds up to 4 * (Kd + 1) <= 256 entries
+  return split_supported(B, d_model, R_ff, R_m, Kg, Ku, Kd) && Kd <= 63 && gu_mt(d_model) == 4 &&
          looped_red_offset<4>(R_ff, Kg) + (size_t)9 * 64 * 4 <= 163840;
 }
 

@@ -168,13 +168,13 @@ def test_swiglu_with_intermediates(gpu, case):
         assert rel <= TOL, f"{name}: rel {rel} abs {ab}"
 
 
-@pytest.mark.parametrize("Kd", [63, 64])
+@pytest.mark.parametrize("Kd", [63, 64, 65])
 @pytest.mark.parametrize("case", [(256, 1024, 16), (128, 512, 16), (1024, 4096, 32)])
 def test_swiglu_duplicate_and_empty_columns(gpu, case, Kd):
     """Rows that name one column block several times sum every copy (as the oracle's
     per-slot sum does); a down row whose slots all fall in the first LDS stage
-    gives that stage a full hit list; empty rows give zeros.  Kd = 63 runs the
-    two-kernel split path, Kd = 64 the row-block path."""
+    gives that stage a full hit list; empty rows give zeros.  Kd <= 64 runs the
+    two-kernel split path, Kd = 65 the row-block path."""
     d_model, d_ff, B = case
     _say(f"swiglu duplicate columns {case} Kd={Kd}")
     rng = np.random.default_rng(21)
