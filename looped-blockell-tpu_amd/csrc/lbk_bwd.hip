@@ -739,40 +739,61 @@ __global__ __launch_bounds__(512) void dw_kernel(DWJobs jobs) {
       for (int v = 0; v < 4; ++v) part[(16 * md + 4 * g + v) * B + 16 * mD + i] = acc[md][mD][v];
 }
 
-// The B = 32 tile gradient with the token slices double-buffered in LDS and filled by direct
-// global->LDS loads (global_load_lds_dwordx4), so slice s + 1 streams in while slice s is
-// multiplied.  The slices are unpadded 64-byte rows whose 16-byte chunk c of row t sits at chunk
-// c ^ ((t & 8) >> 2): the transposed reads of a half-wave (rows t..t+3 and t+8..t+11, two
-// chunks each) then cover all 64 banks once.  A load instruction fills 1 KB (16 rows) in place:
-// lane l of instruction j brings the chunk whose swizzled position is 64 j + l.  The waits are
-// explicit (s_waitcnt vmcnt with the next slice's loads still in flight) and the barriers carry
-// no fence, which would wait for those loads too.
+// The tile gradient (B = 16, 32) with the token slices double-buffered in LDS and filled by
+// direct global->LDS loads (global_load_lds_dwordx4), so slice s + 1 streams in while slice s is
+// multiplied.  The slices are unpadded rows (64 bytes at B = 32, 32 at B = 16), laid out so that
+// the transposed reads of a half-wave (rows t..t+3 and t+8..t+11) cover all 64 banks once:
+// at B = 32 the 16-byte chunk c of row t sits at chunk c ^ ((t & 8) >> 2); at B = 16 (a row is two
+// chunks) row t sits at row slot t ^ ((t & 8) >> 1).  A load instruction fills 1 KB in place: lane
+// l of instruction j brings the chunk whose position is 64 j + l.  The waits are explicit
+// (s_waitcnt vmcnt with the next slice's loads still in flight) and the barriers carry no fence,
+// which would wait for those loads too.
 namespace {
-constexpr int DWD_TS = 64;   // tokens per slice
+template <int B>
+struct DWD {
+  static_assert(B == 16 || B == 32, "tile gradients through LDS loads: B = 16 or 32");
+  static constexpr int TS = B == 32 ? 64 : 128;   // tokens per slice (4 KB of one operand)
+  static constexpr int CPR = B / 8;                // 16-byte chunks per token row
+  // row slot of token row t (B = 16), identity at B = 32
+  __device__ static int slot(int t) { return B == 16 ? (t ^ ((t & 8) >> 1)) : t; }
+  // element offset of (row t, column col) in a slice
+  __device__ static int at(int t, int col) {
+    if constexpr (B == 32) return t * 32 + 8 * ((col >> 3) ^ ((t & 8) >> 2)) + (col & 7);
+    else return slot(t) * 16 + col;
+  }
+  // (token row, chunk) of 16-byte position P of a slice (the inverse of the layout)
+  __device__ static void pos(int P, int& t, int& c) {
+    if constexpr (B == 32) {
+      t = P >> 2;
+      c = (P & 3) ^ ((t & 8) >> 2);
+    } else {
+      t = slot(P >> 1);   // the row permutation is its own inverse
+      c = P & 1;
+    }
+  }
+};
 
-__device__ __forceinline__ int dwd_swz(int row) { return (row & 8) >> 2; }
-
-// transposed operand of a swizzled [64][32] bf16 slice: lane (s, g) gets column c0 + 4 (s & 3) ..
-// + 3 of rows t0 + 8 g + s / 4 and + 4 (as tr_frag on a plain row-major slice)
+// transposed operand of a slice: lane (s, g) gets column c0 + 4 (s & 3) .. + 3 of rows
+// t0 + 8 g + s / 4 and + 4 (as tr_frag on a plain row-major slice)
+template <int B>
 __device__ __forceinline__ u32x4 dwd_frag(const uint16_t* slice, int t0, int c0, int lane) {
   const int s = lane & 15, g = lane >> 4;
   const int row = t0 + 8 * g + (s >> 2);
   const int col = c0 + 4 * (s & 3);
-  const uint16_t* p = slice + row * 32 + 8 * ((col >> 3) ^ dwd_swz(row)) + (col & 7);
   typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
-  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * 32));   // rows + 4: same swizzle
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(slice + DWD<B>::at(row, col)));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(slice + DWD<B>::at(row + 4, col)));
   const u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
   return u32x4{a[0], a[1], b[0], b[1]};
 }
 
-// 1 KB of a slice (instruction j: rows 16 j .. 16 j + 15) from rows t0.. of a [N, ld] matrix,
-// columns col0 .. col0 + 31, rows at or past N read from row N - 1
+// 1 KB of a slice (instruction j) from rows t0.. of a [N, ld] matrix, columns col0 .. col0 + B - 1,
+// rows at or past N read from row N - 1
+template <int B>
 __device__ __forceinline__ void dwd_load(const uint16_t* src, int64_t ld, int64_t col0, int64_t t0, int64_t N,
                                          uint16_t* slice, int j, int lane) {
-  const int P = 64 * j + lane;
-  const int row = P >> 2;
-  const int c = (P & 3) ^ dwd_swz(row);
+  int row, c;
+  DWD<B>::pos(64 * j + lane, row, c);
   const int64_t t = t0 + row < N ? t0 + row : N - 1;
   // issued from inline assembly, so the compiler counts no load of its own here and inserts no
   // wait for these LDS writes before the reads of the other buffer; the kernel waits explicitly
@@ -786,8 +807,9 @@ __device__ __forceinline__ void dwd_load(const uint16_t* src, int64_t ld, int64_
 __device__ __forceinline__ void dwd_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 }  // namespace
 
+template <int B>
 __global__ __launch_bounds__(512) void dw_dma_kernel(DWJobs jobs) {
-  constexpr int B = 32, CW = 2, TS = DWD_TS;
+  constexpr int CW = B / 16, TS = DWD<B>::TS, CPR = DWD<B>::CPR;
   int jt = 0;
 #pragma unroll
   for (int u = 1; u < DWJobs::kMax; ++u)
@@ -825,8 +847,8 @@ __global__ __launch_bounds__(512) void dw_dma_kernel(DWJobs jobs) {
   auto issue = [&](int s, uint16_t* xd, uint16_t* gd) {
     const int64_t t0 = tbeg + (int64_t)s * TS;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dwd_load(J.x, J.ldx, xcol, t0, N, xd, j, lane);
-    if (w < 4) dwd_load(J.gy, J.ldg, gcol, t0, N, gd, w, lane);
+    for (int j = 0; j < 4; ++j) dwd_load<B>(J.x, J.ldx, xcol, t0, N, xd, j, lane);
+    if (w < 4) dwd_load<B>(J.gy, J.ldg, gcol, t0, N, gd, w, lane);
   };
   // slice s from (xb, gb) while slice s + 1 streams into (xn, gn); the loop below passes the
   // buffers as the fixed arrays, so the compiler sees that the reads and the loads in flight
@@ -845,10 +867,16 @@ __global__ __launch_bounds__(512) void dw_dma_kernel(DWJobs jobs) {
     if (t0 + TS > tend) {
       // the last slice of the data: rows at or past tend hold clamped copies; zero them
       const int valid = (int)(tend - t0);
-      for (int q = lane; q < TS * 4; q += 64)
-        if (q / 4 >= valid) *reinterpret_cast<u32x4*>(xb + 8 * q) = u32x4{0, 0, 0, 0};
-      for (int q = tid; q < TS * 4; q += 512)
-        if (q / 4 >= valid) *reinterpret_cast<u32x4*>(gb + 8 * q) = u32x4{0, 0, 0, 0};
+      for (int q = lane; q < TS * CPR; q += 64) {
+        int row, c;
+        DWD<B>::pos(q, row, c);
+        if (row >= valid) *reinterpret_cast<u32x4*>(xb + 8 * q) = u32x4{0, 0, 0, 0};
+      }
+      for (int q = tid; q < TS * CPR; q += 512) {
+        int row, c;
+        DWD<B>::pos(q, row, c);
+        if (row >= valid) *reinterpret_cast<u32x4*>(gb + 8 * q) = u32x4{0, 0, 0, 0};
+      }
       __syncthreads();
     }
     // dW[d][D] += sum_t X[t][d] G[t][D] (operands as in dw_kernel)
@@ -856,10 +884,10 @@ __global__ __launch_bounds__(512) void dw_dma_kernel(DWJobs jobs) {
     for (int ks = 0; ks < TS / 32; ++ks) {
       u32x4 bv[CW];
 #pragma unroll
-      for (int mD = 0; mD < CW; ++mD) bv[mD] = dwd_frag(gb, 32 * ks, 16 * mD, lane);
+      for (int mD = 0; mD < CW; ++mD) bv[mD] = dwd_frag<B>(gb, 32 * ks, 16 * mD, lane);
 #pragma unroll
       for (int md = 0; md < CW; ++md) {
-        const u32x4 av = dwd_frag(xb, 32 * ks, 16 * md, lane);
+        const u32x4 av = dwd_frag<B>(xb, 32 * ks, 16 * md, lane);
 #pragma unroll
         for (int mD = 0; mD < CW; ++mD) acc[md][mD] = mfma_bf16(av, bv[mD], acc[md][mD]);
       }
@@ -916,8 +944,8 @@ int launch_dw(int B, const DWJob* jobs, int n, int64_t N, int chunk, hipStream_t
     rblocks += ((int64_t)jobs[t].R * jobs[t].K * B * B + 255) / 256;
   }
   if (blocks > 0) {
-    if (B == 16) hipLaunchKernelGGL(dw_kernel<16>, dim3((unsigned)blocks), dim3(512), 0, st, J);
-    else if (B == 32) hipLaunchKernelGGL(dw_dma_kernel, dim3((unsigned)blocks), dim3(512), 0, st, J);
+    if (B == 16) hipLaunchKernelGGL(dw_dma_kernel<16>, dim3((unsigned)blocks), dim3(512), 0, st, J);
+    else if (B == 32) hipLaunchKernelGGL(dw_dma_kernel<32>, dim3((unsigned)blocks), dim3(512), 0, st, J);
     else if (B == 64) hipLaunchKernelGGL(dw_kernel<64>, dim3((unsigned)blocks), dim3(512), 0, st, J);
     else return -2;
     if (hipGetLastError() != hipSuccess) return -1;

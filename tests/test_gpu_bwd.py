@@ -44,6 +44,7 @@ BWD_CASES = [
     (256, 1024, 16, 0.25, 100, 0.1),
     (512, 1024, 16, 0.125, 90, 0.05),      # 32 output blocks: dx with 16 waves of two blocks
     (1024, 512, 16, 0.125, 70, 0.0),       # 64 output blocks: 16 waves of four
+    (256, 1024, 16, 0.25, 2100, 0.05),     # B = 16 tile gradients: two token chunks, 128-token slices, ragged tail
     (512, 1024, 32, 0.25, 130, 0.05),
     (128, 512, 64, 0.5, 70, 0.0),
     (1024, 4096, 32, 0.25, 2100, 0.0),     # two token chunks of the tile gradients, ragged tail
