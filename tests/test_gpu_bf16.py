@@ -269,6 +269,42 @@ def test_swiglu_full_headline_sampled_rows(gpu):
     assert np.isfinite(out).all()
 
 
+def test_swiglu_b16_full_size_sampled_rows(gpu):
+    """B = 16 at d_model 1024, d_ff 4096, density 0.25 (64 down slots per row) on 16384 + 5 tokens:
+    one row slice per token block (the 12-wave gate/up kernel), a ragged last block; sampled rows."""
+    rng = np.random.default_rng(1016)
+    d_model, d_ff, B, N = 1024, 4096, 16, 16384 + 5
+    _say("swiglu d1024 ff4096 B16 N16389 full size")
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25, sentinel_frac=0.05)
+    x = T.act(rng, N, d_model)
+    out, *_ = T.abi_swiglu(T.to_gpu_bf16(x), T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d), add_residual=True)
+    out = T.to_np(out)
+    rows = np.concatenate([np.sort(rng.choice(N, 256, replace=False)), [0, N - 1]])
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref, *_ = O.swiglu_fwd(x[rows].astype(np.float64), f64(g), f64(u), f64(d), add_residual=True)
+    rel, ab = T.rel_err(out[rows], ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
+def test_looped_b16_full_size_sampled_rows(gpu):
+    """The looped block (the operator's per-iteration launches) at B = 16 on 16384 tokens, L = 3:
+    the normalising 12-wave gate/up kernel; sampled rows."""
+    rng = np.random.default_rng(1017)
+    d_model, d_ff, B, N, L = 512, 2048, 16, 16384, 3
+    _say("looped L3 d512 ff2048 B16 N16384 full size")
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25)
+    h = T.act(rng, N, d_model)
+    scale = (1.0 + 0.1 * rng.standard_normal(d_model)).astype(np.float32)
+    out = T.to_np(T.abi_looped(T.to_gpu_bf16(h), T.to_gpu(scale), T.gpu_weight(g), T.gpu_weight(u),
+                               T.gpu_weight(d), L, 1e-5))
+    rows = np.sort(rng.choice(N, 128, replace=False))
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref = O.looped_swiglu(h[rows].astype(np.float64), scale.astype(np.float64), f64(g), f64(u), f64(d), L=L,
+                          eps=1e-5)
+    rel, ab = T.rel_err(out[rows], ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
 @pytest.mark.parametrize("shape", [(1024, 4096), (4096, 1024)])
 def test_matmul_full_size_sampled_rows(gpu, shape):
     """The plain product at the headline gate and down shapes, 16384 tokens, through the workspace
