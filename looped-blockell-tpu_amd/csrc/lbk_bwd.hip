@@ -22,9 +22,9 @@
 //                  the SiLU*mul backward (dh -> dg, du) or the optional + dy (-> dx).
 //   dh_panel_kernel  dh -> dg, du when d_model <= 2048: the dy rows of 64 (32)
 //                  tokens sit in LDS as the forward's XOR-swizzled panel and each
-//                  of 8 waves streams the list entries of its column blocks
-//                  (c = w, w + 8, ...): tile rows from global memory, dy
-//                  fragments from the panel.
+//                  of NW waves (8; 16 at B = 16) streams the list entries of its
+//                  column blocks (c = w, w + NW, ...): tile rows from global memory,
+//                  dy fragments from the panel.
 //   dx_stage_kernel  dx when the output blocks fit the waves' accumulators (16
 //                  waves where they fit 128 VGPRs, else 8): the dg and du columns
 //                  of 64 tokens pass through LDS 512 at a time, and a cursor per
@@ -247,8 +247,9 @@ __device__ __forceinline__ uint32_t bpanel_addr(int row, int chunk, int rowb) {
   return (uint32_t)((n * MT + q) * rowb + ((chunk ^ n) << 4));
 }
 
-template <int B, int MT>
-__global__ __launch_bounds__(512, 1) void dh_panel_kernel(TProdArgs a) {
+template <int B, int MT, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void dh_panel_kernel(TProdArgs a) {
+  constexpr int NT = 64 * NW;
   constexpr int CW = B / 16;
   constexpr int NKS = B >= 32 ? B / 32 : 1;
   constexpr int TM = 16 * MT;
@@ -266,12 +267,12 @@ __global__ __launch_bounds__(512, 1) void dh_panel_kernel(TProdArgs a) {
   // ---- panel: dy rows t0 .. t0 + TM - 1, every load at a clamped address
   {
     constexpr int CPR = ROWB / 16;
-    constexpr int PIT = TM * CPR / 512;
+    constexpr int PIT = TM * CPR / NT;
     const int cpr = d_model / 8;
     u32x4 pv[PIT];
 #pragma unroll
     for (int it = 0; it < PIT; ++it) {
-      const int e = tid + 512 * it;
+      const int e = tid + NT * it;
       const int row = e / CPR, cc = e % CPR;
       const int64_t t = t0 + row;
       const bool ok = cc < cpr && t < a.N;
@@ -279,7 +280,7 @@ __global__ __launch_bounds__(512, 1) void dh_panel_kernel(TProdArgs a) {
     }
 #pragma unroll
     for (int it = 0; it < PIT; ++it) {
-      const int e = tid + 512 * it;
+      const int e = tid + NT * it;
       const int row = e / CPR, cc = e % CPR;
       const bool ok = cc < cpr && t0 + row < a.N;
       if (cc < cpr) *reinterpret_cast<u32x4*>(panel + bpanel_addr<MT>(row, cc, ROWB)) = ok ? pv[it] : u32x4{0, 0, 0, 0};
@@ -324,7 +325,7 @@ __global__ __launch_bounds__(512, 1) void dh_panel_kernel(TProdArgs a) {
   typedef uint32_t raw_t __attribute__((ext_vector_type(NV / 2)));
   raw_t graw[MT][NP], uraw[MT][NP];
   auto col_of = [&](int c, int p) { return (int64_t)c * B + (CW == 1 ? 4 * g : 32 * p + 8 * g); };
-  for (int c = sl + a.nsl * w; c < a.C; c += 8 * a.nsl) {
+  for (int c = sl + a.nsl * w; c < a.C; c += NW * a.nsl) {
 #pragma unroll
     for (int q = 0; q < MT; ++q) {
       const int64_t tn = t0 + 16 * q + i;
@@ -388,18 +389,18 @@ __global__ __launch_bounds__(512, 1) void dh_panel_kernel(TProdArgs a) {
 // dh through the LDS panel when the dy rows of 16*MT tokens fit (d_model <= 2048, one source)
 // With fewer token blocks than CUs, the column blocks are split over nsl workgroups per token
 // block (about 256 workgroups, at least one column block per wave), each loading the dy panel.
-template <int B, int MT>
+template <int B, int MT, int NW>
 static int launch_dh_panel_t(const TProdArgs& a0, hipStream_t st) {
   constexpr size_t lds = (size_t)16 * MT * (8192 / MT);
-  auto kern = dh_panel_kernel<B, MT>;
+  auto kern = dh_panel_kernel<B, MT, NW>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)lds) != hipSuccess)
     return -1;
   TProdArgs a = a0;
   const int64_t ntb = (a.N + 16 * MT - 1) / (16 * MT);
-  const int smax = a.C / 8 > 1 ? a.C / 8 : 1;
+  const int smax = a.C / NW > 1 ? a.C / NW : 1;
   a.nsl = ntb >= 256 ? 1 : (int)std::min<int64_t>((256 + ntb - 1) / ntb, smax);
-  hipLaunchKernelGGL(kern, dim3((unsigned)(ntb * a.nsl)), dim3(512), lds, st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(ntb * a.nsl)), dim3(64 * NW), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -407,7 +408,10 @@ static int launch_dh_panel(int B, const TProdArgs& a, hipStream_t st) {
   const int64_t d_model = a.src[0].lda;
   const int mt = d_model <= 1024 ? 4 : (d_model <= 2048 ? 2 : 0);
   if (mt == 0 || d_model % 8) return -2;
-#define LBK_DH(BB, MM) if (B == BB && mt == MM) return launch_dh_panel_t<BB, MM>(a, st);
+  // 16 waves at B = 16 (their registers fit 128 VGPRs): B = 16 backward at d_model 1024, d_ff 4096
+  // 1.93 -> 1.87 ms; at B = 32 16 waves spill (0.739 against 0.715 ms)
+  if (B == 16 && mt == 4) return launch_dh_panel_t<16, 4, 16>(a, st);
+#define LBK_DH(BB, MM) if (B == BB && mt == MM) return launch_dh_panel_t<BB, MM, 8>(a, st);
   LBK_DH(16, 4) LBK_DH(16, 2) LBK_DH(32, 4) LBK_DH(32, 2) LBK_DH(64, 4) LBK_DH(64, 2)
 #undef LBK_DH
   return -2;
