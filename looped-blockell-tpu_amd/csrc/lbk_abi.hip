@@ -561,6 +561,30 @@ static int looped_launches(const uint16_t* h_in, int64_t N, int32_t d_model, con
   if (!a16(workspace)) return LBK_ERR_ALIGN;
   char* ws = static_cast<char*>(workspace);
   uint16_t* h = reinterpret_cast<uint16_t*>(ws + sbytes);
+  if (split && N <= kDecodeMaxTokens && decode_supported(gate->K, up->K, down->K) && a16(down->values) &&
+      pbytes >= align256((size_t)N * d_model * 2)) {
+    // decode-sized token counts: per application the RMSNorm of the fp32 state into bf16 rows
+    // (in the packed weights' part of the workspace, which this path does not use), then the
+    // decode kernels, whose down kernel adds the product to the state
+    float* state = reinterpret_cast<float*>(ws);
+    uint16_t* xn = reinterpret_cast<uint16_t*>(ws + sbytes + hbytes);
+    if (launch_bf16_to_f32(h_in, N * d_model, state, s) != 0) return LBK_ERR_LAUNCH;
+    DecodeArgs a{};
+    a.x = xn; a.N = (int)N; a.d_model = d_model;
+    a.vg = gate->values; a.cg = gate->col_idx; a.Kg = gate->K;
+    a.vu = up->values; a.cu = up->col_idx; a.Ku = up->K;
+    a.R_ff = gate->R;
+    a.vd = down->values; a.cd = down->col_idx; a.Kd = down->K;
+    a.R_m = down->R;
+    a.h = h; a.state = state;
+    a.bg = bs.g; a.bu = bs.u; a.bd = bs.d;
+    for (int l = 0; l < L; ++l) {
+      if (launch_rmsnorm_f32(state, N, d_model, norm_scale, eps, xn, s) != 0) return LBK_ERR_LAUNCH;
+      a.out = l == L - 1 ? h_out : nullptr;
+      if (launch_decode(gate->B, a, s) != 0) return LBK_ERR_LAUNCH;
+    }
+    return LBK_OK;
+  }
   if (split) {
     // fp32 state carried across the L applications; bf16 written once, after the last
     float* state = reinterpret_cast<float*>(ws);

@@ -134,6 +134,37 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
   for (int c = lane; c < d; c += 64) orow[c] = f2bf(bf2f(xr[c]) * rs * scale[c]);
 }
 
+// RMSNorm of fp32 rows into bf16 (the looped block's normalisation on the decode kernels' path):
+// one wave per row; lane l holds columns 8 l + 512 j .. + 7 and sums their squares in the order
+// of the gate/up kernel's normalising panel fill, so both produce the same bf16 rows.
+// d % 8 == 0; x, scale and out 16-byte aligned.
+__global__ __launch_bounds__(256) void rmsnorm_f32_kernel(const float* __restrict__ x, int64_t N, int d,
+                                                          const float* __restrict__ scale, float eps,
+                                                          uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= N) return;
+  const float* xr = x + row * d;
+  float ss = 0.f;
+  for (int col = 8 * lane; col < d; col += 512) {
+    const f32x4 v0 = *reinterpret_cast<const f32x4*>(xr + col), v1 = *reinterpret_cast<const f32x4*>(xr + col + 4);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ss += v0[q] * v0[q];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ss += v1[q] * v1[q];
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  const float rs = 1.0f / sqrtf(ss / (float)d + eps);
+  for (int col = 8 * lane; col < d; col += 512) {
+    const f32x4 v0 = *reinterpret_cast<const f32x4*>(xr + col), v1 = *reinterpret_cast<const f32x4*>(xr + col + 4);
+    const f32x4 s0 = *reinterpret_cast<const f32x4*>(scale + col), s1 = *reinterpret_cast<const f32x4*>(scale + col + 4);
+    *reinterpret_cast<u32x4*>(out + row * d + col) =
+        u32x4{pack2_bf16(v0[0] * rs * s0[0], v0[1] * rs * s0[1]), pack2_bf16(v0[2] * rs * s0[2], v0[3] * rs * s0[3]),
+              pack2_bf16(v1[0] * rs * s1[0], v1[1] * rs * s1[1]), pack2_bf16(v1[2] * rs * s1[2], v1[3] * rs * s1[3])};
+  }
+}
+
 // Backward of out = x * rs * scale, rs = 1 / sqrt(mean(x^2) + eps), per row of length d:
 //   dx     = rs * scale * dy - x * rs^3 * mean(scale * dy * x)
 //   dscale = sum over rows of dy * x * rs
@@ -333,6 +364,14 @@ int launch_rowblock(int B, int mode, const RowblockLaunch& a, hipStream_t st) {
   LBK_RB(64)
 #undef LBK_RB
   return -2;
+}
+
+int launch_rmsnorm_f32(const float* x, int64_t N, int d, const float* scale, float eps, uint16_t* out,
+                       hipStream_t st) {
+  if (N == 0) return 0;
+  if (d % 8) return -2;
+  hipLaunchKernelGGL(rmsnorm_f32_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, x, N, d, scale, eps, out);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_rmsnorm(const uint16_t* x, int64_t N, int d, const float* scale, float eps, uint16_t* out,

@@ -305,9 +305,16 @@ __global__ __launch_bounds__(512, 1) void decode_dn_kernel(DecodeArgs a) {
     for (int v = 0; v < 4; ++v) {
       const int tk = 16 * mt + 4 * (l >> 4) + v;
       if (tk < a.N) {
+        const int64_t idx = (int64_t)tk * a.d_model + col;
         float o = ps[v] + (a.bd ? a.bd[col] : 0.f);
-        if (a.resid) o += bf2f(a.resid[(int64_t)tk * a.d_model + col]);
-        a.out[(int64_t)tk * a.d_model + col] = f2bf(o);
+        if (a.state) {
+          o += a.state[idx];
+          a.state[idx] = o;
+          if (a.out) a.out[idx] = f2bf(o);
+        } else {
+          if (a.resid) o += bf2f(a.resid[idx]);
+          a.out[idx] = f2bf(o);
+        }
       }
     }
   }

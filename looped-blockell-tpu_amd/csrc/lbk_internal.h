@@ -119,12 +119,17 @@ struct DecodeArgs {
   uint16_t* out;             // [N, d_model]
   uint16_t* h;               // [N, d_ff] workspace (or the caller's h)
   const float* bg; const float* bu; const float* bd;   // optional biases
+  float* state;              // optional fp32 [N, d_model]: added to the product and written back
+                             // (resid is then ignored; out, if given, gets the bf16 of the sum)
 };
 bool decode_supported(int Kg, int Ku, int Kd);
 int launch_decode(int B, const DecodeArgs& a, hipStream_t st);
 
 int launch_rmsnorm(const uint16_t* x, int64_t N, int d, const float* scale, float eps, uint16_t* out,
                    hipStream_t st);
+// fp32 rows -> bf16 RMSNorm (d % 8 == 0, 16-byte aligned operands)
+int launch_rmsnorm_f32(const float* x, int64_t N, int d, const float* scale, float eps, uint16_t* out,
+                       hipStream_t st);
 size_t rmsnorm_bwd_bytes(int64_t N, int d);   // fp32 dscale partials of the workgroups
 // fp32 column sums out[C] of a bf16 [N, C] matrix (deterministic: per-64-row partials in part)
 size_t colsum_bytes(int64_t N, int C);

@@ -344,6 +344,9 @@ LOOP_CASES = [
     (1024, 4096, 32, 0.25, 130, 8),       # the looped-block geometry
     (128, 512, 64, 0.5, 40, 2),           # general path (per-iteration launches)
     (2048, 2048, 32, 0.125, 70, 2),       # 64 down rows: 8 row groups per token block
+    (1024, 4096, 32, 0.25, 16, 4),        # <= 64 tokens: RMSNorm of the state + the decode kernels
+    (256, 1024, 16, 0.25, 64, 3),
+    (512, 1024, 32, 0.25, 1, 2),
 ]
 
 
@@ -398,7 +401,7 @@ def test_looped_persistent_matches_two_kernel_path(gpu, case):
     per-iteration gate/up + down launches; its down phase computes the next iteration's RMSNorm
     (per-token sums of squares in another order), so the two agree to bf16 rounding, and both
     are within TOL of the oracle.  With one iteration, or two row groups (norm not fused), they
-    are bit-identical."""
+    are bit-identical above 64 tokens (at most 64, the launches run the decode kernels)."""
     d_model, d_ff, B, dens, N, L, shared = case
     _say(f"looped persistent {case}")
     rng = np.random.default_rng(abs(hash(case)) % 2 ** 31)
@@ -414,7 +417,9 @@ def test_looped_persistent_matches_two_kernel_path(gpu, case):
     two = T.to_np(T.abi_looped(ht, st, *ws, L, 1e-5, launches=True))
     one = T.to_np(T.abi_looped(ht, st, *ws, L, 1e-5, persistent=True))
     assert np.array_equal(two, T.to_np(T.abi_looped(ht, st, *ws, L, 1e-5)))   # the default path
-    if L == 1 or d_model // B > 32:
+    # bit-identical where the launches run the two-kernel path (above 64 tokens; at most 64 they
+    # run the decode kernels, which sum the slots in another order)
+    if (L == 1 or d_model // B > 32) and N > 64:
         assert np.array_equal(one, two)
     else:
         assert T.rel_err(one, two)[0] <= TOL
