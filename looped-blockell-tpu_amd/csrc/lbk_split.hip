@@ -194,16 +194,21 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
   // The weight tile is the A operand and the panel rows the B operand, so an accumulator
   // holds h transposed: lane (n, g) of ag[mt][m] has token 16 mt + n and h columns
   // 8 g + 4 m + v (B = 32, with the gate/up tile packing) or 4 g + v (B = 16), v < 4.
-  auto compute = [&](const GUSlot<B>& S, const AFrags& A) {
+  // FIRST: the row's first position, whose MFMAs start from zero (an inline constant, where
+  // clearing the accumulators would take 64 moves per row at B = 32).
+  auto compute = [&](const GUSlot<B>& S, const AFrags& A, auto first) {
+    constexpr bool FIRST = decltype(first)::value;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int m = 0; m < CW; ++m) ag[mt][m] = mfma_bf16(S.g[0][m], A.g[mt], ag[mt][m]);
+      for (int m = 0; m < CW; ++m) ag[mt][m] = mfma_bf16(S.g[0][m], A.g[mt], FIRST ? z : ag[mt][m]);
     if constexpr (!LIN) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int m = 0; m < CW; ++m) au[mt][m] = mfma_bf16(S.u[0][m], SHARED ? A.g[mt] : A.u[mt], au[mt][m]);
+        for (int m = 0; m < CW; ++m)
+          au[mt][m] = mfma_bf16(S.u[0][m], SHARED ? A.g[mt] : A.u[mt], FIRST ? z : au[mt][m]);
     }
   };
 
@@ -337,30 +342,30 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
   AFrags A0, A1;
   load_a(P[0], A0);
   __builtin_amdgcn_sched_barrier(0);
-  for (int n = 0; n < nrows; ++n) {
+  // one group of RING positions (slot sl holds position sl of the group); the scheduling
+  // barriers keep each slot's use after the previous slot's refill, so the wait before it
+  // covers only that slot's loads
+  auto ring_group = [&](auto first_group) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int m = 0; m < CW; ++m) {
-        ag[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-        au[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int sl = 0; sl < RING; ++sl) {
+      const auto first = std::integral_constant<bool, decltype(first_group)::value>{};
+      const std::integral_constant<bool, false> later{};
+      if (sl % 2 == 0) {
+        load_a(P[(sl + 1) % RING], A1);
+        if (sl == 0) compute(P[sl], A0, first);
+        else compute(P[sl], A0, later);
+      } else {
+        load_a(P[(sl + 1) % RING], A0);
+        compute(P[sl], A1, later);
       }
-    // the scheduling barriers keep each slot's use after the previous slot's
-    // refill, so the wait before it covers only that slot's loads
-    for (int k = 0; k < KP; k += RING) {
-#pragma unroll
-      for (int sl = 0; sl < RING; ++sl) {
-        if (sl % 2 == 0) {
-          load_a(P[(sl + 1) % RING], A1);
-          compute(P[sl], A0);
-        } else {
-          load_a(P[(sl + 1) % RING], A0);
-          compute(P[sl], A1);
-        }
-        fetch(P[sl]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      fetch(P[sl]);
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  for (int n = 0; n < nrows; ++n) {
+    // a row takes KP >= RING positions, so its first group always exists
+    ring_group(std::true_type{});
+    for (int k = RING; k < KP; k += RING) ring_group(std::false_type{});
     // epilogue of row r: h = silu(g) * u (and the pre-activations); each lane stores the
     // 4 * CW consecutive columns it holds of one token with one store
     const int r = r_lo + w + NW * n;
