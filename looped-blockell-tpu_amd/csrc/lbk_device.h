@@ -51,6 +51,15 @@ __device__ __forceinline__ f32x4 mfma_bf16(const u32x4& a, const u32x4& b, const
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
+// 16x16x16 bf16: lane (n, q), n = lane % 16, q = lane / 16, holds k = 4q .. 4q + 3 (8 bytes) of
+// row n of A and column n of B; D has the layout of the 16x16x32 form.  A B = 16 tile's K fits
+// exactly, with no zero half to mask.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f32x4 mfma_bf16_k16(const u32x2& a, const u32x2& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a),
+                                                   __builtin_bit_cast(s16x4_t, b), c, 0, 0, 0);
+}
+
 // int8 MFMAs: 16x16x64 (16 bytes of K per lane) and 16x16x32 (8 bytes).
 __device__ __forceinline__ i32x4 mfma_i8_k64(const i32x4& a, const i32x4& b, const i32x4& c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -161,6 +170,16 @@ struct PackedTile {
   static constexpr int LANES = B == 16 ? 32 : 64;                       // lanes stored per tile
   static constexpr int U32X4 = LANES * CHUNKS;                          // chunks per tile
 };
+
+// Byte offset, within a packed B = 16 tile, of the 8-byte 16x16x16 fragment of `lane`: stored
+// lane l' (row l' % 16, k = 8 (l' / 16) .. + 7) holds k = 4q .. 4q + 3 of row n at byte
+// 16 l' + 8 (q & 1), l' = n + 16 (q >> 1).
+__device__ __forceinline__ uint32_t pfrag16_off(int lane) {
+  return (uint32_t)((lane & 15) * 16 + (lane >> 5) * 256 + ((lane >> 4) & 1) * 8);
+}
+__device__ __forceinline__ u32x2 load_pfrag16(const u32x4* __restrict__ tile, uint32_t off) {
+  return *reinterpret_cast<const u32x2*>(reinterpret_cast<const unsigned char*>(tile) + off);
+}
 
 template <int B>
 __device__ __forceinline__ void load_pfrag(const u32x4* __restrict__ tile, int lane,

@@ -56,6 +56,21 @@ struct GUSlot {
   u32x4 g[1][TileShape<B>::CW], u[1][TileShape<B>::CW];
   int cg, cu;
 };
+// B = 16: the 8-byte fragments of the 16x16x16 form
+template <>
+struct GUSlot<16> {
+  u32x2 g, u;
+  int cg, cu;
+};
+
+__device__ __forceinline__ u32x2 lds8(const unsigned char* base, uint32_t off) {
+  return *reinterpret_cast<const u32x2*>(base + off);
+}
+// panel byte address of lane (i, g)'s 16x16x16 B = 16 fragment of column block cb (k = 4g .. 4g + 3
+// of the block: 16-byte chunk 2 cb + g / 2, its half g & 1)
+__device__ __forceinline__ uint32_t k16_addr(uint32_t lbase, int cb, int g, int i) {
+  return lbase + ((uint32_t)(((cb * 2 + (g >> 1)) ^ i) << 4) | (uint32_t)((g & 1) << 3));
+}
 
 // gate/up ring depth (positions in flight + 1)
 constexpr int GU_RING = 4;
@@ -137,12 +152,18 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
 
   int rn = 0, rk = 0;   // next position to fetch
   // weight loads of the next position (the column table is not needed yet)
+  const uint32_t f16 = pfrag16_off(lane);
   auto fetch_w = [&](GUSlot<B>& S) {
     const bool live = rn < nrows && rk < K;
     const int el = (w + NW * rn) * K + rk;   // entry of the slice's column table
     const int64_t e = live ? cbase + el : ztile;
-    load_pfrag<B>(pg + e * PackedTile<B>::U32X4, lane, S.g);
-    if constexpr (!LIN) load_pfrag<B>(pu + e * PackedTile<B>::U32X4, lane, S.u);
+    if constexpr (B == 16) {
+      S.g = load_pfrag16(pg + e * PackedTile<B>::U32X4, f16);
+      if constexpr (!LIN) S.u = load_pfrag16(pu + e * PackedTile<B>::U32X4, f16);
+    } else {
+      load_pfrag<B>(pg + e * PackedTile<B>::U32X4, lane, S.g);
+      if constexpr (!LIN) load_pfrag<B>(pu + e * PackedTile<B>::U32X4, lane, S.u);
+    }
     S.cg = live ? el : -1;   // table entry until fetch_c replaces it by columns
   };
   auto fetch_c = [&](GUSlot<B>& S) {
@@ -178,17 +199,27 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
   f32x4 ag[MT][CW], au[MT][CW];
   // A fragments of a position's gate and up column blocks (shared topology: gate and up
   // read the same column list, so one panel read feeds both products)
+  using AF = std::conditional_t<B == 16, u32x2, u32x4>;
   struct AFrags {
-    u32x4 g[MT], u[SHARED ? 1 : MT];
+    AF g[MT], u[SHARED ? 1 : MT];
   };
   auto load_a = [&](const GUSlot<B>& S, AFrags& A) {
     const int cg = uniform(S.cg), cu = uniform(S.cu);
-    const uint32_t ag0 = lbase + (((cg * (B / 8) + g) ^ i) << 4);
-    const uint32_t au0 = lbase + (((cu * (B / 8) + g) ^ i) << 4);
+    if constexpr (B == 16) {
+      const uint32_t ag0 = k16_addr(lbase, cg, g, i), au0 = k16_addr(lbase, cu, g, i);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      A.g[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(smem, ag0 + mt * ROWB);
-      if constexpr (!SHARED) A.u[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(smem, au0 + mt * ROWB);
+      for (int mt = 0; mt < MT; ++mt) {
+        A.g[mt] = lds8(smem, ag0 + mt * ROWB);
+        if constexpr (!SHARED) A.u[mt] = lds8(smem, au0 + mt * ROWB);
+      }
+    } else {
+      const uint32_t ag0 = lbase + (((cg * (B / 8) + g) ^ i) << 4);
+      const uint32_t au0 = lbase + (((cu * (B / 8) + g) ^ i) << 4);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        A.g[mt] = lds16(smem, ag0 + mt * ROWB);
+        if constexpr (!SHARED) A.u[mt] = lds16(smem, au0 + mt * ROWB);
+      }
     }
   };
   // The weight tile is the A operand and the panel rows the B operand, so an accumulator
@@ -199,16 +230,24 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
   auto compute = [&](const GUSlot<B>& S, const AFrags& A, auto first) {
     constexpr bool FIRST = decltype(first)::value;
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (B == 16) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int m = 0; m < CW; ++m) ag[mt][m] = mfma_bf16(S.g[0][m], A.g[mt], FIRST ? z : ag[mt][m]);
-    if constexpr (!LIN) {
+      for (int mt = 0; mt < MT; ++mt) {
+        ag[mt][0] = mfma_bf16_k16(S.g, A.g[mt], FIRST ? z : ag[mt][0]);
+        if constexpr (!LIN) au[mt][0] = mfma_bf16_k16(S.u, SHARED ? A.g[mt] : A.u[mt], FIRST ? z : au[mt][0]);
+      }
+    } else {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int m = 0; m < CW; ++m)
-          au[mt][m] = mfma_bf16(S.u[0][m], SHARED ? A.g[mt] : A.u[mt], FIRST ? z : au[mt][m]);
+        for (int m = 0; m < CW; ++m) ag[mt][m] = mfma_bf16(S.g[0][m], A.g[mt], FIRST ? z : ag[mt][m]);
+      if constexpr (!LIN) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int m = 0; m < CW; ++m)
+            au[mt][m] = mfma_bf16(S.u[0][m], SHARED ? A.g[mt] : A.u[mt], FIRST ? z : au[mt][m]);
+      }
     }
   };
 
@@ -619,9 +658,10 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
 
   // ring slots: weight fragments and column block
   struct Slot {
-    u32x4 f[1][CW];
+    std::conditional_t<B == 16, u32x2, u32x4> f[1][CW];   // B = 16: 16x16x16 fragments
     int cb;
   };
+  const uint32_t f16 = pfrag16_off(lane);
   FetchList<RPW> cur, nxt;
   // position q of the stream made of the current stage's list followed by the
   // next stage's; beyond both, the zero tile
@@ -629,21 +669,30 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
     int d = ztile << 6;
     if (q < cur.tot) d = list_get(cur.v, q);
     else if (q - cur.tot < nxt.tot) d = list_get(nxt.v, q - cur.tot);
-    load_pfrag<B>(pd + (int64_t)(d >> 6) * PackedTile<B>::U32X4, lane, S.f);
+    if constexpr (B == 16) S.f[0][0] = load_pfrag16(pd + (int64_t)(d >> 6) * PackedTile<B>::U32X4, f16);
+    else load_pfrag<B>(pd + (int64_t)(d >> 6) * PackedTile<B>::U32X4, lane, S.f);
     S.cb = d & 63;
   };
   const uint32_t lbase = (uint32_t)(i * MT * SROWB);
   auto compute = [&](const Slot& S, const unsigned char* sb, f32x4 (&ac)[MT][CW]) {
     const int cb = uniform(S.cb);
-    const uint32_t a0 = lbase + (((cb * (B / 8) + g) ^ i) << 4);
-    u32x4 av[MT];
+    if constexpr (B == 16) {
+      const uint32_t a0 = k16_addr(lbase, cb, g, i);
+      u32x2 av[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      av[mt] = (B == 16 && g >= 2) ? u32x4{0, 0, 0, 0} : lds16(sb, a0 + mt * SROWB);
+      for (int mt = 0; mt < MT; ++mt) av[mt] = lds8(sb, a0 + mt * SROWB);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt) ac[mt][0] = mfma_bf16_k16(av[mt], S.f[0][0], ac[mt][0]);
+    } else {
+      const uint32_t a0 = lbase + (((cb * (B / 8) + g) ^ i) << 4);
+      u32x4 av[MT];
 #pragma unroll
-      for (int m = 0; m < CW; ++m) ac[mt][m] = mfma_bf16(av[mt], S.f[0][m], ac[mt][m]);
+      for (int mt = 0; mt < MT; ++mt) av[mt] = lds16(sb, a0 + mt * SROWB);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int m = 0; m < CW; ++m) ac[mt][m] = mfma_bf16(av[mt], S.f[0][m], ac[mt][m]);
+    }
   };
 
   const bool any_rows = (row0 + w * RPW < a.R_m) && a.Kd > 0;
