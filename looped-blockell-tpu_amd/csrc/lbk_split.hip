@@ -3,13 +3,14 @@
 // gu_kernel<B, MT, NORM, INTER>: a workgroup owns 16*MT tokens.  Their input
 // rows sit in LDS as an XOR-swizzled panel (optionally RMSNorm-ed on the way in
 // from an fp32 state), next to a table of the gate/up column indices.  Eight
-// waves (two per SIMD; twelve with a shallower ring, gu_kernel_w12, at B = 32 with distinct
-// gate/up topologies, no exports and no biases) each stream their own d_ff block rows (r = w,
-// w+8, ...):
+// waves (two per SIMD; gu_kernel_w12, for distinct gate/up topologies with no exports and no
+// biases, runs twelve with a shallower ring at B = 32 and sixteen at B = 16) each stream their
+// own d_ff block rows (r = w, w+8, ...):
 // gate and up tiles are consumed in (gate k, up k) pairs from a GU_RING-deep
 // register ring that runs across row boundaries.  The weight tile is the A
 // operand of the MFMA, so the accumulators hold h transposed and every lane
-// stores 8 (B = 32) or 4 (B = 16) consecutive columns of one token at once.  Weights come pre-packed in
+// stores 8 (B = 32) or 4 (B = 16) consecutive columns of one token at once.  B = 16 uses the
+// 16x16x16 MFMA (a 16-deep tile fills its K), B = 32 the 16x16x32 one.  Weights come pre-packed in
 // fragment-major order (two dwordx4 loads per lane per B = 32 tile); every
 // position issues the same loads (padding and dead slots read the packed zero
 // tile), so the compiler's memory-counter waits stay exact.  h = silu(g) * u is
@@ -468,14 +469,15 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
 // gate/up with distinct gate/up topologies, without exported pre-activations or biases, one row
 // slice, with 12 waves and a 2-deep
 // ring: at most 168 VGPRs fit three waves per SIMD, and the extra waves hide more of the
-// panel-read and weight-load latency than the shallower ring gives up
-// (B = 16, with half the accumulators, keeps a 4-deep ring: forward at d_model 1024, d_ff 4096,
-// 25 %, 16384 tokens 0.328 -> 0.302 ms; 16 waves with a 2-deep ring spilled 4 VGPRs for 0.300)
+// panel-read and weight-load latency than the shallower ring gives up.  B = 16, with a quarter
+// of the accumulators and 8-byte fragments (113 VGPRs), runs 16 waves with a 4-deep ring
+// (forward at d_model 1024, d_ff 4096, 25 %, 16384 tokens: 0.2490 ms with 12 waves, 0.2467 with 16).
+template <int B> constexpr int gu_w12_waves() { return B == 16 ? 16 : 12; }
 template <int B, int MT, bool NORM>
-__global__ __launch_bounds__(768, 1) void gu_kernel_w12(GUArgs a) {
+__global__ __launch_bounds__(64 * gu_w12_waves<B>(), 1) void gu_kernel_w12(GUArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  gu_tile<B, MT, NORM, false, false, false, false, false, 12, B == 16 ? 4 : 2>(a, (int64_t)blockIdx.x, 0, a.R_ff,
-                                                                               smem, (int)threadIdx.x);
+  gu_tile<B, MT, NORM, false, false, false, false, false, gu_w12_waves<B>(), B == 16 ? 4 : 2>(
+      a, (int64_t)blockIdx.x, 0, a.R_ff, smem, (int)threadIdx.x);
 }
 
 // plain Block-ELL product y = x W (+ bias) over an LDS panel of x (the gate/up kernel's gate
@@ -1004,7 +1006,8 @@ static int launch_gu_w12(const GUArgs& a, hipStream_t st) {
   auto kern = gu_kernel_w12<B, MT, NORM>;
   static std::atomic<uint64_t> configured{0};
   if (set_lds_limit_once((const void*)kern, 163840, configured)) return -1;
-  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 16 * MT - 1) / (16 * MT))), dim3(768), gu_lds(a.R_ff, a.Kg, MT), st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 16 * MT - 1) / (16 * MT))), dim3(64 * gu_w12_waves<B>()),
+                     gu_lds(a.R_ff, a.Kg, MT), st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
