@@ -293,19 +293,32 @@ __global__ __launch_bounds__(64 * NW, 1) void dh_panel_kernel(TProdArgs a) {
   const uint32_t lbase = (uint32_t)(i * MT * ROWB);
   struct Ent {
     u32x4 av[NKS][CW];
+    u32x2 a16;   // B = 16: the 16x16x16 fragment (tile row i, k = 4g .. 4g + 3)
     int r;
   };
   auto load = [&](int e, Ent& E) {
-    const uint16_t* tile = S.w + (int64_t)e * B * B + 8 * gk;
+    if constexpr (B == 16) {
+      E.a16 = *reinterpret_cast<const u32x2*>(S.w + (int64_t)e * B * B + i * B + 4 * g);
+    } else {
+      const uint16_t* tile = S.w + (int64_t)e * B * B + 8 * gk;
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks)
+      for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-      for (int m = 0; m < CW; ++m) E.av[ks][m] = ld16(tile + op_row<CW>(i, m) * B + 32 * ks);
+        for (int m = 0; m < CW; ++m) E.av[ks][m] = ld16(tile + op_row<CW>(i, m) * B + 32 * ks);
+    }
     E.r = e / S.K;
   };
   f32x4 acc[MT][CW];
   auto compute = [&](const Ent& E) {
     const int r = uniform(E.r);
+    if constexpr (B == 16) {
+      // dy[16q + i][16r + 4g ..]: 16-byte chunk 2r + g / 2 of the swizzled row, its half g & 1
+      const uint32_t pa = lbase + ((uint32_t)(((r * 2 + (g >> 1)) ^ i) << 4) | (uint32_t)((g & 1) << 3));
+#pragma unroll
+      for (int q = 0; q < MT; ++q)
+        acc[q][0] = mfma_bf16_k16(E.a16, *reinterpret_cast<const u32x2*>(panel + pa + q * ROWB), acc[q][0]);
+      return;
+    }
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
       const uint32_t pa = lbase + ((((r * (B / 8) + 4 * ks + gk)) ^ i) << 4);
@@ -491,6 +504,7 @@ __global__ __launch_bounds__(64 * NW, 1) void dx_stage_kernel(TProdArgs a) {
 
   struct Ent {
     u32x4 av[NKS][CW];
+    u32x2 a16;                                       // B = 16: the 16x16x16 fragment
     int r;                                           // source column block
   };
   const uint32_t lbase = (uint32_t)(i * MT * SROWB);
@@ -519,11 +533,15 @@ __global__ __launch_bounds__(64 * NW, 1) void dx_stage_kernel(TProdArgs a) {
     const unsigned char* sb = stg + (s & 1) * SBYTES;
     const int rlo = st * G, rhi = rlo + G;           // source column blocks of this stage
     auto load = [&](int e, Ent& E) {
-      const uint16_t* tile = S.w + (int64_t)e * B * B + 8 * gk;
+      if constexpr (B == 16) {
+        E.a16 = *reinterpret_cast<const u32x2*>(S.w + (int64_t)e * B * B + i * B + 4 * g);
+      } else {
+        const uint16_t* tile = S.w + (int64_t)e * B * B + 8 * gk;
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks)
+        for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-        for (int m = 0; m < CW; ++m) E.av[ks][m] = ld16(tile + op_row<CW>(i, m) * B + 32 * ks);
+          for (int m = 0; m < CW; ++m) E.av[ks][m] = ld16(tile + op_row<CW>(i, m) * B + 32 * ks);
+      }
       E.r = e / S.K;
     };
 #pragma unroll
@@ -532,6 +550,13 @@ __global__ __launch_bounds__(64 * NW, 1) void dx_stage_kernel(TProdArgs a) {
       if (c >= a.C) continue;
       auto compute = [&](const Ent& E) {
         const int rb = uniform(E.r) - rlo;           // column block within the stage
+        if constexpr (B == 16) {
+          const uint32_t pa = lbase + ((uint32_t)(((rb * 2 + (g >> 1)) ^ i) << 4) | (uint32_t)((g & 1) << 3));
+#pragma unroll
+          for (int q = 0; q < MT; ++q)
+            acc[o][q][0] = mfma_bf16_k16(E.a16, *reinterpret_cast<const u32x2*>(sb + pa + q * SROWB), acc[o][q][0]);
+          return;
+        }
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
           const uint32_t pa = lbase + (((rb * (B / 8) + 4 * ks + gk) ^ i) << 4);
