@@ -473,10 +473,11 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
 // of the accumulators and 8-byte fragments (113 VGPRs), runs 16 waves with a 4-deep ring
 // (forward at d_model 1024, d_ff 4096, 25 %, 16384 tokens: 0.2490 ms with 12 waves, 0.2467 with 16).
 template <int B> constexpr int gu_w12_waves() { return B == 16 ? 16 : 12; }
-template <int B, int MT, bool NORM>
+// (B = 16 also takes shared topologies and biases here, within the same 128 VGPRs)
+template <int B, int MT, bool NORM, bool SHARED = false, bool BIAS = false>
 __global__ __launch_bounds__(64 * gu_w12_waves<B>(), 1) void gu_kernel_w12(GUArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  gu_tile<B, MT, NORM, false, false, false, false, false, gu_w12_waves<B>(), B == 16 ? 4 : 2>(
+  gu_tile<B, MT, NORM, false, SHARED, false, BIAS, false, gu_w12_waves<B>(), B == 16 ? 4 : 2>(
       a, (int64_t)blockIdx.x, 0, a.R_ff, smem, (int)threadIdx.x);
 }
 
@@ -1001,9 +1002,9 @@ static int launch_gu_b(const GUArgs& a, hipStream_t st) {
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-template <int B, int MT, bool NORM>
+template <int B, int MT, bool NORM, bool SHARED = false, bool BIAS = false>
 static int launch_gu_w12(const GUArgs& a, hipStream_t st) {
-  auto kern = gu_kernel_w12<B, MT, NORM>;
+  auto kern = gu_kernel_w12<B, MT, NORM, SHARED, BIAS>;
   static std::atomic<uint64_t> configured{0};
   if (set_lds_limit_once((const void*)kern, 163840, configured)) return -1;
   hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 16 * MT - 1) / (16 * MT))), dim3(64 * gu_w12_waves<B>()),
@@ -1034,8 +1035,19 @@ int launch_gu(int B, bool norm, const GUArgs& a0, hipStream_t st) {
   // fast or faster, 0.1378 against 0.1381-0.1429 ms)
   if (B == 32 && mt == 4 && a.H == 1 && !inter && !shared && !a.bg && !a.bu)
     return norm ? launch_gu_w12<32, 4, true>(a, st) : launch_gu_w12<32, 4, false>(a, st);
-  if (B == 16 && mt == 4 && a.H == 1 && !inter && !shared && !a.bg && !a.bu)
-    return norm ? launch_gu_w12<16, 4, true>(a, st) : launch_gu_w12<16, 4, false>(a, st);
+  if (B == 16 && mt == 4 && a.H == 1 && !inter) {
+    const int sel = (norm ? 4 : 0) | (shared ? 2 : 0) | ((a.bg || a.bu) ? 1 : 0);
+    switch (sel) {
+      case 0: return launch_gu_w12<16, 4, false, false, false>(a, st);
+      case 1: return launch_gu_w12<16, 4, false, false, true>(a, st);
+      case 2: return launch_gu_w12<16, 4, false, true, false>(a, st);
+      case 3: return launch_gu_w12<16, 4, false, true, true>(a, st);
+      case 4: return launch_gu_w12<16, 4, true, false, false>(a, st);
+      case 5: return launch_gu_w12<16, 4, true, false, true>(a, st);
+      case 6: return launch_gu_w12<16, 4, true, true, false>(a, st);
+      default: return launch_gu_w12<16, 4, true, true, true>(a, st);
+    }
+  }
 #define LBK_GU2(BB, MM, SH)                                                                          \
   if (norm) return launch_gu_t<BB, MM, true, false, SH>(a, st);                                     \
   return inter ? launch_gu_t<BB, MM, false, true, SH>(a, st) : launch_gu_t<BB, MM, false, false, SH>(a, st);
