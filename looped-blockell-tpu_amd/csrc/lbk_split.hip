@@ -1035,6 +1035,8 @@ int launch_gu(int B, bool norm, const GUArgs& a0, hipStream_t st) {
   // fast or faster, 0.1378 against 0.1381-0.1429 ms)
   if (B == 32 && mt == 4 && a.H == 1 && !inter && !shared && !a.bg && !a.bu)
     return norm ? launch_gu_w12<32, 4, true>(a, st) : launch_gu_w12<32, 4, false>(a, st);
+  // B = 16 with one row slice and no exports: 16 waves for every topology and bias combination
+  // (at most 113 VGPRs; reference-default layer forward 0.2615 -> 0.2408 ms against 8 waves)
   if (B == 16 && mt == 4 && a.H == 1 && !inter) {
     const int sel = (norm ? 4 : 0) | (shared ? 2 : 0) | ((a.bg || a.bu) ? 1 : 0);
     switch (sel) {
