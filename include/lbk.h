@@ -4,8 +4,10 @@
  * Everything here is plain C: pointers, sizes, status codes.  No torch types.
  * The library never allocates, frees or synchronises: callers own every buffer
  * (inputs, outputs, workspace) and pass the HIP stream the work is queued on.
- * Entry points are reentrant and keep no global state; a workspace buffer may
- * be shared by calls only if those calls do not overlap in time.
+ * Entry points are reentrant and keep no global state, with one exception:
+ * lbk_swiglu_fwd_bf16_noalloc works in a fixed device array per GPU (below), so
+ * its calls that overlap in time on one GPU race.  A workspace buffer may be
+ * shared by calls only if those calls do not overlap in time.
  *
  * Block-ELL layout (reference looped_blockell/layers/block_ell.py:1-8, :53-66):
  *   values      [R, K, B, B]  bf16; tile values[r, k] is [B_in, B_out]
@@ -138,6 +140,18 @@ int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model,
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Which kernels lbk_swiglu_fwd_bf16 (and its biased and prepacked forms) runs for a geometry:
+ * LBK_PATH_DECODE (N <= 64 tokens: the decode pair), LBK_PATH_SPLIT (the two-kernel gate/up +
+ * down path on packed tiles), LBK_PATH_ROWBLOCK (the general row-block kernels), or
+ * LBK_PATH_NONE for N <= 0 or an invalid geometry.  want_intermediates as for
+ * lbk_swiglu_workspace_bytes.  A query only (no launch); no counterpart in the reference, for
+ * callers and tests that need to know which kernels serve a shape.
+ */
+enum lbk_path { LBK_PATH_NONE = 0, LBK_PATH_DECODE = 1, LBK_PATH_SPLIT = 2, LBK_PATH_ROWBLOCK = 3 };
+int lbk_swiglu_forward_path(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
+                            const lbk_bell* down, int want_intermediates);
+
+/*
  * lbk_swiglu_fwd_bf16 (no optional outputs) for callers that cannot allocate: code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc.  No counterpart in the
  * reference.  Instead of a workspace it uses a fixed array of LBK_NOALLOC_SCRATCH_BYTES (4 MiB)
@@ -147,8 +161,15 @@ int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model,
  * anything: decode shapes fit (16 tokens at d_ff = 14336 need 459 KB).  All calls on one GPU
  * share its array: calls that overlap in time on one GPU race.  Same kernels, same results as
  * lbk_swiglu_fwd_bf16.
+ *
+ * lbk_noalloc_init looks up the device address of the current device's array (once per
+ * device; later calls return at once).  The first lbk_swiglu_fwd_bf16_noalloc call on a device
+ * does it too, but a caller about to capture a HIP graph calls lbk_noalloc_init (and makes one
+ * eager call of each geometry, which sets the kernels' LDS limits) before the capture, so that
+ * the captured call makes no runtime lookups.  The captured call records kernel launches only.
  */
 size_t lbk_noalloc_scratch_bytes(void);
+int lbk_noalloc_init(void);
 int lbk_swiglu_fwd_bf16_noalloc(const uint16_t* x, int64_t N, int32_t d_model,
                                 const lbk_bell* gate, const lbk_bell* up, const lbk_bell* down,
                                 int add_residual, uint16_t* out, void* stream);

@@ -311,6 +311,16 @@ size_t lbk_swiglu_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* ga
   return b;
 }
 
+int lbk_swiglu_forward_path(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
+                            const lbk_bell* down, int want_intermediates) {
+  if (!gate || !up || !down || N <= 0) return LBK_PATH_NONE;
+  if (check_bell(gate) || check_bell(up) || check_bell(down)) return LBK_PATH_NONE;
+  int64_t d_ff = 0;
+  if (check_ffn(gate, up, down, d_model, &d_ff)) return LBK_PATH_NONE;
+  if (use_decode(N, gate, up, down, want_intermediates != 0)) return LBK_PATH_DECODE;
+  return use_split(gate, up, down, d_model) ? LBK_PATH_SPLIT : LBK_PATH_ROWBLOCK;
+}
+
 int lbk_swiglu_fwd_bf16(const uint16_t* x, int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
                         const lbk_bell* down, int add_residual, uint16_t* out, uint16_t* h_out,
                         uint16_t* gate_pre_out, uint16_t* up_out, void* workspace, size_t workspace_bytes,

@@ -51,6 +51,11 @@ extern "C" {
 
 size_t lbk_noalloc_scratch_bytes(void) { return (size_t)LBK_NOALLOC_SCRATCH_BYTES; }
 
+int lbk_noalloc_init(void) {
+  void* ws = nullptr;
+  return scratch_address(&ws);
+}
+
 int lbk_swiglu_fwd_bf16_noalloc(const uint16_t* x, int64_t N, int32_t d_model, const lbk_bell* gate,
                                 const lbk_bell* up, const lbk_bell* down, int add_residual, uint16_t* out,
                                 void* stream) {

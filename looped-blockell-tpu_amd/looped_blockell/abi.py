@@ -82,6 +82,8 @@ SIGNATURES = {
     "lbk_swiglu_workspace_bytes": (_SZ, [_I64, _I32, _PB, _PB, _PB, C.c_int]),
     "lbk_swiglu_fwd_bf16": (C.c_int, [_P, _I64, _I32, _PB, _PB, _PB, C.c_int, _P, _P, _P, _P, _P, _SZ, _P]),
     "lbk_noalloc_scratch_bytes": (_SZ, []),
+    "lbk_noalloc_init": (C.c_int, []),
+    "lbk_swiglu_forward_path": (C.c_int, [_I64, _I32, _PB, _PB, _PB, C.c_int]),
     "lbk_swiglu_fwd_bf16_noalloc": (C.c_int, [_P, _I64, _I32, _PB, _PB, _PB, C.c_int, _P, _P]),
     "lbk_swiglu_fwd_bias_bf16": (C.c_int, [_P, _I64, _I32, _PB, _PB, _PB, _P, _P, _P, C.c_int, _P, _P, _P, _P, _P,
                                            _SZ, _P]),

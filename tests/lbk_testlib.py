@@ -137,6 +137,18 @@ def abi_matmul_ws(x_t, w_t, bias_t=None):
     return y, wsb
 
 
+PATHS = {0: "none", 1: "decode", 2: "split", 3: "rowblock"}
+
+
+def swiglu_path(N, d_model, g_t, u_t, d_t, intermediates=False):
+    """Which kernels lbk_swiglu_fwd_bf16 runs for this geometry: "decode", "split" (two-kernel
+    gate/up + down), "rowblock", or "none" (lbk_swiglu_forward_path)."""
+    A = abi()
+    gb, ub, db = bell_struct(*g_t), bell_struct(*u_t), bell_struct(*d_t)
+    return PATHS[A.load().lbk_swiglu_forward_path(N, d_model, C.byref(gb), C.byref(ub), C.byref(db),
+                                                  1 if intermediates else 0)]
+
+
 def abi_swiglu(x_t, g_t, u_t, d_t, add_residual=False, intermediates=False):
     import torch
     A = abi()

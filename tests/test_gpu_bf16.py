@@ -95,28 +95,31 @@ def test_matmul_out_of_range_column_is_skipped(gpu):
 
 
 SWIGLU_CASES = [
-    # (d_model, d_ff, B, density, N, sentinel_frac)   panel path unless noted
-    (256, 1024, 16, 0.25, 512, 0.0),      # the small CPU-runnable geometry
-    (256, 1024, 16, 0.25, 77, 0.1),       # ragged N, dead slots
-    (512, 1024, 32, 0.25, 130, 0.0),
-    (512, 256, 32, 0.5, 90, 0.1),         # 8 h rows: fewer than the 12 gate/up waves
-    (256, 1408, 32, 0.25, 100, 0.05),     # 44 h rows in 5 uneven row slices (few token blocks)
-    (1024, 4096, 32, 0.25, 200, 0.05),    # the headline geometry, small N
-    (128, 512, 64, 0.5, 70, 0.0),         # B = 64 -> general two-kernel path
-    (2048, 1024, 32, 0.125, 40, 0.0),     # d_model > 1024: 32-token gate/up panels, 64 down rows
-    (2048, 2048, 16, 0.125, 100, 0.05),   # 128 down rows: 16 row groups per token block
+    # (d_model, d_ff, B, density, N, sentinel_frac, kernels the library picks)
+    (256, 1024, 16, 0.25, 512, 0.0, "split"),      # the small CPU-runnable geometry
+    (256, 1024, 16, 0.25, 77, 0.1, "split"),       # ragged N, dead slots
+    (512, 1024, 32, 0.25, 130, 0.0, "split"),
+    (512, 256, 32, 0.5, 90, 0.1, "split"),         # 8 h rows: fewer than the 12 gate/up waves
+    (256, 1408, 32, 0.25, 100, 0.05, "split"),     # 44 h rows in 5 uneven row slices (few token blocks)
+    (1024, 4096, 32, 0.25, 200, 0.05, "split"),    # the headline geometry, small N
+    (128, 512, 64, 0.5, 70, 0.0, "rowblock"),      # B = 64 -> general row-block kernels
+    (2048, 1024, 32, 0.125, 40, 0.0, "decode"),    # d_model > 1024 at decode size
+    (2048, 1024, 32, 0.125, 100, 0.0, "split"),    # d_model > 1024: 32-token gate/up panels, 64 down rows
+    (2048, 2048, 16, 0.125, 100, 0.05, "split"),   # 128 down rows: 16 row groups per token block
 ]
 
 
 @pytest.mark.parametrize("case", SWIGLU_CASES)
 @pytest.mark.parametrize("resid", [False, True])
 def test_swiglu_parity(gpu, case, resid):
-    d_model, d_ff, B, dens, N, sf = case
+    d_model, d_ff, B, dens, N, sf, path = case
     _say(f"swiglu {case} resid={resid}")
-    rng = np.random.default_rng(hash(case) % 2 ** 31)
+    rng = np.random.default_rng(hash(case[:6]) % 2 ** 31)
     g, u, d = T.ffn_weights(rng, d_model, d_ff, B, dens, sentinel_frac=sf)
     x = T.act(rng, N, d_model)
-    out, *_ = T.abi_swiglu(T.to_gpu_bf16(x), T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d), add_residual=resid)
+    gw, uw, dw = T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d)
+    assert T.swiglu_path(N, d_model, gw, uw, dw) == path
+    out, *_ = T.abi_swiglu(T.to_gpu_bf16(x), gw, uw, dw, add_residual=resid)
     f64 = lambda w: (w[0].astype(np.float64), w[1])
     ref, *_ = O.swiglu_fwd(x.astype(np.float64), f64(g), f64(u), f64(d), add_residual=resid)
     rel, ab = T.rel_err(T.to_np(out), ref)

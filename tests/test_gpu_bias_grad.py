@@ -26,25 +26,27 @@ def _biases(rng, d_model, d_ff, scale=0.05):
 
 
 BIAS_CASES = [
-    # (d_model, d_ff, B, density, N)  paths: two-kernel (B 16/32), row-block (B 64), decode (N <= 16)
-    (1024, 4096, 32, 0.25, 130),
-    (256, 1024, 16, 0.25, 70),
-    (512, 1024, 64, 0.25, 33),
-    (1024, 3072, 64, 0.125, 16),
-    (512, 1024, 32, 0.25, 9),
+    # (d_model, d_ff, B, density, N, kernels of the plain forward)
+    (1024, 4096, 32, 0.25, 130, "split"),
+    (256, 1024, 16, 0.25, 70, "split"),
+    (512, 1024, 64, 0.25, 33, "decode"),
+    (512, 1024, 64, 0.25, 100, "rowblock"),
+    (1024, 3072, 64, 0.125, 16, "decode"),
+    (512, 1024, 32, 0.25, 9, "decode"),
 ]
 
 
 @pytest.mark.parametrize("case", BIAS_CASES)
 def test_swiglu_bias_forward_and_intermediates(gpu, case):
     from looped_blockell import kernels
-    d_model, d_ff, B, dens, N = case
+    d_model, d_ff, B, dens, N, path = case
     _say(f"swiglu bias {case}")
-    rng = np.random.default_rng(abs(hash(case)) % 2 ** 31)
+    rng = np.random.default_rng(abs(hash(case[:5])) % 2 ** 31)
     g, u, d = T.ffn_weights(rng, d_model, d_ff, B, dens, sentinel_frac=0.05)
     bs = _biases(rng, d_model, d_ff)
     x = T.act(rng, N, d_model)
     ws = [t for w in (g, u, d) for t in T.gpu_weight(w)]
+    assert T.swiglu_path(N, d_model, ws[0:2], ws[2:4], ws[4:6]) == path
     bt = [T.to_gpu(b) for b in bs]
     xt = T.to_gpu_bf16(x)
     args = (xt, ws[0], ws[1], bt[0], ws[2], ws[3], bt[1], ws[4], ws[5], bt[2])
@@ -202,3 +204,38 @@ def test_ops_without_derivative_raise_on_backward(gpu):
     out = kernels.ops().looped_swiglu(h, scale, *ws, 2, 1e-5)
     with pytest.raises(RuntimeError):
         out.float().sum().backward()
+
+
+def test_b16_shared_topology_bias_full_size(gpu):
+    """The reference-default layer (tile 16, gate and up from one seed, so one shared topology,
+    with biases) at full size: 16384 + 5 tokens at d_model 1024, d_ff 4096, density 0.25 take the
+    16-wave gate/up kernel's shared-topology, bias instantiations (the plain forward) and their
+    normalising forms (the looped block).  The up weight is given the gate's column-index tensor
+    itself; sampled rows against the float64 oracle."""
+    from looped_blockell import kernels
+    rng = np.random.default_rng(1618)
+    d_model, d_ff, B, N, L = 1024, 4096, 16, 16384 + 5, 2
+    _say("b16 shared topology + biases d1024 ff4096 N16389 full size")
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25, sentinel_frac=0.05)
+    u = (u[0], g[1])                       # one topology for gate and up
+    bs = _biases(rng, d_model, d_ff)
+    bs64 = tuple(b.astype(np.float64) for b in bs)
+    x = T.act(rng, N, d_model)
+    vg, cg = T.gpu_weight(g)
+    vu = T.to_gpu_bf16(u[0])
+    vd, cd = T.gpu_weight(d)
+    bt = [T.to_gpu(b) for b in bs]
+    xt = T.to_gpu_bf16(x)
+    rows = np.concatenate([np.sort(rng.choice(N, 192, replace=False)), [0, N - 1]])
+
+    out, *_ = kernels.ops().block_ell_swiglu_fwd_bias(xt, vg, cg, bt[0], vu, cg, bt[1], vd, cd, bt[2], True, False)
+    ref, *_ = O.swiglu_fwd(x[rows].astype(np.float64), f64(g), f64(u), f64(d), add_residual=True, biases=bs64)
+    rel, ab = T.rel_err(T.to_np(out)[rows], ref)
+    assert rel <= TOL, f"forward rel {rel} abs {ab}"
+
+    scale = (1.0 + 0.1 * rng.standard_normal(d_model)).astype(np.float32)
+    lo = kernels.ops().looped_swiglu_bias(xt, T.to_gpu(scale), vg, cg, bt[0], vu, cg, bt[1], vd, cd, bt[2], L, 1e-5)
+    ref = O.looped_swiglu(x[rows].astype(np.float64), scale.astype(np.float64), f64(g), f64(u), f64(d), L, 1e-5,
+                          biases=bs64)
+    rel, ab = T.rel_err(T.to_np(lo)[rows], ref)
+    assert rel <= TOL, f"looped rel {rel} abs {ab}"
