@@ -391,6 +391,58 @@ int lbk_looped_swiglu_persistent_bf16(const uint16_t* h_in, int64_t N, int32_t d
                                       void* stream);
 
 /*
+ * The looped application of the FFN core (reference looped_blockell/looping/looped_model.py:293-340,
+ * the scan body, and interop/pt_model.py:1441-1509, the PyTorch loop, on their FFN path;
+ * csrc/loop/loop_ops.cpp:52-66 persistent_mlp_step is one iteration of it without the freeze).
+ * For t = 0 .. L-1, per token row n:
+ *   h_agg = h
+ *   h_new = decay * h_agg + dt * e           (diagonal injection, per feature; skipped if e is NULL)
+ *   for each core block c in order:          h_new = h_new + SwiGLU_c(RMSNorm_c(h_new))
+ *   h = (t < depth(n)) ? h_new : h_agg        (depth(n) = depths[n / seq_len]; all L if depths is NULL)
+ * with dt = softplus(log_dt), decay = exp(-dt * exp(log_A)) (as lbk_diagonal_injection_bf16),
+ * RMSNorm_c with blocks[c].norm_scale and eps, SwiGLU_c as lbk_swiglu_fwd_bias_bf16 with the
+ * block's weights and optional biases.  The state is carried in fp32 between blocks and
+ * iterations; h_out = bf16(h).  h_in, e, h_out are [N, d_model] bf16 (h_out may alias h_in);
+ * log_A, log_dt [d_model] fp32 (required with e); depths int32, one entry per run of seq_len
+ * consecutive rows (the reference's per-sequence depths over [batch, seq]).  1 <= n_core <=
+ * LBK_MAX_CORE_BLOCKS; every block maps d_model -> d_ff -> d_model.
+ * The two-kernel path (every block within its shapes) runs a gate/up launch (RMSNorm of the
+ * state in its prologue; token blocks whose rows are all past their depth are skipped) and a
+ * down launch (state update with the depth mask; the last block also applies the next
+ * iteration's injection) per block and iteration; other shapes run the decode or row-block
+ * kernels and an elementwise state update.  Workspace: lbk_looped_core_workspace_bytes.
+ */
+#define LBK_MAX_CORE_BLOCKS 8
+typedef struct lbk_core_block {
+    const float* norm_scale;     /* [d_model] RMSNorm scale (16-byte aligned) */
+    lbk_bell gate, up, down;     /* gate, up [d_ff / B, K, B, B]; down [d_model / B, K_d, B, B] */
+    const float* b_gate;         /* [d_ff] or NULL */
+    const float* b_up;           /* [d_ff] or NULL */
+    const float* b_down;         /* [d_model] or NULL */
+} lbk_core_block;
+size_t lbk_looped_core_workspace_bytes(int64_t N, int32_t d_model, int32_t n_core, const lbk_core_block* blocks);
+int lbk_looped_core_bf16(const uint16_t* h_in, const uint16_t* e, const float* log_A, const float* log_dt,
+                         int64_t N, int32_t d_model, int32_t n_core, const lbk_core_block* blocks, float eps,
+                         int32_t L, const int32_t* depths, int64_t seq_len, uint16_t* h_out,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * lbk_looped_core_bf16 in one persistent launch (the reference design's K5 persistent_core_loop,
+ * Ai-notes/05-02-2026/CUDA-Kernel-Spec/spec.md:184-243, MLP path: injection, n_core blocks, the
+ * active-mask where, all L iterations): each workgroup owns 64 tokens for the whole loop, runs
+ * only as many iterations as its deepest row and keeps the state of rows past their depth.
+ * Same results as lbk_looped_core_bf16 up to the rounding of the fused normalisation.  Takes the
+ * shapes of lbk_looped_swiglu_persistent_bf16 for every block, all blocks with the same tile size
+ * and either all or none sharing the gate/up column buffer; LBK_ERR_SHAPE otherwise.  Same
+ * workspace.
+ */
+int lbk_looped_core_persistent_bf16(const uint16_t* h_in, const uint16_t* e, const float* log_A,
+                                    const float* log_dt, int64_t N, int32_t d_model, int32_t n_core,
+                                    const lbk_core_block* blocks, float eps, int32_t L, const int32_t* depths,
+                                    int64_t seq_len, uint16_t* h_out, void* workspace, size_t workspace_bytes,
+                                    void* stream);
+
+/*
  * Per-token absmax int8 quantisation of bf16 activations:
  *   absmax = max(max|x|, 1e-8); q = clamp(rint(x * (128/absmax)), -128, 127);
  *   sx = absmax / 128 (the dequantisation multiplier).

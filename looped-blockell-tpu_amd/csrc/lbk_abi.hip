@@ -654,16 +654,209 @@ static int looped_persistent(const uint16_t* h_in, int64_t N, int32_t d_model, c
   PackedFFN pk{};
   if ((st = pack_ffn(gate, up, down, ws + sbytes + hbytes, &pk, s))) return st;
   LoopArgs la{};
-  la.gu.xf = state; la.gu.N = N; la.gu.d_model = d_model; la.gu.norm_scale = norm_scale; la.gu.eps = eps;
-  la.gu.pg = pk.g; la.gu.cg = gate->col_idx; la.gu.Kg = gate->K;
-  la.gu.pu = pk.u; la.gu.cu = up->col_idx; la.gu.Ku = up->K;
-  la.gu.R_ff = gate->R; la.gu.h = h; la.gu.bg = bs.g; la.gu.bu = bs.u;
+  la.gu.xf = state; la.gu.N = N; la.gu.d_model = d_model; la.gu.eps = eps;
+  la.gu.R_ff = gate->R; la.gu.h = h;
   la.dn.h = h; la.dn.N = N; la.dn.d_ff = d_ff; la.dn.d_model = d_model;
-  la.dn.pd = pk.d; la.dn.cd = down->col_idx; la.dn.Kd = down->K;
-  la.dn.R_m = down->R; la.dn.C_d = gate->R; la.dn.state = state; la.dn.out = h_out; la.dn.bd = bs.d;
+  la.dn.R_m = down->R; la.dn.C_d = gate->R; la.dn.state = state; la.dn.out = h_out;
   la.h_in = h_in; la.L = L;
+  la.n_core = 1;
+  la.core[0] = CoreW{pk.g, pk.u, pk.d, gate->col_idx, up->col_idx, down->col_idx, gate->K, down->K, norm_scale,
+                     bs.g, bs.u, bs.d};
   // h_out may alias h_in: the kernel reads a token block's h_in rows before any write to them
   return launch_looped(gate->B, la, s) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+}
+
+// ---- looped core: injection -> n_core blocks -> depth freeze, L iterations
+enum { CORE_DECODE = 1, CORE_SPLIT = 2, CORE_GENERAL = 3 };
+struct CorePlan {
+  int path;
+  int64_t d_ff;                 // widest d_ff of the blocks
+  size_t state, h, tdep, coef, xn, y, packed[LBK_MAX_CORE_BLOCKS], total;
+};
+
+// validates the blocks and lays out the workspace:
+// [fp32 state][h][per-token depths][injection coefficients][xn, y (decode / row-block paths) or
+// the packed tiles of every block (two-kernel path)]
+static int core_plan(int64_t N, int32_t d_model, int32_t n_core, const lbk_core_block* blocks, CorePlan* p) {
+  if (!blocks) return LBK_ERR_NULL;
+  if (n_core < 1 || n_core > LBK_MAX_CORE_BLOCKS || N < 0 || d_model <= 0) return LBK_ERR_ARG;
+  *p = CorePlan{};
+  bool dec = N <= kDecodeMaxTokens, split = true;
+  for (int c = 0; c < n_core; ++c) {
+    const lbk_core_block& b = blocks[c];
+    int st;
+    if ((st = check_bell(&b.gate)) || (st = check_bell(&b.up)) || (st = check_bell(&b.down))) return st;
+    int64_t d_ff = 0;
+    if ((st = check_ffn(&b.gate, &b.up, &b.down, d_model, &d_ff))) return st;
+    if (!b.norm_scale) return LBK_ERR_NULL;
+    p->d_ff = d_ff > p->d_ff ? d_ff : p->d_ff;
+    dec = dec && use_decode(N, &b.gate, &b.up, &b.down, false);
+    split = split && use_split(&b.gate, &b.up, &b.down, d_model) && a16(b.norm_scale);
+  }
+  p->path = dec ? CORE_DECODE : (split ? CORE_SPLIT : CORE_GENERAL);
+  p->state = align256((size_t)N * d_model * 4);
+  p->h = align256((size_t)N * p->d_ff * 2);
+  p->tdep = align256((size_t)N * 4);
+  p->coef = align256((size_t)d_model * 8);
+  // after the fixed part: the packed tiles (two-kernel path, and the persistent form of any
+  // two-kernel geometry) or xn and y (decode and row-block paths), whichever is larger
+  size_t packed = 0, rows = 0;
+  if (split) {
+    for (int c = 0; c < n_core; ++c) {
+      p->packed[c] = packed_ffn_bytes(&blocks[c].gate, &blocks[c].up, &blocks[c].down);
+      packed += p->packed[c];
+    }
+  }
+  if (p->path != CORE_SPLIT) {
+    p->xn = p->y = align256((size_t)N * d_model * 2);
+    rows = p->xn + p->y;
+  }
+  p->total = p->state + p->h + p->tdep + p->coef + (packed > rows ? packed : rows);
+  return LBK_OK;
+}
+
+size_t lbk_looped_core_workspace_bytes(int64_t N, int32_t d_model, int32_t n_core, const lbk_core_block* blocks) {
+  CorePlan p{};
+  if (N <= 0 || core_plan(N, d_model, n_core, blocks, &p)) return 0;
+  return p.total;
+}
+
+static int looped_core_impl(const uint16_t* h_in, const uint16_t* e, const float* log_A, const float* log_dt,
+                            int64_t N, int32_t d_model, int32_t n_core, const lbk_core_block* blocks, float eps,
+                            int32_t L, const int32_t* depths, int64_t seq_len, uint16_t* h_out, void* workspace,
+                            size_t workspace_bytes, hipStream_t s, bool persistent) {
+  CorePlan p{};
+  int st;
+  if ((st = core_plan(N, d_model, n_core, blocks, &p))) return st;
+  if (L < 0 || !(eps >= 0.f) || (depths && seq_len < 1)) return LBK_ERR_ARG;
+  if (e && (!log_A || !log_dt)) return LBK_ERR_NULL;
+  if (persistent) {
+    // one kernel for every block: the same tile size, the persistent launch's shapes
+    const int B = blocks[0].gate.B;
+    int kmax = 0;
+    for (int c = 0; c < n_core; ++c) {
+      const lbk_core_block& b = blocks[c];
+      if (b.gate.B != B || b.gate.R != blocks[0].gate.R || !a16(b.norm_scale)) return LBK_ERR_SHAPE;
+      if (!looped_persistent_supported(B, d_model, b.gate.R, b.down.R, b.gate.K, b.up.K, b.down.K))
+        return LBK_ERR_SHAPE;
+      kmax = b.gate.K > kmax ? b.gate.K : kmax;
+      // one kernel for every block: all or none share their gate/up column buffer
+      if ((b.gate.col_idx == b.up.col_idx) != (blocks[0].gate.col_idx == blocks[0].up.col_idx)) return LBK_ERR_SHAPE;
+    }
+    if (!looped_persistent_supported(B, d_model, blocks[0].gate.R, blocks[0].down.R, kmax, kmax, 1))
+      return LBK_ERR_SHAPE;
+    p.path = CORE_SPLIT;
+  }
+  if (N == 0) return LBK_OK;
+  if (!h_in || !h_out) return LBK_ERR_NULL;
+  if (!a16(h_in) || !a16(h_out) || (e && !a16(e)) || (d_model % 8)) return LBK_ERR_ALIGN;
+  if (L == 0) {
+    if (h_out != h_in &&
+        hipMemcpyAsync(h_out, h_in, (size_t)N * d_model * 2, hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return LBK_ERR_LAUNCH;
+    return LBK_OK;
+  }
+  if (!workspace || workspace_bytes < p.total) return LBK_ERR_WORKSPACE;
+  if (!a16(workspace)) return LBK_ERR_ALIGN;
+  char* ws = static_cast<char*>(workspace);
+  float* state = reinterpret_cast<float*>(ws);
+  uint16_t* h = reinterpret_cast<uint16_t*>(ws + p.state);
+  int32_t* tdepth = depths ? reinterpret_cast<int32_t*>(ws + p.state + p.h) : nullptr;
+  float* coef = e ? reinterpret_cast<float*>(ws + p.state + p.h + p.tdep) : nullptr;
+  char* rest = ws + p.state + p.h + p.tdep + p.coef;
+  if (launch_core_prep(log_A, log_dt, d_model, coef, depths, seq_len, N, tdepth, s) != 0) return LBK_ERR_LAUNCH;
+
+  if (p.path == CORE_SPLIT) {
+    PackedFFN pk[LBK_MAX_CORE_BLOCKS];
+    for (int c = 0; c < n_core; ++c) {
+      if ((st = pack_ffn(&blocks[c].gate, &blocks[c].up, &blocks[c].down, rest, &pk[c], s))) return st;
+      rest += p.packed[c];
+    }
+    if (persistent) {
+      LoopArgs la{};
+      la.gu.xf = state; la.gu.N = N; la.gu.d_model = d_model; la.gu.eps = eps;
+      la.gu.R_ff = blocks[0].gate.R; la.gu.h = h;
+      la.dn.h = h; la.dn.N = N; la.dn.d_ff = p.d_ff; la.dn.d_model = d_model;
+      la.dn.R_m = blocks[0].down.R; la.dn.C_d = blocks[0].gate.R; la.dn.state = state; la.dn.out = h_out;
+      la.h_in = h_in; la.L = L; la.n_core = n_core;
+      for (int c = 0; c < n_core; ++c) {
+        const lbk_core_block& b = blocks[c];
+        la.core[c] = CoreW{pk[c].g, pk[c].u, pk[c].d, b.gate.col_idx, b.up.col_idx, b.down.col_idx, b.gate.K, b.down.K,
+                           b.norm_scale, b.b_gate, b.b_up, b.b_down};
+      }
+      la.tdepth = tdepth; la.e = e; la.inj_coef = coef;
+      // h_out may alias h_in: the kernel reads a token block's h_in rows before any write to them
+      return launch_looped(blocks[0].gate.B, la, s) == 0 ? LBK_OK : LBK_ERR_LAUNCH;
+    }
+    if (launch_core_init(h_in, e, coef, tdepth, L, N, d_model, state, s) != 0) return LBK_ERR_LAUNCH;
+    for (int l = 0; l < L; ++l)
+      for (int c = 0; c < n_core; ++c) {
+        const lbk_core_block& b = blocks[c];
+        GUArgs g{};
+        g.xf = state; g.N = N; g.d_model = d_model; g.norm_scale = b.norm_scale; g.eps = eps;
+        g.pg = pk[c].g; g.cg = b.gate.col_idx; g.Kg = b.gate.K;
+        g.pu = pk[c].u; g.cu = b.up.col_idx; g.Ku = b.up.K;
+        g.R_ff = b.gate.R; g.h = h; g.bg = b.b_gate; g.bu = b.b_up;
+        g.tdepth = tdepth; g.it = l;
+        if (launch_gu(b.gate.B, true, g, s) != 0) return LBK_ERR_LAUNCH;
+        DNArgs d{};
+        d.h = h; d.N = N; d.d_ff = (int64_t)b.gate.R * b.gate.B; d.d_model = d_model;
+        d.pd = pk[c].d; d.cd = b.down.col_idx; d.Kd = b.down.K;
+        d.R_m = b.down.R; d.C_d = b.gate.R;
+        d.state = state; d.out = (l == L - 1 && c == n_core - 1) ? h_out : nullptr; d.bd = b.b_down;
+        d.tdepth = tdepth; d.it = l;
+        d.inj_e = (c == n_core - 1 && l + 1 < L) ? e : nullptr; d.inj_coef = coef;
+        if (launch_dn(b.gate.B, d, s) != 0) return LBK_ERR_LAUNCH;
+      }
+    return LBK_OK;
+  }
+
+  // decode / row-block kernels: RMSNorm of the state into xn, the block's FFN into y, then the
+  // elementwise state update (depth mask, next injection, output after the last block)
+  uint16_t* xn = reinterpret_cast<uint16_t*>(rest);
+  uint16_t* y = reinterpret_cast<uint16_t*>(rest + p.xn);
+  if (launch_core_init(h_in, e, coef, tdepth, L, N, d_model, state, s) != 0) return LBK_ERR_LAUNCH;
+  for (int l = 0; l < L; ++l)
+    for (int c = 0; c < n_core; ++c) {
+      const lbk_core_block& b = blocks[c];
+      if (launch_rmsnorm_f32(state, N, d_model, b.norm_scale, eps, xn, s) != 0) return LBK_ERR_LAUNCH;
+      if (p.path == CORE_DECODE) {
+        DecodeArgs a{};
+        a.x = xn; a.N = (int)N; a.d_model = d_model;
+        a.vg = b.gate.values; a.cg = b.gate.col_idx; a.Kg = b.gate.K;
+        a.vu = b.up.values; a.cu = b.up.col_idx; a.Ku = b.up.K;
+        a.R_ff = b.gate.R;
+        a.vd = b.down.values; a.cd = b.down.col_idx; a.Kd = b.down.K;
+        a.R_m = b.down.R;
+        a.out = y; a.h = h;
+        a.bg = b.b_gate; a.bu = b.b_up; a.bd = b.b_down;
+        if (launch_decode(b.gate.B, a, s) != 0) return LBK_ERR_LAUNCH;
+      } else if ((st = swiglu_general(xn, N, d_model, &b.gate, &b.up, &b.down, nullptr, y, h, nullptr, nullptr, s,
+                                      Biases{b.b_gate, b.b_up, b.b_down}))) {
+        return st;
+      }
+      if (launch_core_update(state, y, tdepth, l, (c == n_core - 1 && l + 1 < L) ? e : nullptr, coef, N, d_model,
+                             (l == L - 1 && c == n_core - 1) ? h_out : nullptr, s) != 0)
+        return LBK_ERR_LAUNCH;
+    }
+  return LBK_OK;
+}
+
+int lbk_looped_core_bf16(const uint16_t* h_in, const uint16_t* e, const float* log_A, const float* log_dt,
+                         int64_t N, int32_t d_model, int32_t n_core, const lbk_core_block* blocks, float eps,
+                         int32_t L, const int32_t* depths, int64_t seq_len, uint16_t* h_out, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  return looped_core_impl(h_in, e, log_A, log_dt, N, d_model, n_core, blocks, eps, L, depths, seq_len, h_out,
+                          workspace, workspace_bytes, S(stream), false);
+}
+
+int lbk_looped_core_persistent_bf16(const uint16_t* h_in, const uint16_t* e, const float* log_A,
+                                    const float* log_dt, int64_t N, int32_t d_model, int32_t n_core,
+                                    const lbk_core_block* blocks, float eps, int32_t L, const int32_t* depths,
+                                    int64_t seq_len, uint16_t* h_out, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  return looped_core_impl(h_in, e, log_A, log_dt, N, d_model, n_core, blocks, eps, L, depths, seq_len, h_out,
+                          workspace, workspace_bytes, S(stream), true);
 }
 
 int lbk_quantize_act_int8(const uint16_t* x, int64_t N, int32_t F, int64_t ldx, int8_t* xq, float* sx,

@@ -542,4 +542,97 @@ int launch_pack_bf16(const uint16_t* values, const int32_t* col, int64_t ntiles,
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// ---------------------------------------------------------------------------
+// looped core helpers: the injection's per-feature coefficients, per-token depths, the fp32 state
+// set-up and the state update of core blocks run outside the split kernels (8 features per
+// thread; d % 8 == 0 and 16-byte aligned rows)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void core_prep_kernel(const float* __restrict__ log_A,
+                                                        const float* __restrict__ log_dt, int d,
+                                                        float* __restrict__ coef, const int32_t* __restrict__ depths,
+                                                        int64_t seq_len, int64_t N, int32_t* __restrict__ tdepth) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (coef && i < d) {
+    // the injection kernel's arithmetic: dt = softplus(log_dt), decay = exp(-dt * exp(log_A))
+    const float ld = log_dt[i];
+    const float dt = ld > 20.f ? ld : log1pf(expf(ld));
+    coef[i] = expf(-dt * expf(log_A[i]));
+    coef[d + i] = dt;
+  }
+  if (tdepth && i < N) tdepth[i] = depths[i / seq_len];
+}
+
+__global__ __launch_bounds__(256) void core_init_kernel(const uint16_t* __restrict__ h_in,
+                                                        const uint16_t* __restrict__ e, const float* __restrict__ coef,
+                                                        const int32_t* __restrict__ tdepth, int L, int64_t N, int d,
+                                                        float* __restrict__ state) {
+  const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (e0 >= N * d) return;
+  const int64_t t = e0 / d;
+  const int c = (int)(e0 - t * d);
+  float s[8];
+  unpack8_bf16(*reinterpret_cast<const u32x4*>(h_in + e0), s);
+  if (e && L > 0 && (!tdepth || tdepth[t] > 0)) inject8(s, e, coef, e0, c, d);
+  *reinterpret_cast<f32x4*>(state + e0) = f32x4{s[0], s[1], s[2], s[3]};
+  *reinterpret_cast<f32x4*>(state + e0 + 4) = f32x4{s[4], s[5], s[6], s[7]};
+}
+
+__global__ __launch_bounds__(256) void core_update_kernel(float* __restrict__ state, const uint16_t* __restrict__ y,
+                                                          const int32_t* __restrict__ tdepth, int it,
+                                                          const uint16_t* __restrict__ e,
+                                                          const float* __restrict__ coef, int64_t N, int d,
+                                                          uint16_t* __restrict__ out) {
+  const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (e0 >= N * d) return;
+  const int64_t t = e0 / d;
+  const int c = (int)(e0 - t * d);
+  const f32x4 v0 = *reinterpret_cast<const f32x4*>(state + e0), v1 = *reinterpret_cast<const f32x4*>(state + e0 + 4);
+  float s[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+  const int dep = tdepth ? tdepth[t] : 0x7fffffff;
+  if (it < dep) {
+    float yf[8];
+    unpack8_bf16(*reinterpret_cast<const u32x4*>(y + e0), yf);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s[q] += yf[q];
+    if (e && it + 1 < dep) inject8(s, e, coef, e0, c, d);
+    *reinterpret_cast<f32x4*>(state + e0) = f32x4{s[0], s[1], s[2], s[3]};
+    *reinterpret_cast<f32x4*>(state + e0 + 4) = f32x4{s[4], s[5], s[6], s[7]};
+  }
+  if (out)
+    *reinterpret_cast<u32x4*>(out + e0) = u32x4{pack2_bf16(s[0], s[1]), pack2_bf16(s[2], s[3]),
+                                                pack2_bf16(s[4], s[5]), pack2_bf16(s[6], s[7])};
+}
+
+int launch_core_prep(const float* log_A, const float* log_dt, int d, float* coef, const int32_t* depths,
+                     int64_t seq_len, int64_t N, int32_t* tdepth, hipStream_t st) {
+  if (!coef && !tdepth) return 0;
+  if (tdepth && seq_len < 1) return -2;
+  const int64_t nc = coef ? (int64_t)d : 0, nt = tdepth ? N : 0;
+  const int64_t n = nc > nt ? nc : nt;
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(core_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, log_A, log_dt, d, coef,
+                     depths, seq_len, N, tdepth);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_core_init(const uint16_t* h_in, const uint16_t* e, const float* coef, const int32_t* tdepth, int L,
+                     int64_t N, int d, float* state, hipStream_t st) {
+  if (N == 0) return 0;
+  if (d % 8) return -2;
+  const int64_t n8 = N * d / 8;
+  hipLaunchKernelGGL(core_init_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, h_in, e, coef, tdepth, L,
+                     N, d, state);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_core_update(float* state, const uint16_t* y, const int32_t* tdepth, int it, const uint16_t* e,
+                       const float* coef, int64_t N, int d, uint16_t* out, hipStream_t st) {
+  if (N == 0) return 0;
+  if (d % 8) return -2;
+  const int64_t n8 = N * d / 8;
+  hipLaunchKernelGGL(core_update_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, state, y, tdepth, it,
+                     e, coef, N, d, out);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 }  // namespace lbk

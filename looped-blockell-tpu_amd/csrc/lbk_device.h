@@ -82,6 +82,29 @@ __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirs
 // For B = 16 the single k-step is half filled: lanes with g >= 2 carry a zero A
 // operand (their B operand repeats lanes g - 2 and is multiplied by zero).
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ void unpack8_bf16(const u32x4& v, float (&f)[8]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    f[2 * q] = bf_lo(v[q]);
+    f[2 * q + 1] = bf_hi(v[q]);
+  }
+}
+
+// The looped core's injection s = decay * s + dt * e over features c .. c + 7 of the element at
+// e0 (coef: decay [d], then dt [d])
+__device__ __forceinline__ void inject8(float (&s)[8], const uint16_t* __restrict__ e, const float* __restrict__ coef,
+                                        int64_t e0, int c, int d) {
+  float ef[8];
+  unpack8_bf16(*reinterpret_cast<const u32x4*>(e + e0), ef);
+  const f32x4 k0 = *reinterpret_cast<const f32x4*>(coef + c), k1 = *reinterpret_cast<const f32x4*>(coef + c + 4);
+  const f32x4 t0 = *reinterpret_cast<const f32x4*>(coef + d + c), t1 = *reinterpret_cast<const f32x4*>(coef + d + c + 4);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    s[q] = k0[q] * s[q] + t0[q] * ef[q];
+    s[4 + q] = k1[q] * s[4 + q] + t1[q] * ef[4 + q];
+  }
+}
+
 template <int B> struct TileShape;
 template <> struct TileShape<16> { static constexpr int NKS = 1, CW = 1; };
 template <> struct TileShape<32> { static constexpr int NKS = 1, CW = 2; };

@@ -73,6 +73,9 @@ struct GUArgs {
   uint16_t* uout;           // [N, d_ff] optional up output
   const float* bg; const float* bu;   // optional [d_ff] gate / up biases (added before SiLU*mul)
   int H;                    // row slices per token block (set by the launcher)
+  // looped core: per-token depths; a token block whose rows all have tdepth[t] <= it is skipped
+  const int32_t* tdepth; int it;
+  int reload_table;         // looped kernel: a gate/up phase on a ready panel re-reads the column table
 };
 struct DNArgs {
   const uint16_t* h;        // [N, d_ff]
@@ -87,6 +90,11 @@ struct DNArgs {
   uint16_t* out;            // optional bf16 output [N, d_model]
   int nrg;                  // row groups per token block (set by the launcher)
   const float* bd;          // optional [d_model] down bias
+  // looped core (state mode): rows with tdepth[t] <= it keep their state; when inj_e is set the
+  // rows that run the next iteration (it + 1 < tdepth[t]) then take its injection
+  // state = decay * state + dt * e (inj_coef: decay [d_model], then dt [d_model])
+  const int32_t* tdepth; int it;
+  const uint16_t* inj_e; const float* inj_coef;
 };
 bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd);
 // plain product y[N, R*B] = x[N, in] W (+ bias in a.bg) on packed tiles (a.pg, a.cg, a.Kg, a.R_ff,
@@ -95,17 +103,44 @@ bool lin_supported(int B, int in_features, int R, int K);
 int launch_lin(int B, const GUArgs& a, hipStream_t st);
 // looped block in one launch: gate/up (RMSNorm of the fp32 state) and down per token block
 // for all L iterations; gu.xf == dn.state == the fp32 state, gu.h == dn.h
+// one core block of the persistent looped kernel (packed tiles, columns, norm scale, biases)
+struct CoreW {
+  const void* pg; const void* pu; const void* pd;
+  const int32_t* cg; const int32_t* cu; const int32_t* cd;
+  int Kg, Kd;
+  const float* norm_scale;
+  const float* bg; const float* bu; const float* bd;
+};
+constexpr int kMaxCore = 8;
 struct LoopArgs {
-  GUArgs gu;
+  GUArgs gu;                 // shared fields (the per-block ones come from core[])
   DNArgs dn;                 // dn.out: bf16 result, written by the last iteration
   const uint16_t* h_in;      // [N, d_model] bf16 initial state
   int L;
+  int n_core;                // core blocks applied in order per iteration (core[0] only: gu/dn as given)
+  CoreW core[kMaxCore];
+  const int32_t* tdepth;     // optional [N] per-token depths (iterations a row runs)
+  const uint16_t* e;         // optional [N, d_model] injection input, applied at every iteration's start
+  const float* inj_coef;     // decay [d_model], dt [d_model] (with e)
+  size_t red_off;            // LDS byte offset of the reduction area (after the widest column table)
 };
 bool looped_persistent_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd);
 int launch_looped(int B, const LoopArgs& a, hipStream_t st);
 int launch_gu(int B, bool norm, const GUArgs& a, hipStream_t st);
 int launch_dn(int B, const DNArgs& a, hipStream_t st);
 int launch_bf16_to_f32(const uint16_t* x, int64_t n, float* y, hipStream_t st);
+// looped core helpers (lbk_bf16.hip): injection coefficients (decay, dt per feature, when log_A)
+// and per-token depths (tdepth[t] = depths[t / seq_len], when depths), in one launch
+int launch_core_prep(const float* log_A, const float* log_dt, int d, float* coef, const int32_t* depths,
+                     int64_t seq_len, int64_t N, int32_t* tdepth, hipStream_t st);
+// state = float(h_in), then the first iteration's injection on the rows that run it (e optional)
+int launch_core_init(const uint16_t* h_in, const uint16_t* e, const float* coef, const int32_t* tdepth, int L,
+                     int64_t N, int d, float* state, hipStream_t st);
+// state update of a core block computed outside the split kernels (y bf16): rows running
+// iteration it add y (the others keep their state), then with e the next iteration's injection
+// on rows that run it; out (optional) = bf16(state)
+int launch_core_update(float* state, const uint16_t* y, const int32_t* tdepth, int it, const uint16_t* e,
+                       const float* coef, int64_t N, int d, uint16_t* out, hipStream_t st);
 
 // decode-shaped SwiGLU FFN (N <= 16): gate/up kernel, then down kernel
 struct DecodeArgs {

@@ -255,7 +255,15 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
   // ---- input panel: all of this thread's loads are issued before any store,
   // and the first ring positions' weight loads go out before the barrier
   if constexpr (READY) {
-    if (nrows > 0) prefetch_ring();
+    // the column table stays in LDS from the first phase unless the phases alternate between
+    // core blocks (each with its own table)
+    if (a.reload_table) {
+      ctab_fetch();
+      if (nrows > 0) prefetch_ring();
+      ctab_store();
+    } else if (nrows > 0) {
+      prefetch_ring();
+    }
   } else if constexpr (!NORM) {
     constexpr int CPR = ROWB / 16;                 // chunk capacity of a panel row
     constexpr int NCH = TM * CPR;                  // chunks of the panel
@@ -446,6 +454,17 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
   }
 }
 
+// Looped core: true when some token of [t0, t0 + tm) below N runs iteration `it` (tdepth[t] > it).
+// tm <= 64: every wave reads the block's depths and takes the same ballot, so the answer is
+// uniform over the workgroup without a barrier (or the LDS word a workgroup-wide vote would take,
+// which would no longer leave the kernels their full 160 KB of dynamic LDS).
+__device__ __forceinline__ bool block_runs(const int32_t* tdepth, int it, int64_t t0, int tm, int64_t N, int tid) {
+  const int lane = tid & 63;
+  bool p = false;
+  if (lane < tm && t0 + lane < N) p = it < tdepth[t0 + lane];
+  return __ballot(p) != 0;
+}
+
 // workgroup b -> (token block b / H, row slice b % H); the slices' rows split R_ff evenly, and
 // with H a multiple of 8 every workgroup of one slice runs on the same XCD (workgroups are dealt
 // to the 8 XCDs round robin), so each XCD's L2 holds the weights of its slices only
@@ -463,6 +482,7 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
   int64_t tb;
   int r_lo, nrs;
   gu_slice(a, tb, r_lo, nrs);
+  if (a.tdepth && !block_runs(a.tdepth, a.it, tb * 16 * MT, 16 * MT, a.N, (int)threadIdx.x)) return;
   gu_tile<B, MT, NORM, INTER, SHARED, false, BIAS>(a, tb, r_lo, nrs, smem, (int)threadIdx.x);
 }
 
@@ -477,6 +497,7 @@ template <int B> constexpr int gu_w12_waves() { return B == 16 ? 16 : 12; }
 template <int B, int MT, bool NORM, bool SHARED = false, bool BIAS = false>
 __global__ __launch_bounds__(64 * gu_w12_waves<B>(), 1) void gu_kernel_w12(GUArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  if (a.tdepth && !block_runs(a.tdepth, a.it, (int64_t)blockIdx.x * 16 * MT, 16 * MT, a.N, (int)threadIdx.x)) return;
   gu_tile<B, MT, NORM, false, SHARED, false, BIAS, false, gu_w12_waves<B>(), B == 16 ? 4 : 2>(
       a, (int64_t)blockIdx.x, 0, a.R_ff, smem, (int)threadIdx.x);
 }
@@ -506,6 +527,15 @@ constexpr int DN_WAVES = 16;
 constexpr int DN_STAGE_COLS = 512;
 template <int B, int SC>
 struct DnStage { static constexpr int G = SC / B; };
+
+// The looped core's injection o = decay * o + dt * e on the CW state columns col .. col + CW - 1
+// of the element at off (coef: decay [d], then dt [d])
+template <int CW>
+__device__ __forceinline__ void inject_cw(float (&o)[CW], const uint16_t* __restrict__ e,
+                                          const float* __restrict__ coef, int64_t off, int col, int d) {
+#pragma unroll
+  for (int m = 0; m < CW; ++m) o[m] = coef[col + m] * o[m] + coef[d + col + m] * bf2f(e[off + m]);
+}
 
 // Per-wave fetch list of one stage: position q (lane q % 64 of v[q / 64]) holds
 // desc = tile << 6 | cb -- the packed down tile (row * Kd + slot) and its column
@@ -589,7 +619,8 @@ __device__ __forceinline__ void dn_build(FetchList<RPW>& L, int c0, int ncb, con
 // RMSNorm of the new state rows (norm_scale, eps), as bf16, into the gate/up panel at the start
 // of dn_smem (row stride GUPanel<MT>::ROWB), for the next iteration's gate/up phase; red holds
 // (NW + 1) * 16 * MT floats for the per-token sums of squares.
-template <int B, int MT, int RPW, int NW, bool NORMOUT = false, bool BIAS = false, int SC = DN_STAGE_COLS>
+template <int B, int MT, int RPW, int NW, bool NORMOUT = false, bool BIAS = false, int SC = DN_STAGE_COLS,
+          bool CORE = false>
 __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, unsigned char* dn_smem,
                                         uint16_t* out, int tid, const float* norm_scale = nullptr,
                                         float eps = 0.f, float* red = nullptr) {
@@ -766,20 +797,35 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
           const int64_t t = t0 + 16 * mt + 4 * g + v;
           const bool ok = t < a.N;
           const int64_t off = (ok ? t : t0) * d_model + rm * B + CW * i;
+          // looped core: a row past its depth keeps its state; one that runs the next iteration
+          // takes that iteration's injection
+          bool run = ok, inj = CORE && ok && a.inj_e;
+          if (CORE && a.tdepth) {
+            const int dep = ok ? a.tdepth[t] : 0;
+            run = a.it < dep;
+            inj = inj && a.it + 1 < dep;
+          }
           float o[CW];
 #pragma unroll
           for (int m = 0; m < CW; ++m) {
             float av = acc[rho][mt][m][v];
-            if constexpr (BIAS) av += a.bd[rm * B + CW * i + m];
-            o[m] = ok ? av + a.state[off + m] : 0.f;
+            if constexpr (BIAS) {
+              if (a.bd) av += a.bd[rm * B + CW * i + m];
+            }
+            const float sv = ok ? a.state[off + m] : 0.f;
+            o[m] = run ? av + sv : sv;
+          }
+          if (inj) inject_cw<CW>(o, a.inj_e, a.inj_coef, off, rm * B + CW * i, d_model);
+#pragma unroll
+          for (int m = 0; m < CW; ++m) {
             acc[rho][mt][m][v] = o[m];
             ssq[mt][v] += o[m] * o[m];
           }
-          if (ok) {
+          if (run) {
 #pragma unroll
             for (int m = 0; m < CW; ++m) a.state[off + m] = o[m];
-            if (out) store_bf16<CW>(out + off, o);
           }
+          if (ok && out) store_bf16<CW>(out + off, o);
         }
     }
 #pragma unroll
@@ -840,13 +886,29 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
 #pragma unroll
         for (int m = 0; m < CW; ++m) {
           o[m] = acc[rho][mt][m][v];
-          if constexpr (BIAS) o[m] += a.bd[rm * B + CW * i + m];
+          if constexpr (BIAS) {
+            if (a.bd) o[m] += a.bd[rm * B + CW * i + m];
+          }
         }
         if (a.state) {
+          // looped core: a row past its depth keeps its state (and its output is that state);
+          // one that runs the next iteration takes that iteration's injection
+          bool run = true, inj = CORE && a.inj_e != nullptr;
+          if (CORE && a.tdepth) {
+            const int dep = a.tdepth[t];
+            run = a.it < dep;
+            inj = inj && a.it + 1 < dep;
+          }
+          if (run) {
 #pragma unroll
-          for (int m = 0; m < CW; ++m) {
-            o[m] += a.state[off + m];
-            a.state[off + m] = o[m];
+            for (int m = 0; m < CW; ++m) o[m] += a.state[off + m];
+            if (inj) inject_cw<CW>(o, a.inj_e, a.inj_coef, off, rm * B + CW * i, d_model);
+#pragma unroll
+            for (int m = 0; m < CW; ++m) a.state[off + m] = o[m];
+          } else {
+            if (!out) continue;
+#pragma unroll
+            for (int m = 0; m < CW; ++m) o[m] = a.state[off + m];
           }
         } else if (a.resid) {
           float rv[CW];
@@ -859,7 +921,9 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
   }
 }
 
-template <int B, int MT, int RPW, int NW, int SC, bool BIAS>
+// CORE: the looped core's state update (depth mask, fused injection); the other instantiations
+// carry none of its code
+template <int B, int MT, int RPW, int NW, int SC, bool BIAS, bool CORE>
 __global__ __launch_bounds__(64 * NW, 1) void dn_kernel(DNArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char dn_smem[];   // two stages
   // workgroup -> (token block, row group).  With several row groups, the groups of one token
@@ -871,7 +935,27 @@ __global__ __launch_bounds__(64 * NW, 1) void dn_kernel(DNArgs a) {
     rg = rest % a.nrg;
     tb = 8 * (rest / a.nrg) + (b & 7);
   }
-  dn_tile<B, MT, RPW, NW, false, BIAS, SC>(a, tb, rg, dn_smem, a.out, (int)threadIdx.x);
+  constexpr int TM = 16 * MT;
+  if (CORE && a.tdepth && !block_runs(a.tdepth, a.it, (int64_t)tb * TM, TM, a.N, (int)threadIdx.x)) {
+    // looped core: every row of the block is past its depth; only the last application's
+    // output (the kept state, as bf16) remains to be written
+    if (a.out) {
+      const int row0 = rg * NW * RPW;
+      const int nrm = a.R_m - row0 < NW * RPW ? a.R_m - row0 : NW * RPW;
+      const int c8 = nrm * B / 8;   // 8-column groups of this workgroup's down rows
+      for (int idx = (int)threadIdx.x; idx < TM * c8; idx += 64 * NW) {
+        const int64_t t = (int64_t)tb * TM + idx / c8;
+        if (t >= a.N) break;
+        const int64_t off = t * a.d_model + row0 * B + 8 * (idx % c8);
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(a.state + off);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(a.state + off + 4);
+        *reinterpret_cast<u32x4*>(a.out + off) = u32x4{pack2_bf16(v0[0], v0[1]), pack2_bf16(v0[2], v0[3]),
+                                                       pack2_bf16(v1[0], v1[1]), pack2_bf16(v1[2], v1[3])};
+      }
+    }
+    return;
+  }
+  dn_tile<B, MT, RPW, NW, false, BIAS, SC, CORE>(a, tb, rg, dn_smem, a.out, (int)threadIdx.x);
 }
 
 // ===========================================================================
@@ -883,15 +967,18 @@ template <int MT>
 __host__ __device__ inline size_t looped_red_offset(int R_ff, int K) {
   return (size_t)16 * MT * GUPanel<MT>::ROWB + (((size_t)R_ff * K * 8 + 255) & ~(size_t)255);
 }
-// looped_kernel<B, MT, SHARED, RPW>: workgroup tb owns token block tb (16 * MT tokens) for
-// all L applications of h <- h + SwiGLU(RMSNorm(h)): it copies its rows of h_in into the fp32
-// state, then per iteration runs the gate/up tile (RMSNorm of its state rows into the LDS
-// panel, h of its tokens to the h buffer) and the down tile of every row group (h staged
-// back through LDS, state += down product), with workgroup barriers between the phases.
-// Only this workgroup reads or writes its state and h rows, so no grid-wide barrier is
-// needed; the weights are read by every workgroup in every iteration (the packed tiles stay
-// in L2 / the memory-side cache across iterations).  The last iteration also writes the
-// bf16 output.
+// looped_kernel<B, MT, SHARED, RPW>: workgroup tb owns token block tb (16 * MT tokens) for all L
+// iterations of the looped core: it copies its rows of h_in into the fp32 state (with the first
+// iteration's injection, state = decay * state + dt * e, when e is given), then per iteration runs
+// the n_core blocks in order, each h <- h + SwiGLU(RMSNorm(h)) as a gate/up tile (RMSNorm of its
+// state rows into the LDS panel, h of its tokens to the h buffer) and the down tile of every row
+// group (h staged back through LDS, state += down product), with workgroup barriers between the
+// phases.  The last block's down phase also applies the next iteration's injection.  With
+// per-token depths a row stops once it has run its depth (its state is kept: the reference's
+// where(active, h_new, h_agg)), and the block stops after its deepest row.  Only this workgroup
+// reads or writes its state and h rows, so no grid-wide barrier is needed; the weights are read by
+// every workgroup in every iteration (the packed tiles stay in L2 / the memory-side cache across
+// iterations).  The block's last phase also writes the bf16 output.
 template <int B, int MT, bool SHARED, int RPW, bool BIAS>
 __global__ __launch_bounds__(512, 1) void looped_kernel(LoopArgs la) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -902,43 +989,94 @@ __global__ __launch_bounds__(512, 1) void looped_kernel(LoopArgs la) {
   const int64_t N = la.gu.N;
   if (t0 >= N) return;
   const int d_model = la.gu.d_model;
-  // state rows <- float(h_in rows): 8 elements per thread per step (d_model % 8 == 0)
+  const int rows = (int)(N - t0 < TM ? N - t0 : TM);
+  float* red = reinterpret_cast<float*>(smem + la.red_off);
+  // iterations this block runs: L, or its deepest row's depth when that is smaller
+  int lrun = la.L;
+  if (la.tdepth) {
+    if (tid < 64) {
+      int dmax = 0;
+      for (int r = tid; r < rows; r += 64) {
+        const int dp = la.tdepth[t0 + r];
+        dmax = dp > dmax ? dp : dmax;
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        const int v = __shfl_xor(dmax, o, 64);
+        dmax = v > dmax ? v : dmax;
+      }
+      if (tid == 0) reinterpret_cast<int*>(red)[0] = dmax;
+    }
+    __syncthreads();
+    const int dmax = reinterpret_cast<const int*>(red)[0];
+    __syncthreads();
+    lrun = dmax < lrun ? dmax : lrun;
+  }
+  // state rows <- float(h_in rows) (+ the first injection on the rows that run it): 8 elements per
+  // thread per step (d_model % 8 == 0); a block that runs no iteration copies h_in to the output
   {
-    const int64_t rows = N - t0 < TM ? N - t0 : TM;
-    const int64_t n = rows * d_model, base = t0 * d_model;
-    for (int64_t e = 8 * (int64_t)tid; e < n; e += 8 * 512) {
+    const int n = rows * d_model;
+    const int64_t base = t0 * d_model;
+    for (int e = 8 * tid; e < n; e += 8 * 512) {
       const u32x4 v = *reinterpret_cast<const u32x4*>(la.h_in + base + e);
+      if (lrun <= 0) {
+        *reinterpret_cast<u32x4*>(la.dn.out + base + e) = v;
+        continue;
+      }
+      float sv[8];
+      unpack8_bf16(v, sv);
+      if (la.e) {
+        const int r = e / d_model;
+        if (!la.tdepth || la.tdepth[t0 + r] > 0) inject8(sv, la.e, la.inj_coef, base + e, e - r * d_model, d_model);
+      }
       float* y = la.dn.state + base + e;
-      *reinterpret_cast<f32x4*>(y) = f32x4{bf_lo(v[0]), bf_hi(v[0]), bf_lo(v[1]), bf_hi(v[1])};
-      *reinterpret_cast<f32x4*>(y + 4) = f32x4{bf_lo(v[2]), bf_hi(v[2]), bf_lo(v[3]), bf_hi(v[3])};
+      *reinterpret_cast<f32x4*>(y) = f32x4{sv[0], sv[1], sv[2], sv[3]};
+      *reinterpret_cast<f32x4*>(y + 4) = f32x4{sv[4], sv[5], sv[6], sv[7]};
     }
   }
+  if (lrun <= 0) return;
   __syncthreads();
   const int nrg = (la.dn.R_m + 8 * RPW - 1) / (8 * RPW);
-  // with every down row in one group, the down phase writes the next iteration's normalised
-  // panel itself (the gate/up phase then reads neither the state nor the column indices again)
+  // with every down row in one group, the down phase writes the next phase's normalised panel
+  // itself (the gate/up phase then reads the state no more)
   const bool fuse = nrg == 1;
-  float* red = reinterpret_cast<float*>(smem + looped_red_offset<MT>(la.gu.R_ff, la.gu.Kg));
-  for (int l = 0; l < la.L; ++l) {
-    // The thread and token-block indices pass through an opaque copy in every phase:
-    // otherwise the compiler hoists the phases' address arithmetic (derived from them) out
-    // of the iteration loop, and the registers it then keeps live across both phases spill.
-    int tg = tid;
-    int64_t tbg = tb;
-    asm volatile("" : "+v"(tg), "+s"(tbg));
-    if (fuse && l > 0) gu_tile<B, MT, true, false, SHARED, true, BIAS>(la.gu, tbg, 0, la.gu.R_ff, smem, tg);
-    else gu_tile<B, MT, true, false, SHARED, false, BIAS>(la.gu, tbg, 0, la.gu.R_ff, smem, tg);
-    __syncthreads();
-    uint16_t* out = l == la.L - 1 ? la.dn.out : nullptr;
-    for (int rg = 0; rg < nrg; ++rg) {
-      int td = tid;
-      int64_t tbd = tb;
-      asm volatile("" : "+v"(td), "+s"(tbd));
-      if (fuse && l < la.L - 1)
-        dn_tile<B, MT, RPW, 8, true, BIAS>(la.dn, tbd, rg, smem, out, td, la.gu.norm_scale, la.gu.eps, red);
-      else
-        dn_tile<B, MT, RPW, 8, false, BIAS>(la.dn, tbd, rg, smem, out, td);
+  const int nc = la.n_core;
+  for (int l = 0; l < lrun; ++l) {
+    for (int c = 0; c < nc; ++c) {
+      // The thread and token-block indices pass through an opaque copy in every phase:
+      // otherwise the compiler hoists the phases' address arithmetic (derived from them) out
+      // of the iteration loop, and the registers it then keeps live across both phases spill.
+      int tg = tid;
+      int64_t tbg = tb;
+      asm volatile("" : "+v"(tg), "+s"(tbg));
+      const CoreW& cw = la.core[c];
+      GUArgs gu = la.gu;
+      gu.pg = cw.pg; gu.cg = cw.cg; gu.Kg = cw.Kg;
+      gu.pu = cw.pu; gu.cu = cw.cu; gu.Ku = cw.Kg;
+      gu.norm_scale = cw.norm_scale; gu.bg = cw.bg; gu.bu = cw.bu;
+      gu.reload_table = nc > 1;
+      if (fuse && (l > 0 || c > 0)) gu_tile<B, MT, true, false, SHARED, true, BIAS>(gu, tbg, 0, gu.R_ff, smem, tg);
+      else gu_tile<B, MT, true, false, SHARED, false, BIAS>(gu, tbg, 0, gu.R_ff, smem, tg);
       __syncthreads();
+      const bool last = l == lrun - 1 && c == nc - 1;
+      uint16_t* out = last ? la.dn.out : nullptr;
+      DNArgs dn = la.dn;
+      dn.pd = cw.pd; dn.cd = cw.cd; dn.Kd = cw.Kd; dn.bd = cw.bd;
+      dn.tdepth = la.tdepth; dn.it = l;
+      dn.inj_e = (c == nc - 1 && l + 1 < lrun) ? la.e : nullptr;
+      dn.inj_coef = la.inj_coef;
+      const float* next_scale = la.core[c + 1 < nc ? c + 1 : 0].norm_scale;
+      for (int rg = 0; rg < nrg; ++rg) {
+        int td = tid;
+        int64_t tbd = tb;
+        asm volatile("" : "+v"(td), "+s"(tbd));
+        if (fuse && !last)
+          dn_tile<B, MT, RPW, 8, true, BIAS, DN_STAGE_COLS, true>(dn, tbd, rg, smem, out, td, next_scale, la.gu.eps,
+                                                                 red);
+        else
+          dn_tile<B, MT, RPW, 8, false, BIAS, DN_STAGE_COLS, true>(dn, tbd, rg, smem, out, td);
+        __syncthreads();
+      }
     }
   }
 }
@@ -1107,7 +1245,9 @@ static int launch_dn_t(const DNArgs& a0, hipStream_t st) {
   const int64_t ntb = (a.N + TM - 1) / TM;
   a.nrg = (a.R_m + NW * RPW - 1) / (NW * RPW);
   const int64_t grid = a.nrg == 1 ? ntb : 8 * a.nrg * ((ntb + 7) / 8);
-  auto kern = a.bd ? dn_kernel<B, MT, RPW, NW, SC, true> : dn_kernel<B, MT, RPW, NW, SC, false>;
+  const bool core = a.tdepth || a.inj_e;
+  auto kern = a.bd ? (core ? dn_kernel<B, MT, RPW, NW, SC, true, true> : dn_kernel<B, MT, RPW, NW, SC, true, false>)
+                   : (core ? dn_kernel<B, MT, RPW, NW, SC, false, true> : dn_kernel<B, MT, RPW, NW, SC, false, false>);
   if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return -1;
@@ -1145,15 +1285,19 @@ int launch_dn(int B, const DNArgs& a, hipStream_t st) {
 }
 
 template <int B, int MT, bool SHARED, int RPW, bool BIAS>
-static int launch_looped_b(const LoopArgs& a, hipStream_t st) {
+static int launch_looped_b(const LoopArgs& a0, hipStream_t st) {
   auto kern = looped_kernel<B, MT, SHARED, RPW, BIAS>;
   static std::atomic<uint64_t> configured{0};
   if (set_lds_limit_once((const void*)kern, 163840, configured)) return -1;
+  LoopArgs a = a0;
+  int kmax = 0;
+  for (int c = 0; c < a.n_core; ++c) kmax = a.core[c].Kg > kmax ? a.core[c].Kg : kmax;
   const int TM = 16 * MT;
   const size_t dn_lds = 2 * (size_t)TM * DN_STAGE_COLS * 2;
-  const size_t g_lds = gu_lds(a.gu.R_ff, a.gu.Kg, MT);
+  const size_t g_lds = gu_lds(a.gu.R_ff, kmax, MT);
   size_t lds = g_lds > dn_lds ? g_lds : dn_lds;
-  const size_t r_end = looped_red_offset<MT>(a.gu.R_ff, a.gu.Kg) + (size_t)9 * TM * 4;
+  a.red_off = looped_red_offset<MT>(a.gu.R_ff, kmax);
+  const size_t r_end = a.red_off + (size_t)9 * TM * 4;
   lds = lds > r_end ? lds : r_end;
   if (lds > 163840) return -2;
   hipLaunchKernelGGL(kern, dim3((unsigned)((a.gu.N + TM - 1) / TM)), dim3(512), lds, st, a);
@@ -1162,8 +1306,9 @@ static int launch_looped_b(const LoopArgs& a, hipStream_t st) {
 
 template <int B, int MT, bool SHARED, int RPW>
 static int launch_looped_t(const LoopArgs& a, hipStream_t st) {
-  return (a.gu.bg || a.gu.bu || a.dn.bd) ? launch_looped_b<B, MT, SHARED, RPW, true>(a, st)
-                                         : launch_looped_b<B, MT, SHARED, RPW, false>(a, st);
+  bool bias = false;
+  for (int c = 0; c < a.n_core; ++c) bias = bias || a.core[c].bg || a.core[c].bu || a.core[c].bd;
+  return bias ? launch_looped_b<B, MT, SHARED, RPW, true>(a, st) : launch_looped_b<B, MT, SHARED, RPW, false>(a, st);
 }
 
 // The persistent looped block takes the shapes of the two-kernel path with MT = 4
@@ -1176,8 +1321,11 @@ bool looped_persistent_supported(int B, int d_model, int R_ff, int R_m, int Kg, 
 
 int launch_looped(int B, const LoopArgs& a, hipStream_t st) {
   if (a.gu.N == 0 || a.L <= 0) return 0;
-  if (gu_mt(a.gu.d_model) != 4) return -2;
-  const bool shared = a.gu.cg == a.gu.cu;
+  if (gu_mt(a.gu.d_model) != 4 || a.n_core < 1 || a.n_core > kMaxCore) return -2;
+  // one kernel shape for all core blocks: either every block shares its gate/up topology or none
+  const bool shared = a.core[0].cg == a.core[0].cu;
+  for (int c = 1; c < a.n_core; ++c)
+    if ((a.core[c].cg == a.core[c].cu) != shared) return -2;
   // four down rows per wave: the 32 rows of a 1024-wide model in one group, h staged once
   // (measured at the looped-block geometry: 1.50 ms against 1.58 with two rows per wave in
   // two groups and 1.87 with one row per wave in four)

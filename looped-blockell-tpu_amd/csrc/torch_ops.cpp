@@ -439,6 +439,83 @@ at::Tensor persistent_mlp_step(const at::Tensor& h, const at::Tensor& e, const a
   return cur;
 }
 
+// The looped application of the FFN core (looped_blockell/looping/looped_model.py:293-340 on its
+// FFN path): per iteration the injection (when e is given), the n_core blocks in order, then the
+// depth freeze (when depths is given, one entry per seq_len rows).  biases: empty, or
+// (b_gate, b_up, b_down) per block, each optional.
+at::Tensor looped_core(const at::Tensor& h_, const c10::optional<at::Tensor>& e_, const c10::optional<at::Tensor>& la_,
+                       const c10::optional<at::Tensor>& ld_, at::TensorList norm_scales, at::TensorList gate_values,
+                       at::TensorList gate_col_idx, at::TensorList up_values, at::TensorList up_col_idx,
+                       at::TensorList down_values, at::TensorList down_col_idx,
+                       const c10::List<c10::optional<at::Tensor>>& biases, int64_t L,
+                       const c10::optional<at::Tensor>& depths_, int64_t seq_len, double eps, bool persistent) {
+  const char* op = "looped_core";
+  at::Tensor x = check_x2d(h_, op);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const size_t n_core = norm_scales.size();
+  TORCH_CHECK(n_core >= 1 && n_core <= LBK_MAX_CORE_BLOCKS, "titan::looped_core: n_core must be in [1, ",
+              LBK_MAX_CORE_BLOCKS, "], got ", n_core);
+  TORCH_CHECK(gate_values.size() == n_core && gate_col_idx.size() == n_core && up_values.size() == n_core &&
+                  up_col_idx.size() == n_core && down_values.size() == n_core && down_col_idx.size() == n_core,
+              "titan::looped_core: all weight lists must have n_core entries");
+  TORCH_CHECK(biases.size() == 0 || biases.size() == 3 * n_core,
+              "titan::looped_core: biases must be empty or hold (b_gate, b_up, b_down) per core block");
+  TORCH_CHECK(L >= 0, "titan::looped_core: L must be >= 0");
+  const int64_t N = x.size(0), d_model = x.size(1);
+  std::vector<at::Tensor> keep;   // contiguous copies alive until the call is queued
+  std::vector<lbk_core_block> blocks(n_core);
+  for (size_t c = 0; c < n_core; ++c) {
+    at::Tensor vg = gate_values[c], cg = gate_col_idx[c], vu = up_values[c], cu = up_col_idx[c],
+               vd = down_values[c], cd = down_col_idx[c];
+    lbk_core_block& b = blocks[c];
+    b.gate = make_bell(vg, cg, op, "gate");
+    b.up = make_bell(vu, cu, op, "up");
+    b.down = make_bell(vd, cd, op, "down");
+    at::Tensor sc = norm_scales[c].to(x.device(), at::kFloat).contiguous();
+    TORCH_CHECK(sc.numel() == d_model, "titan::looped_core: norm scale ", c, " must have d_model elements");
+    b.norm_scale = sc.data_ptr<float>();
+    const int64_t d_ff = (int64_t)b.gate.R * b.gate.B;
+    at::Tensor bt[3];
+    if (biases.size()) {
+      bt[0] = opt_bias(biases.get(3 * c), d_ff, x, op, "b_gate");
+      bt[1] = opt_bias(biases.get(3 * c + 1), d_ff, x, op, "b_up");
+      bt[2] = opt_bias(biases.get(3 * c + 2), d_model, x, op, "b_down");
+    }
+    b.b_gate = fptr(bt[0]);
+    b.b_up = fptr(bt[1]);
+    b.b_down = fptr(bt[2]);
+    for (at::Tensor* t : {&vg, &cg, &vu, &cu, &vd, &cd, &sc, &bt[0], &bt[1], &bt[2]})
+      if (t->defined()) keep.push_back(*t);
+  }
+  at::Tensor e, la, ld, dep;
+  if (e_.has_value() && e_->defined()) {
+    e = check_x2d(*e_, op);
+    TORCH_CHECK(e.sizes() == x.sizes(), "titan::looped_core: e must match h, got ", e.sizes());
+    TORCH_CHECK(la_.has_value() && la_->defined() && ld_.has_value() && ld_->defined(),
+                "titan::looped_core: the injection needs log_A and log_dt");
+    la = la_->to(x.device(), at::kFloat).contiguous();
+    ld = ld_->to(x.device(), at::kFloat).contiguous();
+    TORCH_CHECK(la.numel() == d_model && ld.numel() == d_model,
+                "titan::looped_core: log_A and log_dt must have d_model elements");
+  }
+  if (depths_.has_value() && depths_->defined()) {
+    TORCH_CHECK(seq_len >= 1, "titan::looped_core: seq_len must be >= 1");
+    dep = depths_->to(x.device(), at::kInt).contiguous();
+    TORCH_CHECK(dep.numel() * seq_len >= N, "titan::looped_core: depths must cover every row (",
+                dep.numel(), " x seq_len ", seq_len, " < N = ", N, ")");
+  }
+  at::Tensor out = at::empty_like(x);
+  const size_t wsb = lbk_looped_core_workspace_bytes(N, (int32_t)d_model, (int32_t)n_core, blocks.data());
+  at::Tensor ws = wsb ? workspace(wsb, x) : at::Tensor();
+  auto fn = persistent ? lbk_looped_core_persistent_bf16 : lbk_looped_core_bf16;
+  LBK_CALL("looped_core",
+           fn(bf(x), e.defined() ? bf(e) : nullptr, la.defined() ? la.data_ptr<float>() : nullptr,
+              ld.defined() ? ld.data_ptr<float>() : nullptr, N, (int32_t)d_model, (int32_t)n_core, blocks.data(),
+              (float)eps, (int32_t)L, dep.defined() ? dep.data_ptr<int32_t>() : nullptr, seq_len, bfm(out),
+              wsb ? ws.data_ptr() : nullptr, wsb, cur_stream(x)));
+  return out;
+}
+
 // ------------------------------------------------------------------ ternary
 std::tuple<at::Tensor, at::Tensor> quantize_act_int8(const at::Tensor& x_) {
   at::Tensor x = check_x2d(x_, "quantize_act_int8");
@@ -778,6 +855,10 @@ TORCH_LIBRARY(titan, m) {
         "Tensor ci_up, Tensor v_down, Tensor ci_down, int L, float eps=1e-05) -> Tensor");
   m.def("looped_swiglu_launches(Tensor h, Tensor norm_scale, Tensor v_gate, Tensor ci_gate, Tensor v_up, "
         "Tensor ci_up, Tensor v_down, Tensor ci_down, int L, float eps=1e-05) -> Tensor");
+  m.def("looped_core(Tensor h, Tensor? e, Tensor? log_A, Tensor? log_dt, Tensor[] norm_scales, "
+        "Tensor[] gate_values, Tensor[] gate_col_idx, Tensor[] up_values, Tensor[] up_col_idx, "
+        "Tensor[] down_values, Tensor[] down_col_idx, Tensor?[] biases, int L, Tensor? depths=None, "
+        "int seq_len=1, float eps=1e-05, bool persistent=False) -> Tensor");
   m.def("rmsnorm(Tensor x, Tensor scale, float eps=1e-05) -> Tensor");
   m.def("rmsnorm_bwd(Tensor grad_out, Tensor x, Tensor scale, float eps=1e-05) -> (Tensor, Tensor)");
   m.def("diagonal_injection(Tensor h, Tensor e, Tensor log_A, Tensor log_dt) -> Tensor");
@@ -824,6 +905,7 @@ TORCH_LIBRARY_IMPL(titan, CUDA, m) {
   m.impl("looped_swiglu", &looped_swiglu);
   m.impl("looped_swiglu_persistent", &looped_swiglu_persistent);
   m.impl("looped_swiglu_launches", &looped_swiglu_launches);
+  m.impl("looped_core", &looped_core);
   m.impl("rmsnorm", &rmsnorm);
   m.impl("rmsnorm_bwd", &rmsnorm_bwd);
   m.impl("diagonal_injection", &diagonal_injection);
@@ -851,7 +933,8 @@ TORCH_LIBRARY_IMPL(titan, Autograd, m) {
        {"block_ell_swiglu_fwd", "block_ell_swiglu_fwd_with_intermediate", "block_ell_swiglu_bwd",
         "persistent_mlp_step", "block_ell_matmul", "block_ell_matmul_bwd", "block_ell_swiglu_bwd_ex",
         "block_ell_matmul_prepack", "block_ell_matmul_prepacked",
-        "looped_swiglu", "looped_swiglu_persistent", "looped_swiglu_launches", "rmsnorm", "rmsnorm_bwd",
+        "looped_swiglu", "looped_swiglu_persistent", "looped_swiglu_launches", "looped_core", "rmsnorm",
+        "rmsnorm_bwd",
         "block_ell_swiglu_fwd_bias", "block_ell_swiglu_bwd_bias", "looped_swiglu_bias",
         "block_ell_swiglu_prepack", "block_ell_swiglu_fwd_prepacked", "diagonal_injection", "diagonal_injection_bwd",
         "quantize_act_int8", "pack_ternary", "ternary_quantize_weights", "ternary_matmul",
@@ -934,6 +1017,11 @@ TORCH_LIBRARY_IMPL(titan, Meta, m) {
   m.impl("looped_swiglu_persistent", [](const at::Tensor& h, const at::Tensor&, const at::Tensor&, const at::Tensor&,
                              const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t,
                              double) { return at::empty_like(h); });
+  m.impl("looped_core",
+         [](const at::Tensor& h, const c10::optional<at::Tensor>&, const c10::optional<at::Tensor>&,
+            const c10::optional<at::Tensor>&, at::TensorList, at::TensorList, at::TensorList, at::TensorList,
+            at::TensorList, at::TensorList, at::TensorList, const c10::List<c10::optional<at::Tensor>>&, int64_t,
+            const c10::optional<at::Tensor>&, int64_t, double, bool) { return at::empty_like(h); });
   m.impl("looped_swiglu_launches", [](const at::Tensor& h, const at::Tensor&, const at::Tensor&, const at::Tensor&,
                              const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, int64_t,
                              double) { return at::empty_like(h); });

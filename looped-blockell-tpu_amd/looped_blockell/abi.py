@@ -47,6 +47,16 @@ class TernaryAcc(C.Structure):
                 ("gate_pre", C.c_void_p), ("up_pre", C.c_void_p)]
 
 
+LBK_MAX_CORE_BLOCKS = 8
+
+
+class CoreBlock(C.Structure):
+    """``lbk_core_block``: one core block of the looped core (norm scale, SwiGLU weights, biases)."""
+
+    _fields_ = [("norm_scale", C.c_void_p), ("gate", Bell), ("up", Bell), ("down", Bell),
+                ("b_gate", C.c_void_p), ("b_up", C.c_void_p), ("b_down", C.c_void_p)]
+
+
 # (name, restype, argtypes) for every entry point of include/lbk.h
 _P = C.c_void_p
 _I64 = C.c_int64
@@ -111,6 +121,11 @@ SIGNATURES = {
     "lbk_looped_swiglu_persistent_bf16": (C.c_int, [_P, _I64, _I32, _P, _F, _I32, _PB, _PB, _PB, _P, _P, _SZ,
                                                     _P]),
     "lbk_looped_swiglu_launches_bf16": (C.c_int, [_P, _I64, _I32, _P, _F, _I32, _PB, _PB, _PB, _P, _P, _SZ, _P]),
+    "lbk_looped_core_workspace_bytes": (_SZ, [_I64, _I32, _I32, C.POINTER(CoreBlock)]),
+    "lbk_looped_core_bf16": (C.c_int, [_P, _P, _P, _P, _I64, _I32, _I32, C.POINTER(CoreBlock), _F, _I32, _P, _I64,
+                                       _P, _P, _SZ, _P]),
+    "lbk_looped_core_persistent_bf16": (C.c_int, [_P, _P, _P, _P, _I64, _I32, _I32, C.POINTER(CoreBlock), _F, _I32,
+                                                  _P, _I64, _P, _P, _SZ, _P]),
     "lbk_quantize_act_int8": (C.c_int, [_P, _I64, _I32, _I64, _P, _P, _P]),
     "lbk_pack_ternary": (C.c_int, [_P, _I32, _I32, _I32, _P, _P]),
     "lbk_ternary_quantize_weights_bf16": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P]),

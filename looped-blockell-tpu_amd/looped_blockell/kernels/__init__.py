@@ -312,6 +312,22 @@ def persistent_mlp_step(h, e, log_A, log_dt, norm_scales, gate_values, gate_col_
                                      list(down_col_idx))
 
 
+def looped_core(h, e, log_A, log_dt, norm_scales, gate_values, gate_col_idx, up_values, up_col_idx, down_values,
+                down_col_idx, L: int, biases=None, depths=None, seq_len: int = 1, eps: float = 1e-5,
+                persistent: bool = False):
+    """``titan::looped_core``: L iterations of injection (``e`` optional) -> the n_core blocks
+    ``h += SwiGLU_c(RMSNorm_c(h))`` in order -> the depth freeze ``h = where(t < depth, h_new, h_agg)``
+    with one depth per ``seq_len`` rows (``depths`` optional), the state carried in fp32.
+    ``biases``: None or one ``(b_gate, b_up, b_down)`` triple (entries may be None) per block.
+    ``persistent`` runs all L iterations in one launch.  Not differentiable (see
+    ``looped_blockell.layers.LoopedCore`` for the training path)."""
+    _gpu(h, *gate_values, *down_values)
+    flat = [] if biases is None else [b for trip in biases for b in trip]
+    return ops().looped_core(h, e, log_A, log_dt, list(norm_scales), list(gate_values), list(gate_col_idx),
+                             list(up_values), list(up_col_idx), list(down_values), list(down_col_idx), flat, L,
+                             depths, seq_len, eps, persistent)
+
+
 def pin_weights_l2(weights) -> None:
     """Kept for API compatibility; HIP has no access-policy window (no-op)."""
     ops().pin_weights_l2(list(weights))

@@ -303,6 +303,46 @@ def looped_swiglu(h, norm_scale, gate, up, down, L: int, eps: float = 1e-5, stat
     return h
 
 
+def looped_core(h, e, log_A, log_dt, blocks, L: int, depths=None, seq_len: int = 1, eps: float = 1e-5,
+                state_round=None):
+    """The looped application of the FFN core: per iteration ``t < L``
+
+    * ``h_agg = h``
+    * ``h_new = diagonal_injection(h_agg, e, log_A, log_dt)`` (skipped when ``e`` is None)
+    * for each core block ``(norm_scale, gate, up, down, biases)`` in order:
+      ``h_new = h_new + SwiGLU(RMSNorm(h_new))``
+    * ``h = where(t < depths[n // seq_len], h_new, h_agg)`` per token row ``n``
+      (``depths`` None: every row runs all L iterations).
+
+    This is the scan body of ``looped_blockell/looping/looped_model.py:293-331`` (and the
+    PyTorch loop ``interop/pt_model.py:1441-1509``) restricted to its FFN path: the injection
+    (``:303``), ``n_core`` distinct pre-norm residual blocks (``:310-311``) with the MLP half of
+    ``looped_blockell/layers/transformer_block.py:83-84``, and the per-sequence depth freeze
+    ``active = step_idx < depths; h = where(active, h_new, h_agg)`` (``:330-331``).  Rows are
+    flattened tokens; ``depths`` holds one entry per run of ``seq_len`` consecutive rows (the
+    reference's per-sequence depths over ``[B, S]``).  ``state_round`` optionally rounds the
+    carried state after each core block.
+    """
+    h = np.asarray(h, dtype=np.float64)
+    N = h.shape[0]
+    if depths is not None:
+        tok_depth = np.repeat(np.asarray(depths, dtype=np.int64), seq_len)[:N]
+        assert tok_depth.shape[0] == N, "depths must cover every row"
+    for t in range(L):
+        h_agg = h
+        h_new = h_agg if e is None else diagonal_injection(h_agg, e, log_A, log_dt)
+        for (scale, gate, up, down, biases) in blocks:
+            y, *_ = swiglu_fwd(rmsnorm(h_new, scale, eps), gate, up, down, biases=biases)
+            h_new = h_new + y
+            if state_round is not None:
+                h_new = state_round(h_new)
+        if depths is None:
+            h = h_new
+        else:
+            h = np.where((t < tok_depth)[:, None], h_new, h_agg)
+    return h
+
+
 # --------------------------------------------------------------------------
 # backward of the SwiGLU FFN (derived from the forward's mathematics)
 # --------------------------------------------------------------------------
@@ -720,6 +760,9 @@ PINS = {
     "swiglu_bias_grads": "torch float64 autograd of the dense biased SwiGLU FFN (the three bias gradients)",
     "rmsnorm": "constant-vector closed form; unit-RMS invariance; scale linearity",
     "looped_swiglu": "L=0 identity; L=1 equals one block; L=2 equals composition",
+    "looped_core": "n_core=1 without injection or depths == looped_swiglu; one iteration == injection then "
+                   "the blocks in order (persistent_mlp_step); a row of depth d == L=d on that row (d=0 "
+                   "keeps h); planted mistakes (injection once, freeze at t <= depth, blocks reversed) differ",
     "diagonal_injection": "closed forms: log_A = -inf keeps h, log_dt = log(e - 1) gives dt = 1; torch's "
                           "DiagonalInjection formula in float64",
     "diagonal_injection_bwd": "torch float64 autograd of the injection (h, e, log_A, log_dt); finite differences",

@@ -203,3 +203,61 @@ def abi_swiglu_bwd(dy_t, x_t, g_t, u_t, h_t, gate_t, up_t, down_t, add_residual=
                                     ptr(dvs[1]), ptr(dvs[2]),
                                     ptr(ws), wsb, stream()), "swiglu_bwd")
     return dx, dvs[0], dvs[1], dvs[2]
+
+
+def core_blocks(rng, n_core, d_model, d_ff, B, density, bias=False, shared=False, sentinel_frac=0.0):
+    """n_core looped-core blocks as numpy: (norm_scale, gate, up, down, biases) with
+    gate/up/down = (values, col) (bf16-representable float32) and biases None or a triple."""
+    out = []
+    for _ in range(n_core):
+        g, u, d = ffn_weights(rng, d_model, d_ff, B, density, sentinel_frac=sentinel_frac)
+        if shared:
+            u = (u[0], g[1])
+        scale = (1.0 + 0.1 * rng.standard_normal(d_model)).astype(np.float32)
+        bs = None
+        if bias:
+            bs = tuple(O.bf16_round((0.05 * rng.standard_normal(n)).astype(np.float32)) for n in (d_ff, d_ff, d_model))
+        out.append((scale, g, u, d, bs))
+    return out
+
+
+def core_blocks_gpu(blocks):
+    """GPU tensors of core_blocks (the up weight shares the gate's column tensor where the
+    numpy columns are the same object)."""
+    res = []
+    for (scale, g, u, d, bs) in blocks:
+        vg, cg = gpu_weight(g)
+        vu = to_gpu_bf16(u[0])
+        cu = cg if u[1] is g[1] else to_gpu(u[1].astype(np.int32))
+        vd, cd = gpu_weight(d)
+        bt = None if bs is None else tuple(to_gpu(b) for b in bs)
+        res.append((to_gpu(scale), (vg, cg), (vu, cu), (vd, cd), bt))
+    return res
+
+
+def abi_looped_core(h_t, blocks_t, L, eps=1e-5, e_t=None, log_A_t=None, log_dt_t=None, depths_t=None, seq_len=1,
+                    persistent=False, out=None, expect=0):
+    """lbk_looped_core_bf16 (or the persistent form) through the C ABI; returns the output, or
+    the status when it is not the expected one (``expect``)."""
+    import torch
+    A = abi()
+    lib = A.load()
+    N, dm = h_t.shape
+    arr = (A.CoreBlock * max(1, len(blocks_t)))()
+    for c, (sc, g, u, d, bt) in enumerate(blocks_t):
+        arr[c].norm_scale = sc.data_ptr()
+        arr[c].gate = bell_struct(*g)
+        arr[c].up = bell_struct(*u)
+        arr[c].down = bell_struct(*d)
+        if bt is not None:
+            arr[c].b_gate, arr[c].b_up, arr[c].b_down = (b.data_ptr() if b is not None else None for b in bt)
+    out = torch.empty_like(h_t) if out is None else out
+    wsb = lib.lbk_looped_core_workspace_bytes(N, dm, len(blocks_t), arr)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=h_t.device)
+    fn = lib.lbk_looped_core_persistent_bf16 if persistent else lib.lbk_looped_core_bf16
+    st = fn(ptr(h_t), ptr(e_t), ptr(log_A_t), ptr(log_dt_t), N, dm, len(blocks_t), arr, C.c_float(eps), L,
+            ptr(depths_t), seq_len, ptr(out), ptr(ws), wsb, stream())
+    if st != expect:
+        A.check(st, "looped_core")
+        raise AssertionError(f"looped_core returned OK, expected status {expect}")
+    return out if st == 0 else st

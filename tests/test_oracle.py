@@ -314,6 +314,74 @@ def test_looped_composition():
     np.testing.assert_allclose(O.looped_swiglu(h, s, gate, up, down, L=2), two, atol=1e-12)
 
 
+def _core_blocks(g, n_core, B=4, dm=8, dff=16, bias=False):
+    out = []
+    for _ in range(n_core):
+        gate = (0.3 * g.standard_normal((dff // B, 1, B, B)), O.random_topology(dff // B, dm // B, 1, g))
+        up = (0.3 * g.standard_normal((dff // B, 1, B, B)), O.random_topology(dff // B, dm // B, 1, g))
+        down = (0.3 * g.standard_normal((dm // B, 2, B, B)), O.random_topology(dm // B, dff // B, 2, g))
+        bs = tuple(0.1 * g.standard_normal(n) for n in (dff, dff, dm)) if bias else None
+        out.append((1.0 + 0.2 * g.standard_normal(dm), gate, up, down, bs))
+    return out
+
+
+def test_looped_core_reduces_to_looped_swiglu_and_mlp_step():
+    g = rng(12)
+    dm = 8
+    h = g.standard_normal((5, dm))
+    blk = _core_blocks(g, 1)
+    s, gate, up, down, _ = blk[0]
+    # one block, no injection, no depths: the shared-weight looped block
+    np.testing.assert_allclose(O.looped_core(h, None, None, None, blk, L=3),
+                               O.looped_swiglu(h, s, gate, up, down, L=3), atol=1e-12)
+    # one iteration: the injection, then every core block in order (persistent_mlp_step)
+    blks = _core_blocks(g, 3, bias=True)
+    e = g.standard_normal((5, dm))
+    la, ld = g.standard_normal(dm), g.standard_normal(dm)
+    want = O.diagonal_injection(h, e, la, ld)
+    for (sc, gt, u, d, bs) in blks:
+        want = want + O.swiglu_fwd(O.rmsnorm(want, sc), gt, u, d, biases=bs)[0]
+    np.testing.assert_allclose(O.looped_core(h, e, la, ld, blks, L=1), want, atol=1e-12)
+    # two iterations: the injection again at the start of the second
+    two = O.diagonal_injection(want, e, la, ld)
+    for (sc, gt, u, d, bs) in blks:
+        two = two + O.swiglu_fwd(O.rmsnorm(two, sc), gt, u, d, biases=bs)[0]
+    np.testing.assert_allclose(O.looped_core(h, e, la, ld, blks, L=2), two, atol=1e-12)
+    np.testing.assert_array_equal(O.looped_core(h, e, la, ld, blks, L=0), h)
+
+
+def test_looped_core_depth_freeze_and_planted_mistakes():
+    g = rng(13)
+    dm, S = 8, 3
+    depths = np.array([0, 1, 4, 2, 7])
+    h = g.standard_normal((len(depths) * S, dm))
+    e = g.standard_normal(h.shape)
+    la, ld = g.standard_normal(dm), g.standard_normal(dm)
+    blks = _core_blocks(g, 2)
+    L = 4
+    got = O.looped_core(h, e, la, ld, blks, L=L, depths=depths, seq_len=S)
+    # each sequence equals the loop run for exactly min(depth, L) iterations on its rows
+    for b, dep in enumerate(depths):
+        rows = slice(b * S, (b + 1) * S)
+        want = O.looped_core(h[rows], e[rows], la, ld, blks, L=min(dep, L))
+        np.testing.assert_allclose(got[rows], want, atol=1e-12)
+    np.testing.assert_array_equal(got[0:S], h[0:S])          # depth 0 keeps h
+    # a ragged last sequence (depths cover N rows in runs of seq_len)
+    got2 = O.looped_core(h[:-1], e[:-1], la, ld, blks, L=L, depths=depths, seq_len=S)
+    np.testing.assert_allclose(got2, got[:-1], atol=1e-12)
+
+    # planted mistakes are caught: the injection applied only once, the freeze at t <= depth,
+    # the blocks in reverse order
+    def once(h0):
+        x = O.diagonal_injection(h0, e, la, ld)
+        return O.looped_core(x, None, None, None, blks, L=L, depths=depths, seq_len=S)
+    assert np.abs(once(h) - got).max() > 1e-3
+    late = O.looped_core(h, e, la, ld, blks, L=L, depths=depths + 1, seq_len=S)
+    assert np.abs(late - got).max() > 1e-3
+    rev = O.looped_core(h, e, la, ld, blks[::-1], L=L, depths=depths, seq_len=S)
+    assert np.abs(rev - got).max() > 1e-3
+
+
 # ---------------------------------------------------------------- ternary
 
 def test_ternary_quantize_hand_block():
