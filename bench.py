@@ -480,18 +480,76 @@ def bench_looped(steps, warmup, device):
         ms_s, _ = time_steps(lambda i: kernels.looped_swiglu_launches(hs, scale, *g, *u, *d, L=w["L"], eps=1e-5),
                              steps, warmup)
         small[str(n)] = dict(persistent_ms=ms_p, launches_ms=ms_s)
+    persistent = dict(workload="weight packing + one persistent launch: a workgroup owns a 64-token block for all "
+                               "L iterations (titan::looped_swiglu_persistent)",
+                      ms_per_step=ms, value=tf, unit="TFLOP/s", frac_of_bf16_peak=tf / PEAK_BF16_TFLOPS,
+                      kernel_ms_avg=sum(per) / len(per))
+    launches = dict(workload="weight packing + an fp32 copy + 2L launches (gate/up and down per iteration; the "
+                             "default of titan::looped_swiglu)",
+                    ms_per_step=ms_l, value=tf_l, unit="TFLOP/s", frac_of_bf16_peak=tf_l / PEAK_BF16_TFLOPS,
+                    kernel_ms_avg=sum(per_l) / len(per_l))
+    # the line's value is the faster of the two forms, named in "mode"; both are reported
+    best, mode = (persistent, "persistent") if ms <= ms_l else (launches, "launches")
     return dict(workload="looped RMSNorm -> SwiGLU -> residual, L=8 shared weights, d_model=1024 d_ff=4096 B=32 "
-                         "density=0.25 N=32x512 (weight packing + one persistent launch: a workgroup owns a "
-                         "64-token block for all L iterations)",
-                ms_per_step=ms, value=tf, unit="TFLOP/s", tokens_per_s=w["N"] / (ms * 1e-3),
-                token_iterations_per_s=w["N"] * w["L"] / (ms * 1e-3), frac_of_bf16_peak=tf / PEAK_BF16_TFLOPS,
-                kernel_ms_avg=sum(per) / len(per),
-                launches=dict(workload="the same looped block as weight packing + an fp32 copy + 2L launches "
-                                       "(gate/up and down per iteration; the default of titan::looped_swiglu)",
-                              ms_per_step=ms_l, value=tf_l, unit="TFLOP/s", frac_of_bf16_peak=tf_l / PEAK_BF16_TFLOPS,
-                              kernel_ms_avg=sum(per_l) / len(per_l)),
+                         "density=0.25 N=32x512 (value: the faster of the persistent launch and the per-iteration "
+                         "launches, named in mode)",
+                mode=mode, ms_per_step=best["ms_per_step"], value=best["value"], unit="TFLOP/s",
+                tokens_per_s=w["N"] / (best["ms_per_step"] * 1e-3),
+                token_iterations_per_s=w["N"] * w["L"] / (best["ms_per_step"] * 1e-3),
+                frac_of_bf16_peak=best["frac_of_bf16_peak"], kernel_ms_avg=best["kernel_ms_avg"],
+                persistent=persistent, launches=launches,
                 fewer_tokens=dict(workload="the same looped block (L=8) on the first N tokens, ms per call",
                                   by_tokens=small))
+
+
+def bench_looped_core(steps, warmup, device):
+    """The looped core (titan::looped_core): per iteration the diagonal injection, n_core = 2 distinct
+    blocks and the per-sequence depth freeze, at the looped-block geometry with L = 4 (eight FFN
+    applications per token at full depth, as the L = 8 shared-weight line)."""
+    import torch
+    from looped_blockell import kernels
+    w = dict(WORKLOADS["looped"])
+    n_core, L, S = 2, 4, 512
+    nseq = w["N"] // S
+    gen = torch.Generator(device=device).manual_seed(w["seed"] + 7)
+    blocks = [make_ffn(w, device, gen) for _ in range(n_core)]
+    h = torch.randn(w["N"], w["d_model"], generator=gen, device=device).to(torch.bfloat16)
+    e = torch.randn(w["N"], w["d_model"], generator=gen, device=device).to(torch.bfloat16)
+    la = torch.zeros(w["d_model"], device=device)
+    ld = torch.full((w["d_model"],), 0.3, device=device)
+    scales = [torch.ones(w["d_model"], device=device) for _ in range(n_core)]
+    full = torch.full((nseq,), L, dtype=torch.int32, device=device)
+    mixed = (torch.arange(nseq, device=device) % L + 1).to(torch.int32)
+    per_app = nonzero_flops(dict(w, L=1))   # one FFN application over all tokens
+
+    def call(depths, persistent):
+        return kernels.looped_core(h, e, la, ld, scales, [b[0][0] for b in blocks], [b[0][1] for b in blocks],
+                                   [b[1][0] for b in blocks], [b[1][1] for b in blocks], [b[2][0] for b in blocks],
+                                   [b[2][1] for b in blocks], L, depths=depths, seq_len=S, persistent=persistent)
+
+    res = {}
+    for name, depths in (("full_depth", full), ("mixed_depths", mixed)):
+        # FLOPs of the applications the rows actually run (a frozen row does no work)
+        apps = float(torch.clamp(depths, max=L).sum().item()) * S / w["N"] * n_core
+        flops = per_app * apps
+        sub = {}
+        for form, persistent in (("launches", False), ("persistent", True)):
+            ms, per = time_steps(lambda i: call(depths, persistent), steps, warmup)
+            sub[form] = dict(ms_per_step=ms, value=flops / (ms * 1e-3) / 1e12, unit="TFLOP/s",
+                             frac_of_bf16_peak=flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                             kernel_ms_avg=sum(per) / len(per))
+        sub["ffn_applications_per_token"] = apps
+        sub["flops"] = flops
+        res[name] = sub
+    best = min(("launches", "persistent"), key=lambda f: res["full_depth"][f]["ms_per_step"])
+    b = res["full_depth"][best]
+    return dict(workload="looped core: per iteration injection (decay*h + dt*e) -> 2 distinct pre-norm SwiGLU "
+                         "blocks -> per-sequence depth freeze; d_model=1024 d_ff=4096 B=32 density=0.25 "
+                         "N=32x512 tokens, L=4 (full_depth: every sequence runs 4 iterations = 8 FFN applications "
+                         "per token; mixed_depths: sequence depths 1..4, frozen rows skipped); value: the faster "
+                         "form at full depth, named in mode",
+                mode=best, ms_per_step=b["ms_per_step"], value=b["value"], unit="TFLOP/s",
+                frac_of_bf16_peak=b["frac_of_bf16_peak"], **res)
 
 
 def bench_decode(steps, warmup, device):
@@ -673,7 +731,7 @@ def main():
                          "headline fields are then null)")
     ap.add_argument("--only", default="",
                     help="comma list of extra workloads to run: shared,backward,matmul,matmul_backward,ternary,"
-                         "looped,decode,topology,formats")
+                         "looped,looped_core,decode,topology,formats")
     ap.add_argument("--no-fewer-tokens", action="store_true",
                     help="skip the fewer-token runs of the headline and looped workloads (profiling: the kernel "
                          "statistics then hold the named workload's launches only)")
@@ -705,13 +763,14 @@ def main():
     extra = {}
     if not args.only_main:
         todo = [s for s in args.only.split(",") if s] or ["shared", "backward", "matmul", "matmul_backward", "ternary",
-                                                           "looped", "decode", "topology", "formats"]
+                                                           "looped", "looped_core", "decode", "topology", "formats"]
         fns = dict(shared=bench_bf16_shared, backward=bench_bf16_backward, matmul=bench_matmul,
                    matmul_backward=bench_matmul_backward,
-                   ternary=bench_ternary, looped=bench_looped, decode=bench_decode, topology=bench_topology,
+                   ternary=bench_ternary, looped=bench_looped, looped_core=bench_looped_core, decode=bench_decode,
+                   topology=bench_topology,
                    formats=bench_formats)
         for name in todo:
-            st = max(5, args.steps // (4 if name == "looped" else 1))
+            st = max(5, args.steps // (4 if name in ("looped", "looped_core") else 1))
             try:
                 extra[name] = fns[name](st, max(2, args.warmup), device)
             except Exception as e:  # report, keep the headline line
