@@ -151,7 +151,7 @@ enum MatmulPath { MM_ROWBLOCK = 0, MM_LIN = 1, MM_STAGED = 2 };
 static MatmulPath matmul_path(int32_t in_features, const lbk_bell* w) {
   if (w->B != 16 && w->B != 32) return MM_ROWBLOCK;
   if (lin_supported(w->B, in_features, w->R, w->K)) return MM_LIN;
-  if (w->K >= 1 && w->K <= 63 && w->R >= 1 && in_features % 8 == 0) return MM_STAGED;
+  if (w->K >= 1 && w->K <= 128 && w->R >= 1 && in_features % 8 == 0) return MM_STAGED;
   return MM_ROWBLOCK;
 }
 

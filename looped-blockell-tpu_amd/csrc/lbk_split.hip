@@ -543,10 +543,12 @@ __device__ __forceinline__ void inject_cw(float (&o)[CW], const uint16_t* __rest
 // a row in slot order; a row with an odd hit count gets one padding position on
 // the packed zero tile, so a two-slot ring consumes every row with the same
 // slot parity.  pcnt[rho] is the padded count of row rho, tot their sum (even).
-// A stage holds at most RPW * (Kd + 1) <= 256 positions.
-template <int RPW>
+// A stage holds at most RPW * (Kd + 1) <= 64 * NV positions: NV = 4 for up to 64 slots per row
+// (RPW <= 2, or RPW = 4 with Kd <= 63), 5 for up to 128 (RPW <= 2).
+template <int KC> constexpr int dn_list_words() { return KC == 1 ? 4 : 5; }
+template <int RPW, int NV>
 struct FetchList {
-  int v[4];
+  int v[NV];
   int pcnt[RPW];
   int tot;
 };
@@ -557,13 +559,14 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
 
 // write `val` of the lanes in `m` (in lane order) to positions base, base+1, ...
 // of the list; positions outside [base, base + popcount(m)) keep their values
-__device__ __forceinline__ void list_scatter(int (&v)[4], uint64_t m, int base, int val, int lane) {
+template <int NV>
+__device__ __forceinline__ void list_scatter(int (&v)[NV], uint64_t m, int base, int val, int lane) {
   const int cnt = __builtin_popcountll(m);
   if (cnt == 0) return;
   const int rank = lanes_below(m);
   const bool src = (m >> lane) & 1;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int t = 0; t < NV; ++t) {
     const int lo = base - 64 * t, hi = base + cnt - 64 * t;   // range of this target, in its lanes
     if (hi <= 0 || lo >= 64) continue;
     const int clo = lo > 0 ? lo : 0, chi = hi < 64 ? hi : 64;
@@ -579,32 +582,44 @@ __device__ __forceinline__ void list_scatter(int (&v)[4], uint64_t m, int base, 
   }
 }
 
-__device__ __forceinline__ void list_set(int (&v)[4], int q, int val, int lane) {
+template <int NV>
+__device__ __forceinline__ void list_set(int (&v)[NV], int q, int val, int lane) {
   const int t = q >> 6, l = q & 63;
 #pragma unroll
-  for (int u = 0; u < 4; ++u)
+  for (int u = 0; u < NV; ++u)
     if (t == u && lane == l) v[u] = val;
 }
 
-__device__ __forceinline__ int list_get(const int (&v)[4], int q) {
+template <int NV>
+__device__ __forceinline__ int list_get(const int (&v)[NV], int q) {
   const int l = q & 63, t = q >> 6;
-  const int e0 = __builtin_amdgcn_readlane(v[0], l), e1 = __builtin_amdgcn_readlane(v[1], l);
-  const int e2 = __builtin_amdgcn_readlane(v[2], l), e3 = __builtin_amdgcn_readlane(v[3], l);
-  return t == 0 ? e0 : (t == 1 ? e1 : (t == 2 ? e2 : e3));
+  int r = __builtin_amdgcn_readlane(v[0], l);
+#pragma unroll
+  for (int u = 1; u < NV; ++u) {
+    const int e = __builtin_amdgcn_readlane(v[u], l);
+    r = t == u ? e : r;
+  }
+  return r;
 }
 
-template <int RPW>
-__device__ __forceinline__ void dn_build(FetchList<RPW>& L, int c0, int ncb, const int (&colreg)[RPW], int wrow0,
-                                         int Kd, int ztile, int lane) {
+// the fetch list of the stage covering column blocks c0 .. c0 + ncb - 1: lane l of colreg[rho][kc]
+// holds the column of slot 64 kc + l of the wave's row rho (-1 beyond Kd)
+template <int RPW, int KC, int NV>
+__device__ __forceinline__ void dn_build(FetchList<RPW, NV>& L, int c0, int ncb, const int (&colreg)[RPW][KC],
+                                         int wrow0, int Kd, int ztile, int lane) {
   int tot = 0;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) L.v[t] = 0;
+  for (int t = 0; t < NV; ++t) L.v[t] = 0;
 #pragma unroll
   for (int rho = 0; rho < RPW; ++rho) {
-    const int cb = colreg[rho] - c0;
-    const uint64_t m = __ballot(cb >= 0 && cb < ncb);
-    const int cnt = __builtin_popcountll(m);
-    list_scatter(L.v, m, tot, (((wrow0 + rho) * Kd + lane) << 6) | (cb & 63), lane);
+    int cnt = 0;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const int cb = colreg[rho][kc] - c0;
+      const uint64_t m = __ballot(cb >= 0 && cb < ncb);
+      list_scatter(L.v, m, tot + cnt, (((wrow0 + rho) * Kd + 64 * kc + lane) << 6) | (cb & 63), lane);
+      cnt += __builtin_popcountll(m);
+    }
     if (cnt & 1) list_set(L.v, tot + cnt, ztile << 6, lane);
     L.pcnt[rho] = cnt + (cnt & 1);
     tot += L.pcnt[rho];
@@ -620,7 +635,7 @@ __device__ __forceinline__ void dn_build(FetchList<RPW>& L, int c0, int ncb, con
 // of dn_smem (row stride GUPanel<MT>::ROWB), for the next iteration's gate/up phase; red holds
 // (NW + 1) * 16 * MT floats for the per-token sums of squares.
 template <int B, int MT, int RPW, int NW, bool NORMOUT = false, bool BIAS = false, int SC = DN_STAGE_COLS,
-          bool CORE = false>
+          bool CORE = false, int KC = 1>
 __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, unsigned char* dn_smem,
                                         uint16_t* out, int tid, const float* norm_scale = nullptr,
                                         float eps = 0.f, float* red = nullptr) {
@@ -649,11 +664,14 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
   const u32x4* pd = static_cast<const u32x4*>(a.pd);
   const int ztile = a.R_m * a.Kd;   // packed zero tile
 
-  int colreg[RPW];
+  // lane l of colreg[rho][kc]: the column of slot 64 kc + l of row rho (-1 beyond the row's slots)
+  int colreg[RPW][KC];
 #pragma unroll
   for (int rho = 0; rho < RPW; ++rho) {
     const int rm = row0 + w * RPW + rho;
-    colreg[rho] = (rm < a.R_m && lane < a.Kd) ? a.cd[(int64_t)rm * a.Kd + lane] : -1;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+      colreg[rho][kc] = (rm < a.R_m && 64 * kc + lane < a.Kd) ? a.cd[(int64_t)rm * a.Kd + 64 * kc + lane] : -1;
   }
 
   f32x4 acc[RPW][MT][CW];
@@ -696,7 +714,8 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
     int cb;
   };
   const uint32_t f16 = pfrag16_off(lane);
-  FetchList<RPW> cur, nxt;
+  constexpr int NV = dn_list_words<KC>();
+  FetchList<RPW, NV> cur, nxt;
   // position q of the stream made of the current stage's list followed by the
   // next stage's; beyond both, the zero tile
   auto fetch = [&](Slot& S, int q) {
@@ -732,8 +751,8 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
   const bool any_rows = (row0 + w * RPW < a.R_m) && a.Kd > 0;
   Slot S0, S1;
   nxt.tot = 0;
-  dn_build<RPW>(cur, 0, (C < G ? C : G), colreg, row0 + w * RPW, a.Kd, ztile, lane);
-  if (nstages > 1) dn_build<RPW>(nxt, G, (C - G) < G ? (C - G) : G, colreg, row0 + w * RPW, a.Kd, ztile, lane);
+  dn_build<RPW, KC, NV>(cur, 0, (C < G ? C : G), colreg, row0 + w * RPW, a.Kd, ztile, lane);
+  if (nstages > 1) dn_build<RPW, KC, NV>(nxt, G, (C - G) < G ? (C - G) : G, colreg, row0 + w * RPW, a.Kd, ztile, lane);
   stage_fetch(0);
   stage_store(0);
   bool ring_ok = false;   // S0/S1 hold positions 0 and 1 of the current stage
@@ -771,7 +790,7 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
     nxt.tot = 0;
     if (s + 2 < nstages) {
       const int c2 = (s + 2) * G;
-      dn_build<RPW>(nxt, c2, (C - c2) < G ? (C - c2) : G, colreg, row0 + w * RPW, a.Kd, ztile, lane);
+      dn_build<RPW, KC, NV>(nxt, c2, (C - c2) < G ? (C - c2) : G, colreg, row0 + w * RPW, a.Kd, ztile, lane);
     }
     __syncthreads();
   }
@@ -923,7 +942,7 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
 
 // CORE: the looped core's state update (depth mask, fused injection); the other instantiations
 // carry none of its code
-template <int B, int MT, int RPW, int NW, int SC, bool BIAS, bool CORE>
+template <int B, int MT, int RPW, int NW, int SC, bool BIAS, bool CORE, int KC>
 __global__ __launch_bounds__(64 * NW, 1) void dn_kernel(DNArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char dn_smem[];   // two stages
   // workgroup -> (token block, row group).  With several row groups, the groups of one token
@@ -955,7 +974,7 @@ __global__ __launch_bounds__(64 * NW, 1) void dn_kernel(DNArgs a) {
     }
     return;
   }
-  dn_tile<B, MT, RPW, NW, false, BIAS, SC, CORE>(a, tb, rg, dn_smem, a.out, (int)threadIdx.x);
+  dn_tile<B, MT, RPW, NW, false, BIAS, SC, CORE, KC>(a, tb, rg, dn_smem, a.out, (int)threadIdx.x);
 }
 
 // ===========================================================================
@@ -1120,7 +1139,7 @@ static int gu_slices(int64_t ntb, int R_ff) {
 bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int Kd) {
   if (B != 16 && B != 32) return false;
   if (Kg != Ku || Kg < 1) return false;               // gate and up stream in lockstep
-  if (Kd > 64) return false;                          // one lane per slot of a down row
+  if (Kd > 128) return false;                         // one or two slot chunks of 64 lanes per down row
   if (d_model % 128) return false;                    // swizzled panel rows
   const int mt = gu_mt(d_model);
   if (mt == 0 || gu_lds(R_ff, Kg, mt) > 163840 || (int64_t)R_ff * Kg > 512 * GU_CT_MAX) return false;
@@ -1237,8 +1256,8 @@ int launch_lin(int B, const GUArgs& a0, hipStream_t st) {
   return -2;
 }
 
-template <int B, int MT, int RPW, int NW, int SC>
-static int launch_dn_t(const DNArgs& a0, hipStream_t st) {
+template <int B, int MT, int RPW, int NW, int SC, int KC>
+static int launch_dn_k(const DNArgs& a0, hipStream_t st) {
   const int TM = 16 * MT;
   constexpr size_t lds = 2 * (size_t)TM * SC * 2;   // two stages
   DNArgs a = a0;
@@ -1246,13 +1265,22 @@ static int launch_dn_t(const DNArgs& a0, hipStream_t st) {
   a.nrg = (a.R_m + NW * RPW - 1) / (NW * RPW);
   const int64_t grid = a.nrg == 1 ? ntb : 8 * a.nrg * ((ntb + 7) / 8);
   const bool core = a.tdepth || a.inj_e;
-  auto kern = a.bd ? (core ? dn_kernel<B, MT, RPW, NW, SC, true, true> : dn_kernel<B, MT, RPW, NW, SC, true, false>)
-                   : (core ? dn_kernel<B, MT, RPW, NW, SC, false, true> : dn_kernel<B, MT, RPW, NW, SC, false, false>);
+  auto kern = a.bd ? (core ? dn_kernel<B, MT, RPW, NW, SC, true, true, KC>
+                           : dn_kernel<B, MT, RPW, NW, SC, true, false, KC>)
+                   : (core ? dn_kernel<B, MT, RPW, NW, SC, false, true, KC>
+                           : dn_kernel<B, MT, RPW, NW, SC, false, false, KC>);
   if (lds > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return -1;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * NW), lds, st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// rows with up to 64 slots take one lane per slot; up to 128 (the reference's tile-16 layers at
+// density 1.0 and d_ff 2048) two slot chunks per lane
+template <int B, int MT, int RPW, int NW, int SC>
+static int launch_dn_t(const DNArgs& a, hipStream_t st) {
+  return a.Kd > 64 ? launch_dn_k<B, MT, RPW, NW, SC, 2>(a, st) : launch_dn_k<B, MT, RPW, NW, SC, 1>(a, st);
 }
 
 // One down row per wave (a workgroup covers DN_WAVES rows; the row groups of one token block

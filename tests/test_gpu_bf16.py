@@ -42,6 +42,8 @@ def test_matmul_parity(gpu, B, N):
     (4096, 1024, 32, 32, 130, "staged"),        # the headline down shape
     (96, 64, 32, 2, 33, "staged"),              # in_features not a multiple of 128
     (4096, 512, 16, 40, 17, "staged"),
+    (2048, 512, 16, 128, 300, "staged"),        # 128 slots per row: two slot chunks per lane
+    (4096, 512, 16, 129, 40, "row-block"),      # beyond 128 slots
     (256, 256, 64, 2, 40, "row-block"),         # B = 64
 ])
 def test_matmul_ws_paths(gpu, case):
@@ -171,13 +173,14 @@ def test_swiglu_with_intermediates(gpu, case):
         assert rel <= TOL, f"{name}: rel {rel} abs {ab}"
 
 
-@pytest.mark.parametrize("Kd", [63, 64, 65])
+@pytest.mark.parametrize("Kd", [63, 64, 65, 127, 128, 129])
 @pytest.mark.parametrize("case", [(256, 1024, 16), (128, 512, 16), (1024, 4096, 32)])
 def test_swiglu_duplicate_and_empty_columns(gpu, case, Kd):
     """Rows that name one column block several times sum every copy (as the oracle's
     per-slot sum does); a down row whose slots all fall in the first LDS stage
     gives that stage a full hit list; empty rows give zeros.  Kd <= 64 runs the
-    two-kernel split path, Kd = 65 the row-block path."""
+    two-kernel split path with one slot per lane, Kd <= 128 with two, Kd = 129 the row-block
+    path."""
     d_model, d_ff, B = case
     _say(f"swiglu duplicate columns {case} Kd={Kd}")
     rng = np.random.default_rng(21)
@@ -190,10 +193,39 @@ def test_swiglu_duplicate_and_empty_columns(gpu, case, Kd):
     dc[0, :] = rng.integers(0, min(Cf, 256 // B), size=Kd)   # row 0: all slots in the first stage
     d = (dv, dc)
     x = T.act(rng, 70, d_model)
-    out, *_ = T.abi_swiglu(T.to_gpu_bf16(x), T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d), add_residual=True)
+    gw, uw, dw = T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d)
+    assert T.swiglu_path(70, d_model, gw, uw, dw) == ("split" if Kd <= 128 else "rowblock")
+    out, *_ = T.abi_swiglu(T.to_gpu_bf16(x), gw, uw, dw, add_residual=True)
     f64 = lambda w: (w[0].astype(np.float64), w[1])
     ref, *_ = O.swiglu_fwd(x.astype(np.float64), f64(g), f64(u), f64(d), add_residual=True)
     rel, ab = T.rel_err(T.to_np(out), ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
+@pytest.mark.parametrize("N", [8192 + 5, 300])
+def test_reference_default_layer_geometry(gpu, N):
+    """The reference's default layer at its ablation geometry (configs/ablation.yaml: d_model 512,
+    d_ff 2048, tile 16, initial density 1.0 -> K_gate = 32, K_down = 128) on the two-kernel path:
+    the down kernel with two slot chunks per lane and two rows per wave (8192 + 5 tokens), rows 0
+    and 1 (one wave's) with all 128 slots in the first stage (258 list positions), and the
+    fewer-token down shapes (300 tokens); the gate/up panel with its 32 K table filling the LDS."""
+    d_model, d_ff, B = 512, 2048, 16
+    _say(f"reference default layer d512 ff2048 B16 density 1.0 N={N}")
+    rng = np.random.default_rng(512 + N)
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 1.0)
+    assert d[1].shape[1] == 128 and g[1].shape[1] == 32
+    dc = d[1]
+    dc[0, :] = rng.integers(0, 512 // B, size=128)          # all in the first 512-column stage
+    dc[1, :] = rng.integers(0, 512 // B, size=128)
+    dc[5, 3] = -1                                           # a dead slot
+    x = T.act(rng, N, d_model)
+    gw, uw, dw = T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d)
+    assert T.swiglu_path(N, d_model, gw, uw, dw) == "split"
+    out = T.to_np(T.abi_swiglu(T.to_gpu_bf16(x), gw, uw, dw, add_residual=True)[0])
+    rows = np.concatenate([np.sort(rng.choice(N, min(N, 160), replace=False)), [0, N - 1]])
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref, *_ = O.swiglu_fwd(x[rows].astype(np.float64), f64(g), f64(u), f64(d), add_residual=True)
+    rel, ab = T.rel_err(out[rows], ref)
     assert rel <= TOL, f"rel {rel} abs {ab}"
 
 
