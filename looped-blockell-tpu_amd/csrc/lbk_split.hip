@@ -75,7 +75,8 @@ __device__ __forceinline__ uint32_t k16_addr(uint32_t lbase, int cb, int g, int 
 
 // gate/up ring depth (positions in flight + 1)
 constexpr int GU_RING = 4;
-// column-table entries per thread (R_ff * K <= 512 * GU_CT_MAX)
+// column-table entries per thread loaded beside the prologue's other loads (a larger table loads
+// the rest in further rounds before the panel barrier)
 constexpr int GU_CT_MAX = 8;
 
 // gate/up panel row stride: 2048 bytes (MT = 4, d_model <= 1024) or 4096 (MT = 2)
@@ -112,30 +113,39 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
   const int64_t d_ff = (int64_t)a.R_ff * B;
   const int K = a.Kg;                        // == a.Ku >= 1
   const int64_t ztile = (int64_t)a.R_ff * K; // index of the packed zero tile
-  // column table after the panel: (gate col, up col) per (row of the slice, slot); dead -> 0
-  int2* ctab = reinterpret_cast<int2*>(smem + (size_t)TM * ROWB);
+  // column table after the panel: (gate col, up col) per (row of the slice, slot) as one byte each
+  // (d_model <= 2048, so at most 128 input column blocks); dead -> 0
+  uint16_t* ctab = reinterpret_cast<uint16_t*>(smem + (size_t)TM * ROWB);
 
-  // ---- column table (at most GU_CT_MAX entries per thread): loads at clamped addresses,
-  // all issued with the panel loads, stored after them
+  // ---- column table: the first GU_CT_MAX entries per thread are loaded (at clamped addresses)
+  // with the panel loads and stored after them; a larger table loads the rest in further rounds
   const int nct = nrs * K;
   const int64_t cbase = (int64_t)r_lo * K;
   int2 ctv[GU_CT_MAX];
-  auto ctab_fetch = [&]() {
+  auto ctab_fetch_at = [&](int base) {
 #pragma unroll
     for (int u = 0; u < GU_CT_MAX; ++u) {
-      const int e = tid + NT * u;
+      const int e = base + tid + NT * u;
       const int64_t ec = cbase + (e < nct ? e : 0);
       ctv[u] = make_int2(a.cg[ec], a.cu[ec]);
     }
   };
-  auto ctab_store = [&]() {
+  auto ctab_store_at = [&](int base) {
 #pragma unroll
     for (int u = 0; u < GU_CT_MAX; ++u) {
-      const int e = tid + NT * u;
+      const int e = base + tid + NT * u;
       int cg = ctv[u].x, cu = ctv[u].y;
       cg = (cg >= 0 && cg < cin) ? cg : 0;
       cu = (cu >= 0 && cu < cin) ? cu : 0;
-      if (e < nct) ctab[e] = make_int2(cg, cu);
+      if (e < nct) ctab[e] = (uint16_t)(cg | (cu << 8));
+    }
+  };
+  auto ctab_fetch = [&]() { ctab_fetch_at(0); };
+  auto ctab_store = [&]() {
+    ctab_store_at(0);
+    for (int base = NT * GU_CT_MAX; base < nct; base += NT * GU_CT_MAX) {
+      ctab_fetch_at(base);
+      ctab_store_at(base);
     }
   };
 
@@ -168,9 +178,9 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
     S.cg = live ? el : -1;   // table entry until fetch_c replaces it by columns
   };
   auto fetch_c = [&](GUSlot<B>& S) {
-    const int2 c = ctab[S.cg >= 0 ? S.cg : 0];
-    S.cg = c.x;
-    S.cu = c.y;
+    const uint32_t c = ctab[S.cg >= 0 ? S.cg : 0];
+    S.cg = (int)(c & 0xffu);
+    S.cu = (int)(c >> 8);
     if (++rk == KP) {
       rk = 0;
       ++rn;
@@ -984,7 +994,7 @@ __global__ __launch_bounds__(64 * NW, 1) void dn_kernel(DNArgs a) {
 // sums of squares of the down phase's normalisation (9 * 16 * MT floats)
 template <int MT>
 __host__ __device__ inline size_t looped_red_offset(int R_ff, int K) {
-  return (size_t)16 * MT * GUPanel<MT>::ROWB + (((size_t)R_ff * K * 8 + 255) & ~(size_t)255);
+  return (size_t)16 * MT * GUPanel<MT>::ROWB + (((size_t)R_ff * K * 2 + 255) & ~(size_t)255);
 }
 // looped_kernel<B, MT, SHARED, RPW>: workgroup tb owns token block tb (16 * MT tokens) for all L
 // iterations of the looped core: it copies its rows of h_in into the fp32 state (with the first
@@ -1121,7 +1131,8 @@ __global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t* __rest
 static int gu_mt(int d_model) { return d_model <= 1024 ? 4 : (d_model <= 2048 ? 2 : 0); }
 
 static size_t gu_lds(int R_ff, int K, int mt) {
-  return (size_t)16 * mt * (8192 / mt) + (size_t)R_ff * K * 8;   // panel (128 KB) + column table
+  // panel (128 KB) + column table (two bytes per entry: up to 16384 entries)
+  return (size_t)16 * mt * (8192 / mt) + (((size_t)R_ff * K * 2 + 15) & ~(size_t)15);
 }
 
 // Row slices per token block for the gate/up kernels: with fewer token blocks than CUs, each
@@ -1142,7 +1153,7 @@ bool split_supported(int B, int d_model, int R_ff, int R_m, int Kg, int Ku, int 
   if (Kd > 128) return false;                         // one or two slot chunks of 64 lanes per down row
   if (d_model % 128) return false;                    // swizzled panel rows
   const int mt = gu_mt(d_model);
-  if (mt == 0 || gu_lds(R_ff, Kg, mt) > 163840 || (int64_t)R_ff * Kg > 512 * GU_CT_MAX) return false;
+  if (mt == 0 || gu_lds(R_ff, Kg, mt) > 163840) return false;
   if (R_m < 1 || R_m * B != d_model) return false;
   if ((R_ff * B) % 8) return false;
   return true;
@@ -1236,7 +1247,7 @@ bool lin_supported(int B, int in_features, int R, int K) {
   if (B != 16 && B != 32) return false;
   if (K < 1 || in_features % 128) return false;
   const int mt = gu_mt(in_features);
-  if (mt == 0 || gu_lds(R, K, mt) > 163840 || (int64_t)R * K > 512 * GU_CT_MAX) return false;
+  if (mt == 0 || gu_lds(R, K, mt) > 163840) return false;
   return (R * B) % 8 == 0;
 }
 

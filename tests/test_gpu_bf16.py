@@ -203,16 +203,20 @@ def test_swiglu_duplicate_and_empty_columns(gpu, case, Kd):
 
 
 @pytest.mark.parametrize("N", [8192 + 5, 300])
-def test_reference_default_layer_geometry(gpu, N):
-    """The reference's default layer at its ablation geometry (configs/ablation.yaml: d_model 512,
-    d_ff 2048, tile 16, initial density 1.0 -> K_gate = 32, K_down = 128) on the two-kernel path:
-    the down kernel with two slot chunks per lane and two rows per wave (8192 + 5 tokens), rows 0
-    and 1 (one wave's) with all 128 slots in the first stage (258 list positions), and the
-    fewer-token down shapes (300 tokens); the gate/up panel with its 32 K table filling the LDS."""
-    d_model, d_ff, B = 512, 2048, 16
-    _say(f"reference default layer d512 ff2048 B16 density 1.0 N={N}")
-    rng = np.random.default_rng(512 + N)
-    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 1.0)
+@pytest.mark.parametrize("geom", [(512, 2048, 1.0), (2048, 8192, 0.25)])
+def test_reference_default_layer_geometry(gpu, geom, N):
+    """The reference's default tile-16 layer on the two-kernel path at its ablation geometry
+    (configs/ablation.yaml: d_model 512, d_ff 2048, initial density 1.0 -> K_gate = 32, K_down =
+    128) and at its large geometry pruned to 25 % (configs/large.yaml: d_model 2048, d_ff 8192 ->
+    K_gate = 32, K_down = 128, 16384-entry gate/up column tables, 32-token gate/up panels): the
+    down kernel with two slot chunks per lane and two rows per wave (8192 + 5 tokens), rows 0 and 1
+    (one wave's) with all 128 slots in the first stage (258 list positions), and the fewer-token
+    shapes (300 tokens)."""
+    d_model, d_ff, dens = geom
+    B = 16
+    _say(f"reference default layer d{d_model} ff{d_ff} B16 density {dens} N={N}")
+    rng = np.random.default_rng(d_model + N)
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, dens)
     assert d[1].shape[1] == 128 and g[1].shape[1] == 32
     dc = d[1]
     dc[0, :] = rng.integers(0, 512 // B, size=128)          # all in the first 512-column stage
