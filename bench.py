@@ -374,6 +374,38 @@ def bench_matmul(steps, warmup, device):
                 down_shape=res["down_shape"])
 
 
+def bench_default_layer(steps, warmup, device):
+    """The reference's default tile-16 SwiGLU layer (biases zero-initialised as in its MLPBlock; gate
+    and up with one shared topology, as its init seeds both from one hash) at its two model
+    geometries, 16384 tokens each, weights packed once as MLPBlock keeps them: configs/ablation.yaml
+    (d_model 512, d_ff 2048, initial density 1.0: K_gate 32, K_down 128) and configs/large.yaml
+    pruned to 25 % (d_model 2048, d_ff 8192: K_gate 32, K_down 128)."""
+    import torch
+    from looped_blockell import kernels
+    res = {}
+    for name, (dm, dff, dens) in dict(ablation=(512, 2048, 1.0), large_25pct=(2048, 8192, 0.25)).items():
+        w = dict(d_model=dm, d_ff=dff, B=16, density=dens, N=16384)
+        gen = torch.Generator(device=device).manual_seed(2000 + dm)
+        (vg, cg), (vu, _), (vd, cd) = make_ffn(w, device, gen)
+        bg = torch.zeros(dff, device=device)
+        bu = torch.zeros(dff, device=device)
+        bd = torch.zeros(dm, device=device)
+        x = torch.randn(w["N"], dm, generator=gen, device=device).to(torch.bfloat16)
+        packed = kernels.swiglu_prepack(vg, cg, vu, cg, vd, cd)
+        ms, per = time_steps(lambda i: kernels.swiglu_fwd_prepacked(x, packed, vg, cg, vu, cg, vd, cd, False,
+                                                                    bg, bu, bd), steps, warmup)
+        flops = nonzero_flops(w)
+        res[name] = dict(workload=f"d_model={dm} d_ff={dff} B=16 density={dens} N=16384, biases, shared gate/up "
+                                  f"topology, prepacked", ms_per_step=ms, value=flops / (ms * 1e-3) / 1e12,
+                         unit="TFLOP/s", frac_of_bf16_peak=flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                         tokens_per_s=w["N"] / (ms * 1e-3), kernel_ms_avg=sum(per) / len(per))
+    a = res["ablation"]
+    return dict(workload="the reference's default tile-16 SwiGLU layer at its ablation geometry (value) and its "
+                         "large geometry at 25 % density (large_25pct)",
+                ms_per_step=a["ms_per_step"], value=a["value"], unit="TFLOP/s",
+                frac_of_bf16_peak=a["frac_of_bf16_peak"], **res)
+
+
 def bench_matmul_backward(steps, warmup, device):
     """Backward of one Block-ELL product at the headline gate shape (x [16384, 1024] -> [16384, 4096],
     B=32, 25 %): dx = dy W and the tile gradients (titan::block_ell_matmul_bwd), 2x the product's
@@ -731,7 +763,7 @@ def main():
                          "headline fields are then null)")
     ap.add_argument("--only", default="",
                     help="comma list of extra workloads to run: shared,backward,matmul,matmul_backward,ternary,"
-                         "looped,looped_core,decode,topology,formats")
+                         "looped,looped_core,default_layer,decode,topology,formats")
     ap.add_argument("--no-fewer-tokens", action="store_true",
                     help="skip the fewer-token runs of the headline and looped workloads (profiling: the kernel "
                          "statistics then hold the named workload's launches only)")
@@ -763,10 +795,12 @@ def main():
     extra = {}
     if not args.only_main:
         todo = [s for s in args.only.split(",") if s] or ["shared", "backward", "matmul", "matmul_backward", "ternary",
-                                                           "looped", "looped_core", "decode", "topology", "formats"]
+                                                           "looped", "looped_core", "default_layer", "decode",
+                                                           "topology", "formats"]
         fns = dict(shared=bench_bf16_shared, backward=bench_bf16_backward, matmul=bench_matmul,
                    matmul_backward=bench_matmul_backward,
-                   ternary=bench_ternary, looped=bench_looped, looped_core=bench_looped_core, decode=bench_decode,
+                   ternary=bench_ternary, looped=bench_looped, looped_core=bench_looped_core,
+                   default_layer=bench_default_layer, decode=bench_decode,
                    topology=bench_topology,
                    formats=bench_formats)
         for name in todo:
