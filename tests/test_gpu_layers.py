@@ -175,7 +175,8 @@ def test_ternary_layer(gpu):
 
     ref = O.ternary_swiglu_fwd(T.to_np(x).reshape(60, 512), w(m.w_gate), w(m.w_up), w(m.w_down),
                                exact_scales=True, h_round=O.bf16_round)
-    assert T.rel_err(T.to_np(y).reshape(60, 512), ref["out"])[0] <= TOL
+    from test_gpu_ternary import ffn_vs_exact
+    ffn_vs_exact(T.to_np(y).reshape(60, 512), ref["out"])
 
 
 def test_op_errors(gpu):

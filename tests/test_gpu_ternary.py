@@ -2,8 +2,9 @@
 
 Bars: activation quantisation (xq, sx) bit-exact; packing bit-exact; the int32
 block partials bit-exact; the fixed-point scaled products bit-exact against the
-oracle's restatement of the same fixed-point arithmetic; outputs within
-1e-2 * max|ref| of the exact-scale (float64) oracle.
+oracle's restatement of the same fixed-point arithmetic; single products within
+1e-2 * max|ref| of the exact-scale (float64) oracle; whole FFNs (with the int8
+re-quantisation of h) within the bounds of ffn_vs_exact.
 """
 
 import ctypes as C
@@ -20,6 +21,32 @@ TOL = 1e-2
 
 def _say(msg):
     print(msg, flush=True)
+
+
+def ffn_vs_exact(out, ref, hq=None, sh=None, down=None, resid=None):
+    """A whole ternary FFN against the exact-scale oracle.
+
+    The int8 re-quantisation of h turns a last-ulp difference of an h value near a rounding
+    boundary into a whole quantum (amax / 128) of the down input.  On the CPU the oracle's own
+    fixed-point and exact-scale pipelines differ by 0.94 % of the output RMS and 1.25 % of
+    max|ref| at d_model 2048, d_ff 8192, 64 tokens (1.6 % of the hq values flipped), so that
+    difference is quantisation noise of the reference semantics, not scaling error.  Hence two
+    checks: given the kernel's own hq (and sh), the exact-scale down product must agree to 2^-8
+    of max|y| (this isolates the fixed-point scaling, <= 2^-12 relative, beside the bf16
+    rounding of the output, <= 2^-9); and the whole FFN must agree to 1.5e-2 in relative RMS and
+    3e-2 of max|ref| per element (the noise allowance).  The exact bars are the int32
+    accumulators and the down product given hq, checked bit for bit elsewhere."""
+    out = np.asarray(out, np.float64)
+    if hq is not None:
+        yd, _ = O.ternary_matmul(hq, sh, *down, exact_scales=True)
+        if resid is not None:
+            yd = yd + np.asarray(resid, np.float64)
+        rel_d, ab_d = T.rel_err(out, yd)
+        assert rel_d <= 2.0 ** -8, f"down given hq: rel {rel_d} abs {ab_d}"
+    ref = np.asarray(ref, np.float64)
+    rms = float(np.sqrt(np.mean((out - ref) ** 2)) / max(np.sqrt(np.mean(ref ** 2)), 1e-30))
+    rel, ab = T.rel_err(out, ref)
+    assert rms <= 1.5 * TOL and rel <= 3 * TOL, f"relative rms {rms}, max {rel} (abs {ab})"
 
 
 def tern_weight(rng, R, C_, K, B, sentinel_frac=0.0):
@@ -175,8 +202,7 @@ def test_ternary_swiglu(gpu, case, resid):
     assert np.array_equal(out, O.bf16_round(yd))
     # whole FFN against the exact-scale oracle
     ref = O.ternary_swiglu_fwd(x, g, u, d, add_residual=resid, exact_scales=True, h_round=O.bf16_round)
-    rel, ab = T.rel_err(out, ref["out"])
-    assert rel <= TOL, f"rel {rel} abs {ab}"
+    ffn_vs_exact(out, ref["out"], hq, sh, d, x if resid else None)
 
 
 # B = 64 geometries served by the two-kernel path (gate/up kernel + down kernel with
@@ -231,8 +257,7 @@ def test_ternary_swiglu_split(gpu, case):
     yd, _ = O.ternary_matmul(hq, sh, *d, exact_scales=False)
     assert np.array_equal(out, O.bf16_round((yd + x).astype(np.float32)))
     ref = O.ternary_swiglu_fwd(x, g, u, d, add_residual=True, exact_scales=True, h_round=O.bf16_round)
-    rel, ab = T.rel_err(out, ref["out"])
-    assert rel <= TOL, f"rel {rel} abs {ab}"
+    ffn_vs_exact(out, ref["out"], hq, sh, d, x)
 
 
 def test_ternary_swiglu_split_extreme(gpu):
@@ -286,7 +311,7 @@ def test_ternary_full_size_sampled_rows(gpu):
     hq_ref, sh_ref = O.activation_quantize_int8(h)
     assert np.array_equal(hq_r, hq_ref) and np.array_equal(sh_r, sh_ref)
     ref = O.ternary_swiglu_fwd(x[rows], g, u, d, exact_scales=True, h_round=O.bf16_round)
-    assert T.rel_err(out, ref["out"])[0] <= TOL
+    ffn_vs_exact(out, ref["out"], hq_r, sh_r, d)
 
 
 @pytest.mark.parametrize("case", [
@@ -346,7 +371,7 @@ def test_ternary_prepared_matches_per_call_preparation(gpu, case):
         for a, b in zip(*outs):
             assert torch.equal(a, b)
         ref = O.ternary_swiglu_fwd(x, g, u, d, add_residual=True, exact_scales=True, h_round=O.bf16_round)
-        assert T.rel_err(T.to_np(outs[1][0]), ref["out"])[0] <= TOL
+        ffn_vs_exact(T.to_np(outs[1][0]), ref["out"])
     if pb:
         small = torch.empty(pb - 256, dtype=torch.uint8, device="cuda")
         assert lib.lbk_ternary_prepare(d_model, C.byref(gs), C.byref(us), C.byref(ds), T.ptr(small), small.numel(),
