@@ -314,6 +314,49 @@ def test_ternary_full_size_sampled_rows(gpu):
     ffn_vs_exact(out, ref["out"], hq_r, sh_r, d)
 
 
+# Large B = 64 geometries on sampled rows: several thousand tokens (row groups dealt over the down
+# rows where the 16-token blocks number fewer than 256), a ragged last block, dead slots, down rows
+# with 9-30 slots, d_ff from 2048 to 8192, with and without the residual.
+LARGE_CASES = [
+    # (d_model, d_ff, Kg, Kd, N, sentinel_frac, residual)
+    (2048, 8192, 3, 13, 4096 + 5, 0.2, True),
+    (1024, 4096, 4, 9, 6000, 0.0, False),
+    (512, 6144, 2, 30, 8192 + 33, 0.1, True),
+    (2048, 2048, 4, 16, 9000, 0.0, True),
+]
+
+
+@pytest.mark.parametrize("case", LARGE_CASES)
+def test_ternary_swiglu_large_sampled(gpu, case):
+    """Sampled rows (the last rows of the ragged block among them): int32 accumulators of gate/up
+    (given xq) and down (given the kernel's hq) bit-exact, hq the oracle's quantisation of the
+    kernel's h, outputs bit-exact given hq; the plain and accumulator-exporting launches agree."""
+    import torch
+    from looped_blockell import kernels
+    d_model, d_ff, Kg, Kd, N, frac, resid = case
+    B = 64
+    _say(f"ternary large sampled {case}")
+    rng = np.random.default_rng(abs(hash(case)) % 2 ** 31)
+    g = tern_weight(rng, d_ff // B, d_model // B, Kg, B, sentinel_frac=frac)
+    u = tern_weight(rng, d_ff // B, d_model // B, Kg, B, sentinel_frac=frac)
+    d = tern_weight(rng, d_model // B, d_ff // B, Kd, B, sentinel_frac=frac)
+    x = T.act(rng, N, d_model)
+    xg = T.to_gpu_bf16(x)
+    xq_t, sx_t = kernels.quantize_act_int8(xg)
+    args = (xq_t, sx_t, gpu_tern(g), gpu_tern(u), gpu_tern(d), xg if resid else None)
+    res = kernels.ternary_swiglu_fwd_accumulators(*args)
+    out_plain = kernels.ternary_swiglu_fwd(*args)
+    assert torch.equal(out_plain, res[0])
+    rows = np.unique(np.concatenate([rng.choice(N, 96, replace=False), np.arange(N - 8, N)]))
+    xq, sx = O.activation_quantize_int8(x[rows])
+    out, h, hq, sh, yd = check_accumulators(res, xq, sx, g, u, d, rows=rows)
+    hq_ref, sh_ref = O.activation_quantize_int8(h)
+    assert np.array_equal(hq, hq_ref) and np.array_equal(sh, sh_ref)
+    if resid:
+        yd = (yd + x[rows]).astype(np.float32)
+    assert np.array_equal(out, O.bf16_round(yd))
+
+
 @pytest.mark.parametrize("case", [
     # (d_model, d_ff, B, Kg, Kd, token counts, sentinel_frac)
     (512, 2048, 64, 2, 7, (300, 17), 0.1),      # the B = 64 two-kernel path: prepared weights
