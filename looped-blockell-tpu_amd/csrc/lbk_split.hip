@@ -27,6 +27,10 @@
 // padded to an even length with a zero-tile entry, and streams it through a
 // two-slot ring that also prefetches the next stage's first tiles.  The
 // epilogue adds the residual, or carries an fp32 state for the looped block.
+//
+// dnf_kernel<B, D>: the plain forward's down kernel at B = 32 on 64-token blocks: the same
+// workgroup and stages, but each wave streams its row through a D-slot ring across the stages
+// (no pair padding, stage changes taken inline); see its comment.
 #include "lbk_device.h"
 #include "lbk_internal.h"
 
@@ -988,6 +992,197 @@ __global__ __launch_bounds__(64 * NW, 1) void dn_kernel(DNArgs a) {
 }
 
 // ===========================================================================
+// down projection with a deep ring (the plain forward)
+// ===========================================================================
+// dnf_kernel<B, D>: the dn_kernel workgroup (16 waves, 64 tokens, one down row per wave, h staged
+// through LDS 512 columns at a time, next stage fetched into registers while the current one is
+// consumed), but each wave streams its tiles through a D-slot ring that runs over its whole row:
+// lane k of a wave holds the column of the row's slot k, the entries of stage s are the lanes
+// whose column lies in it (ballot), taken in lane order, so the ring's positions follow the
+// stages with no padding and no restart, and a stage change is a workgroup barrier taken inline
+// when the next position belongs to a later stage.  The tile loads a wave keeps in flight (D) hide
+// the L2 latency that the two-slot pairs of dn_kernel could not.
+template <int B, int D, bool BIAS>
+__global__ __launch_bounds__(64 * DN_WAVES, 1) void dnf_kernel(DNArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char dn_smem[];   // two stages
+  constexpr int MT = 4, NW = DN_WAVES;
+  constexpr int CW = TileShape<B>::CW;
+  constexpr int TM = 16 * MT;
+  constexpr int G = DnStage<B, DN_STAGE_COLS>::G;    // column blocks per stage
+  constexpr int SROWB = G * B * 2;                   // bytes per token row of a stage
+  constexpr int SBYTES = TM * SROWB;                 // bytes per stage
+  constexpr int CHUNKS = SBYTES / 16;
+  constexpr int NT = 64 * NW;
+  constexpr int PER_T = (CHUNKS + NT - 1) / NT;
+  static_assert(TileShape<B>::NKS == 1, "B <= 32");
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int w = uniform(tid >> 6);
+  const int i = lane & 15, g = lane >> 4;
+  int tb = (int)blockIdx.x, rg = 0;
+  if (a.nrg > 1) {   // the row groups of one token block on one XCD (ids equal mod 8)
+    const int b = (int)blockIdx.x, rest = b >> 3;
+    rg = rest % a.nrg;
+    tb = 8 * (rest / a.nrg) + (b & 7);
+  }
+  const int64_t t0 = (int64_t)tb * TM;
+  if (t0 >= a.N) return;   // the whole workgroup, before any barrier
+  const int rm = rg * NW + w;   // this wave's down row
+  const int d_model = a.d_model;
+  const int64_t d_ff = a.d_ff;
+  const int C = a.C_d;
+  const int nstages = (C + G - 1) / G;
+  const u32x4* pd = static_cast<const u32x4*>(a.pd);
+  const int ztile = a.R_m * a.Kd;
+
+  // lane k: slot k of the row (dead slots and lanes beyond Kd take no part)
+  int ecol = -1;
+  if (rm < a.R_m && lane < a.Kd) ecol = a.cd[(int64_t)rm * a.Kd + lane];
+  const bool live = ecol >= 0 && ecol < C;
+  const int est = live ? ecol / G : 0;
+
+  f32x4 acc[MT][CW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int m = 0; m < CW; ++m) acc[mt][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // stage loads: unconditional (clamped address), zeros selected at the LDS store
+  u32x4 sreg[PER_T];
+  int sok = 0;
+  auto stage_fetch = [&](int s) {
+    sok = 0;
+#pragma unroll
+    for (int u = 0; u < PER_T; ++u) {
+      const int e = tid + NT * u;
+      const int ec = e < CHUNKS ? e : CHUNKS - 1;
+      const int row = ec / (SROWB / 16), c = ec - row * (SROWB / 16);
+      const int64_t t = t0 + row;
+      const int64_t col = (int64_t)s * G * B + 8 * c;
+      sok |= (e < CHUNKS && t < a.N && col < d_ff) ? 1 << u : 0;
+      sreg[u] = *reinterpret_cast<const u32x4*>(a.h + (t < a.N ? t : a.N - 1) * d_ff + (col < d_ff ? col : 0));
+    }
+  };
+  auto stage_store = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < PER_T; ++u) {
+      const int e = tid + NT * u;
+      if (e < CHUNKS) {
+        const int row = e / (SROWB / 16), c = e - row * (SROWB / 16);
+        *reinterpret_cast<u32x4*>(dn_smem + buf * SBYTES + panel_addr<MT>(row, c, SROWB)) =
+            (sok >> u) & 1 ? sreg[u] : u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+
+  struct Slot {
+    std::conditional_t<B == 16, u32x2, u32x4> f[1][CW];
+    int el;   // entry lane (-1: none left)
+    int st;   // stage
+    int cb;   // column block within the stage
+  };
+  const uint32_t f16 = pfrag16_off(lane);
+  // fetch cursor: stage fs and the entries of it not yet fetched
+  int fs = 0;
+  uint64_t fmask = __builtin_amdgcn_ballot_w64(live && est == 0);
+  auto fetch = [&](Slot& S) {
+    while (fmask == 0 && fs + 1 < nstages) {
+      ++fs;
+      fmask = __builtin_amdgcn_ballot_w64(live && est == fs);
+    }
+    int el = -1;
+    if (fmask) {
+      el = (int)__builtin_ctzll(fmask);
+      fmask &= fmask - 1;
+    }
+    const int tile = el >= 0 ? rm * a.Kd + el : ztile;
+    if constexpr (B == 16) S.f[0][0] = load_pfrag16(pd + (int64_t)tile * PackedTile<B>::U32X4, f16);
+    else load_pfrag<B>(pd + (int64_t)tile * PackedTile<B>::U32X4, lane, S.f);
+    S.el = el;
+    S.st = fs;
+    S.cb = __builtin_amdgcn_readlane(ecol, el >= 0 ? el : 0) - fs * G;
+  };
+  const uint32_t lbase = (uint32_t)(i * MT * SROWB);
+  auto compute = [&](const Slot& S, const unsigned char* sb) {
+    const int cb = S.cb;
+    if constexpr (B == 16) {
+      const uint32_t a0 = k16_addr(lbase, cb, g, i);
+      u32x2 av[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) av[mt] = lds8(sb, a0 + mt * SROWB);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt][0] = mfma_bf16_k16(av[mt], S.f[0][0], acc[mt][0]);
+    } else {
+      const uint32_t a0 = lbase + (((cb * (B / 8) + g) ^ i) << 4);
+      u32x4 av[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) av[mt] = lds16(sb, a0 + mt * SROWB);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int m = 0; m < CW; ++m) acc[mt][m] = mfma_bf16(av[mt], S.f[0][m], acc[mt][m]);
+    }
+  };
+
+  Slot R[D];
+#pragma unroll
+  for (int sl = 0; sl < D; ++sl) fetch(R[sl]);
+  stage_fetch(0);
+  stage_store(0);
+  __syncthreads();
+  if (nstages > 1) stage_fetch(1);
+  // stage cs -> cs + 1: the registers fetched at the start of stage cs go to the other buffer;
+  // after the barrier every wave is past stage cs, whose buffer takes the stage after next
+  int cs = 0;
+  auto transition = [&]() {
+    stage_store((cs + 1) & 1);
+    __syncthreads();
+    ++cs;
+    if (cs + 1 < nstages) stage_fetch(cs + 1);
+  };
+  // Every slot is refetched on every pass, also past the row's last entry (the zero tile), so the
+  // tile loads are never skipped and the compiler's memory-counter waits stay exact; the entries
+  // are consumed in fetch order, so once slot 0 comes back empty every slot is.
+  for (;;) {
+#pragma unroll
+    for (int sl = 0; sl < D; ++sl) {
+      Slot& S = R[sl];
+      if (S.el >= 0) {
+        while (cs < S.st) transition();
+        compute(S, dn_smem + (cs & 1) * SBYTES);
+      }
+      fetch(S);
+    }
+    if (R[0].el < 0) break;
+  }
+  while (cs + 1 < nstages) transition();
+
+  // ---- epilogue: (+ down bias) + residual; store bf16
+  if (rm >= a.R_m) return;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t t = t0 + 16 * mt + 4 * g + v;
+      if (t >= a.N) continue;
+      const int64_t off = t * d_model + rm * B + CW * i;
+      float o[CW];
+#pragma unroll
+      for (int m = 0; m < CW; ++m) {
+        o[m] = acc[mt][m][v];
+        if constexpr (BIAS) o[m] += a.bd[rm * B + CW * i + m];
+      }
+      if (a.resid) {
+        float rv[CW];
+        load_bf16<CW>(a.resid + off, rv);
+#pragma unroll
+        for (int m = 0; m < CW; ++m) o[m] += rv[m];
+      }
+      store_bf16<CW>(a.out + off, o);
+    }
+}
+
+// ===========================================================================
 // looped block in one persistent launch
 // ===========================================================================
 // LDS of the looped kernel: gate/up panel (or the two down stages) | column table | per-token
@@ -1299,8 +1494,29 @@ static int launch_dn_t(const DNArgs& a, hipStream_t st) {
 // workgroups, which halve the weight bytes each CU streams, measured slower at the headline
 // geometry: 154 us with 8 waves of two rows and 256-column stages, 161 us with 16 waves of one
 // row, against 144 us; the smaller stages add padding and per-stage imbalance.)
+// the deep-ring down kernel on 64-token blocks, rows of at most 64 slots
+constexpr int DNF_RING = 4;
+template <int B>
+static int launch_dnf(const DNArgs& a0, hipStream_t st) {
+  constexpr int TM = 64;
+  constexpr size_t lds = 2 * (size_t)TM * DN_STAGE_COLS * 2;   // two stages
+  DNArgs a = a0;
+  const int64_t ntb = (a.N + TM - 1) / TM;
+  a.nrg = (a.R_m + DN_WAVES - 1) / DN_WAVES;
+  const int64_t grid = a.nrg == 1 ? ntb : 8 * a.nrg * ((ntb + 7) / 8);
+  auto kern = a.bd ? dnf_kernel<B, DNF_RING, true> : dnf_kernel<B, DNF_RING, false>;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds) != hipSuccess)
+    return -1;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * DN_WAVES), lds, st, a);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 int launch_dn(int B, const DNArgs& a, hipStream_t st) {
   if (a.N == 0) return 0;
+  // the deep-ring kernel takes the plain forward (with an fp32 state, as the looped block's
+  // iterations run it, it measured slower: L = 8 at the headline geometry 1.270 -> 1.281 ms)
+  const bool plain = !a.state && !a.tdepth && !a.inj_e && a.out && a.Kd <= 64;
   // Fewer 64-token blocks than the 16-row groups need to fill the CUs: smaller workgroups with
   // longer stages, so that more of them run and each walks fewer stages -- 16 tokens and 4 rows
   // per workgroup with 2048-column stages (1024 for B = 16) while they number at most 128, else
@@ -1319,6 +1535,7 @@ int launch_dn(int B, const DNArgs& a, hipStream_t st) {
   // row groups re-read h (d_model 1024, d_ff 4096: forward 0.301 -> 0.293 ms)
   if (B == 16 && a.R_m > DN_WAVES) return launch_dn_t<16, 4, 2, DN_WAVES, DN_STAGE_COLS>(a, st);
   if (B == 16) return launch_dn_t<16, 4, 1, DN_WAVES, DN_STAGE_COLS>(a, st);
+  if (B == 32 && plain) return launch_dnf<32>(a, st);
   if (B == 32) return launch_dn_t<32, 4, 1, DN_WAVES, DN_STAGE_COLS>(a, st);
   return -2;
 }

@@ -308,6 +308,52 @@ def test_swiglu_full_headline_sampled_rows(gpu):
     assert np.isfinite(out).all()
 
 
+@pytest.mark.parametrize("case", [
+    # (d_model, d_ff, density, N, sentinel_frac, residual, biases, prepacked)
+    (640, 4352, 0.27, 8192 + 7, 0.15, True, False, False),   # 20 down rows, 136 column blocks
+    (1024, 4096, 0.25, 16384 - 40, 0.0, False, True, True),  # headline geometry, biases, prepacked
+])
+def test_swiglu_deep_ring_down_sampled_rows(gpu, case):
+    """The B = 32 down kernel of the large-token forward (a ring over each row's slots across the
+    512-column h stages): a second row group with 4 of its 16 waves holding rows, a last stage of
+    8 column blocks, 36 slots per row with dead slots, a row with no live slot, a column past the
+    end, a ragged last token block; biases through the prepacked forward.  Sampled rows against the
+    fp64 oracle."""
+    import torch
+    from looped_blockell import kernels
+    d_model, d_ff, dens, N, frac, resid, biases, prepacked = case
+    B = 32
+    _say(f"swiglu deep-ring down {case}")
+    rng = np.random.default_rng(2024 + d_model)
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, dens, sentinel_frac=frac)
+    if frac:
+        d[1][3, :] = -1                       # a down row with no live slot
+        d[1][5, 0] = d_ff // B + 2            # past the last column block: skipped
+    x = T.act(rng, N, d_model)
+    bs = [None, None, None]
+    if biases:
+        bs = [rng.standard_normal(n).astype(np.float32) * 0.1 for n in (d_ff, d_ff, d_model)]
+    xg = T.to_gpu_bf16(x)
+    wg, wu, wd = T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d)
+    if prepacked or biases:
+        pk = kernels.swiglu_prepack(*wg, *wu, *wd)
+        bt = [None if b is None else torch.as_tensor(b, device="cuda") for b in bs]
+        out = kernels.swiglu_fwd_prepacked(xg, pk, *wg, *wu, *wd, add_residual=resid, b_gate=bt[0], b_up=bt[1],
+                                           b_down=bt[2])
+    else:
+        out, *_ = T.abi_swiglu(xg, wg, wu, wd, add_residual=resid)
+    out = T.to_np(out)
+    rows = np.concatenate([np.sort(rng.choice(N, 256, replace=False)), np.arange(N - 8, N), [0]])
+    # the kernels skip a column past the end as they skip -1: the reference takes it as -1
+    d_ref = (d[0], np.where(d[1] < d_ff // B, d[1], -1))
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref, *_ = O.swiglu_fwd(x[rows].astype(np.float64), f64(g), f64(u), f64(d_ref), add_residual=resid,
+                           biases=tuple(None if b is None else b.astype(np.float64) for b in bs))
+    rel, ab = T.rel_err(out[rows], ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+    assert np.isfinite(out).all()
+
+
 def test_swiglu_b16_full_size_sampled_rows(gpu):
     """B = 16 at d_model 1024, d_ff 4096, density 0.25 (64 down slots per row) on 16384 + 5 tokens:
     one row slice per token block (the 12-wave gate/up kernel), a ragged last block; sampled rows."""
