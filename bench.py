@@ -212,13 +212,13 @@ def bench_bf16(steps, warmup, device):
                       traffic_source=os.path.relpath(TRAFFIC_PROFILE_BF16, ROOT) + " (2 x FETCH_SIZE + WRITE_SIZE "
                                      "of the two launches, the factors a copy of known size reads)",
                       kernel="SwiGLU forward launch pair gu_kernel_w12<32,4,false> + "
-                             "dn_kernel<32,4,1,16,512,false>, timed together with HIP events around each step",
+                             "dnf_kernel<32,4,false>, timed together with HIP events around each step",
                       algorithmic_flops_per_launch=flops,
                       algorithmic_bytes_per_launch=algorithmic_bytes(w)),
         fewer_tokens=dict(workload="the same forward (weights packed once) on the first N tokens", unit="TFLOP/s",
                           by_tokens=by_tokens),
         with_pack=dict(workload="the same forward packing the weights on every call (titan::block_ell_swiglu_fwd: "
-                                "pack_bf16_multi_kernel + gu_kernel + dn_kernel)",
+                                "pack_bf16_multi_kernel + gu_kernel_w12 + dnf_kernel)",
                        ms_per_step=ms_p, value=flops / (ms_p * 1e-3) / 1e12, unit="TFLOP/s",
                        kernel_ms_avg=sum(per_p) / len(per_p)),
     )
