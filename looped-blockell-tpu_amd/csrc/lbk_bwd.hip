@@ -30,6 +30,9 @@
 //                  of 64 tokens pass through LDS 512 at a time, and a cursor per
 //                  output block walks its sorted list, whose first 64 entries
 //                  stay in a register.
+//   dxf_kernel     dx at B = 32: the same stages, one output block per wave and a
+//                  4-slot ring of tiles over the wave's whole list (both sources,
+//                  all stages), the list entries read one pass ahead.
 //   dw_kernel      tile gradients: a workgroup owns one block row, up to 8 of
 //                  its slots (one per wave) and a chunk of tokens; token slices
 //                  of X and G are staged row-major in LDS and read back
@@ -625,6 +628,190 @@ static int launch_dx_stage_t(const TProdArgs& a, hipStream_t st) {
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// dxf_kernel<B, D>: dx at B = 32 with one output block per wave (16 waves; the output blocks are
+// dealt to nsl workgroups per 64-token block, which share an XCD) and a D-slot ring of tiles that
+// runs over the wave's whole list -- the sorted entries of source 0, then of source 1 -- across
+// the 512-column stages of both sources, so D tile loads stay in flight where dx_stage_kernel
+// had one.  A stage change is a workgroup barrier taken inline when the next entry lies in a
+// later stage; every wave passes all of them.  The list entries a pass fetches are read one pass
+// ahead (lane j of a window holds entry j of the pass), so no load waits on a list read.
+constexpr int DXF_WAVES = 16;
+constexpr int DXF_RING = 4;
+template <int B, int D>
+__global__ __launch_bounds__(64 * DXF_WAVES, 1) void dxf_kernel(TProdArgs a) {
+  constexpr int NW = DXF_WAVES, NT = 64 * NW;
+  constexpr int CW = B / 16, MT = 4;
+  constexpr int COLS = DxStage<B>::COLS;
+  constexpr int G = COLS / B;                        // source column blocks per stage
+  constexpr int SROWB = COLS * 2;
+  constexpr int SBYTES = 64 * SROWB;
+  constexpr int PER_T = SBYTES / 16 / NT;
+  static_assert(B == 32, "one 32-deep k-step per tile");
+  extern __shared__ __attribute__((aligned(16))) unsigned char stg[];   // two stages
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = uniform(tid >> 6);
+  const int i = lane & 15, g = lane >> 4;
+  // workgroup -> (64-token block tb, slice sl); the slices of a token block share an XCD
+  int64_t tb = blockIdx.x;
+  int sl = 0;
+  if (a.nsl > 1) {
+    const int64_t b = blockIdx.x, rest = b >> 3;
+    sl = (int)(rest % a.nsl);
+    tb = 8 * (rest / a.nsl) + (b & 7);
+  }
+  const int64_t t0 = tb * 64;
+  if (t0 >= a.N) return;   // the whole workgroup, before any barrier
+  const int c = sl + a.nsl * w;                      // this wave's output column block
+  const bool has = c < a.C;
+  const int cs_ = has ? c : 0;
+
+  const int R0 = (int)(a.src[0].lda / B);
+  const int ns0 = (R0 + G - 1) / G;
+  const int ns1 = a.nsrc > 1 ? ((int)(a.src[1].lda / B) + G - 1) / G : 0;
+  const int nstages = ns0 + ns1;
+  const TProdSrc& S0 = a.src[0];
+  const TProdSrc& S1 = a.src[a.nsrc > 1 ? 1 : 0];
+
+  // stage loads: unconditional (clamped address), zeros selected at the LDS store
+  u32x4 sreg[PER_T];
+  int sok = 0;
+  auto stage_fetch = [&](int s) {
+    const TProdSrc& S = s < ns0 ? S0 : S1;
+    const int64_t col0 = (int64_t)(s < ns0 ? s : s - ns0) * COLS;
+    sok = 0;
+#pragma unroll
+    for (int u = 0; u < PER_T; ++u) {
+      const int e = tid + NT * u;
+      const int row = e / (SROWB / 16), cc = e - row * (SROWB / 16);
+      const int64_t t = t0 + row, col = col0 + 8 * cc;
+      const bool ok = t < a.N && col < S.lda;
+      sok |= ok ? 1 << u : 0;
+      sreg[u] = ld16(S.a + (ok ? t : t0) * S.lda + (ok ? col : 0));
+    }
+  };
+  auto stage_store = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < PER_T; ++u) {
+      const int e = tid + NT * u;
+      const int row = e / (SROWB / 16), cc = e - row * (SROWB / 16);
+      *reinterpret_cast<u32x4*>(stg + buf * SBYTES + bpanel_addr<MT>(row, cc, SROWB)) =
+          (sok >> u) & 1 ? sreg[u] : u32x4{0, 0, 0, 0};
+    }
+  };
+
+  // the wave's list: entries 0 .. n0 - 1 from source 0, then n1 from source 1
+  const int n0 = has ? S0.cnt[cs_] : 0;
+  const int n1 = has && a.nsrc > 1 ? S1.cnt[cs_] : 0;
+  const int32_t* L0 = S0.list + (int64_t)cs_ * S0.cap;
+  const int32_t* L1 = S1.list + (int64_t)cs_ * S1.cap;
+  // entries base .. base + 2D - 1 in lanes 0 .. 2D - 1 (an unconditional load at a clamped
+  // index; entries past the list are recognised by their index, not by the loaded value)
+  auto window = [&](int base) {
+    const int j = base + (lane < 2 * D ? lane : 0);
+    const int32_t* p = j < n0 ? L0 + j : (j - n0 < n1 ? L1 + (j - n0) : L0);
+    return *p;
+  };
+
+  struct Slot {
+    u32x4 av[CW];
+    int st;   // stage (-1: past the list)
+    int cb;   // column block within the stage
+  };
+  // slot S <- entry j of the list (its value e read from the window)
+  auto fetch = [&](Slot& S, int j, int e) {
+    const bool live = j < n0 + n1;
+    const bool s1 = j >= n0;
+    const TProdSrc& Sx = s1 ? S1 : S0;
+    const int r = live ? e / Sx.K : 0;
+    const int64_t tile = live ? e : 0;              // past the list: tile 0 of source 0, unused
+    const uint16_t* tp = (live && s1 ? S1.w : S0.w) + tile * B * B + 8 * g;
+#pragma unroll
+    for (int m = 0; m < CW; ++m) S.av[m] = ld16(tp + op_row<CW>(i, m) * B);
+    S.st = live ? (s1 ? ns0 : 0) + r / G : -1;
+    S.cb = r - (r / G) * G;
+  };
+  const uint32_t lbase = (uint32_t)(i * MT * SROWB);
+  f32x4 acc[MT][CW];
+#pragma unroll
+  for (int q = 0; q < MT; ++q)
+#pragma unroll
+    for (int m = 0; m < CW; ++m) acc[q][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](const Slot& S, const unsigned char* sb) {
+    const uint32_t pa = lbase + (((S.cb * (B / 8) + g) ^ i) << 4);
+#pragma unroll
+    for (int q = 0; q < MT; ++q) {
+      const u32x4 bv = *reinterpret_cast<const u32x4*>(sb + pa + q * SROWB);
+#pragma unroll
+      for (int m = 0; m < CW; ++m) acc[q][m] = mfma_bf16(S.av[m], bv, acc[q][m]);
+    }
+  };
+
+  Slot R[D];
+  // the ring's first entries, and those of the first pass in lanes D .. 2D - 1 of the same window
+  // (read here, so the window register enters the loop with its load complete)
+  int wcur = window(0);
+#pragma unroll
+  for (int s = 0; s < D; ++s) fetch(R[s], s, __builtin_amdgcn_readlane(wcur, s));
+  int nxt = D;                                      // list index of the next entry to fetch
+  int woff = D;                                     // lane of the pass's first entry in its window
+  stage_fetch(0);
+  stage_store(0);
+  __syncthreads();
+  if (nstages > 1) stage_fetch(1);
+  int cs = 0;
+  auto transition = [&]() {
+    stage_store((cs + 1) & 1);
+    __syncthreads();
+    ++cs;
+    if (cs + 1 < nstages) stage_fetch(cs + 1);
+  };
+  // every slot is refetched on every pass (past the list: tile 0, not computed), so the tile
+  // loads are never skipped and the compiler's memory-counter waits stay exact.  Two passes per
+  // iteration with the two window registers in turn (no copy of a window whose load is in flight)
+  int walt = 0;
+  auto pass = [&](const int& wuse, int& wload) {
+    wload = window(nxt + D);                         // the next pass's entries
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      Slot& S = R[s];
+      if (S.st >= 0) {
+        while (cs < S.st) transition();
+        compute(S, stg + (cs & 1) * SBYTES);
+      }
+      fetch(S, nxt + s, __builtin_amdgcn_readlane(wuse, woff + s));
+    }
+    nxt += D;
+    woff = 0;
+    return R[0].st >= 0;
+  };
+  while (pass(wcur, walt) && pass(walt, wcur)) {
+  }
+  while (cs + 1 < nstages) transition();
+
+  // epilogue: dx = acc (+ dy)
+  if (!has) return;
+#pragma unroll
+  for (int q = 0; q < MT; ++q) {
+    const int64_t tn = t0 + 16 * q + i;
+    if (tn < a.N) tprod_store<1, CW>(a, tn, c, g, acc[q]);
+  }
+}
+
+template <int B>
+static int launch_dxf(const TProdArgs& a0, hipStream_t st) {
+  constexpr size_t lds = 2 * (size_t)64 * DxStage<B>::COLS * 2;
+  TProdArgs a = a0;
+  const int64_t ntb = (a.N + 63) / 64;
+  a.nsl = (a.C + DXF_WAVES - 1) / DXF_WAVES;
+  const int64_t grid = a.nsl == 1 ? ntb : 8 * a.nsl * ((ntb + 7) / 8);
+  auto kern = dxf_kernel<B, DXF_RING>;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds) != hipSuccess)
+    return -1;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * DXF_WAVES), lds, st, a);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // staged dx when every output block fits the waves' accumulators (OPW * B / 16 <= 8) and the
 // sources' widths are whole stages of 16-byte chunks
 static int launch_dx_stage(int B, const TProdArgs& a0, hipStream_t st) {
@@ -638,6 +825,9 @@ static int launch_dx_stage(int B, const TProdArgs& a0, hipStream_t st) {
   const int per_wg = B == 64 ? 8 : 16;
   a.nsl = ntb >= 256 ? 1 : (a.C + per_wg - 1) / per_wg;
   const int cs = (a.C + a.nsl - 1) / a.nsl;        // output blocks per slice
+  // B = 32: the deep-ring kernel (headline backward 0.710 -> 0.688 ms; 64 / 1024 / 4096 tokens
+  // 0.109 / 0.131 / 0.213 -> 0.105 / 0.127 / 0.199 ms)
+  if (B == 32) return launch_dxf<32>(a0, st);
   // 16 waves (four per SIMD to hide the tile loads) when their accumulators fit 128 VGPRs:
   // headline backward 0.785 -> 0.740 ms, B = 16 at d_model 512 / 1024 0.497 -> 0.447 and
   // 2.10 -> 1.95 ms against 8 waves; B = 64 keeps 8 waves (16 would spill)

@@ -48,7 +48,7 @@ BWD_CASES = [
     (512, 1024, 32, 0.25, 130, 0.05),
     (128, 512, 64, 0.5, 70, 0.0),
     (1024, 4096, 32, 0.25, 2100, 0.0),     # two token chunks of the tile gradients, ragged tail
-    (2048, 1024, 32, 0.125, 40, 0.05),     # 64 output blocks: dx through the per-entry gather kernel
+    (2048, 1024, 32, 0.125, 40, 0.05),     # 64 output blocks: dx over four workgroups per token block
     (4096, 512, 64, 0.25, 20, 0.0),        # d_model > 2048: dh through the per-entry gather kernel too
 ]
 
@@ -173,6 +173,8 @@ MM_CASES = [
     (512, 256, 64, 0.25, 40, 0.05),
     (1024, 4096, 32, 0.25, 2100, 0.0),      # two token chunks of the tile gradients
     (256, 2048, 16, 0.125, 33, 0.0),       # 128 output blocks: dx through the per-entry gather kernel
+    (256, 800, 32, 0.25, 150, 0.1),        # 25 output blocks: the second workgroup of a token block has 7 idle waves
+    (2048, 256, 32, 0.5, 70, 0.0),         # one source, 32 list entries per output block over 4 stages
 ]
 
 
