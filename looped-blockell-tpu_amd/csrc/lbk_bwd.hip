@@ -33,6 +33,10 @@
 //   dxf_kernel     dx at B = 32: the same stages, one output block per wave and a
 //                  4-slot ring of tiles over the wave's whole list (both sources,
 //                  all stages), the list entries read one pass ahead.
+//   dwg_kernel     tile gradients of a weight with narrow input rows (gate / up,
+//                  d_model <= 1024, B = 32, K <= 8): a workgroup owns 8 block rows
+//                  and stages the whole x row slice once per 32 tokens for their
+//                  64 tiles (taken when it fills the CUs, 256 workgroups).
 //   dw_kernel      tile gradients: a workgroup owns one block row, up to 8 of
 //                  its slots (one per wave) and a chunk of tokens; token slices
 //                  of X and G are staged row-major in LDS and read back
@@ -1129,6 +1133,170 @@ __global__ __launch_bounds__(512) void dw_dma_kernel(DWJobs jobs) {
       for (int v = 0; v < 4; ++v) part[(16 * md + 4 * g + v) * B + 16 * mD + i] = acc[md][mD][v];
 }
 
+// ---------------------------------------------------------------------------
+// tile gradients of a weight whose input rows are narrow (gate / up: x at most 1024 wide)
+// ---------------------------------------------------------------------------
+// dwg_kernel<XI>: a workgroup owns 8 block rows r0 .. r0 + 7 (one per wave, at most 8 slots each)
+// and a chunk of tokens.  Per 32-token slice it stages the whole input row x[t, 0 : C B] and
+// G[t, r0 B : (r0 + 8) B] in LDS (double-buffered, direct global->LDS loads as in dw_dma_kernel;
+// XI load instructions of x per wave), and each wave computes the K tiles of its row from them,
+// so x is read once per slice for the 64 tiles of the workgroup instead of once per tile:
+// 2.5 KB per tile and 64 tokens against 4.5.  Row t of a slice keeps its 16-byte chunk c at
+// c ^ h(t), h(t) = 2 (t & 3) | (t & 8): the transposed reads of a half-wave (rows t .. t + 3 and
+// t + 8 .. t + 11, two chunks each) then cover the 64 banks once (the row strides are multiples
+// of 256 bytes).  Tokens are accumulated in the order of dw_dma_kernel (32-token k-steps).
+namespace {
+struct DWG {
+  static constexpr int TS = 32;          // tokens per slice
+  static constexpr int RB = 8;           // block rows per workgroup, one per wave
+  static constexpr int GW = RB * 32;     // G slice row (elements)
+  static constexpr int XWMAX = 1024;     // x slice row (elements)
+  __device__ static int h(int t) { return ((t & 3) << 1) | (t & 8); }
+  __device__ static int at(int t, int col, int rowe) { return t * rowe + 8 * ((col >> 3) ^ h(t)) + (col & 7); }
+};
+
+// transposed operand of a slice with rows of rowe elements (the lane mapping of dwd_frag)
+__device__ __forceinline__ u32x4 dwg_frag(const uint16_t* slice, int rowe, int c0, int lane) {
+  const int s = lane & 15, g = lane >> 4;
+  const int row = 8 * g + (s >> 2);
+  const int col = c0 + 4 * (s & 3);
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(slice + DWG::at(row, col, rowe)));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(slice + DWG::at(row + 4, col, rowe)));
+  const u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
+
+// 1 KB (instruction j) of a slice with rows of rowe elements from rows t0.. of a [N, ld] matrix,
+// columns col0 .. col0 + rowe - 1: lane l brings the chunk stored at position 64 j + l; rows at or
+// past N read row N - 1 (zeroed before use)
+__device__ __forceinline__ void dwg_load(const uint16_t* src, int64_t ld, int64_t col0, int rowe, int64_t t0,
+                                         int64_t N, uint16_t* slice, int j, int lane) {
+  const int cpr = rowe / 8;
+  const int P = 64 * j + lane;
+  const int t = P / cpr, cp = P - t * cpr;
+  const int c = cp ^ DWG::h(t);
+  const int64_t tt = t0 + t < N ? t0 + t : N - 1;
+  const uint32_t lds = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void*)(slice + 512 * j)));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src + tt * ld + col0 + 8 * c),
+               "s"(lds) : "memory", "m0");
+}
+}  // namespace
+
+template <int XI>
+__global__ __launch_bounds__(512, 1) void dwg_kernel(DWJobs jobs) {
+  constexpr int B = 32, CW = 2, TS = DWG::TS, GW = DWG::GW, KMAX = 8;
+  constexpr int XW = XI * 8 * 16;                  // x slice row: 8 waves x XI KB over 32 tokens
+  static_assert(XW <= DWG::XWMAX, "x slice row");
+  extern __shared__ __attribute__((aligned(16))) uint16_t dwg_smem[];
+  int jt = 0;
+#pragma unroll
+  for (int u = 1; u < DWJobs::kMax; ++u)
+    if (u < jobs.n && (int64_t)blockIdx.x >= jobs.first[u]) jt = u;
+  const DWJob& J = jobs.job[jt];
+  const int64_t b = (int64_t)blockIdx.x - jobs.first[jt];
+  const int ch = (int)(b % jobs.nchunk);
+  const int r0 = DWG::RB * (int)(b / jobs.nchunk);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = uniform(tid >> 6);
+  const int i = lane & 15, g = lane >> 4;
+  const int r = r0 + w;                            // this wave's block row (R is a multiple of 8)
+  uint16_t* const xs0 = dwg_smem;
+  uint16_t* const xs1 = dwg_smem + TS * XW;
+  uint16_t* const gs0 = dwg_smem + 2 * TS * XW;
+  uint16_t* const gs1 = gs0 + TS * GW;
+  // the row's live slots (scalar loads, consumed here so that no wait for them falls in the loop)
+  int cl[KMAX];
+  unsigned live = 0;
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    cl[k] = k < J.K ? J.col[(int64_t)r * J.K + k] : -1;
+    live |= (cl[k] >= 0 && cl[k] < J.C) ? 1u << k : 0u;
+  }
+  live = (unsigned)uniform((int)live);
+
+  f32x4 acc[KMAX][CW][CW];
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k)
+#pragma unroll
+    for (int md = 0; md < CW; ++md)
+#pragma unroll
+      for (int mD = 0; mD < CW; ++mD) acc[k][md][mD] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t N = jobs.N;
+  const int64_t tbeg = (int64_t)ch * jobs.chunk;
+  const int64_t tend = (tbeg + jobs.chunk) < N ? (tbeg + jobs.chunk) : N;
+  const int ns = tbeg < tend ? (int)((tend - tbeg + TS - 1) / TS) : 0;
+  const int64_t gcol = (int64_t)r0 * B;
+  // the job's operands in registers (the loads' memory clobber would reload them from the
+  // argument block before every issue)
+  const uint16_t* const jx = J.x;
+  const uint16_t* const jg = J.gy;
+  const int64_t ldx = J.ldx, ldg = J.ldg;
+  auto issue = [&](int s, uint16_t* xd, uint16_t* gd) {
+    const int64_t t0 = tbeg + (int64_t)s * TS;
+#pragma unroll
+    for (int j = 0; j < XI; ++j) dwg_load(jx, ldx, 0, XW, t0, N, xd, w * XI + j, lane);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dwg_load(jg, ldg, gcol, GW, t0, N, gd, w * 2 + j, lane);
+  };
+  auto step = [&](int s, uint16_t* xb, uint16_t* gb, uint16_t* xn, uint16_t* gn) {
+    const int64_t t0 = tbeg + (int64_t)s * TS;
+    if (s + 1 < ns) {
+      issue(s + 1, xn, gn);
+      // this wave's loads of slice s are done once only slice s + 1's (XI + 2) are in flight
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (XI + 2));
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+    }
+    dwd_barrier();
+    if (t0 + TS > tend) {
+      // the last slice of the data: rows at or past tend hold clamped copies; zero them
+      const int valid = (int)(tend - t0);
+      for (int q = tid; q < (TS - valid) * (XW / 8); q += 512)
+        *reinterpret_cast<u32x4*>(xb + (int64_t)valid * XW + 8 * q) = u32x4{0, 0, 0, 0};
+      for (int q = tid; q < (TS - valid) * (GW / 8); q += 512)
+        *reinterpret_cast<u32x4*>(gb + (int64_t)valid * GW + 8 * q) = u32x4{0, 0, 0, 0};
+      __syncthreads();
+    }
+    // dW[d][D] += sum_t X[t][d] G[t][D] over the slice's 32 tokens (one k-step)
+    u32x4 bv[CW];
+#pragma unroll
+    for (int mD = 0; mD < CW; ++mD) bv[mD] = dwg_frag(gb, GW, 32 * w + 16 * mD, lane);
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      if ((live >> k) & 1) {
+        const int c = uniform(cl[k]);
+#pragma unroll
+        for (int md = 0; md < CW; ++md) {
+          const u32x4 av = dwg_frag(xb, XW, 32 * c + 16 * md, lane);
+#pragma unroll
+          for (int mD = 0; mD < CW; ++mD) acc[k][md][mD] = mfma_bf16(av, bv[mD], acc[k][md][mD]);
+        }
+      }
+    }
+    // every wave's reads of this buffer pair have returned before slice s + 2 is loaded into it
+    dwd_barrier();
+  };
+  if (ns > 0) issue(0, xs0, gs0);
+  for (int s = 0; s < ns; s += 2) {
+    step(s, xs0, gs0, xs1, gs1);
+    if (s + 1 < ns) step(s + 1, xs1, gs1, xs0, gs0);
+  }
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    if (!((live >> k) & 1)) continue;
+    float* part = J.part + ((int64_t)ch * J.R * J.K + (int64_t)r * J.K + k) * B * B;
+#pragma unroll
+    for (int md = 0; md < CW; ++md)
+#pragma unroll
+      for (int mD = 0; mD < CW; ++mD)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) part[(16 * md + 4 * g + v) * B + 16 * mD + i] = acc[k][md][mD][v];
+  }
+}
+
 // dW[e] = sum over chunks of the partial tiles (fixed order), bf16; dead slots -> 0
 __global__ __launch_bounds__(256) void dw_reduce_kernel(DWJobs jobs, int B) {
   int jt = 0;
@@ -1154,15 +1322,58 @@ int launch_dw(int B, const DWJob* jobs, int n, int64_t N, int chunk, hipStream_t
   J.N = N;
   J.chunk = chunk;
   J.nchunk = N > 0 ? (int)((N + chunk - 1) / chunk) : 0;
-  int64_t blocks = 0, rblocks = 0;
+  int64_t rblocks = 0;
   for (int t = 0; t < n; ++t) {
     J.job[t] = jobs[t];
-    J.first[t] = blocks;
-    blocks += (int64_t)jobs[t].R * ((jobs[t].K + 7) / 8) * J.nchunk;
     J.rfirst[t] = rblocks;
     rblocks += ((int64_t)jobs[t].R * jobs[t].K * B * B + 255) / 256;
   }
+  // B = 32 weights with at most 8 slots per row, rows in whole groups of 8 and narrow input rows
+  // (the gate and up weights of d_model <= 1024) take dwg_kernel, one launch per input width;
+  // the rest dw_dma_kernel (dw_kernel at B = 64)
+  auto narrow = [&](const DWJob& j) {
+    return B == 32 && j.K <= 8 && j.R % DWG::RB == 0 && j.C % 4 == 0 && j.C * 32 <= 1024 && j.ldx >= (int64_t)j.C * 32;
+  };
+  bool taken[DWJobs::kMax] = {};
+  for (int t = 0; t < n; ++t) {
+    if (taken[t] || !narrow(jobs[t])) continue;
+    DWJobs G = J;
+    G.n = 0;
+    int64_t gb = 0;
+    for (int u = t; u < n; ++u)
+      if (!taken[u] && narrow(jobs[u]) && jobs[u].C == jobs[t].C) {
+        taken[u] = true;
+        G.job[G.n] = jobs[u];
+        G.first[G.n++] = gb;
+        gb += (int64_t)(jobs[u].R / DWG::RB) * J.nchunk;
+      }
+    // one workgroup per CU (160 KB of LDS each): with fewer than 256 the wide-grid kernel is faster
+    // (at 4096 tokens, 64 workgroups: whole backward 0.198 -> 0.258 ms)
+    if (gb < 256) {
+      for (int u = t; u < n; ++u)
+        if (narrow(jobs[u]) && jobs[u].C == jobs[t].C) taken[u] = false;
+      continue;
+    }
+    const int xi = jobs[t].C / 4;                    // 1 KB load instructions of x per wave and slice
+    const size_t lds = (size_t)2 * 32 * 2 * (jobs[t].C * 32 + DWG::RB * 32);
+    auto kern = xi == 8 ? dwg_kernel<8> : xi == 4 ? dwg_kernel<4> : xi == 2 ? dwg_kernel<2> : dwg_kernel<1>;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      return -1;
+    hipLaunchKernelGGL(kern, dim3((unsigned)gb), dim3(512), lds, st, G);
+    if (hipGetLastError() != hipSuccess) return -1;
+  }
+  DWJobs D = J;
+  D.n = 0;
+  int64_t blocks = 0;
+  for (int t = 0; t < n; ++t) {
+    if (taken[t]) continue;
+    D.job[D.n] = jobs[t];
+    D.first[D.n++] = blocks;
+    blocks += (int64_t)jobs[t].R * ((jobs[t].K + 7) / 8) * J.nchunk;
+  }
   if (blocks > 0) {
+    const DWJobs& J = D;
     if (B == 16) hipLaunchKernelGGL(dw_dma_kernel<16>, dim3((unsigned)blocks), dim3(512), 0, st, J);
     else if (B == 32) hipLaunchKernelGGL(dw_dma_kernel<32>, dim3((unsigned)blocks), dim3(512), 0, st, J);
     else if (B == 64) hipLaunchKernelGGL(dw_kernel<64>, dim3((unsigned)blocks), dim3(512), 0, st, J);

@@ -299,16 +299,23 @@ def test_gelu_mlpblock_backward_runs(gpu):
         assert lin.bias.grad is not None
 
 
-def test_swiglu_bwd_full_size_sampled(gpu):
-    """The headline shape (d_model 1024, d_ff 4096, B 32, 25 %, 16384 tokens), saved tensors from
-    the GPU forward: dx checked on sampled token rows (a row of dx depends only on that row), the
-    tile gradients on sampled tiles (each a sum over all 16384 tokens, recomputed in float64 from
-    the same saved tensors); two calls agree bit for bit."""
+@pytest.mark.parametrize("case", [
+    # (d_model, d_ff, N, sentinel_frac)
+    (1024, 4096, 16384, 0.0),          # the headline shape
+    (512, 4096, 16384 + 37, 0.1),      # 16 input column blocks, dead slots, a ragged last token chunk
+])
+def test_swiglu_bwd_full_size_sampled(gpu, case):
+    """Full token counts (the gate/up tile gradients take the workgroup-per-8-rows kernel from
+    256 workgroups on), saved tensors from the GPU forward: dx checked on sampled token rows (a
+    row of dx depends only on that row), the tile gradients on sampled tiles (each a sum over all
+    the tokens, recomputed in float64 from the same saved tensors; dead slots zero); two calls
+    agree bit for bit."""
     import torch
-    _say("full size d_model=1024 d_ff=4096 B=32 N=16384 (sampled)")
-    rng = np.random.default_rng(2024)
-    d_model, d_ff, B, N = 1024, 4096, 32, 16384
-    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25)
+    d_model, d_ff, N, frac = case
+    B = 32
+    _say(f"full size d_model={d_model} d_ff={d_ff} B=32 N={N} sentinel {frac} (sampled)")
+    rng = np.random.default_rng(2024 + d_model)
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25, sentinel_frac=frac)
     x, dy = T.act(rng, N, d_model), T.act(rng, N, d_model)
     gw, uw, dw = T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d)
     x_t, dy_t = T.to_gpu_bf16(x), T.to_gpu_bf16(dy)
@@ -337,8 +344,10 @@ def test_swiglu_bwd_full_size_sampled(gpu):
         R, K = col.shape
         picks = [(int(r), int(k)) for r, k in zip(rng.integers(0, R, 12), rng.integers(0, K, 12))]
         gt = T.to_np(got_t)
-        refs = [ref_tile(r, k) for r, k in picks]
+        refs = [ref_tile(r, k) if col[r, k] >= 0 else np.zeros((B, B)) for r, k in picks]
         den = max(np.abs(np.stack(refs)).max(), 1e-30)
+        picks += [(int(r), int(k)) for r, k in zip(*np.nonzero(col < 0))][:4]   # dead slots
+        refs += [np.zeros((B, B))] * (len(picks) - len(refs))
         for (r, k), ref in zip(picks, refs):
             err = np.abs(gt[r, k] - ref).max() / den
             assert err <= TOL, f"{name} tile ({r},{k}): rel {err}"
