@@ -254,6 +254,21 @@ __device__ __forceinline__ uint32_t bpanel_addr(int row, int chunk, int rowb) {
   return (uint32_t)((n * MT + q) * rowb + ((chunk ^ n) << 4));
 }
 
+// magic numbers of the division by each source's K (round-up method: s = ceil(log2 K); exact for
+// dividends below 2^31): e / K = (umulhi(e, kmul) + e) >> ksh
+static void set_kdiv(TProdArgs& a) {
+  for (int s = 0; s < a.nsrc; ++s) {
+    const uint64_t d = (uint64_t)(a.src[s].K > 0 ? a.src[s].K : 1);
+    int sh = 0;
+    while ((1ull << sh) < d) ++sh;
+    a.src[s].kmul = (uint32_t)(((1ull << 32) * ((1ull << sh) - d)) / d + 1);
+    a.src[s].ksh = sh;
+  }
+}
+__device__ __forceinline__ int kdiv(const TProdSrc& S, int e) {
+  return (int)((__umulhi((uint32_t)e, S.kmul) + (uint32_t)e) >> S.ksh);
+}
+
 template <int B, int MT, int NW>
 __global__ __launch_bounds__(64 * NW, 1) void dh_panel_kernel(TProdArgs a) {
   constexpr int NT = 64 * NW;
@@ -313,7 +328,7 @@ __global__ __launch_bounds__(64 * NW, 1) void dh_panel_kernel(TProdArgs a) {
 #pragma unroll
         for (int m = 0; m < CW; ++m) E.av[ks][m] = ld16(tile + op_row<CW>(i, m) * B + 32 * ks);
     }
-    E.r = e / S.K;
+    E.r = kdiv(S, e);
   };
   f32x4 acc[MT][CW];
   auto compute = [&](const Ent& E) {
@@ -417,6 +432,7 @@ static int launch_dh_panel_t(const TProdArgs& a0, hipStream_t st) {
                           (int)lds) != hipSuccess)
     return -1;
   TProdArgs a = a0;
+  set_kdiv(a);
   const int64_t ntb = (a.N + 16 * MT - 1) / (16 * MT);
   const int smax = a.C / NW > 1 ? a.C / NW : 1;
   a.nsl = ntb >= 256 ? 1 : (int)std::min<int64_t>((256 + ntb - 1) / ntb, smax);
@@ -725,8 +741,8 @@ __global__ __launch_bounds__(64 * DXF_WAVES, 1) void dxf_kernel(TProdArgs a) {
   auto fetch = [&](Slot& S, int j, int e) {
     const bool live = j < n0 + n1;
     const bool s1 = j >= n0;
-    const TProdSrc& Sx = s1 ? S1 : S0;
-    const int r = live ? e / Sx.K : 0;
+    // r = e / K by multiply and shift (a division by a run-time value is a long sequence)
+    const int r = live ? kdiv(s1 ? S1 : S0, e) : 0;
     const int64_t tile = live ? e : 0;              // past the list: tile 0 of source 0, unused
     const uint16_t* tp = (live && s1 ? S1.w : S0.w) + tile * B * B + 8 * g;
 #pragma unroll
@@ -805,6 +821,7 @@ template <int B>
 static int launch_dxf(const TProdArgs& a0, hipStream_t st) {
   constexpr size_t lds = 2 * (size_t)64 * DxStage<B>::COLS * 2;
   TProdArgs a = a0;
+  set_kdiv(a);
   const int64_t ntb = (a.N + 63) / 64;
   a.nsl = (a.C + DXF_WAVES - 1) / DXF_WAVES;
   const int64_t grid = a.nsl == 1 ? ntb : 8 * a.nsl * ((ntb + 7) / 8);
@@ -1297,22 +1314,41 @@ __global__ __launch_bounds__(512, 1) void dwg_kernel(DWJobs jobs) {
   }
 }
 
-// dW[e] = sum over chunks of the partial tiles (fixed order), bf16; dead slots -> 0
+// dW[e] = sum over chunks of the partial tiles (fixed order), bf16; dead slots -> 0.  Four
+// consecutive elements of one tile per thread (16-byte partial loads, four chunks in flight)
 __global__ __launch_bounds__(256) void dw_reduce_kernel(DWJobs jobs, int B) {
   int jt = 0;
 #pragma unroll
   for (int u = 1; u < DWJobs::kMax; ++u)
     if (u < jobs.n && (int64_t)blockIdx.x >= jobs.rfirst[u]) jt = u;
   const DWJob& J = jobs.job[jt];
-  const int64_t idx = ((int64_t)blockIdx.x - jobs.rfirst[jt]) * 256 + threadIdx.x;
+  const int64_t idx = (((int64_t)blockIdx.x - jobs.rfirst[jt]) * 256 + threadIdx.x) * 4;
   const int64_t per = (int64_t)J.R * J.K * B * B;
   if (idx >= per) return;
   const int64_t e = idx / ((int64_t)B * B);
   const int col = J.col[e];
-  float s = 0.f;
-  if (col >= 0 && col < J.C)
-    for (int ch = 0; ch < jobs.nchunk; ++ch) s += J.part[(int64_t)ch * per + idx];
-  J.dw[idx] = f2bf(s);
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  if (col >= 0 && col < J.C) {
+    const float* p = J.part + idx;
+    const int nc = jobs.nchunk;
+    int ch = 0;
+    for (; ch + 4 <= nc; ch += 4) {
+      f32x4 v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const f32x4*>(p + (int64_t)(ch + q) * per);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) s[m] += v[q][m];
+    }
+    for (; ch < nc; ++ch) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(p + (int64_t)ch * per);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) s[m] += v[m];
+    }
+  }
+  const float o[4] = {s[0], s[1], s[2], s[3]};
+  store_bf16<4>(J.dw + idx, o);
 }
 
 int launch_dw(int B, const DWJob* jobs, int n, int64_t N, int chunk, hipStream_t st) {
@@ -1326,7 +1362,7 @@ int launch_dw(int B, const DWJob* jobs, int n, int64_t N, int chunk, hipStream_t
   for (int t = 0; t < n; ++t) {
     J.job[t] = jobs[t];
     J.rfirst[t] = rblocks;
-    rblocks += ((int64_t)jobs[t].R * jobs[t].K * B * B + 255) / 256;
+    rblocks += ((int64_t)jobs[t].R * jobs[t].K * B * B / 4 + 255) / 256;
   }
   // B = 32 weights with at most 8 slots per row, rows in whole groups of 8 and narrow input rows
   // (the gate and up weights of d_model <= 1024) take dwg_kernel, one launch per input width;

@@ -269,6 +269,8 @@ struct TProdSrc {
   const uint16_t* a; int64_t lda;   // activations [N, R*B]
   const uint16_t* w; int K;         // raw tiles [R, K, B, B]
   const int32_t* cnt; const int32_t* list; int64_t cap;
+  // e / K = (umulhi(e, kmul) + e) >> ksh for 0 <= e < 2^31 (set by the launchers that use it)
+  uint32_t kmul; int ksh;
 };
 struct TProdArgs {
   TProdSrc src[2]; int nsrc;
