@@ -354,6 +354,38 @@ def test_swiglu_deep_ring_down_sampled_rows(gpu, case):
     assert np.isfinite(out).all()
 
 
+@pytest.mark.parametrize("shared", [False, True])
+@pytest.mark.parametrize("biases", [False, True])
+def test_swiglu_b16_wide_panel_sampled_rows(gpu, shared, biases):
+    """B = 16 at d_model 2048 on 8192 + 3 tokens (32-token gate/up panels, one row slice: the
+    16-wave gate/up kernel) with and without a shared gate/up topology and biases, dead slots, a
+    ragged last block; sampled rows against the fp64 oracle."""
+    import torch
+    from looped_blockell import kernels
+    d_model, d_ff, B, N = 2048, 2048, 16, 8192 + 3
+    _say(f"swiglu B16 d_model 2048 shared={shared} biases={biases}")
+    rng = np.random.default_rng(2048 + 2 * shared + biases)
+    g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25, sentinel_frac=0.05)
+    if shared:
+        u = (u[0], g[1].copy())
+    x = T.act(rng, N, d_model)
+    bs = [rng.standard_normal(n).astype(np.float32) * 0.1 for n in (d_ff, d_ff, d_model)] if biases else [None] * 3
+    xg = T.to_gpu_bf16(x)
+    wg, wu, wd = T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d)
+    if shared:
+        wu = (wu[0], wg[1])                           # gate's column buffer: the shared-topology kernel
+    pk = kernels.swiglu_prepack(*wg, *wu, *wd)
+    bt = [None if b is None else torch.as_tensor(b, device="cuda") for b in bs]
+    out = T.to_np(kernels.swiglu_fwd_prepacked(xg, pk, *wg, *wu, *wd, add_residual=True, b_gate=bt[0],
+                                               b_up=bt[1], b_down=bt[2]))
+    rows = np.concatenate([np.sort(rng.choice(N, 192, replace=False)), np.arange(N - 4, N), [0]])
+    f64 = lambda w: (w[0].astype(np.float64), w[1])
+    ref, *_ = O.swiglu_fwd(x[rows].astype(np.float64), f64(g), f64(u), f64(d), add_residual=True,
+                           biases=tuple(None if b is None else b.astype(np.float64) for b in bs))
+    rel, ab = T.rel_err(out[rows], ref)
+    assert rel <= TOL, f"rel {rel} abs {ab}"
+
+
 def test_swiglu_b16_full_size_sampled_rows(gpu):
     """B = 16 at d_model 1024, d_ff 4096, density 0.25 (64 down slots per row) on 16384 + 5 tokens:
     one row slice per token block (the 12-wave gate/up kernel), a ragged last block; sampled rows."""
