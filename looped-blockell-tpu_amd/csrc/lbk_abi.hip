@@ -1088,7 +1088,11 @@ int lbk_swiglu_fwd_ternary_prepared(const int8_t* xq, const float* sx, int64_t N
 static size_t tlist_bytes(const lbk_bell* w, int C) {
   return align256((size_t)C * 4) + align256((size_t)C * w->R * w->K * 4);
 }
-static int64_t dw_chunks(int64_t N) { return (N + DW_CHUNK - 1) / DW_CHUNK; }
+// fp32 partial tiles of one weight's tile gradients (the token chunking of launch_dw)
+static size_t dw_part_floats(int64_t N, const lbk_bell* w, int C, int64_t ldg) {
+  const int64_t ch = dw_job_chunk(w->B, w->R, C, ldg, N);
+  return (size_t)((N + ch - 1) / ch) * w->R * w->K * w->B * w->B;
+}
 
 size_t lbk_swiglu_bwd_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
                                       const lbk_bell* down) {
@@ -1096,9 +1100,10 @@ size_t lbk_swiglu_bwd_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell
   const int B = gate->B;
   const int C_in = d_model / B, C_d = gate->R;
   const size_t d_ff = (size_t)gate->R * B;
-  const size_t tiles = (size_t)gate->R * gate->K + (size_t)up->R * up->K + (size_t)down->R * down->K;
+  const size_t parts = dw_part_floats(N, gate, C_in, (int64_t)d_ff) + dw_part_floats(N, up, C_in, (int64_t)d_ff) +
+                       dw_part_floats(N, down, C_d, d_model);
   return tlist_bytes(down, C_d) + tlist_bytes(gate, C_in) + tlist_bytes(up, C_in) +
-         2 * align256((size_t)N * d_ff * 2) + align256((size_t)dw_chunks(N) * tiles * B * B * 4);
+         2 * align256((size_t)N * d_ff * 2) + align256(parts * 4);
 }
 
 size_t lbk_swiglu_bwd_bias_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate, const lbk_bell* up,
@@ -1192,25 +1197,25 @@ int lbk_swiglu_bwd_bias_bf16(const uint16_t* grad_out, const uint16_t* x, const 
     if (launch_tprod(B, 1, b, s)) return LBK_ERR_LAUNCH;
   }
   // tile gradients: gate (x, dg), up (x, du), down (h, dy)
-  const int64_t nch = dw_chunks(N);
   DWJob dj[3];
   int nj = 0;
   size_t poff = 0;
   auto add = [&](const uint16_t* xx, int64_t ldx, const uint16_t* gy, int64_t ldg, const lbk_bell* w, int C,
-                 uint16_t* out) {
+                 uint16_t* out, const TListJob* tl) {
     const int64_t nt = (int64_t)w->R * w->K;
     if (nt == 0) return;
-    dj[nj++] = DWJob{xx, ldx, gy, ldg, w->col_idx, w->R, w->K, C, part + poff, out};
-    poff += (size_t)nch * nt * B * B;
+    dj[nj++] = DWJob{xx, ldx, gy, ldg, w->col_idx, w->R, w->K, C, part + poff, out, tl ? tl->cnt : nullptr,
+                     tl ? tl->list : nullptr, 0, 0};
+    poff += dw_part_floats(N, w, C, ldg);
   };
-  add(x, d_model, dg, d_ff, gate, C_in, d_gate_values);
-  add(x, d_model, du, d_ff, up, C_in, d_up_values);
-  add(h, d_ff, grad_out, d_model, down, C_d, d_down_values);
-  if (nj && launch_dw(B, dj, nj, N, DW_CHUNK, s)) return LBK_ERR_LAUNCH;
+  add(x, d_model, dg, d_ff, gate, C_in, d_gate_values, nullptr);
+  add(x, d_model, du, d_ff, up, C_in, d_up_values, nullptr);
+  // the down weight's transposed lists (built above when N > 0) serve its tile gradients too
+  add(h, d_ff, grad_out, d_model, down, C_d, d_down_values, N > 0 ? &lj[0] : nullptr);
+  if (nj && launch_dw(B, dj, nj, N, s)) return LBK_ERR_LAUNCH;
   // bias gradients: column sums of dg, du and grad_out (the partials after the tile partials)
   if (want_db) {
-    float* cpart = reinterpret_cast<float*>(reinterpret_cast<char*>(part) + align256((size_t)nch * (
-        (size_t)gate->R * gate->K + (size_t)up->R * up->K + (size_t)down->R * down->K) * B * B * 4));
+    float* cpart = reinterpret_cast<float*>(reinterpret_cast<char*>(part) + align256(poff * 4));
     if (d_b_gate && launch_colsum(dg, N, (int)d_ff, d_ff, cpart, d_b_gate, s)) return LBK_ERR_LAUNCH;
     if (d_b_up && launch_colsum(du, N, (int)d_ff, d_ff, cpart, d_b_up, s)) return LBK_ERR_LAUNCH;
     if (d_b_down && launch_colsum(grad_out, N, d_model, d_model, cpart, d_b_down, s)) return LBK_ERR_LAUNCH;
@@ -1221,7 +1226,7 @@ int lbk_swiglu_bwd_bias_bf16(const uint16_t* grad_out, const uint16_t* x, const 
 size_t lbk_block_ell_matmul_bwd_workspace_bytes(int64_t N, int32_t in_features, const lbk_bell* w) {
   if (!w || N < 0 || in_features <= 0 || !tile_ok(w->B) || in_features % w->B) return 0;
   const int C = in_features / w->B;
-  return tlist_bytes(w, C) + align256((size_t)dw_chunks(N) * w->R * w->K * w->B * w->B * 4);
+  return tlist_bytes(w, C) + align256(dw_part_floats(N, w, C, (int64_t)w->R * w->B) * 4);
 }
 
 int lbk_block_ell_matmul_bwd_bf16(const uint16_t* grad_out, const uint16_t* x, int64_t N, int32_t in_features,
@@ -1267,8 +1272,11 @@ int lbk_block_ell_matmul_bwd_bf16(const uint16_t* grad_out, const uint16_t* x, i
     if (launch_tprod(B, 1, a, s)) return LBK_ERR_LAUNCH;
   }
   if (d_values && nt > 0) {
-    DWJob dj{x, in_features, grad_out, out_f, w->col_idx, w->R, w->K, C, part, d_values};
-    if (launch_dw(B, &dj, 1, N, DW_CHUNK, s)) return LBK_ERR_LAUNCH;
+    // the transposed lists exist when dx was computed above
+    const bool lists = dx && N > 0;
+    DWJob dj{x, in_features, grad_out, out_f, w->col_idx, w->R, w->K, C, part, d_values,
+             lists ? lj.cnt : nullptr, lists ? lj.list : nullptr, 0, 0};
+    if (launch_dw(B, &dj, 1, N, s)) return LBK_ERR_LAUNCH;
   }
   return LBK_OK;
 }

@@ -37,6 +37,10 @@
 //                  d_model <= 1024, B = 32, K <= 8): a workgroup owns 8 block rows
 //                  and stages the whole x row slice once per 32 tokens for their
 //                  64 tiles (taken when it fills the CUs, 256 workgroups).
+//   dwt_kernel     the same with the roles exchanged for a weight with narrow output
+//                  rows (down, d_model <= 1024, B = 32): a workgroup owns 8 input
+//                  column blocks, stages the whole dy row slice, and its waves walk
+//                  the pooled transposed lists of the 8 blocks.
 //   dw_kernel      tile gradients: a workgroup owns one block row, up to 8 of
 //                  its slots (one per wave) and a chunk of tokens; token slices
 //                  of X and G are staged row-major in LDS and read back
@@ -910,8 +914,8 @@ __global__ __launch_bounds__(512) void dw_kernel(DWJobs jobs) {
   const DWJob& J = jobs.job[jt];
   const int64_t b = (int64_t)blockIdx.x - jobs.first[jt];
   const int KG = (J.K + 7) / 8;              // slot groups of a row
-  const int ch = (int)(b % jobs.nchunk);
-  const int rg = (int)(b / jobs.nchunk);
+  const int ch = (int)(b % J.nchunk);
+  const int rg = (int)(b / J.nchunk);
   const int r = rg / KG, kg = rg - r * KG;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = uniform(tid >> 6);
@@ -930,8 +934,8 @@ __global__ __launch_bounds__(512) void dw_kernel(DWJobs jobs) {
 #pragma unroll
     for (int mD = 0; mD < CW; ++mD) acc[md][mD] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int64_t tbeg = (int64_t)ch * jobs.chunk;
-  const int64_t tend = (tbeg + jobs.chunk) < jobs.N ? (tbeg + jobs.chunk) : jobs.N;
+  const int64_t tbeg = (int64_t)ch * J.chunk;
+  const int64_t tend = (tbeg + J.chunk) < jobs.N ? (tbeg + J.chunk) : jobs.N;
   const int64_t xcol = (int64_t)(live ? col : 0) * B;
   const int64_t gcol = (int64_t)r * B;
   for (int64_t t0 = tbeg; t0 < tend; t0 += TS) {
@@ -1057,8 +1061,8 @@ __global__ __launch_bounds__(512) void dw_dma_kernel(DWJobs jobs) {
   const DWJob& J = jobs.job[jt];
   const int64_t b = (int64_t)blockIdx.x - jobs.first[jt];
   const int KG = (J.K + 7) / 8;
-  const int ch = (int)(b % jobs.nchunk);
-  const int rg = (int)(b / jobs.nchunk);
+  const int ch = (int)(b % J.nchunk);
+  const int rg = (int)(b / J.nchunk);
   const int r = rg / KG, kg = rg - r * KG;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = uniform(tid >> 6);
@@ -1077,8 +1081,8 @@ __global__ __launch_bounds__(512) void dw_dma_kernel(DWJobs jobs) {
     for (int mD = 0; mD < CW; ++mD) acc[md][mD] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int64_t N = jobs.N;
-  const int64_t tbeg = (int64_t)ch * jobs.chunk;
-  const int64_t tend = (tbeg + jobs.chunk) < N ? (tbeg + jobs.chunk) : N;
+  const int64_t tbeg = (int64_t)ch * J.chunk;
+  const int64_t tend = (tbeg + J.chunk) < N ? (tbeg + J.chunk) : N;
   const int ns = tbeg < tend ? (int)((tend - tbeg + TS - 1) / TS) : 0;
   const int64_t xcol = (int64_t)(live ? col : 0) * B;
   const int64_t gcol = (int64_t)r * B;
@@ -1213,8 +1217,8 @@ __global__ __launch_bounds__(512, 1) void dwg_kernel(DWJobs jobs) {
     if (u < jobs.n && (int64_t)blockIdx.x >= jobs.first[u]) jt = u;
   const DWJob& J = jobs.job[jt];
   const int64_t b = (int64_t)blockIdx.x - jobs.first[jt];
-  const int ch = (int)(b % jobs.nchunk);
-  const int r0 = DWG::RB * (int)(b / jobs.nchunk);
+  const int ch = (int)(b % J.nchunk);
+  const int r0 = DWG::RB * (int)(b / J.nchunk);
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = uniform(tid >> 6);
   const int i = lane & 15, g = lane >> 4;
@@ -1242,8 +1246,8 @@ __global__ __launch_bounds__(512, 1) void dwg_kernel(DWJobs jobs) {
       for (int mD = 0; mD < CW; ++mD) acc[k][md][mD] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int64_t N = jobs.N;
-  const int64_t tbeg = (int64_t)ch * jobs.chunk;
-  const int64_t tend = (tbeg + jobs.chunk) < N ? (tbeg + jobs.chunk) : N;
+  const int64_t tbeg = (int64_t)ch * J.chunk;
+  const int64_t tend = (tbeg + J.chunk) < N ? (tbeg + J.chunk) : N;
   const int ns = tbeg < tend ? (int)((tend - tbeg + TS - 1) / TS) : 0;
   const int64_t gcol = (int64_t)r0 * B;
   // the job's operands in registers (the loads' memory clobber would reload them from the
@@ -1314,6 +1318,151 @@ __global__ __launch_bounds__(512, 1) void dwg_kernel(DWJobs jobs) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// tile gradients of a weight whose output rows are narrow (down: G = dy at most 1024 wide)
+// ---------------------------------------------------------------------------
+// dwt_kernel<XI>: dwg_kernel with the operands' roles exchanged.  A workgroup owns 8 input column
+// blocks c0 .. c0 + 7 and a chunk of tokens; per 32-token slice it stages the whole G row
+// G[t, 0 : R B] (XI load instructions per wave) and X[t, c0 B : (c0 + 8) B].  The slots that read
+// the 8 column blocks (the transposed lists, in list order, block after block) are pooled and
+// wave w takes pooled entries w, w + 8, ..., at most KT of them per pass over the tokens (a second
+// pass only when the 8 blocks have more than 8 KT slots together).  Entry e = r K + k multiplies
+// X[:, c B ..] (A operand, from the narrow slice) by G[:, r B ..] (B operand, from the wide one)
+// into its partial tile, stored where dw_dma_kernel stores it, in the same token order.
+template <int XI>
+__global__ __launch_bounds__(512, 1) void dwt_kernel(DWJobs jobs) {
+  constexpr int B = 32, CW = 2, TS = DWG::TS, GW = DWG::GW, KT = 11;
+  constexpr int XW = XI * 8 * 16;                  // G slice row: 8 waves x XI KB over 32 tokens
+  static_assert(XW <= DWG::XWMAX, "G slice row");
+  extern __shared__ __attribute__((aligned(16))) uint16_t dwg_smem[];
+  int jt = 0;
+#pragma unroll
+  for (int u = 1; u < DWJobs::kMax; ++u)
+    if (u < jobs.n && (int64_t)blockIdx.x >= jobs.first[u]) jt = u;
+  const DWJob& J = jobs.job[jt];
+  const int64_t b = (int64_t)blockIdx.x - jobs.first[jt];
+  const int ch = (int)(b % J.nchunk);
+  const int c0 = 8 * (int)(b / J.nchunk);         // C is a multiple of 8
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = uniform(tid >> 6);
+  const int i = lane & 15, g = lane >> 4;
+  uint16_t* const ws0 = dwg_smem;                  // G slices (wide)
+  uint16_t* const ws1 = dwg_smem + TS * XW;
+  uint16_t* const ns0 = dwg_smem + 2 * TS * XW;    // X slices (narrow)
+  uint16_t* const ns1 = ns0 + TS * GW;
+  const int K = J.K, RK = J.R * J.K;
+  // pooled slot count of the 8 column blocks
+  int total = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) total += J.tcnt[c0 + q];
+  total = uniform(total);
+  const int npass = (total + 8 * KT - 1) / (8 * KT);
+
+  const int64_t N = jobs.N;
+  const int64_t tbeg = (int64_t)ch * J.chunk;
+  const int64_t tend = (tbeg + J.chunk) < N ? (tbeg + J.chunk) : N;
+  const int ns = tbeg < tend ? (int)((tend - tbeg + TS - 1) / TS) : 0;
+  const uint16_t* const jx = J.x;
+  const uint16_t* const jg = J.gy;
+  const int64_t ldx = J.ldx, ldg = J.ldg;
+  const int64_t xcol = (int64_t)c0 * B;
+  auto issue = [&](int s, uint16_t* wd, uint16_t* nd) {
+    const int64_t t0 = tbeg + (int64_t)s * TS;
+    // the lane index through an empty asm: the load addresses are formed per slice instead of
+    // being kept in registers across the loop (the accumulators leave no room for them)
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+#pragma unroll
+    for (int j = 0; j < XI; ++j) dwg_load(jg, ldg, 0, XW, t0, N, wd, w * XI + j, ln);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dwg_load(jx, ldx, xcol, GW, t0, N, nd, w * 2 + j, ln);
+  };
+  for (int p = 0; p < npass; ++p) {
+    // this wave's entries of pass p: lane u < KT holds entry u as one word, row r (R <= 32) |
+    // column block within the group << 6 | slot index e = r K + k << 9 (e < 2^23)
+    int pre[8];                                    // start of each block's run in the pool
+    pre[0] = 0;
+#pragma unroll
+    for (int q = 1; q < 8; ++q) pre[q] = pre[q - 1] + J.tcnt[c0 + q - 1];
+    const int j = 8 * KT * p + w + 8 * lane;
+    const bool valid = lane < KT && j < total;
+    int cb = 0, base = 0;
+#pragma unroll
+    for (int q = 1; q < 8; ++q)
+      if (j >= pre[q]) {
+        cb = q;
+        base = pre[q];
+      }
+    const int e = valid ? J.tlist[(int64_t)(c0 + cb) * RK + (j - base)] : 0;
+    const int entv = (e / K) | (cb << 6) | (e << 9);
+    const unsigned live = (unsigned)__ballot(valid);
+    f32x4 acc[KT][CW][CW];
+#pragma unroll
+    for (int u = 0; u < KT; ++u)
+#pragma unroll
+      for (int md = 0; md < CW; ++md)
+#pragma unroll
+        for (int mD = 0; mD < CW; ++mD) acc[u][md][mD] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto step = [&](int s, uint16_t* wb, uint16_t* nb, uint16_t* wn, uint16_t* nn) {
+      const int64_t t0 = tbeg + (int64_t)s * TS;
+      if (s + 1 < ns) {
+        issue(s + 1, wn, nn);
+        // this wave's loads of slice s are done once only slice s + 1's (XI + 2) are in flight
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (XI + 2));
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+      }
+      dwd_barrier();
+      if (t0 + TS > tend) {
+        // the last slice of the data: rows at or past tend hold clamped copies; zero them
+        const int valid = (int)(tend - t0);
+        for (int q = tid; q < (TS - valid) * (XW / 8); q += 512)
+          *reinterpret_cast<u32x4*>(wb + (int64_t)valid * XW + 8 * q) = u32x4{0, 0, 0, 0};
+        for (int q = tid; q < (TS - valid) * (GW / 8); q += 512)
+          *reinterpret_cast<u32x4*>(nb + (int64_t)valid * GW + 8 * q) = u32x4{0, 0, 0, 0};
+        __syncthreads();
+      }
+      // dW[e][d][D] += sum_t X[t][c B + d] G[t][r B + D] over the slice's 32 tokens
+#pragma unroll
+      for (int u = 0; u < KT; ++u) {
+        if ((live >> u) & 1) {
+          const int word = __builtin_amdgcn_readlane(entv, u);
+          const int cb = (word >> 6) & 7, rm = word & 63;
+          u32x4 av[CW], bv[CW];
+#pragma unroll
+          for (int md = 0; md < CW; ++md) av[md] = dwg_frag(nb, GW, 32 * cb + 16 * md, lane);
+#pragma unroll
+          for (int mD = 0; mD < CW; ++mD) bv[mD] = dwg_frag(wb, XW, 32 * rm + 16 * mD, lane);
+#pragma unroll
+          for (int md = 0; md < CW; ++md)
+#pragma unroll
+            for (int mD = 0; mD < CW; ++mD) acc[u][md][mD] = mfma_bf16(av[md], bv[mD], acc[u][md][mD]);
+        }
+        // one entry's fragments live at a time (the accumulators take 176 VGPRs)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // every wave's reads of this buffer pair have returned before slice s + 2 is loaded into it
+      dwd_barrier();
+    };
+    if (ns > 0) issue(0, ws0, ns0);
+    for (int s = 0; s < ns; s += 2) {
+      step(s, ws0, ns0, ws1, ns1);
+      if (s + 1 < ns) step(s + 1, ws1, ns1, ws0, ns0);
+    }
+#pragma unroll
+    for (int u = 0; u < KT; ++u) {
+      if (!((live >> u) & 1)) continue;
+      float* part = J.part + ((int64_t)ch * RK + ((unsigned)__builtin_amdgcn_readlane(entv, u) >> 9)) * B * B;
+#pragma unroll
+      for (int md = 0; md < CW; ++md)
+#pragma unroll
+        for (int mD = 0; mD < CW; ++mD)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) part[(16 * md + 4 * g + v) * B + 16 * mD + i] = acc[u][md][mD][v];
+    }
+  }
+}
+
 // dW[e] = sum over chunks of the partial tiles (fixed order), bf16; dead slots -> 0.  Four
 // consecutive elements of one tile per thread (16-byte partial loads, four chunks in flight)
 __global__ __launch_bounds__(256) void dw_reduce_kernel(DWJobs jobs, int B) {
@@ -1330,7 +1479,7 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(DWJobs jobs, int B) {
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
   if (col >= 0 && col < J.C) {
     const float* p = J.part + idx;
-    const int nc = jobs.nchunk;
+    const int nc = J.nchunk;
     int ch = 0;
     for (; ch + 4 <= nc; ch += 4) {
       f32x4 v[4];
@@ -1351,13 +1500,27 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(DWJobs jobs, int B) {
   store_bf16<4>(J.dw + idx, o);
 }
 
-int launch_dw(int B, const DWJob* jobs, int n, int64_t N, int chunk, hipStream_t st) {
-  if (n < 1 || n > DWJobs::kMax || chunk < 64 || chunk % 64) return -2;   // whole slices of 32 and 64 tokens
+int dw_job_chunk(int B, int R, int C, int64_t ldg, int64_t N) {
+  const bool wide_in = (int64_t)C * 32 > 1024;
+  const bool narrow_out = B == 32 && C % 8 == 0 && (R == 8 || R == 16 || R == 32) && ldg >= (int64_t)R * 32;
+  // one workgroup per CU (160 KB of LDS): with fewer than 256 the slot-per-wave kernel is faster
+  // (at 128 workgroups: 151 against 117 us for the config-2 down weight)
+  const int64_t half = DW_CHUNK / 2;
+  const bool fills = (int64_t)(C / 8) * ((N + half - 1) / half) >= 256;
+  return wide_in && narrow_out && fills ? (int)half : DW_CHUNK;
+}
+
+int launch_dw(int B, const DWJob* jobs_in, int n, int64_t N, hipStream_t st) {
+  if (n < 1 || n > DWJobs::kMax) return -2;
+  DWJob jobs[DWJobs::kMax];
+  for (int t = 0; t < n; ++t) {
+    jobs[t] = jobs_in[t];
+    jobs[t].chunk = dw_job_chunk(B, jobs[t].R, jobs[t].C, jobs[t].ldg, N);   // whole slices of 32 and 64 tokens
+    jobs[t].nchunk = N > 0 ? (int)((N + jobs[t].chunk - 1) / jobs[t].chunk) : 0;
+  }
   DWJobs J{};
   J.n = n;
   J.N = N;
-  J.chunk = chunk;
-  J.nchunk = N > 0 ? (int)((N + chunk - 1) / chunk) : 0;
   int64_t rblocks = 0;
   for (int t = 0; t < n; ++t) {
     J.job[t] = jobs[t];
@@ -1381,7 +1544,7 @@ int launch_dw(int B, const DWJob* jobs, int n, int64_t N, int chunk, hipStream_t
         taken[u] = true;
         G.job[G.n] = jobs[u];
         G.first[G.n++] = gb;
-        gb += (int64_t)(jobs[u].R / DWG::RB) * J.nchunk;
+        gb += (int64_t)(jobs[u].R / DWG::RB) * jobs[u].nchunk;
       }
     // one workgroup per CU (160 KB of LDS each): with fewer than 256 the wide-grid kernel is faster
     // (at 4096 tokens, 64 workgroups: whole backward 0.198 -> 0.258 ms)
@@ -1399,6 +1562,31 @@ int launch_dw(int B, const DWJob* jobs, int n, int64_t N, int chunk, hipStream_t
     hipLaunchKernelGGL(kern, dim3((unsigned)gb), dim3(512), lds, st, G);
     if (hipGetLastError() != hipSuccess) return -1;
   }
+  // weights given the half chunk (narrow output rows, R B <= 1024: the down weight of d_model <=
+  // 1024, with enough workgroups) and their transposed lists take dwt_kernel, one launch per
+  // output width
+  auto narrow_out = [&](const DWJob& j) { return j.chunk == DW_CHUNK / 2 && j.tcnt && j.tlist; };
+  for (int t = 0; t < n; ++t) {
+    if (taken[t] || !narrow_out(jobs[t])) continue;
+    DWJobs G = J;
+    G.n = 0;
+    int64_t gb = 0;
+    for (int u = t; u < n; ++u)
+      if (!taken[u] && narrow_out(jobs[u]) && jobs[u].R == jobs[t].R) {
+        taken[u] = true;
+        G.job[G.n] = jobs[u];
+        G.first[G.n++] = gb;
+        gb += (int64_t)(jobs[u].C / 8) * jobs[u].nchunk;
+      }
+    const int xi = jobs[t].R / 4;                    // 1 KB load instructions of G per wave and slice
+    const size_t lds = (size_t)2 * 32 * 2 * (jobs[t].R * 32 + DWG::GW);
+    auto kern = xi == 8 ? dwt_kernel<8> : xi == 4 ? dwt_kernel<4> : dwt_kernel<2>;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      return -1;
+    hipLaunchKernelGGL(kern, dim3((unsigned)gb), dim3(512), lds, st, G);
+    if (hipGetLastError() != hipSuccess) return -1;
+  }
   DWJobs D = J;
   D.n = 0;
   int64_t blocks = 0;
@@ -1406,7 +1594,7 @@ int launch_dw(int B, const DWJob* jobs, int n, int64_t N, int chunk, hipStream_t
     if (taken[t]) continue;
     D.job[D.n] = jobs[t];
     D.first[D.n++] = blocks;
-    blocks += (int64_t)jobs[t].R * ((jobs[t].K + 7) / 8) * J.nchunk;
+    blocks += (int64_t)jobs[t].R * ((jobs[t].K + 7) / 8) * jobs[t].nchunk;
   }
   if (blocks > 0) {
     const DWJobs& J = D;

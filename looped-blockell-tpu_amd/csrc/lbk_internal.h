@@ -288,6 +288,11 @@ struct DWJob {
   const int32_t* col; int R, K, C;
   float* part;                       // [nchunk, R*K, B, B]
   uint16_t* dw;                      // [R, K, B, B] bf16
+  // optional transposed topology of launch_tlist (per column block c: tcnt[c] slots e at
+  // tlist[c * R * K ..]); lets a weight with wide input rows and narrow output rows (the down
+  // projection) stage its G rows whole and walk the slots of each input column block
+  const int32_t* tcnt; const int32_t* tlist;
+  int chunk, nchunk;                 // tokens per partial tile and their count (set by launch_dw)
 };
 struct DWJobs {
   static constexpr int kMax = 3;
@@ -296,7 +301,13 @@ struct DWJobs {
   int n; int64_t N; int chunk; int nchunk;
 };
 constexpr int DW_CHUNK = 2048;   // tokens per partial tile
-int launch_dw(int B, const DWJob* jobs, int n, int64_t N, int chunk, hipStream_t st);
+// tokens per partial tile of a weight [R, K, B, B] with C input column blocks, G rows of ldg
+// elements and N tokens: DW_CHUNK / 2 where the tile gradients take the transposed-list kernel
+// (input rows too wide to stage whole, output rows at most 1024 wide, and at least 256 of its
+// workgroups at that chunk), else DW_CHUNK
+int dw_job_chunk(int B, int R, int C, int64_t ldg, int64_t N);
+// per job: chunk = dw_job_chunk(...) (a multiple of 64), partials [ceil(N / chunk), R*K, B, B]
+int launch_dw(int B, const DWJob* jobs, int n, int64_t N, hipStream_t st);
 
 // ---- topology transforms (lbk_topo.hip)
 int launch_topo_count(const uint8_t* alive, int R, int K, int32_t* counts, int32_t* mx, hipStream_t st);

@@ -212,6 +212,56 @@ def test_block_ell_matmul_bwd_parity(gpu, case):
     assert np.all(T.to_np(dv)[col < 0] == 0)
 
 
+@pytest.mark.parametrize("case", [
+    # (out_features, in_features, N, topology, sentinel_frac): B = 32, at least 128 workgroups of
+    # 8 input column blocks x token chunks, so the tile gradients take the transposed-list kernel
+    (512, 8192, 8192 + 5, "random", 0.0),          # 16 output blocks, 32 column-block groups, 5 chunks
+    (1024, 4096, 16384 + 3, "concentrated", 0.05),  # every row reads blocks 0-31: 256 slots per group, 3 passes
+    (256, 8192, 16384 + 40, "random", 0.1),         # 8 output blocks, dead and out-of-range slots
+])
+def test_block_ell_matmul_bwd_transposed_tile_grads(gpu, case):
+    """Tile gradients through the transposed lists of the input column blocks: every tile against
+    float32 x^T dy (bf16 inputs, exact products), dead and out-of-range slots zero, two calls
+    bit-identical."""
+    import torch
+    out_f, in_f, N, topo, sf = case
+    B = 32
+    _say(f"matmul bwd transposed tile gradients {case}")
+    rng = np.random.default_rng(out_f + in_f + N)
+    R, Cb = out_f // B, in_f // B
+    K = O.k_for_density(Cb, 0.25)
+    if topo == "concentrated":
+        col = np.stack([rng.permutation(K) for _ in range(R)]).astype(np.int32)
+        vals = (rng.standard_normal((R, K, B, B)) * 0.02).astype(np.float32)
+        vals = O.bf16_round(vals)
+    else:
+        vals, col = T.bell_weight(rng, R, Cb, K, B)
+    dead = rng.random(col.shape) < sf
+    col[dead] = -1
+    if sf > 0:
+        col[0, 0] = Cb + 3                               # out of range: a dead slot too
+    x, dy = T.act(rng, N, in_f), T.act(rng, N, out_f)
+    w = T.gpu_weight((vals, col))
+    dx, dv = _abi_matmul_bwd(T.to_gpu_bf16(dy), T.to_gpu_bf16(x), w)
+    dx2, dv2 = _abi_matmul_bwd(T.to_gpu_bf16(dy), T.to_gpu_bf16(x), w)
+    assert torch.equal(dv, dv2) and torch.equal(dx, dx2)
+    full = x.astype(np.float32).T @ dy.astype(np.float32)          # [in_f, out_f]
+    got = T.to_np(dv)
+    ref = np.zeros_like(got, dtype=np.float32)
+    for r in range(R):
+        for k in range(K):
+            c = col[r, k]
+            if 0 <= c < Cb:
+                ref[r, k] = full[c * B:(c + 1) * B, r * B:(r + 1) * B]
+    rel, ab = T.rel_err(got, ref)
+    assert rel <= TOL, f"d_values: rel {rel} abs {ab}"
+    live = (col >= 0) & (col < Cb)
+    assert np.all(got[~live] == 0)
+    rdx = O.block_ell_matmul_t(dy[:64].astype(np.float64), vals.astype(np.float64), col, Cb)
+    rel, ab = T.rel_err(T.to_np(dx)[:64], rdx)
+    assert rel <= TOL, f"dx (first 64 rows): rel {rel} abs {ab}"
+
+
 def test_block_ell_matmul_bwd_optional_outputs_and_no_tiles(gpu):
     """Either output may be skipped; a weight whose slots are all dead gives dx = 0."""
     import torch
