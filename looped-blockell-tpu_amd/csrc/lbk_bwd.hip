@@ -1203,6 +1203,13 @@ __device__ __forceinline__ void dwg_load(const uint16_t* src, int64_t ld, int64_
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src + tt * ld + col0 + 8 * c),
                "s"(lds) : "memory", "m0");
 }
+// 1 KB of a slice into LDS at slice_j from this lane's source address (dwg_load's transfer with
+// the address formed by the caller)
+__device__ __forceinline__ void dwt_load(const uint16_t* src, uint16_t* slice_j) {
+  const uint32_t lds = static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void*)slice_j));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
 }  // namespace
 
 template <int XI>
@@ -1366,16 +1373,41 @@ __global__ __launch_bounds__(512, 1) void dwt_kernel(DWJobs jobs) {
   const uint16_t* const jg = J.gy;
   const int64_t ldx = J.ldx, ldg = J.ldg;
   const int64_t xcol = (int64_t)c0 * B;
+  // element offsets of this lane's slice loads from the slice's first row (row t, stored chunk
+  // position P = 64 j + lane of instruction j, source chunk c = (P mod cpr) ^ h(t)), formed once:
+  // a full slice then needs only its row base, a scalar (32-bit offsets: 32 rows of ldg and ldx
+  // elements stay below 2^31)
+  uint32_t offw[XI], offn[2];
+#pragma unroll
+  for (int j = 0; j < XI; ++j) {
+    const int P = 64 * (w * XI + j) + lane, t = P / (XW / 8), c = (P - t * (XW / 8)) ^ DWG::h(t);
+    offw[j] = (uint32_t)(t * ldg + 8 * c);
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int P = 64 * (w * 2 + j) + lane, t = P / (GW / 8), c = (P - t * (GW / 8)) ^ DWG::h(t);
+    offn[j] = (uint32_t)(t * ldx + xcol + 8 * c);
+  }
   auto issue = [&](int s, uint16_t* wd, uint16_t* nd) {
-    const int64_t t0 = tbeg + (int64_t)s * TS;
-    // the lane index through an empty asm: the load addresses are formed per slice instead of
-    // being kept in registers across the loop (the accumulators leave no room for them)
-    int ln = lane;
-    asm volatile("" : "+v"(ln));
+    int64_t t0 = tbeg + (int64_t)s * TS;
+    asm volatile("" : "+s"(t0));   // no addresses of the first slice formed ahead of the pass loop
+    if (t0 + TS <= N) {
+      const uint16_t* bw = jg + t0 * ldg;
+      const uint16_t* bn = jx + t0 * ldx;
 #pragma unroll
-    for (int j = 0; j < XI; ++j) dwg_load(jg, ldg, 0, XW, t0, N, wd, w * XI + j, ln);
+      for (int j = 0; j < XI; ++j) dwt_load(bw + offw[j], wd + 512 * (w * XI + j));
 #pragma unroll
-    for (int j = 0; j < 2; ++j) dwg_load(jx, ldx, xcol, GW, t0, N, nd, w * 2 + j, ln);
+      for (int j = 0; j < 2; ++j) dwt_load(bn + offn[j], nd + 512 * (w * 2 + j));
+    } else {
+      // the last slice of the data: rows at or past N read row N - 1 (the lane index through an
+      // empty asm, so that these addresses are not formed ahead and kept across the loop)
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+#pragma unroll
+      for (int j = 0; j < XI; ++j) dwg_load(jg, ldg, 0, XW, t0, N, wd, w * XI + j, ln);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) dwg_load(jx, ldx, xcol, GW, t0, N, nd, w * 2 + j, ln);
+    }
   };
   for (int p = 0; p < npass; ++p) {
     // this wave's entries of pass p: lane u < KT holds entry u as one word, row r (R <= 32) |
@@ -1395,7 +1427,8 @@ __global__ __launch_bounds__(512, 1) void dwt_kernel(DWJobs jobs) {
       }
     const int e = valid ? J.tlist[(int64_t)(c0 + cb) * RK + (j - base)] : 0;
     const int entv = (e / K) | (cb << 6) | (e << 9);
-    const unsigned live = (unsigned)__ballot(valid);
+    // a wave's entries of the pass are a prefix u < nu
+    const int nu = uniform(__popcll(__ballot(valid)));
     f32x4 acc[KT][CW][CW];
 #pragma unroll
     for (int u = 0; u < KT; ++u)
@@ -1425,7 +1458,7 @@ __global__ __launch_bounds__(512, 1) void dwt_kernel(DWJobs jobs) {
       // dW[e][d][D] += sum_t X[t][c B + d] G[t][r B + D] over the slice's 32 tokens
 #pragma unroll
       for (int u = 0; u < KT; ++u) {
-        if ((live >> u) & 1) {
+        if (u < nu) {
           const int word = __builtin_amdgcn_readlane(entv, u);
           const int cb = (word >> 6) & 7, rm = word & 63;
           u32x4 av[CW], bv[CW];
@@ -1451,7 +1484,7 @@ __global__ __launch_bounds__(512, 1) void dwt_kernel(DWJobs jobs) {
     }
 #pragma unroll
     for (int u = 0; u < KT; ++u) {
-      if (!((live >> u) & 1)) continue;
+      if (u >= nu) continue;
       float* part = J.part + ((int64_t)ch * RK + ((unsigned)__builtin_amdgcn_readlane(entv, u) >> 9)) * B * B;
 #pragma unroll
       for (int md = 0; md < CW; ++md)
