@@ -275,11 +275,21 @@ def bench_bf16_backward(steps, warmup, device):
         sl = [t[:n].contiguous() for t in (dy, x, gp, uo, h)]
         ms_n, _ = time_steps(lambda i: kernels.swiglu_bwd(*sl, *g, *u, *d), steps, warmup)
         by_tokens[str(n)] = dict(ms_per_step=ms_n, value=2 * nonzero_flops(dict(w, N=n)) / (ms_n * 1e-3) / 1e12)
+    # the same geometry at B = 16 (the reference's default tile)
+    w16 = dict(w, B=16)
+    g16, u16, d16 = make_ffn(w16, device, gen)
+    _, h16, gp16, uo16 = kernels.swiglu_fwd_with_intermediate(x, *g16, *u16, *d16, add_residual=True)
+    ms16, per16 = time_steps(lambda i: kernels.swiglu_bwd(dy, x, gp16, uo16, h16, *g16, *u16, *d16), steps, warmup)
+    f16 = 2 * nonzero_flops(w16)
     return dict(workload="backward of the headline workload (dx and the gate/up/down tile gradients)",
                 ms_per_step=ms, value=flops / (ms * 1e-3) / 1e12, unit="TFLOP/s",
                 frac_of_bf16_peak=flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, kernel_ms_avg=sum(per) / len(per),
                 fewer_tokens=dict(workload="the same backward on the first N tokens", unit="TFLOP/s",
-                                  by_tokens=by_tokens))
+                                  by_tokens=by_tokens),
+                b16=dict(workload="the same geometry at B = 16", ms_per_step=ms16,
+                         value=f16 / (ms16 * 1e-3) / 1e12, unit="TFLOP/s",
+                         frac_of_bf16_peak=f16 / (ms16 * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                         kernel_ms_avg=sum(per16) / len(per16)))
 
 
 def bench_topology(steps, warmup, device):

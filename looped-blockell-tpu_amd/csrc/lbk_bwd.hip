@@ -1496,6 +1496,240 @@ __global__ __launch_bounds__(512, 1) void dwt_kernel(DWJobs jobs) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// tile gradients at B = 16: the blocked forms above with 16 waves
+// ---------------------------------------------------------------------------
+// A 16 x 16 tile over a 32-token slice is one 16x16x32 MFMA whose operands are one transposed
+// fragment each (dwg_frag covers 16 columns), so a wave's accumulators are one f32x4 per tile and
+// 16 waves fit 128 VGPRs.  The slices keep the layout of dwg_kernel: 32 rows of the wide operand
+// (XW elements) and of a 256-column narrow one, double-buffered (160 KB at XW = 1024).
+//
+// dwg16_kernel<XI>: a workgroup owns 16 block rows r0 .. r0 + 15 (one per wave, at most 16 slots
+// each) and a token chunk; per slice it stages x[t, 0 : C 16] and G[t, r0 16 : (r0 + 16) 16].
+template <int XI>
+__global__ __launch_bounds__(1024, 1) void dwg16_kernel(DWJobs jobs) {
+  constexpr int B = 16, TS = DWG::TS, NW = 16, RB = 16, GW = RB * 16, KMAX = 16;
+  constexpr int XW = XI * NW * 16;                 // x slice row: 16 waves x XI KB over 32 tokens
+  static_assert(XW <= DWG::XWMAX && GW == DWG::GW, "slice rows");
+  extern __shared__ __attribute__((aligned(16))) uint16_t dwg_smem[];
+  int jt = 0;
+#pragma unroll
+  for (int u = 1; u < DWJobs::kMax; ++u)
+    if (u < jobs.n && (int64_t)blockIdx.x >= jobs.first[u]) jt = u;
+  const DWJob& J = jobs.job[jt];
+  const int64_t b = (int64_t)blockIdx.x - jobs.first[jt];
+  const int ch = (int)(b % J.nchunk);
+  const int r0 = RB * (int)(b / J.nchunk);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = uniform(tid >> 6);
+  const int i = lane & 15, g = lane >> 4;
+  const int r = r0 + w;                            // this wave's block row (R is a multiple of 16)
+  uint16_t* const xs0 = dwg_smem;
+  uint16_t* const xs1 = dwg_smem + TS * XW;
+  uint16_t* const gs0 = dwg_smem + 2 * TS * XW;
+  uint16_t* const gs1 = gs0 + TS * GW;
+  int cl[KMAX];
+  unsigned live = 0;
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    cl[k] = k < J.K ? J.col[(int64_t)r * J.K + k] : -1;
+    live |= (cl[k] >= 0 && cl[k] < J.C) ? 1u << k : 0u;
+  }
+  live = (unsigned)uniform((int)live);
+  f32x4 acc[KMAX];
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t N = jobs.N;
+  const int64_t tbeg = (int64_t)ch * J.chunk;
+  const int64_t tend = (tbeg + J.chunk) < N ? (tbeg + J.chunk) : N;
+  const int ns = tbeg < tend ? (int)((tend - tbeg + TS - 1) / TS) : 0;
+  const int64_t gcol = (int64_t)r0 * B;
+  const uint16_t* const jx = J.x;
+  const uint16_t* const jg = J.gy;
+  const int64_t ldx = J.ldx, ldg = J.ldg;
+  auto issue = [&](int s, uint16_t* xd, uint16_t* gd) {
+    const int64_t t0 = tbeg + (int64_t)s * TS;
+#pragma unroll
+    for (int j = 0; j < XI; ++j) dwg_load(jx, ldx, 0, XW, t0, N, xd, w * XI + j, lane);
+    dwg_load(jg, ldg, gcol, GW, t0, N, gd, w, lane);
+  };
+  auto step = [&](int s, uint16_t* xb, uint16_t* gb, uint16_t* xn, uint16_t* gn) {
+    const int64_t t0 = tbeg + (int64_t)s * TS;
+    if (s + 1 < ns) {
+      issue(s + 1, xn, gn);
+      // this wave's loads of slice s are done once only slice s + 1's (XI + 1) are in flight
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (XI + 1));
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+    }
+    dwd_barrier();
+    if (t0 + TS > tend) {
+      const int valid = (int)(tend - t0);
+      for (int q = tid; q < (TS - valid) * (XW / 8); q += 1024)
+        *reinterpret_cast<u32x4*>(xb + (int64_t)valid * XW + 8 * q) = u32x4{0, 0, 0, 0};
+      for (int q = tid; q < (TS - valid) * (GW / 8); q += 1024)
+        *reinterpret_cast<u32x4*>(gb + (int64_t)valid * GW + 8 * q) = u32x4{0, 0, 0, 0};
+      __syncthreads();
+    }
+    // dW[d][D] += sum_t X[t][c 16 + d] G[t][r 16 + D] over the slice's 32 tokens
+    const u32x4 bv = dwg_frag(gb, GW, 16 * w, lane);
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      if ((live >> k) & 1) {
+        const u32x4 av = dwg_frag(xb, XW, 16 * uniform(cl[k]), lane);
+        acc[k] = mfma_bf16(av, bv, acc[k]);
+      }
+    }
+    dwd_barrier();
+  };
+  if (ns > 0) issue(0, xs0, gs0);
+  for (int s = 0; s < ns; s += 2) {
+    step(s, xs0, gs0, xs1, gs1);
+    if (s + 1 < ns) step(s + 1, xs1, gs1, xs0, gs0);
+  }
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    if (!((live >> k) & 1)) continue;
+    float* part = J.part + ((int64_t)ch * J.R * J.K + (int64_t)r * J.K + k) * B * B;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) part[(4 * g + v) * B + i] = acc[k][v];
+  }
+}
+
+// dwt16_kernel<XI>: dwt_kernel at B = 16 with 16 waves: a workgroup owns 16 input column blocks
+// (256 columns) and stages the whole G row (R 16 <= 1024); the slots of the 16 blocks are pooled
+// and wave w takes pooled entries w, w + 16, ..., at most KT per pass.
+template <int XI>
+__global__ __launch_bounds__(1024, 1) void dwt16_kernel(DWJobs jobs) {
+  constexpr int B = 16, TS = DWG::TS, NW = 16, GW = 256, KT = 20, NCB = 16;
+  constexpr int XW = XI * NW * 16;                 // G slice row: 16 waves x XI KB over 32 tokens
+  static_assert(XW <= DWG::XWMAX && GW == DWG::GW, "slice rows");
+  extern __shared__ __attribute__((aligned(16))) uint16_t dwg_smem[];
+  int jt = 0;
+#pragma unroll
+  for (int u = 1; u < DWJobs::kMax; ++u)
+    if (u < jobs.n && (int64_t)blockIdx.x >= jobs.first[u]) jt = u;
+  const DWJob& J = jobs.job[jt];
+  const int64_t b = (int64_t)blockIdx.x - jobs.first[jt];
+  const int ch = (int)(b % J.nchunk);
+  const int c0 = NCB * (int)(b / J.nchunk);       // C is a multiple of 16
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = uniform(tid >> 6);
+  const int i = lane & 15, g = lane >> 4;
+  uint16_t* const ws0 = dwg_smem;                  // G slices (wide)
+  uint16_t* const ws1 = dwg_smem + TS * XW;
+  uint16_t* const ns0 = dwg_smem + 2 * TS * XW;    // X slices (narrow)
+  uint16_t* const ns1 = ns0 + TS * GW;
+  const int K = J.K, RK = J.R * J.K;
+  int total = 0;
+#pragma unroll
+  for (int q = 0; q < NCB; ++q) total += J.tcnt[c0 + q];
+  total = uniform(total);
+  const int npass = (total + NW * KT - 1) / (NW * KT);
+
+  const int64_t N = jobs.N;
+  const int64_t tbeg = (int64_t)ch * J.chunk;
+  const int64_t tend = (tbeg + J.chunk) < N ? (tbeg + J.chunk) : N;
+  const int ns = tbeg < tend ? (int)((tend - tbeg + TS - 1) / TS) : 0;
+  const uint16_t* const jx = J.x;
+  const uint16_t* const jg = J.gy;
+  const int64_t ldx = J.ldx, ldg = J.ldg;
+  const int64_t xcol = (int64_t)c0 * B;
+  // per-lane element offsets of the slice loads from the slice's first row (as in dwt_kernel)
+  uint32_t offw[XI], offn;
+#pragma unroll
+  for (int j = 0; j < XI; ++j) {
+    const int P = 64 * (w * XI + j) + lane, t = P / (XW / 8), c = (P - t * (XW / 8)) ^ DWG::h(t);
+    offw[j] = (uint32_t)(t * ldg + 8 * c);
+  }
+  {
+    const int P = 64 * w + lane, t = P / (GW / 8), c = (P - t * (GW / 8)) ^ DWG::h(t);
+    offn = (uint32_t)(t * ldx + xcol + 8 * c);
+  }
+  auto issue = [&](int s, uint16_t* wd, uint16_t* nd) {
+    int64_t t0 = tbeg + (int64_t)s * TS;
+    asm volatile("" : "+s"(t0));   // no addresses of the first slice formed ahead of the pass loop
+    if (t0 + TS <= N) {
+      const uint16_t* bw = jg + t0 * ldg;
+#pragma unroll
+      for (int j = 0; j < XI; ++j) dwt_load(bw + offw[j], wd + 512 * (w * XI + j));
+      dwt_load(jx + t0 * ldx + offn, nd + 512 * w);
+    } else {
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+#pragma unroll
+      for (int j = 0; j < XI; ++j) dwg_load(jg, ldg, 0, XW, t0, N, wd, w * XI + j, ln);
+      dwg_load(jx, ldx, xcol, GW, t0, N, nd, w, ln);
+    }
+  };
+  for (int p = 0; p < npass; ++p) {
+    // lane u < KT holds entry u of this wave's pass: row r (R <= 64) | column block within the
+    // group << 6 | slot index e = r K + k << 10 (e < 2^22)
+    int pre[NCB];
+    pre[0] = 0;
+#pragma unroll
+    for (int q = 1; q < NCB; ++q) pre[q] = pre[q - 1] + J.tcnt[c0 + q - 1];
+    const int j = NW * KT * p + w + NW * lane;
+    const bool valid = lane < KT && j < total;
+    int cb = 0, base = 0;
+#pragma unroll
+    for (int q = 1; q < NCB; ++q)
+      if (j >= pre[q]) {
+        cb = q;
+        base = pre[q];
+      }
+    const int e = valid ? J.tlist[(int64_t)(c0 + cb) * RK + (j - base)] : 0;
+    const int entv = (e / K) | (cb << 6) | (e << 10);
+    const int nu = uniform(__popcll(__ballot(valid)));
+    f32x4 acc[KT];
+#pragma unroll
+    for (int u = 0; u < KT; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto step = [&](int s, uint16_t* wb, uint16_t* nb, uint16_t* wn, uint16_t* nn) {
+      const int64_t t0 = tbeg + (int64_t)s * TS;
+      if (s + 1 < ns) {
+        issue(s + 1, wn, nn);
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (XI + 1));
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+      }
+      dwd_barrier();
+      if (t0 + TS > tend) {
+        const int valid_t = (int)(tend - t0);
+        for (int q = tid; q < (TS - valid_t) * (XW / 8); q += 1024)
+          *reinterpret_cast<u32x4*>(wb + (int64_t)valid_t * XW + 8 * q) = u32x4{0, 0, 0, 0};
+        for (int q = tid; q < (TS - valid_t) * (GW / 8); q += 1024)
+          *reinterpret_cast<u32x4*>(nb + (int64_t)valid_t * GW + 8 * q) = u32x4{0, 0, 0, 0};
+        __syncthreads();
+      }
+      // dW[e][d][D] += sum_t X[t][c 16 + d] G[t][r 16 + D] over the slice's 32 tokens
+#pragma unroll
+      for (int u = 0; u < KT; ++u) {
+        if (u < nu) {
+          const int word = __builtin_amdgcn_readlane(entv, u);
+          const int cbu = (word >> 6) & 15, rm = word & 63;
+          const u32x4 av = dwg_frag(nb, GW, 16 * cbu, lane);
+          const u32x4 bv = dwg_frag(wb, XW, 16 * rm, lane);
+          acc[u] = mfma_bf16(av, bv, acc[u]);
+        }
+      }
+      dwd_barrier();
+    };
+    if (ns > 0) issue(0, ws0, ns0);
+    for (int s = 0; s < ns; s += 2) {
+      step(s, ws0, ns0, ws1, ns1);
+      if (s + 1 < ns) step(s + 1, ws1, ns1, ws0, ns0);
+    }
+#pragma unroll
+    for (int u = 0; u < KT; ++u) {
+      if (u >= nu) continue;
+      float* part = J.part + ((int64_t)ch * RK + ((unsigned)__builtin_amdgcn_readlane(entv, u) >> 10)) * B * B;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) part[(4 * g + v) * B + i] = acc[u][v];
+    }
+  }
+}
+
 // dW[e] = sum over chunks of the partial tiles (fixed order), bf16; dead slots -> 0.  Four
 // consecutive elements of one tile per thread (16-byte partial loads, four chunks in flight)
 __global__ __launch_bounds__(256) void dw_reduce_kernel(DWJobs jobs, int B) {
@@ -1533,14 +1767,21 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(DWJobs jobs, int B) {
   store_bf16<4>(J.dw + idx, o);
 }
 
+// the transposed-list kernels: column blocks per workgroup, and whether a weight's shape fits
+static int dwt_blocks(int B) { return B == 32 ? 8 : 16; }
+static bool dwt_shape(int B, int R, int C, int64_t ldg) {
+  if (B == 32) return C % 8 == 0 && (R == 8 || R == 16 || R == 32) && ldg >= (int64_t)R * 32;
+  if (B == 16) return C % 16 == 0 && (R == 16 || R == 32 || R == 64) && ldg >= (int64_t)R * 16;
+  return false;
+}
+
 int dw_job_chunk(int B, int R, int C, int64_t ldg, int64_t N) {
-  const bool wide_in = (int64_t)C * 32 > 1024;
-  const bool narrow_out = B == 32 && C % 8 == 0 && (R == 8 || R == 16 || R == 32) && ldg >= (int64_t)R * 32;
+  const bool wide_in = (int64_t)C * B > 1024;
   // one workgroup per CU (160 KB of LDS): with fewer than 256 the slot-per-wave kernel is faster
   // (at 128 workgroups: 151 against 117 us for the config-2 down weight)
   const int64_t half = DW_CHUNK / 2;
-  const bool fills = (int64_t)(C / 8) * ((N + half - 1) / half) >= 256;
-  return wide_in && narrow_out && fills ? (int)half : DW_CHUNK;
+  const bool fills = (int64_t)(C / dwt_blocks(B)) * ((N + half - 1) / half) >= 256;
+  return wide_in && dwt_shape(B, R, C, ldg) && fills ? (int)half : DW_CHUNK;
 }
 
 int launch_dw(int B, const DWJob* jobs_in, int n, int64_t N, hipStream_t st) {
@@ -1595,9 +1836,41 @@ int launch_dw(int B, const DWJob* jobs_in, int n, int64_t N, hipStream_t st) {
     hipLaunchKernelGGL(kern, dim3((unsigned)gb), dim3(512), lds, st, G);
     if (hipGetLastError() != hipSuccess) return -1;
   }
+  // B = 16 weights with at most 16 slots per row, rows in whole groups of 16 and input rows of
+  // 256 to 1024 elements (the gate and up weights of such models) take dwg16_kernel
+  auto narrow16 = [&](const DWJob& j) {
+    return B == 16 && j.K <= 16 && j.R % 16 == 0 && j.C % 16 == 0 && j.C * 16 <= 1024 &&
+           j.ldx >= (int64_t)j.C * 16;
+  };
+  for (int t = 0; t < n; ++t) {
+    if (taken[t] || !narrow16(jobs[t])) continue;
+    DWJobs G = J;
+    G.n = 0;
+    int64_t gb = 0;
+    for (int u = t; u < n; ++u)
+      if (!taken[u] && narrow16(jobs[u]) && jobs[u].C == jobs[t].C) {
+        taken[u] = true;
+        G.job[G.n] = jobs[u];
+        G.first[G.n++] = gb;
+        gb += (int64_t)(jobs[u].R / 16) * jobs[u].nchunk;
+      }
+    if (gb < 256) {
+      for (int u = t; u < n; ++u)
+        if (narrow16(jobs[u]) && jobs[u].C == jobs[t].C) taken[u] = false;
+      continue;
+    }
+    const int xi = jobs[t].C / 16;                   // 1 KB load instructions of x per wave and slice
+    const size_t lds = (size_t)2 * 32 * 2 * (jobs[t].C * 16 + DWG::GW);
+    auto kern = xi == 4 ? dwg16_kernel<4> : xi == 2 ? dwg16_kernel<2> : dwg16_kernel<1>;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      return -1;
+    hipLaunchKernelGGL(kern, dim3((unsigned)gb), dim3(1024), lds, st, G);
+    if (hipGetLastError() != hipSuccess) return -1;
+  }
   // weights given the half chunk (narrow output rows, R B <= 1024: the down weight of d_model <=
-  // 1024, with enough workgroups) and their transposed lists take dwt_kernel, one launch per
-  // output width
+  // 1024, with enough workgroups) and their transposed lists take dwt_kernel (dwt16_kernel at
+  // B = 16), one launch per output width
   auto narrow_out = [&](const DWJob& j) { return j.chunk == DW_CHUNK / 2 && j.tcnt && j.tlist; };
   for (int t = 0; t < n; ++t) {
     if (taken[t] || !narrow_out(jobs[t])) continue;
@@ -1609,15 +1882,17 @@ int launch_dw(int B, const DWJob* jobs_in, int n, int64_t N, hipStream_t st) {
         taken[u] = true;
         G.job[G.n] = jobs[u];
         G.first[G.n++] = gb;
-        gb += (int64_t)(jobs[u].C / 8) * jobs[u].nchunk;
+        gb += (int64_t)(jobs[u].C / dwt_blocks(B)) * jobs[u].nchunk;
       }
-    const int xi = jobs[t].R / 4;                    // 1 KB load instructions of G per wave and slice
-    const size_t lds = (size_t)2 * 32 * 2 * (jobs[t].R * 32 + DWG::GW);
-    auto kern = xi == 8 ? dwt_kernel<8> : xi == 4 ? dwt_kernel<4> : dwt_kernel<2>;
+    // 1 KB load instructions of G per wave and slice: R B / 128 over 8 waves (B = 32) or 16 (B = 16)
+    const int xi = B == 32 ? jobs[t].R / 4 : jobs[t].R / 16;
+    const size_t lds = (size_t)2 * 32 * 2 * (jobs[t].R * B + DWG::GW);
+    auto kern = B == 32 ? (xi == 8 ? dwt_kernel<8> : xi == 4 ? dwt_kernel<4> : dwt_kernel<2>)
+                        : (xi == 4 ? dwt16_kernel<4> : xi == 2 ? dwt16_kernel<2> : dwt16_kernel<1>);
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)lds) != hipSuccess)
       return -1;
-    hipLaunchKernelGGL(kern, dim3((unsigned)gb), dim3(512), lds, st, G);
+    hipLaunchKernelGGL(kern, dim3((unsigned)gb), dim3(B == 32 ? 512 : 1024), lds, st, G);
     if (hipGetLastError() != hipSuccess) return -1;
   }
   DWJobs D = J;

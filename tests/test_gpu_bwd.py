@@ -213,21 +213,27 @@ def test_block_ell_matmul_bwd_parity(gpu, case):
 
 
 @pytest.mark.parametrize("case", [
-    # (out_features, in_features, N, topology, sentinel_frac): B = 32, at least 128 workgroups of
-    # 8 input column blocks x token chunks, so the tile gradients take the transposed-list kernel
-    (512, 8192, 8192 + 5, "random", 0.0),          # 16 output blocks, 32 column-block groups, 5 chunks
-    (1024, 4096, 16384 + 3, "concentrated", 0.05),  # every row reads blocks 0-31: 256 slots per group, 3 passes
-    (256, 8192, 16384 + 40, "random", 0.1),         # 8 output blocks, dead and out-of-range slots
+    # (out_features, in_features, B, N, topology, sentinel_frac).  Enough workgroups (column-block
+    # groups x token chunks, or row groups x chunks) that the tile gradients take the blocked kernels:
+    # B = 32: the transposed-list kernel (8 input column blocks per workgroup)
+    (512, 8192, 32, 8192 + 5, "random", 0.0),          # 16 output blocks, 32 column-block groups, 5 chunks
+    (1024, 4096, 32, 16384 + 3, "concentrated", 0.05),  # every row reads blocks 0-31: 256 slots per group, 3 passes
+    (256, 8192, 32, 16384 + 40, "random", 0.1),         # 8 output blocks, dead and out-of-range slots
+    # B = 16: the transposed-list kernel with 16 waves (16 column blocks per workgroup)
+    (1024, 8192, 16, 8192 + 5, "random", 0.0),          # 64 output blocks, 32 groups, 9 chunks
+    (512, 4096, 16, 16384 + 3, "concentrated", 0.05),   # every row reads blocks 0-63: 512 slots per group, 2 passes
+    (256, 4096, 16, 16384 + 40, "random", 0.1),         # 16 output blocks, dead and out-of-range slots
+    # B = 16: the row-blocked kernel (16 block rows per workgroup, input rows of 512)
+    (8192, 512, 16, 16384 + 9, "random", 0.05),         # 512 block rows, 8 slots each, 32 row groups x 9 chunks
 ])
-def test_block_ell_matmul_bwd_transposed_tile_grads(gpu, case):
-    """Tile gradients through the transposed lists of the input column blocks: every tile against
-    float32 x^T dy (bf16 inputs, exact products), dead and out-of-range slots zero, two calls
-    bit-identical."""
+def test_block_ell_matmul_bwd_blocked_tile_grads(gpu, case):
+    """Tile gradients through the blocked kernels (transposed lists of the input column blocks, or
+    16 block rows per workgroup at B = 16): every tile against float32 x^T dy (bf16 inputs, exact
+    products), dead and out-of-range slots zero, two calls bit-identical."""
     import torch
-    out_f, in_f, N, topo, sf = case
-    B = 32
-    _say(f"matmul bwd transposed tile gradients {case}")
-    rng = np.random.default_rng(out_f + in_f + N)
+    out_f, in_f, B, N, topo, sf = case
+    _say(f"matmul bwd blocked tile gradients {case}")
+    rng = np.random.default_rng(out_f + in_f + N + B)
     R, Cb = out_f // B, in_f // B
     K = O.k_for_density(Cb, 0.25)
     if topo == "concentrated":
@@ -350,20 +356,19 @@ def test_gelu_mlpblock_backward_runs(gpu):
 
 
 @pytest.mark.parametrize("case", [
-    # (d_model, d_ff, N, sentinel_frac)
-    (1024, 4096, 16384, 0.0),          # the headline shape
-    (512, 4096, 16384 + 37, 0.1),      # 16 input column blocks, dead slots, a ragged last token chunk
+    # (d_model, d_ff, N, sentinel_frac, B)
+    (1024, 4096, 16384, 0.0, 32),          # the headline shape
+    (512, 4096, 16384 + 37, 0.1, 32),      # 16 input column blocks, dead slots, a ragged last token chunk
+    (1024, 4096, 16384 + 5, 0.05, 16),     # the headline geometry at B = 16 (the blocked tile gradients)
 ])
 def test_swiglu_bwd_full_size_sampled(gpu, case):
-    """Full token counts (the gate/up tile gradients take the workgroup-per-8-rows kernel from
-    256 workgroups on), saved tensors from the GPU forward: dx checked on sampled token rows (a
-    row of dx depends only on that row), the tile gradients on sampled tiles (each a sum over all
-    the tokens, recomputed in float64 from the same saved tensors; dead slots zero); two calls
-    agree bit for bit."""
+    """Full token counts (the tile gradients take the blocked kernels from 256 workgroups on),
+    saved tensors from the GPU forward: dx checked on sampled token rows (a row of dx depends only
+    on that row), the tile gradients on sampled tiles (each a sum over all the tokens, recomputed in
+    float64 from the same saved tensors; dead slots zero); two calls agree bit for bit."""
     import torch
-    d_model, d_ff, N, frac = case
-    B = 32
-    _say(f"full size d_model={d_model} d_ff={d_ff} B=32 N={N} sentinel {frac} (sampled)")
+    d_model, d_ff, N, frac, B = case
+    _say(f"full size d_model={d_model} d_ff={d_ff} B={B} N={N} sentinel {frac} (sampled)")
     rng = np.random.default_rng(2024 + d_model)
     g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25, sentinel_frac=frac)
     x, dy = T.act(rng, N, d_model), T.act(rng, N, d_model)
