@@ -611,13 +611,29 @@ __global__ __launch_bounds__(64 * NW, 1) void dx_stage_kernel(TProdArgs a) {
         const int n = __builtin_popcountll(m);       // a contiguous run of lanes (sorted list)
         if (n == 0) break;
         auto ent = [&](int jj) { return __builtin_amdgcn_readlane(lv, base + (jj < n ? jj : n - 1)); };
-        Ent E0, E1;
-        load(ent(0), E0);
-        for (int jj = 0; jj < n; jj += 2) {
-          load(ent(jj + 1), E1);
-          compute(E0);
-          load(ent(jj + 2), E0);
-          if (jj + 1 < n) compute(E1);
+        if constexpr (B == 16) {
+          // 8-byte tile fragments: a 3-entry ring keeps two loads in flight ahead of the MFMAs
+          // (positions past the run reload its last entry and are not computed)
+          constexpr int DXR = 3;
+          Ent E[DXR];
+#pragma unroll
+          for (int k = 0; k < DXR - 1; ++k) load(ent(k), E[k]);
+          for (int jj = 0; jj < n; jj += DXR) {
+#pragma unroll
+            for (int k = 0; k < DXR; ++k) {
+              load(ent(jj + k + DXR - 1), E[(k + DXR - 1) % DXR]);
+              if (jj + k < n) compute(E[k]);
+            }
+          }
+        } else {
+          Ent E0, E1;
+          load(ent(0), E0);
+          for (int jj = 0; jj < n; jj += 2) {
+            load(ent(jj + 1), E1);
+            compute(E0);
+            load(ent(jj + 2), E0);
+            if (jj + 1 < n) compute(E1);
+          }
         }
         jc += n;
         if (base + n < 64) break;                    // the run ended inside this chunk
