@@ -364,7 +364,25 @@ __global__ __launch_bounds__(64 * NW, 1) void dh_panel_kernel(TProdArgs a) {
   typedef uint32_t raw_t __attribute__((ext_vector_type(NV / 2)));
   raw_t graw[MT][NP], uraw[MT][NP];
   auto col_of = [&](int c, int p) { return (int64_t)c * B + (CW == 1 ? 4 * g : 32 * p + 8 * g); };
-  for (int c = sl + a.nsl * w; c < a.C; c += NW * a.nsl) {
+  // a block's count and first 64 list entries are read one block ahead (the list read at a
+  // clamped index, so it needs no count), so that a block issues its tile loads at once instead
+  // of waiting for its list behind its g / u loads
+  const int cstep = NW * a.nsl;
+  const int clast = (int)(S.cap < 64 ? S.cap : 64) - 1;
+  int cnt_n = 0, lv_n = 0;
+  {
+    const int cf = sl + a.nsl * w;
+    if (cf < a.C) {
+      cnt_n = S.cnt[cf];
+      lv_n = S.list[(int64_t)cf * S.cap + (lane < clast ? lane : clast)];
+    }
+  }
+  for (int c = sl + a.nsl * w; c < a.C; c += cstep) {
+    const int cnt = cnt_n, lv0 = lv_n;
+    if (c + cstep < a.C) {
+      cnt_n = S.cnt[c + cstep];
+      lv_n = S.list[(int64_t)(c + cstep) * S.cap + (lane < clast ? lane : clast)];
+    }
 #pragma unroll
     for (int q = 0; q < MT; ++q) {
       const int64_t tn = t0 + 16 * q + i;
@@ -379,10 +397,10 @@ __global__ __launch_bounds__(64 * NW, 1) void dh_panel_kernel(TProdArgs a) {
     for (int q = 0; q < MT; ++q)
 #pragma unroll
       for (int m = 0; m < CW; ++m) acc[q][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int cnt = S.cnt[c];
     const int32_t* L = S.list + (int64_t)c * S.cap;
     for (int j0 = 0; j0 < cnt; j0 += 64) {
-      const int lv = (j0 + lane < cnt) ? L[j0 + lane] : 0;   // 64 entries, one per lane
+      // 64 entries, one per lane (the first 64 from the read ahead)
+      const int lv = j0 == 0 ? lv0 : ((j0 + lane < cnt) ? L[j0 + lane] : 0);
       const int jn = (cnt - j0) < 64 ? (cnt - j0) : 64;
       auto ent = [&](int jj) { return __builtin_amdgcn_readlane(lv, jj < jn ? jj : jn - 1); };
       // a DHR-entry ring: DHR - 1 tile loads in flight ahead of the MFMAs (positions past the
