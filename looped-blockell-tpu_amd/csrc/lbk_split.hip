@@ -76,6 +76,18 @@ __device__ __forceinline__ u32x2 lds8(const unsigned char* base, uint32_t off) {
 __device__ __forceinline__ uint32_t k16_addr(uint32_t lbase, int cb, int g, int i) {
   return lbase + ((uint32_t)(((cb * 2 + (g >> 1)) ^ i) << 4) | (uint32_t)((g & 1) << 3));
 }
+// the same in a stage whose rows with (i & 8) hold their chunk halves swapped: the 16 lanes
+// i = 0 .. 15 of one 8-byte read then fall on 16 different bank pairs (with the chunk XOR alone,
+// lanes i and i + 8 share them)
+__device__ __forceinline__ uint32_t k16s_addr(uint32_t lbase, int cb, int g, int i) {
+  return lbase + ((uint32_t)(((cb * 2 + (g >> 1)) ^ i) << 4) | (uint32_t)(((g & 1) ^ ((i >> 3) & 1)) << 3));
+}
+// a 16-byte chunk of token row `row` as the B = 16 layouts store it (halves swapped when row & 8)
+template <int B>
+__device__ __forceinline__ u32x4 k16s_chunk(const u32x4& v, int row) {
+  if constexpr (B == 16) return (row & 8) ? u32x4{v[2], v[3], v[0], v[1]} : v;
+  else return v;
+}
 
 // gate/up ring depth (positions in flight + 1)
 constexpr int GU_RING = 4;
@@ -221,7 +233,7 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
   auto load_a = [&](const GUSlot<B>& S, AFrags& A) {
     const int cg = uniform(S.cg), cu = uniform(S.cu);
     if constexpr (B == 16) {
-      const uint32_t ag0 = k16_addr(lbase, cg, g, i), au0 = k16_addr(lbase, cu, g, i);
+      const uint32_t ag0 = k16s_addr(lbase, cg, g, i), au0 = k16s_addr(lbase, cu, g, i);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         A.g[mt] = lds8(smem, ag0 + mt * ROWB);
@@ -303,7 +315,8 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
       const int e = tid + NT * it;
       const int row = e / CPR, cc = e % CPR;
       const bool ok = cc < cpr && t0 + row < a.N;
-      if ((NCH % NT == 0 || e < NCH) && cc < cpr) *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, cc, ROWB)) = ok ? pv[it] : u32x4{0, 0, 0, 0};
+      if ((NCH % NT == 0 || e < NCH) && cc < cpr)
+        *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, cc, ROWB)) = k16s_chunk<B>(ok ? pv[it] : u32x4{0, 0, 0, 0}, row);
     }
   } else {
     // fp32 state rows -> RMSNorm -> bf16 panel; wave w owns rows w, w+NW, ...;
@@ -370,7 +383,7 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
                            pack2_bf16(v1[0] * rs * s1[0], v1[1] * rs * s1[1]),
                            pack2_bf16(v1[2] * rs * s1[2], v1[3] * rs * s1[3])};
           *reinterpret_cast<u32x4*>(smem + panel_addr<MT>(row, col / 8, ROWB)) =
-              col < d_model ? o : u32x4{0, 0, 0, 0};
+              k16s_chunk<B>(col < d_model ? o : u32x4{0, 0, 0, 0}, row);
         }
       }
     };
@@ -717,7 +730,7 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
       const int e = tid + NT * u;
       if (e < CHUNKS) {
         const int row = e / (SROWB / 16), c = e - row * (SROWB / 16);
-        *reinterpret_cast<u32x4*>(dn_smem + buf * SBYTES + panel_addr<MT>(row, c, SROWB)) = sreg[u];
+        *reinterpret_cast<u32x4*>(dn_smem + buf * SBYTES + panel_addr<MT>(row, c, SROWB)) = k16s_chunk<B>(sreg[u], row);
       }
     }
   };
@@ -744,7 +757,7 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
   auto compute = [&](const Slot& S, const unsigned char* sb, f32x4 (&ac)[MT][CW]) {
     const int cb = uniform(S.cb);
     if constexpr (B == 16) {
-      const uint32_t a0 = k16_addr(lbase, cb, g, i);
+      const uint32_t a0 = k16s_addr(lbase, cb, g, i);
       u32x2 av[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) av[mt] = lds8(sb, a0 + mt * SROWB);
@@ -891,7 +904,9 @@ __device__ __forceinline__ void dn_tile(const DNArgs& a, int64_t tb, int rg, uns
         for (int v = 0; v < 4; ++v) {
           const int row = 16 * mt + 4 * g + v;
           const float rs = red[NW * TM + row];
-          unsigned char* dst = dn_smem + panel_addr<MT>(row, col / 8, ROWB) + 2 * (col % 8);
+          // (B = 16: the element's half of the chunk swapped in rows with row & 8, as k16s_chunk)
+          unsigned char* dst = dn_smem + panel_addr<MT>(row, col / 8, ROWB) +
+                               ((2 * (col % 8)) ^ (B == 16 ? ((row >> 3) & 1) << 3 : 0));
           if constexpr (CW == 2) {
             *reinterpret_cast<uint32_t*>(dst) =
                 pack2_bf16(acc[rho][mt][0][v] * rs * sc[0], acc[rho][mt][1][v] * rs * sc[1]);
