@@ -228,7 +228,9 @@ int lbk_swiglu_fwd_prepacked_bf16(const uint16_t* x, int64_t N, int32_t d_model,
 /*
  * Workspace bytes needed by lbk_swiglu_bwd_bf16 for this geometry: the transposed
  * column lists of the three weights, dg and du [N, d_ff] bf16, and fp32 partial
- * tile gradients (one set per 2048 tokens).
+ * tile gradients (one set per 2048 tokens; per 1024 for a weight whose input rows are too
+ * wide to stage and whose output rows are at most 1024 wide, e.g. the down weight, when
+ * the token count fills the GPU).
  */
 size_t lbk_swiglu_bwd_workspace_bytes(int64_t N, int32_t d_model, const lbk_bell* gate,
                                       const lbk_bell* up, const lbk_bell* down);
