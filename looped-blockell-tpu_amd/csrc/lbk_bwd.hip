@@ -1838,8 +1838,10 @@ int launch_dw(int B, const DWJob* jobs_in, int n, int64_t N, hipStream_t st) {
   // B = 32 weights with at most 8 slots per row, rows in whole groups of 8 and narrow input rows
   // (the gate and up weights of d_model <= 1024) take dwg_kernel, one launch per input width;
   // the rest dw_dma_kernel (dw_kernel at B = 64)
+  // (the x slice row C * 32 is XI KB per wave over the 8 waves, XI in {1, 2, 4, 8}: C in {4, 8, 16, 32})
   auto narrow = [&](const DWJob& j) {
-    return B == 32 && j.K <= 8 && j.R % DWG::RB == 0 && j.C % 4 == 0 && j.C * 32 <= 1024 && j.ldx >= (int64_t)j.C * 32;
+    return B == 32 && j.K <= 8 && j.R % DWG::RB == 0 && (j.C == 4 || j.C == 8 || j.C == 16 || j.C == 32) &&
+           j.ldx >= (int64_t)j.C * 32;
   };
   bool taken[DWJobs::kMax] = {};
   for (int t = 0; t < n; ++t) {
@@ -1872,8 +1874,9 @@ int launch_dw(int B, const DWJob* jobs_in, int n, int64_t N, hipStream_t st) {
   }
   // B = 16 weights with at most 16 slots per row, rows in whole groups of 16 and input rows of
   // 256 to 1024 elements (the gate and up weights of such models) take dwg16_kernel
+  // (XI = C / 16 in {1, 2, 4}: C in {16, 32, 64})
   auto narrow16 = [&](const DWJob& j) {
-    return B == 16 && j.K <= 16 && j.R % 16 == 0 && j.C % 16 == 0 && j.C * 16 <= 1024 &&
+    return B == 16 && j.K <= 16 && j.R % 16 == 0 && (j.C == 16 || j.C == 32 || j.C == 64) &&
            j.ldx >= (int64_t)j.C * 16;
   };
   for (int t = 0; t < n; ++t) {

@@ -360,6 +360,7 @@ def test_gelu_mlpblock_backward_runs(gpu):
     (1024, 4096, 16384, 0.0, 32),          # the headline shape
     (512, 4096, 16384 + 37, 0.1, 32),      # 16 input column blocks, dead slots, a ragged last token chunk
     (1024, 4096, 16384 + 5, 0.05, 16),     # the headline geometry at B = 16 (the blocked tile gradients)
+    (768, 4096, 16384, 0.0, 32),           # 24 input column blocks: a width the row-blocked kernel has no form for
 ])
 def test_swiglu_bwd_full_size_sampled(gpu, case):
     """Full token counts (the tile gradients take the blocked kernels from 256 workgroups on),
