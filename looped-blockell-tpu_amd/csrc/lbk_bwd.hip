@@ -686,8 +686,9 @@ static int launch_dx_stage_t(const TProdArgs& a, hipStream_t st) {
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// dxf_kernel<B, D>: dx at B = 32 with one output block per wave (16 waves; the output blocks are
-// dealt to nsl workgroups per 64-token block, which share an XCD) and a D-slot ring of tiles that
+// dxf_kernel<B, D>: dx at B = 32 (and at B = 16 past the staged kernel's widths) with one output
+// block per wave (16 waves; the output blocks are dealt to nsl workgroups per 64-token block,
+// which share an XCD) and a D-slot ring of tiles that
 // runs over the wave's whole list -- the sorted entries of source 0, then of source 1 -- across
 // the 512-column stages of both sources, so D tile loads stay in flight where dx_stage_kernel
 // had one.  A stage change is a workgroup barrier taken inline when the next entry lies in a
@@ -704,7 +705,8 @@ __global__ __launch_bounds__(64 * DXF_WAVES, 1) void dxf_kernel(TProdArgs a) {
   constexpr int SROWB = COLS * 2;
   constexpr int SBYTES = 64 * SROWB;
   constexpr int PER_T = SBYTES / 16 / NT;
-  static_assert(B == 32, "one 32-deep k-step per tile");
+  // B = 32: one 32-deep k-step per tile; B = 16: the 16x16x16 form (8-byte fragments)
+  static_assert(B == 32 || B == 16, "tile size");
   extern __shared__ __attribute__((aligned(16))) unsigned char stg[];   // two stages
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = uniform(tid >> 6);
@@ -772,8 +774,9 @@ __global__ __launch_bounds__(64 * DXF_WAVES, 1) void dxf_kernel(TProdArgs a) {
 
   struct Slot {
     u32x4 av[CW];
-    int st;   // stage (-1: past the list)
-    int cb;   // column block within the stage
+    u32x2 a16;   // B = 16: the 16x16x16 fragment (tile row i, k = 4g .. 4g + 3)
+    int st;      // stage (-1: past the list)
+    int cb;      // column block within the stage
   };
   // slot S <- entry j of the list (its value e read from the window)
   auto fetch = [&](Slot& S, int j, int e) {
@@ -782,9 +785,13 @@ __global__ __launch_bounds__(64 * DXF_WAVES, 1) void dxf_kernel(TProdArgs a) {
     // r = e / K by multiply and shift (a division by a run-time value is a long sequence)
     const int r = live ? kdiv(s1 ? S1 : S0, e) : 0;
     const int64_t tile = live ? e : 0;              // past the list: tile 0 of source 0, unused
-    const uint16_t* tp = (live && s1 ? S1.w : S0.w) + tile * B * B + 8 * g;
+    if constexpr (B == 16) {
+      S.a16 = *reinterpret_cast<const u32x2*>((live && s1 ? S1.w : S0.w) + tile * B * B + i * B + 4 * g);
+    } else {
+      const uint16_t* tp = (live && s1 ? S1.w : S0.w) + tile * B * B + 8 * g;
 #pragma unroll
-    for (int m = 0; m < CW; ++m) S.av[m] = ld16(tp + op_row<CW>(i, m) * B);
+      for (int m = 0; m < CW; ++m) S.av[m] = ld16(tp + op_row<CW>(i, m) * B);
+    }
     S.st = live ? (s1 ? ns0 : 0) + r / G : -1;
     S.cb = r - (r / G) * G;
   };
@@ -795,6 +802,14 @@ __global__ __launch_bounds__(64 * DXF_WAVES, 1) void dxf_kernel(TProdArgs a) {
 #pragma unroll
     for (int m = 0; m < CW; ++m) acc[q][m] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto compute = [&](const Slot& S, const unsigned char* sb) {
+    if constexpr (B == 16) {
+      // rows 16q + i, k = 4g .. 4g + 3 of the block: 16-byte chunk 2 cb + g / 2, its half g & 1
+      const uint32_t pa = lbase + ((uint32_t)(((S.cb * 2 + (g >> 1)) ^ i) << 4) | (uint32_t)((g & 1) << 3));
+#pragma unroll
+      for (int q = 0; q < MT; ++q)
+        acc[q][0] = mfma_bf16_k16(S.a16, *reinterpret_cast<const u32x2*>(sb + pa + q * SROWB), acc[q][0]);
+      return;
+    }
     const uint32_t pa = lbase + (((S.cb * (B / 8) + g) ^ i) << 4);
 #pragma unroll
     for (int q = 0; q < MT; ++q) {
@@ -902,6 +917,12 @@ static int launch_dx_stage(int B, const TProdArgs& a0, hipStream_t st) {
   if (B == 32) { LBK_DX(32, 1) LBK_DX(32, 2) LBK_DX(32, 4) }
   if (B == 64) { LBK_DX(64, 1) LBK_DX(64, 2) }
 #undef LBK_DX
+  // B = 16 with more output blocks than the staged kernel's accumulators hold (N >= 16321 tokens
+  // and more than 64 output blocks): the deep-ring kernel, one output block per wave, in place of
+  // the per-entry kernel (1024 x 8192 product backward at 16384 tokens 1.275 -> 0.658 ms).  Where
+  // the staged kernel fits it stays: the deep ring stages the activations once per 16 output
+  // blocks and was slower there (SwiGLU backward at d_model 1024 0.823 -> 0.886 ms)
+  if (B == 16) return launch_dxf<16>(a0, st);
   return -2;
 }
 

@@ -172,7 +172,8 @@ MM_CASES = [
     (128, 256, 16, 0.5, 77, 0.0),
     (512, 256, 64, 0.25, 40, 0.05),
     (1024, 4096, 32, 0.25, 2100, 0.0),      # two token chunks of the tile gradients
-    (256, 2048, 16, 0.125, 33, 0.0),       # 128 output blocks: dx through the per-entry gather kernel
+    (256, 2048, 16, 0.125, 33, 0.0),       # 128 output blocks over 8 workgroups per token block
+    (256, 2048, 16, 0.125, 16400, 0.05),   # 128 output blocks at 257 token blocks: the deep-ring dx kernel
     (256, 800, 32, 0.25, 150, 0.1),        # 25 output blocks: the second workgroup of a token block has 7 idle waves
     (2048, 256, 32, 0.5, 70, 0.0),         # one source, 32 list entries per output block over 4 stages
 ]
