@@ -50,6 +50,8 @@ BWD_CASES = [
     (1024, 4096, 32, 0.25, 2100, 0.0),     # two token chunks of the tile gradients, ragged tail
     (2048, 1024, 32, 0.125, 40, 0.05),     # 64 output blocks: dx over four workgroups per token block
     (4096, 512, 64, 0.25, 20, 0.0),        # d_model > 2048: dh through the per-entry gather kernel too
+    (2048, 512, 16, 1.0, 70, 0.0),         # every h block read by 128 down slots: dh over two 64-entry list windows
+    (2048, 1024, 32, 1.0, 130, 0.05),      # every h block read by up to 64 slots (one full window), dead slots
 ]
 
 
