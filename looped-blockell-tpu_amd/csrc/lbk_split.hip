@@ -67,6 +67,16 @@ struct GUSlot<16> {
   u32x2 g, u;
   int cg, cu;
 };
+// B = 16 with one panel stream (a shared gate/up topology, or the plain product): a position is
+// a pair of slots (2p, 2p + 1) of a row, one 16x16x32 MFMA per product.  Lanes g < 2 hold
+// k = 8 (g & 1) .. + 7 of slot 2p's tile, lanes g >= 2 those of slot 2p + 1's (the packed B = 16
+// tile stores exactly these 16-byte pieces); cg / cu hold the two slots' gate / up column blocks
+// in bytes 0 and 1.  With two panel streams the panel reads, not the MFMAs, bound the kernel
+// (16 eight-byte reads per 8 MFMAs), and the pairs measured slower there.
+struct GUSlotPair {
+  u32x4 g, u;
+  int cg, cu;
+};
 
 __device__ __forceinline__ u32x2 lds8(const unsigned char* base, uint32_t off) {
   return *reinterpret_cast<const u32x2*>(base + off);
@@ -172,41 +182,67 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
   // loads, so the compiler's memory-counter waits stay exact and RING - 1
   // positions stay in flight across row boundaries.
   const int nrows = (nrs - w + NW - 1) / NW;   // may be <= 0: such a wave only helps fill the panel
-  const int KP = (K + RING - 1) / RING * RING;
+  constexpr bool PAIR = B == 16 && (SHARED || LIN);
+  using Slot = std::conditional_t<PAIR, GUSlotPair, GUSlot<B>>;
+  const int KS = PAIR ? (K + 1) / 2 : K;      // positions of a row: slots, or slot pairs
+  const int KP = (KS + RING - 1) / RING * RING;
   const u32x4* pg = static_cast<const u32x4*>(a.pg);
   const u32x4* pu = static_cast<const u32x4*>(a.pu);
   const uint32_t lbase = (uint32_t)(i * MT * ROWB);   // this lane's first panel row
 
   int rn = 0, rk = 0;   // next position to fetch
   // weight loads of the next position (the column table is not needed yet)
+  // byte offsets in a packed B = 16 tile of this lane's 8-byte 16x16x16 fragment and (slot pairs)
+  // of its 16-byte piece (row i, k = 8 (g & 1) .. + 7)
   const uint32_t f16 = pfrag16_off(lane);
-  auto fetch_w = [&](GUSlot<B>& S) {
-    const bool live = rn < nrows && rk < K;
-    const int el = (w + NW * rn) * K + rk;   // entry of the slice's column table
-    const int64_t e = live ? cbase + el : ztile;
-    if constexpr (B == 16) {
-      S.g = load_pfrag16(pg + e * PackedTile<B>::U32X4, f16);
-      if constexpr (!LIN) S.u = load_pfrag16(pu + e * PackedTile<B>::U32X4, f16);
+  const uint32_t f32 = (uint32_t)(16 * (i + 16 * (g & 1)));
+  auto fetch_w = [&](Slot& S) {
+    if constexpr (PAIR) {
+      // slots 2 rk and 2 rk + 1 of the row (past the row's slots: the zero tile)
+      const int k0 = 2 * rk;
+      const bool la = rn < nrows && k0 < K, lb = rn < nrows && k0 + 1 < K;
+      const int el = (w + NW * rn) * K + k0;   // entry of the slice's column table
+      const int64_t ea = la ? cbase + el : ztile, eb = lb ? cbase + el + 1 : ztile;
+      const int64_t e = g < 2 ? ea : eb;
+      S.g = *reinterpret_cast<const u32x4*>(reinterpret_cast<const unsigned char*>(pg + e * PackedTile<B>::U32X4) + f32);
+      if constexpr (!LIN)
+        S.u = *reinterpret_cast<const u32x4*>(reinterpret_cast<const unsigned char*>(pu + e * PackedTile<B>::U32X4) + f32);
+      S.cg = la ? el : -1;   // table entries until fetch_c replaces them by columns
+      S.cu = lb ? el + 1 : -1;
     } else {
-      load_pfrag<B>(pg + e * PackedTile<B>::U32X4, lane, S.g);
-      if constexpr (!LIN) load_pfrag<B>(pu + e * PackedTile<B>::U32X4, lane, S.u);
+      const bool live = rn < nrows && rk < K;
+      const int el = (w + NW * rn) * K + rk;   // entry of the slice's column table
+      const int64_t e = live ? cbase + el : ztile;
+      if constexpr (B == 16) {
+        S.g = load_pfrag16(pg + e * PackedTile<B>::U32X4, f16);
+        if constexpr (!LIN) S.u = load_pfrag16(pu + e * PackedTile<B>::U32X4, f16);
+      } else {
+        load_pfrag<B>(pg + e * PackedTile<B>::U32X4, lane, S.g);
+        if constexpr (!LIN) load_pfrag<B>(pu + e * PackedTile<B>::U32X4, lane, S.u);
+      }
+      S.cg = live ? el : -1;   // table entry until fetch_c replaces it by columns
     }
-    S.cg = live ? el : -1;   // table entry until fetch_c replaces it by columns
   };
-  auto fetch_c = [&](GUSlot<B>& S) {
-    const uint32_t c = ctab[S.cg >= 0 ? S.cg : 0];
-    S.cg = (int)(c & 0xffu);
-    S.cu = (int)(c >> 8);
+  auto fetch_c = [&](Slot& S) {
+    if constexpr (PAIR) {
+      const uint32_t ca = ctab[S.cg >= 0 ? S.cg : 0], cb = ctab[S.cu >= 0 ? S.cu : 0];
+      S.cg = (int)((ca & 0xffu) | ((cb & 0xffu) << 8));
+      S.cu = (int)((ca >> 8) | ((cb >> 8) << 8));
+    } else {
+      const uint32_t c = ctab[S.cg >= 0 ? S.cg : 0];
+      S.cg = (int)(c & 0xffu);
+      S.cu = (int)(c >> 8);
+    }
     if (++rk == KP) {
       rk = 0;
       ++rn;
     }
   };
-  auto fetch = [&](GUSlot<B>& S) {
+  auto fetch = [&](Slot& S) {
     fetch_w(S);
     fetch_c(S);
   };
-  GUSlot<B> P[RING];
+  Slot P[RING];
   auto prefetch_ring = [&]() {
     int sn = 0, sk = 0;
 #pragma unroll
@@ -226,18 +262,35 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
   f32x4 ag[MT][CW], au[MT][CW];
   // A fragments of a position's gate and up column blocks (shared topology: gate and up
   // read the same column list, so one panel read feeds both products)
-  using AF = std::conditional_t<B == 16, u32x2, u32x4>;
+  using AF = std::conditional_t<B == 16 && !PAIR, u32x2, u32x4>;
   struct AFrags {
     AF g[MT], u[SHARED ? 1 : MT];
   };
-  auto load_a = [&](const GUSlot<B>& S, AFrags& A) {
+  auto load_a = [&](const Slot& S, AFrags& A) {
     const int cg = uniform(S.cg), cu = uniform(S.cu);
-    if constexpr (B == 16) {
+    if constexpr (B == 16 && !PAIR) {
       const uint32_t ag0 = k16s_addr(lbase, cg, g, i), au0 = k16s_addr(lbase, cu, g, i);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         A.g[mt] = lds8(smem, ag0 + mt * ROWB);
         if constexpr (!SHARED) A.u[mt] = lds8(smem, au0 + mt * ROWB);
+      }
+    } else if constexpr (PAIR) {
+      // lane (i, g): token row i, k = 8 (g & 1) .. + 7 of its slot's column block: the 16-byte
+      // chunk 2 c + (g & 1), whose halves rows with (i & 8) store swapped, read as two 8-byte
+      // halves in order
+      const int lcg = g < 2 ? (cg & 0xff) : (cg >> 8), lcu = g < 2 ? (cu & 0xff) : (cu >> 8);
+      const uint32_t sw = (uint32_t)((i >> 3) & 1) << 3;
+      const uint32_t ag0 = lbase + ((uint32_t)((lcg * 2 + (g & 1)) ^ i) << 4);
+      const uint32_t au0 = lbase + ((uint32_t)((lcu * 2 + (g & 1)) ^ i) << 4);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const u32x2 glo = lds8(smem, ag0 + sw + mt * ROWB), ghi = lds8(smem, ag0 + (sw ^ 8) + mt * ROWB);
+        A.g[mt] = u32x4{glo[0], glo[1], ghi[0], ghi[1]};
+        if constexpr (!SHARED) {
+          const u32x2 ulo = lds8(smem, au0 + sw + mt * ROWB), uhi = lds8(smem, au0 + (sw ^ 8) + mt * ROWB);
+          A.u[mt] = u32x4{ulo[0], ulo[1], uhi[0], uhi[1]};
+        }
       }
     } else {
       const uint32_t ag0 = lbase + (((cg * (B / 8) + g) ^ i) << 4);
@@ -251,13 +304,20 @@ __device__ __forceinline__ void gu_tile(const GUArgs& a, int64_t tb, int r_lo, i
   };
   // The weight tile is the A operand and the panel rows the B operand, so an accumulator
   // holds h transposed: lane (n, g) of ag[mt][m] has token 16 mt + n and h columns
-  // 8 g + 4 m + v (B = 32, with the gate/up tile packing) or 4 g + v (B = 16), v < 4.
+  // 8 g + 4 m + v (B = 32, with the gate/up tile packing) or 4 g + v (B = 16, from one slot or a
+  // slot pair), v < 4.
   // FIRST: the row's first position, whose MFMAs start from zero (an inline constant, where
   // clearing the accumulators would take 64 moves per row at B = 32).
-  auto compute = [&](const GUSlot<B>& S, const AFrags& A, auto first) {
+  auto compute = [&](const Slot& S, const AFrags& A, auto first) {
     constexpr bool FIRST = decltype(first)::value;
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (B == 16) {
+    if constexpr (PAIR) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        ag[mt][0] = mfma_bf16(S.g, A.g[mt], FIRST ? z : ag[mt][0]);
+        if constexpr (!LIN) au[mt][0] = mfma_bf16(S.u, SHARED ? A.g[mt] : A.u[mt], FIRST ? z : au[mt][0]);
+      }
+    } else if constexpr (B == 16) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         ag[mt][0] = mfma_bf16_k16(S.g, A.g[mt], FIRST ? z : ag[mt][0]);
@@ -516,16 +576,19 @@ __global__ __launch_bounds__(512, 1) void gu_kernel(GUArgs a) {
 // gate/up with distinct gate/up topologies, without exported pre-activations or biases, one row
 // slice, with 12 waves and a 2-deep
 // ring: at most 168 VGPRs fit three waves per SIMD, and the extra waves hide more of the
-// panel-read and weight-load latency than the shallower ring gives up.  B = 16, with a quarter
-// of the accumulators and 8-byte fragments (113 VGPRs), runs 16 waves with a 4-deep ring
-// (forward at d_model 1024, d_ff 4096, 25 %, 16384 tokens: 0.2490 ms with 12 waves, 0.2467 with 16).
-template <int B> constexpr int gu_w12_waves() { return B == 16 ? 16 : 12; }
-// (B = 16 also takes shared topologies and biases here, within the same 128 VGPRs)
+// panel-read and weight-load latency than the shallower ring gives up.  B = 16 with a shared
+// topology (slot pairs, so a 2-deep ring keeps four slots in flight) takes the same shape; B = 16
+// with distinct topologies, with a quarter of the accumulators and 8-byte fragments (113 VGPRs),
+// runs 16 waves with a 4-deep ring (forward at d_model 1024, d_ff 4096, 25 %, 16384 tokens:
+// 0.2490 ms with 12 waves, 0.2467 with 16).
+template <int B, bool SHARED> constexpr int gu_w12_waves() { return B == 16 && !SHARED ? 16 : 12; }
+template <int B, bool SHARED> constexpr int gu_w12_ring() { return B == 16 && !SHARED ? 4 : 2; }
+// (B = 16 also takes shared topologies and biases here)
 template <int B, int MT, bool NORM, bool SHARED = false, bool BIAS = false>
-__global__ __launch_bounds__(64 * gu_w12_waves<B>(), 1) void gu_kernel_w12(GUArgs a) {
+__global__ __launch_bounds__((64 * gu_w12_waves<B, SHARED>()), 1) void gu_kernel_w12(GUArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   if (a.tdepth && !block_runs(a.tdepth, a.it, (int64_t)blockIdx.x * 16 * MT, 16 * MT, a.N, (int)threadIdx.x)) return;
-  gu_tile<B, MT, NORM, false, SHARED, false, BIAS, false, gu_w12_waves<B>(), B == 16 ? 4 : 2>(
+  gu_tile<B, MT, NORM, false, SHARED, false, BIAS, false, gu_w12_waves<B, SHARED>(), gu_w12_ring<B, SHARED>()>(
       a, (int64_t)blockIdx.x, 0, a.R_ff, smem, (int)threadIdx.x);
 }
 
@@ -1385,7 +1448,7 @@ static int launch_gu_w12(const GUArgs& a, hipStream_t st) {
   auto kern = gu_kernel_w12<B, MT, NORM, SHARED, BIAS>;
   static std::atomic<uint64_t> configured{0};
   if (set_lds_limit_once((const void*)kern, 163840, configured)) return -1;
-  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 16 * MT - 1) / (16 * MT))), dim3(64 * gu_w12_waves<B>()),
+  hipLaunchKernelGGL(kern, dim3((unsigned)((a.N + 16 * MT - 1) / (16 * MT))), dim3(64 * gu_w12_waves<B, SHARED>()),
                      gu_lds(a.R_ff, a.Kg, MT), st, a);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -37,6 +37,7 @@ def test_matmul_parity(gpu, B, N):
 @pytest.mark.parametrize("case", [
     # (in_features, out_features, B, K, N, path)
     (256, 512, 16, 4, 77, "panel"),
+    (256, 512, 16, 5, 77, "panel"),             # odd K: the last slot pair's second half is the zero tile
     (1024, 4096, 32, 8, 200, "panel"),          # the headline gate shape
     (2048, 1024, 32, 8, 70, "panel"),           # 32-token panels
     (4096, 1024, 32, 32, 130, "staged"),        # the headline down shape
@@ -233,7 +234,10 @@ def test_reference_default_layer_geometry(gpu, geom, N):
     assert rel <= TOL, f"rel {rel} abs {ab}"
 
 
-@pytest.mark.parametrize("case", [(1024, 4096, 32, 4096 + 5), (512, 1024, 16, 300), (1024, 2048, 32, 70)])
+@pytest.mark.parametrize("case", [(1024, 4096, 32, 4096 + 5), (512, 1024, 16, 300), (1024, 2048, 32, 70),
+                                  # B = 16 with 5 slots per row (slot pairs, the last one half zero);
+                                  # 16389 tokens take the one-slice 12-wave kernel
+                                  (320, 1024, 16, 300), (320, 1024, 16, 16384 + 5)])
 @pytest.mark.parametrize("intermediates", [False, True])
 def test_swiglu_shared_topology(gpu, case, intermediates):
     """Gate and up passing one column-index buffer (the shared-topology gate/up kernel, one
