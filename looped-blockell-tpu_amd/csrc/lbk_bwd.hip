@@ -403,17 +403,52 @@ __global__ __launch_bounds__(64 * NW, 1) void dh_panel_kernel(TProdArgs a) {
       const int lv = j0 == 0 ? lv0 : ((j0 + lane < cnt) ? L[j0 + lane] : 0);
       const int jn = (cnt - j0) < 64 ? (cnt - j0) : 64;
       auto ent = [&](int jj) { return __builtin_amdgcn_readlane(lv, jj < jn ? jj : jn - 1); };
-      // a DHR-entry ring: DHR - 1 tile loads in flight ahead of the MFMAs (positions past the
-      // end reload the last entry and are not computed)
-      constexpr int DHR = B == 64 ? 2 : 6;
-      Ent E[DHR];
+      if constexpr (B == 16) {
+        // slot pairs: ring position p holds entries 2p and 2p + 1, one 16x16x32 MFMA per token
+        // tile.  Lanes g < 2 hold row i, columns 8 (g & 1) .. + 7 of entry 2p's tile, lanes
+        // g >= 2 those of entry 2p + 1's (zeroed when the list ends at 2p + 1); the dy panel
+        // fragment is the 16-byte chunk 2 r + (g & 1) of the lane's entry's row block r.  A
+        // DHP-position ring as below (positions past the end reload the last entry)
+        constexpr int DHP = 4;
+        const int np = (jn + 1) >> 1;
+        Ent E[DHP];
+        auto loadp = [&](int p, Ent& E) {
+          const int e1 = ent(2 * p), e2 = ent(2 * p + 1);
+          const int e = g < 2 ? e1 : e2;
+          E.av[0][0] = *reinterpret_cast<const u32x4*>(S.w + (int64_t)e * (B * B) + i * B + 8 * (g & 1));
+          E.r = kdiv(S, e1) | (kdiv(S, e2) << 10) | (2 * p + 1 < jn ? 1 << 20 : 0);
+        };
+        auto computep = [&](const Ent& E) {
+          const int rr = uniform(E.r);
+          const int rl = g < 2 ? (rr & 1023) : ((rr >> 10) & 1023);
+          const u32x4 av = (g < 2 || ((rr >> 20) & 1)) ? E.av[0][0] : u32x4{0, 0, 0, 0};
+          const uint32_t pa = lbase + ((uint32_t)((rl * 2 + (g & 1)) ^ i) << 4);
 #pragma unroll
-      for (int k = 0; k < DHR - 1; ++k) load(ent(k), E[k]);
-      for (int jj = 0; jj < jn; jj += DHR) {
+          for (int q = 0; q < MT; ++q)
+            acc[q][0] = mfma_bf16(av, *reinterpret_cast<const u32x4*>(panel + pa + q * ROWB), acc[q][0]);
+        };
 #pragma unroll
-        for (int k = 0; k < DHR; ++k) {
-          load(ent(jj + k + DHR - 1), E[(k + DHR - 1) % DHR]);
-          if (k == 0 || jj + k < jn) compute(E[k]);
+        for (int k = 0; k < DHP - 1; ++k) loadp(k, E[k]);
+        for (int pp = 0; pp < np; pp += DHP) {
+#pragma unroll
+          for (int k = 0; k < DHP; ++k) {
+            loadp(pp + k + DHP - 1, E[(k + DHP - 1) % DHP]);
+            if (k == 0 || pp + k < np) computep(E[k]);
+          }
+        }
+      } else {
+        // a DHR-entry ring: DHR - 1 tile loads in flight ahead of the MFMAs (positions past the
+        // end reload the last entry and are not computed)
+        constexpr int DHR = B == 64 ? 2 : 6;
+        Ent E[DHR];
+#pragma unroll
+        for (int k = 0; k < DHR - 1; ++k) load(ent(k), E[k]);
+        for (int jj = 0; jj < jn; jj += DHR) {
+#pragma unroll
+          for (int k = 0; k < DHR; ++k) {
+            load(ent(jj + k + DHR - 1), E[(k + DHR - 1) % DHR]);
+            if (k == 0 || jj + k < jn) compute(E[k]);
+          }
         }
       }
     }
