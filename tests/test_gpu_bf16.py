@@ -38,6 +38,7 @@ def test_matmul_parity(gpu, B, N):
     # (in_features, out_features, B, K, N, path)
     (256, 512, 16, 4, 77, "panel"),
     (256, 512, 16, 5, 77, "panel"),             # odd K: the last slot pair's second half is the zero tile
+    (2048, 512, 16, 9, 70, "panel"),            # the same on 32-token panels (in_features 2048)
     (1024, 4096, 32, 8, 200, "panel"),          # the headline gate shape
     (2048, 1024, 32, 8, 70, "panel"),           # 32-token panels
     (4096, 1024, 32, 32, 130, "staged"),        # the headline down shape
