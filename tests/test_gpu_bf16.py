@@ -264,22 +264,30 @@ def test_swiglu_shared_topology(gpu, case, intermediates):
     assert rel <= TOL, f"rel {rel} abs {ab}"
 
 
-def test_looped_shared_topology(gpu):
+@pytest.mark.parametrize("geom", [(1024, 4096, 32), (512, 2048, 16)])
+def test_looped_shared_topology(gpu, geom):
     """The looped block with gate and up sharing one index buffer equals the same topology in
-    two buffers, bit for bit."""
+    two buffers, bit for bit; at B = 16 the shared topology takes the slot-pair gate/up form (in
+    the persistent kernel on the panel its down phase writes), the two buffers the single-slot
+    form, in both looped forms."""
     from looped_blockell import kernels
     import torch
     rng = np.random.default_rng(24)
-    d_model, d_ff, B, N = 1024, 4096, 32, 1000
-    _say("looped shared topology")
+    d_model, d_ff, B = geom
+    N = 1000
+    _say(f"looped shared topology {geom}")
     g, u, d = T.ffn_weights(rng, d_model, d_ff, B, 0.25)
     u = (u[0], g[1].copy())
     gt, ut, dt = T.gpu_weight(g), T.gpu_weight(u), T.gpu_weight(d)
     h = T.to_gpu_bf16(T.act(rng, N, d_model))
     scale = torch.ones(d_model, device="cuda")
-    a = kernels.looped_swiglu(h, scale, *gt, *ut, *dt, L=3)
-    b = kernels.looped_swiglu(h, scale, *gt, ut[0], gt[1], *dt, L=3)
-    assert np.array_equal(T.to_np(a), T.to_np(b))
+    forms = [kernels.looped_swiglu]
+    if B == 16:
+        forms += [kernels.looped_swiglu_persistent, kernels.looped_swiglu_launches]
+    for f in forms:
+        a = f(h, scale, *gt, *ut, *dt, L=3)
+        b = f(h, scale, *gt, ut[0], gt[1], *dt, L=3)
+        assert np.array_equal(T.to_np(a), T.to_np(b)), f.__name__
 
 
 def test_swiglu_zero_k(gpu):
